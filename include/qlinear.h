@@ -1,0 +1,162 @@
+/*
+ * qlinear.h — C ABI of libqlinear.so: GPTQ int4 quantized linears on MI355X (gfx950).
+ *
+ * Drop-in for the quantized-linear hot path of intplusplus/webllm. Plain pointers, sizes and
+ * byte offsets only; every function returns an int status (QL_OK = 0, negative = error class)
+ * and ql_last_error() holds the message of the calling thread's last failure. No exceptions
+ * cross the ABI. Weights stay GPTQ-packed in device memory; dequantization is fused into the
+ * kernels.
+ *
+ * Reference interfaces each entry point replaces (paths relative to the reference checkout):
+ *   ql_create / ql_destroy        src/gpu/device.ts:40-98 initGpu (one device, one queue)
+ *   ql_arena_*                    src/gpu/buffer.ts:20-34 createStorageBuffer, :103-120 writeF16 /
+ *                                 device.queue.writeBuffer, :123-170 readback; src/gpu/arena.ts:17-59
+ *   ql_gptq_desc / ql_gptq_check  src/weights/quant.ts:16-30 GptqInt4Params, :44-79 validation
+ *   ql_unpack_f16                 src/weights/qwen-loader.ts:55-67 dequantGptqLinear +
+ *                                 src/model/qwen.ts:262-266 uploadF16 (CPU dequant + f16 encode)
+ *   ql_plan_linear                src/model/qwen.ts:61-74 planGemvSplit + the branch in :568-618
+ *   ql_linear                     src/model/qwen.ts:568-618 QwenGpt.gemm (GEMV / split-K / GEMM)
+ *   ql_linear_batch               src/model/qwen.ts:411-413, :464-465 (q/k/v and gate/up issued
+ *                                 back to back on one input inside one CommandBatch pass)
+ *   ql_sync, ql_timer_*           src/gpu/buffer.ts:123-145 mapAsync readback,
+ *                                 src/gpu/pipeline.ts:119-161 timestamp-query profiling
+ *   ql_graph_*                    src/gpu/pipeline.ts:55-117 CommandBatch (one submit per forward)
+ */
+#ifndef QLINEAR_H
+#define QLINEAR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes. -1..-7 are the failure classes of quant.ts:46-79, in its check order. */
+#define QL_OK 0
+#define QL_E_BITS (-1)          /* bits != 4                                    quant.ts:46 */
+#define QL_E_GROUP (-2)         /* group <= 0                                   quant.ts:47 */
+#define QL_E_DIMS (-3)          /* K <= 0 or N <= 0                             quant.ts:48 */
+#define QL_E_QWEIGHT_SHORT (-4) /* qweight [ceil(K/8), N] int32 outside arena   quant.ts:58 */
+#define QL_E_SCALES_SHORT (-5)  /* scales [ceil(K/group), N] outside arena      quant.ts:62 */
+#define QL_E_QZEROS_SHORT (-6)  /* qzeros [ceil(K/group), ceil(N/8)] outside    quant.ts:69 */
+#define QL_E_GROUP_PACK (-7)    /* group % 8 != 0                               quant.ts:76 */
+#define QL_E_INVALID (-10)      /* null handle/pointer, bad M, bad dtype                     */
+#define QL_E_RANGE (-11)        /* activation/output/scratch range outside its arena         */
+#define QL_E_ALIGN (-12)        /* misaligned offset (int32/f32: 4 B, f16: 2 B)              */
+#define QL_E_HIP (-13)          /* HIP runtime failure (message in ql_last_error)            */
+#define QL_E_STATE (-14)        /* call not valid in the current state (graph capture)       */
+
+/* Sentinel for optional offsets (no qzeros -> symmetric zero 8, quant.ts:73-74; no bias). */
+#define QL_NONE UINT64_MAX
+
+#define QL_DTYPE_F32 0
+#define QL_DTYPE_F16 1
+
+/* kernel families returned by ql_plan_linear */
+#define QL_KIND_GEMV_MFMA 1   /* M <= 16: packed-int4 GEMV on MFMA, hi/lo split activations */
+#define QL_KIND_GEMV_SIMPLE 2 /* any shape: one lane per output column, fp32                */
+#define QL_KIND_GEMM_MFMA 3   /* M > 16: LDS-dequant f16 tiles, MFMA f16, fp32 accumulate   */
+#define QL_KIND_GEMM_SIMPLE 4 /* any shape: f16 operands, fp32 accumulate, no MFMA          */
+
+typedef struct ql_ctx ql_ctx;
+typedef struct ql_arena ql_arena;
+typedef struct ql_graph ql_graph;
+
+/* GPTQ int4 linear inside a weight arena (byte offsets). Mirrors GptqInt4Params
+ * (quant.ts:16-30) except that scales stay raw fp16 as stored in the checkpoint.
+ *   qweight int32 [ceil(K/8), N]   8 nibbles per word, low nibble = smallest input index
+ *   qzeros  int32 [ceil(K/group), ceil(N/8)] stored zero - 1, or QL_NONE (zero = 8)
+ *   scales  fp16  [ceil(K/group), N]
+ *   bias    fp32  [N] or QL_NONE
+ * W[n,k] = (q[k,n] - (qz[g,n] + 1)) * s[g,n], g = k / group. */
+typedef struct ql_gptq_desc {
+    uint64_t qweight_off;
+    uint64_t qzeros_off;
+    uint64_t scales_off;
+    uint64_t bias_off;
+    int32_t K;     /* in_features  */
+    int32_t N;     /* out_features */
+    int32_t group; /* group size (128 for Qwen2.5 GPTQ) */
+    int32_t bits;  /* must be 4 */
+} ql_gptq_desc;
+
+typedef struct ql_plan {
+    int32_t kind;          /* QL_KIND_* */
+    int32_t split;         /* K segments; partial sums reduced in fixed ascending order */
+    int32_t waves;         /* waves per workgroup splitting each segment */
+    int32_t grid_x;        /* workgroups along N */
+    int32_t grid_y;        /* workgroups along K (split) or M (GEMM) */
+    int32_t block;         /* threads per workgroup */
+    uint64_t scratch_bytes;/* bytes the caller must provide at scratch_off (0 if none) */
+    int32_t ref_split;     /* planGemvSplit(ceil(N/256), K) of the reference, for comparison */
+    int32_t reserved;
+} ql_plan;
+
+/* ---- context: one device, one HIP stream (default priority). */
+int ql_create(int device, ql_ctx** out);
+int ql_destroy(ql_ctx* ctx);
+const char* ql_last_error(void);
+int ql_device_info(ql_ctx* ctx, char* name, int name_len, int* cu_count, uint64_t* hbm_bytes);
+
+/* ---- arenas: one device allocation addressed by byte offset (256-B aligned base). */
+int ql_arena_reserve(ql_ctx* ctx, uint64_t bytes, ql_arena** out);
+int ql_arena_release(ql_arena* arena);
+uint64_t ql_arena_size(const ql_arena* arena);
+/* device address of arena byte 0, for interop (e.g. wrapping as a framework tensor) */
+uint64_t ql_arena_device_ptr(const ql_arena* arena);
+/* synchronous host<->device copies; the host pointer is borrowed for the call only */
+int ql_arena_write(ql_arena* arena, uint64_t off, const void* src, uint64_t bytes);
+int ql_arena_read(ql_arena* arena, uint64_t off, void* dst, uint64_t bytes);
+/* device-side copy between arenas, enqueued on the context stream */
+int ql_arena_copy(ql_ctx* ctx, ql_arena* dst, uint64_t dst_off, const ql_arena* src,
+                  uint64_t src_off, uint64_t bytes);
+
+/* ---- GPTQ descriptors (host only, no GPU work). */
+/* sizes in bytes of the three packed tensors of a K x N linear */
+int ql_gptq_sizes(int32_t K, int32_t N, int32_t group, uint64_t* qweight_bytes,
+                  uint64_t* qzeros_bytes, uint64_t* scales_bytes);
+/* validates like quant.ts:44-79 (same classes, same order) against a weight arena of
+ * arena_bytes bytes, then the bias range (QL_E_RANGE) and alignment (QL_E_ALIGN). Host only. */
+int ql_gptq_validate(const ql_gptq_desc* desc, uint64_t arena_bytes);
+/* ql_gptq_validate against the arena's size */
+int ql_gptq_check(const ql_gptq_desc* desc, const ql_arena* weights);
+
+/* ---- load time: fp16 [N,K] row-major, bit-identical to
+ * f32ToF16Bits(dequantizeGptqInt4(...)) (quant.ts:42-118, buffer.ts:57-100). */
+int ql_unpack_f16(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights,
+                  ql_arena* out, uint64_t out_off);
+
+/* ---- dispatch plan (host only, deterministic, pure). */
+int ql_plan_linear(int32_t M, int32_t N, int32_t K, int32_t group, ql_plan* out);
+
+/* ---- y[M,N] (fp32) = x[M,K] * W^T (+ bias), enqueued on the context stream.
+ * x_dtype: QL_DTYPE_F32 (decode path) or QL_DTYPE_F16. Offsets are into `act`.
+ * scratch_off: plan.scratch_bytes bytes in `act` for split-K partial sums (ignored when 0).
+ * The caller orders work by issuing it on this one stream (stream order replaces the
+ * reference's passBreak, qwen.ts:556-559). */
+int ql_linear(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights, ql_arena* act,
+              uint64_t x_off, int32_t x_dtype, int32_t M, uint64_t y_off, uint64_t scratch_off);
+
+/* several independent linears in one launch (e.g. q/k/v on one input, gate/up on another);
+ * linear i reads x_offs[i] and writes y_offs[i]; scratch for all of them starts at scratch_off
+ * (ql_plan_batch gives the size). M and x_dtype are shared; at most 8 linears. */
+int ql_plan_batch(int32_t count, const ql_gptq_desc* descs, int32_t M, uint64_t* scratch_bytes);
+int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
+                    const ql_arena* weights, ql_arena* act, const uint64_t* x_offs,
+                    int32_t x_dtype, int32_t M, const uint64_t* y_offs, uint64_t scratch_off);
+
+/* ---- ordering and timing on the context stream */
+int ql_sync(ql_ctx* ctx);
+int ql_timer_start(ql_ctx* ctx);
+int ql_timer_stop(ql_ctx* ctx, float* elapsed_ms); /* waits for the stop event */
+
+/* ---- stream capture into a HIP graph (one replayable submit per forward). */
+int ql_graph_begin(ql_ctx* ctx);
+int ql_graph_end(ql_ctx* ctx, ql_graph** out);
+int ql_graph_launch(ql_ctx* ctx, ql_graph* graph);
+int ql_graph_destroy(ql_graph* graph);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QLINEAR_H */

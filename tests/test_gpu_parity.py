@@ -1,0 +1,356 @@
+"""GPU parity: libqlinear.so (called through its C ABI) against the CPU oracle on the same bytes.
+
+Bars: dequant bit-exact; GEMV |d| <= 1e-5 + 1e-4*|ref| against fp32
+weights with double accumulation (gemmNTRef, src/reference/qwen-ref.ts:126-145); MFMA GEMM
+|d| <= 1e-5 + 2e-3*|ref| against the oracle on fp16-rounded x and W.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from webllm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+GEMV_ATOL, GEMV_RTOL = 1e-5, 1e-4
+GEMM_ATOL, GEMM_RTOL = 1e-5, 2e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+class Linear:
+    """One GPTQ linear uploaded to its own weight arena."""
+
+    def __init__(self, ql, ctx, t: synth.GptqTensors, bias=None, no_qzeros=False):
+        lay = ql.ArenaLayout()
+        qw_off = lay.take(t.qweight.nbytes)
+        qz_off = None if no_qzeros else lay.take(t.qzeros.nbytes)
+        sc_off = lay.take(t.scales.nbytes)
+        b_off = None if bias is None else lay.take(bias.nbytes)
+        self.arena = ctx.arena(lay.used)
+        self.arena.write(qw_off, t.qweight)
+        if qz_off is not None:
+            self.arena.write(qz_off, t.qzeros)
+        self.arena.write(sc_off, t.scales)
+        if bias is not None:
+            self.arena.write(b_off, bias)
+        self.desc = ql.make_desc(qw_off, qz_off, sc_off, t.K, t.N, t.group, b_off)
+        self.t = t
+        self.bias = bias
+        self.qzeros = None if no_qzeros else t.qzeros
+
+
+def run_linear(ql, ctx, lin: Linear, x: np.ndarray, x_dtype=0):
+    M, K = x.shape
+    N = lin.t.N
+    plan = ql.plan_linear(M, N, K, lin.t.group)
+    lay = ql.ArenaLayout()
+    x_off = lay.take(x.nbytes)
+    y_off = lay.take(M * N * 4)
+    s_off = lay.take(max(plan.scratch_bytes, 16))
+    act = ctx.arena(lay.used)
+    act.write(x_off, x)
+    ctx.linear(lin.desc, lin.arena, act, x_off, x_dtype, M, y_off, s_off)
+    y = act.read(y_off, (M, N), np.float32)
+    act.release()
+    return y, plan
+
+
+def oracle_gemv(orc, lin: Linear, x):
+    return orc.gptq_linear(lin.t.qweight, lin.qzeros, lin.t.scales, x, lin.bias, lin.t.group)
+
+
+def assert_close(orc, got, ref, atol, rtol, label):
+    ok, max_abs, max_rel = orc.check_tolerance(got, ref, atol, rtol)
+    norm = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+    say(f"  {label}: maxAbs={max_abs:.3e} maxRel={max_rel:.3e} normwise={norm:.3e}")
+    assert ok, f"{label}: |d| > {atol} + {rtol}|ref| (maxAbs {max_abs:.3e})"
+
+
+# ------------------------------------------------------------------------- load-time unpack
+
+UNPACK_CASES = [
+    # (K, N, group, stored_zero, no_qzeros, label)
+    (896, 4864, 128, 7, False, "0.5B gate"),
+    (4864, 896, 128, None, False, "0.5B down, random zeros"),
+    (896, 128, 128, 7, True, "0.5B k, no qzeros"),
+    (16, 5, 8, None, False, "reference KAT shape"),
+    (20, 13, 8, None, False, "K%8!=0, N%8!=0 (generic)"),
+    (136, 12, 8, 15, False, "zero 16"),
+    (256, 64, 64, None, False, "group 64"),
+]
+
+
+@pytest.mark.parametrize("K,N,group,zero,noqz,label", UNPACK_CASES)
+def test_unpack_bitexact(ql, ctx, orc, K, N, group, zero, noqz, label):
+    say(f"unpack {label}: K={K} N={N} group={group}")
+    t = synth.gptq_linear(K, N, group, seed=0x7A11, key=(K, N), stored_zero=zero)
+    lin = Linear(ql, ctx, t, no_qzeros=noqz)
+    out = ctx.arena(N * K * 2 + 256)
+    ctx.unpack_f16(lin.desc, lin.arena, out, 0)
+    got = out.read(0, (N, K), np.uint16)
+    want = orc.dequantize_gptq_int4_f16(t.qweight, lin.qzeros, t.scales, K, N, group)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"{bad.size} mismatches, first at {bad[:4]}"
+
+
+def test_unpack_subnormal_overflow_scales(ql, ctx, orc):
+    """fp16-subnormal scales (about 0.5% of |N(0,1)|*0.01), the smallest subnormal, and large
+    scales whose products overflow to +-Inf, all bit-exact."""
+    K, N = 512, 256
+    t = synth.gptq_linear(K, N, 128, seed=0x5AB, stored_zero=None)
+    s = t.scales.view(np.float16).copy()
+    s[0, :64] = np.float16(2.0 ** -20)
+    s[1, :32] = np.float16(2.0 ** -24)
+    s[1, 32:64] = np.float16(6.1e-5)
+    s[2, :16] = np.float16(8192.0)
+    s[3, :16] = np.float16(65504.0)
+    t.scales = s.view(np.uint16)
+    lin = Linear(ql, ctx, t)
+    out = ctx.arena(N * K * 2)
+    ctx.unpack_f16(lin.desc, lin.arena, out, 0)
+    got = out.read(0, (N, K), np.uint16)
+    want = orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, K, N, 128)
+    assert np.array_equal(got, want)
+    assert np.any(got == 0x7C00) or np.any(got == 0xFC00)
+
+
+def test_unpack_all_168_tensors_05b(ql, ctx, orc):
+    """Config 5: every int4 tensor of a Qwen2.5-0.5B-shaped model into one fp16 [N,K] arena."""
+    linears = synth.model_linears("0.5b")
+    lay = ql.ArenaLayout()
+    tensors, offs = [], []
+    for (layer, proj, K, N) in linears:
+        t = synth.gptq_linear(K, N, 128, seed=0xC5, key=(layer, synth.PROJ_INDEX[proj]))
+        tensors.append(t)
+        offs.append((lay.take(t.qweight.nbytes), lay.take(t.qzeros.nbytes), lay.take(t.scales.nbytes)))
+    w = ctx.arena(lay.used)
+    olay = ql.ArenaLayout()
+    out_offs = [olay.take(t.N * t.K * 2) for t in tensors]
+    out = ctx.arena(olay.used)
+    say(f"unpack 168 tensors: packed {lay.used/1e6:.1f} MB -> fp16 {olay.used/1e6:.1f} MB")
+    for t, (a, b, c), o in zip(tensors, offs, out_offs):
+        w.write(a, t.qweight); w.write(b, t.qzeros); w.write(c, t.scales)
+        ctx.unpack_f16(ql.make_desc(a, b, c, t.K, t.N, 128), w, out, o)
+    ctx.sync()
+    for i, (t, o) in enumerate(zip(tensors, out_offs)):
+        got = out.read(o, (t.N, t.K), np.uint16)
+        want = orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, t.K, t.N, 128)
+        assert np.array_equal(got, want), f"tensor {i} {linears[i]}"
+
+
+# ------------------------------------------------------------------------- decode GEMV
+
+GEMV_CASES = [
+    # (K, N, M, stored_zero, bias, label)
+    (896, 4864, 1, 7, False, "cfg1 gate M=1"),
+    (896, 4864, 2, 7, False, "gate M=2"),
+    (896, 4864, 4, None, False, "gate M=4 random zeros"),
+    (896, 4864, 8, 7, False, "gate M=8"),
+    (896, 4864, 16, None, False, "gate M=16 random zeros"),
+    (896, 896, 1, 7, True, "q +bias"),
+    (896, 128, 1, 7, True, "k +bias"),
+    (4864, 896, 1, None, False, "down"),
+    (4864, 896, 9, 7, False, "down M=9"),
+    (3584, 18944, 1, 7, False, "7B gate M=1"),
+    (18944, 3584, 4, 7, False, "7B down M=4"),
+    (3584, 3584, 16, None, False, "7B q M=16"),
+]
+
+
+@pytest.mark.parametrize("K,N,M,zero,with_bias,label", GEMV_CASES)
+def test_gemv_parity(ql, ctx, orc, K, N, M, zero, with_bias, label):
+    t = synth.gptq_linear(K, N, 128, seed=0x9EF0, key=(K, N), stored_zero=zero)
+    bias = synth.activations(1, N, seed=0xB1A5, key=(N,))[0] if with_bias else None
+    x = synth.activations(M, K, seed=0x9EF1, key=(K, M))
+    lin = Linear(ql, ctx, t, bias=bias)
+    plan = ql.plan_linear(M, N, K)
+    say(f"gemv {label}: M={M} K={K} N={N} kind={plan.kind_name} split={plan.split}")
+    y, _ = run_linear(ql, ctx, lin, x)
+    ref = oracle_gemv(orc, lin, x)
+    assert plan.kind_name == "gemv_mfma"
+    assert_close(orc, y, ref, GEMV_ATOL, GEMV_RTOL, label)
+
+
+def test_gemv_f16_activations(ql, ctx, orc):
+    K, N, M = 896, 896, 3
+    t = synth.gptq_linear(K, N, 128, seed=0x16)
+    x16 = synth.activations(M, K, seed=0x17).astype(np.float16)
+    lin = Linear(ql, ctx, t)
+    y, _ = run_linear(ql, ctx, lin, x16.view(np.uint16), x_dtype=1)
+    ref = oracle_gemv(orc, lin, x16.astype(np.float32))
+    assert_close(orc, y, ref, GEMV_ATOL, GEMV_RTOL, "f16 x")
+
+
+def test_gemv_deterministic(ql, ctx):
+    """Split-K partials are reduced in fixed ascending order: repeated runs are bit-identical."""
+    K, N, M = 18944, 3584, 2
+    t = synth.gptq_linear(K, N, 128, seed=0xDE7)
+    x = synth.activations(M, K, seed=0xDE8)
+    lin = Linear(ql, ctx, t)
+    assert ql.plan_linear(M, N, K).split > 1
+    ys = [run_linear(ql, ctx, lin, x)[0] for _ in range(3)]
+    assert all(np.array_equal(ys[0].view(np.uint32), y.view(np.uint32)) for y in ys[1:])
+
+
+def test_batch_matches_single(ql, ctx, orc):
+    """q/k/v on one input in one launch == three separate launches (bit-identical)."""
+    K = 896
+    ts = [synth.gptq_linear(K, n, 128, seed=0xBA7, key=(i,)) for i, n in enumerate((896, 128, 128))]
+    biases = [synth.activations(1, t.N, seed=0xBA8, key=(i,))[0] for i, t in enumerate(ts)]
+    lins = [Linear(ql, ctx, t, bias=b) for t, b in zip(ts, biases)]
+    # one shared weight arena is required by the batch entry point: repack
+    lay = ql.ArenaLayout()
+    descs, parts = [], []
+    for t, b in zip(ts, biases):
+        a, z, s, bo = lay.take(t.qweight.nbytes), lay.take(t.qzeros.nbytes), lay.take(t.scales.nbytes), lay.take(b.nbytes)
+        parts.append((a, z, s, bo, t, b))
+        descs.append(ql.make_desc(a, z, s, K, t.N, 128, bo))
+    w = ctx.arena(lay.used)
+    for a, z, s, bo, t, b in parts:
+        w.write(a, t.qweight); w.write(z, t.qzeros); w.write(s, t.scales); w.write(bo, b)
+    for M in (1, 5, 16):
+        x = synth.activations(M, K, seed=0xBA9, key=(M,))
+        scratch = ql.plan_batch(descs, M)
+        alay = ql.ArenaLayout()
+        x_off = alay.take(x.nbytes)
+        y_offs = [alay.take(M * t.N * 4) for t in ts]
+        s_off = alay.take(scratch)
+        act = ctx.arena(alay.used)
+        act.write(x_off, x)
+        ctx.linear_batch(descs, w, act, [x_off] * 3, 0, M, y_offs, s_off)
+        for lin, yo, t in zip(lins, y_offs, ts):
+            yb = act.read(yo, (M, t.N), np.float32)
+            ys, _ = run_linear(ql, ctx, lin, x)
+            assert np.array_equal(yb.view(np.uint32), ys.view(np.uint32))
+            assert_close(orc, yb, oracle_gemv(orc, lin, x), GEMV_ATOL, GEMV_RTOL, f"batch M={M} N={t.N}")
+
+
+# ------------------------------------------------------------------------- prefill GEMM
+
+GEMM_CASES = [
+    (896, 4864, 128, 7, "cfg3 gate M=128"),
+    (4864, 896, 64, None, "down M=64"),
+    (896, 896, 512, 7, "q M=512"),
+    (896, 128, 17, 7, "k M=17 (ragged tiles)"),
+    (896, 4864, 100, None, "gate M=100 ragged"),
+]
+
+
+@pytest.mark.parametrize("K,N,M,zero,label", GEMM_CASES)
+def test_gemm_parity(ql, ctx, orc, K, N, M, zero, label):
+    t = synth.gptq_linear(K, N, 128, seed=0x6E33, key=(K, N, M), stored_zero=zero)
+    bias = synth.activations(1, N, seed=0x6E34, key=(N,))[0]
+    x = synth.activations(M, K, seed=0x6E35, key=(K, M))
+    lin = Linear(ql, ctx, t, bias=bias)
+    plan = ql.plan_linear(M, N, K)
+    say(f"gemm {label}: M={M} K={K} N={N} kind={plan.kind_name}")
+    assert plan.kind_name == "gemm_mfma"
+    for x_dtype in (0, 1):
+        xin = x if x_dtype == 0 else x.astype(np.float16).view(np.uint16)
+        y, _ = run_linear(ql, ctx, lin, xin, x_dtype)
+        W16 = orc.f16_bits_to_f32(orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, K, N, 128))
+        x16 = orc.f16_bits_to_f32(orc.f32_to_f16_bits(x))
+        ref = orc.gemm_nt(x16, W16, bias)
+        assert_close(orc, y, ref, GEMM_ATOL, GEMM_RTOL, f"{label} x_dtype={x_dtype}")
+        ref32 = oracle_gemv(orc, lin, x)   # against the pure-fp32 oracle, reported only
+        say(f"    vs fp32 oracle normwise={np.abs(y-ref32).max()/np.abs(ref32).max():.3e}")
+
+
+# ------------------------------------------------------------------------- generic paths
+
+def test_simple_paths_reference_kat_shape(ql, ctx, orc):
+    """Shapes outside the MFMA kernels' constraints (N % 4 != 0, K % 32 != 0) still run on the GPU
+    (one lane per column) and meet the same bars."""
+    K, N = 20, 13
+    t = synth.gptq_linear(K, N, 8, seed=0x51, stored_zero=None)
+    lin = Linear(ql, ctx, t, bias=synth.activations(1, N, seed=0x52)[0])
+    for M in (1, 3):
+        x = synth.activations(M, K, seed=0x53, key=(M,))
+        y, plan = run_linear(ql, ctx, lin, x)
+        assert plan.kind_name == "gemv_simple"
+        assert_close(orc, y, oracle_gemv(orc, lin, x), GEMV_ATOL, GEMV_RTOL, f"simple gemv M={M}")
+    x = synth.activations(40, K, seed=0x54)
+    y, plan = run_linear(ql, ctx, lin, x)
+    assert plan.kind_name == "gemm_simple"
+    W16 = orc.f16_bits_to_f32(orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, K, N, 8))
+    ref = orc.gemm_nt(orc.f16_bits_to_f32(orc.f32_to_f16_bits(x)), W16, lin.bias)
+    assert_close(orc, y, ref, GEMM_ATOL, GEMM_RTOL, "simple gemm")
+
+
+def test_misaligned_offsets_fall_back_correctly(ql, ctx, orc):
+    """x at a 4-byte (not 16-byte) offset uses the generic kernel, same bar."""
+    K, N, M = 896, 256, 2
+    t = synth.gptq_linear(K, N, 128, seed=0xA1)
+    lin = Linear(ql, ctx, t)
+    x = synth.activations(M, K, seed=0xA2)
+    act = ctx.arena(1 << 20)
+    act.write(4, x)
+    ctx.linear(lin.desc, lin.arena, act, 4, 0, M, 65536, 131072)
+    y = act.read(65536, (M, N), np.float32)
+    assert_close(orc, y, oracle_gemv(orc, lin, x), GEMV_ATOL, GEMV_RTOL, "misaligned x")
+
+
+def test_range_errors_raise(ql, ctx):
+    t = synth.gptq_linear(128, 64, 128, seed=0xE1)
+    lin = Linear(ql, ctx, t)
+    act = ctx.arena(4096)
+    with pytest.raises(ql.QlError) as e:
+        ctx.linear(lin.desc, lin.arena, act, 0, 0, 1, 4000, 0)    # y runs past the arena
+    assert e.value.name == "QL_E_RANGE"
+    with pytest.raises(ql.QlError) as e:
+        ctx.linear(lin.desc, lin.arena, act, 0, 2, 1, 1024, 0)    # bad dtype
+    assert e.value.name == "QL_E_INVALID"
+    bad = ql.make_desc(lin.desc.qweight_off, lin.desc.qzeros_off, lin.desc.scales_off, 128, 64, 128, bits=3)
+    with pytest.raises(ql.QlError) as e:
+        ctx.linear(bad, lin.arena, act, 0, 0, 1, 1024, 2048)
+    assert e.value.name == "QL_E_BITS"
+
+
+# ------------------------------------------------------------------------- graph replay
+
+def test_graph_replay_matches_eager(ql, ctx):
+    """A captured sequence (two dependent linears, the second split-K) replayed several times,
+    with eager work between replays, gives the eager result every time."""
+    K1, N1, K2, N2 = 896, 4864, 4864, 896
+    t1 = synth.gptq_linear(K1, N1, 128, seed=0x61)
+    t2 = synth.gptq_linear(K2, N2, 128, seed=0x62)
+    lay = ql.ArenaLayout()
+    o1 = (lay.take(t1.qweight.nbytes), lay.take(t1.qzeros.nbytes), lay.take(t1.scales.nbytes))
+    o2 = (lay.take(t2.qweight.nbytes), lay.take(t2.qzeros.nbytes), lay.take(t2.scales.nbytes))
+    w = ctx.arena(lay.used)
+    for t, o in ((t1, o1), (t2, o2)):
+        w.write(o[0], t.qweight); w.write(o[1], t.qzeros); w.write(o[2], t.scales)
+    d1 = ql.make_desc(*o1, K1, N1, 128)
+    d2 = ql.make_desc(*o2, K2, N2, 128)
+    p1, p2 = ql.plan_linear(1, N1, K1), ql.plan_linear(1, N2, K2)
+    assert p2.split > 1
+    alay = ql.ArenaLayout()
+    x_off = alay.take(K1 * 4); h_off = alay.take(N1 * 4); y_off = alay.take(N2 * 4)
+    s1 = alay.take(p1.scratch_bytes); s2 = alay.take(p2.scratch_bytes)
+    act = ctx.arena(alay.used)
+    x = synth.activations(1, K1, seed=0x63)
+    act.write(x_off, x)
+
+    def step():
+        ctx.linear(d1, w, act, x_off, 0, 1, h_off, s1)
+        ctx.linear(d2, w, act, h_off, 0, 1, y_off, s2)
+
+    step()
+    eager = act.read(y_off, (1, N2), np.float32)
+    ctx.graph_begin()
+    step()
+    g = ctx.graph_end()
+    for i in range(4):
+        act.write(y_off, np.zeros(N2, np.float32))
+        g.launch()
+        ctx.sync()
+        got = act.read(y_off, (1, N2), np.float32)
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {i}"
+        step()                     # eager work between replays
+        ctx.sync()
+    g.destroy()

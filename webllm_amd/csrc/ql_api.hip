@@ -1,0 +1,617 @@
+// C ABI of libqlinear.so (declared in include/qlinear.h): context, arenas, GPTQ descriptor
+// validation, dispatch planning and kernel dispatch. No exceptions cross the ABI; every entry
+// point returns a status and records a message for ql_last_error().
+#include "../../include/qlinear.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "ql_internal.h"
+
+struct ql_ctx {
+    int device;
+    hipStream_t stream;
+    uint32_t* counters;   // split-K arrival counters, zero between launches
+    hipEvent_t ev_start, ev_stop;
+    bool capturing;
+    int cu_count;
+    uint64_t hbm_bytes;
+    char name[256];
+};
+
+struct ql_arena {
+    ql_ctx* ctx;
+    char* base;
+    uint64_t size;
+};
+
+struct ql_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+    return fail(QL_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define QL_HIP(call)                                   \
+    do {                                               \
+        hipError_t e_ = (call);                        \
+        if (e_ != hipSuccess) return hip_fail(e_, #call); \
+    } while (0)
+
+bool in_range(uint64_t off, uint64_t bytes, uint64_t size)
+{
+    return off <= size && bytes <= size - off;
+}
+
+uint64_t align256(uint64_t v) { return (v + 255) & ~(uint64_t)255; }
+
+// planGemvSplit of the reference (src/model/qwen.ts:42-44, :61-74), reported in ql_plan.ref_split.
+int ref_plan_gemv_split(int wg_n, int K)
+{
+    if (wg_n >= 256) return 1;
+    const int cands[4] = {8, 16, 32, 64};
+    int s = 1;
+    for (int c : cands) {
+        if (K % c == 0 && (K / c) % 2 == 0) {
+            s = c;
+            if (wg_n * c >= 256) break;
+        }
+    }
+    return s;
+}
+
+int plan_impl(int M, int N, int K, int group, ql_plan* p)
+{
+    memset(p, 0, sizeof *p);
+    if (group <= 0) return fail(QL_E_GROUP, "group must be positive (got %d)", group);
+    if (M <= 0 || N <= 0 || K <= 0) return fail(QL_E_DIMS, "M, N, K must be positive (M=%d N=%d K=%d)", M, N, K);
+    p->ref_split = ref_plan_gemv_split((N + 255) / 256, K);
+    if (M <= ql::kGemvMaxM) {
+        if (ql::gemv_fast_ok(M, N, K, group)) {
+            const ql::GemvShape s = ql::gemv_shape(M, N, K, group);
+            p->kind = QL_KIND_GEMV_MFMA;
+            p->split = s.split;
+            p->waves = s.waves;
+            p->grid_x = s.strips * s.split;
+            p->grid_y = 1;
+            p->block = 256;
+            p->scratch_bytes = ql::gemv_xs_bytes(M, K) + ql::gemv_partial_bytes(M, N, s.split);
+        } else {
+            p->kind = QL_KIND_GEMV_SIMPLE;
+            p->split = 1;
+            p->waves = 4;
+            p->grid_x = (N + 255) / 256;
+            p->grid_y = (M + 7) / 8;
+            p->block = 256;
+        }
+    } else if (ql::gemm_fast_ok(M, N, K, group)) {
+        p->kind = QL_KIND_GEMM_MFMA;
+        p->split = 1;
+        p->waves = 4;
+        ql::gemm_grid(M, N, &p->grid_x, &p->grid_y, &p->block);
+    } else {
+        p->kind = QL_KIND_GEMM_SIMPLE;
+        p->split = 1;
+        p->waves = 4;
+        p->grid_x = (N + 255) / 256;
+        p->grid_y = (M + 7) / 8;
+        p->block = 256;
+    }
+    return QL_OK;
+}
+
+int validate_desc(const ql_gptq_desc* d, uint64_t arena_bytes)
+{
+    if (!d) return fail(QL_E_INVALID, "null descriptor");
+    if (d->bits != 4) return fail(QL_E_BITS, "GPTQ: only 4-bit is supported, got bits=%d", d->bits);
+    if (d->group <= 0) return fail(QL_E_GROUP, "GPTQ: group size must be positive");
+    if (d->K <= 0 || d->N <= 0) return fail(QL_E_DIMS, "GPTQ: in/out features must be positive");
+    uint64_t qw, qz, sc;
+    ql_gptq_sizes(d->K, d->N, d->group, &qw, &qz, &sc);
+    if (!in_range(d->qweight_off, qw, arena_bytes))
+        return fail(QL_E_QWEIGHT_SHORT, "GPTQ: qweight needs %llu bytes at offset %llu, arena has %llu",
+                    (unsigned long long)qw, (unsigned long long)d->qweight_off,
+                    (unsigned long long)arena_bytes);
+    if (!in_range(d->scales_off, sc, arena_bytes))
+        return fail(QL_E_SCALES_SHORT, "GPTQ: scales need %llu bytes at offset %llu, arena has %llu",
+                    (unsigned long long)sc, (unsigned long long)d->scales_off,
+                    (unsigned long long)arena_bytes);
+    if (d->qzeros_off != QL_NONE && !in_range(d->qzeros_off, qz, arena_bytes))
+        return fail(QL_E_QZEROS_SHORT, "GPTQ: qzeros need %llu bytes at offset %llu, arena has %llu",
+                    (unsigned long long)qz, (unsigned long long)d->qzeros_off,
+                    (unsigned long long)arena_bytes);
+    if (d->group % 8 != 0)
+        return fail(QL_E_GROUP_PACK, "GPTQ: group size %d must be a multiple of 8", d->group);
+    if (d->bias_off != QL_NONE && !in_range(d->bias_off, (uint64_t)d->N * 4, arena_bytes))
+        return fail(QL_E_RANGE, "bias [N] f32 outside the weight arena");
+    if (d->qweight_off % 4 || (d->qzeros_off != QL_NONE && d->qzeros_off % 4) || d->scales_off % 2 ||
+        (d->bias_off != QL_NONE && d->bias_off % 4))
+        return fail(QL_E_ALIGN, "misaligned GPTQ tensor offset (int32/f32: 4 B, f16: 2 B)");
+    return QL_OK;
+}
+
+int check_desc(const ql_gptq_desc* d, const ql_arena* w)
+{
+    if (!d || !w) return fail(QL_E_INVALID, "null descriptor or weight arena");
+    return validate_desc(d, w->size);
+}
+
+ql::GemvLinear make_linear(const ql_gptq_desc* d, const ql_arena* w)
+{
+    ql::GemvLinear L{};
+    L.qweight = reinterpret_cast<const uint32_t*>(w->base + d->qweight_off);
+    L.qzeros = d->qzeros_off == QL_NONE ? nullptr
+                                        : reinterpret_cast<const uint32_t*>(w->base + d->qzeros_off);
+    L.scales = reinterpret_cast<const uint16_t*>(w->base + d->scales_off);
+    L.bias = d->bias_off == QL_NONE ? nullptr : reinterpret_cast<const float*>(w->base + d->bias_off);
+    L.N = d->N;
+    L.K = d->K;
+    L.group = d->group;
+    L.split = 1;
+    return L;
+}
+
+bool gemv_aligned(const ql_gptq_desc* d, uint64_t x_off)
+{
+    return d->qweight_off % 16 == 0 && d->scales_off % 8 == 0 && x_off % 16 == 0;
+}
+
+int check_io(const ql_gptq_desc* d, const ql_arena* act, uint64_t x_off, int x_dtype, int M,
+             uint64_t y_off)
+{
+    if (x_dtype != QL_DTYPE_F32 && x_dtype != QL_DTYPE_F16)
+        return fail(QL_E_INVALID, "x_dtype must be QL_DTYPE_F32 or QL_DTYPE_F16");
+    if (M <= 0 || M > (1 << 20)) return fail(QL_E_INVALID, "M out of range (%d)", M);
+    const uint64_t es = x_dtype == QL_DTYPE_F32 ? 4 : 2;
+    if (!in_range(x_off, (uint64_t)M * d->K * es, act->size))
+        return fail(QL_E_RANGE, "x [M,K] outside the activation arena");
+    if (!in_range(y_off, (uint64_t)M * d->N * 4, act->size))
+        return fail(QL_E_RANGE, "y [M,N] outside the activation arena");
+    if (x_off % es || y_off % 4) return fail(QL_E_ALIGN, "misaligned x or y offset");
+    return QL_OK;
+}
+
+int set_device(ql_ctx* ctx)
+{
+    QL_HIP(hipSetDevice(ctx->device));
+    return QL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ql_last_error(void) { return g_err; }
+
+int ql_create(int device, ql_ctx** out)
+{
+    if (!out) return fail(QL_E_INVALID, "null output pointer");
+    *out = nullptr;
+    int n = 0;
+    QL_HIP(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(QL_E_INVALID, "device %d not present (%d devices)", device, n);
+    QL_HIP(hipSetDevice(device));
+    ql_ctx* c = new ql_ctx();
+    c->device = device;
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) { delete c; return hip_fail(e, "hipGetDeviceProperties"); }
+    c->cu_count = prop.multiProcessorCount;
+    c->hbm_bytes = prop.totalGlobalMem;
+    snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
+    if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
+        delete c;
+        return hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    if ((e = hipMalloc(&c->counters, sizeof(uint32_t) * ql::kCounterCapacity)) != hipSuccess ||
+        (e = hipMemset(c->counters, 0, sizeof(uint32_t) * ql::kCounterCapacity)) != hipSuccess ||
+        (e = hipEventCreate(&c->ev_start)) != hipSuccess ||
+        (e = hipEventCreate(&c->ev_stop)) != hipSuccess) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return hip_fail(e, "ql_create");
+    }
+    *out = c;
+    return QL_OK;
+}
+
+int ql_destroy(ql_ctx* ctx)
+{
+    if (!ctx) return fail(QL_E_INVALID, "null context");
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipEventDestroy(ctx->ev_start);
+    (void)hipEventDestroy(ctx->ev_stop);
+    (void)hipFree(ctx->counters);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return QL_OK;
+}
+
+int ql_device_info(ql_ctx* ctx, char* name, int name_len, int* cu_count, uint64_t* hbm_bytes)
+{
+    if (!ctx) return fail(QL_E_INVALID, "null context");
+    if (name && name_len > 0) snprintf(name, (size_t)name_len, "%s", ctx->name);
+    if (cu_count) *cu_count = ctx->cu_count;
+    if (hbm_bytes) *hbm_bytes = ctx->hbm_bytes;
+    return QL_OK;
+}
+
+int ql_arena_reserve(ql_ctx* ctx, uint64_t bytes, ql_arena** out)
+{
+    if (!ctx || !out) return fail(QL_E_INVALID, "null context or output pointer");
+    if (bytes == 0) return fail(QL_E_INVALID, "arena size must be positive");
+    if (ctx->capturing) return fail(QL_E_STATE, "cannot allocate during graph capture");
+    *out = nullptr;
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    void* p = nullptr;
+    QL_HIP(hipMalloc(&p, bytes));
+    ql_arena* a = new ql_arena();
+    a->ctx = ctx;
+    a->base = static_cast<char*>(p);
+    a->size = bytes;
+    *out = a;
+    return QL_OK;
+}
+
+int ql_arena_release(ql_arena* arena)
+{
+    if (!arena) return fail(QL_E_INVALID, "null arena");
+    (void)hipSetDevice(arena->ctx->device);
+    (void)hipStreamSynchronize(arena->ctx->stream);
+    (void)hipFree(arena->base);
+    delete arena;
+    return QL_OK;
+}
+
+uint64_t ql_arena_size(const ql_arena* arena) { return arena ? arena->size : 0; }
+
+uint64_t ql_arena_device_ptr(const ql_arena* arena)
+{
+    return arena ? (uint64_t)(uintptr_t)arena->base : 0;
+}
+
+int ql_arena_write(ql_arena* arena, uint64_t off, const void* src, uint64_t bytes)
+{
+    if (!arena || (!src && bytes)) return fail(QL_E_INVALID, "null arena or source");
+    if (arena->ctx->capturing) return fail(QL_E_STATE, "synchronous copy during graph capture");
+    if (!in_range(off, bytes, arena->size)) return fail(QL_E_RANGE, "write outside the arena");
+    if (!bytes) return QL_OK;
+    int rc = set_device(arena->ctx);
+    if (rc) return rc;
+    QL_HIP(hipStreamSynchronize(arena->ctx->stream));
+    QL_HIP(hipMemcpy(arena->base + off, src, bytes, hipMemcpyHostToDevice));
+    return QL_OK;
+}
+
+int ql_arena_read(ql_arena* arena, uint64_t off, void* dst, uint64_t bytes)
+{
+    if (!arena || (!dst && bytes)) return fail(QL_E_INVALID, "null arena or destination");
+    if (arena->ctx->capturing) return fail(QL_E_STATE, "synchronous copy during graph capture");
+    if (!in_range(off, bytes, arena->size)) return fail(QL_E_RANGE, "read outside the arena");
+    if (!bytes) return QL_OK;
+    int rc = set_device(arena->ctx);
+    if (rc) return rc;
+    QL_HIP(hipStreamSynchronize(arena->ctx->stream));
+    QL_HIP(hipMemcpy(dst, arena->base + off, bytes, hipMemcpyDeviceToHost));
+    return QL_OK;
+}
+
+int ql_arena_copy(ql_ctx* ctx, ql_arena* dst, uint64_t dst_off, const ql_arena* src,
+                  uint64_t src_off, uint64_t bytes)
+{
+    if (!ctx || !dst || !src) return fail(QL_E_INVALID, "null context or arena");
+    if (!in_range(dst_off, bytes, dst->size) || !in_range(src_off, bytes, src->size))
+        return fail(QL_E_RANGE, "copy outside an arena");
+    if (!bytes) return QL_OK;
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(hipMemcpyAsync(dst->base + dst_off, src->base + src_off, bytes,
+                          hipMemcpyDeviceToDevice, ctx->stream));
+    return QL_OK;
+}
+
+int ql_gptq_sizes(int32_t K, int32_t N, int32_t group, uint64_t* qweight_bytes,
+                  uint64_t* qzeros_bytes, uint64_t* scales_bytes)
+{
+    if (K <= 0 || N <= 0) return fail(QL_E_DIMS, "GPTQ: in/out features must be positive");
+    if (group <= 0) return fail(QL_E_GROUP, "GPTQ: group size must be positive");
+    const uint64_t pack_rows = ((uint64_t)K + 7) / 8;
+    const uint64_t pack_cols = ((uint64_t)N + 7) / 8;
+    const uint64_t groups = ((uint64_t)K + group - 1) / (uint64_t)group;
+    if (qweight_bytes) *qweight_bytes = pack_rows * (uint64_t)N * 4;
+    if (qzeros_bytes) *qzeros_bytes = groups * pack_cols * 4;
+    if (scales_bytes) *scales_bytes = groups * (uint64_t)N * 2;
+    return QL_OK;
+}
+
+int ql_gptq_validate(const ql_gptq_desc* desc, uint64_t arena_bytes)
+{
+    return validate_desc(desc, arena_bytes);
+}
+
+int ql_gptq_check(const ql_gptq_desc* desc, const ql_arena* weights)
+{
+    return check_desc(desc, weights);
+}
+
+int ql_unpack_f16(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_arena* out,
+                  uint64_t out_off)
+{
+    if (!ctx || !out) return fail(QL_E_INVALID, "null context or output arena");
+    int rc = check_desc(d, weights);
+    if (rc) return rc;
+    if (!in_range(out_off, (uint64_t)d->N * d->K * 2, out->size))
+        return fail(QL_E_RANGE, "fp16 [N,K] output outside the arena");
+    if (out_off % 2) return fail(QL_E_ALIGN, "fp16 output offset must be 2-byte aligned");
+    const int P = (d->K + 7) / 8;
+    if (P > 65535) return fail(QL_E_INVALID, "K too large (%d)", d->K);
+    if ((rc = set_device(ctx))) return rc;
+    ql::UnpackArgs a;
+    a.qweight = reinterpret_cast<const uint32_t*>(weights->base + d->qweight_off);
+    a.qzeros = d->qzeros_off == QL_NONE ? nullptr
+                                        : reinterpret_cast<const uint32_t*>(weights->base + d->qzeros_off);
+    a.scales = reinterpret_cast<const uint16_t*>(weights->base + d->scales_off);
+    a.out = reinterpret_cast<uint16_t*>(out->base + out_off);
+    a.N = d->N;
+    a.K = d->K;
+    a.group = d->group;
+    const bool fast = d->N % 4 == 0 && d->K % 8 == 0 && d->qweight_off % 16 == 0 &&
+                      d->scales_off % 8 == 0 && out_off % 16 == 0;
+    QL_HIP(ql::launch_unpack(a, fast, ctx->stream));
+    return QL_OK;
+}
+
+int ql_plan_linear(int32_t M, int32_t N, int32_t K, int32_t group, ql_plan* out)
+{
+    if (!out) return fail(QL_E_INVALID, "null plan pointer");
+    return plan_impl(M, N, K, group, out);
+}
+
+int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act,
+              uint64_t x_off, int32_t x_dtype, int32_t M, uint64_t y_off, uint64_t scratch_off)
+{
+    if (!ctx || !act) return fail(QL_E_INVALID, "null context or activation arena");
+    int rc = check_desc(d, weights);
+    if (rc) return rc;
+    if ((rc = check_io(d, act, x_off, x_dtype, M, y_off))) return rc;
+    ql_plan p;
+    if ((rc = plan_impl(M, d->N, d->K, d->group, &p))) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    ql::GemvLinear L = make_linear(d, weights);
+    L.x = act->base + x_off;
+    L.y = reinterpret_cast<float*>(act->base + y_off);
+
+    if (p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(d, x_off)) {
+        if (!in_range(scratch_off, p.scratch_bytes, act->size))
+            return fail(QL_E_RANGE, "scratch (%llu bytes) outside the activation arena",
+                        (unsigned long long)p.scratch_bytes);
+        if (scratch_off % 16) return fail(QL_E_ALIGN, "scratch offset must be 16-byte aligned");
+        const ql::GemvShape s = ql::gemv_shape(M, d->N, d->K, d->group);
+        ql::GemvBatch b{};
+        L.split = s.split;
+        L.strips = s.strips;
+        L.wg_begin = 0;
+        L.xs_owner = 1;
+        L.xs = reinterpret_cast<const uint4*>(act->base + scratch_off);
+        L.partial = reinterpret_cast<float*>(act->base + scratch_off + ql::gemv_xs_bytes(M, d->K));
+        L.counters = ctx->counters;
+        if (s.strips > ql::kCounterCapacity) return fail(QL_E_INVALID, "N too large");
+        b.L[0] = L;
+        b.count = 1;
+        b.M = M;
+        b.x_dtype = x_dtype;
+        b.wg_total = s.strips * s.split;
+        QL_HIP(ql::launch_gemv_batch(b, ctx->stream));
+        return QL_OK;
+    }
+    if (p.kind == QL_KIND_GEMV_MFMA || p.kind == QL_KIND_GEMV_SIMPLE) {
+        QL_HIP(ql::launch_gemv_simple(L, M, x_dtype, ctx->stream));
+        return QL_OK;
+    }
+    ql::GemmArgs g;
+    g.qweight = L.qweight;
+    g.qzeros = L.qzeros;
+    g.scales = L.scales;
+    g.bias = L.bias;
+    g.x = L.x;
+    g.y = L.y;
+    g.M = M;
+    g.N = d->N;
+    g.K = d->K;
+    g.group = d->group;
+    g.x_dtype = x_dtype;
+    if (p.kind == QL_KIND_GEMM_MFMA && x_off % 16 == 0) {
+        QL_HIP(ql::launch_gemm(g, ctx->stream));
+    } else {
+        QL_HIP(ql::launch_gemm_simple(g, ctx->stream));
+    }
+    return QL_OK;
+}
+
+int ql_plan_batch(int32_t count, const ql_gptq_desc* descs, int32_t M, uint64_t* scratch_bytes)
+{
+    if (!descs || !scratch_bytes || count <= 0 || count > ql::kMaxBatch)
+        return fail(QL_E_INVALID, "batch needs 1..%d descriptors", ql::kMaxBatch);
+    uint64_t total = 0;
+    for (int i = 0; i < count; i++) {
+        ql_plan p;
+        int rc = plan_impl(M, descs[i].N, descs[i].K, descs[i].group, &p);
+        if (rc) return rc;
+        total += align256(p.scratch_bytes);
+    }
+    *scratch_bytes = total;
+    return QL_OK;
+}
+
+int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
+                    const ql_arena* weights, ql_arena* act, const uint64_t* x_offs,
+                    int32_t x_dtype, int32_t M, const uint64_t* y_offs, uint64_t scratch_off)
+{
+    if (!ctx || !descs || !act || !x_offs || !y_offs || count <= 0 || count > ql::kMaxBatch)
+        return fail(QL_E_INVALID, "batch needs a context, arenas and 1..%d linears", ql::kMaxBatch);
+    uint64_t total = 0;
+    int rc = ql_plan_batch(count, descs, M, &total);
+    if (rc) return rc;
+    if (!in_range(scratch_off, total, act->size))
+        return fail(QL_E_RANGE, "batch scratch (%llu bytes) outside the activation arena",
+                    (unsigned long long)total);
+    if (scratch_off % 16) return fail(QL_E_ALIGN, "scratch offset must be 16-byte aligned");
+    bool fused = true;
+    for (int i = 0; i < count; i++) {
+        if ((rc = check_desc(&descs[i], weights))) return rc;
+        if ((rc = check_io(&descs[i], act, x_offs[i], x_dtype, M, y_offs[i]))) return rc;
+        ql_plan p;
+        plan_impl(M, descs[i].N, descs[i].K, descs[i].group, &p);
+        fused &= p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(&descs[i], x_offs[i]);
+    }
+    if (!fused) {
+        uint64_t off = scratch_off;
+        for (int i = 0; i < count; i++) {
+            ql_plan p;
+            plan_impl(M, descs[i].N, descs[i].K, descs[i].group, &p);
+            if ((rc = ql_linear(ctx, &descs[i], weights, act, x_offs[i], x_dtype, M, y_offs[i], off)))
+                return rc;
+            off += align256(p.scratch_bytes);
+        }
+        return QL_OK;
+    }
+    if ((rc = set_device(ctx))) return rc;
+    ql::GemvBatch b{};
+    b.count = count;
+    b.M = M;
+    b.x_dtype = x_dtype;
+    uint64_t off = scratch_off;
+    int wg = 0, counter_base = 0;
+    for (int i = 0; i < count; i++) {
+        const ql_gptq_desc* d = &descs[i];
+        const ql::GemvShape s = ql::gemv_shape(M, d->N, d->K, d->group);
+        ql::GemvLinear L = make_linear(d, weights);
+        L.x = act->base + x_offs[i];
+        L.y = reinterpret_cast<float*>(act->base + y_offs[i]);
+        L.split = s.split;
+        L.strips = s.strips;
+        L.wg_begin = wg;
+        // linears reading the same x with the same K share one split-activation buffer
+        int owner = -1;
+        for (int k = 0; k < i; k++)
+            if (x_offs[k] == x_offs[i] && descs[k].K == d->K) { owner = k; break; }
+        L.xs_owner = owner < 0;
+        L.xs = owner < 0 ? reinterpret_cast<const uint4*>(act->base + off) : b.L[owner].xs;
+        L.partial = reinterpret_cast<float*>(act->base + off + ql::gemv_xs_bytes(M, d->K));
+        L.counters = ctx->counters + counter_base;
+        counter_base += s.strips;
+        if (counter_base > ql::kCounterCapacity) return fail(QL_E_INVALID, "batch too wide");
+        off += align256(ql::gemv_xs_bytes(M, d->K) + ql::gemv_partial_bytes(M, d->N, s.split));
+        wg += s.strips * s.split;
+        b.L[i] = L;
+    }
+    b.wg_total = wg;
+    QL_HIP(ql::launch_gemv_batch(b, ctx->stream));
+    return QL_OK;
+}
+
+int ql_sync(ql_ctx* ctx)
+{
+    if (!ctx) return fail(QL_E_INVALID, "null context");
+    if (ctx->capturing) return fail(QL_E_STATE, "ql_sync during graph capture");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(hipStreamSynchronize(ctx->stream));
+    return QL_OK;
+}
+
+int ql_timer_start(ql_ctx* ctx)
+{
+    if (!ctx) return fail(QL_E_INVALID, "null context");
+    if (ctx->capturing) return fail(QL_E_STATE, "timer during graph capture");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(hipEventRecord(ctx->ev_start, ctx->stream));
+    return QL_OK;
+}
+
+int ql_timer_stop(ql_ctx* ctx, float* elapsed_ms)
+{
+    if (!ctx || !elapsed_ms) return fail(QL_E_INVALID, "null context or output");
+    if (ctx->capturing) return fail(QL_E_STATE, "timer during graph capture");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(hipEventRecord(ctx->ev_stop, ctx->stream));
+    QL_HIP(hipEventSynchronize(ctx->ev_stop));
+    QL_HIP(hipEventElapsedTime(elapsed_ms, ctx->ev_start, ctx->ev_stop));
+    return QL_OK;
+}
+
+int ql_graph_begin(ql_ctx* ctx)
+{
+    if (!ctx) return fail(QL_E_INVALID, "null context");
+    if (ctx->capturing) return fail(QL_E_STATE, "capture already active");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    return QL_OK;
+}
+
+int ql_graph_end(ql_ctx* ctx, ql_graph** out)
+{
+    if (!ctx || !out) return fail(QL_E_INVALID, "null context or output");
+    if (!ctx->capturing) return fail(QL_E_STATE, "no capture active");
+    *out = nullptr;
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    QL_HIP(hipStreamEndCapture(ctx->stream, &g));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    ql_graph* gr = new ql_graph();
+    gr->graph = g;
+    gr->exec = exec;
+    *out = gr;
+    return QL_OK;
+}
+
+int ql_graph_launch(ql_ctx* ctx, ql_graph* graph)
+{
+    if (!ctx || !graph) return fail(QL_E_INVALID, "null context or graph");
+    if (ctx->capturing) return fail(QL_E_STATE, "graph launch during capture");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(hipGraphLaunch(graph->exec, ctx->stream));
+    return QL_OK;
+}
+
+int ql_graph_destroy(ql_graph* graph)
+{
+    if (!graph) return fail(QL_E_INVALID, "null graph");
+    (void)hipGraphExecDestroy(graph->exec);
+    (void)hipGraphDestroy(graph->graph);
+    delete graph;
+    return QL_OK;
+}
+
+}  // extern "C"

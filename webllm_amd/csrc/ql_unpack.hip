@@ -1,0 +1,106 @@
+// Load-time unpack: GPTQ int4 -> fp16 [N, K] row-major, bit-identical to the reference loader's
+// f32ToF16Bits(dequantizeGptqInt4(...)) (src/weights/quant.ts:42-118, src/gpu/buffer.ts:57-100).
+//
+// HBM-bound (read K*N/2 + scales/zeros, write 2*K*N bytes). The fast kernel reads a 16-packed-row
+// x 64-column tile of qweight with 16-byte loads along N (the GPTQ layout is contiguous along N),
+// dequantizes in packed fp16, transposes through LDS and writes 256 contiguous bytes per output
+// row segment. The generic kernel covers any K, N and alignment, one packed word per lane.
+#include "ql_device.h"
+#include "ql_internal.h"
+
+namespace ql {
+
+namespace {
+
+constexpr int kTileRows = 16;  // packed rows (128 k)
+constexpr int kTileCols = 64;  // output rows n
+constexpr int kPad = 17;       // LDS row pitch in 16-byte chunks (16 + 1 against bank conflicts)
+
+__global__ __launch_bounds__(256) void unpack_tile_kernel(UnpackArgs a)
+{
+    __shared__ uint4 tile[kTileCols * kPad];
+    const int t = threadIdx.x;
+    const int n0 = blockIdx.x * kTileCols;
+    const int p0 = blockIdx.y * kTileRows;
+    const int P = a.K >> 3;               // K % 8 == 0 on this path
+    const int NC = (a.N + 7) >> 3;
+
+    const int r = t >> 4;                 // packed row within tile
+    const int cq = t & 15;                // column quad
+    const int p = p0 + r;
+    const int n = n0 + 4 * cq;
+    if (p < P && n < a.N) {               // N % 4 == 0: the whole quad is in range
+        const uint4 w = *reinterpret_cast<const uint4*>(a.qweight + (size_t)p * a.N + n);
+        const int g = (p * 8) / a.group;
+        const uint2 sv = *reinterpret_cast<const uint2*>(a.scales + (size_t)g * a.N + n);
+        uint32_t z[4];
+        if (a.qzeros) {
+            const uint32_t zw = a.qzeros[(size_t)g * NC + (n >> 3)] >> (4 * (n & 7));
+#pragma unroll
+            for (int u = 0; u < 4; u++) z[u] = ((zw >> (4 * u)) & 15u) + 1u;
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; u++) z[u] = 8u;
+        }
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+        const uint32_t s2[4] = {(sv.x & 0xffffu) * 0x10001u, (sv.x >> 16) * 0x10001u,
+                                (sv.y & 0xffffu) * 0x10001u, (sv.y >> 16) * 0x10001u};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const f16x8 h = dequant_word_natural(words[u], zero_pair(z[u]), s2[u]);
+            tile[(4 * cq + u) * kPad + r] = __builtin_bit_cast(uint4, h);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = t + 256 * i;        // chunk: column c/16, packed row c%16
+        const int col = c >> 4;
+        const int rr = c & 15;
+        const int nn = n0 + col;
+        const int pp = p0 + rr;
+        if (nn < a.N && pp < P) {
+            *reinterpret_cast<uint4*>(a.out + (size_t)nn * a.K + (size_t)pp * 8) =
+                tile[col * kPad + rr];
+        }
+    }
+}
+
+// Any shape: lane = one packed word (p, n); up to 8 fp16 stores with the reference's K tail.
+__global__ __launch_bounds__(256) void unpack_generic_kernel(UnpackArgs a)
+{
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int p = blockIdx.y;
+    if (n >= a.N) return;
+    const int NC = (a.N + 7) >> 3;
+    const int g = (p * 8) / a.group;
+    const uint32_t w = a.qweight[(size_t)p * a.N + n];
+    const uint32_t z = zero_of(a.qzeros, g, NC, n);
+    const _Float16 s = __builtin_bit_cast(_Float16, a.scales[(size_t)g * a.N + n]);
+    const float sf = (float)s;
+    for (int k = 0; k < 8; k++) {
+        const int i = p * 8 + k;
+        if (i >= a.K) break;
+        const int q = (int)((w >> (4 * k)) & 15u);
+        // (q - z) * s is exact in fp32 (at most 16 significant bits); one RNE rounding to fp16.
+        const _Float16 h = (_Float16)((float)(q - (int)z) * sf);
+        a.out[(size_t)n * a.K + i] = __builtin_bit_cast(uint16_t, h);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_unpack(const UnpackArgs& a, bool fast, hipStream_t stream)
+{
+    const int P = (a.K + 7) / 8;
+    if (fast) {
+        dim3 grid((a.N + kTileCols - 1) / kTileCols, (P + kTileRows - 1) / kTileRows);
+        hipLaunchKernelGGL(unpack_tile_kernel, grid, dim3(256), 0, stream, a);
+    } else {
+        dim3 grid((a.N + 255) / 256, P);
+        hipLaunchKernelGGL(unpack_generic_kernel, grid, dim3(256), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace ql
