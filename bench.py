@@ -1,0 +1,387 @@
+#!/usr/bin/env python3
+"""Benchmark of the GPTQ int4 quantized-linear hot path on one MI355X.
+
+Headline (BASELINE.json metric): microseconds per Qwen2.5-0.5B-shaped decode step — 168 GPTQ
+int4 linears (24 layers x q,k,v,o,gate,up,down; group 128), M = 1, fp32 activations, weights
+resident in HBM. The step is issued the way the model's data dependencies allow: per layer
+{q,k,v} on one input, {o}, {gate,up} on one input, {down} — 96 launches, captured once into a
+HIP graph; one step = one graph replay. Inputs are synthetic (random nibbles, zero 8, fp16 scales
+|N(0,1)|*0.01, x ~ N(0,1)); no checkpoint is available offline.
+
+Also measured (reported under "extra"): the same step with the 256 MB MALL flushed before each
+step; the 7B-shaped step (140 linears, 3.34 GB, HBM-bound) at M = 1, 4, 16; the M sweep
+{1,2,4,8,16}; prefill GEMM at M = 128, 512 (TFLOP/s); the load-time unpack of all 168 tensors.
+The CPU baseline is the reference CPU path (dequantizeGptqInt4 + gemmNTRef) restated for Node,
+run single-threaded on this host on layer 0 of the same inputs and scaled to a whole step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from webllm_amd import qlinear as ql  # noqa: E402
+from webllm_amd import synth  # noqa: E402
+
+METRIC = "int4 dequant-GEMV µs per Qwen-0.5B decode step; achieved HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+F16_PEAK_TFLOPS = 2500.0
+GROUP = 128
+
+LAYER_LAUNCHES_05B = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
+LAYER_LAUNCHES_7B = [("q",), ("o",), ("gate", "up"), ("down",)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def linear_bytes(K, N, M):
+    """Algorithmic HBM bytes of one linear: packed weights, zeros, scales, x and y."""
+    return K * N // 2 + K * N // 256 + K * N // 64 + M * K * 4 + M * N * 4
+
+
+class Model:
+    """All linears of one model shape packed into a single weight arena."""
+
+    def __init__(self, ctx, shape: str, seed: int):
+        self.shape = shape
+        self.linears = synth.model_linears(shape)
+        self.layers = synth.QWEN05_LAYERS if shape == "0.5b" else synth.QWEN7_LAYERS
+        lay = ql.ArenaLayout()
+        self.descs = {}
+        self.tensors_for_cpu = {}
+        plan = []
+        for (layer, proj, K, N) in self.linears:
+            qw, qz, sc = ql.gptq_sizes(K, N, GROUP)
+            offs = (lay.take(qw), lay.take(qz), lay.take(sc))
+            plan.append((layer, proj, K, N, offs))
+        self.arena = ctx.arena(lay.used)
+        self.weight_bytes = 0
+        for (layer, proj, K, N, offs) in plan:
+            t = synth.gptq_linear(K, N, GROUP, seed=seed, key=(layer, synth.PROJ_INDEX[proj]))
+            self.arena.write(offs[0], t.qweight)
+            self.arena.write(offs[1], t.qzeros)
+            self.arena.write(offs[2], t.scales)
+            self.weight_bytes += t.nbytes
+            self.descs[(layer, proj)] = ql.make_desc(offs[0], offs[1], offs[2], K, N, GROUP)
+            if layer == 0:
+                self.tensors_for_cpu[proj] = t
+        self.shapes = {(l, p): (K, N) for (l, p, K, N) in self.linears}
+
+
+class Step:
+    """One decode (or prefill) step over a Model: launch groups, activations, scratch, graph."""
+
+    def __init__(self, ctx, model: Model, M: int, x_dtype: int = ql.DTYPE_F32, seed: int = 0x5EED):
+        self.ctx, self.model, self.M, self.x_dtype = ctx, model, M, x_dtype
+        groups = LAYER_LAUNCHES_05B if model.shape == "0.5b" else LAYER_LAUNCHES_7B
+        es = 4 if x_dtype == ql.DTYPE_F32 else 2
+        lay = ql.ArenaLayout()
+        self.launches = []
+        for layer in range(model.layers):
+            for gi, projs in enumerate(groups):
+                descs = [model.descs[(layer, p)] for p in projs]
+                K = descs[0].K
+                x_off = lay.take(M * K * es)
+                y_offs = [lay.take(M * d.N * 4) for d in descs]
+                scratch = ql.plan_batch(descs, M)
+                s_off = lay.take(max(scratch, 16))
+                self.launches.append((layer, gi, projs, descs, x_off, y_offs, s_off))
+        self.act = ctx.arena(lay.used)
+        for (layer, gi, projs, descs, x_off, _, _) in self.launches:
+            x = synth.activations(M, descs[0].K, seed=seed, key=(layer, gi, M))
+            if x_dtype == ql.DTYPE_F16:
+                x = x.astype(np.float16).view(np.uint16)
+            self.act.write(x_off, x)
+        self.bytes = sum(linear_bytes(model.shapes[(l, p)][0], model.shapes[(l, p)][1], M)
+                         for (l, p, _, _) in model.linears)
+        self.flops = sum(2 * M * K * N for (_, _, K, N) in model.linears)
+        self.graph = None
+
+    def issue(self):
+        for (_, _, projs, descs, x_off, y_offs, s_off) in self.launches:
+            if len(descs) == 1:
+                self.ctx.linear(descs[0], self.model.arena, self.act, x_off, self.x_dtype, self.M,
+                                y_offs[0], s_off)
+            else:
+                self.ctx.linear_batch(descs, self.model.arena, self.act, [x_off] * len(descs),
+                                      self.x_dtype, self.M, y_offs, s_off)
+
+    def capture(self):
+        self.issue()                      # eager run first (validates every launch)
+        self.ctx.sync()
+        self.ctx.graph_begin()
+        self.issue()
+        self.graph = self.ctx.graph_end()
+
+    def run(self, steps: int) -> float:
+        """Issues `steps` graph replays between two events; returns total milliseconds."""
+        self.ctx.sync()
+        self.ctx.timer_start()
+        for _ in range(steps):
+            self.graph.launch()
+        return self.ctx.timer_stop()
+
+    def release(self):
+        if self.graph:
+            self.graph.destroy()
+        self.act.release()
+
+
+def timed(step: Step, steps: int, warmup: int) -> float:
+    if step.graph is None:
+        step.capture()
+    if warmup:
+        step.run(warmup)
+    return step.run(steps) / steps
+
+
+def flushed_step_ms(ctx, step: Step, reps: int = 5) -> float:
+    """Step time with the MALL (256 MB) evicted first: a 1 GiB device copy precedes each step."""
+    flush = ctx.arena(1 << 30)
+    times = []
+    for _ in range(reps):
+        ctx.copy(flush, 0, flush, 1 << 29, 1 << 29)
+        ctx.sync()
+        times.append(step.run(1))
+    flush.release()
+    return float(np.median(times))
+
+
+def unpack_all(ctx, model: Model, steps: int):
+    lay = ql.ArenaLayout()
+    offs = {k: lay.take(d.N * d.K * 2) for k, d in model.descs.items()}
+    out = ctx.arena(lay.used)
+
+    def issue():
+        for k, d in model.descs.items():
+            ctx.unpack_f16(d, model.arena, out, offs[k])
+
+    issue()
+    ctx.sync()
+    ctx.graph_begin()
+    issue()
+    g = ctx.graph_end()
+    g.launch()
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(steps):
+        g.launch()
+    ms = ctx.timer_stop() / steps
+    g.destroy()
+    out.release()
+    read = model.weight_bytes
+    write = sum(d.N * d.K * 2 for d in model.descs.values())
+    return ms, read + write
+
+
+def cpu_baseline(model: Model, step: Step, min_seconds: float):
+    """Reference CPU path (Node restatement, oracle/js) on layer 0 of the same inputs."""
+    node = shutil.which("node")
+    t0_layer = [l for l in step.launches if l[0] == 0]
+    with tempfile.TemporaryDirectory() as d:
+        meta = {"linears": []}
+        gpu_y = []
+        for (layer, gi, projs, descs, x_off, y_offs, s_off) in t0_layer:
+            x = step.act.read(x_off, (step.M, descs[0].K), np.float32)
+            for p, desc, yo in zip(projs, descs, y_offs):
+                t = model.tensors_for_cpu[p]
+                i = len(meta["linears"])
+                t.qweight.tofile(os.path.join(d, f"qw_{i}"))
+                t.qzeros.tofile(os.path.join(d, f"qz_{i}"))
+                t.scales.tofile(os.path.join(d, f"sc_{i}"))
+                x.tofile(os.path.join(d, f"x_{i}"))
+                meta["linears"].append({"K": t.K, "N": t.N, "group": GROUP, "M": step.M,
+                                        "qweight": f"qw_{i}", "qzeros": f"qz_{i}",
+                                        "scales": f"sc_{i}", "x": f"x_{i}"})
+                gpu_y.append(step.act.read(yo, (step.M, desc.N), np.float32))
+        json.dump(meta, open(os.path.join(d, "meta.json"), "w"))
+        macs = sum(l["M"] * l["K"] * l["N"] for l in meta["linears"])
+        if node:
+            r = subprocess.run([node, os.path.join(ROOT, "oracle", "js", "gptq_ref.js"), d,
+                                str(min_seconds)], capture_output=True, text=True, timeout=600)
+            if r.returncode != 0:
+                raise RuntimeError(f"node baseline failed: {r.stderr[-2000:]}")
+            res = json.loads(r.stdout.strip().splitlines()[-1])
+            cpu_y = [np.fromfile(os.path.join(d, f"y_{i}.f32"), dtype=np.float32)
+                     for i in range(len(gpu_y))]
+            kind_note = f"Node {res['node']} restatement of quant.ts dequantizeGptqInt4 + qwen-ref.ts gemmNTRef"
+        else:   # no Node on this host: the C oracle restatement of the same CPU path
+            from oracle import oracle as orc
+            t1 = time.perf_counter()
+            reps = 0
+            while True:
+                cpu_y = []
+                for l in meta["linears"]:
+                    t = model.tensors_for_cpu[[p for p in model.tensors_for_cpu
+                                               if model.tensors_for_cpu[p].K == l["K"] and
+                                               model.tensors_for_cpu[p].N == l["N"]][0]]
+                    x = np.fromfile(os.path.join(d, l["x"]), dtype=np.float32).reshape(l["M"], l["K"])
+                    cpu_y.append(orc.gptq_linear(t.qweight, t.qzeros, t.scales, x).reshape(-1))
+                reps += 1
+                if time.perf_counter() - t1 > min_seconds:
+                    break
+            res = {"matvec_ms": (time.perf_counter() - t1) * 1e3 / reps, "dequant_ms": None,
+                   "reps": reps, "cpu": "", "cpus": os.cpu_count()}
+            kind_note = "C oracle (node not found)"
+    rel = max(float(np.max(np.abs(g.reshape(-1) - c) / (1e-5 / 1e-4 + np.abs(c))))
+              for g, c in zip(gpu_y, cpu_y))
+    ok = all(np.all(np.abs(g.reshape(-1) - c) <= 1e-5 + 1e-4 * np.abs(c)) for g, c in zip(gpu_y, cpu_y))
+    per_step_us = res["matvec_ms"] * model.layers * 1e3
+    return {
+        "value": round(per_step_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
+        "sample": (f"layer 0 (7 linears, {macs/1e6:.1f} M MACs) matvec x {res['reps']} reps, "
+                   f"scaled x{model.layers} layers; dequant at load {res['dequant_ms']:.0f} ms "
+                   f"for layer 0 ({kind_note})" if res.get("dequant_ms") is not None else
+                   f"layer 0 matvec x {res['reps']} reps, scaled x{model.layers} ({kind_note})"),
+        "host_cpu": res.get("cpu", ""), "host_threads": res.get("cpus"),
+        "dequant_ms_layer0": None if res.get("dequant_ms") is None else round(res["dequant_ms"], 1),
+        "gpu_vs_cpu_ok": bool(ok), "gpu_vs_cpu_max_rel_atol": rel,
+    }
+
+
+def traffic_from_profiles(workload: str):
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return None
+    return json.load(open(p)).get(workload)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="all",
+                    help="all | step05 | step7b | sweep | prefill | unpack (profiling subsets)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus "
+              f"{args.gpus}. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    ctx = ql.Context(0)
+    info = ctx.info()
+    log(f"device: {info['name']} CUs={info['cu_count']}")
+    extra = {}
+    only = args.only
+
+    m05 = None
+    if only in ("all", "step05", "sweep", "prefill", "unpack"):
+        t0 = time.time()
+        m05 = Model(ctx, "0.5b", seed=0x9EF0)
+        log(f"0.5B weights: {m05.weight_bytes/1e6:.1f} MB uploaded in {time.time()-t0:.1f}s")
+
+    value = ms_step = None
+    roof = None
+    step1 = None
+    if only in ("all", "step05"):
+        step1 = Step(ctx, m05, 1)
+        ms_step = timed(step1, args.steps, args.warmup)
+        value = ms_step * 1e3
+        gbs = step1.bytes / (ms_step * 1e-3) / 1e9
+        n_launch = len(step1.launches)
+        log(f"0.5B step M=1: {value:.1f} us/step, {gbs:.0f} GB/s, {n_launch} launches")
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": traffic_from_profiles("step05_m1"),
+                "kernel": "gemv_mfma_kernel<1,4,true>",
+                "launches_per_step": n_launch,
+                "bytes_per_launch": step1.bytes // n_launch,
+                "avg_launch_us": round(value / n_launch, 3),
+                "note": "avg launch duration = event-timed graph replay / launches (includes "
+                        "inter-kernel gaps); the 0.5B weights (186 MB) fit the 256 MB MALL"}
+        flushed = flushed_step_ms(ctx, step1)
+        extra["step05_m1_flushed_us"] = round(flushed * 1e3, 1)
+        extra["step05_m1_flushed_gbs"] = round(step1.bytes / (flushed * 1e-3) / 1e9, 1)
+        log(f"0.5B step M=1 MALL-flushed: {flushed*1e3:.1f} us")
+
+    if only in ("all", "sweep"):
+        sweep = {}
+        for M in (1, 2, 4, 8, 16):
+            st = Step(ctx, m05, M)
+            ms = timed(st, max(10, args.steps // 2), 2)
+            sweep[str(M)] = {"us": round(ms * 1e3, 1), "gbs": round(st.bytes / (ms * 1e-3) / 1e9, 1)}
+            st.release()
+        extra["step05_m_sweep"] = sweep
+        log(f"M sweep: {sweep}")
+
+    if only in ("all", "prefill"):
+        pre = {}
+        for M in (128, 512):
+            st = Step(ctx, m05, M, x_dtype=ql.DTYPE_F16)
+            ms = timed(st, max(5, args.steps // 5), 2)
+            tf = st.flops / (ms * 1e-3) / 1e12
+            pre[str(M)] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 2),
+                           "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4)}
+            st.release()
+        extra["prefill05"] = pre
+        log(f"prefill: {pre}")
+
+    if only in ("all", "unpack"):
+        ms, nbytes = unpack_all(ctx, m05, max(5, args.steps // 5))
+        extra["unpack05"] = {"us": round(ms * 1e3, 1), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "bytes": nbytes}
+        log(f"unpack 168 tensors: {extra['unpack05']}")
+
+    cpu = None
+    if only in ("all", "step05") and not args.no_cpu:
+        cpu = cpu_baseline(m05, step1, args.cpu_seconds)
+        log(f"cpu baseline: {cpu}")
+
+    if step1 is not None:
+        step1.release()
+    if m05 is not None:
+        m05.arena.release()
+
+    if only in ("all", "step7b"):
+        t0 = time.time()
+        m7 = Model(ctx, "7b", seed=0x7B)
+        log(f"7B weights: {m7.weight_bytes/1e9:.2f} GB uploaded in {time.time()-t0:.1f}s")
+        s7 = {}
+        for M in (1, 4, 16):
+            st = Step(ctx, m7, M)
+            ms = timed(st, max(10, args.steps // 2), 2)
+            gbs = st.bytes / (ms * 1e-3) / 1e9
+            s7[str(M)] = {"us": round(ms * 1e3, 1), "gbs": round(gbs, 1),
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": st.bytes,
+                          "launches": len(st.launches)}
+            st.release()
+        extra["step7b"] = s7
+        log(f"7B step: {s7}")
+        m7.arena.release()
+
+    ctx.destroy()
+    if value is None:
+        print(json.dumps({"partial": only, "extra": extra}))
+        return
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "us/step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int4xf32", "data": "synthetic",
+        "config": {"workload": "Qwen2.5-0.5B-shaped decode step: 168 GPTQ int4 linears "
+                               "(group 128), M=1, fp32 activations, hipGraph replay",
+                   "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)",
+                   "launches_per_step": roof["launches_per_step"] if roof else None},
+        "roofline": roof, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

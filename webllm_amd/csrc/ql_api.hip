@@ -483,7 +483,8 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
         if ((rc = check_io(&descs[i], act, x_offs[i], x_dtype, M, y_offs[i]))) return rc;
         ql_plan p;
         plan_impl(M, descs[i].N, descs[i].K, descs[i].group, &p);
-        fused &= p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(&descs[i], x_offs[i]);
+        fused &= p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(&descs[i], x_offs[i]) &&
+                 descs[i].group == descs[0].group;
     }
     if (!fused) {
         uint64_t off = scratch_off;

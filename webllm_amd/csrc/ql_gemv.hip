@@ -30,6 +30,8 @@ namespace ql {
 namespace {
 
 constexpr int kTargetWaves = 4096;
+constexpr int kGemvFusedMaxM = 4;          // M <= 4: activations split in the kernel prologue
+constexpr int kGemvLdsXsBytes = 32768;     // LDS budget for that split (per workgroup)
 
 // x [M,K] (f32 or f16) -> split activations in the MFMA A-operand order:
 //   xs[(c * R + 2m + h)] = 8 fp16 values of row m, chunk c (k = 8c..8c+7) in perm_k order,
@@ -70,9 +72,10 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const GemvBatch b)
     dst[1] = __builtin_bit_cast(uint4, lo);
 }
 
-template <int T, int KBPG>
+template <int T, int KB, bool FUSED>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
 {
+    extern __shared__ uint4 xs_lds[];     // FUSED: split activations of this K segment
     __shared__ float red[kGemvWaves][kGemvMaxM][kGemvCols];
     __shared__ uint32_t is_last;
 
@@ -96,10 +99,61 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
     const int NC = (N + 7) >> 3;
     const int n = strip * kGemvCols + 4 * j;
     const bool col_ok = n < N;
-    const int kbpg = KBPG > 0 ? KBPG : (L.group >> 5);
-    const int G = L.K / L.group;
+    const int G = L.K / (KB * 32);
     const int g0 = (int)((int64_t)G * seg / L.split);
     const int g1 = (int)((int64_t)G * (seg + 1) / L.split);
+    const int p0 = g0 * KB * 4;           // first packed row (8-k chunk) of the segment
+
+    // software pipeline: the next group's packed words, zeros and scales are in flight while
+    // the current group is converted and multiplied
+    uint4 wn[KB];
+    uint32_t zn = 0x77777777u;
+    uint2 sn = uint2{0u, 0u};
+    auto fetch = [&](int g) {
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++)
+            wn[kb] = *reinterpret_cast<const uint4*>(L.qweight +
+                                                     (size_t)((g * KB + kb) * 4 + kq) * N + n);
+        if (L.qzeros) zn = L.qzeros[(size_t)g * NC + (n >> 3)];
+        sn = *reinterpret_cast<const uint2*>(L.scales + (size_t)g * N + n);
+    };
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) wn[kb] = uint4{0u, 0u, 0u, 0u};
+    int g = g0 + wave;
+    if (g < g1 && col_ok) fetch(g);
+
+    if (FUSED) {
+        // x [M,K] -> x_hi/x_lo fp16 in MFMA A-operand order, for this segment only
+        const int chunks = (g1 - g0) * KB * 4;
+        for (int idx = threadIdx.x; idx < chunks * M; idx += 256) {
+            const int c = idx / M;
+            const int m = idx - c * M;
+            float v[8];
+            const size_t base = (size_t)m * L.K + (size_t)(p0 + c) * 8;
+            if (b.x_dtype == 0) {
+                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(L.x) + base);
+                const float4 a0 = src[0], a1 = src[1];
+                v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+                v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+            } else {
+                const f16x8 h = __builtin_bit_cast(
+                    f16x8, *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(L.x) + base));
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = (float)h[e];
+            }
+            f16x8 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float xv = v[perm_k(e)];
+                const _Float16 h = (_Float16)xv;
+                hi[e] = h;
+                lo[e] = (_Float16)(xv - (float)h);
+            }
+            xs_lds[c * R + 2 * m] = __builtin_bit_cast(uint4, hi);
+            xs_lds[c * R + 2 * m + 1] = __builtin_bit_cast(uint4, lo);
+        }
+        __syncthreads();
+    }
 
     f32x4 acc[4][T];
 #pragma unroll
@@ -107,50 +161,46 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
 #pragma unroll
         for (int t = 0; t < T; t++) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int g = g0 + wave; g < g1; g += kGemvWaves) {
+    for (; g < g1; g += kGemvWaves) {
+        uint4 w[KB];
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) w[kb] = wn[kb];
+        const uint32_t zw = L.qzeros ? (zn >> (4 * (n & 7))) : 0x7777u;
+        const uint2 sv = sn;
+        if (g + kGemvWaves < g1 && col_ok) fetch(g + kGemvWaves);
+
         uint32_t zz[4];
         float s[4];
-        if (col_ok) {
-            const uint32_t zw = L.qzeros ? (L.qzeros[(size_t)g * NC + (n >> 3)] >> (4 * (n & 7)))
-                                         : 0x7777u;
-            const uint2 sv = *reinterpret_cast<const uint2*>(L.scales + (size_t)g * N + n);
-            const uint32_t sw[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
+        const uint32_t sw[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                zz[u] = zero_pair(((zw >> (4 * u)) & 15u) + 1u);
-                s[u] = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < 4; u++) { zz[u] = zero_pair(8u); s[u] = 0.f; }
+        for (int u = 0; u < 4; u++) {
+            zz[u] = zero_pair(((zw >> (4 * u)) & 15u) + 1u);
+            s[u] = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
         }
         f32x4 c[4][T];
 #pragma unroll
         for (int u = 0; u < 4; u++)
 #pragma unroll
             for (int t = 0; t < T; t++) c[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
 #pragma unroll
-        for (int kb = 0; kb < (KBPG > 0 ? KBPG : 1); kb++) {
-            // runtime-group variant loops inside; fixed-group variants are fully unrolled
-            for (int kk = (KBPG > 0 ? kb : 0); kk < (KBPG > 0 ? kb + 1 : kbpg); kk++) {
-                const int p = (g * kbpg + kk) * 4 + kq;   // packed row = 8-k chunk index
-                uint4 w = uint4{0u, 0u, 0u, 0u};
-                if (col_ok) w = *reinterpret_cast<const uint4*>(L.qweight + (size_t)p * N + n);
-                f16x8 a[T];
+        for (int kb = 0; kb < KB; kb++) {
+            const int p = (g * KB + kb) * 4 + kq;
+            f16x8 a[T];
 #pragma unroll
-                for (int t = 0; t < T; t++) {
-                    const int row = 16 * t + j;
-                    a[t] = row < R ? __builtin_bit_cast(f16x8, L.xs[(size_t)p * R + row])
-                                   : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-                }
-                const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+            for (int t = 0; t < T; t++) {
+                const int row = 16 * t + j;
+                if (row < R)
+                    a[t] = __builtin_bit_cast(f16x8, FUSED ? xs_lds[(p - p0) * R + row]
+                                                           : L.xs[(size_t)p * R + row]);
+                else
+                    a[t] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+            const uint32_t words[4] = {w[kb].x, w[kb].y, w[kb].z, w[kb].w};
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const f16x8 bq = centered_nibbles(words[u], zz[u]);
+            for (int u = 0; u < 4; u++) {
+                const f16x8 bq = centered_nibbles(words[u], zz[u]);
 #pragma unroll
-                    for (int t = 0; t < T; t++) c[u][t] = mfma_16x16x32_f16(a[t], bq, c[u][t]);
-                }
+                for (int t = 0; t < T; t++) c[u][t] = mfma_16x16x32_f16(a[t], bq, c[u][t]);
             }
         }
 #pragma unroll
@@ -254,15 +304,16 @@ __global__ __launch_bounds__(256) void linear_simple_kernel(GemvLinear L, int M,
     }
 }
 
-template <int T>
-hipError_t launch_tiles(const GemvBatch& b, int kbpg, hipStream_t stream)
+template <int T, bool FUSED>
+hipError_t launch_tiles(const GemvBatch& b, int kb, size_t lds, hipStream_t stream)
 {
     dim3 grid(b.wg_total), block(256);
-    switch (kbpg) {
-    case 4: hipLaunchKernelGGL((gemv_mfma_kernel<T, 4>), grid, block, 0, stream, b); break;
-    case 2: hipLaunchKernelGGL((gemv_mfma_kernel<T, 2>), grid, block, 0, stream, b); break;
-    case 1: hipLaunchKernelGGL((gemv_mfma_kernel<T, 1>), grid, block, 0, stream, b); break;
-    default: hipLaunchKernelGGL((gemv_mfma_kernel<T, 0>), grid, block, 0, stream, b); break;
+    switch (kb) {
+    case 1: hipLaunchKernelGGL((gemv_mfma_kernel<T, 1, FUSED>), grid, block, lds, stream, b); break;
+    case 2: hipLaunchKernelGGL((gemv_mfma_kernel<T, 2, FUSED>), grid, block, lds, stream, b); break;
+    case 4: hipLaunchKernelGGL((gemv_mfma_kernel<T, 4, FUSED>), grid, block, lds, stream, b); break;
+    case 8: hipLaunchKernelGGL((gemv_mfma_kernel<T, 8, FUSED>), grid, block, lds, stream, b); break;
+    default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -271,13 +322,14 @@ hipError_t launch_tiles(const GemvBatch& b, int kbpg, hipStream_t stream)
 
 bool gemv_fast_ok(int M, int N, int K, int group)
 {
-    return M >= 1 && M <= kGemvMaxM && N > 0 && K > 0 && N % 4 == 0 && K % 32 == 0 &&
-           group > 0 && group % 32 == 0 && K % group == 0;
+    return M >= 1 && M <= kGemvMaxM && N > 0 && K > 0 && N % 4 == 0 &&
+           (group == 32 || group == 64 || group == 128 || group == 256) && K % group == 0;
 }
+
+bool gemv_fused(int M) { return M <= kGemvFusedMaxM; }
 
 GemvShape gemv_shape(int M, int N, int K, int group)
 {
-    (void)M;
     GemvShape s;
     s.strips = (N + kGemvCols - 1) / kGemvCols;
     s.groups = K / group;
@@ -286,12 +338,23 @@ GemvShape gemv_shape(int M, int N, int K, int group)
     if (slices < 1) slices = 1;
     s.waves = kGemvWaves;
     s.split = (slices + kGemvWaves - 1) / kGemvWaves;
+    if (gemv_fused(M)) {
+        // the segment's split activations must fit the LDS budget: 2M rows x group/8 chunks x 16 B
+        int max_groups = kGemvLdsXsBytes / (4 * M * group);
+        if (max_groups < 1) max_groups = 1;
+        const int need = (s.groups + max_groups - 1) / max_groups;
+        if (s.split < need) s.split = need;
+    }
     if (s.split > s.groups) s.split = s.groups;
     if (s.split < 1) s.split = 1;
     return s;
 }
 
-uint64_t gemv_xs_bytes(int M, int K) { return ((uint64_t)4 * M * K + 255) & ~(uint64_t)255; }
+uint64_t gemv_xs_bytes(int M, int K)
+{
+    if (gemv_fused(M)) return 0;
+    return ((uint64_t)4 * M * K + 255) & ~(uint64_t)255;
+}
 
 uint64_t gemv_partial_bytes(int M, int N, int split)
 {
@@ -301,6 +364,19 @@ uint64_t gemv_partial_bytes(int M, int N, int split)
 
 hipError_t launch_gemv_batch(const GemvBatch& b, hipStream_t stream)
 {
+    const int group = b.L[0].group;
+    for (int i = 1; i < b.count; i++)
+        if (b.L[i].group != group) return hipErrorInvalidValue;
+    const int kb = group / 32;
+    if (gemv_fused(b.M)) {
+        size_t lds = 0;
+        for (int i = 0; i < b.count; i++) {
+            const int G = b.L[i].K / group;
+            const int gmax = (G + b.L[i].split - 1) / b.L[i].split;
+            lds = max(lds, (size_t)gmax * kb * 4 * (2 * b.M) * 16);
+        }
+        return launch_tiles<1, true>(b, kb, lds, stream);
+    }
     int max_chunks = 0;
     for (int i = 0; i < b.count; i++)
         if (b.L[i].xs_owner) max_chunks = max(max_chunks, (b.L[i].K >> 3) * b.M);
@@ -308,11 +384,8 @@ hipError_t launch_gemv_batch(const GemvBatch& b, hipStream_t stream)
     hipLaunchKernelGGL(xsplit_kernel, xgrid, dim3(256), 0, stream, b);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int kbpg = b.L[0].group >> 5;
-    int uniform = 1;
-    for (int i = 1; i < b.count; i++) uniform &= (b.L[i].group >> 5) == kbpg;
-    const int kb = uniform && (kbpg == 1 || kbpg == 2 || kbpg == 4) ? kbpg : 0;
-    return b.M <= 8 ? launch_tiles<1>(b, kb, stream) : launch_tiles<2>(b, kb, stream);
+    return b.M <= 8 ? launch_tiles<1, false>(b, kb, 0, stream)
+                    : launch_tiles<2, false>(b, kb, 0, stream);
 }
 
 hipError_t launch_gemv_simple(const GemvLinear& L, int M, int x_dtype, hipStream_t stream)

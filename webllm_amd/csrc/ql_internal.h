@@ -40,6 +40,7 @@ struct GemvShape {
 };
 GemvShape gemv_shape(int M, int N, int K, int group);
 bool gemv_fast_ok(int M, int N, int K, int group);
+bool gemv_fused(int M);
 uint64_t gemv_xs_bytes(int M, int K);
 uint64_t gemv_partial_bytes(int M, int N, int split);
 
