@@ -14,7 +14,7 @@
 struct ql_ctx {
     int device;
     hipStream_t stream;
-    uint32_t* counters;   // split-K arrival counters, zero between launches
+    uint32_t* counters;   // split-K arrival counters; every launch leaves them at zero
     hipEvent_t ev_start, ev_stop;
     bool capturing;
     int cu_count;
@@ -413,10 +413,10 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_ar
         L.strips = s.strips;
         L.wg_begin = 0;
         L.xs_owner = 1;
-        L.xs = reinterpret_cast<const uint4*>(act->base + scratch_off);
+        ql::gemv_xs_layout(L, act->base + scratch_off, M);
         L.partial = reinterpret_cast<float*>(act->base + scratch_off + ql::gemv_xs_bytes(M, d->K));
         L.counters = ctx->counters;
-        if (s.strips > ql::kCounterCapacity) return fail(QL_E_INVALID, "N too large");
+        if (s.strips > ql::kCounterCapacity) return fail(QL_E_INVALID, "N too large (%d)", d->N);
         b.L[0] = L;
         b.count = 1;
         b.M = M;
@@ -518,7 +518,13 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
         for (int k = 0; k < i; k++)
             if (x_offs[k] == x_offs[i] && descs[k].K == d->K) { owner = k; break; }
         L.xs_owner = owner < 0;
-        L.xs = owner < 0 ? reinterpret_cast<const uint4*>(act->base + off) : b.L[owner].xs;
+        if (owner < 0) {
+            ql::gemv_xs_layout(L, act->base + off, M);
+        } else {
+            L.xs = b.L[owner].xs;
+            L.sxs = b.L[owner].sxs;
+            L.bscale = b.L[owner].bscale;
+        }
         L.partial = reinterpret_cast<float*>(act->base + off + ql::gemv_xs_bytes(M, d->K));
         L.counters = ctx->counters + counter_base;
         counter_base += s.strips;

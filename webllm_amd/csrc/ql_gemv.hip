@@ -3,25 +3,30 @@
 // Replaces the reference's gemm_gemv_f16 / gemm_gemv_split_f16 + gemm_gemv_split_reduce pair
 // (src/gpu/kernels/gemm/*.wgsl, dispatched by src/model/qwen.ts:568-610), which streams fp16
 // weights that the CPU dequantized at load time. Here the weights stay packed (4 bits/weight)
-// and are dequantized in registers.
+// and are unpacked in registers; the multiply-adds run on MFMA.
 //
-// Arithmetic (chosen so the result tracks the reference CPU path — fp32 weights, double
-// accumulation — to well under 1e-4 relative):
-//   y[m,n] = sum_g s[g,n] * sum_{k in g} (q[k,n] - z[g,n]) * x[m,k]
-//   * (q - z) is an exact small integer in fp16 (magic-number unpack, ql_device.h);
-//   * x is split into x_hi = f16(x) and x_lo = f16(x - x_hi) (x = x_hi + x_lo to ~2^-22 rel), so
-//     each row m becomes two MFMA rows and products are exact in the fp32 MFMA accumulator;
-//   * the per-group scale is applied in fp32 to the group's partial sums.
-// The multiply-adds run on v_mfma_f32_16x16x32_f16: one MFMA consumes 4 packed rows (32 k) of
-// 16 columns; each lane feeds one packed word per column, which is exactly the B-operand
-// fragment (8 consecutive k of one column), so no LDS or shuffles are needed for weights.
+// Arithmetic (tracks the reference CPU path — fp32 weights, double accumulation — to ~1e-6):
+//   y[m,n] = sum_g s[g,n] * ( sum_{k in g} q[k,n] * x[m,k]  -  z[g,n] * Sx[g,m] ),
+//   Sx[g,m] = sum_{k in g} x[m,k]   (fp32, fixed order).
+// * q is taken straight from the packed word by masking: a nibble masked in place inside a
+//   16-bit half is an exact fp16 subnormal q * 2^-24, q * 2^-20 or q * 2^-16 depending on its
+//   bit position (no shifts or conversions for 3 of the 4 nibble pairs).
+// * x is scaled per row by a power of two (range normalisation: max |x| * 2^E * 256 < 2^15) and
+//   the factor matching each nibble position (256, 16, 1) is folded into the activation side;
+//   the scaled value a is split into a_hi = f16(a), a_lo = f16(a - a_hi), so each row m becomes
+//   two MFMA rows and every product is exact in the fp32 accumulator.
+// * all products then carry the same factor 2^(E-16), removed once at the end.
+// One v_mfma_f32_16x16x32_f16 consumes 4 packed rows (32 k) of 16 columns: each lane feeds one
+// packed word of one column, which is exactly the B-operand fragment (8 k of one column).
 //
 // Work split: a workgroup (4 waves) owns 64 output columns and one K segment (a range of whole
 // quantization groups); its waves take the segment's groups round-robin and are reduced through
-// LDS in wave order. With split > 1 segments, partial sums go to scratch and the last workgroup
-// of a column strip to finish (atomic arrival counter) adds them in ascending segment order —
-// deterministic, like the reference's two-pass reduce (gemm_gemv_split_reduce.wgsl:32-38),
-// without a second launch. The counter is reset by that workgroup, so no memset is needed.
+// LDS in wave order. With split > 1 segments, each workgroup stores its partial sums with
+// agent-scope (cross-XCD coherent) stores and bumps a per-strip arrival counter; the last one
+// adds the partials in ascending segment order — deterministic, like the reference's two-pass
+// reduce (gemm_gemv_split_reduce.wgsl:32-38), in one launch — and resets the counter.
+// Agent-scope *fences* are avoided on purpose: on this part they write back and invalidate the
+// whole L2, which was measured to cost more than the GEMV itself.
 #include "ql_device.h"
 #include "ql_internal.h"
 
@@ -30,53 +35,116 @@ namespace ql {
 namespace {
 
 constexpr int kTargetWaves = 4096;
-constexpr int kGemvFusedMaxM = 4;          // M <= 4: activations split in the kernel prologue
-constexpr int kGemvLdsXsBytes = 32768;     // LDS budget for that split (per workgroup)
+constexpr int kGemvFusedMaxM = 4;          // M <= 4: activations prepared in the kernel prologue
+constexpr int kGemvLdsXsBytes = 32768;     // LDS budget for them (per workgroup)
 
-// x [M,K] (f32 or f16) -> split activations in the MFMA A-operand order:
-//   xs[(c * R + 2m + h)] = 8 fp16 values of row m, chunk c (k = 8c..8c+7) in perm_k order,
-//   h = 0: x_hi, h = 1: x_lo;  R = 2M.
-__global__ __launch_bounds__(256) void xsplit_kernel(const GemvBatch b)
+// Factor folded into the activation for each element slot (perm_k order {0,4,1,5,2,6,3,7}):
+// slots 0,1 meet nibbles scaled 2^-24, slots 2,3 meet 2^-20, slots 4..7 meet 2^-16.
+__device__ __forceinline__ float slot_scale(int e) { return e < 2 ? 256.f : (e < 4 ? 16.f : 1.f); }
+
+// Per-row exponent E with max|x| * 2^(E+8) < 2^15 (E = 0 for an all-zero row).
+__device__ __forceinline__ int row_exponent(float amax)
 {
-    const GemvLinear& L = b.L[blockIdx.y];
-    if (!L.xs_owner) return;
-    const int M = b.M;
-    const int chunks = L.K >> 3;
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    if (t >= chunks * M) return;
-    const int c = t / M;
-    const int m = t - c * M;
-    float v[8];
-    if (b.x_dtype == 0) {
-        const float4* src = reinterpret_cast<const float4*>(
-            static_cast<const float*>(L.x) + (size_t)m * L.K + (size_t)c * 8);
+    if (!(amax > 0.f)) return 0;
+    int ex;
+    (void)frexpf(amax, &ex);                 // amax < 2^ex
+    int E = 7 - ex;
+    return E < -100 ? -100 : (E > 100 ? 100 : E);
+}
+
+__device__ __forceinline__ void load8(const void* x, int x_dtype, size_t base, float v[8])
+{
+    if (x_dtype == 0) {
+        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base);
         const float4 a0 = src[0], a1 = src[1];
         v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
         v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
     } else {
-        const f16x8 h = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(
-            static_cast<const uint16_t*>(L.x) + (size_t)m * L.K + (size_t)c * 8));
+        const f16x8 h = __builtin_bit_cast(
+            f16x8, *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base));
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = (float)h[e];
     }
+}
+
+// 8 activations (natural k order) -> scaled hi/lo fp16 fragments in perm_k slot order.
+__device__ __forceinline__ void split8(const float v[8], float scale, uint4* hi_out, uint4* lo_out)
+{
     f16x8 hi, lo;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        const float xv = v[perm_k(e)];
-        const _Float16 h = (_Float16)xv;
+        const float a = v[perm_k(e)] * (scale * slot_scale(e));
+        const _Float16 h = (_Float16)a;
         hi[e] = h;
-        lo[e] = (_Float16)(xv - (float)h);
+        lo[e] = (_Float16)(a - (float)h);
     }
-    uint4* dst = const_cast<uint4*>(L.xs) + (size_t)c * (2 * M) + 2 * m;
-    dst[0] = __builtin_bit_cast(uint4, hi);
-    dst[1] = __builtin_bit_cast(uint4, lo);
+    *hi_out = __builtin_bit_cast(uint4, hi);
+    *lo_out = __builtin_bit_cast(uint4, lo);
+}
+
+// 8 nibbles of a packed word as exact fp16 subnormals, in perm_k slot order.
+__device__ __forceinline__ f16x8 nibbles_subnormal(uint32_t w)
+{
+    const uint32_t p0 = w & 0x000F000Fu;          // k0, k4: q * 2^-24
+    const uint32_t p1 = w & 0x00F000F0u;          // k1, k5: q * 2^-20
+    const uint32_t p2 = w & 0x0F000F00u;          // k2, k6: q * 2^-16
+    const uint32_t p3 = (w >> 4) & 0x0F000F00u;   // k3, k7: q * 2^-16
+    const f16x2 a = as_f16x2(p0), b = as_f16x2(p1), c = as_f16x2(p2), d = as_f16x2(p3);
+    return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// Activations for rows m of a linear with M > 4, prepared once per call (one workgroup per row):
+//   xs[c * 2M + 2m + h]  (h: hi/lo) for every 8-k chunk c; sxs[g * M + m] = Sx[g,m] * 2^(E-16);
+//   bscale[m] = 2^(16-E).
+__global__ __launch_bounds__(256) void xsplit_kernel(const GemvBatch b)
+{
+    __shared__ float red[256];
+    const GemvLinear& L = b.L[blockIdx.y];
+    if (!L.xs_owner) return;
+    const int M = b.M;
+    const int m = blockIdx.x;
+    const int K = L.K;
+    float amax = 0.f;
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const float v = b.x_dtype == 0 ? static_cast<const float*>(L.x)[(size_t)m * K + k]
+                                       : (float)__builtin_bit_cast(_Float16,
+                                             static_cast<const uint16_t*>(L.x)[(size_t)m * K + k]);
+        amax = fmaxf(amax, fabsf(v));
+    }
+    red[threadIdx.x] = amax;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    const int E = row_exponent(red[0]);
+    const float scale = ldexpf(1.f, E);
+    uint4* xs = const_cast<uint4*>(L.xs);
+    for (int c = threadIdx.x; c < (K >> 3); c += 256) {
+        float v[8];
+        load8(L.x, b.x_dtype, (size_t)m * K + (size_t)c * 8, v);
+        split8(v, scale, &xs[(size_t)c * 2 * M + 2 * m], &xs[(size_t)c * 2 * M + 2 * m + 1]);
+    }
+    const int G = K / L.group;
+    float* sxs = const_cast<float*>(L.sxs);
+    for (int g = threadIdx.x; g < G; g += 256) {
+        float s = 0.f;
+        for (int c = 0; c < (L.group >> 3); c++) {
+            float v[8];
+            load8(L.x, b.x_dtype, (size_t)m * K + (size_t)g * L.group + (size_t)c * 8, v);
+            s += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        }
+        sxs[(size_t)g * M + m] = ldexpf(s, E - 16);
+    }
+    if (threadIdx.x == 0) const_cast<float*>(L.bscale)[m] = ldexpf(1.f, 16 - E);
 }
 
 template <int T, int KB, bool FUSED>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
 {
-    extern __shared__ uint4 xs_lds[];     // FUSED: split activations of this K segment
+    extern __shared__ uint4 dyn_lds[];        // FUSED: split activations + Sx of this segment
     __shared__ float red[kGemvWaves][kGemvMaxM][kGemvCols];
+    __shared__ float row_amax[kGemvWaves][kGemvFusedMaxM];
     __shared__ uint32_t is_last;
 
     int wg = blockIdx.x;
@@ -85,6 +153,12 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
     for (int i = 1; i < kMaxBatch; i++)
         if (i < b.count && wg >= b.L[i].wg_begin) li = i;
     const GemvLinear& L = b.L[li];
+    const uint32_t* __restrict__ qweight = L.qweight;
+    const uint32_t* __restrict__ qzeros = L.qzeros;
+    const uint16_t* __restrict__ scales = L.scales;
+    const int N = L.N;
+    const int K = L.K;
+    const int split = L.split;
     wg -= L.wg_begin;
     const int strip = wg % L.strips;
     const int seg = wg / L.strips;
@@ -95,62 +169,91 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
     const int wave = threadIdx.x >> 6;
     const int j = lane & 15;
     const int kq = lane >> 4;
-    const int N = L.N;
     const int NC = (N + 7) >> 3;
     const int n = strip * kGemvCols + 4 * j;
     const bool col_ok = n < N;
-    const int G = L.K / (KB * 32);
-    const int g0 = (int)((int64_t)G * seg / L.split);
-    const int g1 = (int)((int64_t)G * (seg + 1) / L.split);
-    const int p0 = g0 * KB * 4;           // first packed row (8-k chunk) of the segment
+    const int G = K / (KB * 32);
+    const int g0 = (int)((int64_t)G * seg / split);
+    const int g1 = (int)((int64_t)G * (seg + 1) / split);
+    const int p0 = g0 * KB * 4;               // first packed row (8-k chunk) of the segment
+    const int chunks = (g1 - g0) * KB * 4;
 
     // software pipeline: the next group's packed words, zeros and scales are in flight while
-    // the current group is converted and multiplied
+    // the current group is unpacked and multiplied
     uint4 wn[KB];
     uint32_t zn = 0x77777777u;
     uint2 sn = uint2{0u, 0u};
     auto fetch = [&](int g) {
 #pragma unroll
         for (int kb = 0; kb < KB; kb++)
-            wn[kb] = *reinterpret_cast<const uint4*>(L.qweight +
-                                                     (size_t)((g * KB + kb) * 4 + kq) * N + n);
-        if (L.qzeros) zn = L.qzeros[(size_t)g * NC + (n >> 3)];
-        sn = *reinterpret_cast<const uint2*>(L.scales + (size_t)g * N + n);
+            wn[kb] = *reinterpret_cast<const uint4*>(qweight + (size_t)((g * KB + kb) * 4 + kq) * N + n);
+        if (qzeros) zn = qzeros[(size_t)g * NC + (n >> 3)];
+        sn = *reinterpret_cast<const uint2*>(scales + (size_t)g * N + n);
     };
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) wn[kb] = uint4{0u, 0u, 0u, 0u};
     int g = g0 + wave;
     if (g < g1 && col_ok) fetch(g);
 
+    uint4* xs_lds = dyn_lds;
+    float* sx_lds = reinterpret_cast<float*>(dyn_lds + (FUSED ? chunks * R : 0));
+    float bscale[kGemvFusedMaxM];
     if (FUSED) {
-        // x [M,K] -> x_hi/x_lo fp16 in MFMA A-operand order, for this segment only
-        const int chunks = (g1 - g0) * KB * 4;
+        // 1) per-row max |x| over the segment  2) scaled hi/lo split  3) group sums Sx
+        float am[kGemvFusedMaxM] = {0.f, 0.f, 0.f, 0.f};
         for (int idx = threadIdx.x; idx < chunks * M; idx += 256) {
             const int c = idx / M;
             const int m = idx - c * M;
             float v[8];
-            const size_t base = (size_t)m * L.K + (size_t)(p0 + c) * 8;
-            if (b.x_dtype == 0) {
-                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(L.x) + base);
-                const float4 a0 = src[0], a1 = src[1];
-                v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-                v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-            } else {
-                const f16x8 h = __builtin_bit_cast(
-                    f16x8, *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(L.x) + base));
+            load8(L.x, b.x_dtype, (size_t)m * K + (size_t)(p0 + c) * 8, v);
 #pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = (float)h[e];
-            }
-            f16x8 hi, lo;
+            for (int e = 0; e < 8; e++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float xv = v[perm_k(e)];
-                const _Float16 h = (_Float16)xv;
-                hi[e] = h;
-                lo[e] = (_Float16)(xv - (float)h);
+                for (int mm = 0; mm < kGemvFusedMaxM; mm++)
+                    if (mm == m) am[mm] = fmaxf(am[mm], fabsf(v[e]));
+        }
+#pragma unroll
+        for (int mm = 0; mm < kGemvFusedMaxM; mm++) {
+            float a = am[mm];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+            if (lane == 0) row_amax[wave][mm] = a;
+        }
+        __syncthreads();
+        float rscale[kGemvFusedMaxM];
+        int E[kGemvFusedMaxM];
+#pragma unroll
+        for (int mm = 0; mm < kGemvFusedMaxM; mm++) {
+            const float a = fmaxf(fmaxf(row_amax[0][mm], row_amax[1][mm]),
+                                  fmaxf(row_amax[2][mm], row_amax[3][mm]));
+            E[mm] = row_exponent(a);
+            rscale[mm] = ldexpf(1.f, E[mm]);
+            bscale[mm] = ldexpf(1.f, 16 - E[mm]);
+        }
+        for (int idx = threadIdx.x; idx < chunks * M; idx += 256) {
+            const int c = idx / M;
+            const int m = idx - c * M;
+            float v[8];
+            load8(L.x, b.x_dtype, (size_t)m * K + (size_t)(p0 + c) * 8, v);
+            float sc = rscale[0];
+#pragma unroll
+            for (int mm = 1; mm < kGemvFusedMaxM; mm++) if (mm == m) sc = rscale[mm];
+            split8(v, sc, &xs_lds[c * R + 2 * m], &xs_lds[c * R + 2 * m + 1]);
+        }
+        const int gseg = g1 - g0;
+        for (int idx = threadIdx.x; idx < gseg * M; idx += 256) {
+            const int gg = idx / M;
+            const int m = idx - gg * M;
+            float s = 0.f;
+            for (int c = 0; c < KB * 4; c++) {
+                float v[8];
+                load8(L.x, b.x_dtype, (size_t)m * K + (size_t)(p0 + gg * KB * 4 + c) * 8, v);
+                s += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
             }
-            xs_lds[c * R + 2 * m] = __builtin_bit_cast(uint4, hi);
-            xs_lds[c * R + 2 * m + 1] = __builtin_bit_cast(uint4, lo);
+            int e = E[0];
+#pragma unroll
+            for (int mm = 1; mm < kGemvFusedMaxM; mm++) if (mm == m) e = E[mm];
+            sx_lds[gg * M + m] = ldexpf(s, e - 16);
         }
         __syncthreads();
     }
@@ -165,18 +268,10 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
         uint4 w[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) w[kb] = wn[kb];
-        const uint32_t zw = L.qzeros ? (zn >> (4 * (n & 7))) : 0x7777u;
+        const uint32_t zw = qzeros ? (zn >> (4 * (n & 7))) : 0x7777u;
         const uint2 sv = sn;
         if (g + kGemvWaves < g1 && col_ok) fetch(g + kGemvWaves);
 
-        uint32_t zz[4];
-        float s[4];
-        const uint32_t sw[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            zz[u] = zero_pair(((zw >> (4 * u)) & 15u) + 1u);
-            s[u] = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
-        }
         f32x4 c[4][T];
 #pragma unroll
         for (int u = 0; u < 4; u++)
@@ -198,15 +293,32 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
             const uint32_t words[4] = {w[kb].x, w[kb].y, w[kb].z, w[kb].w};
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const f16x8 bq = centered_nibbles(words[u], zz[u]);
+                const f16x8 bq = nibbles_subnormal(words[u]);
 #pragma unroll
                 for (int t = 0; t < T; t++) c[u][t] = mfma_16x16x32_f16(a[t], bq, c[u][t]);
             }
         }
+        // group epilogue: acc += s * C  (all rows), acc -= s * z * Sx' (hi rows only)
+        const uint32_t sw[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
+        float sx[T][2];
 #pragma unroll
-        for (int u = 0; u < 4; u++)
+        for (int t = 0; t < T; t++)
 #pragma unroll
-            for (int t = 0; t < T; t++) acc[u][t] += s[u] * c[u][t];
+            for (int h = 0; h < 2; h++) {
+                const int m = 8 * t + 2 * kq + h;
+                sx[t][h] = m < M ? (FUSED ? sx_lds[(g - g0) * M + m] : L.sxs[(size_t)g * M + m]) : 0.f;
+            }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
+            const float sz = s * (float)(((zw >> (4 * u)) & 15u) + 1u);
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                acc[u][t] += s * c[u][t];
+                acc[u][t][0] -= sz * sx[t][0];
+                acc[u][t][2] -= sz * sx[t][1];
+            }
+        }
     }
 
     // MFMA D layout: lane (j, kq) holds rows 4kq..4kq+3 of column j; rows are (m, hi/lo) pairs.
@@ -215,47 +327,61 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
 #pragma unroll
         for (int t = 0; t < T; t++) {
             const int m0 = 8 * t + 2 * kq;
-            if (m0 < M) red[wave][m0][4 * j + u] = acc[u][t][0] + acc[u][t][1];
-            if (m0 + 1 < M) red[wave][m0 + 1][4 * j + u] = acc[u][t][2] + acc[u][t][3];
+            float b0, b1;
+            if (FUSED) {
+                b0 = bscale[0]; b1 = bscale[0];
+#pragma unroll
+                for (int mm = 1; mm < kGemvFusedMaxM; mm++) {
+                    if (mm == m0) b0 = bscale[mm];
+                    if (mm == m0 + 1) b1 = bscale[mm];
+                }
+            } else {
+                b0 = m0 < M ? L.bscale[m0] : 0.f;
+                b1 = m0 + 1 < M ? L.bscale[m0 + 1] : 0.f;
+            }
+            if (m0 < M) red[wave][m0][4 * j + u] = (acc[u][t][0] + acc[u][t][1]) * b0;
+            if (m0 + 1 < M) red[wave][m0 + 1][4 * j + u] = (acc[u][t][2] + acc[u][t][3]) * b1;
         }
     }
     __syncthreads();
 
-    const bool split = L.split > 1;
     for (int idx = threadIdx.x; idx < M * kGemvCols; idx += 256) {
         const int m = idx >> 6;
         const int col = idx & 63;
         const int nn = strip * kGemvCols + col;
         if (nn >= N) continue;
         const float sum = ((red[0][m][col] + red[1][m][col]) + red[2][m][col]) + red[3][m][col];
-        if (!split) {
+        if (split == 1) {
             L.y[(size_t)m * N + nn] = L.bias ? sum + L.bias[nn] : sum;
         } else {
-            L.partial[((size_t)seg * M + m) * N + nn] = sum;
+            __hip_atomic_store(&L.partial[((size_t)seg * M + m) * N + nn], sum, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (!split) return;
+    if (split == 1) return;
 
-    __threadfence();
+    // this wave's partial stores are complete (written through to the coherence point) before
+    // the workgroup signals arrival
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&L.counters[strip], 1u, __ATOMIC_ACQ_REL,
+        const uint32_t prev = __hip_atomic_fetch_add(&L.counters[strip], 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t last = prev == (uint32_t)(L.split - 1);
-        if (last) __hip_atomic_store(&L.counters[strip], 0u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t last = prev == (uint32_t)(split - 1);
+        if (last) __hip_atomic_store(&L.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         is_last = last;
     }
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
     for (int idx = threadIdx.x; idx < M * kGemvCols; idx += 256) {
         const int m = idx >> 6;
         const int col = idx & 63;
         const int nn = strip * kGemvCols + col;
         if (nn >= N) continue;
-        float sum = L.partial[(size_t)m * N + nn];
-        for (int s2 = 1; s2 < L.split; s2++) sum += L.partial[((size_t)s2 * M + m) * N + nn];
+        float sum = 0.f;
+        for (int s2 = 0; s2 < split; s2++)
+            sum += __hip_atomic_load(&L.partial[((size_t)s2 * M + m) * N + nn], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
         L.y[(size_t)m * N + nn] = L.bias ? sum + L.bias[nn] : sum;
     }
 }
@@ -339,8 +465,9 @@ GemvShape gemv_shape(int M, int N, int K, int group)
     s.waves = kGemvWaves;
     s.split = (slices + kGemvWaves - 1) / kGemvWaves;
     if (gemv_fused(M)) {
-        // the segment's split activations must fit the LDS budget: 2M rows x group/8 chunks x 16 B
-        int max_groups = kGemvLdsXsBytes / (4 * M * group);
+        // the segment's split activations (2M rows x group/8 chunks x 16 B) plus its group sums
+        // (M floats per group) must fit the LDS budget
+        int max_groups = kGemvLdsXsBytes / (4 * M * group + 4 * M);
         if (max_groups < 1) max_groups = 1;
         const int need = (s.groups + max_groups - 1) / max_groups;
         if (s.split < need) s.split = need;
@@ -350,16 +477,26 @@ GemvShape gemv_shape(int M, int N, int K, int group)
     return s;
 }
 
+// scratch layout for M > 4: xs [K/8][2M] uint4, then Sx' [G][M] f32, then 2^(16-E) [M] f32
 uint64_t gemv_xs_bytes(int M, int K)
 {
     if (gemv_fused(M)) return 0;
-    return ((uint64_t)4 * M * K + 255) & ~(uint64_t)255;
+    const uint64_t xs = (uint64_t)4 * M * K;
+    const uint64_t sx = (uint64_t)4 * M * (K / 32 + 1) + 4 * (uint64_t)M;
+    return (xs + sx + 255) & ~(uint64_t)255;
 }
 
 uint64_t gemv_partial_bytes(int M, int N, int split)
 {
     if (split <= 1) return 0;
     return ((uint64_t)split * M * N * 4 + 255) & ~(uint64_t)255;
+}
+
+void gemv_xs_layout(GemvLinear& L, char* base, int M)
+{
+    L.xs = reinterpret_cast<const uint4*>(base);
+    L.sxs = reinterpret_cast<const float*>(base + (size_t)4 * M * L.K);
+    L.bscale = L.sxs + (size_t)M * (L.K / L.group);
 }
 
 hipError_t launch_gemv_batch(const GemvBatch& b, hipStream_t stream)
@@ -373,19 +510,14 @@ hipError_t launch_gemv_batch(const GemvBatch& b, hipStream_t stream)
         for (int i = 0; i < b.count; i++) {
             const int G = b.L[i].K / group;
             const int gmax = (G + b.L[i].split - 1) / b.L[i].split;
-            lds = max(lds, (size_t)gmax * kb * 4 * (2 * b.M) * 16);
+            lds = max(lds, (size_t)gmax * kb * 4 * (2 * b.M) * 16 + (size_t)gmax * b.M * 4);
         }
         return launch_tiles<1, true>(b, kb, lds, stream);
     }
-    int max_chunks = 0;
-    for (int i = 0; i < b.count; i++)
-        if (b.L[i].xs_owner) max_chunks = max(max_chunks, (b.L[i].K >> 3) * b.M);
-    dim3 xgrid((max_chunks + 255) / 256, b.count);
-    hipLaunchKernelGGL(xsplit_kernel, xgrid, dim3(256), 0, stream, b);
+    hipLaunchKernelGGL(xsplit_kernel, dim3(b.M, b.count), dim3(256), 0, stream, b);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return b.M <= 8 ? launch_tiles<1, false>(b, kb, 0, stream)
-                    : launch_tiles<2, false>(b, kb, 0, stream);
+    return b.M <= 8 ? launch_tiles<1, false>(b, kb, 0, stream) : launch_tiles<2, false>(b, kb, 0, stream);
 }
 
 hipError_t launch_gemv_simple(const GemvLinear& L, int M, int x_dtype, hipStream_t stream)
