@@ -103,9 +103,9 @@ def test_plan_kinds_and_determinism(ql):
         assert a.split >= 1 and a.grid_x == -(-N // 64) * a.split
         G = K // 128
         assert a.split <= G
-        # M <= 4 prepares activations inside the kernel; M > 4 needs [K/8][2M] fragments,
-        # group sums [K/32+1][M] and row scales [M]
-        xs = 0 if M <= 4 else 4 * M * K + 4 * M * (K // 32 + 1) + 4 * M
+        # M <= 4 prepares activations inside the kernel; M > 4 needs [K/8][2M] fragments and
+        # per (group, row) {scale, sum} pairs (sized for the smallest group, 32)
+        xs = 0 if M <= 4 else 4 * M * K + 8 * M * (K // 32)
         part = a.split * M * N * 4 if a.split > 1 else 0
         assert a.scratch_bytes == (xs + 255) // 256 * 256 + (part + 255) // 256 * 256
 

@@ -176,6 +176,37 @@ def test_gemv_parity(ql, ctx, orc, K, N, M, zero, with_bias, label):
     assert_close(orc, y, ref, GEMV_ATOL, GEMV_RTOL, label)
 
 
+@pytest.mark.parametrize("group,M", [(32, 1), (64, 3), (256, 2), (32, 7), (64, 12), (256, 16)])
+def test_gemv_group_sizes(ql, ctx, orc, group, M):
+    """GPTQ group sizes 32/64/256 on the MFMA path (in-kernel and prepared activations)."""
+    K, N = 1024, 512
+    t = synth.gptq_linear(K, N, group, seed=0x6A, key=(group, M), stored_zero=None)
+    x = synth.activations(M, K, seed=0x6B, key=(group, M))
+    lin = Linear(ql, ctx, t)
+    y, plan = run_linear(ql, ctx, lin, x)
+    assert plan.kind_name == "gemv_mfma"
+    assert_close(orc, y, oracle_gemv(orc, lin, x), GEMV_ATOL, GEMV_RTOL, f"group {group} M={M}")
+
+
+def test_gemv_activation_range(ql, ctx, orc):
+    """Per-group power-of-two range normalisation: huge, tiny and zero activation groups."""
+    K, N, M = 1024, 256, 2
+    t = synth.gptq_linear(K, N, 128, seed=0x6C)
+    x = synth.activations(M, K, seed=0x6D)
+    x[0, :128] *= 3.0e4          # |x| up to ~1e5, beyond fp16 range
+    x[0, 128:256] *= 1e-6
+    x[1, 256:384] = 0.0
+    x[1, 384:512] *= 1e-30
+    lin = Linear(ql, ctx, t)
+    for M_ in (1, 2):
+        y, _ = run_linear(ql, ctx, lin, np.ascontiguousarray(x[:M_]))
+        ref = oracle_gemv(orc, lin, x[:M_])
+        assert_close(orc, y, ref, GEMV_ATOL, GEMV_RTOL, f"range M={M_}")
+    xb = np.concatenate([x] * 4)            # M = 8: prepared-activation path
+    y, _ = run_linear(ql, ctx, lin, xb)
+    assert_close(orc, y, oracle_gemv(orc, lin, xb), GEMV_ATOL, GEMV_RTOL, "range M=8")
+
+
 def test_gemv_f16_activations(ql, ctx, orc):
     K, N, M = 896, 896, 3
     t = synth.gptq_linear(K, N, 128, seed=0x16)

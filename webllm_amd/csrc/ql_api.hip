@@ -23,7 +23,8 @@ struct ql_ctx {
 };
 
 struct ql_arena {
-    ql_ctx* ctx;
+    ql_ctx* ctx;          // owner; copies use its stream
+    int device;           // release needs only this, so it stays valid after ql_destroy
     char* base;
     uint64_t size;
 };
@@ -268,6 +269,7 @@ int ql_arena_reserve(ql_ctx* ctx, uint64_t bytes, ql_arena** out)
     QL_HIP(hipMalloc(&p, bytes));
     ql_arena* a = new ql_arena();
     a->ctx = ctx;
+    a->device = ctx->device;
     a->base = static_cast<char*>(p);
     a->size = bytes;
     *out = a;
@@ -277,9 +279,8 @@ int ql_arena_reserve(ql_ctx* ctx, uint64_t bytes, ql_arena** out)
 int ql_arena_release(ql_arena* arena)
 {
     if (!arena) return fail(QL_E_INVALID, "null arena");
-    (void)hipSetDevice(arena->ctx->device);
-    (void)hipStreamSynchronize(arena->ctx->stream);
-    (void)hipFree(arena->base);
+    (void)hipSetDevice(arena->device);
+    (void)hipFree(arena->base);   // hipFree waits for outstanding work on the device
     delete arena;
     return QL_OK;
 }
@@ -522,8 +523,7 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
             ql::gemv_xs_layout(L, act->base + off, M);
         } else {
             L.xs = b.L[owner].xs;
-            L.sxs = b.L[owner].sxs;
-            L.bscale = b.L[owner].bscale;
+            L.gs = b.L[owner].gs;
         }
         L.partial = reinterpret_cast<float*>(act->base + off + ql::gemv_xs_bytes(M, d->K));
         L.counters = ctx->counters + counter_base;

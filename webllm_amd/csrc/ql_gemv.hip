@@ -8,14 +8,16 @@
 // Arithmetic (tracks the reference CPU path — fp32 weights, double accumulation — to ~1e-6):
 //   y[m,n] = sum_g s[g,n] * ( sum_{k in g} q[k,n] * x[m,k]  -  z[g,n] * Sx[g,m] ),
 //   Sx[g,m] = sum_{k in g} x[m,k]   (fp32, fixed order).
-// * q is taken straight from the packed word by masking: a nibble masked in place inside a
-//   16-bit half is an exact fp16 subnormal q * 2^-24, q * 2^-20 or q * 2^-16 depending on its
-//   bit position (no shifts or conversions for 3 of the 4 nibble pairs).
-// * x is scaled per row by a power of two (range normalisation: max |x| * 2^E * 256 < 2^15) and
-//   the factor matching each nibble position (256, 16, 1) is folded into the activation side;
-//   the scaled value a is split into a_hi = f16(a), a_lo = f16(a - a_hi), so each row m becomes
-//   two MFMA rows and every product is exact in the fp32 accumulator.
-// * all products then carry the same factor 2^(E-16), removed once at the end.
+// * q is taken straight from the packed word by shifting and masking: a nibble at bits 4-7 of a
+//   16-bit half is an exact fp16 subnormal q * 2^-20 (7 integer ops per packed word of 8
+//   weights, no conversions). Bits 4-7 and not 0-3: MFMA products with operands at the bottom of
+//   the subnormal range (q * 2^-24) were measured to lose ~1e-6 relative accuracy, bits 4-7 none.
+// * x is scaled per (row, group) by a power of two 2^E (range normalisation:
+//   max_{k in g} |x| * 2^E * 16 < 2^15), times the factor 16 matching the nibble position; the
+//   scaled value a is split into a_hi = f16(a), a_lo = f16(a - a_hi), so each row m becomes two
+//   MFMA rows and every product is exact in the fp32 accumulator. The group's products carry
+//   2^(E-16), removed with the group scale in the group epilogue. 16 lanes own one group of one
+//   row: max, exponent, split and group sum are one pass with 16-lane butterflies.
 // One v_mfma_f32_16x16x32_f16 consumes 4 packed rows (32 k) of 16 columns: each lane feeds one
 // packed word of one column, which is exactly the B-operand fragment (8 k of one column).
 //
@@ -38,17 +40,16 @@ constexpr int kTargetWaves = 4096;
 constexpr int kGemvFusedMaxM = 4;          // M <= 4: activations prepared in the kernel prologue
 constexpr int kGemvLdsXsBytes = 32768;     // LDS budget for them (per workgroup)
 
-// Factor folded into the activation for each element slot (perm_k order {0,4,1,5,2,6,3,7}):
-// slots 0,1 meet nibbles scaled 2^-24, slots 2,3 meet 2^-20, slots 4..7 meet 2^-16.
-__device__ __forceinline__ float slot_scale(int e) { return e < 2 ? 256.f : (e < 4 ? 16.f : 1.f); }
+// Factor folded into the activations: every nibble arrives as q * 2^-20.
+constexpr float kActScale = 16.f;
 
-// Per-row exponent E with max|x| * 2^(E+8) < 2^15 (E = 0 for an all-zero row).
+// Exponent E with max|x| * 2^E * 16 < 2^15 (E = 0 when all values are zero).
 __device__ __forceinline__ int row_exponent(float amax)
 {
     if (!(amax > 0.f)) return 0;
     int ex;
     (void)frexpf(amax, &ex);                 // amax < 2^ex
-    int E = 7 - ex;
+    int E = 11 - ex;
     return E < -100 ? -100 : (E > 100 ? 100 : E);
 }
 
@@ -73,7 +74,7 @@ __device__ __forceinline__ void split8(const float v[8], float scale, uint4* hi_
     f16x8 hi, lo;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        const float a = v[perm_k(e)] * (scale * slot_scale(e));
+        const float a = v[perm_k(e)] * (scale * kActScale);
         const _Float16 h = (_Float16)a;
         hi[e] = h;
         lo[e] = (_Float16)(a - (float)h);
@@ -82,61 +83,62 @@ __device__ __forceinline__ void split8(const float v[8], float scale, uint4* hi_
     *lo_out = __builtin_bit_cast(uint4, lo);
 }
 
-// 8 nibbles of a packed word as exact fp16 subnormals, in perm_k slot order.
+// 8 nibbles of a packed word as exact fp16 subnormals q * 2^-20, in perm_k slot order.
 __device__ __forceinline__ f16x8 nibbles_subnormal(uint32_t w)
 {
-    const uint32_t p0 = w & 0x000F000Fu;          // k0, k4: q * 2^-24
-    const uint32_t p1 = w & 0x00F000F0u;          // k1, k5: q * 2^-20
-    const uint32_t p2 = w & 0x0F000F00u;          // k2, k6: q * 2^-16
-    const uint32_t p3 = (w >> 4) & 0x0F000F00u;   // k3, k7: q * 2^-16
+    const uint32_t p0 = (w << 4) & 0x00F000F0u;   // k0, k4
+    const uint32_t p1 = w & 0x00F000F0u;          // k1, k5
+    const uint32_t p2 = (w >> 4) & 0x00F000F0u;   // k2, k6
+    const uint32_t p3 = (w >> 8) & 0x00F000F0u;   // k3, k7
     const f16x2 a = as_f16x2(p0), b = as_f16x2(p1), c = as_f16x2(p2), d = as_f16x2(p3);
     return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
 }
 
-// Activations for rows m of a linear with M > 4, prepared once per call (one workgroup per row):
-//   xs[c * 2M + 2m + h]  (h: hi/lo) for every 8-k chunk c; sxs[g * M + m] = Sx[g,m] * 2^(E-16);
-//   bscale[m] = 2^(16-E).
+// One 8-k chunk of activations, owned by one of CPG lanes (CPG = group / 8, consecutive lanes)
+// that together hold one quantization group of one row: returns the group's {2^(16-E), Sx} to
+// every lane and writes the lane's scaled hi/lo fragments. Butterfly reductions give every lane
+// the same bits (IEEE addition is commutative), so the result does not depend on the lane.
+template <int CPG>
+__device__ __forceinline__ float2 prep_group_chunk(const float v[8], uint4* hi_out, uint4* lo_out)
+{
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+#pragma unroll
+    for (int off = 1; off < CPG; off <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off));
+        sum += __shfl_xor(sum, off);
+    }
+    const int E = row_exponent(amax);
+    split8(v, ldexpf(1.f, E), hi_out, lo_out);
+    return float2{ldexpf(1.f, 16 - E), sum};
+}
+
+// Activations of a linear with M > 4, prepared once per call:
+//   xs[c * 2M + 2m + h] (h: hi/lo) for every 8-k chunk c; gs[g * M + m] = {2^(16-E), Sx[g,m]}.
+// group/8 lanes per (group, row); grid.x covers G * M * group/8 lanes, grid.y the batch.
+template <int CPG>
 __global__ __launch_bounds__(256) void xsplit_kernel(const GemvBatch b)
 {
-    __shared__ float red[256];
     const GemvLinear& L = b.L[blockIdx.y];
     if (!L.xs_owner) return;
     const int M = b.M;
-    const int m = blockIdx.x;
-    const int K = L.K;
-    float amax = 0.f;
-    for (int k = threadIdx.x; k < K; k += 256) {
-        const float v = b.x_dtype == 0 ? static_cast<const float*>(L.x)[(size_t)m * K + k]
-                                       : (float)__builtin_bit_cast(_Float16,
-                                             static_cast<const uint16_t*>(L.x)[(size_t)m * K + k]);
-        amax = fmaxf(amax, fabsf(v));
-    }
-    red[threadIdx.x] = amax;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
-    }
-    const int E = row_exponent(red[0]);
-    const float scale = ldexpf(1.f, E);
+    const int G = L.K / L.group;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const int item = idx / CPG;                        // (group, row) pair, uniform per CPG lanes
+    if (item >= G * M) return;
+    const int c = idx - item * CPG;
+    const int cpg = CPG;
+    const int g = item / M;
+    const int m = item - g * M;
+    const int chunk = g * cpg + c;
+    float v[8];
+    load8(L.x, b.x_dtype, (size_t)m * L.K + (size_t)chunk * 8, v);
     uint4* xs = const_cast<uint4*>(L.xs);
-    for (int c = threadIdx.x; c < (K >> 3); c += 256) {
-        float v[8];
-        load8(L.x, b.x_dtype, (size_t)m * K + (size_t)c * 8, v);
-        split8(v, scale, &xs[(size_t)c * 2 * M + 2 * m], &xs[(size_t)c * 2 * M + 2 * m + 1]);
-    }
-    const int G = K / L.group;
-    float* sxs = const_cast<float*>(L.sxs);
-    for (int g = threadIdx.x; g < G; g += 256) {
-        float s = 0.f;
-        for (int c = 0; c < (L.group >> 3); c++) {
-            float v[8];
-            load8(L.x, b.x_dtype, (size_t)m * K + (size_t)g * L.group + (size_t)c * 8, v);
-            s += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-        }
-        sxs[(size_t)g * M + m] = ldexpf(s, E - 16);
-    }
-    if (threadIdx.x == 0) const_cast<float*>(L.bscale)[m] = ldexpf(1.f, 16 - E);
+    const float2 gs = prep_group_chunk<CPG>(v, &xs[(size_t)chunk * 2 * M + 2 * m],
+                                       &xs[(size_t)chunk * 2 * M + 2 * m + 1]);
+    if (c == 0) const_cast<float2*>(L.gs)[(size_t)g * M + m] = gs;
 }
 
 template <int T, int KB, bool FUSED>
@@ -144,7 +146,6 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
 {
     extern __shared__ uint4 dyn_lds[];        // FUSED: split activations + Sx of this segment
     __shared__ float red[kGemvWaves][kGemvMaxM][kGemvCols];
-    __shared__ float row_amax[kGemvWaves][kGemvFusedMaxM];
     __shared__ uint32_t is_last;
 
     int wg = blockIdx.x;
@@ -196,64 +197,24 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
     if (g < g1 && col_ok) fetch(g);
 
     uint4* xs_lds = dyn_lds;
-    float* sx_lds = reinterpret_cast<float*>(dyn_lds + (FUSED ? chunks * R : 0));
-    float bscale[kGemvFusedMaxM];
+    float2* gs_lds = reinterpret_cast<float2*>(dyn_lds + (FUSED ? chunks * R : 0));
     if (FUSED) {
-        // 1) per-row max |x| over the segment  2) scaled hi/lo split  3) group sums Sx
-        float am[kGemvFusedMaxM] = {0.f, 0.f, 0.f, 0.f};
-        for (int idx = threadIdx.x; idx < chunks * M; idx += 256) {
-            const int c = idx / M;
-            const int m = idx - c * M;
-            float v[8];
-            load8(L.x, b.x_dtype, (size_t)m * K + (size_t)(p0 + c) * 8, v);
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-#pragma unroll
-                for (int mm = 0; mm < kGemvFusedMaxM; mm++)
-                    if (mm == m) am[mm] = fmaxf(am[mm], fabsf(v[e]));
-        }
-#pragma unroll
-        for (int mm = 0; mm < kGemvFusedMaxM; mm++) {
-            float a = am[mm];
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
-            if (lane == 0) row_amax[wave][mm] = a;
-        }
-        __syncthreads();
-        float rscale[kGemvFusedMaxM];
-        int E[kGemvFusedMaxM];
-#pragma unroll
-        for (int mm = 0; mm < kGemvFusedMaxM; mm++) {
-            const float a = fmaxf(fmaxf(row_amax[0][mm], row_amax[1][mm]),
-                                  fmaxf(row_amax[2][mm], row_amax[3][mm]));
-            E[mm] = row_exponent(a);
-            rscale[mm] = ldexpf(1.f, E[mm]);
-            bscale[mm] = ldexpf(1.f, 16 - E[mm]);
-        }
-        for (int idx = threadIdx.x; idx < chunks * M; idx += 256) {
-            const int c = idx / M;
-            const int m = idx - c * M;
-            float v[8];
-            load8(L.x, b.x_dtype, (size_t)m * K + (size_t)(p0 + c) * 8, v);
-            float sc = rscale[0];
-#pragma unroll
-            for (int mm = 1; mm < kGemvFusedMaxM; mm++) if (mm == m) sc = rscale[mm];
-            split8(v, sc, &xs_lds[c * R + 2 * m], &xs_lds[c * R + 2 * m + 1]);
-        }
-        const int gseg = g1 - g0;
-        for (int idx = threadIdx.x; idx < gseg * M; idx += 256) {
-            const int gg = idx / M;
-            const int m = idx - gg * M;
-            float s = 0.f;
-            for (int c = 0; c < KB * 4; c++) {
+        // the segment's activations: KB*4 lanes per (group, row), one chunk of 8 k per lane
+        constexpr int CPG = KB * 4;
+        const int items = (g1 - g0) * M;
+        for (int base = 0; base < items * CPG; base += 256) {
+            const int idx = base + threadIdx.x;
+            const int item = idx / CPG;                 // uniform per CPG lanes
+            if (item < items) {
+                const int cl = idx - item * CPG;
+                const int gg = item / M;
+                const int m = item - gg * M;
+                const int c = gg * CPG + cl;            // chunk within the segment
                 float v[8];
-                load8(L.x, b.x_dtype, (size_t)m * K + (size_t)(p0 + gg * KB * 4 + c) * 8, v);
-                s += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                load8(L.x, b.x_dtype, (size_t)m * K + (size_t)(p0 + c) * 8, v);
+                const float2 gsv = prep_group_chunk<CPG>(v, &xs_lds[c * R + 2 * m], &xs_lds[c * R + 2 * m + 1]);
+                if (cl == 0) gs_lds[gg * M + m] = gsv;
             }
-            int e = E[0];
-#pragma unroll
-            for (int mm = 1; mm < kGemvFusedMaxM; mm++) if (mm == m) e = E[mm];
-            sx_lds[gg * M + m] = ldexpf(s, e - 16);
         }
         __syncthreads();
     }
@@ -298,15 +259,16 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
                 for (int t = 0; t < T; t++) c[u][t] = mfma_16x16x32_f16(a[t], bq, c[u][t]);
             }
         }
-        // group epilogue: acc += s * C  (all rows), acc -= s * z * Sx' (hi rows only)
+        // group epilogue: acc += s * 2^(16-E) * C (all rows), acc -= s * z * Sx (hi rows only)
         const uint32_t sw[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
-        float sx[T][2];
+        float2 gsr[T][2];
 #pragma unroll
         for (int t = 0; t < T; t++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int m = 8 * t + 2 * kq + h;
-                sx[t][h] = m < M ? (FUSED ? sx_lds[(g - g0) * M + m] : L.sxs[(size_t)g * M + m]) : 0.f;
+                gsr[t][h] = m < M ? (FUSED ? gs_lds[(g - g0) * M + m] : L.gs[(size_t)g * M + m])
+                                  : float2{0.f, 0.f};
             }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -314,9 +276,11 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
             const float sz = s * (float)(((zw >> (4 * u)) & 15u) + 1u);
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                acc[u][t] += s * c[u][t];
-                acc[u][t][0] -= sz * sx[t][0];
-                acc[u][t][2] -= sz * sx[t][1];
+                const float sb0 = s * gsr[t][0].x, sb1 = s * gsr[t][1].x;
+                acc[u][t][0] += sb0 * c[u][t][0] - sz * gsr[t][0].y;
+                acc[u][t][1] += sb0 * c[u][t][1];
+                acc[u][t][2] += sb1 * c[u][t][2] - sz * gsr[t][1].y;
+                acc[u][t][3] += sb1 * c[u][t][3];
             }
         }
     }
@@ -327,20 +291,8 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
 #pragma unroll
         for (int t = 0; t < T; t++) {
             const int m0 = 8 * t + 2 * kq;
-            float b0, b1;
-            if (FUSED) {
-                b0 = bscale[0]; b1 = bscale[0];
-#pragma unroll
-                for (int mm = 1; mm < kGemvFusedMaxM; mm++) {
-                    if (mm == m0) b0 = bscale[mm];
-                    if (mm == m0 + 1) b1 = bscale[mm];
-                }
-            } else {
-                b0 = m0 < M ? L.bscale[m0] : 0.f;
-                b1 = m0 + 1 < M ? L.bscale[m0 + 1] : 0.f;
-            }
-            if (m0 < M) red[wave][m0][4 * j + u] = (acc[u][t][0] + acc[u][t][1]) * b0;
-            if (m0 + 1 < M) red[wave][m0 + 1][4 * j + u] = (acc[u][t][2] + acc[u][t][3]) * b1;
+            if (m0 < M) red[wave][m0][4 * j + u] = acc[u][t][0] + acc[u][t][1];
+            if (m0 + 1 < M) red[wave][m0 + 1][4 * j + u] = acc[u][t][2] + acc[u][t][3];
         }
     }
     __syncthreads();
@@ -465,9 +417,9 @@ GemvShape gemv_shape(int M, int N, int K, int group)
     s.waves = kGemvWaves;
     s.split = (slices + kGemvWaves - 1) / kGemvWaves;
     if (gemv_fused(M)) {
-        // the segment's split activations (2M rows x group/8 chunks x 16 B) plus its group sums
-        // (M floats per group) must fit the LDS budget
-        int max_groups = kGemvLdsXsBytes / (4 * M * group + 4 * M);
+        // the segment's split activations (2M rows x group/8 chunks x 16 B) plus its per-group
+        // {scale, sum} pairs (M float2 per group) must fit the LDS budget
+        int max_groups = kGemvLdsXsBytes / (4 * M * group + 8 * M);
         if (max_groups < 1) max_groups = 1;
         const int need = (s.groups + max_groups - 1) / max_groups;
         if (s.split < need) s.split = need;
@@ -477,13 +429,13 @@ GemvShape gemv_shape(int M, int N, int K, int group)
     return s;
 }
 
-// scratch layout for M > 4: xs [K/8][2M] uint4, then Sx' [G][M] f32, then 2^(16-E) [M] f32
+// scratch layout for M > 4: xs [K/8][2M] uint4, then gs [K/group][M] float2
 uint64_t gemv_xs_bytes(int M, int K)
 {
     if (gemv_fused(M)) return 0;
     const uint64_t xs = (uint64_t)4 * M * K;
-    const uint64_t sx = (uint64_t)4 * M * (K / 32 + 1) + 4 * (uint64_t)M;
-    return (xs + sx + 255) & ~(uint64_t)255;
+    const uint64_t gs = (uint64_t)8 * M * (K / 32);
+    return (xs + gs + 255) & ~(uint64_t)255;
 }
 
 uint64_t gemv_partial_bytes(int M, int N, int split)
@@ -495,8 +447,7 @@ uint64_t gemv_partial_bytes(int M, int N, int split)
 void gemv_xs_layout(GemvLinear& L, char* base, int M)
 {
     L.xs = reinterpret_cast<const uint4*>(base);
-    L.sxs = reinterpret_cast<const float*>(base + (size_t)4 * M * L.K);
-    L.bscale = L.sxs + (size_t)M * (L.K / L.group);
+    L.gs = reinterpret_cast<const float2*>(base + (size_t)4 * M * L.K);
 }
 
 hipError_t launch_gemv_batch(const GemvBatch& b, hipStream_t stream)
@@ -510,11 +461,20 @@ hipError_t launch_gemv_batch(const GemvBatch& b, hipStream_t stream)
         for (int i = 0; i < b.count; i++) {
             const int G = b.L[i].K / group;
             const int gmax = (G + b.L[i].split - 1) / b.L[i].split;
-            lds = max(lds, (size_t)gmax * kb * 4 * (2 * b.M) * 16 + (size_t)gmax * b.M * 4);
+            lds = max(lds, (size_t)gmax * kb * 4 * (2 * b.M) * 16 + (size_t)gmax * b.M * 8);
         }
         return launch_tiles<1, true>(b, kb, lds, stream);
     }
-    hipLaunchKernelGGL(xsplit_kernel, dim3(b.M, b.count), dim3(256), 0, stream, b);
+    int lanes = 0;
+    for (int i = 0; i < b.count; i++) lanes = max(lanes, (b.L[i].K >> 3) * b.M);
+    const dim3 xg((lanes + 255) / 256, b.count);
+    switch (kb) {
+    case 1: hipLaunchKernelGGL(xsplit_kernel<4>, xg, dim3(256), 0, stream, b); break;
+    case 2: hipLaunchKernelGGL(xsplit_kernel<8>, xg, dim3(256), 0, stream, b); break;
+    case 4: hipLaunchKernelGGL(xsplit_kernel<16>, xg, dim3(256), 0, stream, b); break;
+    case 8: hipLaunchKernelGGL(xsplit_kernel<32>, xg, dim3(256), 0, stream, b); break;
+    default: return hipErrorInvalidValue;
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return b.M <= 8 ? launch_tiles<1, false>(b, kb, 0, stream) : launch_tiles<2, false>(b, kb, 0, stream);

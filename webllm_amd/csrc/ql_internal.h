@@ -20,8 +20,7 @@ struct GemvLinear {
     const float* bias;         // [N] or nullptr
     const void* x;             // [M, K] f32 or f16
     const uint4* xs;           // M > 4: prepared activations [K/8][2M] (gemv_xs_layout)
-    const float* sxs;          // M > 4: scaled group sums of x [K/group][M]
-    const float* bscale;       // M > 4: per-row 2^(16-E)
+    const float2* gs;          // M > 4: per (group, row) {2^(16-E), sum of x} [K/group][M]
     float* y;                  // [M, N]
     float* partial;            // [split, M, N] (split > 1)
     uint32_t* counters;        // per-strip arrival counters (split > 1), zero between launches

@@ -10,6 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 import re
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -158,6 +159,7 @@ class Arena:
         self.ctx = ctx
         self.handle = h
         self.size = nbytes
+        ctx._owned.add(self)
 
     def write(self, off: int, data: np.ndarray | bytes):
         buf = np.ascontiguousarray(np.frombuffer(data, dtype=np.uint8) if isinstance(data, bytes)
@@ -189,6 +191,7 @@ class Graph:
     def __init__(self, ctx: "Context", handle):
         self.ctx = ctx
         self.handle = handle
+        ctx._owned.add(self)
 
     def launch(self):
         _check(lib().ql_graph_launch(self.ctx.handle, self.handle))
@@ -206,6 +209,7 @@ class Context:
         h = ctypes.c_void_p()
         _check(lib().ql_create(device, ctypes.byref(h)))
         self.handle = h
+        self._owned = weakref.WeakSet()    # arenas and graphs, released before the context
 
     def info(self) -> dict:
         name = ctypes.create_string_buffer(256)
@@ -262,6 +266,12 @@ class Context:
 
     def destroy(self):
         if self.handle:
+            for obj in list(self._owned):
+                if isinstance(obj, Graph):
+                    obj.destroy()
+            for obj in list(self._owned):
+                if isinstance(obj, Arena):
+                    obj.release()
             _check(lib().ql_destroy(self.handle))
             self.handle = None
 
