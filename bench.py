@@ -265,6 +265,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
                     help="all | step05 | step7b | sweep | prefill | unpack (profiling subsets)")
+    ap.add_argument("--m7b", default="1,4,16", help="decode batch sizes for the 7B-shaped step")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -353,7 +354,7 @@ def main():
         m7 = Model(ctx, "7b", seed=0x7B)
         log(f"7B weights: {m7.weight_bytes/1e9:.2f} GB uploaded in {time.time()-t0:.1f}s")
         s7 = {}
-        for M in (1, 4, 16):
+        for M in [int(v) for v in args.m7b.split(",")]:
             st = Step(ctx, m7, M)
             ms = timed(st, max(10, args.steps // 2), 2)
             gbs = st.bytes / (ms * 1e-3) / 1e9

@@ -95,7 +95,7 @@ int plan_impl(int M, int N, int K, int group, ql_plan* p)
             p->grid_x = s.strips * s.split;
             p->grid_y = 1;
             p->block = 256;
-            p->scratch_bytes = ql::gemv_xs_bytes(M, K) + ql::gemv_partial_bytes(M, N, s.split);
+            p->scratch_bytes = ql::gemv_partial_bytes(M, N, s.split);
         } else {
             p->kind = QL_KIND_GEMV_SIMPLE;
             p->split = 1;
@@ -171,9 +171,10 @@ ql::GemvLinear make_linear(const ql_gptq_desc* d, const ql_arena* w)
     return L;
 }
 
-bool gemv_aligned(const ql_gptq_desc* d, uint64_t x_off)
+bool gemv_aligned(const ql_gptq_desc* d, uint64_t x_off, uint64_t y_off)
 {
-    return d->qweight_off % 16 == 0 && d->scales_off % 8 == 0 && x_off % 16 == 0;
+    return d->qweight_off % 16 == 0 && d->scales_off % 8 == 0 && x_off % 16 == 0 && y_off % 16 == 0 &&
+           (d->bias_off == QL_NONE || d->bias_off % 16 == 0);
 }
 
 int check_io(const ql_gptq_desc* d, const ql_arena* act, uint64_t x_off, int x_dtype, int M,
@@ -403,7 +404,7 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_ar
     L.x = act->base + x_off;
     L.y = reinterpret_cast<float*>(act->base + y_off);
 
-    if (p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(d, x_off)) {
+    if (p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(d, x_off, y_off)) {
         if (!in_range(scratch_off, p.scratch_bytes, act->size))
             return fail(QL_E_RANGE, "scratch (%llu bytes) outside the activation arena",
                         (unsigned long long)p.scratch_bytes);
@@ -413,9 +414,7 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_ar
         L.split = s.split;
         L.strips = s.strips;
         L.wg_begin = 0;
-        L.xs_owner = 1;
-        ql::gemv_xs_layout(L, act->base + scratch_off, M);
-        L.partial = reinterpret_cast<float*>(act->base + scratch_off + ql::gemv_xs_bytes(M, d->K));
+        L.partial = reinterpret_cast<float*>(act->base + scratch_off);
         L.counters = ctx->counters;
         if (s.strips > ql::kCounterCapacity) return fail(QL_E_INVALID, "N too large (%d)", d->N);
         b.L[0] = L;
@@ -484,7 +483,7 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
         if ((rc = check_io(&descs[i], act, x_offs[i], x_dtype, M, y_offs[i]))) return rc;
         ql_plan p;
         plan_impl(M, descs[i].N, descs[i].K, descs[i].group, &p);
-        fused &= p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(&descs[i], x_offs[i]) &&
+        fused &= p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(&descs[i], x_offs[i], y_offs[i]) &&
                  descs[i].group == descs[0].group;
     }
     if (!fused) {
@@ -514,22 +513,11 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
         L.split = s.split;
         L.strips = s.strips;
         L.wg_begin = wg;
-        // linears reading the same x with the same K share one split-activation buffer
-        int owner = -1;
-        for (int k = 0; k < i; k++)
-            if (x_offs[k] == x_offs[i] && descs[k].K == d->K) { owner = k; break; }
-        L.xs_owner = owner < 0;
-        if (owner < 0) {
-            ql::gemv_xs_layout(L, act->base + off, M);
-        } else {
-            L.xs = b.L[owner].xs;
-            L.gs = b.L[owner].gs;
-        }
-        L.partial = reinterpret_cast<float*>(act->base + off + ql::gemv_xs_bytes(M, d->K));
+        L.partial = reinterpret_cast<float*>(act->base + off);
         L.counters = ctx->counters + counter_base;
         counter_base += s.strips;
         if (counter_base > ql::kCounterCapacity) return fail(QL_E_INVALID, "batch too wide");
-        off += align256(ql::gemv_xs_bytes(M, d->K) + ql::gemv_partial_bytes(M, d->N, s.split));
+        off += align256(ql::gemv_partial_bytes(M, d->N, s.split));
         wg += s.strips * s.split;
         b.L[i] = L;
     }

@@ -3,32 +3,29 @@
 // Replaces the reference's gemm_gemv_f16 / gemm_gemv_split_f16 + gemm_gemv_split_reduce pair
 // (src/gpu/kernels/gemm/*.wgsl, dispatched by src/model/qwen.ts:568-610), which streams fp16
 // weights that the CPU dequantized at load time. Here the weights stay packed (4 bits/weight)
-// and are unpacked in registers; the multiply-adds run on MFMA.
+// and the products run on the int8 matrix cores with exact integer accumulation.
 //
-// Arithmetic (tracks the reference CPU path — fp32 weights, double accumulation — to ~1e-6):
-//   y[m,n] = sum_g s[g,n] * ( sum_{k in g} q[k,n] * x[m,k]  -  z[g,n] * Sx[g,m] ),
-//   Sx[g,m] = sum_{k in g} x[m,k]   (fp32, fixed order).
-// * q is taken straight from the packed word by shifting and masking: a nibble at bits 4-7 of a
-//   16-bit half is an exact fp16 subnormal q * 2^-20 (7 integer ops per packed word of 8
-//   weights, no conversions). Bits 4-7 and not 0-3: MFMA products with operands at the bottom of
-//   the subnormal range (q * 2^-24) were measured to lose ~1e-6 relative accuracy, bits 4-7 none.
-// * x is scaled per (row, group) by a power of two 2^E (range normalisation:
-//   max_{k in g} |x| * 2^E * 16 < 2^15), times the factor 16 matching the nibble position; the
-//   scaled value a is split into a_hi = f16(a), a_lo = f16(a - a_hi), so each row m becomes two
-//   MFMA rows and every product is exact in the fp32 accumulator. The group's products carry
-//   2^(E-16), removed with the group scale in the group epilogue. 16 lanes own one group of one
-//   row: max, exponent, split and group sum are one pass with 16-lane butterflies.
-// One v_mfma_f32_16x16x32_f16 consumes 4 packed rows (32 k) of 16 columns: each lane feeds one
-// packed word of one column, which is exactly the B-operand fragment (8 k of one column).
+// Arithmetic (tracks the reference CPU path — fp32 weights, double accumulation — to ~1e-7):
+//   y[m,n] = sum_g s[g,n] * ( 2^-E[g,m] * sum_{k in g} q[k,n] * X[m,k] * 2^-24  -  z[g,n] * Sx[g,m] )
+//   X[m,k] = round(x[m,k] * 2^(E+24)),  E[g,m] chosen so max_{k in g} |x| * 2^E < 64,
+//   Sx[g,m] = sum_{k in g} x[m,k]  (fp32, fixed order).
+// * q: a packed word w holds 8 nibbles; w & 0x0F0F0F0F and (w >> 4) & 0x0F0F0F0F are 8 int8
+//   values (3 integer ops per word, no conversions).
+// * X is split into 4 signed base-256 digits: with V = (X + 0x808080) ^ 0x808080 the four bytes
+//   of V are exactly the two's-complement digits b0..b3, X = sum_i b_i 256^i. Each digit is one
+//   MFMA row (row 4m + i), so v_mfma_i32_16x16x64_i8 gives exact int32 dot products sum q*b_i;
+//   the group epilogue combines them in fp32 (x precision ~2^-30 of the group maximum).
+// * Per 64-k block a lane feeds packed rows 2kq, 2kq+1 of one column (16 nibbles); the
+//   activation digits are staged in the same byte order, so the dot product is unchanged.
 //
-// Work split: a workgroup (4 waves) owns 64 output columns and one K segment (a range of whole
-// quantization groups); its waves take the segment's groups round-robin and are reduced through
-// LDS in wave order. With split > 1 segments, each workgroup stores its partial sums with
-// agent-scope (cross-XCD coherent) stores and bumps a per-strip arrival counter; the last one
-// adds the partials in ascending segment order — deterministic, like the reference's two-pass
-// reduce (gemm_gemv_split_reduce.wgsl:32-38), in one launch — and resets the counter.
-// Agent-scope *fences* are avoided on purpose: on this part they write back and invalidate the
-// whole L2, which was measured to cost more than the GEMV itself.
+// Work split: a workgroup (4 waves) owns 256 output columns (64 per wave) and one K segment of
+// whole quantization groups; the segment's activation digits are built once in LDS and shared by
+// the 4 waves. Each wave streams its columns' groups with kPrefetch groups of packed words in
+// flight. With split > 1 segments, each workgroup stores its partial sums with agent-scope
+// (cross-XCD coherent) stores and bumps a per-strip arrival counter; the last one adds the
+// partials in ascending segment order — deterministic, like the reference's two-pass reduce
+// (gemm_gemv_split_reduce.wgsl:32-38), in one launch — and resets the counter. Agent-scope
+// *fences* are avoided on purpose: on this part they write back and invalidate the whole L2.
 #include "ql_device.h"
 #include "ql_internal.h"
 
@@ -36,20 +33,38 @@ namespace ql {
 
 namespace {
 
-constexpr int kTargetWaves = 4096;
-constexpr int kGemvFusedMaxM = 4;          // M <= 4: activations prepared in the kernel prologue
-constexpr int kGemvLdsXsBytes = 32768;     // LDS budget for them (per workgroup)
+// Tunables (compile-time; the defaults are the measured best on MI355X):
+//   QL_GEMV_TARGET_WAVES  waves a launch aims for (K segments per column strip follow from it)
+//   QL_GEMV_PREFETCH      groups each wave keeps in flight ahead of the one it multiplies
+//   QL_GEMV_MIN_GROUPS    fewest quantization groups per K segment (caps the split)
+#ifndef QL_GEMV_TARGET_WAVES
+#define QL_GEMV_TARGET_WAVES 1024
+#endif
+#ifndef QL_GEMV_MIN_GROUPS
+#define QL_GEMV_MIN_GROUPS 2
+#endif
+#ifndef QL_GEMV_PREFETCH
+#define QL_GEMV_PREFETCH 2
+#endif
+constexpr int kTargetWaves = QL_GEMV_TARGET_WAVES;
+constexpr int kPrefetch = QL_GEMV_PREFETCH;
+constexpr int kMinGroupsPerWave = QL_GEMV_MIN_GROUPS;   // split-K stops where segments get shorter
+constexpr int kLdsBudget = 49152;          // activation digits + group stats per workgroup
 
-// Factor folded into the activations: every nibble arrives as q * 2^-20.
-constexpr float kActScale = 16.f;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-// Exponent E with max|x| * 2^E * 16 < 2^15 (E = 0 when all values are zero).
-__device__ __forceinline__ int row_exponent(float amax)
+__device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c)
+{
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Exponent E with max|x| * 2^E < 64 (E = 0 when all values are zero).
+__device__ __forceinline__ int group_exponent(float amax)
 {
     if (!(amax > 0.f)) return 0;
     int ex;
     (void)frexpf(amax, &ex);                 // amax < 2^ex
-    int E = 11 - ex;
+    const int E = 6 - ex;
     return E < -100 ? -100 : (E > 100 ? 100 : E);
 }
 
@@ -68,38 +83,33 @@ __device__ __forceinline__ void load8(const void* x, int x_dtype, size_t base, f
     }
 }
 
-// 8 activations (natural k order) -> scaled hi/lo fp16 fragments in perm_k slot order.
-__device__ __forceinline__ void split8(const float v[8], float scale, uint4* hi_out, uint4* lo_out)
+// 4x4 byte transpose: out[i] = byte i of (a, b, c, d), packed low to high.
+__device__ __forceinline__ void byte_transpose(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                               uint32_t out[4])
 {
-    f16x8 hi, lo;
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float a = v[perm_k(e)] * (scale * kActScale);
-        const _Float16 h = (_Float16)a;
-        hi[e] = h;
-        lo[e] = (_Float16)(a - (float)h);
-    }
-    *hi_out = __builtin_bit_cast(uint4, hi);
-    *lo_out = __builtin_bit_cast(uint4, lo);
+    const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);   // a0 b0 a1 b1
+    const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);   // a2 b2 a3 b3
+    const uint32_t cd_lo = __builtin_amdgcn_perm(d, c, 0x05010400u);
+    const uint32_t cd_hi = __builtin_amdgcn_perm(d, c, 0x07030602u);
+    out[0] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);         // a0 b0 c0 d0
+    out[1] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);         // a1 b1 c1 d1
+    out[2] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);
+    out[3] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);
 }
 
-// 8 nibbles of a packed word as exact fp16 subnormals q * 2^-20, in perm_k slot order.
-__device__ __forceinline__ f16x8 nibbles_subnormal(uint32_t w)
+// Signed base-256 digits of round(v * scale): byte i of the result is digit i.
+__device__ __forceinline__ uint32_t digits_of(float v, float scale)
 {
-    const uint32_t p0 = (w << 4) & 0x00F000F0u;   // k0, k4
-    const uint32_t p1 = w & 0x00F000F0u;          // k1, k5
-    const uint32_t p2 = (w >> 4) & 0x00F000F0u;   // k2, k6
-    const uint32_t p3 = (w >> 8) & 0x00F000F0u;   // k3, k7
-    const f16x2 a = as_f16x2(p0), b = as_f16x2(p1), c = as_f16x2(p2), d = as_f16x2(p3);
-    return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+    const int X = (int)rintf(v * scale);
+    return ((uint32_t)X + 0x00808080u) ^ 0x00808080u;
 }
 
-// One 8-k chunk of activations, owned by one of CPG lanes (CPG = group / 8, consecutive lanes)
-// that together hold one quantization group of one row: returns the group's {2^(16-E), Sx} to
-// every lane and writes the lane's scaled hi/lo fragments. Butterfly reductions give every lane
-// the same bits (IEEE addition is commutative), so the result does not depend on the lane.
+// Activation digits for one 8-k chunk, owned by one of CPG lanes (CPG = group / 8, consecutive
+// lanes) that together hold one quantization group of one row. Writes the chunk's digit rows
+// (8 bytes each, k order {0,2,4,6,1,3,5,7}) and returns the group's {2^-E, Sx} to every lane.
+// Butterfly reductions give every lane identical bits (IEEE addition is commutative).
 template <int CPG>
-__device__ __forceinline__ float2 prep_group_chunk(const float v[8], uint4* hi_out, uint4* lo_out)
+__device__ __forceinline__ float2 prep_chunk(const float v[8], uint2* rows, int row_stride)
 {
     float amax = 0.f;
 #pragma unroll
@@ -110,42 +120,23 @@ __device__ __forceinline__ float2 prep_group_chunk(const float v[8], uint4* hi_o
         amax = fmaxf(amax, __shfl_xor(amax, off));
         sum += __shfl_xor(sum, off);
     }
-    const int E = row_exponent(amax);
-    split8(v, ldexpf(1.f, E), hi_out, lo_out);
-    return float2{ldexpf(1.f, 16 - E), sum};
+    const int E = group_exponent(amax);
+    const float scale = ldexpf(1.f, E + 24);
+    uint32_t ev[4], od[4];
+    byte_transpose(digits_of(v[0], scale), digits_of(v[2], scale), digits_of(v[4], scale),
+                   digits_of(v[6], scale), ev);
+    byte_transpose(digits_of(v[1], scale), digits_of(v[3], scale), digits_of(v[5], scale),
+                   digits_of(v[7], scale), od);
+#pragma unroll
+    for (int i = 0; i < 4; i++) rows[i * row_stride] = uint2{ev[i], od[i]};
+    return float2{ldexpf(1.f, -E), sum};
 }
 
-// Activations of a linear with M > 4, prepared once per call:
-//   xs[c * 2M + 2m + h] (h: hi/lo) for every 8-k chunk c; gs[g * M + m] = {2^(16-E), Sx[g,m]}.
-// group/8 lanes per (group, row); grid.x covers G * M * group/8 lanes, grid.y the batch.
-template <int CPG>
-__global__ __launch_bounds__(256) void xsplit_kernel(const GemvBatch b)
-{
-    const GemvLinear& L = b.L[blockIdx.y];
-    if (!L.xs_owner) return;
-    const int M = b.M;
-    const int G = L.K / L.group;
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    const int item = idx / CPG;                        // (group, row) pair, uniform per CPG lanes
-    if (item >= G * M) return;
-    const int c = idx - item * CPG;
-    const int cpg = CPG;
-    const int g = item / M;
-    const int m = item - g * M;
-    const int chunk = g * cpg + c;
-    float v[8];
-    load8(L.x, b.x_dtype, (size_t)m * L.K + (size_t)chunk * 8, v);
-    uint4* xs = const_cast<uint4*>(L.xs);
-    const float2 gs = prep_group_chunk<CPG>(v, &xs[(size_t)chunk * 2 * M + 2 * m],
-                                       &xs[(size_t)chunk * 2 * M + 2 * m + 1]);
-    if (c == 0) const_cast<float2*>(L.gs)[(size_t)g * M + m] = gs;
-}
-
-template <int T, int KB, bool FUSED>
+template <int T, int NB>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
 {
-    extern __shared__ uint4 dyn_lds[];        // FUSED: split activations + Sx of this segment
-    __shared__ float red[kGemvWaves][kGemvMaxM][kGemvCols];
+    // dynamic LDS: activation digits [segment block][kq][row] (16 B), then {2^-E, Sx}[group][m]
+    extern __shared__ uint4 dyn_lds[];
     __shared__ uint32_t is_last;
 
     int wg = blockIdx.x;
@@ -165,153 +156,163 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
     const int seg = wg / L.strips;
 
     const int M = b.M;
-    const int R = 2 * M;
+    const int R = 4 * M;                      // MFMA rows: 4 digits per activation row
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int j = lane & 15;
     const int kq = lane >> 4;
     const int NC = (N + 7) >> 3;
-    const int n = strip * kGemvCols + 4 * j;
+    const int n = strip * kGemvStripCols + wave * 64 + 4 * j;
     const bool col_ok = n < N;
-    const int G = K / (KB * 32);
+    const int G = K / (NB * 64);
     const int g0 = (int)((int64_t)G * seg / split);
     const int g1 = (int)((int64_t)G * (seg + 1) / split);
-    const int p0 = g0 * KB * 4;               // first packed row (8-k chunk) of the segment
-    const int chunks = (g1 - g0) * KB * 4;
+    const int gseg = g1 - g0;
 
-    // software pipeline: the next group's packed words, zeros and scales are in flight while
-    // the current group is unpacked and multiplied
-    uint4 wn[KB];
-    uint32_t zn = 0x77777777u;
-    uint2 sn = uint2{0u, 0u};
-    auto fetch = [&](int g) {
+    uint4* xd = dyn_lds;                                                   // digits
+    float2* gst = reinterpret_cast<float2*>(dyn_lds + gseg * NB * 4 * R);  // group stats
+
+    // software pipeline: each wave keeps the packed words, zeros and scales of its next
+    // kPrefetch groups in flight (static register slots; the group loop is unrolled by
+    // kPrefetch). Every load is unconditional — past-the-end groups and columns are clamped to
+    // valid addresses and contribute with scale 0 — so the loop is straight-line and the
+    // compiler waits for exactly the slot it consumes.
+    const int n_ld = col_ok ? n : N - 4;
+    uint4 wb[kPrefetch][2 * NB];
+    uint32_t zb[kPrefetch];
+    uint2 sb[kPrefetch];
+    auto fetch = [&](int d, int g) {
+        g = min(g, g1 - 1);
 #pragma unroll
-        for (int kb = 0; kb < KB; kb++)
-            wn[kb] = *reinterpret_cast<const uint4*>(qweight + (size_t)((g * KB + kb) * 4 + kq) * N + n);
-        if (qzeros) zn = qzeros[(size_t)g * NC + (n >> 3)];
-        sn = *reinterpret_cast<const uint2*>(scales + (size_t)g * N + n);
+        for (int r = 0; r < 2 * NB; r++) {
+            const int prow = (g * NB + (r >> 1)) * 8 + 2 * kq + (r & 1);
+            wb[d][r] = *reinterpret_cast<const uint4*>(qweight + (size_t)prow * N + n_ld);
+        }
+        zb[d] = qzeros ? qzeros[(size_t)g * NC + (n_ld >> 3)] : 0x77777777u;
+        sb[d] = *reinterpret_cast<const uint2*>(scales + (size_t)g * N + n_ld);
     };
 #pragma unroll
-    for (int kb = 0; kb < KB; kb++) wn[kb] = uint4{0u, 0u, 0u, 0u};
-    int g = g0 + wave;
-    if (g < g1 && col_ok) fetch(g);
+    for (int d = 0; d < kPrefetch; d++) fetch(d, g0 + d);
 
-    uint4* xs_lds = dyn_lds;
-    float2* gs_lds = reinterpret_cast<float2*>(dyn_lds + (FUSED ? chunks * R : 0));
-    if (FUSED) {
-        // the segment's activations: KB*4 lanes per (group, row), one chunk of 8 k per lane
-        constexpr int CPG = KB * 4;
-        const int items = (g1 - g0) * M;
+    {
+        // the segment's activation digits: 8*NB lanes per (group, row), one 8-k chunk per lane
+        constexpr int CPG = NB * 8;
+        const int items = gseg * M;
         for (int base = 0; base < items * CPG; base += 256) {
             const int idx = base + threadIdx.x;
             const int item = idx / CPG;                 // uniform per CPG lanes
             if (item < items) {
-                const int cl = idx - item * CPG;
+                const int c = idx - item * CPG;         // chunk within the group
                 const int gg = item / M;
                 const int m = item - gg * M;
-                const int c = gg * CPG + cl;            // chunk within the segment
                 float v[8];
-                load8(L.x, b.x_dtype, (size_t)m * K + (size_t)(p0 + c) * 8, v);
-                const float2 gsv = prep_group_chunk<CPG>(v, &xs_lds[c * R + 2 * m], &xs_lds[c * R + 2 * m + 1]);
-                if (cl == 0) gs_lds[gg * M + m] = gsv;
+                load8(L.x, b.x_dtype, (size_t)m * K + (size_t)(g0 + gg) * (NB * 64) + (size_t)c * 8, v);
+                const int blk = gg * NB + (c >> 3);     // 64-k block within the segment
+                const int ckq = (c & 7) >> 1;
+                uint2* rows = reinterpret_cast<uint2*>(&xd[(blk * 4 + ckq) * R + 4 * m]) + (c & 1);
+                const float2 st = prep_chunk<CPG>(v, rows, 2);
+                if (c == 0) gst[gg * M + m] = st;
             }
         }
         __syncthreads();
     }
 
-    f32x4 acc[4][T];
+    float acc[4][T];
 #pragma unroll
     for (int u = 0; u < 4; u++)
 #pragma unroll
-        for (int t = 0; t < T; t++) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < T; t++) acc[u][t] = 0.f;
 
-    for (; g < g1; g += kGemvWaves) {
-        uint4 w[KB];
-#pragma unroll
-        for (int kb = 0; kb < KB; kb++) w[kb] = wn[kb];
-        const uint32_t zw = qzeros ? (zn >> (4 * (n & 7))) : 0x7777u;
-        const uint2 sv = sn;
-        if (g + kGemvWaves < g1 && col_ok) fetch(g + kGemvWaves);
-
-        f32x4 c[4][T];
+    auto consume = [&](int gg, const uint4* w, uint32_t zn, uint2 sv) {
+        i32x4 c[4][T];
 #pragma unroll
         for (int u = 0; u < 4; u++)
 #pragma unroll
-            for (int t = 0; t < T; t++) c[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < T; t++) c[u][t] = i32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int kb = 0; kb < KB; kb++) {
-            const int p = (g * KB + kb) * 4 + kq;
-            f16x8 a[T];
+        for (int bb = 0; bb < NB; bb++) {
+            i32x4 a[T];
 #pragma unroll
             for (int t = 0; t < T; t++) {
                 const int row = 16 * t + j;
-                if (row < R)
-                    a[t] = __builtin_bit_cast(f16x8, FUSED ? xs_lds[(p - p0) * R + row]
-                                                           : L.xs[(size_t)p * R + row]);
-                else
-                    a[t] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                a[t] = row < R ? __builtin_bit_cast(i32x4, xd[((gg * NB + bb) * 4 + kq) * R + row])
+                               : i32x4{0, 0, 0, 0};
             }
-            const uint32_t words[4] = {w[kb].x, w[kb].y, w[kb].z, w[kb].w};
+            const uint4 w0 = w[2 * bb], w1 = w[2 * bb + 1];
+            const uint32_t lo[4] = {w0.x, w0.y, w0.z, w0.w};
+            const uint32_t hi[4] = {w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const f16x8 bq = nibbles_subnormal(words[u]);
+                const i32x4 bq = i32x4{(int)(lo[u] & 0x0F0F0F0Fu), (int)((lo[u] >> 4) & 0x0F0F0F0Fu),
+                                       (int)(hi[u] & 0x0F0F0F0Fu), (int)((hi[u] >> 4) & 0x0F0F0F0Fu)};
 #pragma unroll
-                for (int t = 0; t < T; t++) c[u][t] = mfma_16x16x32_f16(a[t], bq, c[u][t]);
+                for (int t = 0; t < T; t++) c[u][t] = mfma_i8(a[t], bq, c[u][t]);
             }
         }
-        // group epilogue: acc += s * 2^(16-E) * C (all rows), acc -= s * z * Sx (hi rows only)
+        // group epilogue: lane (j, kq) holds, per tile t, digits 0..3 of row m = 4t + kq
+        const uint32_t zw = zn >> (4 * (n & 7));
         const uint32_t sw[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
-        float2 gsr[T][2];
+        float2 st[T];
 #pragma unroll
-        for (int t = 0; t < T; t++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int m = 8 * t + 2 * kq + h;
-                gsr[t][h] = m < M ? (FUSED ? gs_lds[(g - g0) * M + m] : L.gs[(size_t)g * M + m])
-                                  : float2{0.f, 0.f};
-            }
+        for (int t = 0; t < T; t++) {
+            const int m = 4 * t + kq;
+            st[t] = m < M ? gst[gg * M + m] : float2{0.f, 0.f};
+        }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
             const float sz = s * (float)(((zw >> (4 * u)) & 15u) + 1u);
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                const float sb0 = s * gsr[t][0].x, sb1 = s * gsr[t][1].x;
-                acc[u][t][0] += sb0 * c[u][t][0] - sz * gsr[t][0].y;
-                acc[u][t][1] += sb0 * c[u][t][1];
-                acc[u][t][2] += sb1 * c[u][t][2] - sz * gsr[t][1].y;
-                acc[u][t][3] += sb1 * c[u][t][3];
+                float v = fmaf((float)c[u][t][0], 0x1p-8f, (float)c[u][t][1]);
+                v = fmaf(v, 0x1p-8f, (float)c[u][t][2]);
+                v = fmaf(v, 0x1p-8f, (float)c[u][t][3]);            // sum q * X * 2^-24
+                acc[u][t] = fmaf(s * st[t].x, v, acc[u][t]);
+                acc[u][t] = fmaf(-sz, st[t].y, acc[u][t]);
             }
         }
+    };
+
+    for (int ib = 0; ib < gseg; ib += kPrefetch) {
+#pragma unroll
+        for (int d = 0; d < kPrefetch; d++) {
+            const int i = ib + d;
+            uint4 w[2 * NB];
+#pragma unroll
+            for (int r = 0; r < 2 * NB; r++) w[r] = wb[d][r];
+            const uint32_t zn = zb[d];
+            const uint2 sv = col_ok ? sb[d] : uint2{0u, 0u};
+            fetch(d, g0 + i + kPrefetch);
+            if (i < gseg) consume(i, w, zn, sv);
+        }
     }
 
-    // MFMA D layout: lane (j, kq) holds rows 4kq..4kq+3 of column j; rows are (m, hi/lo) pairs.
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
+    // results: lane holds y[4t + kq][n + u] in acc[u][t]
+    if (split == 1) {
 #pragma unroll
         for (int t = 0; t < T; t++) {
-            const int m0 = 8 * t + 2 * kq;
-            if (m0 < M) red[wave][m0][4 * j + u] = acc[u][t][0] + acc[u][t][1];
-            if (m0 + 1 < M) red[wave][m0 + 1][4 * j + u] = acc[u][t][2] + acc[u][t][3];
+            const int m = 4 * t + kq;
+            if (m < M && col_ok) {
+                float4 o = float4{acc[0][t], acc[1][t], acc[2][t], acc[3][t]};
+                if (L.bias) {
+                    const float4 bv = *reinterpret_cast<const float4*>(L.bias + n);
+                    o.x += bv.x; o.y += bv.y; o.z += bv.z; o.w += bv.w;
+                }
+                *reinterpret_cast<float4*>(L.y + (size_t)m * N + n) = o;
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const int m = 4 * t + kq;
+        if (m < M && col_ok) {
+            float* p = L.partial + ((size_t)seg * M + m) * N + n;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                __hip_atomic_store(p + u, acc[u][t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    __syncthreads();
-
-    for (int idx = threadIdx.x; idx < M * kGemvCols; idx += 256) {
-        const int m = idx >> 6;
-        const int col = idx & 63;
-        const int nn = strip * kGemvCols + col;
-        if (nn >= N) continue;
-        const float sum = ((red[0][m][col] + red[1][m][col]) + red[2][m][col]) + red[3][m][col];
-        if (split == 1) {
-            L.y[(size_t)m * N + nn] = L.bias ? sum + L.bias[nn] : sum;
-        } else {
-            __hip_atomic_store(&L.partial[((size_t)seg * M + m) * N + nn], sum, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    if (split == 1) return;
-
     // this wave's partial stores are complete (written through to the coherence point) before
     // the workgroup signals arrival
     __builtin_amdgcn_s_waitcnt(0);
@@ -325,15 +326,26 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const GemvBatch b)
     }
     __syncthreads();
     if (!is_last) return;
-    for (int idx = threadIdx.x; idx < M * kGemvCols; idx += 256) {
-        const int m = idx >> 6;
-        const int col = idx & 63;
-        const int nn = strip * kGemvCols + col;
+    for (int idx = threadIdx.x; idx < M * kGemvStripCols; idx += 256) {
+        const int m = idx / kGemvStripCols;
+        const int nn = strip * kGemvStripCols + (idx - m * kGemvStripCols);
         if (nn >= N) continue;
+        // coherent loads in batches of 8 (issued together, one wait per batch), summed in
+        // ascending segment order
+        const float* pp = L.partial + (size_t)m * N + nn;
+        const size_t stride = (size_t)M * N;
         float sum = 0.f;
-        for (int s2 = 0; s2 < split; s2++)
-            sum += __hip_atomic_load(&L.partial[((size_t)s2 * M + m) * N + nn], __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+        for (int s0 = 0; s0 < split; s0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                v[e] = s0 + e < split ? __hip_atomic_load(pp + (size_t)(s0 + e) * stride, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                                      : 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (s0 + e < split) sum += v[e];
+        }
         L.y[(size_t)m * N + nn] = L.bias ? sum + L.bias[nn] : sum;
     }
 }
@@ -382,60 +394,45 @@ __global__ __launch_bounds__(256) void linear_simple_kernel(GemvLinear L, int M,
     }
 }
 
-template <int T, bool FUSED>
-hipError_t launch_tiles(const GemvBatch& b, int kb, size_t lds, hipStream_t stream)
+template <int T>
+hipError_t launch_tiles(const GemvBatch& b, int nb, size_t lds, hipStream_t stream)
 {
     dim3 grid(b.wg_total), block(256);
-    switch (kb) {
-    case 1: hipLaunchKernelGGL((gemv_mfma_kernel<T, 1, FUSED>), grid, block, lds, stream, b); break;
-    case 2: hipLaunchKernelGGL((gemv_mfma_kernel<T, 2, FUSED>), grid, block, lds, stream, b); break;
-    case 4: hipLaunchKernelGGL((gemv_mfma_kernel<T, 4, FUSED>), grid, block, lds, stream, b); break;
-    case 8: hipLaunchKernelGGL((gemv_mfma_kernel<T, 8, FUSED>), grid, block, lds, stream, b); break;
+    switch (nb) {
+    case 1: hipLaunchKernelGGL((gemv_mfma_kernel<T, 1>), grid, block, lds, stream, b); break;
+    case 2: hipLaunchKernelGGL((gemv_mfma_kernel<T, 2>), grid, block, lds, stream, b); break;
+    case 4: hipLaunchKernelGGL((gemv_mfma_kernel<T, 4>), grid, block, lds, stream, b); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
+
+size_t lds_per_group(int M, int group) { return (size_t)(group / 64) * 4 * (4 * M) * 16 + 8 * (size_t)M; }
 
 }  // namespace
 
 bool gemv_fast_ok(int M, int N, int K, int group)
 {
     return M >= 1 && M <= kGemvMaxM && N > 0 && K > 0 && N % 4 == 0 &&
-           (group == 32 || group == 64 || group == 128 || group == 256) && K % group == 0;
+           (group == 64 || group == 128 || group == 256) && K % group == 0;
 }
-
-bool gemv_fused(int M) { return M <= kGemvFusedMaxM; }
 
 GemvShape gemv_shape(int M, int N, int K, int group)
 {
     GemvShape s;
-    s.strips = (N + kGemvCols - 1) / kGemvCols;
+    s.strips = (N + kGemvStripCols - 1) / kGemvStripCols;
     s.groups = K / group;
-    int slices = (kTargetWaves + s.strips - 1) / s.strips;   // K slices wanted per strip
-    if (slices > s.groups) slices = s.groups;
-    if (slices < 1) slices = 1;
-    s.waves = kGemvWaves;
-    s.split = (slices + kGemvWaves - 1) / kGemvWaves;
-    if (gemv_fused(M)) {
-        // the segment's split activations (2M rows x group/8 chunks x 16 B) plus its per-group
-        // {scale, sum} pairs (M float2 per group) must fit the LDS budget
-        int max_groups = kGemvLdsXsBytes / (4 * M * group + 8 * M);
-        if (max_groups < 1) max_groups = 1;
-        const int need = (s.groups + max_groups - 1) / max_groups;
-        if (s.split < need) s.split = need;
-    }
+    s.waves = 4;
+    s.split = (kTargetWaves + 4 * s.strips - 1) / (4 * s.strips);
+    const int max_split = s.groups / kMinGroupsPerWave;
+    if (s.split > max_split) s.split = max_split;
+    // the segment's activation digits and group stats must fit the LDS budget
+    const int max_groups = (int)(kLdsBudget / lds_per_group(M, group));
+    const int need = (s.groups + max_groups - 1) / (max_groups > 0 ? max_groups : 1);
+    if (s.split < need) s.split = need;
     if (s.split > s.groups) s.split = s.groups;
     if (s.split < 1) s.split = 1;
     return s;
-}
-
-// scratch layout for M > 4: xs [K/8][2M] uint4, then gs [K/group][M] float2
-uint64_t gemv_xs_bytes(int M, int K)
-{
-    if (gemv_fused(M)) return 0;
-    const uint64_t xs = (uint64_t)4 * M * K;
-    const uint64_t gs = (uint64_t)8 * M * (K / 32);
-    return (xs + gs + 255) & ~(uint64_t)255;
 }
 
 uint64_t gemv_partial_bytes(int M, int N, int split)
@@ -444,40 +441,21 @@ uint64_t gemv_partial_bytes(int M, int N, int split)
     return ((uint64_t)split * M * N * 4 + 255) & ~(uint64_t)255;
 }
 
-void gemv_xs_layout(GemvLinear& L, char* base, int M)
-{
-    L.xs = reinterpret_cast<const uint4*>(base);
-    L.gs = reinterpret_cast<const float2*>(base + (size_t)4 * M * L.K);
-}
-
 hipError_t launch_gemv_batch(const GemvBatch& b, hipStream_t stream)
 {
     const int group = b.L[0].group;
     for (int i = 1; i < b.count; i++)
         if (b.L[i].group != group) return hipErrorInvalidValue;
-    const int kb = group / 32;
-    if (gemv_fused(b.M)) {
-        size_t lds = 0;
-        for (int i = 0; i < b.count; i++) {
-            const int G = b.L[i].K / group;
-            const int gmax = (G + b.L[i].split - 1) / b.L[i].split;
-            lds = max(lds, (size_t)gmax * kb * 4 * (2 * b.M) * 16 + (size_t)gmax * b.M * 8);
-        }
-        return launch_tiles<1, true>(b, kb, lds, stream);
+    size_t lds = 0;
+    for (int i = 0; i < b.count; i++) {
+        const int G = b.L[i].K / group;
+        const int gmax = (G + b.L[i].split - 1) / b.L[i].split;
+        lds = max(lds, (size_t)gmax * lds_per_group(b.M, group));
     }
-    int lanes = 0;
-    for (int i = 0; i < b.count; i++) lanes = max(lanes, (b.L[i].K >> 3) * b.M);
-    const dim3 xg((lanes + 255) / 256, b.count);
-    switch (kb) {
-    case 1: hipLaunchKernelGGL(xsplit_kernel<4>, xg, dim3(256), 0, stream, b); break;
-    case 2: hipLaunchKernelGGL(xsplit_kernel<8>, xg, dim3(256), 0, stream, b); break;
-    case 4: hipLaunchKernelGGL(xsplit_kernel<16>, xg, dim3(256), 0, stream, b); break;
-    case 8: hipLaunchKernelGGL(xsplit_kernel<32>, xg, dim3(256), 0, stream, b); break;
-    default: return hipErrorInvalidValue;
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    return b.M <= 8 ? launch_tiles<1, false>(b, kb, 0, stream) : launch_tiles<2, false>(b, kb, 0, stream);
+    const int nb = group / 64;
+    if (b.M <= 4) return launch_tiles<1>(b, nb, lds, stream);
+    if (b.M <= 8) return launch_tiles<2>(b, nb, lds, stream);
+    return launch_tiles<4>(b, nb, lds, stream);
 }
 
 hipError_t launch_gemv_simple(const GemvLinear& L, int M, int x_dtype, hipStream_t stream)

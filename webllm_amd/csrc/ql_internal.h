@@ -7,8 +7,7 @@
 namespace ql {
 
 constexpr int kMaxBatch = 8;
-constexpr int kGemvCols = 64;      // output columns per GEMV workgroup (16 lanes x 4 columns)
-constexpr int kGemvWaves = 4;      // waves per GEMV workgroup
+constexpr int kGemvStripCols = 256;  // output columns per GEMV workgroup (4 waves x 64)
 constexpr int kGemvMaxM = 16;      // rows handled by the GEMV path (2 MFMA row tiles)
 constexpr int kCounterCapacity = 1 << 16;  // split-K arrival counters per context
 
@@ -19,12 +18,10 @@ struct GemvLinear {
     const uint16_t* scales;    // [K/group, N] fp16 bits
     const float* bias;         // [N] or nullptr
     const void* x;             // [M, K] f32 or f16
-    const uint4* xs;           // M > 4: prepared activations [K/8][2M] (gemv_xs_layout)
-    const float2* gs;          // M > 4: per (group, row) {2^(16-E), sum of x} [K/group][M]
     float* y;                  // [M, N]
     float* partial;            // [split, M, N] (split > 1)
     uint32_t* counters;        // per-strip arrival counters (split > 1), zero between launches
-    int N, K, group, split, strips, wg_begin, xs_owner;
+    int N, K, group, split, strips, wg_begin;
 };
 
 struct GemvBatch {
@@ -41,10 +38,7 @@ struct GemvShape {
 };
 GemvShape gemv_shape(int M, int N, int K, int group);
 bool gemv_fast_ok(int M, int N, int K, int group);
-bool gemv_fused(int M);
-uint64_t gemv_xs_bytes(int M, int K);
 uint64_t gemv_partial_bytes(int M, int N, int split);
-void gemv_xs_layout(GemvLinear& L, char* base, int M);
 
 hipError_t launch_gemv_batch(const GemvBatch& b, hipStream_t stream);
 hipError_t launch_gemv_simple(const GemvLinear& L, int M, int x_dtype, hipStream_t stream);
