@@ -14,6 +14,7 @@
  *   ql_gptq_desc / ql_gptq_check  src/weights/quant.ts:16-30 GptqInt4Params, :44-79 validation
  *   ql_unpack_f16                 src/weights/qwen-loader.ts:55-67 dequantGptqLinear +
  *                                 src/model/qwen.ts:262-266 uploadF16 (CPU dequant + f16 encode)
+ *   ql_unpack_f32                 src/weights/quant.ts:42-118 dequantizeGptqInt4
  *   ql_plan_linear                src/model/qwen.ts:61-74 planGemvSplit + the branch in :568-618
  *   ql_linear                     src/model/qwen.ts:568-618 QwenGpt.gemm (GEMV / split-K / GEMM)
  *   ql_linear_batch               src/model/qwen.ts:411-413, :464-465 (q/k/v and gate/up issued
@@ -124,6 +125,11 @@ int ql_gptq_check(const ql_gptq_desc* desc, const ql_arena* weights);
 /* ---- load time: fp16 [N,K] row-major, bit-identical to
  * f32ToF16Bits(dequantizeGptqInt4(...)) (quant.ts:42-118, buffer.ts:57-100). */
 int ql_unpack_f16(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights,
+                  ql_arena* out, uint64_t out_off);
+/* fp32 [N,K] row-major, bit-identical to dequantizeGptqInt4(...) itself (quant.ts:42-118) with
+ * the scales decoded from fp16 as the loader does (safetensors.ts:180-182, qwen-loader.ts:65).
+ * out_off must be 16-byte aligned. */
+int ql_unpack_f32(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights,
                   ql_arena* out, uint64_t out_off);
 
 /* ---- dispatch plan (host only, deterministic, pure). */

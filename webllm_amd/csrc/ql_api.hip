@@ -384,6 +384,30 @@ int ql_unpack_f16(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, q
     return QL_OK;
 }
 
+int ql_unpack_f32(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_arena* out,
+                  uint64_t out_off)
+{
+    if (!ctx || !out) return fail(QL_E_INVALID, "null context or output arena");
+    int rc = check_desc(d, weights);
+    if (rc) return rc;
+    if (!in_range(out_off, (uint64_t)d->N * d->K * 4, out->size))
+        return fail(QL_E_RANGE, "fp32 [N,K] output outside the arena");
+    if (out_off % 16) return fail(QL_E_ALIGN, "fp32 output offset must be 16-byte aligned");
+    if ((d->K + 7) / 8 > 65535) return fail(QL_E_INVALID, "K too large (%d)", d->K);
+    if ((rc = set_device(ctx))) return rc;
+    ql::UnpackArgs a;
+    a.qweight = reinterpret_cast<const uint32_t*>(weights->base + d->qweight_off);
+    a.qzeros = d->qzeros_off == QL_NONE ? nullptr
+                                        : reinterpret_cast<const uint32_t*>(weights->base + d->qzeros_off);
+    a.scales = reinterpret_cast<const uint16_t*>(weights->base + d->scales_off);
+    a.out = out->base + out_off;
+    a.N = d->N;
+    a.K = d->K;
+    a.group = d->group;
+    QL_HIP(ql::launch_unpack_f32(a, ctx->stream));
+    return QL_OK;
+}
+
 int ql_plan_linear(int32_t M, int32_t N, int32_t K, int32_t group, ql_plan* out)
 {
     if (!out) return fail(QL_E_INVALID, "null plan pointer");

@@ -63,9 +63,10 @@ struct UnpackArgs {
     const uint32_t* qweight;
     const uint32_t* qzeros;
     const uint16_t* scales;
-    uint16_t* out;
+    void* out;                 // fp16 [N,K] (launch_unpack) or fp32 [N,K] (launch_unpack_f32)
     int N, K, group;
 };
 hipError_t launch_unpack(const UnpackArgs& a, bool fast, hipStream_t stream);
+hipError_t launch_unpack_f32(const UnpackArgs& a, hipStream_t stream);
 
 }  // namespace ql

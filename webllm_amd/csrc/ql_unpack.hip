@@ -60,9 +60,34 @@ __global__ __launch_bounds__(256) void unpack_tile_kernel(UnpackArgs a)
         const int nn = n0 + col;
         const int pp = p0 + rr;
         if (nn < a.N && pp < P) {
-            *reinterpret_cast<uint4*>(a.out + (size_t)nn * a.K + (size_t)pp * 8) =
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + (size_t)nn * a.K + (size_t)pp * 8) =
                 tile[col * kPad + rr];
         }
+    }
+}
+
+// fp32 [N, K]: exactly dequantizeGptqInt4 (quant.ts:112, (q - zero) * scale with the scale
+// decoded from fp16; the product is exact in fp32). One packed word per lane, 2 x 16-byte stores
+// when the row allows it.
+__global__ __launch_bounds__(256) void unpack_f32_kernel(UnpackArgs a)
+{
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int p = blockIdx.y;
+    if (n >= a.N) return;
+    const int NC = (a.N + 7) >> 3;
+    const int g = (p * 8) / a.group;
+    const uint32_t w = a.qweight[(size_t)p * a.N + n];
+    const int z = (int)zero_of(a.qzeros, g, NC, n);
+    const float s = (float)__builtin_bit_cast(_Float16, a.scales[(size_t)g * a.N + n]);
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = (float)((int)((w >> (4 * k)) & 15u) - z) * s;
+    float* row = reinterpret_cast<float*>(a.out) + (size_t)n * a.K + (size_t)p * 8;
+    if (a.K % 4 == 0 && (p + 1) * 8 <= a.K) {
+        reinterpret_cast<float4*>(row)[0] = float4{v[0], v[1], v[2], v[3]};
+        reinterpret_cast<float4*>(row)[1] = float4{v[4], v[5], v[6], v[7]};
+    } else {
+        for (int k = 0; k < 8 && p * 8 + k < a.K; k++) row[k] = v[k];
     }
 }
 
@@ -84,11 +109,18 @@ __global__ __launch_bounds__(256) void unpack_generic_kernel(UnpackArgs a)
         const int q = (int)((w >> (4 * k)) & 15u);
         // (q - z) * s is exact in fp32 (at most 16 significant bits); one RNE rounding to fp16.
         const _Float16 h = (_Float16)((float)(q - (int)z) * sf);
-        a.out[(size_t)n * a.K + i] = __builtin_bit_cast(uint16_t, h);
+        static_cast<uint16_t*>(a.out)[(size_t)n * a.K + i] = __builtin_bit_cast(uint16_t, h);
     }
 }
 
 }  // namespace
+
+hipError_t launch_unpack_f32(const UnpackArgs& a, hipStream_t stream)
+{
+    dim3 grid((a.N + 255) / 256, (a.K + 7) / 8);
+    hipLaunchKernelGGL(unpack_f32_kernel, grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_unpack(const UnpackArgs& a, bool fast, hipStream_t stream)
 {
