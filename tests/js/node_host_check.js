@@ -1,0 +1,123 @@
+'use strict';
+/**
+ * Drives the Node host (webllm_amd/js) for tests/test_node_host.py.
+ *
+ *   node node_host_check.js abi <dir>   no GPU: addon exports, plans, validation codes, parse of
+ *                                       <dir>/model.safetensors; prints one JSON line
+ *   node node_host_check.js gpu <dir>   loads <dir>/model.safetensors with loadQwenWeights and
+ *                                       runs the cases of <dir>/cases.json, writing each output
+ *                                       to <dir>/<out>; prints one JSON line
+ * Correctness is judged by the Python side against the C oracle.
+ */
+const fs = require('fs');
+const path = require('path');
+const q = require('../../webllm_amd/js');
+
+function readF32(file) {
+    const b = fs.readFileSync(file);
+    return new Float32Array(b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength));
+}
+
+function writeTyped(file, typed) {
+    fs.writeFileSync(file, Buffer.from(typed.buffer, typed.byteOffset, typed.byteLength));
+}
+
+function abi(dir) {
+    const plans = [[1, 4864, 896], [4, 896, 4864], [16, 128, 896], [64, 896, 896], [1, 13, 20]]
+        .map(([M, N, K]) => Object.assign({ M, N, K }, q.addon.planLinear(M, N, K, 128)));
+    const desc = (K, N, group, bits) => q.makeDesc(0, null, 0, K, N, group, null, bits);
+    const validate = {
+        ok: q.addon.validate(desc(896, 128, 128, 4), 1 << 30),
+        bits: q.addon.validate(desc(896, 128, 128, 3), 1 << 30),
+        group: q.addon.validate(desc(896, 128, 0, 4), 1 << 30),
+        dims: q.addon.validate(desc(0, 128, 128, 4), 1 << 30),
+        pack: q.addon.validate(desc(896, 128, 100, 4), 1 << 30),
+    };
+    const file = q.parseSafetensors(fs.readFileSync(path.join(dir, 'model.safetensors')));
+    let badParse = null;
+    try { q.parseSafetensors(new Uint8Array(4)); } catch (e) { badParse = e.message; }
+    console.log(JSON.stringify({
+        exports: Object.keys(q.addon).sort(),
+        plans,
+        validate,
+        sizes: q.addon.gptqSizes(896, 4864, 128),
+        tensors: Object.keys(file.header).length,
+        embedShape: q.requireTensor(file, 'model.embed_tokens.weight').shape,
+        badParse,
+    }));
+}
+
+function gpu(dir) {
+    const spec = JSON.parse(fs.readFileSync(path.join(dir, 'cases.json'), 'utf8'));
+    const ctx = new q.Context(0);
+    try {
+        const model = new q.QuantLinearModel(ctx, 64 << 20);
+        const progress = [];
+        const res = q.loadQwenWeights(ctx, model, {
+            path: path.join(dir, 'model.safetensors'), config: spec.config, keepLayer: 0,
+            onProgress: (i, n) => progress.push(i),
+        });
+        writeTyped(path.join(dir, 'kept_qW.f32'), res.layer.qW);
+        const pool = new q.ActivationArena(ctx, 32 << 20);
+        for (const c of spec.gemm) {
+            const A = pool.alloc([c.M, c.K], c.f16 ? 'f16' : 'f32');
+            A.write(Uint8Array.from(fs.readFileSync(path.join(dir, c.x))));  // f32 or f16 bits
+            const C = pool.alloc([c.M, c.N]);
+            model.gemm(A, c.weight, C, c.bias, c.M, c.N, c.K);
+            ctx.sync();
+            writeTyped(path.join(dir, c.out), C.read());
+            pool.reset();
+        }
+        for (const b of spec.batch) {
+            const A = pool.alloc([b.M, b.K]);
+            A.write(readF32(path.join(dir, b.x)));
+            const Cs = b.weights.map((w, i) => pool.alloc([b.M, b.N[i]]));
+            model.gemmBatch(A, b.weights, Cs, b.M);
+            ctx.sync();
+            Cs.forEach((C, i) => writeTyped(path.join(dir, b.outs[i]), C.read()));
+            pool.reset();
+        }
+        const u = spec.unpack;
+        const U = pool.alloc([u.N, u.K], 'f16');
+        model.unpackF16(u.weight, U);
+        ctx.sync();
+        writeTyped(path.join(dir, u.out), U.read());
+        pool.reset();
+
+        // dequantizeGptqInt4 with the reference's params object, from the parsed file
+        const file = q.parseSafetensors(fs.readFileSync(path.join(dir, 'model.safetensors')));
+        const d = spec.dequant;
+        const W = q.dequantizeGptqInt4({
+            qweight: q.readTensorBytes(file, `${d.prefix}.qweight`),
+            qzeros: q.readTensorBytes(file, `${d.prefix}.qzeros`),
+            scales: q.readTensorF32(file, `${d.prefix}.scales`),
+            inFeatures: d.K, outFeatures: d.N, groupSize: 128,
+        }, ctx);
+        writeTyped(path.join(dir, d.out), W);
+
+        const errors = {};
+        const expectThrow = (key, fn) => {
+            try { fn(); errors[key] = null; } catch (e) { errors[key] = e.message; }
+        };
+        const A = pool.alloc([1, spec.config.nEmbd]);
+        const C = pool.alloc([1, spec.config.nEmbd]);
+        expectThrow('missingWeight', () => model.gemm(A, 'L9.qW', C, null, 1, spec.config.nEmbd, spec.config.nEmbd));
+        expectThrow('wrongShape', () => model.gemm(A, 'L0.qW', C, null, 1, spec.config.nEmbd + 8, spec.config.nEmbd));
+        expectThrow('missingBias', () => model.gemm(A, 'L0.oW', C, 'L0.oB', 1, spec.config.nEmbd, spec.config.nEmbd));
+        expectThrow('duplicate', () => model.uploadF32('finalNorm', new Float32Array(4)));
+        expectThrow('bits', () => q.dequantizeGptqInt4({ qweight: new Uint8Array(4), scales: new Float32Array(1), inFeatures: 8, outFeatures: 1, bits: 8 }, ctx));
+        pool.release();
+        model.release();
+        console.log(JSON.stringify({
+            device: ctx.info(), tensorCount: res.tensorCount, gpuBytes: res.gpuBytes,
+            fileBytes: res.fileBytes, progress, errors,
+        }));
+    } finally {
+        ctx.destroy();
+    }
+}
+
+const [mode, dir] = process.argv.slice(2);
+if (mode === 'abi') abi(dir);
+else if (mode === 'gpu') gpu(dir);
+else { console.error('usage: node node_host_check.js abi|gpu <dir>'); process.exit(2); }

@@ -11,42 +11,11 @@ import pytest
 from webllm_amd import gptq, synth
 from webllm_amd import qlinear as ql
 
+from .checkpoint import TINY, write_checkpoint as _checkpoint
+
 pytestmark = pytest.mark.gpu
 
-TINY = gptq.QwenConfig(vocab_size=512, block_size=16, n_layer=2, n_head=4, n_kv_head=2,
-                       n_embd=256, intermediate=640)
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-
-
-def _checkpoint(path, cfg):
-    shapes = gptq.qwen_linear_shapes(cfg)
-    names = dict(gptq._PROJ)
-    tensors, kept = {}, {}
-    rng = np.random.default_rng(1)
-    emb = (rng.standard_normal((cfg.vocab_size, cfg.n_embd)) * 0.02).astype(np.float16)
-    tensors["model.embed_tokens.weight"] = ("F16", emb.shape, emb.tobytes())
-    tensors["model.norm.weight"] = ("F32", (cfg.n_embd,), np.ones(cfg.n_embd, np.float32).tobytes())
-    for i in range(cfg.n_layer):
-        p = f"model.layers.{i}"
-        tensors[f"{p}.input_layernorm.weight"] = ("F32", (cfg.n_embd,), np.ones(cfg.n_embd, np.float32).tobytes())
-        tensors[f"{p}.post_attention_layernorm.weight"] = ("F32", (cfg.n_embd,), np.ones(cfg.n_embd, np.float32).tobytes())
-        for j, (key, proj) in enumerate(gptq._PROJ):
-            K, N = shapes[key]
-            t = synth.gptq_linear(K, N, 128, seed=0x10AD, key=(i, j), stored_zero=None if j % 2 else 7)
-            pre = f"{p}.{proj}"
-            tensors[f"{pre}.qweight"] = ("I32", t.qweight.shape, t.qweight.tobytes())
-            tensors[f"{pre}.qzeros"] = ("I32", t.qzeros.shape, t.qzeros.tobytes())
-            tensors[f"{pre}.scales"] = ("F16", t.scales.shape, t.scales.tobytes())
-            g_idx = (np.arange(K) // 128).astype(np.int32)
-            tensors[f"{pre}.g_idx"] = ("I32", g_idx.shape, g_idx.tobytes())
-            b = None
-            if key in gptq._BIASED:
-                b = rng.standard_normal(N).astype(np.float16)
-                tensors[f"{pre}.bias"] = ("F16", (N,), b.tobytes())
-                b = b.astype(np.float32)
-            kept[(i, key)] = (t, b)
-    gptq.write_safetensors(path, tensors)
-    return kept
 
 
 @pytest.fixture(scope="module")

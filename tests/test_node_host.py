@@ -1,0 +1,137 @@
+"""The Node host (webllm_amd/js over the Node-API addon): the reference's own host language.
+
+CPU: the addon loads under Node and exports the binding of every C-ABI entry point the host
+needs; its plans and validation codes equal the Python binding's. GPU: loadQwenWeights on a
+synthetic checkpoint, QuantLinearModel.gemm / gemmBatch / unpackF16 and dequantizeGptqInt4 from
+JavaScript, checked against the C oracle with the same bars as the Python-host tests."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from webllm_amd import gptq, synth
+from webllm_amd import qlinear as ql
+
+from .checkpoint import TINY, write_checkpoint
+
+NODE = shutil.which("node")
+HERE = os.path.dirname(os.path.abspath(__file__))
+SCRIPT = os.path.join(HERE, "js", "node_host_check.js")
+ADDON = os.path.join(os.path.dirname(HERE), "webllm_amd", "lib", "qlinear_napi.node")
+
+needs_node = pytest.mark.skipif(NODE is None, reason="node not installed")
+
+# the N-API exports and the C-ABI entry points each one forwards to
+BINDING = {
+    "create": "ql_create", "destroy": "ql_destroy", "deviceInfo": "ql_device_info",
+    "lastError": "ql_last_error", "arenaReserve": "ql_arena_reserve",
+    "arenaRelease": "ql_arena_release", "arenaSize": "ql_arena_size",
+    "arenaWrite": "ql_arena_write", "arenaRead": "ql_arena_read", "gptqSizes": "ql_gptq_sizes",
+    "validate": "ql_gptq_validate", "planLinear": "ql_plan_linear", "planBatch": "ql_plan_batch",
+    "unpack": "ql_unpack_f16", "linear": "ql_linear", "linearBatch": "ql_linear_batch",
+    "sync": "ql_sync", "timerStart": "ql_timer_start", "timerStop": "ql_timer_stop",
+    "graphBegin": "ql_graph_begin", "graphEnd": "ql_graph_end", "graphLaunch": "ql_graph_launch",
+    "graphDestroy": "ql_graph_destroy",
+}
+
+
+def _node(mode, d, timeout):
+    r = subprocess.run([NODE, SCRIPT, mode, str(d)], capture_output=True, text=True,
+                       timeout=timeout)
+    assert r.returncode == 0, r.stderr[-4000:]
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def _js_config(c):
+    return {"vocabSize": c.vocab_size, "blockSize": c.block_size, "nLayer": c.n_layer,
+            "nHead": c.n_head, "nKvHead": c.n_kv_head, "nEmbd": c.n_embd,
+            "intermediate": c.intermediate}
+
+
+@needs_node
+def test_addon_exports_and_host_logic(tmp_path):
+    assert os.path.exists(ADDON), "run __graft_entry__.build() first"
+    write_checkpoint(str(tmp_path / "model.safetensors"), TINY)
+    res = _node("abi", tmp_path, 120)
+    assert res["exports"] == sorted(BINDING)
+    declared = set(ql.header_functions())
+    assert set(BINDING.values()) <= declared
+    for p in res["plans"]:
+        want = ql.plan_linear(p["M"], p["N"], p["K"], 128)
+        assert p["kind"] == want.kind_name and p["split"] == want.split
+        assert p["gridX"] == want.grid_x and p["scratchBytes"] == want.scratch_bytes
+        assert p["refSplit"] == want.ref_split
+    assert res["validate"] == {"ok": 0, "bits": -1, "group": -2, "dims": -3, "pack": -7}
+    assert tuple(res["sizes"].values()) == ql.gptq_sizes(896, 4864, 128)
+    assert res["tensors"] == 2 + TINY.n_layer * (2 + 7 * 4 + 3)
+    assert res["embedShape"] == [TINY.vocab_size, TINY.n_embd]
+    assert "too short" in res["badParse"]
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_host_matches_oracle(tmp_path, orc):
+    kept = write_checkpoint(str(tmp_path / "model.safetensors"), TINY)
+    shapes = gptq.qwen_linear_shapes(TINY)
+    cases = {"config": _js_config(TINY), "gemm": [], "batch": []}
+    refs = {}
+    for i, (key, M, f16) in enumerate([("qW", 1, False), ("gateW", 1, False), ("downW", 3, False),
+                                       ("upW", 16, False), ("kW", 64, False), ("oW", 70, True)]):
+        K, N = shapes[key]
+        t, b = kept[(0, key)]
+        x = synth.activations(M, K, seed=0x40DE, key=(i,))
+        if f16:
+            x = x.astype(np.float16).astype(np.float32)
+            x.astype(np.float16).tofile(tmp_path / f"x{i}")
+        else:
+            x.tofile(tmp_path / f"x{i}")
+        bias = f"L0.{key[0]}B" if b is not None else None
+        cases["gemm"].append({"weight": f"L0.{key}", "M": M, "N": N, "K": K, "bias": bias,
+                              "f16": f16, "x": f"x{i}", "out": f"y{i}.f32"})
+        refs[f"y{i}.f32"] = (orc.gptq_linear(t.qweight, t.qzeros, t.scales, x, b), M >= 17)
+    xb = synth.activations(2, TINY.n_embd, seed=0x40DF)
+    xb.tofile(tmp_path / "xb")
+    names = ["qW", "kW", "vW"]
+    cases["batch"].append({"weights": [f"L1.{k}" for k in names], "M": 2, "K": TINY.n_embd,
+                           "N": [shapes[k][1] for k in names], "x": "xb",
+                           "outs": [f"b{k}.f32" for k in names]})
+    for k in names:
+        t, b = kept[(1, k)]
+        refs[f"b{k}.f32"] = (orc.gptq_linear(t.qweight, t.qzeros, t.scales, xb, b), False)
+    K, N = shapes["gateW"]
+    cases["unpack"] = {"weight": "L1.gateW", "N": N, "K": K, "out": "u.f16"}
+    cases["dequant"] = {"prefix": "model.layers.1.mlp.down_proj", "K": shapes["downW"][0],
+                        "N": shapes["downW"][1], "out": "w.f32"}
+    (tmp_path / "cases.json").write_text(json.dumps(cases))
+
+    print(f"node host: {len(cases['gemm'])} gemm cases, 1 batch", flush=True)
+    res = _node("gpu", tmp_path, 300)
+
+    assert res["tensorCount"] == 2 + TINY.n_layer * (2 + 7 + 3)
+    assert res["progress"] == list(range(1, TINY.n_layer + 1))
+    for out, (ref, gemm) in refs.items():
+        got = np.fromfile(tmp_path / out, dtype=np.float32).reshape(ref.shape)
+        # decode GEMV: |d| <= 1e-5 + 1e-4|ref|; MFMA f16 GEMM (M >= 17): 2e-3 normwise
+        if gemm:
+            err = np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+            assert err <= 2e-3, (out, err)
+        else:
+            ok, max_abs, max_rel = orc.check_tolerance(got, ref, 1e-5, 1e-4)
+            assert ok, (out, max_abs, max_rel)
+    t, _ = kept[(1, "gateW")]
+    u = np.fromfile(tmp_path / "u.f16", dtype=np.uint16).reshape(t.N, t.K)
+    assert np.array_equal(u, orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, t.K, t.N, 128))
+    for out, (t, _) in (("w.f32", kept[(1, "downW")]), ("kept_qW.f32", kept[(0, "qW")])):
+        _, W = orc.dequantize_gptq_int4(t.qweight, t.qzeros, orc.f16_bits_to_f32(t.scales), t.K,
+                                        t.N, 128)
+        got = np.fromfile(tmp_path / out, dtype=np.float32).reshape(t.N, t.K)
+        assert np.array_equal(got.view(np.uint32), W.view(np.uint32)), out
+    e = res["errors"]
+    assert "missing int4 weight: L9.qW" in e["missingWeight"]
+    assert "called with N=" in e["wrongShape"]
+    assert "missing f32 weight: L0.oB" in e["missingBias"]
+    assert "already exists" in e["duplicate"]
+    assert "QL_E_BITS" in e["bits"]

@@ -1,0 +1,98 @@
+// Types of the Node host for libqlinear (index.js), for the reference's TypeScript code.
+
+export interface QwenConfig {
+    vocabSize: number; blockSize: number; nLayer: number; nHead: number; nKvHead: number;
+    nEmbd: number; intermediate: number; rmsEps?: number; ropeTheta?: number;
+}
+export const QWEN25_05B: Readonly<QwenConfig>;
+export function qwenHeadDim(c: QwenConfig): number;
+export function qwenKvDim(c: QwenConfig): number;
+
+export type SafetensorDtype = 'F64' | 'F32' | 'F16' | 'BF16' | 'I64' | 'I32' | 'I16' | 'I8' | 'U8' | 'BOOL';
+export interface SafetensorEntry { dtype: SafetensorDtype; shape: number[]; data_offsets: [number, number]; }
+export interface SafetensorFile { buffer: Uint8Array; dataStart: number; header: Record<string, SafetensorEntry>; }
+export function dtypeByteSize(dtype: SafetensorDtype): number;
+export function parseSafetensorsHeader(headerBytes: Uint8Array): Record<string, SafetensorEntry>;
+export function parseSafetensors(buffer: ArrayBuffer | Uint8Array): SafetensorFile;
+export function tensorCount(entry: SafetensorEntry): number;
+export function requireTensor(file: SafetensorFile, name: string): SafetensorEntry;
+export function expectTensor(file: SafetensorFile, name: string, dtype: SafetensorDtype, shape: readonly number[]): SafetensorEntry;
+export function f16BitsToF32(bits: number): number;
+export function readTensorBytes(file: SafetensorFile, name: string): Uint8Array;
+export function readTensorF32(file: SafetensorFile, name: string): Float32Array;
+
+/** Error thrown by the library: `code` is 'QL_E_*'. */
+export interface QlError extends Error { code: string; }
+
+export interface GptqDesc {
+    qweightOff: number; qzerosOff: number | null; scalesOff: number; biasOff: number | null;
+    K: number; N: number; group: number; bits: number;
+}
+export function makeDesc(qweightOff: number, qzerosOff: number | null, scalesOff: number, K: number,
+                         N: number, group?: number, biasOff?: number | null, bits?: number): GptqDesc;
+
+export class ArenaLayout { used: number; take(nbytes: number, align?: number): number; }
+export class Arena {
+    readonly size: number;
+    write(off: number, data: ArrayBufferView): void;
+    read<T extends ArrayBufferView>(off: number, into: T): T;
+    release(): void;
+}
+export class Context {
+    constructor(device?: number);
+    info(): { name: string; cuCount: number; hbmBytes: number };
+    arena(bytes: number): Arena;
+    sync(): void;
+    timerStart(): void;
+    timerStop(): number;
+    destroy(): void;
+}
+
+export interface GptqInt4Params {
+    qweight: Uint8Array; qzeros?: Uint8Array | null; scales: Float32Array;
+    inFeatures: number; outFeatures: number; groupSize?: number; bits?: number;
+}
+/** quant.ts dequantizeGptqInt4, computed on the GPU: fp32 [outFeatures, inFeatures]. */
+export function dequantizeGptqInt4(params: GptqInt4Params, ctx?: Context): Float32Array;
+
+export class Tensor {
+    readonly arena: Arena; readonly offset: number; readonly length: number;
+    readonly shape: number[]; readonly dtype: 'f32' | 'f16';
+    read(): Float32Array | Uint16Array;
+    write(data: ArrayBufferView): void;
+}
+export class ActivationArena {
+    constructor(ctx: Context, bytes: number);
+    alloc(shape: number[], dtype?: 'f32' | 'f16'): Tensor;
+    scratchOffset(nbytes: number): number;
+    reset(): void;
+    release(): void;
+}
+export interface GptqLinearUpload {
+    qweight: Uint8Array; qzeros?: Uint8Array | null; scalesF16: Uint8Array | Uint16Array;
+    inFeatures: number; outFeatures: number; groupSize?: number; bias?: Float32Array | null;
+}
+export class QuantLinearModel {
+    constructor(ctx: Context, weightCapacity: number);
+    readonly weightBytes: number;
+    uploadGptqLinear(name: string, p: GptqLinearUpload): void;
+    uploadF32(name: string, data: ArrayLike<number>): void;
+    uploadF16Bits(name: string, bytes: ArrayBufferView, shape: number[]): void;
+    /** QwenGpt.gemm: C[M,N] = A[M,K] @ W^T (+ bias). */
+    gemm(A: Tensor, weight: string, C: Tensor, bias: string | null, M: number, N: number, K: number): void;
+    gemmBatch(A: Tensor, weights: string[], Cs: Tensor[], M: number): void;
+    unpackF16(name: string, out: Tensor): void;
+    dequantize(name: string): Float32Array;
+    release(): void;
+}
+
+export interface QwenLoadOptions {
+    path?: string; buffer?: ArrayBuffer | Uint8Array; config?: QwenConfig; groupSize?: number;
+    keepLayer?: number; onProgress?: (done: number, total: number, label: string) => void;
+}
+export interface QwenLoadResult {
+    gpuBytes: number; tensorCount: number; fileBytes: number;
+    layer?: Record<'qW' | 'kW' | 'vW' | 'oW' | 'gateW' | 'upW' | 'downW', Float32Array>;
+}
+export function qwenLinearShapes(c: QwenConfig): Record<string, [number, number]>;
+export function loadQwenWeights(ctx: Context | null, model: QuantLinearModel, options: QwenLoadOptions): QwenLoadResult;

@@ -1,0 +1,498 @@
+'use strict';
+/**
+ * Node host for libqlinear: the reference's TypeScript surface for the GPTQ int4 path, with the
+ * int4 work on the MI355X through the Node-API addon (webllm_amd/lib/qlinear_napi.node).
+ *
+ * Same names, argument meaning and error behaviour as (paths in the intplusplus/webllm checkout):
+ *   parseSafetensors, parseSafetensorsHeader,    src/weights/safetensors.ts:40-222
+ *   requireTensor, expectTensor, tensorCount,
+ *   readTensorBytes, readTensorF32, f16BitsToF32,
+ *   dtypeByteSize
+ *   dequantizeGptqInt4(params)                   src/weights/quant.ts:42-118 (exact, on the GPU)
+ *   QuantLinearModel.gemm(A, weight, C, bias,    src/model/qwen.ts:568-618 QwenGpt.gemm
+ *     M, N, K)
+ *   loadQwenWeights(ctx, model, options)         src/weights/qwen-loader.ts:102-177, with the
+ *                                                packed int4 tensors uploaded as they are
+ *   QWEN25_05B, qwenKvDim                        src/model/qwen-config.ts:1-54
+ *
+ * Errors are thrown as Error (the reference's `throw new Error(msg)`); library status codes carry
+ * `err.code` = 'QL_E_*'. There is no CPU fallback: a missing addon throws at require time.
+ */
+const fs = require('fs');
+const path = require('path');
+
+const ADDON_PATH = path.join(__dirname, '..', 'lib', 'qlinear_napi.node');
+if (!fs.existsSync(ADDON_PATH)) {
+    throw new Error(`qlinear: addon not built at ${ADDON_PATH} (run __graft_entry__.build())`);
+}
+const addon = require(ADDON_PATH);
+
+const QL_DTYPE_F32 = 0;
+const QL_DTYPE_F16 = 1;
+
+// ------------------------------------------------------------------ config (qwen-config.ts)
+
+const QWEN25_05B = Object.freeze({
+    vocabSize: 151936, blockSize: 128, nLayer: 24, nHead: 14, nKvHead: 2, nEmbd: 896,
+    intermediate: 4864, rmsEps: 1e-6, ropeTheta: 1000000,
+});
+
+function qwenHeadDim(c) { return c.nEmbd / c.nHead; }
+function qwenKvDim(c) { return c.nKvHead * qwenHeadDim(c); }
+
+// ------------------------------------------------------------------ safetensors.ts
+
+const DTYPE_BYTES = { F64: 8, I64: 8, F32: 4, I32: 4, F16: 2, BF16: 2, I16: 2, I8: 1, U8: 1, BOOL: 1 };
+
+function dtypeByteSize(dtype) {
+    const n = DTYPE_BYTES[dtype];
+    if (n === undefined) throw new Error(`unknown safetensors dtype: ${dtype}`);
+    return n;
+}
+
+function parseSafetensorsHeader(headerBytes) {
+    let parsed;
+    try {
+        parsed = JSON.parse(Buffer.from(headerBytes.buffer, headerBytes.byteOffset,
+            headerBytes.byteLength).toString('utf8'));
+    } catch (err) {
+        throw new Error(`safetensors: header JSON parse failed: ${err.message}`);
+    }
+    if (typeof parsed !== 'object' || parsed === null) {
+        throw new Error('safetensors: header is not a JSON object');
+    }
+    const header = {};
+    for (const name of Object.keys(parsed)) {
+        if (name === '__metadata__') continue;
+        const item = parsed[name];
+        if (typeof item !== 'object' || item === null) throw new Error(`safetensors: ${name} entry invalid`);
+        if (typeof item.dtype !== 'string') throw new Error(`safetensors: ${name} missing dtype`);
+        if (!Array.isArray(item.shape)) throw new Error(`safetensors: ${name} missing shape`);
+        if (!Array.isArray(item.data_offsets) || item.data_offsets.length !== 2) {
+            throw new Error(`safetensors: ${name} data_offsets invalid`);
+        }
+        const start = Number(item.data_offsets[0]);
+        const end = Number(item.data_offsets[1]);
+        if (!Number.isFinite(start) || !Number.isFinite(end) || start < 0 || end < start) {
+            throw new Error(`safetensors: ${name} data_offsets out of range`);
+        }
+        header[name] = { dtype: item.dtype, shape: item.shape.map(Number), data_offsets: [start, end] };
+    }
+    return header;
+}
+
+/** buffer: ArrayBuffer or Node Buffer / Uint8Array (the whole file). */
+function parseSafetensors(buffer) {
+    const bytes = buffer instanceof ArrayBuffer ? new Uint8Array(buffer)
+        : new Uint8Array(buffer.buffer, buffer.byteOffset, buffer.byteLength);
+    if (bytes.byteLength < 8) throw new Error('safetensors: buffer too short');
+    const dv = new DataView(bytes.buffer, bytes.byteOffset, bytes.byteLength);
+    const headerLen = dv.getUint32(0, true);
+    if (dv.getUint32(4, true) !== 0) throw new Error('safetensors: header longer than 4 GiB is not supported');
+    const dataStart = 8 + headerLen;
+    if (headerLen <= 0 || dataStart > bytes.byteLength) {
+        throw new Error(`safetensors: invalid header length headerLen=${headerLen} bufferSize=${bytes.byteLength}`);
+    }
+    const header = parseSafetensorsHeader(bytes.subarray(8, dataStart));
+    for (const name of Object.keys(header)) {
+        if (dataStart + header[name].data_offsets[1] > bytes.byteLength) {
+            throw new Error(`safetensors: ${name} data out of bounds end=${header[name].data_offsets[1]}`);
+        }
+    }
+    return { buffer: bytes, dataStart, header };
+}
+
+function tensorCount(entry) { return entry.shape.reduce((a, b) => a * b, 1); }
+
+function requireTensor(file, name) {
+    const entry = file.header[name];
+    if (!entry) throw new Error(`safetensors: missing tensor ${name}`);
+    return entry;
+}
+
+function expectTensor(file, name, dtype, shape) {
+    const entry = requireTensor(file, name);
+    if (entry.dtype !== dtype) throw new Error(`safetensors: ${name} dtype=${entry.dtype}, expected ${dtype}`);
+    if (entry.shape.length !== shape.length || entry.shape.some((v, i) => v !== shape[i])) {
+        throw new Error(`safetensors: ${name} shape=[${entry.shape}], expected [${shape}]`);
+    }
+    return entry;
+}
+
+function f16BitsToF32(bits) {
+    const sign = (bits & 0x8000) !== 0 ? -1 : 1;
+    const exp = (bits >>> 10) & 0x1f;
+    const mant = bits & 0x03ff;
+    if (exp === 0) return sign * mant * Math.pow(2, -24);
+    if (exp === 31) return mant === 0 ? sign * Infinity : NaN;
+    return sign * (1 + mant / 1024) * Math.pow(2, exp - 15);
+}
+
+/** Raw bytes of one tensor, as a copy (aligned for typed views). */
+function readTensorBytes(file, name) {
+    const entry = requireTensor(file, name);
+    const start = file.dataStart + entry.data_offsets[0];
+    const length = tensorCount(entry) * dtypeByteSize(entry.dtype);
+    return Uint8Array.from(file.buffer.subarray(start, start + length));
+}
+
+function readTensorF32(file, name) {
+    const entry = requireTensor(file, name);
+    const count = tensorCount(entry);
+    const start = file.dataStart + entry.data_offsets[0];
+    const view = new DataView(file.buffer.buffer, file.buffer.byteOffset + start,
+        entry.data_offsets[1] - entry.data_offsets[0]);
+    const out = new Float32Array(count);
+    const tmp = new DataView(new ArrayBuffer(4));
+    for (let i = 0; i < count; i++) {
+        switch (entry.dtype) {
+            case 'F32': out[i] = view.getFloat32(i * 4, true); break;
+            case 'F16': out[i] = f16BitsToF32(view.getUint16(i * 2, true)); break;
+            case 'BF16':
+                tmp.setUint32(0, view.getUint16(i * 2, true) << 16, true);
+                out[i] = tmp.getFloat32(0, true);
+                break;
+            case 'U8': out[i] = view.getUint8(i); break;
+            case 'I8': out[i] = view.getInt8(i); break;
+            default: throw new Error(`readTensorF32: unsupported dtype ${entry.dtype} (${name})`);
+        }
+    }
+    return out;
+}
+
+// ------------------------------------------------------------------ device objects
+
+/** Bump allocator over one arena, 256-byte aligned slices (the library's alignment contract). */
+class ArenaLayout {
+    constructor() { this.used = 0; }
+    take(nbytes, align) {
+        const a = align || 256;
+        const off = Math.ceil(this.used / a) * a;
+        this.used = off + nbytes;
+        return off;
+    }
+}
+
+class Arena {
+    constructor(ctx, bytes) {
+        this.ctx = ctx;
+        this.handle = addon.arenaReserve(ctx.handle, bytes);
+        this.size = bytes;
+        ctx._arenas.add(this);
+    }
+    write(off, typed) { addon.arenaWrite(this.handle, off, typed); }
+    read(off, typed) { addon.arenaRead(this.handle, off, typed); return typed; }
+    release() {
+        if (this.handle) {
+            addon.arenaRelease(this.handle);
+            this.handle = null;
+            this.ctx._arenas.delete(this);
+        }
+    }
+}
+
+/** One device, one stream (ql_create). */
+class Context {
+    constructor(device) {
+        this.handle = addon.create(device === undefined ? 0 : device);
+        this._arenas = new Set();
+    }
+    info() { return addon.deviceInfo(this.handle); }
+    arena(bytes) { return new Arena(this, bytes); }
+    sync() { addon.sync(this.handle); }
+    timerStart() { addon.timerStart(this.handle); }
+    timerStop() { return addon.timerStop(this.handle); }
+    destroy() {
+        for (const a of Array.from(this._arenas)) a.release();
+        if (this.handle) { addon.destroy(this.handle); this.handle = null; }
+    }
+}
+
+function makeDesc(qweightOff, qzerosOff, scalesOff, K, N, group, biasOff, bits) {
+    return {
+        qweightOff, qzerosOff: qzerosOff === undefined ? null : qzerosOff, scalesOff,
+        biasOff: biasOff === undefined ? null : biasOff, K, N,
+        group: group === undefined ? 128 : group, bits: bits === undefined ? 4 : bits,
+    };
+}
+
+const CODE_NAMES = {
+    '-1': 'QL_E_BITS', '-2': 'QL_E_GROUP', '-3': 'QL_E_DIMS', '-4': 'QL_E_QWEIGHT_SHORT',
+    '-5': 'QL_E_SCALES_SHORT', '-6': 'QL_E_QZEROS_SHORT', '-7': 'QL_E_GROUP_PACK',
+};
+
+function libError(code, message) {
+    const e = new Error(`${code}: ${message}`);
+    e.code = code;
+    return e;
+}
+
+// ------------------------------------------------------------------ quant.ts
+
+function toF16Bits(scales) {
+    const f32 = Float32Array.from(scales);
+    const out = new Uint16Array(f32.length);
+    const u = new Uint32Array(f32.buffer);
+    for (let i = 0; i < f32.length; i++) {
+        // fp16-representable inputs only (checked below): exact re-encode, no rounding needed
+        const x = u[i];
+        const sign = (x >>> 16) & 0x8000;
+        const e = (x >>> 23) & 0xff;
+        const m = x & 0x7fffff;
+        let h;
+        if (e === 0xff) h = sign | 0x7c00 | (m ? 0x200 | (m >>> 13) : 0);
+        else if (e === 0 && m === 0) h = sign;
+        else if (e >= 113) h = sign | ((e - 112) << 10) | (m >>> 13);
+        else h = sign | ((0x800000 | m) >>> (126 - e));
+        out[i] = h;
+        if (!(f16BitsToF32(h) === f32[i] || (Number.isNaN(f32[i]) && Number.isNaN(f16BitsToF32(h))))) {
+            throw new Error('dequantizeGptqInt4: scales must be fp16-representable (F16 checkpoint)');
+        }
+    }
+    return out;
+}
+
+let defaultCtx = null;
+
+/**
+ * quant.ts:42-118: GptqInt4Params -> fp32 [outFeatures, inFeatures], computed on the GPU
+ * (ql_unpack_f32, bit-identical to the reference's loop). `ctx` defaults to device 0.
+ */
+function dequantizeGptqInt4(params, ctx) {
+    const groupSize = params.groupSize === undefined || params.groupSize === null ? 128 : params.groupSize;
+    const bits = params.bits === undefined || params.bits === null ? 4 : params.bits;
+    const inF = params.inFeatures;
+    const outF = params.outFeatures;
+    // quant.ts:46-79 order: bits, group, dims, qweight bytes, scales count, qzeros bytes, group % 8
+    const shapeRc = addon.validate(makeDesc(0, null, 0, inF, outF, groupSize, null, bits), 2 ** 52);
+    if (shapeRc === -1 || shapeRc === -2 || shapeRc === -3) throw libError(CODE_NAMES[shapeRc], addon.lastError());
+    const need = addon.gptqSizes(inF, outF, groupSize);
+    if (params.qweight.byteLength < need.qweightBytes) {
+        throw libError('QL_E_QWEIGHT_SHORT', `GPTQ: qweight needs ${need.qweightBytes} bytes, got ${params.qweight.byteLength}`);
+    }
+    if (params.scales.length < need.scalesBytes / 2) {
+        throw libError('QL_E_SCALES_SHORT', `GPTQ: scales need ${need.scalesBytes / 2} values, got ${params.scales.length}`);
+    }
+    const qz = params.qzeros || null;
+    if (qz && qz.byteLength < need.qzerosBytes) {
+        throw libError('QL_E_QZEROS_SHORT', `GPTQ: qzeros need ${need.qzerosBytes} bytes, got ${qz.byteLength}`);
+    }
+    if (shapeRc === -7) throw libError('QL_E_GROUP_PACK', `GPTQ: groupSize=${groupSize} must be a multiple of 8`);
+    const s16 = toF16Bits(params.scales.subarray(0, need.scalesBytes / 2));
+    if (!ctx) { if (!defaultCtx) defaultCtx = new Context(0); ctx = defaultCtx; }
+    const lay = new ArenaLayout();
+    const oQw = lay.take(need.qweightBytes);
+    const oQz = qz ? lay.take(need.qzerosBytes) : null;
+    const oSc = lay.take(need.scalesBytes);
+    const w = ctx.arena(lay.used + 256);
+    const out = ctx.arena(Math.max(inF * outF * 4, 16));
+    try {
+        w.write(oQw, params.qweight.subarray(0, need.qweightBytes));
+        if (qz) w.write(oQz, qz.subarray(0, need.qzerosBytes));
+        w.write(oSc, s16);
+        addon.unpack(ctx.handle, makeDesc(oQw, oQz, oSc, inF, outF, groupSize, null, bits), w.handle,
+            out.handle, 0, true);
+        return out.read(0, new Float32Array(outF * inF));
+    } finally {
+        w.release();
+        out.release();
+    }
+}
+
+// ------------------------------------------------------------------ QwenGpt weight side (qwen.ts)
+
+/** Slice of a device arena: {arena, offset, length, shape, dtype} (buffer.ts:12-18). */
+class Tensor {
+    constructor(arena, offset, length, shape, dtype, pool) {
+        this.arena = arena; this.offset = offset; this.length = length; this.shape = shape;
+        this.dtype = dtype; this.pool = pool || null;
+    }
+    read() {
+        const T = this.dtype === 'f16' ? Uint16Array : Float32Array;
+        return this.arena.read(this.offset, new T(this.length));
+    }
+    write(data) { this.arena.write(this.offset, data); }
+}
+
+/** Per-step activation arena (arena.ts): bump allocation from the front, split-K scratch from the back. */
+class ActivationArena {
+    constructor(ctx, bytes) {
+        this.arena = ctx.arena(bytes);
+        this.layout = new ArenaLayout();
+    }
+    alloc(shape, dtype) {
+        const dt = dtype || 'f32';
+        const n = shape.reduce((a, b) => a * b, 1);
+        const off = this.layout.take(n * (dt === 'f16' ? 2 : 4));
+        if (this.layout.used > this.arena.size) throw new Error('activation arena exhausted');
+        return new Tensor(this.arena, off, n, shape.slice(), dt, this);
+    }
+    scratchOffset(nbytes) {
+        const off = Math.floor((this.arena.size - nbytes) / 256) * 256;
+        if (off < this.layout.used) throw new Error(`activation arena: no room for ${nbytes} scratch bytes`);
+        return off;
+    }
+    reset() { this.layout = new ArenaLayout(); }
+    release() { this.arena.release(); }
+}
+
+class QuantLinearModel {
+    /** Weight side of QwenGpt with GPTQ weights kept packed in one device arena, addressed by name. */
+    constructor(ctx, weightCapacity) {
+        this.ctx = ctx;
+        this.weights = ctx.arena(weightCapacity);
+        this.layout = new ArenaLayout();
+        this.linears = new Map();
+        this.f32Weights = new Map();
+        this.f16Weights = new Map();
+    }
+    get weightBytes() { return this.layout.used; }
+    _place(typed) {
+        const off = this.layout.take(typed.byteLength);
+        if (this.layout.used > this.weights.size) {
+            throw new Error(`weight arena exhausted (${this.layout.used} > ${this.weights.size})`);
+        }
+        this.weights.write(off, typed);
+        return off;
+    }
+    /** qweight I32 [in/8, out], qzeros I32 [in/g, out/8] or null, scales F16 bits [in/g, out], bias F32 [out] or null. */
+    uploadGptqLinear(name, p) {
+        if (this.linears.has(name)) throw new Error(`weight already exists: ${name}`);
+        const group = p.groupSize || 128;
+        const qw = this._place(p.qweight);
+        const qz = p.qzeros ? this._place(p.qzeros) : null;
+        const sc = this._place(p.scalesF16);
+        const b = p.bias ? this._place(Float32Array.from(p.bias)) : null;
+        const desc = makeDesc(qw, qz, sc, p.inFeatures, p.outFeatures, group, b);
+        const rc = addon.validate(desc, this.weights.size);
+        if (rc !== 0) throw libError(CODE_NAMES[rc] || 'QL_E_INVALID', addon.lastError());
+        this.linears.set(name, { desc, K: p.inFeatures, N: p.outFeatures });
+    }
+    uploadF32(name, data) {
+        if (this.f32Weights.has(name)) throw new Error(`weight already exists: ${name}`);
+        const a = Float32Array.from(data);
+        this.f32Weights.set(name, new Tensor(this.weights, this._place(a), a.length, [a.length], 'f32'));
+    }
+    uploadF16Bits(name, bytes, shape) {
+        if (this.f16Weights.has(name)) throw new Error(`weight already exists: ${name}`);
+        const n = shape.reduce((x, y) => x * y, 1);
+        this.f16Weights.set(name, new Tensor(this.weights, this._place(bytes), n, shape.slice(), 'f16'));
+    }
+    linear(name) {
+        const l = this.linears.get(name);
+        if (!l) throw new Error(`missing int4 weight: ${name}`);
+        return l;
+    }
+    /** C[M,N] = A[M,K] @ W^T (+ bias) — qwen.ts:568-618. A f32 or f16, C f32. */
+    gemm(A, weight, C, bias, M, N, K) {
+        const lin = this.linear(weight);
+        if (lin.K !== K || lin.N !== N) throw new Error(`gemm: ${weight} is [${lin.N},${lin.K}], called with N=${N} K=${K}`);
+        if (bias !== null && bias !== undefined && lin.desc.biasOff === null) throw new Error(`missing f32 weight: ${bias}`);
+        let desc = lin.desc;
+        if ((bias === null || bias === undefined) && desc.biasOff !== null) desc = Object.assign({}, desc, { biasOff: null });
+        if (A.arena !== C.arena || !A.pool || A.pool !== C.pool) throw new Error('gemm: A and C must come from one ActivationArena');
+        if (A.length < M * K || C.length < M * N) throw new Error('gemm: tensor too small for [M,K] / [M,N]');
+        const plan = addon.planLinear(M, N, K, desc.group);
+        const scratch = A.pool.scratchOffset(plan.scratchBytes);
+        addon.linear(this.ctx.handle, desc, this.weights.handle, A.arena.handle, A.offset,
+            A.dtype === 'f16' ? QL_DTYPE_F16 : QL_DTYPE_F32, M, C.offset, scratch);
+    }
+    /** Several linears on one input in one launch (q/k/v, gate/up; qwen.ts:411-413, :464-465). */
+    gemmBatch(A, weights, Cs, M) {
+        const descs = weights.map((w) => this.linear(w).desc);
+        if (!A.pool || Cs.some((c) => c.pool !== A.pool)) throw new Error('gemmBatch: A and every C must come from one ActivationArena');
+        const scratch = A.pool.scratchOffset(addon.planBatch(descs, M));
+        addon.linearBatch(this.ctx.handle, descs, this.weights.handle, A.arena.handle,
+            descs.map(() => A.offset), A.dtype === 'f16' ? QL_DTYPE_F16 : QL_DTYPE_F32, M,
+            Cs.map((c) => c.offset), scratch);
+    }
+    /** fp16 [N,K] copy, bit-identical to the reference's uploaded f16 weight buffer. */
+    unpackF16(name, out) {
+        const lin = this.linear(name);
+        if (out.dtype !== 'f16' || out.length < lin.N * lin.K) throw new Error('unpackF16: output must be an f16 tensor of N*K elements');
+        addon.unpack(this.ctx.handle, lin.desc, this.weights.handle, out.arena.handle, out.offset, false);
+    }
+    /** fp32 [N,K] = dequantizeGptqInt4 of the stored tensors (computed on the GPU). */
+    dequantize(name) {
+        const lin = this.linear(name);
+        const tmp = this.ctx.arena(lin.N * lin.K * 4);
+        try {
+            addon.unpack(this.ctx.handle, lin.desc, this.weights.handle, tmp.handle, 0, true);
+            return tmp.read(0, new Float32Array(lin.N * lin.K));
+        } finally {
+            tmp.release();
+        }
+    }
+    release() { this.weights.release(); }
+}
+
+// ------------------------------------------------------------------ qwen-loader.ts
+
+const PROJ = [['qW', 'self_attn.q_proj'], ['kW', 'self_attn.k_proj'], ['vW', 'self_attn.v_proj'],
+    ['oW', 'self_attn.o_proj'], ['gateW', 'mlp.gate_proj'], ['upW', 'mlp.up_proj'], ['downW', 'mlp.down_proj']];
+const BIASED = new Set(['qW', 'kW', 'vW']);
+
+function qwenLinearShapes(c) {
+    const C = c.nEmbd, HI = qwenKvDim(c), I = c.intermediate;
+    return { qW: [C, C], kW: [C, HI], vW: [C, HI], oW: [C, C], gateW: [C, I], upW: [C, I], downW: [I, C] };
+}
+
+/**
+ * loadQwenWeights (qwen-loader.ts:102-177) for a QuantLinearModel; `ctx` is unused (the model holds
+ * its context), as the reference's `_gpu` is. options: {path | buffer,
+ * config, keepLayer, onProgress, groupSize}. The int4 tensors go to the GPU packed after the
+ * shape checks of tests/qwen/qwen-format.ts:72-80; a kept layer is returned dequantized (fp32).
+ */
+function loadQwenWeights(ctx, model, options) {
+    const opt = options || {};
+    const config = opt.config || QWEN25_05B;
+    const group = opt.groupSize || 128;
+    const raw = opt.buffer || fs.readFileSync(opt.path);
+    const file = parseSafetensors(raw);
+    const C = config.nEmbd;
+    let tensorCount = 0;
+    const emb = requireTensor(file, 'model.embed_tokens.weight');
+    if (emb.shape.join(',') !== `${config.vocabSize},${C}`) {
+        throw new Error(`qwen-loader: embed_tokens shape [${emb.shape}], expected [${config.vocabSize},${C}]`);
+    }
+    if (emb.dtype !== 'F16') throw new Error(`qwen-loader: model.embed_tokens.weight expected F16, got ${emb.dtype}`);
+    model.uploadF16Bits('embed', readTensorBytes(file, 'model.embed_tokens.weight'), [config.vocabSize, C]);
+    tensorCount += 1;
+    model.uploadF32('finalNorm', readTensorF32(file, 'model.norm.weight'));
+    tensorCount += 1;
+    const shapes = qwenLinearShapes(config);
+    let kept;
+    for (let i = 0; i < config.nLayer; i++) {
+        const p = `model.layers.${i}`;
+        model.uploadF32(`L${i}.inNorm`, readTensorF32(file, `${p}.input_layernorm.weight`));
+        model.uploadF32(`L${i}.postNorm`, readTensorF32(file, `${p}.post_attention_layernorm.weight`));
+        tensorCount += 2;
+        const layer = {};
+        for (const [key, proj] of PROJ) {
+            const [K, N] = shapes[key];
+            const pre = `${p}.${proj}`;
+            expectTensor(file, `${pre}.qweight`, 'I32', [Math.ceil(K / 8), N]);
+            expectTensor(file, `${pre}.qzeros`, 'I32', [Math.ceil(K / group), Math.ceil(N / 8)]);
+            expectTensor(file, `${pre}.scales`, 'F16', [Math.ceil(K / group), N]);
+            const bias = BIASED.has(key) ? readTensorF32(file, `${pre}.bias`) : null;
+            model.uploadGptqLinear(`L${i}.${key}`, {
+                qweight: readTensorBytes(file, `${pre}.qweight`), qzeros: readTensorBytes(file, `${pre}.qzeros`),
+                scalesF16: readTensorBytes(file, `${pre}.scales`), inFeatures: K, outFeatures: N,
+                groupSize: group, bias,
+            });
+            tensorCount += bias ? 2 : 1;
+            if (opt.keepLayer === i) layer[key] = model.dequantize(`L${i}.${key}`);
+        }
+        if (opt.keepLayer === i) kept = layer;
+        if (opt.onProgress) opt.onProgress(i + 1, config.nLayer, `layer ${i + 1}/${config.nLayer}`);
+    }
+    return { gpuBytes: model.weightBytes, tensorCount, fileBytes: raw.byteLength, layer: kept };
+}
+
+module.exports = {
+    addon, ADDON_PATH, QL_DTYPE_F32, QL_DTYPE_F16, QWEN25_05B, qwenHeadDim, qwenKvDim,
+    dtypeByteSize, parseSafetensorsHeader, parseSafetensors, tensorCount, requireTensor,
+    expectTensor, f16BitsToF32, readTensorBytes, readTensorF32, ArenaLayout, Arena, Context,
+    makeDesc, dequantizeGptqInt4, Tensor, ActivationArena, QuantLinearModel,
+    qwenLinearShapes, loadQwenWeights,
+};
