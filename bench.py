@@ -40,6 +40,10 @@ GROUP = 128
 
 LAYER_LAUNCHES_05B = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
 LAYER_LAUNCHES_7B = [("q",), ("o",), ("gate", "up"), ("down",)]
+# one layer of a linear sequence: (proj, the proj whose output it reads; None = the layer input)
+SEQ_LAYER_05B = [("q", None), ("k", None), ("v", None), ("o", "q"), ("gate", "o"), ("up", "o"),
+                 ("down", "gate")]
+SEQ_LAYER_7B = [("q", None), ("o", "q"), ("gate", "o"), ("up", "o"), ("down", "gate")]
 
 
 def log(*a):
@@ -139,7 +143,71 @@ class Step:
         self.act.release()
 
 
-def timed(step: Step, steps: int, warmup: int) -> float:
+class SeqStep:
+    """The decode step as ONE persistent launch (ql_seq_*): the linears chained through their
+    outputs the way a layer consumes them — (q,k,v) <- h, o <- q, (gate,up) <- o, down <- gate,
+    next layer's h <- down — so each linear waits on the device for the one it reads, as after a
+    pass break in the reference (src/model/qwen.ts:556-559). Attention and the elementwise ops
+    between linears are outside the sequence (o reads q in attention's place, down reads gate in
+    SiLU(gate)*up's place); every one of the model's linears runs, with its real dependency."""
+
+    def __init__(self, ctx, model: Model, M: int, seed: int = 0x5EED):
+        self.ctx, self.model, self.M, self.x_dtype = ctx, model, M, ql.DTYPE_F32
+        lay = ql.ArenaLayout()
+        descs, xs, ys = [], [], []
+        self.order = []
+        C = model.shapes[(0, "q")][0]
+        h0 = lay.take(M * C * 4)
+        h = h0
+        for layer in range(model.layers):
+            y = {}
+            for proj, src in SEQ_LAYER_05B if model.shape == "0.5b" else SEQ_LAYER_7B:
+                d = model.descs[(layer, proj)]
+                x_off = h if src is None else y[src]
+                y[proj] = lay.take(M * d.N * 4)
+                descs.append(d)
+                xs.append(x_off)
+                ys.append(y[proj])
+                self.order.append((layer, proj))
+            h = y["down"]
+        self.act = ctx.arena(lay.used)
+        self.act.write(h0, synth.activations(M, C, seed=seed, key=(0, 0, M)))
+        self.x_offs, self.y_offs = xs, ys
+        self.seq = ctx.seq(descs, model.arena, self.act, xs, ql.DTYPE_F32, M, ys)
+        self.info = self.seq.info
+        self.bytes = sum(linear_bytes(model.shapes[lp][0], model.shapes[lp][1], M) for lp in self.order)
+        self.flops = sum(2 * M * model.shapes[lp][0] * model.shapes[lp][1] for lp in self.order)
+        # layer-0 view for the CPU baseline: (layer, group, projs, descs, x_off, y_offs, scratch)
+        self.launches = []
+        for i, (layer, proj) in enumerate(self.order):
+            if layer == 0:
+                self.launches.append((0, i, (proj,), [descs[i]], xs[i], [ys[i]], 0))
+        self.graph = None
+
+    def capture(self):
+        self.seq.run()
+        self.seq.status()
+        self.ctx.graph_begin()
+        self.seq.run()
+        self.graph = self.ctx.graph_end()
+
+    def run(self, steps: int) -> float:
+        self.ctx.sync()
+        self.ctx.timer_start()
+        for _ in range(steps):
+            self.graph.launch()
+        ms = self.ctx.timer_stop()
+        self.seq.status()
+        return ms
+
+    def release(self):
+        if self.graph:
+            self.graph.destroy()
+        self.seq.destroy()
+        self.act.release()
+
+
+def timed(step, steps: int, warmup: int) -> float:
     if step.graph is None:
         step.capture()
     if warmup:
@@ -193,6 +261,7 @@ def cpu_baseline(model: Model, step: Step, min_seconds: float):
     with tempfile.TemporaryDirectory() as d:
         meta = {"linears": []}
         gpu_y = []
+        atols_x = []
         for (layer, gi, projs, descs, x_off, y_offs, s_off) in t0_layer:
             x = step.act.read(x_off, (step.M, descs[0].K), np.float32)
             for p, desc, yo in zip(projs, descs, y_offs):
@@ -206,6 +275,7 @@ def cpu_baseline(model: Model, step: Step, min_seconds: float):
                                         "qweight": f"qw_{i}", "qzeros": f"qz_{i}",
                                         "scales": f"sc_{i}", "x": f"x_{i}"})
                 gpu_y.append(step.act.read(yo, (step.M, desc.N), np.float32))
+                atols_x.append(1e-5 * max(1.0, float(np.sqrt(np.mean(x.astype(np.float64) ** 2)))))
         json.dump(meta, open(os.path.join(d, "meta.json"), "w"))
         macs = sum(l["M"] * l["K"] * l["N"] for l in meta["linears"])
         if node:
@@ -235,9 +305,13 @@ def cpu_baseline(model: Model, step: Step, min_seconds: float):
             res = {"matvec_ms": (time.perf_counter() - t1) * 1e3 / reps, "dequant_ms": None,
                    "reps": reps, "cpu": "", "cpus": os.cpu_count()}
             kind_note = "C oracle (node not found)"
-    rel = max(float(np.max(np.abs(g.reshape(-1) - c) / (1e-5 / 1e-4 + np.abs(c))))
-              for g, c in zip(gpu_y, cpu_y))
-    ok = all(np.all(np.abs(g.reshape(-1) - c) <= 1e-5 + 1e-4 * np.abs(c)) for g, c in zip(gpu_y, cpu_y))
+    # |d| <= atol + 1e-4|ref| with atol = 1e-5 * rms(x): the reference's 1e-5 for N(0,1) inputs,
+    # scaled for the larger inputs of chained linears
+    atols = atols_x
+    rel = max(float(np.max(np.abs(g.reshape(-1) - c) / (a / 1e-4 + np.abs(c))))
+              for g, c, a in zip(gpu_y, cpu_y, atols))
+    ok = all(np.all(np.abs(g.reshape(-1) - c) <= a + 1e-4 * np.abs(c))
+             for g, c, a in zip(gpu_y, cpu_y, atols))
     per_step_us = res["matvec_ms"] * model.layers * 1e3
     return {
         "value": round(per_step_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
@@ -290,30 +364,42 @@ def main():
     roof = None
     step1 = None
     if only in ("all", "step05"):
-        step1 = Step(ctx, m05, 1)
+        step1 = SeqStep(ctx, m05, 1)
         ms_step = timed(step1, args.steps, args.warmup)
         value = ms_step * 1e3
         gbs = step1.bytes / (ms_step * 1e-3) / 1e9
-        n_launch = len(step1.launches)
-        log(f"0.5B step M=1: {value:.1f} us/step, {gbs:.0f} GB/s, {n_launch} launches")
+        si = step1.info
+        log(f"0.5B step M=1 (one launch): {value:.1f} us/step, {gbs:.0f} GB/s; plan {si.as_dict()}")
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "traffic": traffic_from_profiles("step05_m1"),
-                "kernel": "gemv_mfma_kernel<1,4,true>",
-                "launches_per_step": n_launch,
-                "bytes_per_launch": step1.bytes // n_launch,
-                "avg_launch_us": round(value / n_launch, 3),
-                "note": "avg launch duration = event-timed graph replay / launches (includes "
-                        "inter-kernel gaps); the 0.5B weights (186 MB) fit the 256 MB MALL"}
+                "traffic": traffic_from_profiles("seq05_m1"),
+                "kernel": "seq_kernel<1,2>",
+                "launches_per_step": 1,
+                "bytes_per_launch": step1.bytes,
+                "avg_launch_us": round(value, 3),
+                "passes": si.passes, "tiles": si.tiles, "reduces": si.reduces, "grid": si.grid,
+                "note": "one persistent launch per step: 168 linears chained through their "
+                        "outputs (96 dependent passes ordered on the device); launch duration = "
+                        "HIP-event time of the graph replays / steps; the 0.5B weights (186 MB) "
+                        "fit the 256 MB MALL"}
         flushed = flushed_step_ms(ctx, step1)
         extra["step05_m1_flushed_us"] = round(flushed * 1e3, 1)
         extra["step05_m1_flushed_gbs"] = round(step1.bytes / (flushed * 1e-3) / 1e9, 1)
         log(f"0.5B step M=1 MALL-flushed: {flushed*1e3:.1f} us")
+        st = Step(ctx, m05, 1)
+        ms = timed(st, args.steps, args.warmup)
+        extra["step05_m1_per_linear_launches"] = {
+            "us": round(ms * 1e3, 1), "gbs": round(st.bytes / (ms * 1e-3) / 1e9, 1),
+            "launches": len(st.launches),
+            "note": "same linears as ql_linear / ql_linear_batch launches (q,k,v | o | gate,up | "
+                    "down per layer) on independent inputs, graph-replayed"}
+        log(f"0.5B step M=1 per-linear launches: {ms*1e3:.1f} us ({len(st.launches)} launches)")
+        st.release()
 
     if only in ("all", "sweep"):
         sweep = {}
         for M in (1, 2, 4, 8, 16):
-            st = Step(ctx, m05, M)
+            st = SeqStep(ctx, m05, M)
             ms = timed(st, max(10, args.steps // 2), 2)
             sweep[str(M)] = {"us": round(ms * 1e3, 1), "gbs": round(st.bytes / (ms * 1e-3) / 1e9, 1)}
             st.release()
@@ -355,13 +441,19 @@ def main():
         log(f"7B weights: {m7.weight_bytes/1e9:.2f} GB uploaded in {time.time()-t0:.1f}s")
         s7 = {}
         for M in [int(v) for v in args.m7b.split(",")]:
-            st = Step(ctx, m7, M)
+            st = SeqStep(ctx, m7, M)
             ms = timed(st, max(10, args.steps // 2), 2)
             gbs = st.bytes / (ms * 1e-3) / 1e9
             s7[str(M)] = {"us": round(ms * 1e3, 1), "gbs": round(gbs, 1),
                           "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": st.bytes,
-                          "launches": len(st.launches)}
+                          "launches": 1, "passes": st.info.passes, "tiles": st.info.tiles}
             st.release()
+        st = Step(ctx, m7, 1)
+        ms = timed(st, max(10, args.steps // 2), 2)
+        s7["1_per_linear_launches"] = {"us": round(ms * 1e3, 1),
+                                       "gbs": round(st.bytes / (ms * 1e-3) / 1e9, 1),
+                                       "launches": len(st.launches)}
+        st.release()
         extra["step7b"] = s7
         log(f"7B step: {s7}")
         m7.arena.release()
@@ -376,7 +468,8 @@ def main():
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "int4xf32", "data": "synthetic",
         "config": {"workload": "Qwen2.5-0.5B-shaped decode step: 168 GPTQ int4 linears "
-                               "(group 128), M=1, fp32 activations, hipGraph replay",
+                               "(group 128) chained through their outputs, M=1, fp32 "
+                               "activations, one persistent launch per step (hipGraph replay)",
                    "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)",
                    "launches_per_step": roof["launches_per_step"] if roof else None},
         "roofline": roof, "cpu_baseline": cpu, "extra": extra,

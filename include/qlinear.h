@@ -22,6 +22,10 @@
  *   ql_sync, ql_timer_*           src/gpu/buffer.ts:123-145 mapAsync readback,
  *                                 src/gpu/pipeline.ts:119-161 timestamp-query profiling
  *   ql_graph_*                    src/gpu/pipeline.ts:55-117 CommandBatch (one submit per forward)
+ *   ql_plan_seq, ql_seq_*         src/gpu/pipeline.ts:71-116 CommandBatch.dispatch/endPass/submit
+ *                                 with src/model/qwen.ts:556-559 passBreak, as runForward uses
+ *                                 them (qwen.ts:382-387, :411-473): a forward's linears recorded
+ *                                 once, then submitted as one unit per step
  */
 #ifndef QLINEAR_H
 #define QLINEAR_H
@@ -150,6 +154,42 @@ int ql_plan_batch(int32_t count, const ql_gptq_desc* descs, int32_t M, uint64_t*
 int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
                     const ql_arena* weights, ql_arena* act, const uint64_t* x_offs,
                     int32_t x_dtype, int32_t M, const uint64_t* y_offs, uint64_t scratch_off);
+
+/* ---- linear sequences: many decode linears (M = 1..16) in ONE persistent launch.
+ * Linear i reads x_offs[i] and writes y_offs[i] (fp32 [M, N_i]) in `act`. When x_offs[i] equals
+ * y_offs[j] of an earlier linear j (with N_j == K_i), linear i consumes linear j's output and the
+ * kernel orders the two on the device (the reference's passBreak); every other input is external
+ * (x_dtype) and must not overlap any output; outputs must not overlap each other. All linears
+ * share one group size (64, 128 or 256), need N % 4 == 0, and 16-byte aligned qweight, bias, x
+ * and y offsets (scales 8-byte).
+ * ql_seq_create validates, plans and allocates the sequence's device tables and exchange
+ * buffers (the arenas are bound by address and must outlive it). ql_seq_run enqueues one launch
+ * on the context stream; it allocates nothing and may be captured into a graph and replayed.
+ * Runs of one sequence must not overlap (one stream). ql_seq_status waits for the stream and
+ * reports whether a run was aborted (a bounded device-side wait ran out: QL_E_STATE). */
+typedef struct ql_seq ql_seq;
+typedef struct ql_seq_info {
+    int32_t linears;
+    int32_t passes;       /* dependency depth: linears that must run one after another */
+    int32_t tiles;        /* GEMV tiles (64 columns x a K segment) */
+    int32_t reduces;      /* split-K reductions (one per column tile of a split linear) */
+    int32_t grid;         /* resident workgroups */
+    int32_t max_split;
+    uint64_t lds_bytes;   /* dynamic LDS per workgroup */
+    uint64_t device_bytes;/* tables + exchange buffers ql_seq_create allocates */
+} ql_seq_info;
+/* plan only (host, pure) for a given grid size: validation and the figures above */
+int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,
+                int32_t x_dtype, const uint64_t* y_offs, int32_t grid, ql_seq_info* info);
+int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights,
+                  ql_arena* act, const uint64_t* x_offs, int32_t x_dtype, int32_t M,
+                  const uint64_t* y_offs, ql_seq** out);
+int ql_seq_get_info(const ql_seq* seq, ql_seq_info* info);
+int ql_seq_run(ql_ctx* ctx, ql_seq* seq);
+int ql_seq_status(ql_ctx* ctx, ql_seq* seq);
+/* diagnostic: polls a device-side wait makes before aborting the run (default 4M, min 64) */
+int ql_seq_set_spin_limit(ql_seq* seq, uint32_t polls);
+int ql_seq_destroy(ql_seq* seq);
 
 /* ---- ordering and timing on the context stream */
 int ql_sync(ql_ctx* ctx);

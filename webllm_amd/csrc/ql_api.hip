@@ -5,9 +5,11 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "ql_internal.h"
 
@@ -32,6 +34,14 @@ struct ql_arena {
 struct ql_graph {
     hipGraph_t graph;
     hipGraphExec_t exec;
+};
+
+struct ql_seq {
+    int device;
+    char* dev;              // one allocation: tables, exchange buffers, tickets, abort/error words
+    ql::SeqArgs args;
+    uint64_t lds;
+    ql_seq_info info;
 };
 
 namespace {
@@ -190,6 +200,135 @@ int check_io(const ql_gptq_desc* d, const ql_arena* act, uint64_t x_off, int x_d
         return fail(QL_E_RANGE, "y [M,N] outside the activation arena");
     if (x_off % es || y_off % 4) return fail(QL_E_ALIGN, "misaligned x or y offset");
     return QL_OK;
+}
+
+uint64_t gptq_weight_bytes(const ql_gptq_desc* d)
+{
+    uint64_t qw, qz, sc;
+    ql_gptq_sizes(d->K, d->N, d->group, &qw, &qz, &sc);
+    return qw + sc + (d->qzeros_off == QL_NONE ? 0 : qz);
+}
+
+// Checks a sequence and finds each linear's producer: linear i reads linear j's output when
+// x_offs[i] == y_offs[j] (j < i, N_j == K_i). Every other input is external and must not overlap
+// any output of the sequence; outputs must not overlap each other.
+int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,
+                int32_t x_dtype, const uint64_t* y_offs, uint64_t w_bytes, uint64_t act_bytes,
+                std::vector<ql::SeqSpec>* specs)
+{
+    if (!descs || !x_offs || !y_offs) return fail(QL_E_INVALID, "null sequence arrays");
+    if (n <= 0 || n > ql::kSeqMaxLinears)
+        return fail(QL_E_INVALID, "a sequence holds 1..%d linears, got %d", ql::kSeqMaxLinears, n);
+    if (M < 1 || M > ql::kGemvMaxM) return fail(QL_E_INVALID, "sequences run decode rows M = 1..%d", ql::kGemvMaxM);
+    if (x_dtype != QL_DTYPE_F32 && x_dtype != QL_DTYPE_F16)
+        return fail(QL_E_INVALID, "x_dtype must be QL_DTYPE_F32 or QL_DTYPE_F16");
+    const uint64_t es = x_dtype == QL_DTYPE_F32 ? 4 : 2;
+    std::vector<std::pair<uint64_t, int>> ys(n);
+    for (int i = 0; i < n; i++) {
+        const ql_gptq_desc* d = &descs[i];
+        int rc = validate_desc(d, w_bytes);
+        if (rc) return rc;
+        if (!ql::gemv_fast_ok(M, d->N, d->K, d->group) || d->group != descs[0].group)
+            return fail(QL_E_INVALID,
+                        "linear %d: a sequence needs N %% 4 == 0, K %% group == 0 and one group size "
+                        "(64, 128 or 256) for all linears", i);
+        if (!gemv_aligned(d, x_offs[i], y_offs[i]))
+            return fail(QL_E_ALIGN, "linear %d: qweight, x, y and bias offsets must be 16-byte aligned, "
+                        "scales 8-byte", i);
+        if (!in_range(y_offs[i], (uint64_t)M * d->N * 4, act_bytes))
+            return fail(QL_E_RANGE, "linear %d: y [M,N] outside the activation arena", i);
+        ys[i] = {y_offs[i], i};
+    }
+    std::sort(ys.begin(), ys.end());
+    for (int k = 1; k < n; k++) {
+        const int a = ys[k - 1].second;
+        if (ys[k - 1].first + (uint64_t)M * descs[a].N * 4 > ys[k].first)
+            return fail(QL_E_INVALID, "outputs of linears %d and %d overlap", a, ys[k].second);
+    }
+    specs->assign(n, ql::SeqSpec{});
+    for (int i = 0; i < n; i++) {
+        const ql_gptq_desc* d = &descs[i];
+        ql::SeqSpec& s = (*specs)[i];
+        s.N = d->N;
+        s.K = d->K;
+        s.group = d->group;
+        s.src = -1;
+        s.weight_bytes = gptq_weight_bytes(d);
+        s.has_qzeros = d->qzeros_off != QL_NONE;
+        // producer: an output starting exactly at x
+        auto it = std::lower_bound(ys.begin(), ys.end(), std::make_pair(x_offs[i], -1));
+        if (it != ys.end() && it->first == x_offs[i]) {
+            const int j = it->second;
+            if (j >= i) return fail(QL_E_INVALID, "linear %d reads the output of linear %d, which runs later", i, j);
+            if (descs[j].N != d->K)
+                return fail(QL_E_INVALID, "linear %d reads linear %d's output, but K=%d != N=%d", i, j, d->K,
+                            descs[j].N);
+            s.src = j;
+            continue;
+        }
+        const uint64_t xb = (uint64_t)M * d->K * es;
+        if (!in_range(x_offs[i], xb, act_bytes))
+            return fail(QL_E_RANGE, "linear %d: x [M,K] outside the activation arena", i);
+        // an external input must not overlap any output
+        if (it != ys.end() && it->first < x_offs[i] + xb)
+            return fail(QL_E_INVALID, "linear %d: input overlaps the output of linear %d", i, it->second);
+        if (it != ys.begin()) {
+            const auto pv = *(it - 1);
+            if (pv.first + (uint64_t)M * descs[pv.second].N * 4 > x_offs[i])
+                return fail(QL_E_INVALID, "linear %d: input overlaps the output of linear %d", i, pv.second);
+        }
+    }
+    return QL_OK;
+}
+
+// Device memory of a planned sequence, laid out in one allocation.
+struct SeqLayout {
+    std::vector<uint64_t> y_ll, part_ll;
+    uint64_t lin, tasks, task_begin, first_tile, tickets, words, sym_zeros, sym_words, total;
+};
+
+SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut& p, int M)
+{
+    SeqLayout L;
+    uint64_t off = 0;
+    auto take = [&](uint64_t bytes) {
+        const uint64_t o = off;
+        off = align256(off + bytes);
+        return o;
+    };
+    const int n = (int)specs.size();
+    L.lin = take(sizeof(ql::SeqLinear) * n);
+    L.tasks = take(sizeof(ql::SeqTask) * std::max<size_t>(1, p.tasks.size()));
+    L.task_begin = take(sizeof(int32_t) * (p.grid + 1));
+    L.first_tile = take(sizeof(int32_t) * p.grid);
+    L.tickets = take(64 * ql::kSeqTickets);
+    L.words = take(64);
+    // stored-7 qzeros words (zero 8) for the largest linear without qzeros
+    L.sym_words = 0;
+    for (int i = 0; i < n; i++)
+        if (!specs[i].has_qzeros)
+            L.sym_words = std::max<uint64_t>(L.sym_words, (uint64_t)(specs[i].K / specs[i].group) *
+                                                              ((specs[i].N + 7) / 8));
+    L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
+    for (int i = 0; i < n; i++) {
+        const int S = p.split[i];
+        L.y_ll.push_back(take((uint64_t)M * specs[i].N * 8));
+        L.part_ll.push_back(S > 1 ? take((uint64_t)S * M * specs[i].N * 8) : 0);
+    }
+    L.total = off;
+    return L;
+}
+
+void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info* info)
+{
+    info->linears = n;
+    info->passes = p.passes;
+    info->tiles = p.tiles;
+    info->reduces = p.reduces;
+    info->grid = p.grid;
+    info->max_split = p.max_split;
+    info->lds_bytes = p.lds_bytes;
+    info->device_bytes = scratch;
 }
 
 int set_device(ql_ctx* ctx)
@@ -547,6 +686,150 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
     }
     b.wg_total = wg;
     QL_HIP(ql::launch_gemv_batch(b, ctx->stream));
+    return QL_OK;
+}
+
+int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,
+                int32_t x_dtype, const uint64_t* y_offs, int32_t grid, ql_seq_info* info)
+{
+    if (!info) return fail(QL_E_INVALID, "null info pointer");
+    if (grid < 1 || grid > (1 << 16)) return fail(QL_E_INVALID, "grid must be 1..65536");
+    std::vector<ql::SeqSpec> specs;
+    int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, UINT64_MAX, UINT64_MAX, &specs);
+    if (rc) return rc;
+    ql::SeqPlanOut p;
+    ql::plan_seq(specs, M, grid, &p);
+    fill_seq_info(p, n, seq_layout(specs, p, M).total, info);
+    return QL_OK;
+}
+
+int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights,
+                  ql_arena* act, const uint64_t* x_offs, int32_t x_dtype, int32_t M,
+                  const uint64_t* y_offs, ql_seq** out)
+{
+    if (!ctx || !weights || !act || !out) return fail(QL_E_INVALID, "null context, arena or output");
+    *out = nullptr;
+    if (ctx->capturing) return fail(QL_E_STATE, "ql_seq_create during graph capture");
+    if (weights->device != ctx->device || act->device != ctx->device)
+        return fail(QL_E_INVALID, "arenas belong to another device");
+    std::vector<ql::SeqSpec> specs;
+    int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, weights->size, act->size, &specs);
+    if (rc) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    int per_cu = 0;
+    QL_HIP(ql::seq_blocks_per_cu(M, descs[0].group, &per_cu));
+    if (per_cu < 1) return fail(QL_E_INVALID, "sequence kernel does not fit on a CU");
+    const int grid = std::min(per_cu, ql::seq_wg_per_cu()) * ctx->cu_count;
+    ql::SeqPlanOut p;
+    ql::plan_seq(specs, M, grid, &p);
+    if (p.lds_bytes > ql::seq_lds_budget()) return fail(QL_E_INVALID, "sequence plan exceeds LDS");
+    const SeqLayout lay = seq_layout(specs, p, M);
+
+    char* dev = nullptr;
+    QL_HIP(hipMalloc(&dev, lay.total));
+    std::vector<ql::SeqLinear> lin(n);
+    for (int i = 0; i < n; i++) {
+        const ql_gptq_desc* d = &descs[i];
+        ql::SeqLinear& L = lin[i];
+        const ql::GemvLinear g = make_linear(d, weights);
+        L.qweight = g.qweight;
+        L.qzeros = g.qzeros ? g.qzeros : reinterpret_cast<const uint32_t*>(dev + lay.sym_zeros);
+        L.scales = g.scales;
+        L.bias = g.bias;
+        L.x = specs[i].src >= 0 ? nullptr : act->base + x_offs[i];
+        L.y = reinterpret_cast<float*>(act->base + y_offs[i]);
+        L.y_ll = reinterpret_cast<uint64_t*>(dev + lay.y_ll[i]);
+        L.part_ll = p.split[i] > 1 ? reinterpret_cast<uint64_t*>(dev + lay.part_ll[i]) : nullptr;
+        L.src = specs[i].src;
+        L.N = d->N;
+        L.K = d->K;
+        L.S = p.split[i];
+        L.x_dtype = x_dtype;
+    }
+    hipError_t e = hipMemset(dev, 0, lay.total);
+    if (e == hipSuccess && lay.sym_words)
+        e = hipMemsetD32(reinterpret_cast<hipDeviceptr_t>(dev + lay.sym_zeros), 0x77777777,
+                         lay.sym_words);
+    if (e == hipSuccess) e = hipMemcpy(dev + lay.lin, lin.data(), sizeof(ql::SeqLinear) * n, hipMemcpyHostToDevice);
+    if (e == hipSuccess && !p.tasks.empty())
+        e = hipMemcpy(dev + lay.tasks, p.tasks.data(), sizeof(ql::SeqTask) * p.tasks.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(dev + lay.task_begin, p.task_begin.data(), sizeof(int32_t) * p.task_begin.size(),
+                      hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(dev + lay.first_tile, p.first_tile.data(), sizeof(int32_t) * p.first_tile.size(),
+                      hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(e, "ql_seq_create upload");
+    }
+    ql_seq* q = new ql_seq();
+    q->device = ctx->device;
+    q->dev = dev;
+    q->lds = p.lds_bytes;
+    ql::SeqArgs& a = q->args;
+    a.lin = reinterpret_cast<const ql::SeqLinear*>(dev + lay.lin);
+    a.tasks = reinterpret_cast<const ql::SeqTask*>(dev + lay.tasks);
+    a.task_begin = reinterpret_cast<const int32_t*>(dev + lay.task_begin);
+    a.first_tile = reinterpret_cast<const int32_t*>(dev + lay.first_tile);
+    a.tickets = reinterpret_cast<unsigned long long*>(dev + lay.tickets);
+    a.abort = reinterpret_cast<uint32_t*>(dev + lay.words);
+    a.err = reinterpret_cast<uint32_t*>(dev + lay.words + 4);
+    a.M = M;
+    a.G = p.grid;
+    a.group = descs[0].group;
+    a.spin_limit = 1u << 22;
+    fill_seq_info(p, n, lay.total, &q->info);
+    *out = q;
+    return QL_OK;
+}
+
+int ql_seq_get_info(const ql_seq* seq, ql_seq_info* info)
+{
+    if (!seq || !info) return fail(QL_E_INVALID, "null sequence or info");
+    *info = seq->info;
+    return QL_OK;
+}
+
+int ql_seq_run(ql_ctx* ctx, ql_seq* seq)
+{
+    if (!ctx || !seq) return fail(QL_E_INVALID, "null context or sequence");
+    if (seq->device != ctx->device) return fail(QL_E_INVALID, "sequence belongs to another device");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(ql::launch_seq(seq->args, seq->lds, ctx->stream));
+    return QL_OK;
+}
+
+int ql_seq_status(ql_ctx* ctx, ql_seq* seq)
+{
+    if (!ctx || !seq) return fail(QL_E_INVALID, "null context or sequence");
+    if (ctx->capturing) return fail(QL_E_STATE, "ql_seq_status during graph capture");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(hipStreamSynchronize(ctx->stream));
+    uint32_t words[2] = {0, 0};
+    QL_HIP(hipMemcpy(words, seq->args.abort, sizeof words, hipMemcpyDeviceToHost));
+    if (words[0] == 0 && words[1] == 0) return QL_OK;
+    QL_HIP(hipMemset(seq->args.abort, 0, sizeof words));
+    return fail(QL_E_STATE, "sequence run aborted (code %u): a wait exceeded its spin limit; outputs "
+                "of that run are invalid", words[1]);
+}
+
+int ql_seq_set_spin_limit(ql_seq* seq, uint32_t polls)
+{
+    if (!seq) return fail(QL_E_INVALID, "null sequence");
+    if (polls < 64) return fail(QL_E_INVALID, "spin limit must be at least 64 polls");
+    seq->args.spin_limit = polls;
+    return QL_OK;
+}
+
+int ql_seq_destroy(ql_seq* seq)
+{
+    if (!seq) return fail(QL_E_INVALID, "null sequence");
+    (void)hipSetDevice(seq->device);
+    (void)hipFree(seq->dev);
+    delete seq;
     return QL_OK;
 }
 

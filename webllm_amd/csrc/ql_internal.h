@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace ql {
 
 constexpr int kMaxBatch = 8;
@@ -68,5 +70,76 @@ struct UnpackArgs {
 };
 hipError_t launch_unpack(const UnpackArgs& a, bool fast, hipStream_t stream);
 hipError_t launch_unpack_f32(const UnpackArgs& a, hipStream_t stream);
+
+// ----------------------------------------------------------------------------------------------
+// Linear sequences: many decode linears (M <= 16) in one persistent launch. Linear i may read the
+// output of an earlier linear; the kernel orders them on the device.
+
+constexpr int kSeqMaxLinears = 4096;
+constexpr int kSeqTileCols = 64;       // output columns per sequence tile (one wave's width)
+constexpr int kSeqMaxSplit = 64;       // K segments per linear
+constexpr int kSeqTickets = 32;        // per-run ticket sub-counters (epoch), 64 B apart
+constexpr int kSeqTile = 0;
+constexpr int kSeqReduce = 1;
+constexpr uint32_t kSeqErrTimeout = 1;
+
+// Device table entry per linear (read-only in the kernel).
+struct SeqLinear {
+    const uint32_t* qweight;
+    const uint32_t* qzeros;    // never null: symmetric linears point at stored-7 words
+    const uint16_t* scales;
+    const float* bias;
+    const void* x;             // external input [M, K] (src < 0)
+    float* y;                  // output [M, N] for the caller
+    uint64_t* y_ll;            // output again as (value bits | epoch << 32) for consumers
+    uint64_t* part_ll;         // [S, M, N] split-K partial sums (S > 1), same encoding
+    int32_t src;               // producer linear (its y is this linear's x), or -1
+    int32_t N, K, S, x_dtype;
+    int32_t pad[3];
+};
+
+// One unit of work: a GEMV tile (64 columns x groups [g0, g1) of K) or the split-K reduction
+// of one column tile. Each workgroup runs its tasks in list order.
+struct SeqTask {
+    int32_t linear, kind, ct, seg, g0, g1;
+    int32_t next_tile;         // index of the same workgroup's next tile task, or -1
+    int32_t pad;
+};
+
+struct SeqArgs {
+    const SeqLinear* lin;
+    const SeqTask* tasks;
+    const int32_t* task_begin;      // [G + 1]
+    const int32_t* first_tile;      // [G], -1 when a workgroup has no tile task
+    unsigned long long* tickets;    // [kSeqTickets * 8]
+    uint32_t* abort;
+    uint32_t* err;
+    int32_t M, G, group;
+    uint32_t spin_limit;
+};
+
+// Host description of one linear of a sequence, for planning.
+struct SeqSpec {
+    int N, K, group, src;
+    bool has_qzeros;
+    uint64_t weight_bytes;
+};
+
+struct SeqPlanOut {
+    int grid = 0, passes = 0, tiles = 0, reduces = 0, max_split = 1, max_gseg = 0;
+    uint64_t lds_bytes = 0;
+    std::vector<int> pass_of, split;
+    std::vector<SeqTask> tasks;
+    std::vector<int32_t> task_begin, first_tile;
+};
+
+// Pure planning (no device calls): passes from the dependencies, a split per linear, tiles and
+// reductions dealt to `grid` workgroups.
+void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out);
+size_t seq_lds_budget();
+// Workgroups of the sequence kernel that fit on one CU at once.
+hipError_t seq_blocks_per_cu(int M, int group, int* blocks);
+int seq_wg_per_cu();
+hipError_t launch_seq(const SeqArgs& a, size_t lds, hipStream_t stream);
 
 }  // namespace ql

@@ -57,6 +57,15 @@ class Plan(ctypes.Structure):
         return KIND_NAMES.get(self.kind, "?")
 
 
+class SeqInfo(ctypes.Structure):
+    _fields_ = [("linears", ctypes.c_int32), ("passes", ctypes.c_int32), ("tiles", ctypes.c_int32),
+                ("reduces", ctypes.c_int32), ("grid", ctypes.c_int32), ("max_split", ctypes.c_int32),
+                ("lds_bytes", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64)]
+
+    def as_dict(self) -> dict:
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
 _lib = None
 
 
@@ -107,6 +116,15 @@ def lib():
         "ql_graph_end": (I, [P, pp]),
         "ql_graph_launch": (I, [P, P]),
         "ql_graph_destroy": (I, [P]),
+        "ql_plan_seq": (I, [I, ctypes.POINTER(GptqDesc), I, ctypes.POINTER(U64), I,
+                            ctypes.POINTER(U64), I, ctypes.POINTER(SeqInfo)]),
+        "ql_seq_create": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64), I, I,
+                              ctypes.POINTER(U64), pp]),
+        "ql_seq_get_info": (I, [P, ctypes.POINTER(SeqInfo)]),
+        "ql_seq_run": (I, [P, P]),
+        "ql_seq_status": (I, [P, P]),
+        "ql_seq_set_spin_limit": (I, [P, ctypes.c_uint32]),
+        "ql_seq_destroy": (I, [P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -138,6 +156,16 @@ def plan_batch(descs: list[GptqDesc], M: int) -> int:
     out = ctypes.c_uint64()
     _check(lib().ql_plan_batch(len(descs), arr, M, ctypes.byref(out)))
     return out.value
+
+
+def plan_seq(descs: list[GptqDesc], M: int, x_offs, y_offs, grid: int,
+             x_dtype: int = DTYPE_F32) -> SeqInfo:
+    """Validation and plan figures of a linear sequence for `grid` workgroups (host only)."""
+    n = len(descs)
+    info = SeqInfo()
+    _check(lib().ql_plan_seq(n, (GptqDesc * n)(*descs), M, (ctypes.c_uint64 * n)(*x_offs), x_dtype,
+                             (ctypes.c_uint64 * n)(*y_offs), grid, ctypes.byref(info)))
+    return info
 
 
 def validate(desc: GptqDesc, arena_bytes: int) -> int:
@@ -203,6 +231,43 @@ class Graph:
             self.handle = None
 
 
+class Seq:
+    """Decode linears run as one persistent launch; linear i consumes linear j's output when
+    x_offs[i] == y_offs[j] (src/gpu/pipeline.ts:71-116 CommandBatch with passBreak)."""
+
+    def __init__(self, ctx: "Context", descs: list[GptqDesc], weights: Arena, act: Arena, x_offs,
+                 x_dtype: int, M: int, y_offs):
+        n = len(descs)
+        h = ctypes.c_void_p()
+        _check(lib().ql_seq_create(ctx.handle, n, (GptqDesc * n)(*descs), weights.handle,
+                                   act.handle, (ctypes.c_uint64 * n)(*x_offs), x_dtype, M,
+                                   (ctypes.c_uint64 * n)(*y_offs), ctypes.byref(h)))
+        self.ctx = ctx
+        self.handle = h
+        ctx._owned.add(self)
+
+    @property
+    def info(self) -> SeqInfo:
+        out = SeqInfo()
+        _check(lib().ql_seq_get_info(self.handle, ctypes.byref(out)))
+        return out
+
+    def run(self):
+        _check(lib().ql_seq_run(self.ctx.handle, self.handle))
+
+    def status(self):
+        """Waits for the stream; raises QlError(QL_E_STATE) if a run was aborted."""
+        _check(lib().ql_seq_status(self.ctx.handle, self.handle))
+
+    def set_spin_limit(self, polls: int):
+        _check(lib().ql_seq_set_spin_limit(self.handle, polls))
+
+    def destroy(self):
+        if self.handle:
+            _check(lib().ql_seq_destroy(self.handle))
+            self.handle = None
+
+
 class Context:
     """One device, one HIP stream (src/gpu/device.ts:40-98 initGpu)."""
 
@@ -250,6 +315,10 @@ class Context:
         _check(lib().ql_linear_batch(self.handle, n, arr, weights.handle, act.handle, xo, x_dtype,
                                      M, yo, scratch_off))
 
+    def seq(self, descs: list[GptqDesc], weights: Arena, act: Arena, x_offs, x_dtype: int, M: int,
+            y_offs) -> Seq:
+        return Seq(self, descs, weights, act, x_offs, x_dtype, M, y_offs)
+
     def sync(self):
         _check(lib().ql_sync(self.handle))
 
@@ -272,7 +341,7 @@ class Context:
     def destroy(self):
         if self.handle:
             for obj in list(self._owned):
-                if isinstance(obj, Graph):
+                if isinstance(obj, (Graph, Seq)):
                     obj.destroy()
             for obj in list(self._owned):
                 if isinstance(obj, Arena):
