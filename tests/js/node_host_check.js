@@ -77,6 +77,24 @@ function gpu(dir) {
             Cs.forEach((C, i) => writeTyped(path.join(dir, b.outs[i]), C.read()));
             pool.reset();
         }
+        // a chained sequence run from JavaScript: each linear reads the previous one's output
+        if (spec.seq) {
+            const sq = spec.seq;
+            const descs = sq.weights.map((w) => model.linear(w).desc);
+            const X = pool.alloc([sq.M, descs[0].K]);
+            X.write(readF32(path.join(dir, sq.x)));
+            const Ys = descs.map((d) => pool.alloc([sq.M, d.N]));
+            const xOffs = descs.map((d, i) => (i === 0 ? X.offset : Ys[i - 1].offset));
+            const seq = ctx.seq(descs, model.weights, pool.arena, xOffs, q.QL_DTYPE_F32, sq.M,
+                Ys.map((y) => y.offset));
+            const info = seq.info;
+            seq.run();
+            seq.status();
+            Ys.forEach((Y, i) => writeTyped(path.join(dir, sq.outs[i]), Y.read()));
+            seq.destroy();
+            pool.reset();
+            spec.seqInfo = info;
+        }
         const u = spec.unpack;
         const U = pool.alloc([u.N, u.K], 'f16');
         model.unpackF16(u.weight, U);
@@ -110,7 +128,7 @@ function gpu(dir) {
         model.release();
         console.log(JSON.stringify({
             device: ctx.info(), tensorCount: res.tensorCount, gpuBytes: res.gpuBytes,
-            fileBytes: res.fileBytes, progress, errors,
+            fileBytes: res.fileBytes, progress, errors, seqInfo: spec.seqInfo || null,
         }));
     } finally {
         ctx.destroy();

@@ -34,7 +34,8 @@ BINDING = {
     "unpack": "ql_unpack_f16", "linear": "ql_linear", "linearBatch": "ql_linear_batch",
     "sync": "ql_sync", "timerStart": "ql_timer_start", "timerStop": "ql_timer_stop",
     "graphBegin": "ql_graph_begin", "graphEnd": "ql_graph_end", "graphLaunch": "ql_graph_launch",
-    "graphDestroy": "ql_graph_destroy",
+    "graphDestroy": "ql_graph_destroy", "seqCreate": "ql_seq_create", "seqRun": "ql_seq_run",
+    "seqStatus": "ql_seq_status", "seqInfo": "ql_seq_get_info", "seqDestroy": "ql_seq_destroy",
 }
 
 
@@ -101,6 +102,11 @@ def test_node_host_matches_oracle(tmp_path, orc):
     for k in names:
         t, b = kept[(1, k)]
         refs[f"b{k}.f32"] = (orc.gptq_linear(t.qweight, t.qzeros, t.scales, xb, b), False)
+    seq_names = ["qW", "oW", "gateW", "downW"]
+    xs = synth.activations(1, TINY.n_embd, seed=0x40E0)
+    xs.tofile(tmp_path / "xs")
+    cases["seq"] = {"weights": [f"L0.{k}" for k in seq_names], "M": 1, "x": "xs",
+                    "outs": [f"s{k}.f32" for k in seq_names]}
     K, N = shapes["gateW"]
     cases["unpack"] = {"weight": "L1.gateW", "N": N, "K": K, "out": "u.f16"}
     cases["dequant"] = {"prefix": "model.layers.1.mlp.down_proj", "K": shapes["downW"][0],
@@ -129,6 +135,17 @@ def test_node_host_matches_oracle(tmp_path, orc):
                                         t.N, 128)
         got = np.fromfile(tmp_path / out, dtype=np.float32).reshape(t.N, t.K)
         assert np.array_equal(got.view(np.uint32), W.view(np.uint32)), out
+    # the JavaScript-built sequence: each linear against the oracle on the input it consumed
+    assert res["seqInfo"]["passes"] == 4 and res["seqInfo"]["linears"] == 4
+    x_in = xs
+    for k in seq_names:
+        t, b = kept[(0, k)]
+        y = np.fromfile(tmp_path / f"s{k}.f32", dtype=np.float32).reshape(1, t.N)
+        ref = orc.gptq_linear(t.qweight, t.qzeros, t.scales, x_in, b)
+        atol = 1e-5 * max(1.0, float(np.sqrt(np.mean(x_in.astype(np.float64) ** 2))))
+        ok, max_abs, _ = orc.check_tolerance(y, ref, atol, 1e-4)
+        assert ok, f"seq {k}: maxAbs {max_abs:.3e}"
+        x_in = y
     e = res["errors"]
     assert "missing int4 weight: L9.qW" in e["missingWeight"]
     assert "called with N=" in e["wrongShape"]

@@ -37,6 +37,11 @@ namespace {
 //   QL_SEQ_MIN_TILE_KB   smallest tile the planner aims for, in KiB of packed weights
 //   QL_SEQ_MIN_GROUPS    fewest groups per K segment when a linear is split across workgroups
 //   QL_SEQ_WG_PER_CU     resident workgroups per CU the grid is sized for
+//   QL_SEQ_SENTINEL      1: a tile first polls one word per 64-value input chunk (wave 0), then
+//                        loads its input; 0: every lane polls its own input words
+#ifndef QL_SEQ_SENTINEL
+#define QL_SEQ_SENTINEL 1
+#endif
 #ifndef QL_SEQ_PREFETCH
 #define QL_SEQ_PREFETCH 3
 #endif
@@ -217,7 +222,9 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
 
     const int wg = blockIdx.x;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform (scalar) so that per-wave branches stay scalar: an exec-masked branch around
+    // the MFMA loop makes the compiler drain every load in flight
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15;
     const int kq = lane >> 4;
     const int M = a.M;
@@ -334,7 +341,7 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
         // the segment's activation digits (for all four waves' groups), from the external input
         // or from the producer's output words: wave 0 first waits for one word of each 64-value
         // chunk of the segment (one producer tile's columns)
-        if (P) {
+        if (P && QL_SEQ_SENTINEL) {
             if (wave == 0) {
                 const int c0 = task.g0 * GK / kCols;
                 const int c1 = task.g1 * GK / kCols;

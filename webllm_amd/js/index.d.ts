@@ -38,8 +38,22 @@ export class Arena {
     read<T extends ArrayBufferView>(off: number, into: T): T;
     release(): void;
 }
+export interface SeqInfo {
+    linears: number; passes: number; tiles: number; reduces: number; grid: number;
+    maxSplit: number; ldsBytes: number; deviceBytes: number;
+}
+/** A forward's decode linears (M <= 16) as one persistent launch; linear i reads linear j's
+ *  output when xOffs[i] === yOffs[j]. */
+export class Seq {
+    readonly info: SeqInfo;
+    run(): void;
+    status(): void;
+    destroy(): void;
+}
 export class Context {
     constructor(device?: number);
+    seq(descs: GptqDesc[], weights: Arena, act: Arena, xOffs: number[], xDtype: number, M: number,
+        yOffs: number[]): Seq;
     info(): { name: string; cuCount: number; hbmBytes: number };
     arena(bytes: number): Arena;
     sync(): void;

@@ -191,11 +191,39 @@ class Arena {
     }
 }
 
+/**
+ * A forward's decode linears as one persistent launch (ql_seq_*; the CommandBatch of
+ * src/gpu/pipeline.ts:71-116 with passBreak, qwen.ts:556-559): linear i consumes linear j's
+ * output when xOffs[i] === yOffs[j], and the kernel orders the two on the device.
+ */
+class Seq {
+    constructor(ctx, descs, weights, act, xOffs, xDtype, M, yOffs) {
+        this.ctx = ctx;
+        this.handle = addon.seqCreate(ctx.handle, descs, weights.handle, act.handle, xOffs, xDtype, M, yOffs);
+        ctx._seqs.add(this);
+    }
+    get info() { return addon.seqInfo(this.handle); }
+    run() { addon.seqRun(this.ctx.handle, this.handle); }
+    /** Waits for the stream; throws QL_E_STATE if a run was aborted. */
+    status() { addon.seqStatus(this.ctx.handle, this.handle); }
+    destroy() {
+        if (this.handle) {
+            addon.seqDestroy(this.handle);
+            this.handle = null;
+            this.ctx._seqs.delete(this);
+        }
+    }
+}
+
 /** One device, one stream (ql_create). */
 class Context {
     constructor(device) {
         this.handle = addon.create(device === undefined ? 0 : device);
         this._arenas = new Set();
+        this._seqs = new Set();
+    }
+    seq(descs, weights, act, xOffs, xDtype, M, yOffs) {
+        return new Seq(this, descs, weights, act, xOffs, xDtype, M, yOffs);
     }
     info() { return addon.deviceInfo(this.handle); }
     arena(bytes) { return new Arena(this, bytes); }
@@ -203,6 +231,7 @@ class Context {
     timerStart() { addon.timerStart(this.handle); }
     timerStop() { return addon.timerStop(this.handle); }
     destroy() {
+        for (const q of Array.from(this._seqs)) q.destroy();
         for (const a of Array.from(this._arenas)) a.release();
         if (this.handle) { addon.destroy(this.handle); this.handle = null; }
     }
@@ -490,7 +519,7 @@ function loadQwenWeights(ctx, model, options) {
 }
 
 module.exports = {
-    addon, ADDON_PATH, QL_DTYPE_F32, QL_DTYPE_F16, QWEN25_05B, qwenHeadDim, qwenKvDim,
+    addon, ADDON_PATH, QL_DTYPE_F32, QL_DTYPE_F16, QWEN25_05B, qwenHeadDim, qwenKvDim, Seq,
     dtypeByteSize, parseSafetensorsHeader, parseSafetensors, tensorCount, requireTensor,
     expectTensor, f16BitsToF32, readTensorBytes, readTensorF32, ArenaLayout, Arena, Context,
     makeDesc, dequantizeGptqInt4, Tensor, ActivationArena, QuantLinearModel,

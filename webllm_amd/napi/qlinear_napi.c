@@ -11,6 +11,7 @@
 
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "../../include/qlinear.h"
@@ -508,6 +509,95 @@ static napi_value js_graph_destroy(napi_env env, napi_callback_info info)
     return NULL;
 }
 
+/* seqCreate(ctx, descs[], weights, act, xOffs[], xDtype, M, yOffs[]) -> sequence handle */
+static napi_value js_seq_create(napi_env env, napi_callback_info info)
+{
+    napi_value argv[8];
+    void *ctx, *w, *act;
+    int32_t xdt, M;
+    uint32_t n, m;
+    if (get_args(env, info, 8, argv) || get_ptr(env, argv[0], &ctx)) return NULL;
+    if (napi_get_array_length(env, argv[1], &n) != napi_ok || n == 0 || n > 4096) {
+        napi_throw_type_error(env, "QL_E_INVALID", "expected an array of 1..4096 descriptors");
+        return NULL;
+    }
+    if (get_ptr(env, argv[2], &w) || get_ptr(env, argv[3], &act) || get_i32(env, argv[5], &xdt) ||
+        get_i32(env, argv[6], &M))
+        return NULL;
+    if (napi_get_array_length(env, argv[4], &m) != napi_ok || m != n ||
+        napi_get_array_length(env, argv[7], &m) != napi_ok || m != n) {
+        napi_throw_type_error(env, "QL_E_INVALID", "offset arrays must match the descriptors");
+        return NULL;
+    }
+    ql_gptq_desc* d = (ql_gptq_desc*)calloc(n, sizeof(ql_gptq_desc));
+    uint64_t* xo = (uint64_t*)calloc(n, sizeof(uint64_t));
+    uint64_t* yo = (uint64_t*)calloc(n, sizeof(uint64_t));
+    napi_value result = NULL;
+    int bad = !d || !xo || !yo;
+    for (uint32_t i = 0; i < n && !bad; i++) {
+        napi_value e;
+        bad = napi_get_element(env, argv[1], i, &e) != napi_ok || get_desc(env, e, &d[i]);
+    }
+    if (!bad) bad = get_u64_array(env, argv[4], xo, n) || get_u64_array(env, argv[7], yo, n);
+    if (!bad) {
+        ql_seq* seq = NULL;
+        if (!throw_rc(env, ql_seq_create((ql_ctx*)ctx, (int32_t)n, d, (ql_arena*)w, (ql_arena*)act, xo,
+                                         xdt, M, yo, &seq)))
+            napi_create_external(env, seq, NULL, NULL, &result);
+    }
+    free(d);
+    free(xo);
+    free(yo);
+    return result;
+}
+
+static napi_value js_seq_run(napi_env env, napi_callback_info info)
+{
+    napi_value argv[2];
+    void *ctx, *seq;
+    if (get_args(env, info, 2, argv) || get_ptr(env, argv[0], &ctx) || get_ptr(env, argv[1], &seq)) return NULL;
+    throw_rc(env, ql_seq_run((ql_ctx*)ctx, (ql_seq*)seq));
+    return NULL;
+}
+
+static napi_value js_seq_status(napi_env env, napi_callback_info info)
+{
+    napi_value argv[2];
+    void *ctx, *seq;
+    if (get_args(env, info, 2, argv) || get_ptr(env, argv[0], &ctx) || get_ptr(env, argv[1], &seq)) return NULL;
+    throw_rc(env, ql_seq_status((ql_ctx*)ctx, (ql_seq*)seq));
+    return NULL;
+}
+
+static napi_value js_seq_info(napi_env env, napi_callback_info info)
+{
+    napi_value argv[1];
+    void* seq;
+    if (get_args(env, info, 1, argv) || get_ptr(env, argv[0], &seq)) return NULL;
+    ql_seq_info si;
+    if (throw_rc(env, ql_seq_get_info((ql_seq*)seq, &si))) return NULL;
+    napi_value o;
+    CHECK_NAPI(env, napi_create_object(env, &o));
+    napi_set_named_property(env, o, "linears", make_i32(env, si.linears));
+    napi_set_named_property(env, o, "passes", make_i32(env, si.passes));
+    napi_set_named_property(env, o, "tiles", make_i32(env, si.tiles));
+    napi_set_named_property(env, o, "reduces", make_i32(env, si.reduces));
+    napi_set_named_property(env, o, "grid", make_i32(env, si.grid));
+    napi_set_named_property(env, o, "maxSplit", make_i32(env, si.max_split));
+    napi_set_named_property(env, o, "ldsBytes", make_u64(env, si.lds_bytes));
+    napi_set_named_property(env, o, "deviceBytes", make_u64(env, si.device_bytes));
+    return o;
+}
+
+static napi_value js_seq_destroy(napi_env env, napi_callback_info info)
+{
+    napi_value argv[1];
+    void* seq;
+    if (get_args(env, info, 1, argv) || get_ptr(env, argv[0], &seq)) return NULL;
+    throw_rc(env, ql_seq_destroy((ql_seq*)seq));
+    return NULL;
+}
+
 static napi_value init(napi_env env, napi_value exports)
 {
     const struct {
@@ -523,6 +613,8 @@ static napi_value init(napi_env env, napi_value exports)
         {"sync", js_sync}, {"timerStart", js_timer_start}, {"timerStop", js_timer_stop},
         {"graphBegin", js_graph_begin}, {"graphEnd", js_graph_end},
         {"graphLaunch", js_graph_launch}, {"graphDestroy", js_graph_destroy},
+        {"seqCreate", js_seq_create}, {"seqRun", js_seq_run}, {"seqStatus", js_seq_status},
+        {"seqInfo", js_seq_info}, {"seqDestroy", js_seq_destroy},
     };
     for (size_t i = 0; i < sizeof fns / sizeof fns[0]; i++) {
         napi_value f;
