@@ -151,19 +151,28 @@ class SeqStep:
     between linears are outside the sequence (o reads q in attention's place, down reads gate in
     SiLU(gate)*up's place); every one of the model's linears runs, with its real dependency."""
 
-    def __init__(self, ctx, model: Model, M: int, seed: int = 0x5EED):
+    def __init__(self, ctx, model: Model, M: int, seed: int = 0x5EED, chained: bool = True):
         self.ctx, self.model, self.M, self.x_dtype = ctx, model, M, ql.DTYPE_F32
+        self.chained = chained
         lay = ql.ArenaLayout()
         descs, xs, ys = [], [], []
         self.order = []
+        inputs = []          # (offset, K, key) of every externally written input
         C = model.shapes[(0, "q")][0]
         h0 = lay.take(M * C * 4)
+        inputs.append((h0, C, (0, 0, M)))
         h = h0
         for layer in range(model.layers):
             y = {}
-            for proj, src in SEQ_LAYER_05B if model.shape == "0.5b" else SEQ_LAYER_7B:
+            for i, (proj, src) in enumerate(SEQ_LAYER_05B if model.shape == "0.5b" else SEQ_LAYER_7B):
                 d = model.descs[(layer, proj)]
-                x_off = h if src is None else y[src]
+                if chained:
+                    x_off = h if src is None else y[src]
+                else:
+                    # the benchmark configs as written: every linear has its own x ~ N(0,1)
+                    x_off = h0 if layer == 0 and i == 0 else lay.take(M * d.K * 4)
+                    if x_off != h0:
+                        inputs.append((x_off, d.K, (layer + 1, i, M)))
                 y[proj] = lay.take(M * d.N * 4)
                 descs.append(d)
                 xs.append(x_off)
@@ -171,7 +180,8 @@ class SeqStep:
                 self.order.append((layer, proj))
             h = y["down"]
         self.act = ctx.arena(lay.used)
-        self.act.write(h0, synth.activations(M, C, seed=seed, key=(0, 0, M)))
+        for off, K, key in inputs:
+            self.act.write(off, synth.activations(M, K, seed=seed, key=key))
         self.x_offs, self.y_offs = xs, ys
         self.seq = ctx.seq(descs, model.arena, self.act, xs, ql.DTYPE_F32, M, ys)
         self.info = self.seq.info

@@ -65,8 +65,8 @@ def test_tiles_cover_every_column_and_segment():
     x = c.ext(3584)
     c.add(3584, 18944, x)
     info = c.plan(grid=512)
-    # 296 tiles of 64 columns, each linear split into at most 64 K segments
-    assert info.tiles % 296 == 0 and info.tiles >= 296
+    # 296 blocks of 64 columns per K segment, dealt as runs to at most 512 workgroups
+    assert 296 <= info.tiles <= 512 + 296 * info.max_split
     assert info.max_split <= 64
     assert info.reduces == (296 if info.max_split > 1 else 0)
     assert info.device_bytes > 0 and info.lds_bytes > 0
@@ -81,7 +81,8 @@ def test_split_respects_lds_for_16_rows():
     assert info.max_split >= 1
     # each segment's activation digits fit the 48 KiB budget
     assert info.lds_bytes <= 49152
-    assert info.tiles == 56 * info.max_split
+    # 56 blocks per segment on 8 workgroups: runs of whole blocks, at most one cut per row
+    assert 8 <= info.tiles <= 8 + info.max_split
     assert info.max_split <= min(groups, 64)
 
 

@@ -13,6 +13,43 @@ namespace ql {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+// Load through the global address space (generic pointers compile to flat loads, which count
+// against both the vector-memory and the LDS wait counters). T must be a scalar or a native
+// (ext_vector_type) vector: HIP's uint4/uint2 are classes whose copy constructor takes a generic
+// reference, which turns the load back into a flat one.
+template <typename T>
+__device__ __forceinline__ T ld_global(const T* p)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *(const __attribute__((address_space(1))) T*)(p);
+#else
+    return *p;   // host pass: never executed
+#endif
+}
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Store through the global address space. A flat store still in flight makes the compiler wait
+// for every outstanding vector-memory operation at the next wait it places (it cannot tell flat
+// from LDS completions apart), which would drain the weight prefetch after each block's output.
+template <typename T>
+__device__ __forceinline__ void st_global(T* p, T v)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    *(__attribute__((address_space(1))) T*)(p) = v;
+#else
+    *p = v;      // host pass: never executed
+#endif
+}
+
+// A pointer as a global-address-space pointer (device pass only; the host pass never runs it).
+#if defined(__HIP_DEVICE_COMPILE__)
+#define QL_GLOBAL(T, p) ((__attribute__((address_space(1))) T*)(p))
+#else
+#define QL_GLOBAL(T, p) (p)
+#endif
+
+
 __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c)
 {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -31,13 +68,13 @@ __device__ __forceinline__ int group_exponent(float amax)
 __device__ __forceinline__ void load8(const void* x, int x_dtype, size_t base, float v[8])
 {
     if (x_dtype == 0) {
-        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base);
-        const float4 a0 = src[0], a1 = src[1];
+        const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + base);
+        const f32x4 a0 = ld_global(src), a1 = ld_global(src + 1);
         v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
         v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
     } else {
         const f16x8 h = __builtin_bit_cast(
-            f16x8, *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base));
+            f16x8, ld_global(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(x) + base)));
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = (float)h[e];
     }

@@ -98,12 +98,13 @@ struct SeqLinear {
     int32_t pad[3];
 };
 
-// One unit of work: a GEMV tile (64 columns x groups [g0, g1) of K) or the split-K reduction
-// of one column tile. Each workgroup runs its tasks in list order.
+// One unit of work: a GEMV tile (nblk blocks of 64 columns from block ct, over groups [g0, g1)
+// of K, segment seg) or the split-K reduction of block ct. Each workgroup runs its tasks in
+// list order.
 struct SeqTask {
     int32_t linear, kind, ct, seg, g0, g1;
     int32_t next_tile;         // index of the same workgroup's next tile task, or -1
-    int32_t pad;
+    int32_t nblk;
 };
 
 struct SeqArgs {
