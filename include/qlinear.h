@@ -174,9 +174,11 @@ typedef struct ql_seq_info {
     int32_t tiles;        /* GEMV tiles (64 columns x a K segment) */
     int32_t reduces;      /* split-K reductions (one per column tile of a split linear) */
     int32_t grid;         /* resident workgroups */
-    int32_t max_split;
+    int32_t max_split;    /* most parts (K pieces) of one 64-column block */
     uint64_t lds_bytes;   /* dynamic LDS per workgroup */
     uint64_t device_bytes;/* tables + exchange buffers ql_seq_create allocates */
+    uint64_t total_units; /* block-groups (64 columns x one quantization group) of all linears */
+    uint64_t busiest_units; /* block-groups of the most loaded workgroup: balance = busiest*grid/total */
 } ql_seq_info;
 /* plan only (host, pure) for a given grid size: validation and the figures above */
 int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,

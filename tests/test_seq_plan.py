@@ -65,10 +65,12 @@ def test_tiles_cover_every_column_and_segment():
     x = c.ext(3584)
     c.add(3584, 18944, x)
     info = c.plan(grid=512)
-    # 296 blocks of 64 columns per K segment, dealt as runs to at most 512 workgroups
-    assert 296 <= info.tiles <= 512 + 296 * info.max_split
-    assert info.max_split <= 64
-    assert info.reduces == (296 if info.max_split > 1 else 0)
+    # 296 blocks x 28 groups = 8288 block-groups on 512 workgroups: runs of 16-17 groups, so a
+    # block is cut where a run boundary falls inside it (at most 3 parts) and reduced
+    assert info.total_units == 296 * 28
+    assert info.busiest_units <= 8288 // 512 + 1
+    assert 2 <= info.max_split <= 3
+    assert 0 < info.reduces <= 296
     assert info.device_bytes > 0 and info.lds_bytes > 0
 
 
@@ -77,13 +79,75 @@ def test_split_respects_lds_for_16_rows():
     x = c.ext(18944)
     c.add(18944, 3584, x)
     info = c.plan(grid=8)
-    groups = 18944 // 128
-    assert info.max_split >= 1
-    # each segment's activation digits fit the 48 KiB budget
-    assert info.lds_bytes <= 49152
-    # 56 blocks per segment on 8 workgroups: runs of whole blocks, at most one cut per row
-    assert 8 <= info.tiles <= 8 + info.max_split
-    assert info.max_split <= min(groups, 64)
+    # 16 rows: 104 KiB of digit LDS per workgroup, 8320 B per group, so a tile covers at most
+    # 12 groups and K (148 groups) splits into 13 segments; 7-block chunks walk all segments
+    # before the next chunk, one chunk per run
+    assert info.lds_bytes <= 104 << 10
+    assert info.max_split == 13
+    assert info.tiles == 8 * 13
+    assert info.busiest_units == 56 * 148 // 8
+    assert info.reduces == 8                 # each run reduces its own 7 blocks in one task
+
+
+def test_lds_budget_of_few_rows():
+    c = Chain(M=4)
+    x = c.ext(3584)
+    c.add(3584, 3584, x)
+    info = c.plan(grid=8)
+    # 4 rows: 104 KiB of digits (2080 B per group): 28 groups fit, so no block is split and
+    # nothing is reduced
+    assert info.lds_bytes <= 104 << 10
+    assert info.max_split == 1 and info.reduces == 0
+
+
+def qwen7b(c: Chain, layers: int, chained: bool, C=3584, I=18944):
+    """The 7B-shaped linears (q, o, gate, up, down per layer), chained through their outputs or
+    each with its own input as the benchmark configs define."""
+    h = c.ext(C)
+    for _ in range(layers):
+        q = c.add(C, C, h if chained else c.ext(C))
+        o = c.add(C, C, q if chained else c.ext(C))
+        g = c.add(C, I, o if chained else c.ext(C))
+        c.add(C, I, o if chained else c.ext(C))
+        h = c.add(I, C, g if chained else c.ext(I))
+    return c
+
+
+@pytest.mark.parametrize("M,grid", [(1, 512), (4, 512), (16, 256)])
+def test_balance_7b_independent(M, grid):
+    info = qwen7b(Chain(M=M), 28, chained=False).plan(grid=grid)
+    assert info.passes == 1 and info.linears == 140
+    # one pass: every workgroup within one group of the mean
+    assert info.busiest_units <= info.total_units // grid + 1
+    assert info.balance < 1.01
+
+
+def test_balance_7b_chained():
+    info = qwen7b(Chain(), 4, chained=True).plan(grid=512)
+    assert info.passes == 16
+    # streaming passes are balanced to one group each; q/o passes are latency-bound
+    assert info.balance < 1.15
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_plans_verify(seed):
+    """Random shapes, batch rows, group sizes, grids and dependency graphs: ql_plan_seq checks
+    each plan (coverage, parts, reductions, pass order) and raises on a violation."""
+    import random
+    rng = random.Random(0x5EC0 + seed)
+    for _ in range(25):
+        group = rng.choice([64, 128, 256])
+        M = rng.choice([1, 2, 3, 4, 8, 16])
+        c = Chain(M=M, group=group)
+        outs = []
+        for _ in range(rng.randint(1, 12)):
+            K = group * rng.randint(1, 160)
+            N = 4 * rng.randint(1, 1200)
+            srcs = [y for y, n in outs if n == K]
+            x = rng.choice(srcs) if srcs and rng.random() < 0.6 else c.ext(K)
+            outs.append((c.add(K, N, x), N))
+        info = c.plan(grid=rng.choice([1, 2, 7, 64, 256, 512, 600]))
+        assert info.total_units > 0 and info.max_split <= 4096
 
 
 @pytest.mark.parametrize("group", [64, 256])

@@ -255,6 +255,7 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
         s.src = -1;
         s.weight_bytes = gptq_weight_bytes(d);
         s.has_qzeros = d->qzeros_off != QL_NONE;
+        s.has_bias = d->bias_off != QL_NONE;
         // producer: an output starting exactly at x
         auto it = std::lower_bound(ys.begin(), ys.end(), std::make_pair(x_offs[i], -1));
         if (it != ys.end() && it->first == x_offs[i]) {
@@ -283,8 +284,8 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
 
 // Device memory of a planned sequence, laid out in one allocation.
 struct SeqLayout {
-    std::vector<uint64_t> y_ll, part_ll;
-    uint64_t lin, tasks, task_begin, first_tile, tickets, words, sym_zeros, sym_words, total;
+    std::vector<uint64_t> y_ll;
+    uint64_t lin, tasks, task_begin, first_tile, tickets, words, sym_zeros, sym_words, part, total;
 };
 
 SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut& p, int M)
@@ -310,11 +311,8 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
             L.sym_words = std::max<uint64_t>(L.sym_words, (uint64_t)(specs[i].K / specs[i].group) *
                                                               ((specs[i].N + 7) / 8));
     L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
-    for (int i = 0; i < n; i++) {
-        const int S = p.split[i];
-        L.y_ll.push_back(take((uint64_t)M * specs[i].N * 8));
-        L.part_ll.push_back(S > 1 ? take((uint64_t)S * M * specs[i].N * 8) : 0);
-    }
+    for (int i = 0; i < n; i++) L.y_ll.push_back(take((uint64_t)M * specs[i].N * 8));
+    L.part = take(std::max<uint64_t>(1, p.slots) * (uint64_t)M * ql::kSeqTileCols * 8);
     L.total = off;
     return L;
 }
@@ -329,6 +327,8 @@ void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info
     info->max_split = p.max_split;
     info->lds_bytes = p.lds_bytes;
     info->device_bytes = scratch;
+    info->total_units = p.total_units;
+    info->busiest_units = p.busiest_units;
 }
 
 int set_device(ql_ctx* ctx)
@@ -699,6 +699,8 @@ int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
     if (rc) return rc;
     ql::SeqPlanOut p;
     ql::plan_seq(specs, M, grid, &p);
+    const std::string bad = ql::verify_seq_plan(specs, M, p);
+    if (!bad.empty()) return fail(QL_E_INVALID, "sequence plan check failed: %s", bad.c_str());
     fill_seq_info(p, n, seq_layout(specs, p, M).total, info);
     return QL_OK;
 }
@@ -722,7 +724,10 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
     const int grid = std::min(per_cu, ql::seq_wg_per_cu()) * ctx->cu_count;
     ql::SeqPlanOut p;
     ql::plan_seq(specs, M, grid, &p);
-    if (p.lds_bytes > ql::seq_lds_budget()) return fail(QL_E_INVALID, "sequence plan exceeds LDS");
+    // a plan that left a group uncomputed or a part unreduced would make the kernel wait forever
+    const std::string bad = ql::verify_seq_plan(specs, M, p);
+    if (!bad.empty()) return fail(QL_E_INVALID, "sequence plan check failed: %s", bad.c_str());
+    if (p.lds_bytes > ql::seq_lds_budget(M, descs[0].group)) return fail(QL_E_INVALID, "sequence plan exceeds LDS");
     const SeqLayout lay = seq_layout(specs, p, M);
 
     char* dev = nullptr;
@@ -739,11 +744,9 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
         L.x = specs[i].src >= 0 ? nullptr : act->base + x_offs[i];
         L.y = reinterpret_cast<float*>(act->base + y_offs[i]);
         L.y_ll = reinterpret_cast<uint64_t*>(dev + lay.y_ll[i]);
-        L.part_ll = p.split[i] > 1 ? reinterpret_cast<uint64_t*>(dev + lay.part_ll[i]) : nullptr;
         L.src = specs[i].src;
         L.N = d->N;
         L.K = d->K;
-        L.S = p.split[i];
         L.x_dtype = x_dtype;
     }
     hipError_t e = hipMemset(dev, 0, lay.total);
@@ -775,6 +778,7 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
     a.tickets = reinterpret_cast<unsigned long long*>(dev + lay.tickets);
     a.abort = reinterpret_cast<uint32_t*>(dev + lay.words);
     a.err = reinterpret_cast<uint32_t*>(dev + lay.words + 4);
+    a.part = reinterpret_cast<uint64_t*>(dev + lay.part);
     a.M = M;
     a.G = p.grid;
     a.group = descs[0].group;

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
 #include <vector>
 
 namespace ql {
@@ -77,11 +78,12 @@ hipError_t launch_unpack_f32(const UnpackArgs& a, hipStream_t stream);
 
 constexpr int kSeqMaxLinears = 4096;
 constexpr int kSeqTileCols = 64;       // output columns per sequence tile (one wave's width)
-constexpr int kSeqMaxSplit = 64;       // K segments per linear
+constexpr int kSeqMaxSplit = 4096;     // parts (K pieces) of one 64-column block, at most
 constexpr int kSeqTickets = 32;        // per-run ticket sub-counters (epoch), 64 B apart
 constexpr int kSeqTile = 0;
 constexpr int kSeqReduce = 1;
 constexpr uint32_t kSeqErrTimeout = 1;
+constexpr int kSeqBiasBlocks = 64;    // most blocks of a tile that adds a bias (staged in LDS)
 
 // Device table entry per linear (read-only in the kernel).
 struct SeqLinear {
@@ -92,19 +94,22 @@ struct SeqLinear {
     const void* x;             // external input [M, K] (src < 0)
     float* y;                  // output [M, N] for the caller
     uint64_t* y_ll;            // output again as (value bits | epoch << 32) for consumers
-    uint64_t* part_ll;         // [S, M, N] split-K partial sums (S > 1), same encoding
     int32_t src;               // producer linear (its y is this linear's x), or -1
-    int32_t N, K, S, x_dtype;
-    int32_t pad[3];
+    int32_t N, K, x_dtype;
 };
 
-// One unit of work: a GEMV tile (nblk blocks of 64 columns from block ct, over groups [g0, g1)
-// of K, segment seg) or the split-K reduction of block ct. Each workgroup runs its tasks in
-// list order.
+// One unit of work, run by one workgroup in list order.
+//  tile:   blocks ct .. ct+nblk-1 (64 columns each) over groups [g0, g1) of K. slot < 0: the
+//          blocks are whole (all of K) and the tile writes the outputs; otherwise block ct+b
+//          writes its partial sums to pool slot (slot + b*stride).
+//  reduce: blocks ct .. ct+nblk-1, each the sum of `parts` partial slots (slot + b*stride + p,
+//          p = 0..parts-1, in ascending K order), plus bias; writes the outputs.
 struct SeqTask {
-    int32_t linear, kind, ct, seg, g0, g1;
+    int32_t linear, kind, ct, nblk;
+    int32_t g0, g1, slot, stride;
+    int32_t parts;
     int32_t next_tile;         // index of the same workgroup's next tile task, or -1
-    int32_t nblk;
+    int32_t pad[2];
 };
 
 struct SeqArgs {
@@ -115,6 +120,7 @@ struct SeqArgs {
     unsigned long long* tickets;    // [kSeqTickets * 8]
     uint32_t* abort;
     uint32_t* err;
+    uint64_t* part;                 // partial-sum pool: slot s holds [M][64] epoch-tagged words
     int32_t M, G, group;
     uint32_t spin_limit;
 };
@@ -122,14 +128,16 @@ struct SeqArgs {
 // Host description of one linear of a sequence, for planning.
 struct SeqSpec {
     int N, K, group, src;
-    bool has_qzeros;
+    bool has_qzeros, has_bias;
     uint64_t weight_bytes;
 };
 
 struct SeqPlanOut {
     int grid = 0, passes = 0, tiles = 0, reduces = 0, max_split = 1, max_gseg = 0;
+    uint64_t slots = 0;             // partial-sum pool slots
+    uint64_t total_units = 0, busiest_units = 0;   // block-groups: all, most on one workgroup
     uint64_t lds_bytes = 0;
-    std::vector<int> pass_of, split;
+    std::vector<int> pass_of;
     std::vector<SeqTask> tasks;
     std::vector<int32_t> task_begin, first_tile;
 };
@@ -137,7 +145,12 @@ struct SeqPlanOut {
 // Pure planning (no device calls): passes from the dependencies, a split per linear, tiles and
 // reductions dealt to `grid` workgroups.
 void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out);
-size_t seq_lds_budget();
+// Checks a plan against its linears: every (linear, column block, group) computed by exactly one
+// tile; a block split into parts reduced exactly once, over slots in ascending K order that its
+// tiles write; passes in order within each workgroup's list, and a pass's reductions after all
+// of that workgroup's tiles of the pass. Returns an empty string or the first violation.
+std::string verify_seq_plan(const std::vector<SeqSpec>& lin, int M, const SeqPlanOut& p);
+size_t seq_lds_budget(int M, int group);   // dynamic LDS a sequence may use per workgroup
 // Workgroups of the sequence kernel that fit on one CU at once.
 hipError_t seq_blocks_per_cu(int M, int group, int* blocks);
 int seq_wg_per_cu();

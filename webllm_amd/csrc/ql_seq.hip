@@ -22,6 +22,8 @@
 // * Every wait is bounded. A wait that runs out sets a shared abort word and an error code; every
 //   other wait sees the abort word and returns, so the grid always drains.
 #include <algorithm>
+#include <cstdio>
+#include <string>
 #include <vector>
 
 #include "ql_device.h"
@@ -34,6 +36,10 @@ namespace {
 
 // Tunables (compile-time):
 //   QL_SEQ_PREFETCH      groups each wave keeps in flight (jobs per wave padded to a multiple)
+//   QL_SEQ_PREFETCH_WIDE the same for M > 8 (one workgroup per CU leaves registers for more)
+//   QL_SEQ_WAVES         waves per workgroup for M <= 8 with groups of at most 128 (8 or 4)
+//   QL_SEQ_CLASS_CUT     1: a streaming pass gives every workgroup an equal share of each
+//                        (K, N) shape class; 0: one cut over all the pass's linears
 //   QL_SEQ_STREAM_KB     weight KiB per workgroup from which a pass is planned for streaming
 //                        (several evenly split blocks per workgroup) instead of one block each
 //   QL_SEQ_MIN_GROUPS    fewest groups per K segment when a linear is split across workgroups
@@ -47,6 +53,15 @@ namespace {
 #ifndef QL_SEQ_PREFETCH
 #define QL_SEQ_PREFETCH 2
 #endif
+#ifndef QL_SEQ_PREFETCH_WIDE
+#define QL_SEQ_PREFETCH_WIDE 4
+#endif
+#ifndef QL_SEQ_CLASS_CUT
+#define QL_SEQ_CLASS_CUT 0
+#endif
+#ifndef QL_SEQ_WAVES
+#define QL_SEQ_WAVES 8
+#endif
 #ifndef QL_SEQ_PRO_CHUNKS
 #define QL_SEQ_PRO_CHUNKS 1
 #endif
@@ -59,12 +74,12 @@ namespace {
 #ifndef QL_SEQ_WG_PER_CU
 #define QL_SEQ_WG_PER_CU 2
 #endif
-constexpr int kP = QL_SEQ_PREFETCH;
 constexpr int kMinGroups = QL_SEQ_MIN_GROUPS;
-constexpr size_t kLdsBudget = 49152;
+// Dynamic LDS (activation digits) per workgroup. Every variant runs one workgroup per CU (160 KB
+// of LDS), of which the reduction ring takes up to 32 KB and the staged bias 16 KB.
+size_t lds_budget(int, int) { return (size_t)104 << 10; }
 constexpr int kCols = kSeqTileCols;     // 64 output columns per tile
 constexpr int kSumBatch = 16;           // partial sums a reduction loads per round trip
-constexpr int kWaves = 4;
 // a pass with at least this many weight bytes per workgroup streams from HBM (7B-shaped linears)
 // rather than waiting on latency (0.5B-shaped linears, MALL-resident)
 constexpr uint64_t kStreamBytes = (uint64_t)QL_SEQ_STREAM_KB << 10;
@@ -203,25 +218,32 @@ __device__ bool finish8_ll(const uint64_t* p, uint32_t e, uint64_t w[8], float v
     return true;
 }
 
-// Where a wave's packed-weight loads come from for one 64-column block of a tile: this wave's
-// groups [g0, glast] of the tile's segment (a wave without groups re-reads the segment start;
-// its jobs are never consumed). Every field is wave-uniform; the lane's column is derived from
-// blk at each fetch, so selecting one source or another stays scalar.
+// One wave's view of a tile for its weight loads: the tile's blocks ct .. ct+nblk-1 and the
+// wave's groups g0 .. g0+wcount-1 of the tile's K segment. Every field is wave-uniform, so
+// selecting one view or another stays scalar.
 struct FetchSrc {
     const uint32_t* qweight;
     const uint32_t* qzeros;
     const uint16_t* scales;
-    int N, g0, glast, blk;
+    int N, ct, nblk, g0, wcount;
 };
 
-template <int T, int NB, int RB>
-__global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
+template <int T, int NB, int RG, int kP, int W>
+__global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
 {
+    constexpr int kThreads = 64 * W;
     // dynamic LDS: activation digits [block][kq][row] (16 B), then {2^-E, Sx}[group][m]
     extern __shared__ uint4 dyn_lds[];
-    // the four waves' sums of one 64-column block, [buffer][wave][m][column]; with two buffers
-    // consecutive blocks alternate and need one barrier each
-    __shared__ float red[RB][kWaves][4 * T][kCols];
+    // Ring of RG slots for the waves' sums of a 64-column block, [slot][wave][m][column]. Each
+    // wave writes its sums and counts itself in (ring_arrive); the last to arrive adds the W sums
+    // in wave order, stores the block and marks the slot free (ring_done = the block's sequence
+    // number). Waves therefore never wait for each other between blocks, only for a slot a full
+    // ring behind.
+    __shared__ float red[RG][W][4 * T][kCols];
+    __shared__ int ring_arrive[RG];
+    __shared__ int ring_done[RG];
+    // the bias of a tile's columns, staged by the prologue (tiles that write whole outputs)
+    __shared__ float bias_lds[kSeqBiasBlocks * kCols];
     __shared__ uint32_t sh_epoch;
     __shared__ int sh_bad;
 
@@ -241,8 +263,9 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
     const int te = ld_const(a.task_begin + wg + 1);
     const int first = ld_const(a.first_tile + wg);
 
-    // groups of a tile's segment per wave (the waves split the segment into contiguous parts)
-    auto per_wave = [](int gseg) { return (gseg + kWaves - 1) / kWaves; };
+    // the waves split a tile's segment into contiguous parts of floor or ceil(gseg / W) groups:
+    // wave w takes local groups [w*gseg/W, (w+1)*gseg/W), so every wave has loads in flight
+    auto wave_lo = [&](int gseg) { return wave * gseg / W; };
     auto src_of = [&](int ti) {
         // uniform index: the table reads become scalar loads, which the weight prefetch does
         // not have to drain before the fields are used
@@ -253,52 +276,101 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
         f.qzeros = uniform_ptr(ld_const(&L->qzeros));
         f.scales = uniform_ptr(ld_const(&L->scales));
         f.N = __builtin_amdgcn_readfirstlane(ld_const(&L->N));
-        const int q = per_wave(t.g1 - t.g0);
-        const int g0 = t.g0 + wave * q;
-        const int g1 = min(t.g1, g0 + q);
-        f.g0 = g1 > g0 ? g0 : t.g0;
-        f.glast = g1 > g0 ? g1 - 1 : t.g0;
-        f.blk = t.ct;
+        f.g0 = t.g0 + wave_lo(t.g1 - t.g0);
+        f.wcount = t.g0 + (wave + 1) * (t.g1 - t.g0) / W - f.g0;
+        f.ct = t.ct;
+        f.nblk = t.nblk;
         return f;
     };
 
-    // software pipeline over the workgroup's blocks: slot d holds job (i + d) of the current
-    // block; refills run past the block's end into the next block (or the next tile's first
-    // block). Loads are unconditional (clamped to the wave's groups), so the compiler waits for
-    // exactly the slot it consumes. Base pointers sit in scalar registers and offsets stay
-    // 32-bit (every GPTQ tensor is far below 4 GiB).
+    // Software pipeline over each wave's job stream. In a tile, the wave's job k is block
+    // k / wcount, group g0 + k % wcount (blocks in order); the stream is padded to a multiple of
+    // kP (at least kP) and continues into the next tile, so slot d always holds a job k with
+    // k % kP == d and the loads stay kP jobs ahead across blocks and tiles. Padding loads
+    // re-read the tile's first job (cached) and are never consumed. Loads are unconditional, so
+    // the compiler waits for exactly the slot it consumes. Base pointers sit in scalar registers
+    // and offsets stay 32-bit (every GPTQ tensor is far below 4 GiB).
     uint4 wb[kP][2 * NB];
     uint32_t zb[kP];
     uint2 sb[kP];
-    auto fetch = [&](int d, const FetchSrc& f, int job) {
-        // the bases are uniform; saying so here keeps them in scalar registers however the
-        // source was selected (a base in vector registers costs 64-bit address math per load and
-        // makes the compiler drain the loads in flight)
-        const uint32_t* qw = uniform_ptr(f.qweight);
-        const uint32_t* qz = uniform_ptr(f.qzeros);   // never null
-        const uint16_t* sc = uniform_ptr(f.scales);
-        const int Ns = __builtin_amdgcn_readfirstlane(f.N);
-        const uint32_t N = (uint32_t)Ns;
-        const int g = __builtin_amdgcn_readfirstlane(min(f.g0 + job, f.glast));
-        const int nc = __builtin_amdgcn_readfirstlane(f.blk) * kCols + 4 * j;
-        const uint32_t n = (uint32_t)(nc < Ns ? nc : Ns - 4);
-        // byte offsets in 32 bits: scalar base + 32-bit vector offset is one load instruction
-        const uint32_t row0 = ((uint32_t)(g * NB * 8 + 2 * kq) * N + n) * 4u;
+    // One wave's fetch cursor over a tile's jobs: scalar bases and byte offsets of the cursor's
+    // group (one add per job), lane offsets of the cursor's block (recomputed per block; a
+    // partial last block clamps its columns to the linear's last four). Past the tile's last job
+    // the cursor stays there, so padding loads re-read cached data.
+    struct Stream {
+        const char* qw;
+        const char* qz;
+        const char* sc;
+        uint32_t gq, gz, gs;               // byte offsets of the cursor's group
+        uint32_t Gq, Gz, Gs;               // byte strides from one group to the next
+        int b, gi, wcount, nblk, ct, N;
+        uint32_t lq[2 * NB], lz, ls;       // lane offsets of the cursor's block
+    };
+    auto set_lanes = [&](Stream& st) {
+        const int nc = (st.ct + st.b) * kCols + 4 * j;
+        const uint32_t n = (uint32_t)(nc < st.N ? nc : st.N - 4);
 #pragma unroll
         for (int r = 0; r < 2 * NB; r++)
-            wb[d][r] = __builtin_bit_cast(uint4, ld_global(reinterpret_cast<const u32x4*>(
-                reinterpret_cast<const char*>(qw) + (row0 + (uint32_t)((r >> 1) * 8 + (r & 1)) * N * 4u))));
-        zb[d] = ld_global(reinterpret_cast<const uint32_t*>(
-            reinterpret_cast<const char*>(qz) + ((uint32_t)g * ((N + 7) >> 3) + (n >> 3)) * 4u));
-        sb[d] = __builtin_bit_cast(uint2, ld_global(reinterpret_cast<const u32x2*>(
-            reinterpret_cast<const char*>(sc) + ((uint32_t)g * N + n) * 2u)));
+            st.lq[r] = ((uint32_t)(2 * kq + (r >> 1) * 8 + (r & 1)) * (uint32_t)st.N + n) * 4u;
+        st.ls = n * 2u;
+        st.lz = (n >> 3) * 4u;
+    };
+    auto open_stream = [&](const FetchSrc& f) {
+        Stream st;
+        st.qw = reinterpret_cast<const char*>(uniform_ptr(f.qweight));
+        st.qz = reinterpret_cast<const char*>(uniform_ptr(f.qzeros));   // never null
+        st.sc = reinterpret_cast<const char*>(uniform_ptr(f.scales));
+        st.N = __builtin_amdgcn_readfirstlane(f.N);
+        st.ct = __builtin_amdgcn_readfirstlane(f.ct);
+        st.nblk = __builtin_amdgcn_readfirstlane(f.nblk);
+        st.wcount = __builtin_amdgcn_readfirstlane(f.wcount);
+        const uint32_t g0 = (uint32_t)__builtin_amdgcn_readfirstlane(f.g0);
+        st.Gq = (uint32_t)(NB * 8) * (uint32_t)st.N * 4u;
+        st.Gs = (uint32_t)st.N * 2u;
+        st.Gz = (((uint32_t)st.N + 7u) >> 3) * 4u;
+        st.gq = g0 * st.Gq;
+        st.gs = g0 * st.Gs;
+        st.gz = g0 * st.Gz;
+        st.b = 0;
+        st.gi = 0;
+        set_lanes(st);
+        return st;
+    };
+    auto advance = [&](Stream& st) {
+        if (st.gi + 1 < st.wcount) {
+            st.gi++;
+            st.gq += st.Gq;
+            st.gs += st.Gs;
+            st.gz += st.Gz;
+        } else if (st.wcount > 0 && st.b + 1 < st.nblk) {
+            // back to the wave's first group, one block on
+            const uint32_t back = (uint32_t)(st.wcount - 1);
+            st.gi = 0;
+            st.gq -= back * st.Gq;
+            st.gs -= back * st.Gs;
+            st.gz -= back * st.Gz;
+            st.b++;
+            set_lanes(st);
+        }
+    };
+    auto fetch = [&](int d, const Stream& st) {
+        // scalar base + 32-bit lane offset: one load instruction each
+        const char* q = st.qw + st.gq;
+#pragma unroll
+        for (int r = 0; r < 2 * NB; r++)
+            wb[d][r] = __builtin_bit_cast(uint4, ld_global(reinterpret_cast<const u32x4*>(q + st.lq[r])));
+        zb[d] = ld_global(reinterpret_cast<const uint32_t*>(st.qz + st.gz + st.lz));
+        sb[d] = __builtin_bit_cast(uint2, ld_global(reinterpret_cast<const u32x2*>(st.sc + st.gs + st.ls)));
     };
 
-    FetchSrc cur{};
+    // the first tile's first kP stream positions
     if (first >= 0) {
-        cur = src_of(first);
+        Stream st = open_stream(src_of(first));
 #pragma unroll
-        for (int d = 0; d < kP; d++) fetch(d, cur, d);
+        for (int d = 0; d < kP; d++) {
+            fetch(d, st);
+            advance(st);
+        }
     }
 
     if (threadIdx.x == 0) {
@@ -309,9 +381,13 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
         sh_epoch = (uint32_t)(old / members) + 1u;
         sh_bad = 0;
     }
+    if (threadIdx.x < RG) {
+        ring_arrive[threadIdx.x] = 0;
+        ring_done[threadIdx.x] = (int)threadIdx.x - RG;   // as if blocks -RG .. -1 were done
+    }
     __syncthreads();
     const uint32_t e = __builtin_amdgcn_readfirstlane(sh_epoch);   // uniform: scalar control flow
-    int rbuf = 0;                                                 // reduction buffer in use
+    int bseq = 0;              // this workgroup's blocks so far (ring position), across tiles
 
     for (int ti = tb; ti < te; ti++) {
         const SeqTask task = ld_const(a.tasks + ti);
@@ -320,21 +396,36 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
         bool ok = true;
 
         if (task.kind == kSeqReduce) {
-            // split-K partial sums of one 64-column block, added in ascending segment order
-            const size_t stride = (size_t)M * N;
-            if (wave == 0)
-                ok = wait_words(L.part_ll + (size_t)task.ct * kCols, stride, L.S, lane, e, a);
+            // blocks ct .. ct+nblk-1: each the sum of its parts (consecutive pool slots, ascending
+            // K order), plus bias. Wave 0 first waits for one word of every slot.
+            const int np = task.parts;
+            const size_t slot_words = (size_t)M * kCols;
+            if (wave == 0) {
+                for (int l = lane; l < task.nblk * np && ok; l += 64) {
+                    const int b = l / np;
+                    const uint64_t* w0 = a.part + (size_t)(task.slot + b * task.stride + (l - b * np)) * slot_words;
+                    uint32_t polls = 0;
+                    while ((uint32_t)(ld_ll(w0) >> 32) != e)
+                        if (!keep_waiting(a, polls)) {
+                            ok = false;
+                            break;
+                        }
+                }
+            }
             if (!ok) sh_bad = 1;
             __syncthreads();
             if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
-            for (int idx = threadIdx.x; idx < M * kCols; idx += 256) {
-                const int m = idx / kCols;
-                const int nn = task.ct * kCols + (idx - m * kCols);
+            for (int idx = threadIdx.x; idx < task.nblk * M * kCols; idx += kThreads) {
+                const int b = idx / (M * kCols);
+                const int r = idx - b * (M * kCols);
+                const int m = r / kCols;
+                const int nn = (task.ct + b) * kCols + (r - m * kCols);
                 if (nn >= N || !ok) continue;
+                const uint64_t* src = a.part + (size_t)(task.slot + b * task.stride) * slot_words + r;
                 float sum = 0.f;
-                for (int s0 = 0; s0 < L.S && ok; s0 += kSumBatch)
-                    ok = sum_ll<kSumBatch>(L.part_ll + (size_t)(s0 * M + m) * N + nn, stride,
-                                           min(kSumBatch, L.S - s0), e, a, &sum);
+                for (int s0 = 0; s0 < np && ok; s0 += kSumBatch)
+                    ok = sum_ll<kSumBatch>(src + (size_t)s0 * slot_words, slot_words, min(kSumBatch, np - s0),
+                                           e, a, &sum);
                 if (!ok) continue;
                 if (L.bias) sum += ld_global(L.bias + nn);
                 st_global(L.y + (size_t)m * N + nn, sum);
@@ -348,13 +439,14 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
 
         // ---- GEMV tile: blocks ct .. ct + nblk - 1 (64 columns each) over the segment [g0, g1) ----
         const int gseg = task.g1 - task.g0;
-        const int q = per_wave(gseg);
-        const int jpw = (q + kP - 1) / kP * kP;
-        const int wcount = max(0, min(q, gseg - wave * q));   // this wave's groups
+        const int wfirst = wave_lo(gseg);                        // this wave's first group
+        const int wcount = (wave + 1) * gseg / W - wfirst;       // and its number of groups
         const bool P = L.src >= 0;
         const uint64_t* p_ll = P ? ld_const(&a.lin[L.src].y_ll) : nullptr;
-        // the next tile's source, read now so that its table loads overlap the prologue
-        const FetchSrc next_tile = task.next_tile >= 0 ? src_of(task.next_tile) : cur;
+        // this tile's and the next tile's views, read now so that their table loads overlap the
+        // prologue (without a next tile the stream's tail re-reads this tile)
+        const FetchSrc cs = src_of(ti);
+        const FetchSrc ns = task.next_tile >= 0 ? src_of(task.next_tile) : cs;
 
         // the segment's activation digits (shared by all blocks of the tile), from the external
         // input or from the producer's output words: wave 0 first waits for one word of each
@@ -372,17 +464,22 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
         uint4* xd = dyn_lds;
         float2* gst = reinterpret_cast<float2*>(dyn_lds + gseg * NB * 4 * R);
         {
+            if (task.slot < 0 && L.bias)
+                for (int idx = threadIdx.x; idx < task.nblk * kCols; idx += kThreads) {
+                    const int col = task.ct * kCols + idx;
+                    bias_lds[idx] = col < N ? ld_global(L.bias + col) : 0.f;
+                }
             // QL_SEQ_PRO_CHUNKS chunks per trip: their input loads are all issued before any is used
             const int items = gseg * M;
             constexpr int H = QL_SEQ_PRO_CHUNKS;
-            for (int base = 0; base < items * CPG; base += 256 * H) {
+            for (int base = 0; base < items * CPG; base += kThreads * H) {
                 uint64_t w[H][8];
                 float v[H][8];
                 size_t xo[H];
                 bool live[H];
 #pragma unroll
                 for (int h = 0; h < H; h++) {
-                    const int idx = base + 256 * h + threadIdx.x;
+                    const int idx = base + kThreads * h + threadIdx.x;
                     const int item = idx / CPG;
                     live[h] = item < items;
                     const int c = idx - item * CPG;
@@ -396,7 +493,7 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
                 }
 #pragma unroll
                 for (int h = 0; h < H; h++) {
-                    const int idx = base + 256 * h + threadIdx.x;
+                    const int idx = base + kThreads * h + threadIdx.x;
                     const int item = idx / CPG;                 // uniform per CPG lanes
                     if (!live[h]) continue;
                     const int c = idx - item * CPG;
@@ -421,30 +518,11 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
         __syncthreads();
         if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
 
-        for (int b = 0; b < task.nblk; b++) {
-            const int blk = task.ct + b;
-            FetchSrc nxt = next_tile;
-            if (b + 1 < task.nblk) {
-                nxt = cur;
-                nxt.blk = blk + 1;
-            }
-            const int n = blk * kCols + 4 * j;
-            const bool col_ok = n < N;
-            // this thread's bias values for the block's output stores, loaded ahead of the
-            // weight prefetch so the stores do not wait for the prefetch to land
-            float bias_v[T];
+        float acc[4][T];
 #pragma unroll
-            for (int k = 0; k < T; k++) {
-                const int idx = threadIdx.x + 256 * k;
-                const int nn = blk * kCols + (idx - idx / kCols * kCols);
-                bias_v[k] = (L.S == 1 && L.bias) ? ld_global(L.bias + (nn < N ? nn : 0)) : 0.f;
-            }
-            float acc[4][T];
+        for (int u = 0; u < 4; u++)
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-#pragma unroll
-                for (int t = 0; t < T; t++) acc[u][t] = 0.f;
-
+            for (int t = 0; t < T; t++) acc[u][t] = 0.f;
             auto consume = [&](int gg, const uint4* w, uint32_t zn, uint2 sv) {
                 i32x4 c[4][T];
 #pragma unroll
@@ -471,7 +549,7 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
                         for (int t = 0; t < T; t++) c[u][t] = mfma_i8(av[t], bq, c[u][t]);
                     }
                 }
-                const uint32_t zw = zn >> (4 * (n & 7));
+                const uint32_t zw = zn >> (4 * ((4 * j) & 7));
                 const uint32_t sw[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
                 float2 st[T];
 #pragma unroll
@@ -494,68 +572,127 @@ __global__ __launch_bounds__(256) void seq_kernel(const SeqArgs a)
                 }
             };
 
-            // slot d is consumed before it is refilled: the refill then lands in the same
-            // registers, so the compiler waits only for the slot it is about to use (no register
-            // rotation at the back-edge, which would drain every load in flight). Every iteration
-            // but the last refills from this block; the last one starts the next block.
-            auto step = [&](int i, const FetchSrc& f, int job0) {
-#pragma unroll
-                for (int d = 0; d < kP; d++) {
-                    const uint2 sv = col_ok ? sb[d] : uint2{0u, 0u};
-                    if (i + d < wcount) consume(wave * q + i + d, wb[d], zb[d], sv);
-                    fetch(d, f, job0 + d);
-                }
-            };
-            int i = 0;
-            for (; i + kP < jpw; i += kP) step(i, cur, i + kP);
-            step(i, nxt, 0);
-            cur = nxt;
-
-            // the four waves' sums of each (row, column), added in wave order
-            if (RB == 1) __syncthreads();          // the previous block's readers are done
+        // Publishes this wave's sums of block b; the last wave to arrive adds the W sums in wave
+        // order and stores the block (lane = column, rows m).
+        auto publish = [&](int b) {
+            const int rs = bseq % RG;
+            {
+                // the slot is free once the block a full ring back has been stored
+                uint32_t polls = 0;
+                while (__hip_atomic_load(&ring_done[rs], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < bseq - RG)
+                    if (!keep_waiting(a, polls)) {
+                        ok = false;
+                        break;
+                    }
+            }
 #pragma unroll
             for (int t = 0; t < T; t++)
 #pragma unroll
-                for (int u = 0; u < 4; u++) red[rbuf][wave][4 * t + kq][4 * j + u] = acc[u][t];
-            __syncthreads();
+                for (int u = 0; u < 4; u++) red[rs][wave][4 * t + kq][4 * j + u] = acc[u][t];
+            // LDS executes a wave's operations in order: the sums land before the arrival is
+            // counted (the fence only keeps the compiler from reordering them)
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            int arrived = 0;
+            if (lane == 0)
+                arrived = __hip_atomic_fetch_add(&ring_arrive[rs], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            arrived = __builtin_amdgcn_readfirstlane(arrived);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (arrived == W - 1) {
+                const int ncol = (task.ct + b) * kCols + lane;
+                for (int m = 0; m < M; m++) {
+                    if (ncol < N) {
+                        float v = red[rs][0][m][lane];
 #pragma unroll
-            for (int k = 0; k < T; k++) {
-                const int idx = threadIdx.x + 256 * k;
-                const int m = idx / kCols;                  // < 4T: inside `red`
-                const int col = idx - m * kCols;
-                const int nn = blk * kCols + col;
-                if (m < M && nn < N) {
-                    float v = ((red[rbuf][0][m][col] + red[rbuf][1][m][col]) + red[rbuf][2][m][col]) +
-                              red[rbuf][3][m][col];
-                    if (L.S == 1) {
-                        v += bias_v[k];
-                        st_global(L.y + (size_t)m * N + nn, v);
-                        st_ll(L.y_ll + (size_t)m * N + nn, v, e);
-                    } else {
-                        st_ll(L.part_ll + ((size_t)task.seg * M + m) * N + nn, v, e);
+                        for (int w = 1; w < W; w++) v += red[rs][w][m][lane];
+                        if (task.slot < 0) {
+                            if (L.bias) v += bias_lds[b * kCols + lane];
+                            st_global(L.y + (size_t)m * N + ncol, v);
+                            st_ll(L.y_ll + (size_t)m * N + ncol, v, e);
+                        } else {
+                            st_ll(a.part + ((size_t)(task.slot + b * task.stride) * M + m) * kCols + lane, v, e);
+                        }
                     }
                 }
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                if (lane == 0) {
+                    ring_arrive[rs] = 0;
+                    __hip_atomic_store(&ring_done[rs], bseq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
             }
-            rbuf = (rbuf + 1) % RB;
+            bseq++;
+        };
+
+        // the wave's job stream over the tile (see the pipeline note above): positions 0..kP-1 are
+        // in flight; the last iteration refills from the next tile
+        const int njobs = task.nblk * wcount;
+        const int njobs_p = njobs > kP ? (njobs + kP - 1) / kP * kP : kP;
+        Stream fs = open_stream(cs);
+#pragma unroll
+        for (int d = 0; d < kP; d++) advance(fs);
+        int cb = 0, cg = 0;                // block and group of the next job consumed
+        auto consume_job = [&](int d) {
+            consume(wfirst + cg, wb[d], zb[d], sb[d]);
+            if (++cg == wcount) {
+                publish(cb);
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int t = 0; t < T; t++) acc[u][t] = 0.f;
+                cg = 0;
+                cb++;
+            }
+        };
+        int k = 0;
+        for (; k + kP < njobs_p; k += kP) {
+#pragma unroll
+            for (int d = 0; d < kP; d++) {
+                if (k + d < njobs) consume_job(d);
+                fetch(d, fs);
+                advance(fs);
+            }
         }
+        {
+            Stream nx = open_stream(ns);
+#pragma unroll
+            for (int d = 0; d < kP; d++) {
+                if (k + d < njobs) consume_job(d);
+                fetch(d, nx);
+                advance(nx);
+            }
+        }
+        // a wave without groups in this tile still counts itself in for every block
+        if (wcount == 0)
+            for (int b = 0; b < task.nblk; b++) publish(b);
+        if (!ok) sh_bad = 1;
         // the next tile's prologue rewrites the digits
         __syncthreads();
     }
 }
 
+struct SeqKernel {
+    const void* fn;
+    int threads;
+};
+
+// Eight waves per workgroup (one workgroup per CU) where two waves per SIMD fit the registers:
+// a single workgroup keeps its waves in step through the per-block barriers, where two
+// co-resident workgroups drift apart (the older one's waves win issue). Otherwise four waves.
 template <int T>
-const void* kernel_for(int nb)
+SeqKernel kernel_for(int nb)
 {
-    constexpr int RB = T == 4 ? 1 : 2;      // M > 8: one reduction buffer keeps LDS for 2 WGs/CU
+    constexpr int RG = T == 1 ? 4 : 2;      // reduction ring slots (32 KB of LDS with 8 waves)
+    // deeper prefetch for M > 8 except with 256-wide groups (it would spill registers)
+    constexpr int P = T == 4 ? QL_SEQ_PREFETCH_WIDE : QL_SEQ_PREFETCH;
+    constexpr int W = T <= 2 ? QL_SEQ_WAVES : 4;
     switch (nb) {
-    case 1: return reinterpret_cast<const void*>(&seq_kernel<T, 1, RB>);
-    case 2: return reinterpret_cast<const void*>(&seq_kernel<T, 2, RB>);
-    case 4: return reinterpret_cast<const void*>(&seq_kernel<T, 4, RB>);
-    default: return nullptr;
+    case 1: return {reinterpret_cast<const void*>(&seq_kernel<T, 1, RG, P, W>), 64 * W};
+    case 2: return {reinterpret_cast<const void*>(&seq_kernel<T, 2, RG, P, W>), 64 * W};
+    case 4: return {reinterpret_cast<const void*>(&seq_kernel<T, 4, RG, QL_SEQ_PREFETCH, 4>), 256};
+    default: return {nullptr, 0};
     }
 }
 
-const void* seq_kernel_for(int M, int group)
+SeqKernel seq_kernel_for(int M, int group)
 {
     const int nb = group / 64;
     if (M <= 4) return kernel_for<1>(nb);
@@ -565,21 +702,82 @@ const void* seq_kernel_for(int M, int group)
 
 }  // namespace
 
-size_t seq_lds_budget() { return kLdsBudget; }
+size_t seq_lds_budget(int M, int group) { return lds_budget(M, group); }
 
-// K segments of one linear for a pass whose share is `units` 64-column blocks
-static int split_for(const SeqSpec& s, int M, double units)
+// Most groups one tile may cover: its activation digits fit the LDS budget and, in a latency-bound
+// pass, its prologue stays within 4 input chunks per lane (one round of loads).
+static int max_tile_groups(const SeqSpec& s, int M, bool latency)
+{
+    const int max_g = std::max<int>(1, (int)(lds_budget(M, s.group) / lds_per_group(M, s.group)));
+    const int max_p = std::max(1, 4 * seq_kernel_for(M, s.group).threads / (M * (s.group / 64) * 8));
+#ifdef QL_SEQ_MAX_TILE_GROUPS
+    return std::min(QL_SEQ_MAX_TILE_GROUPS, latency ? std::min(max_g, max_p) : max_g);
+#else
+    return latency ? std::min(max_g, max_p) : max_g;
+#endif
+}
+
+// K segments of a linear in a latency-bound pass: about `units` (block, segment) items for the
+// whole linear, at least kMinGroups groups each, within the tile limit.
+static int latency_split(const SeqSpec& s, int M, double units)
 {
     const int ct = (s.N + kCols - 1) / kCols;
     const int groups = s.K / s.group;
     int S = (int)(units / ct + 0.5);
     S = std::min(S, std::max(1, groups / kMinGroups));
-    // the segment's digits fit the LDS budget, and the prologue stays within 4 chunks per lane
-    const int max_g = std::max<int>(1, (int)(kLdsBudget / lds_per_group(M, s.group)));
-    const int max_p = std::max(1, 4 * 256 / (M * (s.group / 64) * 8));
-    S = std::max({S, 1, (groups + max_g - 1) / max_g, (groups + max_p - 1) / max_p});
+    const int mg = max_tile_groups(s, M, true);
+    S = std::max({S, 1, (groups + mg - 1) / mg});
     return std::min({S, groups, kSeqMaxSplit});
 }
+
+namespace {
+
+// Groups [g0, g1) of column block c of linear `lin`.
+struct Piece {
+    int lin, c, g0, g1;
+};
+
+// Deals a pass's items to `runs` workgroups (run w -> workgroup (cursor + w) % grid) so that
+// every run carries the same number of block-groups to within one group. With `split`, an item
+// that straddles a run boundary is cut at the group nearest to it. Without, items stay whole:
+// one per run when they are no more than the runs, else each goes to the run holding its
+// midpoint.
+void cut_runs(const std::vector<Piece>& items, int runs, bool split, std::vector<std::vector<Piece>>* out)
+{
+    out->assign(runs, {});
+    if (!split && items.size() <= (size_t)runs) {
+        for (size_t k = 0; k < items.size(); k++) (*out)[k].push_back(items[k]);
+        return;
+    }
+    uint64_t total = 0;
+    for (const Piece& it : items) total += (uint64_t)(it.g1 - it.g0);
+    if (total == 0 || runs == 0) return;
+    // boundary of run w: total * (w + 1) / runs, in exact integer arithmetic
+    auto bound = [&](int w) { return (total * (uint64_t)(w + 1) + runs / 2) / (uint64_t)runs; };
+    uint64_t acc = 0;
+    int w = 0;
+    for (const Piece& it : items) {
+        const uint64_t len = (uint64_t)(it.g1 - it.g0);
+        if (!split) {
+            const uint64_t mid2 = 2 * acc + len;          // twice the item's midpoint
+            while (w + 1 < runs && mid2 > 2 * bound(w)) w++;
+            (*out)[w].push_back(it);
+            acc += len;
+            continue;
+        }
+        int g = it.g0;
+        while (g < it.g1) {
+            while (w + 1 < runs && acc >= bound(w)) w++;
+            const uint64_t room = w + 1 < runs ? bound(w) - acc : UINT64_MAX;
+            const int take = (int)std::min<uint64_t>(room, (uint64_t)(it.g1 - g));
+            (*out)[w].push_back(Piece{it.lin, it.c, g, g + take});
+            g += take;
+            acc += (uint64_t)take;
+        }
+    }
+}
+
+}  // namespace
 
 void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
 {
@@ -588,7 +786,6 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
     p.grid = grid;
     const int n = (int)lin.size();
     p.pass_of.assign(n, 0);
-    p.split.assign(n, 1);
     for (int i = 0; i < n; i++) {
         p.pass_of[i] = lin[i].src >= 0 ? p.pass_of[lin[i].src] + 1 : 0;
         p.passes = std::max(p.passes, p.pass_of[i] + 1);
@@ -603,79 +800,238 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
                 ids.push_back(i);
                 bytes += lin[i].weight_bytes;
             }
-        // Splits: a pass whose weights are small per workgroup is latency-bound and gets about one
-        // block per workgroup; a streaming pass gets the smallest multiple k of the grid whose
-        // blocks divide evenly enough (the busiest workgroup carries at most ~15% above average).
+        // A pass whose weights are small per workgroup is latency-bound: about one (block,
+        // K segment) item per workgroup. A streaming pass is cut into equal runs of block-groups
+        // on every workgroup; blocks are split along K only where the LDS limit forces it or a
+        // run boundary falls inside them. A linear with forced segments is walked in chunks of
+        // blocks, all segments of a chunk before the next, so a block's parts mostly share a run.
         const bool streaming = bytes / (uint64_t)grid >= kStreamBytes;
-        std::vector<int> best;
-        double best_bal = -1.0;
-        for (int k = 1; k <= (streaming ? 8 : 1); k++) {
-            std::vector<int> S(ids.size());
-            uint64_t U = 0;
-            for (size_t x = 0; x < ids.size(); x++) {
-                const SeqSpec& s = lin[ids[x]];
-                S[x] = split_for(s, M, (double)k * grid * s.weight_bytes / std::max<uint64_t>(1, bytes));
-                U += (uint64_t)((s.N + kCols - 1) / kCols) * S[x];
+        // Items of a set of linears: (linear, block, K segment) in linear order; a linear with
+        // forced segments is walked in chunks of blocks (about one run's worth), all segments of
+        // a chunk before the next, so a block's parts mostly share a run.
+        auto build_items = [&](const std::vector<int>& set, double budget, std::vector<Piece>* items) {
+            for (int i : set) {
+                const SeqSpec& s = lin[i];
+                const int ct = (s.N + kCols - 1) / kCols;
+                const int groups = s.K / s.group;
+                const int mgs = max_tile_groups(s, M, false);
+                const int S = streaming ? std::min((groups + mgs - 1) / mgs, groups)
+                                        : latency_split(s, M, (double)grid * s.weight_bytes / std::max<uint64_t>(1, bytes));
+                auto seg = [&](int k, int* g0, int* g1) {
+                    *g0 = (int)((int64_t)groups * k / S);
+                    *g1 = (int)((int64_t)groups * (k + 1) / S);
+                };
+                int g0, g1;
+                if (!streaming) {
+                    for (int k = 0; k < S; k++) {
+                        seg(k, &g0, &g1);
+                        for (int c = 0; c < ct; c++) items->push_back(Piece{i, c, g0, g1});
+                    }
+                } else {
+                    const int chunk = S == 1 ? ct : std::max(1, (int)(budget / groups));
+                    for (int c0 = 0; c0 < ct; c0 += chunk)
+                        for (int k = 0; k < S; k++) {
+                            seg(k, &g0, &g1);
+                            for (int c = c0; c < std::min(ct, c0 + chunk); c++) items->push_back(Piece{i, c, g0, g1});
+                        }
+                }
             }
-            const double per = (double)U / grid;
-            const double bal = per >= 1.0 ? per / std::ceil(per) : 1.0;
-            if (bal > best_bal + 1e-9) {
-                best_bal = bal;
-                best = S;
+        };
+        auto units_of = [&](int i) { return (uint64_t)((lin[i].N + kCols - 1) / kCols) * (lin[i].K / lin[i].group); };
+        std::vector<std::vector<Piece>> run_pieces;
+        int runs = grid;
+        if (!streaming) {
+            std::vector<Piece> items;
+            build_items(ids, 0.0, &items);
+            runs = (int)std::min<size_t>(items.size(), (size_t)grid);
+            cut_runs(items, runs, false, &run_pieces);
+        } else {
+            // Shape classes (K, N): every workgroup gets an equal share of each class, so every
+            // workgroup carries the same mix of shapes. Shapes stream at different rates when
+            // they share the memory system, and equal mixes finish together. Classes below 16
+            // block-groups per workgroup are cut together.
+            std::vector<std::pair<std::pair<int, int>, std::vector<int>>> classes;
+            std::vector<int> small;
+            for (int i : ids) {
+                const std::pair<int, int> key{lin[i].K, lin[i].N};
+                size_t c = 0;
+                while (c < classes.size() && classes[c].first != key) c++;
+                if (c == classes.size()) classes.push_back({key, {}});
+                classes[c].second.push_back(i);
             }
-            if (bal >= 0.85) break;
+            std::vector<std::vector<int>> sets;
+            for (auto& c : classes) {
+                uint64_t u = 0;
+                for (int i : c.second) u += units_of(i);
+                if (QL_SEQ_CLASS_CUT && u >= 16 * (uint64_t)grid) sets.push_back(c.second);
+                else small.insert(small.end(), c.second.begin(), c.second.end());
+            }
+            if (!small.empty()) {
+                std::sort(small.begin(), small.end());
+                sets.push_back(small);
+            }
+            run_pieces.assign(grid, {});
+            std::vector<std::vector<std::vector<Piece>>> per_set(sets.size());
+            for (size_t c = 0; c < sets.size(); c++) {
+                uint64_t u = 0;
+                for (int i : sets[c]) u += units_of(i);
+                std::vector<Piece> items;
+                build_items(sets[c], (double)u / grid, &items);
+                cut_runs(items, grid, true, &per_set[c]);
+            }
+            // each run takes the sets in a rotated order, so the chip-wide mix stays even in time
+            for (int r = 0; r < grid; r++)
+                for (size_t c = 0; c < sets.size(); c++) {
+                    const auto& v = per_set[(c + r) % sets.size()][r];
+                    run_pieces[r].insert(run_pieces[r].end(), v.begin(), v.end());
+                }
         }
-        // rows of blocks: (linear, segment) in order; cut into `grid` nearly equal runs
-        struct Row { int lin, seg, g0, g1, blocks; };
-        std::vector<Row> rows;
-        uint64_t U = 0;
-        for (size_t x = 0; x < ids.size(); x++) {
-            const int i = ids[x];
-            const SeqSpec& s = lin[i];
-            const int S = best[x];
-            const int groups = s.K / s.group;
-            const int ct = (s.N + kCols - 1) / kCols;
-            p.split[i] = S;
-            p.max_split = std::max(p.max_split, S);
-            for (int seg = 0; seg < S; seg++) {
-                const int g0 = (int)((int64_t)groups * seg / S);
-                const int g1 = (int)((int64_t)groups * (seg + 1) / S);
-                p.max_gseg = std::max(p.max_gseg, g1 - g0);
-                rows.push_back(Row{i, seg, g0, g1, ct});
-                U += ct;
+
+        // parts of each block, in ascending K order; slots for blocks of more than one part
+        std::vector<std::vector<std::vector<Piece>>> parts(n);   // [linear][block] -> pieces
+        for (int i : ids) parts[i].assign((lin[i].N + kCols - 1) / kCols, {});
+        for (const auto& r : run_pieces)
+            for (const Piece& q : r) parts[q.lin][q.c].push_back(q);
+        std::vector<std::vector<int64_t>> base(n);
+        for (int i : ids) {
+            base[i].assign(parts[i].size(), -1);
+            for (size_t c = 0; c < parts[i].size(); c++) {
+                auto& v = parts[i][c];
+                std::sort(v.begin(), v.end(), [](const Piece& a, const Piece& b) { return a.g0 < b.g0; });
+                p.max_split = std::max(p.max_split, (int)v.size());
+                if (v.size() > 1) {
+                    base[i][c] = (int64_t)p.slots;
+                    p.slots += v.size();
+                }
             }
         }
-        const int runs = (int)std::min<uint64_t>(U, (uint64_t)grid);
-        size_t r = 0;
-        uint64_t row_start = 0;
-        for (int w = 0; w < runs; w++) {
-            uint64_t lo = U * w / runs, hi = U * (w + 1) / runs;
-            const int dst = (cursor + w) % grid;
-            while (lo < hi) {
-                while (row_start + rows[r].blocks <= lo) row_start += rows[r++].blocks;
-                const Row& row = rows[r];
-                const uint64_t end = std::min<uint64_t>(hi, row_start + row.blocks);
-                per_wg[dst].push_back(SeqTask{row.lin, kSeqTile, (int)(lo - row_start), row.seg,
-                                              row.g0, row.g1, -1, (int)(end - lo)});
+        auto slot_of = [&](const Piece& q) -> int64_t {
+            const int64_t b = base[q.lin][q.c];
+            if (b < 0) return -1;
+            const auto& v = parts[q.lin][q.c];
+            for (size_t r = 0; r < v.size(); r++)
+                if (v[r].g0 == q.g0) return b + (int64_t)r;
+            return -1;
+        };
+
+        // tiles: consecutive pieces of a run merged while they continue the same columns and
+        // K range and their slots advance by a fixed stride. A split block is reduced by the run
+        // that computes its last part (the latest in that run): right after that tile when all of
+        // the block's parts are in this run (no wait on another workgroup), otherwise after all of
+        // the run's tiles of the pass.
+        struct Host { int run; uint64_t pos; bool local; };
+        std::vector<std::vector<Host>> host(n);
+        std::vector<std::vector<int>> owner(n);      // run of the block's parts, -2 when several
+        for (int i : ids) {
+            host[i].assign(parts[i].size(), Host{-1, 0, false});
+            owner[i].assign(parts[i].size(), -1);
+        }
+        for (int r = 0; r < runs; r++)
+            for (const Piece& q : run_pieces[r]) {
+                int& o = owner[q.lin][q.c];
+                o = (o == -1 || o == r) ? r : -2;
+            }
+        std::vector<std::vector<std::pair<size_t, int>>> after(runs);   // (tile end index, block)
+        for (int r = 0; r < runs; r++) {
+            const auto& v = run_pieces[r];
+            uint64_t pos = 0;                 // block-groups of the run up to the current tile's end
+            for (size_t k = 0; k < v.size();) {
+                const Piece& a = v[k];
+                const int64_t s0 = slot_of(a);
+                int64_t stride = 0;
+                size_t e = k + 1;
+                while (e < v.size()) {
+                    const Piece& b = v[e];
+                    if (b.lin != a.lin || b.c != a.c + (int)(e - k) || b.g0 != a.g0 || b.g1 != a.g1) break;
+                    const int64_t sb = slot_of(b);
+                    if ((s0 < 0) != (sb < 0)) break;
+                    if (s0 >= 0) {
+                        const int64_t d = sb - slot_of(v[e - 1]);
+                        if (e == k + 1) stride = d;
+                        else if (d != stride) break;
+                    }
+                    e++;
+                }
+                pos += (uint64_t)(e - k) * (uint64_t)(a.g1 - a.g0);
+                for (size_t x = k; x < e; x++) {
+                    const Piece& q = v[x];
+                    if (base[q.lin][q.c] < 0) continue;
+                    Host& h = host[q.lin][q.c];
+                    if (h.run < 0 || pos >= h.pos) h = Host{r, pos, owner[q.lin][q.c] == r};
+                }
+                k = e;
+            }
+        }
+        // emit: tiles in run order with local reductions after the tile that completes them, then
+        // the run's remaining reductions
+        auto emit_reduces = [&](int w, int r, int i, const std::vector<int>& blocks) {
+            for (size_t k = 0; k < blocks.size();) {
+                const int c = blocks[k];
+                const int np = (int)parts[i][c].size();
+                size_t e = k + 1;
+                while (e < blocks.size() && e - k < 8 && blocks[e] == blocks[e - 1] + 1 &&
+                       (int)parts[i][blocks[e]].size() == np && base[i][blocks[e]] == base[i][blocks[e - 1]] + np)
+                    e++;
+                per_wg[w].push_back(SeqTask{i, kSeqReduce, c, (int)(e - k), 0, 0, (int32_t)base[i][c], np, np, -1, {0, 0}});
+                p.reduces++;
+                k = e;
+            }
+            (void)r;
+        };
+        for (int r = 0; r < runs; r++) {
+            const auto& v = run_pieces[r];
+            const int w = (cursor + r) % grid;
+            for (size_t k = 0; k < v.size();) {
+                const Piece& a = v[k];
+                const int64_t s0 = slot_of(a);
+                int64_t stride = 0;
+                size_t e = k + 1;
+                while (e < v.size()) {
+                    const Piece& b = v[e];
+                    if (b.lin != a.lin || b.c != a.c + (int)(e - k) || b.g0 != a.g0 || b.g1 != a.g1) break;
+                    const int64_t sb = slot_of(b);
+                    if ((s0 < 0) != (sb < 0)) break;
+                    if (s0 < 0 && lin[a.lin].has_bias && e - k == (size_t)kSeqBiasBlocks) break;
+                    if (s0 >= 0) {
+                        const int64_t d = sb - slot_of(v[e - 1]);
+                        if (e == k + 1) stride = d;
+                        else if (d != stride) break;
+                    }
+                    e++;
+                }
+                per_wg[w].push_back(SeqTask{a.lin, kSeqTile, a.c, (int)(e - k), a.g0, a.g1, (int32_t)s0,
+                                            (int32_t)stride, 0, -1, {0, 0}});
                 p.tiles++;
-                lo = end;
+                p.max_gseg = std::max(p.max_gseg, a.g1 - a.g0);
+                // blocks whose parts all sit in this run and end with this tile
+                std::vector<int> done;
+                for (size_t x = k; x < e; x++) {
+                    const Piece& q = v[x];
+                    const Host& h = host[q.lin][q.c];
+                    if (base[q.lin][q.c] >= 0 && h.run == r && h.local && parts[q.lin][q.c].back().g0 <= q.g0 &&
+                        parts[q.lin][q.c].back().g1 == q.g1)
+                        done.push_back(q.c);
+                }
+                if (!done.empty()) emit_reduces(w, r, a.lin, done);
+                k = e;
+            }
+            for (int i : ids) {
+                std::vector<int> rest;
+                for (int c = 0; c < (int)parts[i].size(); c++)
+                    if (base[i][c] >= 0 && host[i][c].run == r && !host[i][c].local) rest.push_back(c);
+                if (!rest.empty()) emit_reduces(w, r, i, rest);
             }
         }
         cursor = (cursor + runs) % grid;
-        // reductions of split linears: one per 64-column block, after the pass's tiles
-        for (int i : ids) {
-            if (p.split[i] == 1) continue;
-            const int ct = (lin[i].N + kCols - 1) / kCols;
-            for (int c = 0; c < ct; c++) {
-                per_wg[cursor].push_back(SeqTask{i, kSeqReduce, c, 0, 0, 0, -1, 1});
-                cursor = (cursor + 1) % grid;
-                p.reduces++;
-            }
-        }
     }
     p.task_begin.assign(grid + 1, 0);
     p.first_tile.assign(grid, -1);
     for (int w = 0; w < grid; w++) {
+        uint64_t units = 0;
+        for (const SeqTask& t : per_wg[w])
+            if (t.kind == kSeqTile) units += (uint64_t)t.nblk * (uint64_t)(t.g1 - t.g0);
+        p.total_units += units;
+        p.busiest_units = std::max(p.busiest_units, units);
         p.task_begin[w] = (int32_t)p.tasks.size();
         int prev = -1;
         for (const SeqTask& t : per_wg[w]) {
@@ -693,21 +1049,145 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
     p.lds_bytes = (uint64_t)std::max(1, p.max_gseg) * lds_per_group(M, group);
 }
 
+std::string verify_seq_plan(const std::vector<SeqSpec>& lin, int M, const SeqPlanOut& p)
+{
+    char msg[256];
+    const int n = (int)lin.size();
+    struct Part { int g0; int64_t slot; int wg; int task; };
+    std::vector<std::vector<int>> cover(n);                  // [i][c * groups + g] -> tile
+    std::vector<std::vector<int>> reduced(n);
+    std::vector<std::vector<std::vector<Part>>> written(n);   // [i][c] -> parts
+    for (int i = 0; i < n; i++) {
+        const int ct = (lin[i].N + kCols - 1) / kCols;
+        cover[i].assign((size_t)ct * (lin[i].K / lin[i].group), -1);
+        reduced[i].assign(ct, 0);
+        written[i].assign(ct, {});
+    }
+    if ((int)p.task_begin.size() != p.grid + 1 || p.task_begin[p.grid] != (int)p.tasks.size())
+        return "task_begin does not bound the task list";
+    // pass 1: tiles (coverage, LDS, chain links), pass order within each workgroup
+    for (int w = 0; w < p.grid; w++) {
+        int last_pass = -1, prev_tile = -1;
+        for (int t = p.task_begin[w]; t < p.task_begin[w + 1]; t++) {
+            const SeqTask& k = p.tasks[t];
+            if (k.linear < 0 || k.linear >= n) return "task names no linear";
+            const SeqSpec& s = lin[k.linear];
+            const int groups = s.K / s.group, ct = (s.N + kCols - 1) / kCols;
+            const int pass = p.pass_of[k.linear];
+            if (pass < last_pass) {
+                snprintf(msg, sizeof msg, "workgroup %d: pass %d after pass %d", w, pass, last_pass);
+                return msg;
+            }
+            last_pass = pass;
+            if (k.nblk < 1 || k.ct < 0 || k.ct + k.nblk > ct) return "task blocks outside the linear";
+            if (k.kind == kSeqReduce) continue;
+            if (k.kind != kSeqTile) return "unknown task kind";
+            if (prev_tile < 0 ? p.first_tile[w] != t : p.tasks[prev_tile].next_tile != t)
+                return "first_tile / next_tile chain broken";
+            prev_tile = t;
+            if (k.g0 < 0 || k.g1 > groups || k.g0 >= k.g1) return "tile groups outside K";
+            if ((uint64_t)(k.g1 - k.g0) * lds_per_group(M, s.group) > p.lds_bytes) return "tile exceeds the LDS plan";
+            if (k.slot < 0 && s.has_bias && k.nblk > kSeqBiasBlocks) return "tile with bias exceeds the staged blocks";
+            for (int b = 0; b < k.nblk; b++) {
+                for (int g = k.g0; g < k.g1; g++) {
+                    int& cv = cover[k.linear][(size_t)(k.ct + b) * groups + g];
+                    if (cv >= 0) {
+                        snprintf(msg, sizeof msg, "linear %d block %d group %d computed twice", k.linear, k.ct + b, g);
+                        return msg;
+                    }
+                    cv = t;
+                }
+                const int64_t slot = k.slot < 0 ? -1 : (int64_t)k.slot + (int64_t)b * k.stride;
+                if (slot >= (int64_t)p.slots) return "tile slot outside the pool";
+                written[k.linear][k.ct + b].push_back(Part{k.g0, slot, w, t});
+            }
+        }
+        if (prev_tile >= 0 ? p.tasks[prev_tile].next_tile != -1 : p.first_tile[w] != -1)
+            return "first_tile / next_tile chain broken";
+    }
+    // every group computed; a block of one part written whole, others in consecutive slots in K order
+    for (int i = 0; i < n; i++) {
+        const SeqSpec& s = lin[i];
+        const int groups = s.K / s.group, ct = (s.N + kCols - 1) / kCols;
+        for (size_t x = 0; x < cover[i].size(); x++)
+            if (cover[i][x] < 0) {
+                snprintf(msg, sizeof msg, "linear %d block %d group %d not computed", i, (int)(x / groups), (int)(x % groups));
+                return msg;
+            }
+        for (int c = 0; c < ct; c++) {
+            auto& v = written[i][c];
+            std::sort(v.begin(), v.end(), [](const Part& a, const Part& b) { return a.g0 < b.g0; });
+            if (v.size() == 1) {
+                if (v[0].slot >= 0) return "whole block routed through a reduction";
+                continue;
+            }
+            if ((int)v.size() > kSeqMaxSplit) return "more parts than the kernel supports";
+            for (size_t r = 0; r < v.size(); r++)
+                if (v[r].slot != v[0].slot + (int64_t)r) return "parts not in consecutive slots in K order";
+        }
+    }
+    // pass 2: reductions. Each reads exactly its blocks' parts; one that precedes some of its
+    // workgroup's tiles of the same pass reads only parts that workgroup already wrote (so a
+    // reduction never waits on a workgroup that could be waiting on it)
+    for (int w = 0; w < p.grid; w++) {
+        // index of the workgroup's last tile of the pass that each task belongs to (lists are
+        // ordered by pass, so one backward scan finds it)
+        std::vector<int> last_tile(p.task_begin[w + 1] - p.task_begin[w], -1);
+        for (int t = p.task_begin[w + 1] - 1, cur_pass = -1, last = -1; t >= p.task_begin[w]; t--) {
+            const SeqTask& k = p.tasks[t];
+            const int pass = p.pass_of[k.linear];
+            if (pass != cur_pass) {
+                cur_pass = pass;
+                last = -1;
+            }
+            if (k.kind == kSeqTile && last < 0) last = t;
+            last_tile[t - p.task_begin[w]] = last;
+        }
+        for (int t = p.task_begin[w]; t < p.task_begin[w + 1]; t++) {
+            const SeqTask& k = p.tasks[t];
+            if (k.kind != kSeqReduce) continue;
+            const bool tiles_after = last_tile[t - p.task_begin[w]] > t;
+            for (int b = 0; b < k.nblk; b++) {
+                const int c = k.ct + b;
+                if (reduced[k.linear][c]++) return "block reduced twice";
+                const auto& v = written[k.linear][c];
+                if (v.size() < 2 || (int)v.size() != k.parts || v[0].slot != (int64_t)k.slot + (int64_t)b * k.stride)
+                    return "reduction slots differ from the parts written";
+                if (tiles_after)
+                    for (const Part& q : v)
+                        if (q.wg != w || q.task > t) {
+                            snprintf(msg, sizeof msg, "workgroup %d: reduction of linear %d block %d may wait on a later tile",
+                                     w, k.linear, c);
+                            return msg;
+                        }
+            }
+        }
+    }
+    for (int i = 0; i < n; i++)
+        for (size_t c = 0; c < written[i].size(); c++)
+            if (written[i][c].size() > 1 && reduced[i][c] != 1) {
+                snprintf(msg, sizeof msg, "linear %d block %zu: %zu parts, reduced %d times", i, c, written[i][c].size(),
+                         reduced[i][c]);
+                return msg;
+            }
+    return "";
+}
+
 hipError_t seq_blocks_per_cu(int M, int group, int* blocks)
 {
-    const void* k = seq_kernel_for(M, group);
-    if (!k) return hipErrorInvalidValue;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, k, 256, kLdsBudget);
+    const SeqKernel k = seq_kernel_for(M, group);
+    if (!k.fn) return hipErrorInvalidValue;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, k.fn, k.threads, lds_budget(M, group));
 }
 
 int seq_wg_per_cu() { return QL_SEQ_WG_PER_CU; }
 
 hipError_t launch_seq(const SeqArgs& a, size_t lds, hipStream_t stream)
 {
-    const void* k = seq_kernel_for(a.M, a.group);
-    if (!k) return hipErrorInvalidValue;
+    const SeqKernel k = seq_kernel_for(a.M, a.group);
+    if (!k.fn) return hipErrorInvalidValue;
     void* args[] = {const_cast<SeqArgs*>(&a)};
-    return hipLaunchKernel(k, dim3(a.G), dim3(256), args, lds, stream);
+    return hipLaunchKernel(k.fn, dim3(a.G), dim3(k.threads), args, lds, stream);
 }
 
 }  // namespace ql

@@ -41,6 +41,8 @@ export class Arena {
 export interface SeqInfo {
     linears: number; passes: number; tiles: number; reduces: number; grid: number;
     maxSplit: number; ldsBytes: number; deviceBytes: number;
+    /** block-groups (64 columns x one group) in total and on the busiest workgroup */
+    totalUnits: number; busiestUnits: number;
 }
 /** A forward's decode linears (M <= 16) as one persistent launch; linear i reads linear j's
  *  output when xOffs[i] === yOffs[j]. */

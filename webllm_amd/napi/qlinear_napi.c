@@ -586,6 +586,8 @@ static napi_value js_seq_info(napi_env env, napi_callback_info info)
     napi_set_named_property(env, o, "maxSplit", make_i32(env, si.max_split));
     napi_set_named_property(env, o, "ldsBytes", make_u64(env, si.lds_bytes));
     napi_set_named_property(env, o, "deviceBytes", make_u64(env, si.device_bytes));
+    napi_set_named_property(env, o, "totalUnits", make_u64(env, si.total_units));
+    napi_set_named_property(env, o, "busiestUnits", make_u64(env, si.busiest_units));
     return o;
 }
 

@@ -60,10 +60,16 @@ class Plan(ctypes.Structure):
 class SeqInfo(ctypes.Structure):
     _fields_ = [("linears", ctypes.c_int32), ("passes", ctypes.c_int32), ("tiles", ctypes.c_int32),
                 ("reduces", ctypes.c_int32), ("grid", ctypes.c_int32), ("max_split", ctypes.c_int32),
-                ("lds_bytes", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64)]
+                ("lds_bytes", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64),
+                ("total_units", ctypes.c_uint64), ("busiest_units", ctypes.c_uint64)]
 
     def as_dict(self) -> dict:
         return {f: getattr(self, f) for f, _ in self._fields_}
+
+    @property
+    def balance(self) -> float:
+        """Block-groups of the busiest workgroup over the mean (1.0 = perfectly even)."""
+        return self.busiest_units * self.grid / max(1, self.total_units)
 
 
 _lib = None
