@@ -556,6 +556,7 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                 for (int t = 0; t < T; t++) {
                     const int m = 4 * t + kq;
                     st[t] = m < M ? gst[gg * M + m] : float2{0.f, 0.f};
+                    st[t].x *= 0x1p-8f;       // the digit pairs below carry a factor 2^8
                 }
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
@@ -563,9 +564,11 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                     const float sz = s * (float)(((zw >> (4 * u)) & 15u) + 1u);
 #pragma unroll
                     for (int t = 0; t < T; t++) {
-                        float v = fmaf((float)c[u][t][0], 0x1p-8f, (float)c[u][t][1]);
-                        v = fmaf(v, 0x1p-8f, (float)c[u][t][2]);
-                        v = fmaf(v, 0x1p-8f, (float)c[u][t][3]);
+                        // digit products (|c| < 2^18, digit 3 most significant) in two exact
+                        // integer pairs: 2^8 * sum_d c_d 2^(8d-24) = (c0 + 2^8 c1) 2^-16 + (c2 + 2^8 c3)
+                        const int lo = c[u][t][0] + c[u][t][1] * 256;
+                        const int hi = c[u][t][2] + c[u][t][3] * 256;
+                        const float v = fmaf((float)lo, 0x1p-16f, (float)hi);
                         acc[u][t] = fmaf(s * st[t].x, v, acc[u][t]);
                         acc[u][t] = fmaf(-sz, st[t].y, acc[u][t]);
                     }
