@@ -293,6 +293,74 @@ def test_gemm_parity(ql, ctx, orc, K, N, M, zero, label):
         say(f"    vs fp32 oracle normwise={np.abs(y-ref32).max()/np.abs(ref32).max():.3e}")
 
 
+def _gemm_ref(orc, t, x, bias, qzeros):
+    W16 = orc.f16_bits_to_f32(orc.dequantize_gptq_int4_f16(t.qweight, qzeros, t.scales, t.K, t.N, t.group))
+    x16 = orc.f16_bits_to_f32(orc.f32_to_f16_bits(x))
+    return orc.gemm_nt(x16, W16, bias)
+
+
+GEMM_SHAPE_CASES = [
+    # (K, N, M, group, no_qzeros, label): K steps per group 1, 2, 8; absent qzeros; 128-row tiles
+    (512, 320, 40, 32, False, "group 32"),
+    (1024, 708, 65, 64, False, "group 64, N % 256 != 0"),
+    (2048, 516, 96, 256, True, "group 256, no qzeros"),
+    (256, 4864, 1800, 128, False, "128-row tiles, ragged M"),
+]
+
+
+@pytest.mark.parametrize("K,N,M,group,noqz,label", GEMM_SHAPE_CASES)
+def test_gemm_shapes(ql, ctx, orc, K, N, M, group, noqz, label):
+    t = synth.gptq_linear(K, N, group, seed=0x6E40, key=(K, N, M, group))
+    bias = synth.activations(1, N, seed=0x6E41, key=(N,))[0]
+    x = synth.activations(M, K, seed=0x6E42, key=(K, M))
+    lin = Linear(ql, ctx, t, bias=bias, no_qzeros=noqz)
+    plan = ql.plan_linear(M, N, K, group)
+    say(f"gemm {label}: M={M} K={K} N={N} group={group} split={plan.split} grid={plan.grid_x}")
+    assert plan.kind_name == "gemm_mfma"
+    ref = _gemm_ref(orc, t, x, bias, lin.qzeros)
+    for x_dtype in (0, 1):
+        xin = x if x_dtype == 0 else x.astype(np.float16).view(np.uint16)
+        y, _ = run_linear(ql, ctx, lin, xin, x_dtype)
+        assert_close(orc, y, ref, GEMM_ATOL, GEMM_RTOL, f"{label} x_dtype={x_dtype}")
+
+
+def test_gemm_batch_and_determinism(ql, ctx, orc):
+    """q/k/v (M=128, f16 input) as one batched GEMM launch: each output matches its own launch
+    bit for bit, split-K results repeat exactly, and all meet the GEMM bar."""
+    K, M = 896, 128
+    ts = [synth.gptq_linear(K, n, 128, seed=0x6E50, key=(i,)) for i, n in enumerate((896, 128, 128))]
+    biases = [synth.activations(1, t.N, seed=0x6E51, key=(i,))[0] for i, t in enumerate(ts)]
+    lay = ql.ArenaLayout()
+    descs, parts = [], []
+    for t, b in zip(ts, biases):
+        a, z, s_, bo = lay.take(t.qweight.nbytes), lay.take(t.qzeros.nbytes), lay.take(t.scales.nbytes), lay.take(b.nbytes)
+        parts.append((a, z, s_, bo, t, b))
+        descs.append(ql.make_desc(a, z, s_, K, t.N, 128, bo))
+    w = ctx.arena(lay.used)
+    for a, z, s_, bo, t, b in parts:
+        w.write(a, t.qweight); w.write(z, t.qzeros); w.write(s_, t.scales); w.write(bo, b)
+    assert any(ql.plan_linear(M, t.N, K).split > 1 for t in ts)
+    x = synth.activations(M, K, seed=0x6E52)
+    x16 = x.astype(np.float16).view(np.uint16)
+    scratch = ql.plan_batch(descs, M)
+    alay = ql.ArenaLayout()
+    x_off = alay.take(x16.nbytes)
+    y_offs = [alay.take(M * t.N * 4) for t in ts]
+    s_off = alay.take(max(scratch, 16))
+    act = ctx.arena(alay.used)
+    act.write(x_off, x16)
+    ctx.linear_batch(descs, w, act, [x_off] * 3, 1, M, y_offs, s_off)
+    first = [act.read(yo, (M, t.N), np.float32) for yo, t in zip(y_offs, ts)]
+    for _ in range(3):
+        ctx.linear_batch(descs, w, act, [x_off] * 3, 1, M, y_offs, s_off)
+        for yo, t, f in zip(y_offs, ts, first):
+            assert np.array_equal(act.read(yo, (M, t.N), np.float32).view(np.uint32), f.view(np.uint32))
+    for d, yo, t, b, f in zip(descs, y_offs, ts, biases, first):
+        ctx.linear(d, w, act, x_off, 1, M, yo, s_off)
+        assert np.array_equal(act.read(yo, (M, t.N), np.float32).view(np.uint32), f.view(np.uint32))
+        assert_close(orc, f, _gemm_ref(orc, t, x, b, t.qzeros), GEMM_ATOL, GEMM_RTOL, f"batch N={t.N}")
+
+
 # ------------------------------------------------------------------------- generic paths
 
 def test_simple_paths_reference_kat_shape(ql, ctx, orc):

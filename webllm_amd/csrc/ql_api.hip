@@ -115,10 +115,14 @@ int plan_impl(int M, int N, int K, int group, ql_plan* p)
             p->block = 256;
         }
     } else if (ql::gemm_fast_ok(M, N, K, group)) {
+        const ql::GemmShape s = ql::gemm_shape(M, N, K, group, ql::kPlanCUs);
         p->kind = QL_KIND_GEMM_MFMA;
-        p->split = 1;
+        p->split = s.split;
         p->waves = 4;
-        ql::gemm_grid(M, N, &p->grid_x, &p->grid_y, &p->block);
+        p->grid_x = s.tiles_n * s.tiles_m * s.split;
+        p->grid_y = 1;
+        p->block = 256;
+        p->scratch_bytes = ql::gemm_partial_bytes(M, N, s.split);
     } else {
         p->kind = QL_KIND_GEMM_SIMPLE;
         p->split = 1;
@@ -547,6 +551,39 @@ int ql_unpack_f32(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, q
     return QL_OK;
 }
 
+namespace {
+
+// One GEMM batch entry: pointers, shape, partial sums at scratch_off and arrival counters from
+// counter_base (both used only when the linear splits K).
+int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, uint64_t x_off, int M,
+               uint64_t y_off, uint64_t scratch_off, uint32_t* counters, int counter_base, int wg_begin,
+               ql::GemmLinear* out)
+{
+    const ql::GemmShape s = ql::gemm_shape(M, d->N, d->K, d->group, ql::kPlanCUs);
+    const ql::GemvLinear g = make_linear(d, weights);
+    ql::GemmLinear& L = *out;
+    L.qweight = g.qweight;
+    L.qzeros = g.qzeros;
+    L.scales = g.scales;
+    L.bias = g.bias;
+    L.x = act->base + x_off;
+    L.y = reinterpret_cast<float*>(act->base + y_off);
+    L.partial = reinterpret_cast<float*>(act->base + scratch_off);
+    L.counters = counters + counter_base;
+    L.N = d->N;
+    L.K = d->K;
+    L.group = d->group;
+    L.split = s.split;
+    L.tiles_n = s.tiles_n;
+    L.tiles_m = s.tiles_m;
+    L.wg_begin = wg_begin;
+    if (s.split > 1 && counter_base + s.tiles_n * s.tiles_m > ql::kCounterCapacity)
+        return fail(QL_E_INVALID, "too many GEMM tiles for the split-K counters");
+    return QL_OK;
+}
+
+}  // namespace
+
 int ql_plan_linear(int32_t M, int32_t N, int32_t K, int32_t group, ql_plan* out)
 {
     if (!out) return fail(QL_E_INVALID, "null plan pointer");
@@ -592,6 +629,22 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_ar
         QL_HIP(ql::launch_gemv_simple(L, M, x_dtype, ctx->stream));
         return QL_OK;
     }
+    if (p.kind == QL_KIND_GEMM_MFMA && gemv_aligned(d, x_off, y_off)) {
+        if (!in_range(scratch_off, p.scratch_bytes, act->size))
+            return fail(QL_E_RANGE, "scratch (%llu bytes) outside the activation arena",
+                        (unsigned long long)p.scratch_bytes);
+        if (scratch_off % 16) return fail(QL_E_ALIGN, "scratch offset must be 16-byte aligned");
+        ql::GemmBatch b{};
+        int rc2 = gemm_entry(d, weights, act, x_off, M, y_off, scratch_off, ctx->counters, 0, 0, &b.L[0]);
+        if (rc2) return rc2;
+        b.count = 1;
+        b.M = M;
+        b.x_dtype = x_dtype;
+        b.bm = ql::gemm_shape(M, d->N, d->K, d->group, ql::kPlanCUs).bm;
+        b.wg_total = b.L[0].tiles_n * b.L[0].tiles_m * b.L[0].split;
+        QL_HIP(ql::launch_gemm_batch(b, ctx->stream));
+        return QL_OK;
+    }
     ql::GemmArgs g;
     g.qweight = L.qweight;
     g.qzeros = L.qzeros;
@@ -604,11 +657,7 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_ar
     g.K = d->K;
     g.group = d->group;
     g.x_dtype = x_dtype;
-    if (p.kind == QL_KIND_GEMM_MFMA && x_off % 16 == 0) {
-        QL_HIP(ql::launch_gemm(g, ctx->stream));
-    } else {
-        QL_HIP(ql::launch_gemm_simple(g, ctx->stream));
-    }
+    QL_HIP(ql::launch_gemm_simple(g, ctx->stream));
     return QL_OK;
 }
 
@@ -640,14 +689,44 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
         return fail(QL_E_RANGE, "batch scratch (%llu bytes) outside the activation arena",
                     (unsigned long long)total);
     if (scratch_off % 16) return fail(QL_E_ALIGN, "scratch offset must be 16-byte aligned");
-    bool fused = true;
+    bool fused = true, gemm = true;
+    int bm = 0;
     for (int i = 0; i < count; i++) {
         if ((rc = check_desc(&descs[i], weights))) return rc;
         if ((rc = check_io(&descs[i], act, x_offs[i], x_dtype, M, y_offs[i]))) return rc;
         ql_plan p;
         plan_impl(M, descs[i].N, descs[i].K, descs[i].group, &p);
-        fused &= p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(&descs[i], x_offs[i], y_offs[i]) &&
-                 descs[i].group == descs[0].group;
+        const bool aligned = gemv_aligned(&descs[i], x_offs[i], y_offs[i]);
+        fused &= p.kind == QL_KIND_GEMV_MFMA && aligned && descs[i].group == descs[0].group;
+        gemm &= p.kind == QL_KIND_GEMM_MFMA && aligned;
+        if (gemm) {
+            const int b = ql::gemm_shape(M, descs[i].N, descs[i].K, descs[i].group, ql::kPlanCUs).bm;
+            gemm &= i == 0 || b == bm;
+            bm = b;
+        }
+    }
+    if (gemm) {
+        // one launch; each linear's partial sums at its own offset, as ql_plan_batch sized them
+        if ((rc = set_device(ctx))) return rc;
+        ql::GemmBatch b{};
+        b.count = count;
+        b.M = M;
+        b.x_dtype = x_dtype;
+        b.bm = bm;
+        uint64_t off = scratch_off;
+        int wg = 0, counter_base = 0;
+        for (int i = 0; i < count; i++) {
+            if ((rc = gemm_entry(&descs[i], weights, act, x_offs[i], M, y_offs[i], off, ctx->counters,
+                                 counter_base, wg, &b.L[i])))
+                return rc;
+            const ql::GemmLinear& L = b.L[i];
+            if (L.split > 1) counter_base += L.tiles_n * L.tiles_m;
+            off += align256(ql::gemm_partial_bytes(M, descs[i].N, L.split));
+            wg += L.tiles_n * L.tiles_m * L.split;
+        }
+        b.wg_total = wg;
+        QL_HIP(ql::launch_gemm_batch(b, ctx->stream));
+        return QL_OK;
     }
     if (!fused) {
         uint64_t off = scratch_off;

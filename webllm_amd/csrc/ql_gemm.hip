@@ -1,162 +1,357 @@
 // Prefill GEMM for GPTQ int4 linears, M > 16: y[M,N] = f16(x)[M,K] * f16(W)[N,K]^T (+ bias),
 // fp32 accumulation. Same arithmetic as the reference's M > 1 path, gemm_nt_f16_from_f32.wgsl
 // (x rounded to fp16 on load, fp16 weights from the load-time dequant), but the weights are
-// dequantized from the packed int4 tiles into LDS inside the kernel, bit-identical to the
-// load-time fp16 arena (dequant_word_perm in ql_device.h).
+// dequantized from the packed int4 words inside the kernel, bit-identical to the load-time fp16
+// arena (dequant_word_perm in ql_device.h).
 //
-// Tile: 64 (M) x 64 (N) x 32 (K) per workgroup of 4 waves (2 x 2), each wave 32 x 32 as 2 x 2
-// v_mfma_f32_16x16x32_f16 tiles. One K step is 4 packed qweight rows, which is one MFMA K block;
-// each packed word dequantizes to exactly one lane's B fragment (8 k of one column), stored to
-// LDS as 16 bytes. Activations are staged to LDS in the same permuted k order. Global loads for
-// step i+1 are issued before the MFMAs of step i.
+// Work split: a workgroup (4 waves) owns BM rows x 256 columns and one K segment of whole
+// quantization groups; each wave owns 64 of the columns for all BM rows. A K step is 32 k (one
+// v_mfma_f32_16x16x32_f16 block = 4 packed qweight rows).
+// * Weights never pass through LDS. Lane (j, kq) loads 16 bytes of packed row 4s + kq: the words
+//   of columns 4j .. 4j+3 of its wave's strip, and each word is exactly the lane's B fragment (8 k
+//   of one column) for one of the wave's 4 N tiles. N tile t therefore holds columns 4j + t,
+//   which makes each lane's 4 outputs of a row adjacent (one 16-byte store).
+// * Activations (shared by the 4 waves) are staged per step in LDS, double-buffered, rounded to
+//   fp16 and permuted into the k order dequant_word_perm emits.
+// * Each thread keeps D steps of loads in flight (a register ring, statically indexed).
+// * With split > 1 K segments, each workgroup stores its partial tile with agent-scope stores and
+//   bumps the tile's arrival counter; the last one adds the partials in ascending segment order
+//   (deterministic, like the reference's gemm_gemv_split_reduce.wgsl:32-38) and resets the
+//   counter, all in one launch.
+// * Several linears can share one launch (q/k/v, gate/up): workgroups are numbered across them.
 #include "ql_device.h"
+#include "ql_digits.h"
 #include "ql_internal.h"
+
+#include <algorithm>
 
 namespace ql {
 
 namespace {
 
-constexpr int BM = 64;
-constexpr int BN = 64;
+// Tunables (compile-time):
+//   QL_GEMM_DEPTH       K steps of loads each thread keeps in flight (even)
+//   QL_GEMM_TARGET_WGS  workgroups per CU a linear aims for when choosing the K split
+//   QL_GEMM_MIN_STEPS   fewest K steps per segment (caps the split)
+#ifndef QL_GEMM_DEPTH
+#define QL_GEMM_DEPTH 8
+#endif
+#ifndef QL_GEMM_TARGET_WGS
+#define QL_GEMM_TARGET_WGS 1
+#endif
+#ifndef QL_GEMM_MIN_STEPS
+#define QL_GEMM_MIN_STEPS 8
+#endif
+static_assert(QL_GEMM_DEPTH % 4 == 0, "the LDS double buffer alternates with the ring slot");
 
-struct Stage {
-    uint4 a;       // 8 activations of one row (fp16, natural order) or f32 pair below
-    float4 af0, af1;
-    uint32_t w;    // one packed word
-    uint32_t zz, ss;
-};
+constexpr int kCols = kGemmTileCols;   // 256 columns per workgroup, 64 per wave
 
-__device__ __forceinline__ void load_stage(const GemmArgs& g, int m0, int n0, int k0, Stage& st)
+constexpr int kSC1 = 16;               // buffer-op cache policy bit SC1 (agent coherence)
+
+// qzeros word of a linear without qzeros: every stored zero 7 (true zero 8)
+__device__ const uint32_t kSymZeros = 0x77777777u;
+
+// 8 activations (natural k order) as fp16 in the order dequant_word_perm emits {0,4,1,5,2,6,3,7}
+__device__ __forceinline__ u32x4 perm_f16(u32x4 nat)
 {
-    const int t = threadIdx.x;
-    // activations: row r, chunk kq
-    const int r = t >> 2, kq = t & 3;
-    const int m = m0 + r;
-    if (m < g.M) {
-        if (g.x_dtype == 0) {
-            const float4* src = reinterpret_cast<const float4*>(
-                static_cast<const float*>(g.x) + (size_t)m * g.K + k0 + 8 * kq);
-            st.af0 = src[0];
-            st.af1 = src[1];
-        } else {
-            st.a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(g.x) +
-                                                   (size_t)m * g.K + k0 + 8 * kq);
-        }
-    } else {
-        st.a = uint4{0u, 0u, 0u, 0u};
-        st.af0 = float4{0.f, 0.f, 0.f, 0.f};
-        st.af1 = st.af0;
-    }
-    // weights: packed row kw, column c
-    const int kw = t >> 6, c = t & 63;
-    const int n = n0 + c;
-    if (n < g.N) {
-        const int p = (k0 >> 3) + kw;
-        const int grp = k0 / g.group;
-        st.w = g.qweight[(size_t)p * g.N + n];
-        st.zz = zero_pair(zero_of(g.qzeros, grp, (g.N + 7) >> 3, n));
-        st.ss = (uint32_t)g.scales[(size_t)grp * g.N + n] * 0x10001u;
-    } else {
-        st.w = 0u;
-        st.zz = zero_pair(8u);
-        st.ss = 0u;
-    }
+    // nat holds (k0,k1) (k2,k3) (k4,k5) (k6,k7); want (k0,k4) (k1,k5) (k2,k6) (k3,k7)
+    u32x4 r;
+    r.x = __builtin_amdgcn_perm(nat.z, nat.x, 0x05040100u);   // lo halves: k0 | k4
+    r.y = __builtin_amdgcn_perm(nat.z, nat.x, 0x07060302u);   // hi halves: k1 | k5
+    r.z = __builtin_amdgcn_perm(nat.w, nat.y, 0x05040100u);   // k2 | k6
+    r.w = __builtin_amdgcn_perm(nat.w, nat.y, 0x07060302u);   // k3 | k7
+    return r;
 }
 
-__device__ __forceinline__ void store_stage(const GemmArgs& g, const Stage& st, uint4* As, uint4* Bs)
+// The same from 8 f32 activations (a: k0..k3, b: k4..k7), each rounded to fp16 (RNE). Written as
+// one vector shuffle + conversion: building the result from four scalar (lo, hi) pair
+// conversions is miscompiled for gfx950 by this toolchain (all four words come out equal to the
+// first pair).
+__device__ __forceinline__ u32x4 perm_f32(u32x4 a, u32x4 b)
 {
-    const int t = threadIdx.x;
-    const int r = t >> 2, kq = t & 3;
-    f16x8 h;
-    if (g.x_dtype == 0) {
-        const float v[8] = {st.af0.x, st.af0.y, st.af0.z, st.af0.w,
-                            st.af1.x, st.af1.y, st.af1.z, st.af1.w};
-#pragma unroll
-        for (int e = 0; e < 8; e++) h[e] = (_Float16)v[perm_k(e)];
-    } else {
-        const f16x8 nat = __builtin_bit_cast(f16x8, st.a);
-#pragma unroll
-        for (int e = 0; e < 8; e++) h[e] = nat[perm_k(e)];
-    }
-    As[kq * BM + r] = __builtin_bit_cast(uint4, h);
-    const int kw = t >> 6, c = t & 63;
-    Bs[kw * BN + c] = __builtin_bit_cast(uint4, dequant_word_perm(st.w, st.zz, st.ss));
+    typedef float f32x8 __attribute__((ext_vector_type(8)));
+    const f32x4 fa = __builtin_bit_cast(f32x4, a), fb = __builtin_bit_cast(f32x4, b);
+    const f32x8 v = __builtin_shufflevector(fa, fb, 0, 4, 1, 5, 2, 6, 3, 7);
+    return __builtin_bit_cast(u32x4, __builtin_convertvector(v, f16x8));
 }
 
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(const GemmArgs g)
+// An empty asm that claims to rewrite v, so nothing computed from v moves above this point
+__device__ __forceinline__ void pin(u32x4& v)
 {
-    __shared__ uint4 As[4 * BM];
-    __shared__ uint4 Bs[4 * BN];
-    const int n0 = blockIdx.x * BN;
-    const int m0 = blockIdx.y * BM;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    uint32_t e0 = v.x, e1 = v.y, e2 = v.z, e3 = v.w;
+    asm volatile("" : "+v"(e0), "+v"(e1), "+v"(e2), "+v"(e3));
+    v = u32x4{e0, e1, e2, e3};
+}
+
+template <int BM, bool XF32, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 2 : 1)))
+void gemm_kernel(const GemmBatch b)
+{
+    constexpr int MT = BM / 16;              // M tiles per wave
+    constexpr int AC = BM * 4 / 256;         // 8-k activation chunks per thread per step
+    constexpr int AV = XF32 ? 2 : 1;         // 16-byte loads per chunk
+    // [buffer][k block][row], fp16 in dequant order; one spare row per k block keeps the 4 k
+    // blocks of a row (written by adjacent threads) in different banks
+    __shared__ u32x4 As[2][4][BM + 1];
+
+    // workgroup -> (linear, N tile, M tile, segment); consecutive numbers share an XCD (the
+    // hardware deals workgroups out to the 8 XCDs in turn), so a strip's M tiles and segments
+    // meet its weights in one L2
+    const int bid = blockIdx.x;
+    const int n8 = b.wg_total / 8 * 8;
+    const int wg = bid < n8 ? (bid % 8) * (n8 / 8) + bid / 8 : bid;
+    int li = 0;
+    while (li + 1 < b.count && wg >= b.L[li + 1].wg_begin) li++;
+    const GemmLinear& L = b.L[li];
+    const int N = L.N, K = L.K, M = b.M;
+    int local = wg - L.wg_begin;
+    const int split = L.split;
+    const int seg = local % split;
+    local /= split;
+    const int mt = local % L.tiles_m;
+    const int nt = local / L.tiles_m;
+    const int groups = K / L.group;
+    const int spg = L.group / 32;                           // K steps per group
+    const int ga = seg * groups / split, gb = (seg + 1) * groups / split;
+    const int s0 = ga * spg, S = (gb - ga) * spg;           // this segment's steps
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, kq = lane >> 4;
+    const int ncol = nt * kCols + wave * 64 + 4 * j;        // this lane's 4 columns
+    const bool col_ok = ncol < N;                           // N % 4 == 0: all 4 or none
+    const int nc = col_ok ? ncol : 0;                       // loads stay inside the tensors
+    const int m0 = mt * BM;
+    const int NZ = (N + 7) >> 3;
+    const uint32_t zshift = 4 * (nc & 7);                   // 0 or 16
 
-    f32x4 c[2][2];
-#pragma unroll
-    for (int a = 0; a < 2; a++)
-#pragma unroll
-        for (int b = 0; b < 2; b++) c[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t* qw = L.qweight + nc + (size_t)kq * N;
+    const uint16_t* sc = L.scales + nc;
+    // every load is unconditional (a conditional one makes the compiler drain the whole ring)
+    const uint32_t* qz = L.qzeros ? L.qzeros + (nc >> 3) : &kSymZeros;
+    const int zstride = L.qzeros ? NZ : 0;
 
-    Stage st;
-    load_stage(g, m0, n0, 0, st);
-    for (int k0 = 0; k0 < g.K; k0 += 32) {
-        store_stage(g, st, As, Bs);
-        __syncthreads();
-        if (k0 + 32 < g.K) load_stage(g, m0, n0, k0 + 32, st);
-        f16x8 af[2], bf[2];
+    // activation chunk c = threadIdx.x + 256 a: row c / 4, k block c % 4 (rows past M read row
+    // M - 1; their results land in rows that are never stored)
+    const void* xb = L.x;
+    size_t xrow[AC];
+    int arow[AC], akb[AC];
 #pragma unroll
-        for (int tm = 0; tm < 2; tm++)
-            af[tm] = __builtin_bit_cast(f16x8, As[kq * BM + wm * 32 + tm * 16 + j]);
-#pragma unroll
-        for (int tn = 0; tn < 2; tn++)
-            bf[tn] = __builtin_bit_cast(f16x8, Bs[kq * BN + wn * 32 + tn * 16 + j]);
-#pragma unroll
-        for (int tm = 0; tm < 2; tm++)
-#pragma unroll
-            for (int tn = 0; tn < 2; tn++) c[tm][tn] = mfma_16x16x32_f16(af[tm], bf[tn], c[tm][tn]);
-        __syncthreads();
+    for (int a = 0; a < AC; a++) {
+        const int c = threadIdx.x + 256 * a;
+        arow[a] = c >> 2;
+        akb[a] = c & 3;
+        xrow[a] = (size_t)min(m0 + arow[a], M - 1) * K + 8 * akb[a];
     }
 
+    u32x4 wq[D], xa[D][AC * AV];
+    u32x2 sv[D];
+    uint32_t zv[D];
+    auto load = [&](int d, int s) {
+        const int sa = s0 + s;
+        const int g = sa / spg;
+        wq[d] = ld_global(reinterpret_cast<const u32x4*>(qw + (size_t)sa * 4 * N));
+        sv[d] = ld_global(reinterpret_cast<const u32x2*>(sc + (size_t)g * N));
+        zv[d] = ld_global(qz + (size_t)g * zstride);
 #pragma unroll
-    for (int tm = 0; tm < 2; tm++) {
-#pragma unroll
-        for (int tn = 0; tn < 2; tn++) {
-            const int n = n0 + wn * 32 + tn * 16 + j;
-            if (n >= g.N) continue;
-            const float bias = g.bias ? g.bias[n] : 0.f;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm * 32 + tm * 16 + 4 * kq + r;
-                if (m < g.M) g.y[(size_t)m * g.N + n] = g.bias ? c[tm][tn][r] + bias : c[tm][tn][r];
+        for (int a = 0; a < AC; a++) {
+            if (XF32) {
+                const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const float*>(xb) + xrow[a] + 32 * sa);
+                xa[d][2 * a] = ld_global(p);
+                xa[d][2 * a + 1] = ld_global(p + 1);
+            } else {
+                xa[d][a] = ld_global(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(xb) + xrow[a] + 32 * sa));
             }
         }
+    };
+
+    f32x4 acc[MT][4];
+#pragma unroll
+    for (int tm = 0; tm < MT; tm++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[tm][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // one K step: this step's activations into LDS buffer d & 1 (its last readers finished
+    // before the previous step's barrier), then 4 x MT MFMAs
+    auto step = [&](int d) {
+        // pin the raw activations here: otherwise the f32 -> f16 conversion is hoisted next to
+        // the loads, which then have to complete at once
+#pragma unroll
+        for (int a = 0; a < AC * AV; a++) pin(xa[d][a]);
+#pragma unroll
+        for (int a = 0; a < AC; a++)
+            As[d & 1][akb[a]][arow[a]] = XF32 ? perm_f32(xa[d][2 * a], xa[d][2 * a + 1]) : perm_f16(xa[d][a]);
+        __syncthreads();
+        f16x8 bf[4];
+        const uint32_t zw = zv[d] >> zshift;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t sbits = (t < 2 ? sv[d].x : sv[d].y) >> (16 * (t & 1)) & 0xFFFFu;
+            bf[t] = dequant_word_perm(wq[d][t], zero_pair(((zw >> (4 * t)) & 15u) + 1u), sbits * 0x10001u);
+        }
+#pragma unroll
+        for (int tm = 0; tm < MT; tm++) {
+            const f16x8 af = __builtin_bit_cast(f16x8, As[d & 1][kq][16 * tm + j]);
+#pragma unroll
+            for (int t = 0; t < 4; t++) acc[tm][t] = mfma_16x16x32_f16(af, bf[t], acc[tm][t]);
+        }
+    };
+    // ring of D steps; loads past the segment's end repeat its last step (never consumed)
+#pragma unroll
+    for (int d = 0; d < D; d++) load(d, min(d, S - 1));
+    int s = 0;
+    for (; s + D <= S; s += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            step(d);
+            load(d, min(s + d + D, S - 1));
+        }
     }
+#pragma unroll
+    for (int d = 0; d < D; d++)
+        if (s + d < S) step(d);
+
+    // lane (j, kq) holds rows 16 tm + 4 kq + r of columns ncol .. ncol + 3 (one per N tile)
+    if (split == 1) {
+        if (!col_ok) return;
+        f32x4 bias = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (L.bias) bias = ld_global(reinterpret_cast<const f32x4*>(L.bias + ncol));
+#pragma unroll
+        for (int tm = 0; tm < MT; tm++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + 16 * tm + 4 * kq + r;
+                if (m < M)
+                    st_global(reinterpret_cast<f32x4*>(L.y + (size_t)m * N + ncol),
+                              f32x4{acc[tm][0][r] + bias.x, acc[tm][1][r] + bias.y, acc[tm][2][r] + bias.z,
+                                    acc[tm][3][r] + bias.w});
+            }
+        return;
+    }
+    // Partial sums go through buffer stores / loads with the SC1 cache policy: the coherence
+    // point of agent-scope accesses (another XCD's workgroup adds them up). Unlike atomics they
+    // can all be in flight at once. The host keeps split * M * N * 4 below 2 GiB.
+    const __amdgpu_buffer_rsrc_t part = __builtin_amdgcn_make_buffer_rsrc(L.partial, 0, 0x7FFFFFFF, 0x00020000);
+    const uint32_t plane = (uint32_t)M * (uint32_t)N * 4u;   // bytes per segment
+    if (col_ok) {
+#pragma unroll
+        for (int tm = 0; tm < MT; tm++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + 16 * tm + 4 * kq + r;
+                if (m < M)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        f32x4{acc[tm][0][r], acc[tm][1][r], acc[tm][2][r], acc[tm][3][r]}, part,
+                        ((uint32_t)m * (uint32_t)N + (uint32_t)ncol) * 4u, seg * plane, kSC1);
+            }
+    }
+    // this wave's partial stores are complete before the workgroup signals arrival
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ uint32_t is_last;
+    __syncthreads();
+    const int tile = nt * L.tiles_m + mt;
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&L.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t last = prev == (uint32_t)(split - 1);
+        if (last) __hip_atomic_store(&L.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = last;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    // the tile's sums in ascending segment order: a thread owns PER 4-column pieces, and each
+    // segment's loads for all of them are issued together (one round trip per segment)
+    // a thread owns PER 4-column pieces, reduced HALF at a time with two segments' loads in flight
+    constexpr int PER = BM * (kCols / 4) / 256;
+    constexpr int HALF = PER / 2;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        f32x4 sum[HALF];
+        bool ok[HALF];
+        int col[HALF];
+        uint32_t off[HALF];
+#pragma unroll
+        for (int i = 0; i < HALF; i++) {
+            const int idx = threadIdx.x + 256 * (h * HALF + i);
+            const int m = m0 + idx / (kCols / 4);
+            const int n = nt * kCols + 4 * (idx % (kCols / 4));
+            ok[i] = m < M && n < N;
+            col[i] = n;
+            off[i] = ok[i] ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * 4u : 0u;
+            sum[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        int sg = 0;
+        for (; sg + 2 <= split; sg += 2) {
+            f32x4 v0[HALF], v1[HALF];
+#pragma unroll
+            for (int i = 0; i < HALF; i++) {
+                v0[i] = __builtin_amdgcn_raw_buffer_load_b128(part, off[i], sg * plane, kSC1);
+                v1[i] = __builtin_amdgcn_raw_buffer_load_b128(part, off[i], (sg + 1) * plane, kSC1);
+            }
+#pragma unroll
+            for (int i = 0; i < HALF; i++) sum[i] = sum[i] + v0[i] + v1[i];
+        }
+        if (sg < split) {
+#pragma unroll
+            for (int i = 0; i < HALF; i++) sum[i] += __builtin_amdgcn_raw_buffer_load_b128(part, off[i], sg * plane, kSC1);
+        }
+#pragma unroll
+        for (int i = 0; i < HALF; i++) {
+            if (!ok[i]) continue;
+            f32x4 v = sum[i];
+            if (L.bias) v += ld_global(reinterpret_cast<const f32x4*>(L.bias + col[i]));
+            st_global(reinterpret_cast<f32x4*>(L.y + off[i] / 4u), v);
+        }
+    }
+}
+
+template <int BM, bool XF32>
+hipError_t launch_bm(const GemmBatch& b, hipStream_t stream)
+{
+    // f32 activations take twice the registers per step: half the depth
+    constexpr int D = XF32 ? QL_GEMM_DEPTH / 2 : QL_GEMM_DEPTH;
+    hipLaunchKernelGGL((gemm_kernel<BM, XF32, D>), dim3(b.wg_total), dim3(256), 0, stream, b);
+    return hipGetLastError();
 }
 
 }  // namespace
 
 bool gemm_fast_ok(int M, int N, int K, int group)
 {
-    return M > 0 && N > 0 && K > 0 && K % 32 == 0 && group > 0 && group % 32 == 0 &&
-           K % group == 0;
+    return M > kGemvMaxM && N > 0 && K > 0 && N % 4 == 0 && group >= 32 && group % 32 == 0 && K % group == 0;
 }
 
-void gemm_grid(int M, int N, int* gx, int* gy, int* block)
+GemmShape gemm_shape(int M, int N, int K, int group, int cu_count)
 {
-    *gx = (N + BN - 1) / BN;
-    *gy = (M + BM - 1) / BM;
-    *block = 256;
+    GemmShape s;
+    s.tiles_n = (N + kCols - 1) / kCols;
+    // 128-row tiles once they alone give every CU a workgroup, else 64
+    s.bm = (long)s.tiles_n * ((M + 127) / 128) >= cu_count ? 128 : 64;
+    s.tiles_m = (M + s.bm - 1) / s.bm;
+    const int tiles = s.tiles_n * s.tiles_m;
+    const int groups = K / group;
+    const int steps_per_group = group / 32;
+    const int max_split = std::max(1, groups * steps_per_group / QL_GEMM_MIN_STEPS);
+    // a K split pays for its partial-sum round trip only when the tiles leave most CUs idle
+    const int want = tiles * 2 >= cu_count ? 1 : (QL_GEMM_TARGET_WGS * cu_count + tiles - 1) / tiles;
+    s.split = std::max(1, std::min({want, max_split, groups}));
+    // partial sums are addressed with 32-bit byte offsets
+    while (s.split > 1 && (uint64_t)s.split * M * N * 4 >= (1ull << 31)) s.split--;
+    return s;
 }
 
-hipError_t launch_gemm(const GemmArgs& a, hipStream_t stream)
+uint64_t gemm_partial_bytes(int M, int N, int split)
 {
-    int gx, gy, block;
-    gemm_grid(a.M, a.N, &gx, &gy, &block);
-    hipLaunchKernelGGL(gemm_mfma_kernel, dim3(gx, gy), dim3(block), 0, stream, a);
-    return hipGetLastError();
+    return split > 1 ? (uint64_t)split * M * N * 4 : 0;
+}
+
+hipError_t launch_gemm_batch(const GemmBatch& b, hipStream_t stream)
+{
+    if (b.count < 1 || b.count > kMaxBatch || b.wg_total < 1) return hipErrorInvalidValue;
+    const int bm = b.bm;
+    for (int i = 1; i < b.count; i++)
+        if (b.L[i].wg_begin <= b.L[i - 1].wg_begin) return hipErrorInvalidValue;
+    if (bm == 64) return b.x_dtype == 0 ? launch_bm<64, true>(b, stream) : launch_bm<64, false>(b, stream);
+    if (bm == 128) return b.x_dtype == 0 ? launch_bm<128, true>(b, stream) : launch_bm<128, false>(b, stream);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace ql

@@ -56,10 +56,34 @@ struct GemmArgs {
     float* y;
     int M, N, K, group, x_dtype;
 };
-bool gemm_fast_ok(int M, int N, int K, int group);
-void gemm_grid(int M, int N, int* gx, int* gy, int* block);
-hipError_t launch_gemm(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_gemm_simple(const GemmArgs& a, hipStream_t stream);
+
+// GEMM on MFMA: workgroups of BM rows x kGemmTileCols columns x one K segment; several linears
+// (same M and x dtype) can share a launch.
+constexpr int kGemmTileCols = 256;
+constexpr int kPlanCUs = 256;          // CU count plans assume (MI355X), so plans are device-free
+struct GemmLinear {
+    const uint32_t* qweight;   // [K/8, N]
+    const uint32_t* qzeros;    // [K/group, ceil(N/8)] or nullptr (zero 8)
+    const uint16_t* scales;    // [K/group, N] fp16 bits
+    const float* bias;         // [N] or nullptr
+    const void* x;             // [M, K] f32 or f16
+    float* y;                  // [M, N]
+    float* partial;            // [split, M, N] (split > 1)
+    uint32_t* counters;        // per-tile arrival counters (split > 1), zero between launches
+    int N, K, group, split, tiles_n, tiles_m, wg_begin;
+};
+struct GemmBatch {
+    GemmLinear L[kMaxBatch];
+    int count, M, x_dtype, bm, wg_total;
+};
+struct GemmShape {
+    int bm, tiles_n, tiles_m, split;
+};
+bool gemm_fast_ok(int M, int N, int K, int group);
+GemmShape gemm_shape(int M, int N, int K, int group, int cu_count);
+uint64_t gemm_partial_bytes(int M, int N, int split);
+hipError_t launch_gemm_batch(const GemmBatch& b, hipStream_t stream);
 
 // load-time unpack to fp16 [N, K]
 struct UnpackArgs {
