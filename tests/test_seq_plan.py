@@ -65,10 +65,12 @@ def test_tiles_cover_every_column_and_segment():
     x = c.ext(3584)
     c.add(3584, 18944, x)
     info = c.plan(grid=512)
-    # 296 blocks x 28 groups = 8288 block-groups on 512 workgroups: runs of 16-17 groups, so a
-    # block is cut where a run boundary falls inside it (at most 3 parts) and reduced
+    # 296 blocks x 28 groups = 8288 block-groups on 512 workgroups: runs of about 16 groups, so a
+    # block is cut where a run boundary falls inside it (at most 3 parts) and reduced. The
+    # weights (34 MB) fit the MALL, where a tile is priced at a quarter of the mean run (4
+    # block-groups): a run with fewer tiles takes up to that many more groups.
     assert info.total_units == 296 * 28
-    assert info.busiest_units <= 8288 // 512 + 1
+    assert info.busiest_units <= 8288 // 512 + 4
     assert 2 <= info.max_split <= 3
     assert 0 < info.reduces <= 296
     assert info.device_bytes > 0 and info.lds_bytes > 0
@@ -117,9 +119,28 @@ def qwen7b(c: Chain, layers: int, chained: bool, C=3584, I=18944):
 def test_balance_7b_independent(M, grid):
     info = qwen7b(Chain(M=M), 28, chained=False).plan(grid=grid)
     assert info.passes == 1 and info.linears == 140
-    # one pass: every workgroup within one group of the mean
-    assert info.busiest_units <= info.total_units // grid + 1
-    assert info.balance < 1.01
+    if M == 1:
+        # streamed from HBM at M = 1: equal block-groups, every workgroup within one of the mean
+        assert info.busiest_units <= info.total_units // grid + 1
+    else:
+        # M > 1: each tile is priced at 48 block-groups, so runs with fewer tiles carry more
+        assert info.busiest_units <= info.total_units // grid + 2 * 48
+    assert info.balance < 1.07
+
+
+def test_05b_independent_prices_tiles():
+    """The 0.5B step on independent inputs (one pass, 186 MB: MALL-resident). With a tile priced
+    at a quarter of the mean run, workgroups whose runs cross many small linears (q/k/v/o) take
+    fewer block-groups, and runs stay in whole blocks (almost no K splits to reduce)."""
+    c = Chain()
+    for _ in range(24):
+        for K, N in ((896, 896), (896, 128), (896, 128), (896, 896), (896, 4864), (896, 4864), (4864, 896)):
+            c.add(K, N, c.ext(K))
+    info = c.plan()
+    assert info.passes == 1 and info.total_units == 43680
+    mean = info.total_units / info.grid
+    assert mean < info.busiest_units <= mean + 2 * (mean // 4)
+    assert info.tiles <= 420 and info.reduces <= 16
 
 
 def test_balance_7b_chained():

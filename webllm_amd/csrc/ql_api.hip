@@ -862,6 +862,7 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
     a.G = p.grid;
     a.group = descs[0].group;
     a.spin_limit = 1u << 22;
+    a.block_mode = p.block_mode ? 1 : 0;
     fill_seq_info(p, n, lay.total, &q->info);
     *out = q;
     return QL_OK;

@@ -147,6 +147,7 @@ struct SeqArgs {
     uint64_t* part;                 // partial-sum pool: slot s holds [M][64] epoch-tagged words
     int32_t M, G, group;
     uint32_t spin_limit;
+    int32_t block_mode;             // some tile runs in block mode: launch the instance with it
 };
 
 // Host description of one linear of a sequence, for planning.
@@ -160,6 +161,7 @@ struct SeqPlanOut {
     int grid = 0, passes = 0, tiles = 0, reduces = 0, max_split = 1, max_gseg = 0;
     uint64_t slots = 0;             // partial-sum pool slots
     uint64_t total_units = 0, busiest_units = 0;   // block-groups: all, most on one workgroup
+    bool block_mode = false;        // some tile runs in block mode
     uint64_t lds_bytes = 0;
     std::vector<int> pass_of;
     std::vector<SeqTask> tasks;

@@ -47,6 +47,20 @@ namespace {
 //   QL_SEQ_PRO_CHUNKS    8-value input chunks per lane whose loads a tile's prologue issues together
 //   QL_SEQ_SENTINEL      1: a tile first polls one word per 64-value input chunk (wave 0), then
 //                        loads its input; 0: every lane polls its own input words
+//   QL_SEQ_BLOCK_MODE    1: tiles of fewer groups than waves may run in block mode (below)
+//   QL_SEQ_TILE_COST_MALL block-groups a tile's fixed work (prologue, pipeline drain) is priced
+//                        at when a streaming pass whose weights fit the MALL is cut into runs
+//   QL_SEQ_TILE_COST     the same for passes streamed from HBM with M > 1 (M = 1 measured best
+//                        with equal block-groups per run: 0)
+#ifndef QL_SEQ_BLOCK_MODE
+#define QL_SEQ_BLOCK_MODE 1
+#endif
+#ifndef QL_SEQ_TILE_COST_MALL
+#define QL_SEQ_TILE_COST_MALL 64
+#endif
+#ifndef QL_SEQ_TILE_COST
+#define QL_SEQ_TILE_COST 48
+#endif
 #ifndef QL_SEQ_SENTINEL
 #define QL_SEQ_SENTINEL 1
 #endif
@@ -83,6 +97,9 @@ constexpr int kSumBatch = 16;           // partial sums a reduction loads per ro
 // a pass with at least this many weight bytes per workgroup streams from HBM (7B-shaped linears)
 // rather than waiting on latency (0.5B-shaped linears, MALL-resident)
 constexpr uint64_t kStreamBytes = (uint64_t)QL_SEQ_STREAM_KB << 10;
+// weight bytes of a pass that stay resident in MI355X's 256 MB MALL across steps (with room
+// for activations and the exchange buffers)
+constexpr uint64_t kMallBytes = 192ull << 20;
 
 size_t lds_per_group(int M, int group) { return (size_t)(group / 64) * 4 * (4 * M) * 16 + 8 * (size_t)M; }
 
@@ -218,6 +235,15 @@ __device__ bool finish8_ll(const uint64_t* p, uint32_t e, uint64_t w[8], float v
     return true;
 }
 
+// Block mode for a tile of `nblk` blocks over a segment of `gseg` groups on W waves (see the
+// kernel): segments shorter than W groups, when the busiest wave has no more jobs than under the
+// K split plus a quarter job per block for the ring. The planner and the kernel use the same rule.
+__host__ __device__ constexpr bool block_mode_for(int gseg, int nblk, int W)
+{
+    return QL_SEQ_BLOCK_MODE && gseg < W &&
+           4 * ((nblk + W - 1) / W * gseg) <= 4 * (nblk * ((gseg + W - 1) / W)) + nblk;
+}
+
 // One wave's view of a tile for its weight loads: the tile's blocks ct .. ct+nblk-1 and the
 // wave's groups g0 .. g0+wcount-1 of the tile's K segment. Every field is wave-uniform, so
 // selecting one view or another stays scalar.
@@ -226,9 +252,10 @@ struct FetchSrc {
     const uint32_t* qzeros;
     const uint16_t* scales;
     int N, ct, nblk, g0, wcount;
+    int b0, bs;                 // the wave's first block of the tile and its block step
 };
 
-template <int T, int NB, int RG, int kP, int W>
+template <int T, int NB, int RG, int kP, int W, bool BMODE>
 __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
 {
     constexpr int kThreads = 64 * W;
@@ -263,9 +290,18 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
     const int te = ld_const(a.task_begin + wg + 1);
     const int first = ld_const(a.first_tile + wg);
 
-    // the waves split a tile's segment into contiguous parts of floor or ceil(gseg / W) groups:
-    // wave w takes local groups [w*gseg/W, (w+1)*gseg/W), so every wave has loads in flight
+    // Two ways to share a tile among the waves:
+    // * K split: the waves split the segment into contiguous parts of floor or ceil(gseg / W)
+    //   groups (wave w takes local groups [w*gseg/W, (w+1)*gseg/W)) and every block's W partial
+    //   sums meet in the LDS ring;
+    // * block mode: wave w takes blocks w, w + W, ... over the whole segment and stores each
+    //   block's sums itself (no ring, no wave without work while nblk >= W).
+    // Block mode (block_mode_for) serves short segments: K = 896 has 7 groups for 8 waves. On
+    // longer segments the K split measured faster even at equal job counts. Its code is only in
+    // the BMODE instance, which the launcher picks for plans that have such tiles: the extra
+    // registers slow the latency-bound tiles of other plans.
     auto wave_lo = [&](int gseg) { return wave * gseg / W; };
+    auto block_mode = [&](int gseg, int nblk) { return BMODE && block_mode_for(gseg, nblk, W); };
     auto src_of = [&](int ti) {
         // uniform index: the table reads become scalar loads, which the weight prefetch does
         // not have to drain before the fields are used
@@ -276,8 +312,18 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         f.qzeros = uniform_ptr(ld_const(&L->qzeros));
         f.scales = uniform_ptr(ld_const(&L->scales));
         f.N = __builtin_amdgcn_readfirstlane(ld_const(&L->N));
-        f.g0 = t.g0 + wave_lo(t.g1 - t.g0);
-        f.wcount = t.g0 + (wave + 1) * (t.g1 - t.g0) / W - f.g0;
+        const int gseg = t.g1 - t.g0;
+        if (block_mode(gseg, t.nblk)) {
+            f.g0 = t.g0;
+            f.wcount = gseg;
+            f.b0 = wave;
+            f.bs = W;
+        } else {
+            f.g0 = t.g0 + wave_lo(gseg);
+            f.wcount = t.g0 + (wave + 1) * gseg / W - f.g0;
+            f.b0 = 0;
+            f.bs = 1;
+        }
         f.ct = t.ct;
         f.nblk = t.nblk;
         return f;
@@ -303,7 +349,7 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         const char* sc;
         uint32_t gq, gz, gs;               // byte offsets of the cursor's group
         uint32_t Gq, Gz, Gs;               // byte strides from one group to the next
-        int b, gi, wcount, nblk, ct, N;
+        int b, bs, gi, wcount, nblk, ct, N;
         uint32_t lq[2 * NB], lz, ls;       // lane offsets of the cursor's block
     };
     auto set_lanes = [&](Stream& st) {
@@ -331,7 +377,8 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         st.gq = g0 * st.Gq;
         st.gs = g0 * st.Gs;
         st.gz = g0 * st.Gz;
-        st.b = 0;
+        st.b = __builtin_amdgcn_readfirstlane(f.b0);
+        st.bs = __builtin_amdgcn_readfirstlane(f.bs);
         st.gi = 0;
         set_lanes(st);
         return st;
@@ -342,14 +389,14 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             st.gq += st.Gq;
             st.gs += st.Gs;
             st.gz += st.Gz;
-        } else if (st.wcount > 0 && st.b + 1 < st.nblk) {
-            // back to the wave's first group, one block on
+        } else if (st.wcount > 0 && st.b + st.bs < st.nblk) {
+            // back to the wave's first group, on to the wave's next block
             const uint32_t back = (uint32_t)(st.wcount - 1);
             st.gi = 0;
             st.gq -= back * st.Gq;
             st.gs -= back * st.Gs;
             st.gz -= back * st.Gz;
-            st.b++;
+            st.b += st.bs;
             set_lanes(st);
         }
     };
@@ -439,8 +486,11 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
 
         // ---- GEMV tile: blocks ct .. ct + nblk - 1 (64 columns each) over the segment [g0, g1) ----
         const int gseg = task.g1 - task.g0;
-        const int wfirst = wave_lo(gseg);                        // this wave's first group
-        const int wcount = (wave + 1) * gseg / W - wfirst;       // and its number of groups
+        const bool bmode = block_mode(gseg, task.nblk);
+        const int wfirst = bmode ? 0 : wave_lo(gseg);                   // this wave's first group
+        const int wcount = bmode ? gseg : (wave + 1) * gseg / W - wfirst; // and its number of groups
+        // the wave's blocks: all of them (K split) or every W-th from its own index
+        const int nbw = !bmode ? task.nblk : wave < task.nblk ? (task.nblk - 1 - wave) / W + 1 : 0;
         const bool P = L.src >= 0;
         const uint64_t* p_ll = P ? ld_const(&a.lin[L.src].y_ll) : nullptr;
         // this tile's and the next tile's views, read now so that their table loads overlap the
@@ -625,9 +675,38 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             bseq++;
         };
 
+        // block mode: this wave's complete sums of block b, stored directly. Lane (j, kq) holds
+        // columns 4j .. 4j+3 of row 4t + kq; a cross-lane exchange gives lane l column l, so each
+        // row of the block goes out as one 64-lane store like the ring's (a consumer polls one
+        // word per block and expects the others with it).
+        auto store_block = [&](int b) {
+            const int nc = (task.ct + b) * kCols + lane;
+            const int u = lane & 3;
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+#pragma unroll
+                for (int mm = 0; mm < 4; mm++) {
+                    const int m = 4 * t + mm;
+                    if (m >= M) break;
+                    const int src = 16 * mm + (lane >> 2);
+                    const float s0 = __shfl(acc[0][t], src), s1 = __shfl(acc[1][t], src);
+                    const float s2 = __shfl(acc[2][t], src), s3 = __shfl(acc[3][t], src);
+                    float v = u == 0 ? s0 : u == 1 ? s1 : u == 2 ? s2 : s3;
+                    if (nc >= N) continue;
+                    if (task.slot < 0) {
+                        if (L.bias) v += bias_lds[b * kCols + lane];
+                        st_global(L.y + (size_t)m * N + nc, v);
+                        st_ll(L.y_ll + (size_t)m * N + nc, v, e);
+                    } else {
+                        st_ll(a.part + ((size_t)(task.slot + b * task.stride) * M + m) * kCols + lane, v, e);
+                    }
+                }
+            }
+        };
+
         // the wave's job stream over the tile (see the pipeline note above): positions 0..kP-1 are
         // in flight; the last iteration refills from the next tile
-        const int njobs = task.nblk * wcount;
+        const int njobs = nbw * wcount;
         const int njobs_p = njobs > kP ? (njobs + kP - 1) / kP * kP : kP;
         Stream fs = open_stream(cs);
 #pragma unroll
@@ -636,7 +715,10 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         auto consume_job = [&](int d) {
             consume(wfirst + cg, wb[d], zb[d], sb[d]);
             if (++cg == wcount) {
-                publish(cb);
+                if (bmode)
+                    store_block(wave + cb * W);
+                else
+                    publish(cb);
 #pragma unroll
                 for (int u = 0; u < 4; u++)
 #pragma unroll
@@ -664,7 +746,7 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             }
         }
         // a wave without groups in this tile still counts itself in for every block
-        if (wcount == 0)
+        if (!bmode && wcount == 0)
             for (int b = 0; b < task.nblk; b++) publish(b);
         if (!ok) sh_bad = 1;
         // the next tile's prologue rewrites the digits
@@ -680,7 +762,7 @@ struct SeqKernel {
 // Eight waves per workgroup (one workgroup per CU) where two waves per SIMD fit the registers:
 // a single workgroup keeps its waves in step through the per-block barriers, where two
 // co-resident workgroups drift apart (the older one's waves win issue). Otherwise four waves.
-template <int T>
+template <int T, bool BM>
 SeqKernel kernel_for(int nb)
 {
     constexpr int RG = T == 1 ? 4 : 2;      // reduction ring slots (32 KB of LDS with 8 waves)
@@ -688,19 +770,19 @@ SeqKernel kernel_for(int nb)
     constexpr int P = T == 4 ? QL_SEQ_PREFETCH_WIDE : QL_SEQ_PREFETCH;
     constexpr int W = T <= 2 ? QL_SEQ_WAVES : 4;
     switch (nb) {
-    case 1: return {reinterpret_cast<const void*>(&seq_kernel<T, 1, RG, P, W>), 64 * W};
-    case 2: return {reinterpret_cast<const void*>(&seq_kernel<T, 2, RG, P, W>), 64 * W};
-    case 4: return {reinterpret_cast<const void*>(&seq_kernel<T, 4, RG, QL_SEQ_PREFETCH, 4>), 256};
+    case 1: return {reinterpret_cast<const void*>(&seq_kernel<T, 1, RG, P, W, BM>), 64 * W};
+    case 2: return {reinterpret_cast<const void*>(&seq_kernel<T, 2, RG, P, W, BM>), 64 * W};
+    case 4: return {reinterpret_cast<const void*>(&seq_kernel<T, 4, RG, QL_SEQ_PREFETCH, 4, BM>), 256};
     default: return {nullptr, 0};
     }
 }
 
-SeqKernel seq_kernel_for(int M, int group)
+SeqKernel seq_kernel_for(int M, int group, bool bmode = false)
 {
     const int nb = group / 64;
-    if (M <= 4) return kernel_for<1>(nb);
-    if (M <= 8) return kernel_for<2>(nb);
-    return kernel_for<4>(nb);
+    if (M <= 4) return bmode ? kernel_for<1, true>(nb) : kernel_for<1, false>(nb);
+    if (M <= 8) return bmode ? kernel_for<2, true>(nb) : kernel_for<2, false>(nb);
+    return bmode ? kernel_for<4, true>(nb) : kernel_for<4, false>(nb);
 }
 
 }  // namespace
@@ -780,6 +862,72 @@ void cut_runs(const std::vector<Piece>& items, int runs, bool split, std::vector
     }
 }
 
+
+// Split runs priced with a fixed cost per tile: a run costs its block-groups plus `tile_cost`
+// for each tile it starts (a new linear, or a piece of a block cut along K, which is a tile of
+// its own). Finds the smallest cap on a run's cost that a greedy fill of `runs` runs meets
+// (binary search), so workgroups with many small linears get fewer block-groups.
+void cut_runs_priced(const std::vector<Piece>& items, int runs, uint64_t tile_cost,
+                     std::vector<std::vector<Piece>>* out)
+{
+    uint64_t total = 0;
+    for (const Piece& it : items) total += (uint64_t)(it.g1 - it.g0);
+    // short runs: the price stays below a quarter of the mean run, so that runs still get cut
+    // inside blocks rather than leave workgroups without work
+    if (runs > 0) tile_cost = std::min<uint64_t>(tile_cost, total / (uint64_t)runs / 4);
+    if (total == 0 || runs == 0 || tile_cost == 0) {
+        cut_runs(items, runs, true, out);
+        return;
+    }
+    // greedy fill under `cap`; false when it needs more than `runs` runs
+    auto fill = [&](uint64_t cap, std::vector<std::vector<Piece>>* res) {
+        if (res) res->assign(runs, {});
+        int w = 0;
+        uint64_t cost = 0;
+        int prev_lin = -1;
+        bool prev_part = false, empty = true;
+        for (const Piece& it : items) {
+            int g = it.g0;
+            while (g < it.g1) {
+                const int rest = it.g1 - g;
+                const bool part_start = g != it.g0;
+                const bool new_tile = empty || prev_lin != it.lin || prev_part || part_start;
+                const uint64_t nt = new_tile ? tile_cost : 0;
+                if (cost + nt + (uint64_t)rest <= cap) {
+                    if (res) (*res)[w].push_back(Piece{it.lin, it.c, g, it.g1});
+                    cost += nt + (uint64_t)rest;
+                    prev_lin = it.lin;
+                    prev_part = part_start;
+                    empty = false;
+                    g = it.g1;
+                    continue;
+                }
+                // the cap falls inside this piece: take what fits (as a K part, its own tile)
+                const uint64_t room = cap > cost + tile_cost ? cap - cost - tile_cost : 0;
+                if (room > 0) {
+                    const int take = (int)std::min<uint64_t>(room, (uint64_t)rest);
+                    if (res) (*res)[w].push_back(Piece{it.lin, it.c, g, g + take});
+                    g += take;
+                } else if (empty) {
+                    return false;              // not even one group fits: cap too small
+                }
+                if (++w >= runs) return false;
+                cost = 0;
+                empty = true;
+                prev_lin = -1;
+                prev_part = false;
+            }
+        }
+        return true;
+    };
+    uint64_t lo = (total + runs - 1) / runs, hi = total + tile_cost * (uint64_t)(items.size() + 1);
+    while (lo < hi) {
+        const uint64_t mid = lo + (hi - lo) / 2;
+        if (fill(mid, nullptr)) hi = mid;
+        else lo = mid + 1;
+    }
+    fill(lo, out);
+}
 }  // namespace
 
 void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
@@ -874,13 +1022,16 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
                 sets.push_back(small);
             }
             run_pieces.assign(grid, {});
+            // a tile's fixed cost in block-groups: higher where the weights stream from the MALL
+            // (a block-group takes about half the time it takes from HBM)
+            const uint64_t tile_cost = bytes <= kMallBytes ? QL_SEQ_TILE_COST_MALL : M == 1 ? 0 : QL_SEQ_TILE_COST;
             std::vector<std::vector<std::vector<Piece>>> per_set(sets.size());
             for (size_t c = 0; c < sets.size(); c++) {
                 uint64_t u = 0;
                 for (int i : sets[c]) u += units_of(i);
                 std::vector<Piece> items;
                 build_items(sets[c], (double)u / grid, &items);
-                cut_runs(items, grid, true, &per_set[c]);
+                cut_runs_priced(items, grid, tile_cost, &per_set[c]);
             }
             // each run takes the sets in a rotated order, so the chip-wide mix stays even in time
             for (int r = 0; r < grid; r++)
@@ -1050,6 +1201,9 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
     p.task_begin[grid] = (int32_t)p.tasks.size();
     const int group = lin.empty() ? 128 : lin[0].group;
     p.lds_bytes = (uint64_t)std::max(1, p.max_gseg) * lds_per_group(M, group);
+    const int W = seq_kernel_for(M, group).threads / 64;
+    for (const SeqTask& t : p.tasks)
+        if (t.kind == kSeqTile && block_mode_for(t.g1 - t.g0, t.nblk, W)) p.block_mode = true;
 }
 
 std::string verify_seq_plan(const std::vector<SeqSpec>& lin, int M, const SeqPlanOut& p)
@@ -1178,16 +1332,23 @@ std::string verify_seq_plan(const std::vector<SeqSpec>& lin, int M, const SeqPla
 
 hipError_t seq_blocks_per_cu(int M, int group, int* blocks)
 {
-    const SeqKernel k = seq_kernel_for(M, group);
-    if (!k.fn) return hipErrorInvalidValue;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, k.fn, k.threads, lds_budget(M, group));
+    // the smaller occupancy of the two instances (with and without block mode)
+    int b[2] = {0, 0};
+    for (int i = 0; i < 2; i++) {
+        const SeqKernel k = seq_kernel_for(M, group, i == 1);
+        if (!k.fn) return hipErrorInvalidValue;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b[i], k.fn, k.threads, lds_budget(M, group));
+        if (e != hipSuccess) return e;
+    }
+    *blocks = std::min(b[0], b[1]);
+    return hipSuccess;
 }
 
 int seq_wg_per_cu() { return QL_SEQ_WG_PER_CU; }
 
 hipError_t launch_seq(const SeqArgs& a, size_t lds, hipStream_t stream)
 {
-    const SeqKernel k = seq_kernel_for(a.M, a.group);
+    const SeqKernel k = seq_kernel_for(a.M, a.group, a.block_mode != 0);
     if (!k.fn) return hipErrorInvalidValue;
     void* args[] = {const_cast<SeqArgs*>(&a)};
     return hipLaunchKernel(k.fn, dim3(a.G), dim3(k.threads), args, lds, stream);
