@@ -130,6 +130,12 @@ int ql_gptq_check(const ql_gptq_desc* desc, const ql_arena* weights);
  * f32ToF16Bits(dequantizeGptqInt4(...)) (quant.ts:42-118, buffer.ts:57-100). */
 int ql_unpack_f16(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights,
                   ql_arena* out, uint64_t out_off);
+/* many tensors at once (the loader's whole weight set, qwen-loader.ts:146-162 calling
+ * dequantGptqLinear + uploadF16 per linear): tensor i into out_offs[i], same bits as
+ * ql_unpack_f16. Tensors are batched into few launches (up to 32 tensors each); every descriptor
+ * and output range is validated before anything is enqueued. */
+int ql_unpack_f16_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
+                        const ql_arena* weights, ql_arena* out, const uint64_t* out_offs);
 /* fp32 [N,K] row-major, bit-identical to dequantizeGptqInt4(...) itself (quant.ts:42-118) with
  * the scales decoded from fp16 as the loader does (safetensors.ts:180-182, qwen-loader.ts:65).
  * out_off must be 16-byte aligned. */

@@ -133,14 +133,70 @@ def test_unpack_all_168_tensors_05b(ql, ctx, orc):
     out_offs = [olay.take(t.N * t.K * 2) for t in tensors]
     out = ctx.arena(olay.used)
     say(f"unpack 168 tensors: packed {lay.used/1e6:.1f} MB -> fp16 {olay.used/1e6:.1f} MB")
+    descs = []
     for t, (a, b, c), o in zip(tensors, offs, out_offs):
         w.write(a, t.qweight); w.write(b, t.qzeros); w.write(c, t.scales)
-        ctx.unpack_f16(ql.make_desc(a, b, c, t.K, t.N, 128), w, out, o)
+        descs.append(ql.make_desc(a, b, c, t.K, t.N, 128))
+        ctx.unpack_f16(descs[-1], w, out, o)
+    ctx.sync()
+    wants = []
+    for i, (t, o) in enumerate(zip(tensors, out_offs)):
+        got = out.read(o, (t.N, t.K), np.uint16)
+        wants.append(orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, t.K, t.N, 128))
+        assert np.array_equal(got, wants[i]), f"tensor {i} {linears[i]}"
+    # the batched entry point (the loader's whole weight set in six launches) into a cleared arena
+    out.release()
+    out = ctx.arena(olay.used)
+    out.write(0, np.full(olay.used // 2, 0xFFFF, np.uint16))
+    ctx.unpack_f16_batch(descs, w, out, out_offs)
     ctx.sync()
     for i, (t, o) in enumerate(zip(tensors, out_offs)):
         got = out.read(o, (t.N, t.K), np.uint16)
-        want = orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, t.K, t.N, 128)
-        assert np.array_equal(got, want), f"tensor {i} {linears[i]}"
+        assert np.array_equal(got, wants[i]), f"batched: tensor {i} {linears[i]}"
+    out.release()
+    w.release()
+
+
+def test_unpack_batch_mixed_shapes(ql, ctx, orc):
+    """The batched unpack over tensors the tile path takes and tensors it does not (ragged K or N,
+    no qzeros, group 32/64/256, an odd output offset) in one call: each bit-exact, nothing written
+    outside its [N,K] range."""
+    shapes = [  # (K, N, group, no_qzeros, out_misalign)
+        (896, 4864, 128, False, 0), (128, 64, 128, True, 0), (1000, 96, 8, False, 0),
+        (896, 130, 128, False, 0), (256, 4, 32, False, 0), (512, 68, 64, True, 0),
+        (2048, 516, 256, False, 0), (896, 128, 128, False, 2), (24, 12, 8, False, 0),
+    ] * 5   # 45 tensors: more than one launch's worth
+    lay = ql.ArenaLayout()
+    tensors, offs = [], []
+    for i, (K, N, group, noqz, _) in enumerate(shapes):
+        t = synth.gptq_linear(K, N, group, seed=0xB0 + i)
+        tensors.append((t, noqz))
+        offs.append((lay.take(t.qweight.nbytes), None if noqz else lay.take(t.qzeros.nbytes),
+                     lay.take(t.scales.nbytes)))
+    w = ctx.arena(lay.used)
+    olay = ql.ArenaLayout()
+    out_offs = [olay.take(t.N * t.K * 2 + 16) + mis for (t, _), (_, _, _, _, mis) in zip(tensors, shapes)]
+    out = ctx.arena(olay.used)
+    out.write(0, np.full(olay.used // 2, 0xFFFF, np.uint16))
+    descs = []
+    for (t, noqz), (a, b, c) in zip(tensors, offs):
+        w.write(a, t.qweight)
+        if b is not None:
+            w.write(b, t.qzeros)
+        w.write(c, t.scales)
+        descs.append(ql.make_desc(a, b, c, t.K, t.N, t.group))
+    say(f"unpack batch: {len(descs)} tensors, {olay.used/1e6:.1f} MB out")
+    ctx.unpack_f16_batch(descs, w, out, out_offs)
+    ctx.sync()
+    for i, ((t, noqz), o) in enumerate(zip(tensors, out_offs)):
+        got = out.read(o, (t.N, t.K), np.uint16)
+        want = orc.dequantize_gptq_int4_f16(t.qweight, None if noqz else t.qzeros, t.scales, t.K,
+                                            t.N, t.group)
+        assert np.array_equal(got, want), f"tensor {i} {shapes[i]}"
+        tail = out.read(o + t.N * t.K * 2, (8 - (o % 16) // 2,), np.uint16)
+        assert np.all(tail == 0xFFFF), f"tensor {i}: write past its end"
+    out.release()
+    w.release()
 
 
 # ------------------------------------------------------------------------- decode GEMV

@@ -527,6 +527,58 @@ int ql_unpack_f16(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, q
     return QL_OK;
 }
 
+int ql_unpack_f16_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs, const ql_arena* weights,
+                        ql_arena* out, const uint64_t* out_offs)
+{
+    if (!ctx || !out || (count > 0 && (!descs || !out_offs)))
+        return fail(QL_E_INVALID, "null context, output arena, descriptors or offsets");
+    if (count < 0) return fail(QL_E_INVALID, "negative tensor count");
+    // validate everything before any work is enqueued
+    for (int i = 0; i < count; i++) {
+        const ql_gptq_desc* d = &descs[i];
+        int rc = check_desc(d, weights);
+        if (rc) return rc;
+        if (!in_range(out_offs[i], (uint64_t)d->N * d->K * 2, out->size))
+            return fail(QL_E_RANGE, "tensor %d: fp16 [N,K] output outside the arena", i);
+        if (out_offs[i] % 2) return fail(QL_E_ALIGN, "tensor %d: fp16 output offset must be 2-byte aligned", i);
+        if ((d->K + 7) / 8 > 65535) return fail(QL_E_INVALID, "tensor %d: K too large (%d)", i, d->K);
+    }
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    ql::UnpackBatch b{};
+    auto flush = [&]() -> hipError_t {
+        hipError_t e = b.count ? ql::launch_unpack_batch(b, ctx->stream) : hipSuccess;
+        b.count = 0;
+        b.tiles = 0;
+        return e;
+    };
+    for (int i = 0; i < count; i++) {
+        const ql_gptq_desc* d = &descs[i];
+        const bool fast = d->N % 4 == 0 && d->K % 8 == 0 && d->qweight_off % 16 == 0 &&
+                          d->scales_off % 8 == 0 && out_offs[i] % 16 == 0;
+        if (!fast) {
+            // the generic kernel, in order with the batch launches around it
+            if ((rc = ql_unpack_f16(ctx, d, weights, out, out_offs[i]))) return rc;
+            continue;
+        }
+        const int tiles = ql::unpack_tiles(d->N, d->K);
+        if (b.count == ql::kUnpackBatch || (int64_t)b.tiles + tiles > INT32_MAX) QL_HIP(flush());
+        ql::UnpackItem& it = b.it[b.count++];
+        it.qweight = reinterpret_cast<const uint32_t*>(weights->base + d->qweight_off);
+        it.qzeros = d->qzeros_off == QL_NONE ? nullptr
+                                             : reinterpret_cast<const uint32_t*>(weights->base + d->qzeros_off);
+        it.scales = reinterpret_cast<const uint16_t*>(weights->base + d->scales_off);
+        it.out = reinterpret_cast<uint16_t*>(out->base + out_offs[i]);
+        it.N = d->N;
+        it.K = d->K;
+        it.group = d->group;
+        it.tile_begin = b.tiles;
+        b.tiles += tiles;
+    }
+    QL_HIP(flush());
+    return QL_OK;
+}
+
 int ql_unpack_f32(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_arena* out,
                   uint64_t out_off)
 {

@@ -94,6 +94,23 @@ struct UnpackArgs {
     int N, K, group;
 };
 hipError_t launch_unpack(const UnpackArgs& a, bool fast, hipStream_t stream);
+// Batched fp16 unpack: up to kUnpackBatch tensors (each meeting the tile path's conditions: N % 4 == 0,
+// K % 8 == 0, 16-byte aligned qweight and output, 8-byte aligned scales) in one launch.
+constexpr int kUnpackBatch = 32;
+struct UnpackItem {
+    const uint32_t* qweight;
+    const uint32_t* qzeros;    // or nullptr (zero 8)
+    const uint16_t* scales;
+    uint16_t* out;             // fp16 [N, K]
+    int N, K, group;
+    int tile_begin;            // the tensor's first tile in the batch numbering
+};
+struct UnpackBatch {
+    UnpackItem it[kUnpackBatch];
+    int count, tiles;
+};
+int unpack_tiles(int N, int K);    // 16-packed-row x 64-column tiles of one tensor
+hipError_t launch_unpack_batch(const UnpackBatch& b, hipStream_t stream);
 hipError_t launch_unpack_f32(const UnpackArgs& a, hipStream_t stream);
 
 // ----------------------------------------------------------------------------------------------

@@ -66,6 +66,101 @@ __global__ __launch_bounds__(256) void unpack_tile_kernel(UnpackArgs a)
     }
 }
 
+// Many tensors in one launch (the loader's whole weight set): the same 16 x 64 tiles, numbered
+// across the batch; each workgroup walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... and issues
+// the next tile's loads before it transposes the current one through LDS, so every workgroup keeps
+// two tiles of packed words in flight. Every tensor here meets the tile path's conditions.
+struct TileLoad {
+    uint4 w;
+    uint2 sv;
+    uint32_t zw;
+    bool live;
+};
+
+__device__ __forceinline__ int batch_item(const UnpackBatch& b, int tile)
+{
+    int lo = 0, hi = b.count - 1;          // last item whose first tile is <= tile
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (b.it[mid].tile_begin <= tile) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+__device__ __forceinline__ TileLoad load_tile(const UnpackItem& it, int local, int r, int cq)
+{
+    const int tiles_n = (it.N + kTileCols - 1) / kTileCols;
+    const int tp = local / tiles_n;
+    const int p = tp * kTileRows + r;
+    const int n = (local - tp * tiles_n) * kTileCols + 4 * cq;
+    TileLoad l;
+    l.live = p < (it.K >> 3) && n < it.N;
+    l.w = uint4{0u, 0u, 0u, 0u};
+    l.sv = uint2{0u, 0u};
+    l.zw = 0x77777777u;                    // stored 7: zero 8 (no qzeros)
+    if (l.live) {
+        const int g = (p * 8) / it.group;
+        l.w = *reinterpret_cast<const uint4*>(it.qweight + (size_t)p * it.N + n);
+        l.sv = *reinterpret_cast<const uint2*>(it.scales + (size_t)g * it.N + n);
+        if (it.qzeros) l.zw = it.qzeros[(size_t)g * ((it.N + 7) >> 3) + (n >> 3)];
+        l.zw >>= 4 * (n & 7);
+    }
+    return l;
+}
+
+__global__ __launch_bounds__(256) void unpack_batch_kernel(const UnpackBatch b)
+{
+    __shared__ uint4 tile[kTileCols * kPad];
+    const int t = threadIdx.x;
+    const int r = t >> 4;                  // packed row within tile
+    const int cq = t & 15;                 // column quad
+    int cur = blockIdx.x;
+    if (cur >= b.tiles) return;
+    int ci = batch_item(b, cur);
+    TileLoad l = load_tile(b.it[ci], cur - b.it[ci].tile_begin, r, cq);
+    for (;;) {
+        const int nxt = cur + (int)gridDim.x;
+        const int ni = nxt < b.tiles ? batch_item(b, nxt) : ci;
+        TileLoad ln{};
+        if (nxt < b.tiles) ln = load_tile(b.it[ni], nxt - b.it[ni].tile_begin, r, cq);
+
+        const UnpackItem& it = b.it[ci];
+        const int local = cur - it.tile_begin;
+        const int tiles_n = (it.N + kTileCols - 1) / kTileCols;
+        const int tp = local / tiles_n;
+        const int n0 = (local - tp * tiles_n) * kTileCols;
+        const int p0 = tp * kTileRows;
+        const int P = it.K >> 3;
+        if (l.live) {
+            const uint32_t words[4] = {l.w.x, l.w.y, l.w.z, l.w.w};
+            const uint32_t s2[4] = {(l.sv.x & 0xffffu) * 0x10001u, (l.sv.x >> 16) * 0x10001u,
+                                    (l.sv.y & 0xffffu) * 0x10001u, (l.sv.y >> 16) * 0x10001u};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const f16x8 h = dequant_word_natural(words[u], zero_pair(((l.zw >> (4 * u)) & 15u) + 1u), s2[u]);
+                tile[(4 * cq + u) * kPad + r] = __builtin_bit_cast(uint4, h);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = t + 256 * i;     // chunk: column c/16, packed row c%16
+            const int col = c >> 4;
+            const int rr = c & 15;
+            const int nn = n0 + col;
+            const int pp = p0 + rr;
+            if (nn < it.N && pp < P)
+                *reinterpret_cast<uint4*>(it.out + (size_t)nn * it.K + (size_t)pp * 8) = tile[col * kPad + rr];
+        }
+        if (nxt >= b.tiles) break;
+        __syncthreads();                   // the tile is read before the next one overwrites it
+        cur = nxt;
+        ci = ni;
+        l = ln;
+    }
+}
+
 // fp32 [N, K]: exactly dequantizeGptqInt4 (quant.ts:112, (q - zero) * scale with the scale
 // decoded from fp16; the product is exact in fp32). One packed word per lane, 2 x 16-byte stores
 // when the row allows it.
@@ -114,6 +209,17 @@ __global__ __launch_bounds__(256) void unpack_generic_kernel(UnpackArgs a)
 }
 
 }  // namespace
+
+hipError_t launch_unpack_batch(const UnpackBatch& b, hipStream_t stream)
+{
+    // resident workgroups: 8 per CU (17 KB of LDS and 4 waves each), fewer for small batches
+    const int grid = b.tiles < kPlanCUs * 8 ? b.tiles : kPlanCUs * 8;
+    if (grid <= 0) return hipSuccess;
+    hipLaunchKernelGGL(unpack_batch_kernel, dim3(grid), dim3(256), 0, stream, b);
+    return hipGetLastError();
+}
+
+int unpack_tiles(int N, int K) { return ((N + kTileCols - 1) / kTileCols) * (((K >> 3) + kTileRows - 1) / kTileRows); }
 
 hipError_t launch_unpack_f32(const UnpackArgs& a, hipStream_t stream)
 {

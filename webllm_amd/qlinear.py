@@ -110,6 +110,7 @@ def lib():
         "ql_gptq_check": (I, [ctypes.POINTER(GptqDesc), P]),
         "ql_unpack_f16": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64]),
         "ql_unpack_f32": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64]),
+        "ql_unpack_f16_batch": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64)]),
         "ql_plan_linear": (I, [I, I, I, I, ctypes.POINTER(Plan)]),
         "ql_linear": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64, I, I, U64, U64]),
         "ql_plan_batch": (I, [I, ctypes.POINTER(GptqDesc), I, ctypes.POINTER(U64)]),
@@ -302,6 +303,12 @@ class Context:
     def unpack_f16(self, desc: GptqDesc, weights: Arena, out: Arena, out_off: int):
         _check(lib().ql_unpack_f16(self.handle, ctypes.byref(desc), weights.handle, out.handle,
                                    out_off))
+
+    def unpack_f16_batch(self, descs, weights: Arena, out: Arena, out_offs):
+        n = len(descs)
+        arr = (GptqDesc * n)(*descs)
+        offs = (ctypes.c_uint64 * n)(*out_offs)
+        _check(lib().ql_unpack_f16_batch(self.handle, n, arr, weights.handle, out.handle, offs))
 
     def unpack_f32(self, desc: GptqDesc, weights: Arena, out: Arena, out_off: int):
         _check(lib().ql_unpack_f32(self.handle, ctypes.byref(desc), weights.handle, out.handle,
