@@ -85,41 +85,58 @@ class Model:
 
 
 class Step:
-    """One decode (or prefill) step over a Model: launch groups, activations, scratch, graph."""
+    """One decode (or prefill) step over a Model: launch groups, activations, scratch, graph.
 
-    def __init__(self, ctx, model: Model, M: int, x_dtype: int = ql.DTYPE_F32, seed: int = 0x5EED):
+    layered=True issues each layer's linears as the model's dependencies allow (q,k,v | o |
+    gate,up | down: one launch per group, each group on one input). layered=False is the
+    benchmark config as written: every linear on its own input, so any 8 of them can share a
+    launch (ql_linear_batch), 8 consecutive linears per launch."""
+
+    def __init__(self, ctx, model: Model, M: int, x_dtype: int = ql.DTYPE_F32, seed: int = 0x5EED,
+                 layered: bool = True):
         self.ctx, self.model, self.M, self.x_dtype = ctx, model, M, x_dtype
         groups = LAYER_LAUNCHES_05B if model.shape == "0.5b" else LAYER_LAUNCHES_7B
         es = 4 if x_dtype == ql.DTYPE_F32 else 2
         lay = ql.ArenaLayout()
         self.launches = []
-        for layer in range(model.layers):
-            for gi, projs in enumerate(groups):
-                descs = [model.descs[(layer, p)] for p in projs]
-                K = descs[0].K
-                x_off = lay.take(M * K * es)
+        if layered:
+            for layer in range(model.layers):
+                for gi, projs in enumerate(groups):
+                    descs = [model.descs[(layer, p)] for p in projs]
+                    K = descs[0].K
+                    x_off = lay.take(M * K * es)
+                    y_offs = [lay.take(M * d.N * 4) for d in descs]
+                    scratch = ql.plan_batch(descs, M)
+                    s_off = lay.take(max(scratch, 16))
+                    self.launches.append((layer, gi, projs, descs, [x_off] * len(descs), y_offs, s_off))
+        else:
+            keys = [(l, p) for (l, p, _, _) in model.linears]
+            for b0 in range(0, len(keys), 8):
+                part = keys[b0:b0 + 8]
+                descs = [model.descs[k] for k in part]
+                x_offs = [lay.take(M * d.K * es) for d in descs]
                 y_offs = [lay.take(M * d.N * 4) for d in descs]
-                scratch = ql.plan_batch(descs, M)
-                s_off = lay.take(max(scratch, 16))
-                self.launches.append((layer, gi, projs, descs, x_off, y_offs, s_off))
+                s_off = lay.take(max(ql.plan_batch(descs, M), 16))
+                self.launches.append((b0, 0, [p for (_, p) in part], descs, x_offs, y_offs, s_off))
         self.act = ctx.arena(lay.used)
-        for (layer, gi, projs, descs, x_off, _, _) in self.launches:
-            x = synth.activations(M, descs[0].K, seed=seed, key=(layer, gi, M))
-            if x_dtype == ql.DTYPE_F16:
-                x = x.astype(np.float16).view(np.uint16)
-            self.act.write(x_off, x)
+        for (layer, gi, projs, descs, x_offs, _, _) in self.launches:
+            for i, x_off in enumerate(x_offs if not layered else x_offs[:1]):
+                x = synth.activations(M, descs[i].K, seed=seed, key=(layer, gi, M, i))
+                if x_dtype == ql.DTYPE_F16:
+                    x = x.astype(np.float16).view(np.uint16)
+                self.act.write(x_off, x)
         self.bytes = sum(linear_bytes(model.shapes[(l, p)][0], model.shapes[(l, p)][1], M)
                          for (l, p, _, _) in model.linears)
         self.flops = sum(2 * M * K * N for (_, _, K, N) in model.linears)
         self.graph = None
 
     def issue(self):
-        for (_, _, projs, descs, x_off, y_offs, s_off) in self.launches:
+        for (_, _, projs, descs, x_offs, y_offs, s_off) in self.launches:
             if len(descs) == 1:
-                self.ctx.linear(descs[0], self.model.arena, self.act, x_off, self.x_dtype, self.M,
+                self.ctx.linear(descs[0], self.model.arena, self.act, x_offs[0], self.x_dtype, self.M,
                                 y_offs[0], s_off)
             else:
-                self.ctx.linear_batch(descs, self.model.arena, self.act, [x_off] * len(descs),
+                self.ctx.linear_batch(descs, self.model.arena, self.act, x_offs,
                                       self.x_dtype, self.M, y_offs, s_off)
 
     def capture(self):
@@ -462,13 +479,18 @@ def main():
 
     if only in ("all", "prefill"):
         pre = {}
-        for M in (128, 512):
-            st = Step(ctx, m05, M, x_dtype=ql.DTYPE_F16)
-            ms = timed(st, max(5, args.steps // 5), 2)
-            tf = st.flops / (ms * 1e-3) / 1e12
-            pre[str(M)] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 2),
-                           "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4)}
-            st.release()
+        for layered in (False, True):
+            for M in (128, 512):
+                st = Step(ctx, m05, M, x_dtype=ql.DTYPE_F16, layered=layered)
+                ms = timed(st, max(5, args.steps // 5), 2)
+                tf = st.flops / (ms * 1e-3) / 1e12
+                pre[f"{M}{'_layered' if layered else ''}"] = {
+                    "us": round(ms * 1e3, 1), "tflops": round(tf, 2),
+                    "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "launches": len(st.launches)}
+                st.release()
+        pre["note"] = ("M x 168 linears, fp16 x, fp32 y. As written (each linear on its own input): "
+                       "8 linears per launch. _layered: the model's dependency order, one launch per "
+                       "(q,k,v | o | gate,up | down) group (96 launches)")
         extra["prefill05"] = pre
         log(f"prefill: {pre}")
 

@@ -417,6 +417,42 @@ def test_gemm_batch_and_determinism(ql, ctx, orc):
         assert_close(orc, f, _gemm_ref(orc, t, x, b, t.qzeros), GEMM_ATOL, GEMM_RTOL, f"batch N={t.N}")
 
 
+def test_gemm_batch_fills_device_without_split(ql, ctx, orc):
+    """Eight linears on their own f16 inputs in one launch whose tiles together fill the device:
+    no linear splits K (each would alone), every output meets the GEMM bar, and repeats are
+    bit-identical."""
+    K, N, M = 512, 4096, 64
+    assert ql.plan_linear(M, N, K).split > 1
+    ts = [synth.gptq_linear(K, N, 128, seed=0x6E60, key=(i,), stored_zero=None) for i in range(8)]
+    lay = ql.ArenaLayout()
+    descs = []
+    for t in ts:
+        a, z, s_ = lay.take(t.qweight.nbytes), lay.take(t.qzeros.nbytes), lay.take(t.scales.nbytes)
+        descs.append((a, z, s_, t))
+    w = ctx.arena(lay.used)
+    for a, z, s_, t in descs:
+        w.write(a, t.qweight); w.write(z, t.qzeros); w.write(s_, t.scales)
+    descs = [ql.make_desc(a, z, s_, K, N, 128) for a, z, s_, _ in descs]
+    xs = [synth.activations(M, K, seed=0x6E61, key=(i,)) for i in range(8)]
+    alay = ql.ArenaLayout()
+    x_offs = [alay.take(M * K * 2) for _ in ts]
+    y_offs = [alay.take(M * N * 4) for _ in ts]
+    s_off = alay.take(max(ql.plan_batch(descs, M), 16))
+    act = ctx.arena(alay.used)
+    for xo, x in zip(x_offs, xs):
+        act.write(xo, x.astype(np.float16).view(np.uint16))
+    say(f"gemm batch: 8 x (M={M} K={K} N={N}), f16 x")
+    ctx.linear_batch(descs, w, act, x_offs, 1, M, y_offs, s_off)
+    first = [act.read(yo, (M, N), np.float32) for yo in y_offs]
+    ctx.linear_batch(descs, w, act, x_offs, 1, M, y_offs, s_off)
+    for yo, f in zip(y_offs, first):
+        assert np.array_equal(act.read(yo, (M, N), np.float32).view(np.uint32), f.view(np.uint32))
+    for i, (t, x, f) in enumerate(zip(ts, xs, first)):
+        assert_close(orc, f, _gemm_ref(orc, t, x, None, t.qzeros), GEMM_ATOL, GEMM_RTOL, f"batch[{i}]")
+    act.release()
+    w.release()
+
+
 # ------------------------------------------------------------------------- generic paths
 
 def test_simple_paths_reference_kat_shape(ql, ctx, orc):

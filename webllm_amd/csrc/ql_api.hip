@@ -609,9 +609,10 @@ namespace {
 // counter_base (both used only when the linear splits K).
 int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, uint64_t x_off, int M,
                uint64_t y_off, uint64_t scratch_off, uint32_t* counters, int counter_base, int wg_begin,
-               ql::GemmLinear* out)
+               ql::GemmLinear* out, bool no_split = false)
 {
-    const ql::GemmShape s = ql::gemm_shape(M, d->N, d->K, d->group, ql::kPlanCUs);
+    ql::GemmShape s = ql::gemm_shape(M, d->N, d->K, d->group, ql::kPlanCUs);
+    if (no_split) s.split = 1;
     const ql::GemvLinear g = make_linear(d, weights);
     ql::GemmLinear& L = *out;
     L.qweight = g.qweight;
@@ -765,11 +766,20 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
         b.M = M;
         b.x_dtype = x_dtype;
         b.bm = bm;
+        // a K split pays for its partial-sum round trips only when the tiles leave CUs idle; the
+        // batch's tiles together may already fill the device (then no linear splits; the scratch
+        // ql_plan_batch sized per linear is an upper bound)
+        long tiles = 0;
+        for (int i = 0; i < count; i++) {
+            const ql::GemmShape s = ql::gemm_shape(M, descs[i].N, descs[i].K, descs[i].group, ql::kPlanCUs);
+            tiles += (long)s.tiles_n * s.tiles_m;
+        }
+        const bool no_split = tiles * 2 >= ql::kPlanCUs;
         uint64_t off = scratch_off;
         int wg = 0, counter_base = 0;
         for (int i = 0; i < count; i++) {
             if ((rc = gemm_entry(&descs[i], weights, act, x_offs[i], M, y_offs[i], off, ctx->counters,
-                                 counter_base, wg, &b.L[i])))
+                                 counter_base, wg, &b.L[i], no_split)))
                 return rc;
             const ql::GemmLinear& L = b.L[i];
             if (L.split > 1) counter_base += L.tiles_n * L.tiles_m;
