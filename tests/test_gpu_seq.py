@@ -218,3 +218,97 @@ def test_seq_agrees_with_single_linears(ql, ctx, orc):
         ok, max_abs, _ = orc.check_tolerance(y, y1, atol, RTOL)
         assert ok, f"{L['name']}: seq vs ql_linear maxAbs {max_abs:.3e}"
     m.release()
+
+
+class IndependentModel:
+    """Independent 7B-shaped linears (q, o, gate, up, down per layer), each on its own input, in
+    one weight arena: `layers` x 120 MB, so three layers exceed the 256 MB from which an
+    independent sequence at M >= 2 runs as column strips."""
+
+    SHAPES = [(3584, 3584), (3584, 3584), (3584, 18944), (3584, 18944), (18944, 3584)]
+
+    def __init__(self, ql, ctx, layers=3, seed=0x57A):
+        wl = ql.ArenaLayout()
+        self.lin = []
+        for layer in range(layers):
+            for p, (K, N) in enumerate(self.SHAPES):
+                idx = len(self.lin)
+                t = synth.gptq_linear(K, N, 128, seed=seed, key=(layer, p),
+                                      stored_zero=7 if idx % 2 == 0 else None)
+                sym = idx % 3 == 1                         # some without qzeros (zero 8)
+                bias = synth.activations(1, N, seed=seed + 1, key=(idx,))[0] if p == 0 else None
+                self.lin.append({"t": t, "qw": wl.take(t.qweight.nbytes),
+                                 "qz": None if sym else wl.take(t.qzeros.nbytes),
+                                 "sc": wl.take(t.scales.nbytes),
+                                 "b": None if bias is None else wl.take(bias.nbytes),
+                                 "bias": bias, "qzeros": None if sym else t.qzeros})
+        self.weights = ctx.arena(wl.used)
+        for L in self.lin:
+            t = L["t"]
+            self.weights.write(L["qw"], t.qweight)
+            if L["qz"] is not None:
+                self.weights.write(L["qz"], t.qzeros)
+            self.weights.write(L["sc"], t.scales)
+            if L["b"] is not None:
+                self.weights.write(L["b"], L["bias"])
+        self.descs = [ql.make_desc(L["qw"], L["qz"], L["sc"], L["t"].K, L["t"].N, 128, L["b"])
+                      for L in self.lin]
+
+
+@pytest.fixture(scope="module")
+def indep7b(ql, ctx):
+    m = IndependentModel(ql, ctx)
+    yield m
+    m.weights.release()
+
+
+@pytest.mark.parametrize("M", [1, 2, 8, 16])
+def test_strips_7b_independent(ql, ctx, orc, indep7b, M):
+    """Fifteen independent 7B-shaped linears (360 MB, each on its own fp32 input) at M rows run
+    as column strips (no K split, nothing reduced): linears with bias, without qzeros and the
+    18944-deep down projection meet the GEMV bar against the oracle, and repeated runs and
+    graph replays are bit-identical."""
+    m = indep7b
+    al = ql.ArenaLayout()
+    x_offs = [al.take(M * L["t"].K * 4) for L in m.lin]
+    y_offs = [al.take(M * L["t"].N * 4) for L in m.lin]
+    act = ctx.arena(al.used)
+    xs = []
+    for i, (L, xo) in enumerate(zip(m.lin, x_offs)):
+        x = synth.activations(M, L["t"].K, seed=0x57B, key=(M, i))
+        act.write(xo, x)
+        xs.append(x)
+    seq = ctx.seq(m.descs, m.weights, act, x_offs, 0, M, y_offs)
+    info = seq.info
+    say(f"strips 7B x3 M={M}: {info.as_dict()}")
+    assert info.passes == 1 and info.reduces == 0 and info.max_split == 1
+    seq.run()
+    seq.status()
+    ys = [act.read(yo, (M, L["t"].N), np.float32) for L, yo in zip(m.lin, y_offs)]
+    for i in (0, 1, 3, 4, 14):              # q + bias, o without qzeros, up, down, last down
+        L, t = m.lin[i], m.lin[i]["t"]
+        ref = orc.gptq_linear(t.qweight, L["qzeros"], t.scales, xs[i], L["bias"], 128)
+        ok, max_abs, max_rel = orc.check_tolerance(ys[i], ref, 1e-5, RTOL)
+        say(f"  linear {i} K={t.K} N={t.N}: maxAbs {max_abs:.3e} maxRel {max_rel:.3e}")
+        assert ok, f"M={M} linear {i}: maxAbs {max_abs:.3e} maxRel {max_rel:.3e}"
+    for i in range(len(m.lin)):
+        assert np.isfinite(ys[i]).all() and np.abs(ys[i]).max() > 0, f"linear {i} not written"
+    zero = np.zeros((M, m.lin[-1]["t"].N), np.float32)
+    act.write(y_offs[-1], zero)
+    seq.run()
+    seq.status()
+    for L, yo, y in zip(m.lin, y_offs, ys):
+        assert np.array_equal(act.read(yo, (M, L["t"].N), np.float32).view(np.uint32), y.view(np.uint32))
+    ctx.graph_begin()
+    seq.run()
+    g = ctx.graph_end()
+    for r in range(3):
+        act.write(y_offs[-1], zero)
+        g.launch()
+        seq.status()
+        for L, yo, y in zip(m.lin, y_offs, ys):
+            assert np.array_equal(act.read(yo, (M, L["t"].N), np.float32).view(np.uint32),
+                                  y.view(np.uint32)), f"graph replay {r}"
+    g.destroy()
+    seq.destroy()
+    act.release()

@@ -119,13 +119,33 @@ def qwen7b(c: Chain, layers: int, chained: bool, C=3584, I=18944):
 def test_balance_7b_independent(M, grid):
     info = qwen7b(Chain(M=M), 28, chained=False).plan(grid=grid)
     assert info.passes == 1 and info.linears == 140
-    if M == 1:
-        # streamed from HBM at M = 1: equal block-groups, every workgroup within one of the mean
-        assert info.busiest_units <= info.total_units // grid + 1
-    else:
-        # M > 1: each tile is priced at 48 block-groups, so runs with fewer tiles carry more
-        assert info.busiest_units <= info.total_units // grid + 2 * 48
+    # independent and streamed from HBM: column strips of whole K (4 blocks at 16 rows, 8 below),
+    # dealt longest first, with no K split and nothing to reduce
+    strip = 4 if M > 8 else 8
+    per_layer = 2 * (18944 // 64 // strip) + 3 * (3584 // 64 // strip)
+    assert info.tiles == 28 * per_layer
+    assert info.reduces == 0 and info.max_split == 1
+    assert info.busiest_units <= info.total_units // grid + strip * 148
     assert info.balance < 1.07
+
+
+def test_strips_only_for_streamed_independent_rows():
+    """The strip path needs independent linears whose weights stream from HBM; the 0.5B step
+    (186 MB, MALL-resident), a single small linear and any chained sequence keep the
+    dependency-ordered tiles."""
+    info = qwen7b(Chain(M=16), 28, chained=True).plan(grid=256)
+    assert info.passes == 28 * 4 and info.reduces > 0
+    c = Chain(M=4)
+    for _ in range(24):
+        for K, N in ((896, 896), (896, 128), (896, 128), (896, 896), (896, 4864), (896, 4864), (4864, 896)):
+            c.add(K, N, c.ext(K))
+    info = c.plan(grid=256)
+    assert info.passes == 1 and info.tiles != 24 * (2 * (896 // 512) + 2 * (4864 // 512))
+    assert info.max_split > 1                      # tiles split along K: not the strip plan
+    c = Chain(M=1)
+    x = c.ext(3584)
+    c.add(3584, 18944, x)                          # 34 MB: below the streaming threshold
+    assert c.plan(grid=256).max_split > 1
 
 
 def test_05b_independent_prices_tiles():

@@ -42,6 +42,8 @@ struct ql_seq {
     ql::SeqArgs args;
     uint64_t lds;
     ql_seq_info info;
+    bool strips;            // independent linears at M >= 2: the column-strip kernel (sargs)
+    ql::StripArgs sargs;
 };
 
 namespace {
@@ -321,6 +323,49 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
     return L;
 }
 
+// Device tables of a column-strip sequence: linears, strips, per-workgroup strip ranges, and
+// stored-7 qzeros words for linears without qzeros.
+struct StripLayout {
+    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, total;
+};
+
+StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripPlan& p)
+{
+    StripLayout L;
+    uint64_t off = 0;
+    auto take = [&](uint64_t bytes) {
+        const uint64_t o = off;
+        off = align256(off + bytes);
+        return o;
+    };
+    const int n = (int)specs.size();
+    L.lin = take(sizeof(ql::SeqLinear) * n);
+    L.tasks = take(sizeof(ql::StripTask) * std::max<size_t>(1, p.tasks.size()));
+    L.task_begin = take(sizeof(int32_t) * (p.grid + 1));
+    L.sym_words = 0;
+    for (int i = 0; i < n; i++)
+        if (!specs[i].has_qzeros)
+            L.sym_words = std::max<uint64_t>(L.sym_words, (uint64_t)(specs[i].K / specs[i].group) *
+                                                              ((specs[i].N + 7) / 8));
+    L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
+    L.total = off;
+    return L;
+}
+
+void fill_strip_info(const ql::StripPlan& p, int n, uint64_t scratch, ql_seq_info* info)
+{
+    info->linears = n;
+    info->passes = 1;
+    info->tiles = p.strips;
+    info->reduces = 0;
+    info->grid = p.grid;
+    info->max_split = 1;
+    info->lds_bytes = p.lds_bytes;
+    info->device_bytes = scratch;
+    info->total_units = p.total_units;
+    info->busiest_units = p.busiest_units;
+}
+
 void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info* info)
 {
     info->linears = n;
@@ -338,6 +383,62 @@ void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info
 int set_device(ql_ctx* ctx)
 {
     QL_HIP(hipSetDevice(ctx->device));
+    return QL_OK;
+}
+
+// ql_seq_create for independent linears at M >= 2: one workgroup per CU walking its strips.
+int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights, ql_arena* act,
+                 const uint64_t* x_offs, int32_t x_dtype, int32_t M, const uint64_t* y_offs,
+                 const std::vector<ql::SeqSpec>& specs, ql_seq** out)
+{
+    ql::StripPlan sp;
+    ql::plan_strips(specs, M, ctx->cu_count, &sp);
+    const StripLayout lay = strip_layout(specs, sp);
+    char* dev = nullptr;
+    QL_HIP(hipMalloc(&dev, lay.total));
+    std::vector<ql::SeqLinear> lin(n);
+    for (int i = 0; i < n; i++) {
+        const ql_gptq_desc* d = &descs[i];
+        ql::SeqLinear& L = lin[i];
+        const ql::GemvLinear g = make_linear(d, weights);
+        L.qweight = g.qweight;
+        L.qzeros = g.qzeros ? g.qzeros : reinterpret_cast<const uint32_t*>(dev + lay.sym_zeros);
+        L.scales = g.scales;
+        L.bias = g.bias;
+        L.x = act->base + x_offs[i];
+        L.y = reinterpret_cast<float*>(act->base + y_offs[i]);
+        L.y_ll = nullptr;
+        L.src = -1;
+        L.N = d->N;
+        L.K = d->K;
+        L.x_dtype = x_dtype;
+    }
+    hipError_t e = hipMemset(dev, 0, lay.total);
+    if (e == hipSuccess && lay.sym_words)
+        e = hipMemsetD32(reinterpret_cast<hipDeviceptr_t>(dev + lay.sym_zeros), 0x77777777, lay.sym_words);
+    if (e == hipSuccess) e = hipMemcpy(dev + lay.lin, lin.data(), sizeof(ql::SeqLinear) * n, hipMemcpyHostToDevice);
+    if (e == hipSuccess && !sp.tasks.empty())
+        e = hipMemcpy(dev + lay.tasks, sp.tasks.data(), sizeof(ql::StripTask) * sp.tasks.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(dev + lay.task_begin, sp.task_begin.data(), sizeof(int32_t) * sp.task_begin.size(),
+                      hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(e, "ql_seq_create upload");
+    }
+    ql_seq* q = new ql_seq();
+    q->device = ctx->device;
+    q->dev = dev;
+    q->lds = sp.lds_bytes;
+    q->strips = true;
+    q->sargs.lin = reinterpret_cast<const ql::SeqLinear*>(dev + lay.lin);
+    q->sargs.tasks = reinterpret_cast<const ql::StripTask*>(dev + lay.tasks);
+    q->sargs.task_begin = reinterpret_cast<const int32_t*>(dev + lay.task_begin);
+    q->sargs.M = M;
+    q->sargs.G = sp.grid;
+    q->sargs.group = descs[0].group;
+    fill_strip_info(sp, n, lay.total, &q->info);
+    *out = q;
     return QL_OK;
 }
 
@@ -838,6 +939,12 @@ int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
     std::vector<ql::SeqSpec> specs;
     int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, UINT64_MAX, UINT64_MAX, &specs);
     if (rc) return rc;
+    if (ql::strip_eligible(specs, M)) {
+        ql::StripPlan sp;
+        ql::plan_strips(specs, M, grid, &sp);
+        fill_strip_info(sp, n, strip_layout(specs, sp).total, info);
+        return QL_OK;
+    }
     ql::SeqPlanOut p;
     ql::plan_seq(specs, M, grid, &p);
     const std::string bad = ql::verify_seq_plan(specs, M, p);
@@ -859,6 +966,8 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
     int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, weights->size, act->size, &specs);
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
+    if (ql::strip_eligible(specs, M)) return strip_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs,
+                                                          specs, out);
     int per_cu = 0;
     QL_HIP(ql::seq_blocks_per_cu(M, descs[0].group, &per_cu));
     if (per_cu < 1) return fail(QL_E_INVALID, "sequence kernel does not fit on a CU");
@@ -943,7 +1052,8 @@ int ql_seq_run(ql_ctx* ctx, ql_seq* seq)
     if (seq->device != ctx->device) return fail(QL_E_INVALID, "sequence belongs to another device");
     int rc = set_device(ctx);
     if (rc) return rc;
-    QL_HIP(ql::launch_seq(seq->args, seq->lds, ctx->stream));
+    if (seq->strips) QL_HIP(ql::launch_strips(seq->sargs, seq->lds, ctx->stream));
+    else QL_HIP(ql::launch_seq(seq->args, seq->lds, ctx->stream));
     return QL_OK;
 }
 
@@ -954,6 +1064,7 @@ int ql_seq_status(ql_ctx* ctx, ql_seq* seq)
     int rc = set_device(ctx);
     if (rc) return rc;
     QL_HIP(hipStreamSynchronize(ctx->stream));
+    if (seq->strips) return QL_OK;          // no device-side waits: nothing can abort
     uint32_t words[2] = {0, 0};
     QL_HIP(hipMemcpy(words, seq->args.abort, sizeof words, hipMemcpyDeviceToHost));
     if (words[0] == 0 && words[1] == 0) return QL_OK;

@@ -199,4 +199,38 @@ hipError_t seq_blocks_per_cu(int M, int group, int* blocks);
 int seq_wg_per_cu();
 hipError_t launch_seq(const SeqArgs& a, size_t lds, hipStream_t stream);
 
+// ----------------------------------------------------------------------------------------------
+// Column strips: a sequence of independent linears (no linear reads another's output) at M >= 2
+// whose weights stream from HBM, as one persistent launch, each workgroup owning strips of 4 or 8
+// whole 64-column blocks over all of K (no K splits, no partial sums). Groups of 64 or 128,
+// N % 64 == 0.
+constexpr int kStripMinM = 1;           // fewest rows the strip path serves
+constexpr uint64_t kStripMinBytesPerCU = 1ull << 20;   // weight bytes per CU from which it does
+constexpr int kStripChunkGroups = 4;    // quantization groups staged per chunk
+
+struct StripTask {
+    int32_t linear, ct, nblk;  // blocks ct .. ct+nblk-1 of the linear, over all of K
+    int32_t chunks;            // chunks of kStripChunkGroups groups
+};
+
+struct StripArgs {
+    const SeqLinear* lin;      // y_ll unused
+    const StripTask* tasks;
+    const int32_t* task_begin; // [G + 1]
+    int32_t M, G, group;
+};
+
+struct StripPlan {
+    int grid = 0, strips = 0;
+    uint64_t lds_bytes = 0;
+    uint64_t total_units = 0, busiest_units = 0;   // block-groups: all, most on one workgroup
+    std::vector<StripTask> tasks;
+    std::vector<int32_t> task_begin;
+};
+
+bool strip_eligible(const std::vector<SeqSpec>& lin, int M);
+size_t strip_lds(int M, int group);
+void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out);
+hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream);
+
 }  // namespace ql

@@ -1,0 +1,488 @@
+// Column strips: independent decode linears (M = 2..16 rows, each on its own input) in ONE
+// persistent launch, without K splits.
+//
+// A sequence whose linears do not feed each other (the reference's q/k/v or gate/up batches,
+// src/model/qwen.ts:411-413, :464-465, or a whole step of independent linears) is one pass. For
+// M > 1 the activation digits of a quantization group take 2*M KiB of LDS, so a tile of the
+// dependency-ordered sequence kernel covers only a few groups and splits long K into parts whose
+// partial sums cost HBM traffic. Here a workgroup instead owns a strip of whole 64-column blocks
+// over ALL of K:
+// * each consumer wave owns BPW blocks of the strip and keeps their sums in registers;
+// * K is walked in chunks of kCG groups; one producer wave turns the next chunk's activations
+//   into base-256 digits (ql_digits.h) in a double-buffered LDS area while the consumers run the
+//   current chunk, and one barrier per chunk hands the buffers over;
+// * each consumer streams its jobs (one quantization group x its BPW blocks) through a register
+//   ring P jobs deep that runs across chunks, barriers and strips; the producer's loads use its
+//   own wave's counters, so waiting for them never drains the consumers' weight loads;
+// * strips are dealt to workgroups on the host (longest first onto the least loaded), so every
+//   workgroup streams about the same number of weight bytes.
+// Arithmetic is the decode kernels' exact int8-digit MFMA product and fp32 group epilogue, so
+// outputs equal the sequence kernel's bit for bit.
+#include <algorithm>
+#include <functional>
+#include <queue>
+#include <vector>
+
+#include "ql_device.h"
+#include "ql_digits.h"
+#include "ql_internal.h"
+
+namespace ql {
+
+namespace {
+
+constexpr int kCG = kStripChunkGroups;   // quantization groups per chunk
+constexpr int kCols = kSeqTileCols;      // 64 output columns per block
+
+template <typename T>
+__device__ __forceinline__ T ld_table(const T* p)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    // tables are written once before any launch: constant address space, scalar loads
+    return *(const __attribute__((address_space(4))) T*)(reinterpret_cast<uintptr_t>(p));
+#else
+    return *p;
+#endif
+}
+
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <typename T>
+__device__ __forceinline__ const T* uni_ptr(const T* p)
+{
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<const T*>((hi << 32) | lo);
+}
+
+// LDS bytes of one chunk buffer: digits [group][k block][k quarter][digit row] (16 B each), then
+// {2^-E, sum x} per (group, row)
+__host__ __device__ constexpr size_t strip_buf_bytes(int M, int NB)
+{
+    return (size_t)kCG * NB * 4 * (4 * M) * 16 + (size_t)kCG * M * 8;
+}
+
+constexpr int kMaxStripBlocks = 8;       // most blocks in one strip
+
+// T: 16-row MFMA tiles of digit rows (4 per activation row); NB: 64-k blocks per group;
+// W: consumer waves; BPW: blocks per consumer wave; P: jobs in flight per consumer.
+template <int T, int NB, int W, int BPW, int P>
+__global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
+{
+    extern __shared__ uint4 dyn_lds[];
+    constexpr int GK = NB * 64;              // k per group
+    constexpr int CPG = NB * 8;              // producer lanes per (group, row)
+    const int M = a.M;
+    const int R = 4 * M;
+    const int lane = threadIdx.x & 63;
+    const int wave = uni(threadIdx.x >> 6);
+    const int j = lane & 15;
+    const int kq = lane >> 4;
+    const int wg = blockIdx.x;
+    const int tb = ld_table(a.task_begin + wg);
+    const int te = ld_table(a.task_begin + wg + 1);
+    const size_t buf_bytes = strip_buf_bytes(M, NB);
+    auto digits = [&](int buf) { return reinterpret_cast<uint4*>(reinterpret_cast<char*>(dyn_lds) + buf * buf_bytes); };
+    auto gstat = [&](int buf) {
+        return reinterpret_cast<float2*>(reinterpret_cast<char*>(dyn_lds) + buf * buf_bytes + (size_t)kCG * NB * 4 * R * 16);
+    };
+    // the bias of a strip's columns, staged by the producer with the strip's first chunk; two
+    // buffers by strip parity (a strip's outputs are stored before the barrier that ends it, and
+    // the producer refills a buffer two strips later)
+    auto bias_lds = [&](int par) {
+        return reinterpret_cast<float*>(reinterpret_cast<char*>(dyn_lds) + 2 * buf_bytes) + par * (kMaxStripBlocks * kCols);
+    };
+
+    if (wave == W) {
+        // ---- producer: chunk after chunk, the activation digits of the whole task list ----
+        int buf = 0;
+        for (int ti = tb; ti < te; ti++) {
+            const StripTask t = ld_table(a.tasks + ti);
+            const SeqLinear* L = a.lin + t.linear;
+            const void* x = uni_ptr(ld_table(&L->x));
+            const int K = ld_table(&L->K);
+            const int xdt = ld_table(&L->x_dtype);
+            const int groups = K / GK;
+            {
+                const float* bias = ld_table(&L->bias);
+                float* bl = bias_lds((ti - tb) & 1);
+                for (int i = lane; i < t.nblk * kCols; i += 64) bl[i] = bias ? bias[t.ct * kCols + i] : 0.f;
+            }
+            for (int ch = 0; ch * kCG < groups; ch++) {
+                const int g0 = ch * kCG;
+                const int cgc = min(kCG, groups - g0);
+                uint4* xd = digits(buf);
+                float2* gst = gstat(buf);
+                const int items = cgc * M * CPG;      // lanes' worth of 8 activations
+                constexpr int H = kCG * 4 * T * CPG / 64;   // most items per lane (M <= 4T)
+                float v[H][8];
+#pragma unroll
+                for (int h = 0; h < H; h++) {
+                    const int idx = lane + 64 * h;
+                    if (idx < items) {
+                        const int item = idx / CPG, c = idx - item * CPG;
+                        const int gg = item / M, m = item - gg * M;
+                        load8(x, xdt, (size_t)m * K + (size_t)(g0 + gg) * GK + (size_t)c * 8, v[h]);
+                    }
+                }
+#pragma unroll
+                for (int h = 0; h < H; h++) {
+                    const int idx = lane + 64 * h;
+                    if (idx < items) {                // whole CPG-lane groups: CPG divides 64
+                        const int item = idx / CPG, c = idx - item * CPG;
+                        const int gg = item / M, m = item - gg * M;
+                        const int blk = gg * NB + (c >> 3);
+                        uint2* rows = reinterpret_cast<uint2*>(&xd[(blk * 4 + ((c & 7) >> 1)) * R + 4 * m]) + (c & 1);
+                        const float2 st = prep_chunk<CPG>(v[h], rows, 2);
+                        if (c == 0) gst[gg * M + m] = st;
+                    }
+                }
+                // barrier k: chunk k is staged, and the consumers have finished chunk k - 1,
+                // whose buffer chunk k + 1 reuses
+                __syncthreads();
+                buf ^= 1;
+            }
+        }
+        // the consumers' last chunk ends with one more barrier
+        if (te > tb) __syncthreads();
+        return;
+    }
+
+    // ---- consumers ----
+    // job stream: per task with blocks for this wave, per chunk, groups g0 .. g0+cgc-1, padded to
+    // a multiple of P positions (padding re-reads the last job and is never consumed)
+    uint4 wb[P][BPW][2 * NB];
+    uint32_t zb[P][BPW];
+    uint2 sb[P][BPW];
+    struct Cur {
+        int ti, ch, nch, pos, pad, cgc, g, nbw, ngroups;
+        const char* qw;
+        const char* qz;
+        const char* sc;
+        uint32_t Gq, Gz, Gs;        // bytes from one group to the next
+        uint32_t cq, cz, cs;        // byte offsets of the wave's first block
+        uint32_t lq[2 * NB], lz, ls;
+    };
+    auto blocks_of = [&](const StripTask& t) { return max(0, min(BPW, t.nblk - wave * BPW)); };
+    auto open = [&](Cur& c, int ti) {
+        // the first task at or after ti with blocks for this wave (or ti = te: the stream ended)
+        for (; ti < te; ti++) {
+            const StripTask t = ld_table(a.tasks + ti);
+            if (blocks_of(t) > 0) break;
+        }
+        if (ti >= te) return false;
+        const StripTask t = ld_table(a.tasks + ti);
+        const SeqLinear* L = a.lin + t.linear;
+        c.ti = ti;
+        c.nbw = uni(blocks_of(t));
+        c.qw = reinterpret_cast<const char*>(uni_ptr(ld_table(&L->qweight)));
+        c.qz = reinterpret_cast<const char*>(uni_ptr(ld_table(&L->qzeros)));
+        c.sc = reinterpret_cast<const char*>(uni_ptr(ld_table(&L->scales)));
+        const int N = uni(ld_table(&L->N));
+        const int K = uni(ld_table(&L->K));
+        c.ngroups = K / GK;
+        c.nch = (c.ngroups + kCG - 1) / kCG;
+        c.ch = 0;
+        c.pos = 0;
+        c.g = 0;
+        c.cgc = min(kCG, c.ngroups);
+        c.pad = (c.cgc + P - 1) / P * P;
+        c.Gq = (uint32_t)(NB * 8) * (uint32_t)N * 4u;
+        c.Gs = (uint32_t)N * 2u;
+        c.Gz = (((uint32_t)N + 7u) >> 3) * 4u;
+        const uint32_t blk0 = (uint32_t)(t.ct + wave * BPW);
+        c.cq = blk0 * (uint32_t)kCols * 4u;
+        c.cs = blk0 * (uint32_t)kCols * 2u;
+        c.cz = blk0 * (uint32_t)(kCols / 8) * 4u;
+#pragma unroll
+        for (int r = 0; r < 2 * NB; r++)
+            c.lq[r] = ((uint32_t)(2 * kq + (r >> 1) * 8 + (r & 1)) * (uint32_t)N + 4u * (uint32_t)j) * 4u;
+        c.ls = 8u * (uint32_t)j;
+        c.lz = (uint32_t)(j >> 1) * 4u;
+        return true;
+    };
+    auto advance = [&](Cur& c) {
+        if (c.pos + 1 < c.pad) {
+            c.pos++;
+            if (c.pos < c.cgc) c.g++;
+        } else if (c.ch + 1 < c.nch) {
+            c.ch++;
+            c.pos = 0;
+            c.g = c.ch * kCG;
+            c.cgc = min(kCG, c.ngroups - c.g);
+            c.pad = (c.cgc + P - 1) / P * P;
+        } else {
+            Cur n = c;
+            if (open(n, c.ti + 1)) c = n;   // else the stream has ended: stay on the last job
+        }
+    };
+    auto fetch = [&](int d, const Cur& c) {
+        const uint32_t g = (uint32_t)c.g;
+#pragma unroll
+        for (int b = 0; b < BPW; b++) {
+            const uint32_t bb = (uint32_t)min(b, c.nbw - 1);   // extra blocks re-read the last one
+            const char* q = c.qw + g * c.Gq + c.cq + bb * (uint32_t)kCols * 4u;
+#pragma unroll
+            for (int r = 0; r < 2 * NB; r++)
+                wb[d][b][r] = __builtin_bit_cast(uint4, ld_global(reinterpret_cast<const u32x4*>(q + c.lq[r])));
+            zb[d][b] = ld_global(reinterpret_cast<const uint32_t*>(c.qz + g * c.Gz + c.cz + bb * (uint32_t)(kCols / 8) * 4u + c.lz));
+            sb[d][b] = __builtin_bit_cast(uint2, ld_global(reinterpret_cast<const u32x2*>(c.sc + g * c.Gs + c.cs + bb * (uint32_t)kCols * 2u + c.ls)));
+        }
+    };
+
+    // A padding slot is never consumed; without a use its registers would be free to reuse on
+    // that path, and reusing a load's destination waits for every load in flight.
+    auto touch_block = [&](int d, int b) {
+#pragma unroll
+        for (int r = 0; r < 2 * NB; r++) asm volatile("" ::"v"(wb[d][b][r].x), "v"(wb[d][b][r].y), "v"(wb[d][b][r].z), "v"(wb[d][b][r].w));
+        asm volatile("" ::"v"(zb[d][b]), "v"(sb[d][b].x), "v"(sb[d][b].y));
+    };
+    auto touch = [&](int d) {
+#pragma unroll
+        for (int b = 0; b < BPW; b++) touch_block(d, b);
+    };
+
+    Cur fc;
+    const bool any = open(fc, tb);
+    if (any) {
+#pragma unroll
+        for (int d = 0; d < P; d++) {
+            fetch(d, fc);
+            advance(fc);
+        }
+    }
+
+    float acc[BPW][4][T];
+    auto clear = [&]() {
+#pragma unroll
+        for (int b = 0; b < BPW; b++)
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int t = 0; t < T; t++) acc[b][u][t] = 0.f;
+    };
+    clear();
+
+    // one job: local group gg of the chunk in buffer `buf`, the wave's nbw blocks
+    auto consume = [&](int d, int buf, int gg, int nbw) {
+        const uint4* xd = digits(buf);
+        const float2* gst = gstat(buf);
+        i32x4 av[NB][T];
+#pragma unroll
+        for (int bb = 0; bb < NB; bb++)
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                const int row = 16 * t + j;
+                av[bb][t] = row < R ? __builtin_bit_cast(i32x4, xd[((gg * NB + bb) * 4 + kq) * R + row])
+                                    : i32x4{0, 0, 0, 0};
+            }
+        float2 st[T];
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const int m = 4 * t + kq;
+            st[t] = m < M ? gst[gg * M + m] : float2{0.f, 0.f};
+            st[t].x *= 0x1p-8f;       // the digit pairs below carry a factor 2^8
+        }
+#pragma unroll
+        for (int b = 0; b < BPW; b++) {
+            // consume() runs only for tasks with blocks for this wave: block 0 always counts
+            if (b > 0 && b >= nbw) {
+                touch_block(d, b);
+                continue;
+            }
+            i32x4 c[4][T];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int t = 0; t < T; t++) c[u][t] = i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int bb = 0; bb < NB; bb++) {
+                const uint4 w0 = wb[d][b][2 * bb], w1 = wb[d][b][2 * bb + 1];
+                const uint32_t lo[4] = {w0.x, w0.y, w0.z, w0.w};
+                const uint32_t hi[4] = {w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const i32x4 bq = i32x4{(int)(lo[u] & 0x0F0F0F0Fu), (int)((lo[u] >> 4) & 0x0F0F0F0Fu),
+                                           (int)(hi[u] & 0x0F0F0F0Fu), (int)((hi[u] >> 4) & 0x0F0F0F0Fu)};
+#pragma unroll
+                    for (int t = 0; t < T; t++) c[u][t] = mfma_i8(av[bb][t], bq, c[u][t]);
+                }
+            }
+            const uint32_t zw = zb[d][b] >> (4 * ((4 * j) & 7));
+            const uint2 sv = sb[d][b];
+            const uint32_t sw[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
+                const float sz = s * (float)(((zw >> (4 * u)) & 15u) + 1u);
+#pragma unroll
+                for (int t = 0; t < T; t++) {
+                    // digit products (|c| < 2^18, digit 3 most significant) in two exact integer
+                    // pairs: 2^8 * sum_d c_d 2^(8d-24) = (c0 + 2^8 c1) 2^-16 + (c2 + 2^8 c3)
+                    const int lo2 = c[u][t][0] + c[u][t][1] * 256;
+                    const int hi2 = c[u][t][2] + c[u][t][3] * 256;
+                    const float v = fmaf((float)lo2, 0x1p-16f, (float)hi2);
+                    acc[b][u][t] = fmaf(s * st[t].x, v, acc[b][u][t]);
+                    acc[b][u][t] = fmaf(-sz, st[t].y, acc[b][u][t]);
+                }
+            }
+        }
+    };
+
+    if (te > tb) __syncthreads();          // the first chunk is staged (the producer skips
+                                           // every barrier of a workgroup without strips)
+    int buf = 0;
+    for (int ti = tb; ti < te; ti++) {
+        const StripTask t = ld_table(a.tasks + ti);
+        const SeqLinear* L = a.lin + t.linear;
+        const int K = ld_table(&L->K);
+        const int groups = K / GK;
+        const int nbw = blocks_of(t);
+        const int nch = (groups + kCG - 1) / kCG;
+        for (int ch = 0; ch < nch; ch++) {
+            const int cgc = min(kCG, groups - ch * kCG);
+            const int njobs = nbw > 0 ? cgc : 0;
+            const int pad = (njobs + P - 1) / P * P;
+            for (int k = 0; k < pad; k += P) {
+#pragma unroll
+                for (int d = 0; d < P; d++) {
+                    if (k + d < njobs) consume(d, buf, k + d, nbw);
+                    else touch(d);
+                    fetch(d, fc);
+                    advance(fc);
+                }
+            }
+            if (ch + 1 == nch && nbw > 0) {
+                // the strip's outputs (bias from LDS: no global load on this path)
+                const int N = ld_table(&L->N);
+                float* y = ld_table(&L->y);
+                const float* bl = bias_lds((ti - tb) & 1);
+#pragma unroll
+                for (int b = 0; b < BPW; b++) {
+                    if (b > 0 && b >= nbw) break;
+                    const int bc = (wave * BPW + b) * kCols + 4 * j;       // column within the strip
+                    const int col = t.ct * kCols + bc;
+                    const f32x4 bv = *reinterpret_cast<const f32x4*>(bl + bc);
+#pragma unroll
+                    for (int tt = 0; tt < T; tt++) {
+                        const int m = 4 * tt + kq;
+                        if (m < M)
+                            st_global(reinterpret_cast<f32x4*>(y + (size_t)m * N + col),
+                                      f32x4{acc[b][0][tt] + bv.x, acc[b][1][tt] + bv.y, acc[b][2][tt] + bv.z,
+                                            acc[b][3][tt] + bv.w});
+                    }
+                }
+            }
+            // the producer has staged the next chunk into the other buffer
+            __syncthreads();
+            buf ^= 1;
+        }
+        clear();
+    }
+}
+
+struct StripKernel {
+    const void* fn;
+    int threads;
+};
+
+// Eight consumers of one block each for M <= 8; four for M 9..16, whose registers (with the
+// producer sharing a SIMD, 256 per wave) leave room for one block each.
+template <int NB>
+StripKernel strip_kernel_for_nb(int M)
+{
+    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, 2>), 64 * 9};
+    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, 2>), 64 * 9};
+    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, 4, 1, 2>), 64 * 5};
+}
+
+StripKernel strip_kernel_for(int M, int group)
+{
+    if (group == 64) return strip_kernel_for_nb<1>(M);
+    if (group == 128) return strip_kernel_for_nb<2>(M);
+    return {nullptr, 0};
+}
+
+// blocks per strip: consumer waves x blocks per wave (8 x 1, or 4 x 1 for M > 8)
+int strip_blocks(int M) { return M > 8 ? 4 : 8; }
+
+}  // namespace
+
+bool strip_eligible(const std::vector<SeqSpec>& lin, int M)
+{
+    if (M < kStripMinM || M > kGemvMaxM || lin.empty()) return false;
+    uint64_t bytes = 0;
+    for (const SeqSpec& s : lin) {
+        if (s.src >= 0 || s.N % kCols != 0 || (s.group != 64 && s.group != 128) || s.group != lin[0].group ||
+            s.K % s.group != 0)
+            return false;
+        bytes += s.weight_bytes;
+    }
+    // streamed from HBM: strips of whole K balance well only when every CU gets many of them
+    // (a MALL-resident step is latency-bound and keeps the dependency-ordered tiles)
+    return bytes >= kStripMinBytesPerCU * (uint64_t)kPlanCUs;
+}
+
+size_t strip_lds(int M, int group)
+{
+    return 2 * strip_buf_bytes(M, group / 64) + 2 * kMaxStripBlocks * kCols * sizeof(float);
+}
+
+void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+{
+    StripPlan& p = *out;
+    p = StripPlan{};
+    p.grid = grid;
+    const int SB = strip_blocks(M);
+    struct Item {
+        StripTask t;
+        uint64_t cost;
+    };
+    std::vector<Item> items;
+    for (int i = 0; i < (int)lin.size(); i++) {
+        const int ct = lin[i].N / kCols;
+        const int groups = lin[i].K / lin[i].group;
+        const int chunks = (groups + kCG - 1) / kCG;
+        for (int c = 0; c < ct; c += SB) {
+            const int nb = std::min(SB, ct - c);
+            // weight bytes in block-groups, plus a chunk of a full strip for the pipeline's start
+            items.push_back(Item{StripTask{i, c, nb, chunks}, (uint64_t)nb * groups + (uint64_t)kCG * SB});
+            p.total_units += (uint64_t)nb * groups;
+        }
+    }
+    // longest first onto the least loaded workgroup
+    std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
+    std::vector<std::vector<StripTask>> per(grid);
+    std::vector<uint64_t> load(grid, 0), units(grid, 0);
+    typedef std::pair<uint64_t, int> Slot;
+    std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>> q;
+    for (int w = 0; w < grid; w++) q.push({0, w});
+    for (const Item& it : items) {
+        const Slot s = q.top();
+        q.pop();
+        per[s.second].push_back(it.t);
+        load[s.second] = s.first + it.cost;
+        units[s.second] += (uint64_t)it.t.nblk * (lin[it.t.linear].K / lin[it.t.linear].group);
+        q.push({load[s.second], s.second});
+    }
+    p.task_begin.assign(grid + 1, 0);
+    for (int w = 0; w < grid; w++) {
+        p.task_begin[w] = (int32_t)p.tasks.size();
+        p.tasks.insert(p.tasks.end(), per[w].begin(), per[w].end());
+        p.busiest_units = std::max(p.busiest_units, units[w]);
+    }
+    p.task_begin[grid] = (int32_t)p.tasks.size();
+    p.strips = (int)items.size();
+    p.lds_bytes = lin.empty() ? 0 : strip_lds(M, lin[0].group);
+}
+
+hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream)
+{
+    const StripKernel k = strip_kernel_for(a.M, a.group);
+    if (!k.fn) return hipErrorInvalidValue;
+    void* args[] = {const_cast<StripArgs*>(&a)};
+    return hipLaunchKernel(k.fn, dim3(a.G), dim3(k.threads), args, lds, stream);
+}
+
+}  // namespace ql
