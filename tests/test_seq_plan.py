@@ -119,9 +119,9 @@ def qwen7b(c: Chain, layers: int, chained: bool, C=3584, I=18944):
 def test_balance_7b_independent(M, grid):
     info = qwen7b(Chain(M=M), 28, chained=False).plan(grid=grid)
     assert info.passes == 1 and info.linears == 140
-    # independent and streamed from HBM: column strips of whole K (4 blocks at 16 rows, 8 below),
-    # dealt longest first, with no K split and nothing to reduce
-    strip = 4 if M > 8 else 8
+    # independent and streamed from HBM: column strips of 8 whole blocks over all of K, dealt
+    # longest first, with no K split and nothing to reduce
+    strip = 8
     per_layer = 2 * (18944 // 64 // strip) + 3 * (3584 // 64 // strip)
     assert info.tiles == 28 * per_layer
     assert info.reduces == 0 and info.max_split == 1

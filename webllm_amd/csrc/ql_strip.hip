@@ -66,13 +66,28 @@ __host__ __device__ constexpr size_t strip_buf_bytes(int M, int NB)
 constexpr int kMaxStripBlocks = 8;       // most blocks in one strip
 
 // T: 16-row MFMA tiles of digit rows (4 per activation row); NB: 64-k blocks per group;
-// W: consumer waves; BPW: blocks per consumer wave; P: jobs in flight per consumer.
+// W: waves; BPW: blocks per wave; P: jobs in flight per wave.
+//
+// Every chunk runs the same fixed sequence, so the number of loads between any two points is
+// known when the kernel is compiled and every wait names exactly the loads it needs:
+//   1. issue the next chunk's activation loads (this wave's share) and a bias load;
+//   2. kCG job positions (a job: one group x the wave's blocks; positions past the chunk's groups,
+//      or of a wave without blocks, are padding whose loads are never consumed), each consuming
+//      its ring slot and refilling it P positions ahead;
+//   3. after the strip's last chunk, store the strip's outputs;
+//   4. wait for step 1's loads (the kCG positions' loads stay in flight), turn them into digits
+//      in the other LDS buffer, stage the next strip's bias with its first chunk;
+//   5. one barrier.
 template <int T, int NB, int W, int BPW, int P>
-__global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
+__global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
 {
+    static_assert(kCG % P == 0, "a chunk's positions fill whole ring rounds");
     extern __shared__ uint4 dyn_lds[];
     constexpr int GK = NB * 64;              // k per group
-    constexpr int CPG = NB * 8;              // producer lanes per (group, row)
+    constexpr int CPG = NB * 8;              // lanes per (group, row) when staging
+    constexpr int kThreads = 64 * W;
+    // most 8-activation items one thread stages per chunk (M <= 4T)
+    constexpr int H = (kCG * 4 * T * CPG + kThreads - 1) / kThreads;
     const int M = a.M;
     const int R = 4 * M;
     const int lane = threadIdx.x & 63;
@@ -82,81 +97,128 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
     const int wg = blockIdx.x;
     const int tb = ld_table(a.task_begin + wg);
     const int te = ld_table(a.task_begin + wg + 1);
+    if (tb >= te) return;
     const size_t buf_bytes = strip_buf_bytes(M, NB);
     auto digits = [&](int buf) { return reinterpret_cast<uint4*>(reinterpret_cast<char*>(dyn_lds) + buf * buf_bytes); };
     auto gstat = [&](int buf) {
         return reinterpret_cast<float2*>(reinterpret_cast<char*>(dyn_lds) + buf * buf_bytes + (size_t)kCG * NB * 4 * R * 16);
     };
-    // the bias of a strip's columns, staged by the producer with the strip's first chunk; two
-    // buffers by strip parity (a strip's outputs are stored before the barrier that ends it, and
-    // the producer refills a buffer two strips later)
+    // the bias of a strip's columns, staged with the strip's first chunk; two buffers by strip
+    // parity (a strip's outputs are stored before the barrier that ends it)
     auto bias_lds = [&](int par) {
         return reinterpret_cast<float*>(reinterpret_cast<char*>(dyn_lds) + 2 * buf_bytes) + par * (kMaxStripBlocks * kCols);
     };
 
-    if (wave == W) {
-        // ---- producer: chunk after chunk, the activation digits of the whole task list ----
-        int buf = 0;
-        for (int ti = tb; ti < te; ti++) {
-            const StripTask t = ld_table(a.tasks + ti);
-            const SeqLinear* L = a.lin + t.linear;
-            const void* x = uni_ptr(ld_table(&L->x));
-            const int K = ld_table(&L->K);
-            const int xdt = ld_table(&L->x_dtype);
-            const int groups = K / GK;
-            {
-                const float* bias = ld_table(&L->bias);
-                float* bl = bias_lds((ti - tb) & 1);
-                for (int i = lane; i < t.nblk * kCols; i += 64) bl[i] = bias ? bias[t.ct * kCols + i] : 0.f;
-            }
-            for (int ch = 0; ch * kCG < groups; ch++) {
-                const int g0 = ch * kCG;
-                const int cgc = min(kCG, groups - g0);
-                uint4* xd = digits(buf);
-                float2* gst = gstat(buf);
-                const int items = cgc * M * CPG;      // lanes' worth of 8 activations
-                constexpr int H = kCG * 4 * T * CPG / 64;   // most items per lane (M <= 4T)
-                float v[H][8];
+    // ---- staging cursor: the chunk being staged (task si, chunk sch) ----
+    struct Stage {
+        int si, sch, ngroups;
+        const void* x;
+        const float* bias;       // the task's bias, or any valid float pointer when it has none
+        int K, xdt, ct, nblk, has_bias;
+    };
+    auto stage_open = [&](Stage& st, int ti) {
+        const StripTask t = ld_table(a.tasks + ti);
+        const SeqLinear* L = a.lin + t.linear;
+        st.si = ti;
+        st.sch = 0;
+        st.x = uni_ptr(ld_table(&L->x));
+        const float* b = ld_table(&L->bias);
+        st.has_bias = b != nullptr;
+        st.bias = uni_ptr(b ? b : static_cast<const float*>(st.x));
+        st.K = ld_table(&L->K);
+        st.xdt = ld_table(&L->x_dtype);
+        st.ngroups = st.K / GK;
+        st.ct = t.ct;
+        st.nblk = t.nblk;
+    };
+    u32x4 xr[H][2];                          // raw activation bits: f32 (both) or f16 ([0])
+    constexpr int BV = kMaxStripBlocks * kCols / kThreads;   // bias values staged per thread
+    static_assert(BV * kThreads == kMaxStripBlocks * kCols, "threads divide a strip's columns");
+    float bv[BV];
+    // step 1: unconditional loads (threads past the chunk's items re-read its last item); the
+    // raw bits are converted only in step 4, so nothing waits for them here
+    auto stage_issue = [&](const Stage& st) {
+        const int g0 = st.sch * kCG;
+        const int cgc = min(kCG, st.ngroups - g0);
+        const int items = cgc * M * CPG;
 #pragma unroll
-                for (int h = 0; h < H; h++) {
-                    const int idx = lane + 64 * h;
-                    if (idx < items) {
-                        const int item = idx / CPG, c = idx - item * CPG;
-                        const int gg = item / M, m = item - gg * M;
-                        load8(x, xdt, (size_t)m * K + (size_t)(g0 + gg) * GK + (size_t)c * 8, v[h]);
-                    }
-                }
-#pragma unroll
-                for (int h = 0; h < H; h++) {
-                    const int idx = lane + 64 * h;
-                    if (idx < items) {                // whole CPG-lane groups: CPG divides 64
-                        const int item = idx / CPG, c = idx - item * CPG;
-                        const int gg = item / M, m = item - gg * M;
-                        const int blk = gg * NB + (c >> 3);
-                        uint2* rows = reinterpret_cast<uint2*>(&xd[(blk * 4 + ((c & 7) >> 1)) * R + 4 * m]) + (c & 1);
-                        const float2 st = prep_chunk<CPG>(v[h], rows, 2);
-                        if (c == 0) gst[gg * M + m] = st;
-                    }
-                }
-                // barrier k: chunk k is staged, and the consumers have finished chunk k - 1,
-                // whose buffer chunk k + 1 reuses
-                __syncthreads();
-                buf ^= 1;
+        for (int h = 0; h < H; h++) {
+            const int idx = min((int)threadIdx.x + kThreads * h, items - 1);
+            const int item = idx / CPG, c = idx - item * CPG;
+            const int gg = item / M, m = item - gg * M;
+            const size_t e = (size_t)m * st.K + (size_t)(g0 + gg) * GK + (size_t)c * 8;
+            if (st.xdt == 0) {
+                const u32x4* q = reinterpret_cast<const u32x4*>(static_cast<const float*>(st.x) + e);
+                xr[h][0] = ld_global(q);
+                xr[h][1] = ld_global(q + 1);
+            } else {
+                // the same number of loads on both paths keeps the step-4 wait exact
+                const u32x4* q = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(st.x) + e);
+                uint64_t q2 = reinterpret_cast<uint64_t>(q);
+                asm volatile("" : "+v"(q2));        // a second load, not merged with the first
+                xr[h][0] = ld_global(q);
+                xr[h][1] = ld_global(reinterpret_cast<const u32x4*>(q2));
             }
         }
-        // the consumers' last chunk ends with one more barrier
-        if (te > tb) __syncthreads();
-        return;
-    }
+#pragma unroll
+        for (int v = 0; v < BV; v++) {
+            const int bi = min((int)threadIdx.x + kThreads * v, st.nblk * kCols - 1);
+            bv[v] = ld_global(st.has_bias ? st.bias + st.ct * kCols + bi : st.bias);
+        }
+    };
+    // step 4: digits of the staged chunk into buffer `buf`
+    auto stage_finish = [&](const Stage& st, int buf) {
+        const int g0 = st.sch * kCG;
+        const int cgc = min(kCG, st.ngroups - g0);
+        const int items = cgc * M * CPG;
+        uint4* xd = digits(buf);
+        float2* gst = gstat(buf);
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            const int idx = (int)threadIdx.x + kThreads * h;
+            if (idx < items) {                    // whole CPG-lane groups: CPG divides 64
+                const int item = idx / CPG, c = idx - item * CPG;
+                const int gg = item / M, m = item - gg * M;
+                const int blk = gg * NB + (c >> 3);
+                float v[8];
+                if (st.xdt == 0) {
+                    const f32x4 lo = __builtin_bit_cast(f32x4, xr[h][0]), hi = __builtin_bit_cast(f32x4, xr[h][1]);
+                    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+                    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+                } else {
+                    const f16x8 hv = __builtin_bit_cast(f16x8, xr[h][0]);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = (float)hv[e];
+                }
+                uint2* rows = reinterpret_cast<uint2*>(&xd[(blk * 4 + ((c & 7) >> 1)) * R + 4 * m]) + (c & 1);
+                const float2 s2 = prep_chunk<CPG>(v, rows, 2);
+                if (c == 0) gst[gg * M + m] = s2;
+            }
+        }
+        if (st.sch == 0) {
+#pragma unroll
+            for (int v = 0; v < BV; v++) {
+                const int bi = (int)threadIdx.x + kThreads * v;
+                if (bi < st.nblk * kCols) bias_lds((st.si - tb) & 1)[bi] = st.has_bias ? bv[v] : 0.f;
+            }
+        }
+    };
+    auto stage_next = [&](Stage& st) {    // false past the last chunk of the last task
+        if ((st.sch + 1) * kCG < st.ngroups) {
+            st.sch++;
+            return true;
+        }
+        if (st.si + 1 >= te) return false;
+        stage_open(st, st.si + 1);
+        return true;
+    };
 
-    // ---- consumers ----
-    // job stream: per task with blocks for this wave, per chunk, groups g0 .. g0+cgc-1, padded to
-    // a multiple of P positions (padding re-reads the last job and is never consumed)
+    // ---- job stream: kCG positions per chunk of every task ----
     uint4 wb[P][BPW][2 * NB];
     uint32_t zb[P][BPW];
     uint2 sb[P][BPW];
     struct Cur {
-        int ti, ch, nch, pos, pad, cgc, g, nbw, ngroups;
+        int ti, ch, nch, pos, g, nbw, ngroups;
         const char* qw;
         const char* qz;
         const char* sc;
@@ -166,11 +228,8 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
     };
     auto blocks_of = [&](const StripTask& t) { return max(0, min(BPW, t.nblk - wave * BPW)); };
     auto open = [&](Cur& c, int ti) {
-        // the first task at or after ti with blocks for this wave (or ti = te: the stream ended)
-        for (; ti < te; ti++) {
-            const StripTask t = ld_table(a.tasks + ti);
-            if (blocks_of(t) > 0) break;
-        }
+        // every task has kCG positions per chunk for every wave; a wave without blocks in it
+        // fetches the task's last block as padding
         if (ti >= te) return false;
         const StripTask t = ld_table(a.tasks + ti);
         const SeqLinear* L = a.lin + t.linear;
@@ -186,12 +245,10 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
         c.ch = 0;
         c.pos = 0;
         c.g = 0;
-        c.cgc = min(kCG, c.ngroups);
-        c.pad = (c.cgc + P - 1) / P * P;
         c.Gq = (uint32_t)(NB * 8) * (uint32_t)N * 4u;
         c.Gs = (uint32_t)N * 2u;
         c.Gz = (((uint32_t)N + 7u) >> 3) * 4u;
-        const uint32_t blk0 = (uint32_t)(t.ct + wave * BPW);
+        const uint32_t blk0 = (uint32_t)(t.ct + min(wave * BPW, t.nblk - 1));
         c.cq = blk0 * (uint32_t)kCols * 4u;
         c.cs = blk0 * (uint32_t)kCols * 2u;
         c.cz = blk0 * (uint32_t)(kCols / 8) * 4u;
@@ -202,16 +259,15 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
         c.lz = (uint32_t)(j >> 1) * 4u;
         return true;
     };
+    // positions: kCG per chunk; a position past the chunk's groups repeats its last group
     auto advance = [&](Cur& c) {
-        if (c.pos + 1 < c.pad) {
+        if (c.pos + 1 < kCG) {
             c.pos++;
-            if (c.pos < c.cgc) c.g++;
+            if (c.ch * kCG + c.pos < c.ngroups) c.g++;
         } else if (c.ch + 1 < c.nch) {
             c.ch++;
             c.pos = 0;
             c.g = c.ch * kCG;
-            c.cgc = min(kCG, c.ngroups - c.g);
-            c.pad = (c.cgc + P - 1) / P * P;
         } else {
             Cur n = c;
             if (open(n, c.ti + 1)) c = n;   // else the stream has ended: stay on the last job
@@ -221,7 +277,7 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
         const uint32_t g = (uint32_t)c.g;
 #pragma unroll
         for (int b = 0; b < BPW; b++) {
-            const uint32_t bb = (uint32_t)min(b, c.nbw - 1);   // extra blocks re-read the last one
+            const uint32_t bb = (uint32_t)min(b, max(c.nbw, 1) - 1);   // extra blocks re-read the first
             const char* q = c.qw + g * c.Gq + c.cq + bb * (uint32_t)kCols * 4u;
 #pragma unroll
             for (int r = 0; r < 2 * NB; r++)
@@ -230,7 +286,6 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
             sb[d][b] = __builtin_bit_cast(uint2, ld_global(reinterpret_cast<const u32x2*>(c.sc + g * c.Gs + c.cs + bb * (uint32_t)kCols * 2u + c.ls)));
         }
     };
-
     // A padding slot is never consumed; without a use its registers would be free to reuse on
     // that path, and reusing a load's destination waits for every load in flight.
     auto touch_block = [&](int d, int b) {
@@ -243,16 +298,6 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
         for (int b = 0; b < BPW; b++) touch_block(d, b);
     };
 
-    Cur fc;
-    const bool any = open(fc, tb);
-    if (any) {
-#pragma unroll
-        for (int d = 0; d < P; d++) {
-            fetch(d, fc);
-            advance(fc);
-        }
-    }
-
     float acc[BPW][4][T];
     auto clear = [&]() {
 #pragma unroll
@@ -262,9 +307,8 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
 #pragma unroll
                 for (int t = 0; t < T; t++) acc[b][u][t] = 0.f;
     };
-    clear();
 
-    // one job: local group gg of the chunk in buffer `buf`, the wave's nbw blocks
+    // one job: local group gg of the chunk in buffer `buf`, the wave's nbw (>= 1) blocks
     auto consume = [&](int d, int buf, int gg, int nbw) {
         const uint4* xd = digits(buf);
         const float2* gst = gstat(buf);
@@ -286,7 +330,6 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
         }
 #pragma unroll
         for (int b = 0; b < BPW; b++) {
-            // consume() runs only for tasks with blocks for this wave: block 0 always counts
             if (b > 0 && b >= nbw) {
                 touch_block(d, b);
                 continue;
@@ -330,21 +373,34 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
         }
     };
 
-    if (te > tb) __syncthreads();          // the first chunk is staged (the producer skips
-                                           // every barrier of a workgroup without strips)
+    // the first chunk, then the ring's first P positions
+    Stage sg;
+    stage_open(sg, tb);
+    stage_issue(sg);
+    stage_finish(sg, 0);
+    __syncthreads();
+    bool staging = stage_next(sg);
+    Cur fc;
+    open(fc, tb);
+#pragma unroll
+    for (int d = 0; d < P; d++) {
+        fetch(d, fc);
+        advance(fc);
+    }
+    clear();
+
     int buf = 0;
     for (int ti = tb; ti < te; ti++) {
         const StripTask t = ld_table(a.tasks + ti);
         const SeqLinear* L = a.lin + t.linear;
-        const int K = ld_table(&L->K);
-        const int groups = K / GK;
+        const int groups = ld_table(&L->K) / GK;
         const int nbw = blocks_of(t);
         const int nch = (groups + kCG - 1) / kCG;
         for (int ch = 0; ch < nch; ch++) {
-            const int cgc = min(kCG, groups - ch * kCG);
-            const int njobs = nbw > 0 ? cgc : 0;
-            const int pad = (njobs + P - 1) / P * P;
-            for (int k = 0; k < pad; k += P) {
+            stage_issue(sg);                 // past the last chunk: repeats it (never finished)
+            const int njobs = nbw > 0 ? min(kCG, groups - ch * kCG) : 0;
+#pragma unroll
+            for (int k = 0; k < kCG; k += P) {
 #pragma unroll
                 for (int d = 0; d < P; d++) {
                     if (k + d < njobs) consume(d, buf, k + d, nbw);
@@ -363,22 +419,23 @@ __global__ __launch_bounds__(64 * (W + 1)) void strip_kernel(const StripArgs a)
                     if (b > 0 && b >= nbw) break;
                     const int bc = (wave * BPW + b) * kCols + 4 * j;       // column within the strip
                     const int col = t.ct * kCols + bc;
-                    const f32x4 bv = *reinterpret_cast<const f32x4*>(bl + bc);
+                    const f32x4 bvv = *reinterpret_cast<const f32x4*>(bl + bc);
 #pragma unroll
                     for (int tt = 0; tt < T; tt++) {
                         const int m = 4 * tt + kq;
                         if (m < M)
                             st_global(reinterpret_cast<f32x4*>(y + (size_t)m * N + col),
-                                      f32x4{acc[b][0][tt] + bv.x, acc[b][1][tt] + bv.y, acc[b][2][tt] + bv.z,
-                                            acc[b][3][tt] + bv.w});
+                                      f32x4{acc[b][0][tt] + bvv.x, acc[b][1][tt] + bvv.y, acc[b][2][tt] + bvv.z,
+                                            acc[b][3][tt] + bvv.w});
                     }
                 }
+                clear();
             }
-            // the producer has staged the next chunk into the other buffer
+            if (staging) stage_finish(sg, buf ^ 1);
             __syncthreads();
             buf ^= 1;
+            if (staging) staging = stage_next(sg);
         }
-        clear();
     }
 }
 
@@ -387,14 +444,14 @@ struct StripKernel {
     int threads;
 };
 
-// Eight consumers of one block each for M <= 8; four for M 9..16, whose registers (with the
-// producer sharing a SIMD, 256 per wave) leave room for one block each.
+// Eight waves of one block each for M <= 8 (two waves per SIMD); four of two blocks each for
+// M 9..16, whose registers take a SIMD per wave.
 template <int NB>
 StripKernel strip_kernel_for_nb(int M)
 {
-    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, 2>), 64 * 9};
-    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, 2>), 64 * 9};
-    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, 4, 1, 2>), 64 * 5};
+    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, 2>), 64 * 8};
+    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, 2>), 64 * 8};
+    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, 4, 2, 2>), 64 * 4};
 }
 
 StripKernel strip_kernel_for(int M, int group)
@@ -404,8 +461,8 @@ StripKernel strip_kernel_for(int M, int group)
     return {nullptr, 0};
 }
 
-// blocks per strip: consumer waves x blocks per wave (8 x 1, or 4 x 1 for M > 8)
-int strip_blocks(int M) { return M > 8 ? 4 : 8; }
+// blocks per strip: waves x blocks per wave (8 x 1, or 4 x 2 for M > 8)
+int strip_blocks(int) { return kMaxStripBlocks; }
 
 }  // namespace
 
