@@ -390,7 +390,7 @@ def main():
                     help="all | step05 | headline | step7b | north | sweep | prefill | unpack "
                          "(subsets for profiling: headline = the 0.5B step and its MALL-flushed "
                          "timing only; north = the 7B-shaped step at M=1 only)")
-    ap.add_argument("--m7b", default="1,4,16", help="decode batch sizes for the 7B-shaped step")
+    ap.add_argument("--m7b", default="1,2,4,8,16", help="decode batch sizes for the 7B-shaped step")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-flush", action="store_true",
@@ -430,7 +430,7 @@ def main():
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
                 "traffic": traffic_from_profiles("seq05_m1_indep"),
-                "kernel": "seq_kernel<1,2,4,2,8>",
+                "kernel": "seq_kernel<1,2,4,2,8,true>",
                 "launches_per_step": 1,
                 "bytes_per_launch": step1.bytes,
                 "avg_launch_us": round(kms * 1e3, 3),

@@ -101,6 +101,13 @@ function gpu(dir) {
         ctx.sync();
         writeTyped(path.join(dir, u.out), U.read());
         pool.reset();
+        // the batched form over several weights at once
+        const ua = spec.unpackAll;
+        const UA = ua.weights.map((w, i) => pool.alloc([ua.N[i], ua.K[i]], 'f16'));
+        model.unpackAllF16(ua.weights, UA);
+        ctx.sync();
+        UA.forEach((t, i) => writeTyped(path.join(dir, ua.outs[i]), t.read()));
+        pool.reset();
 
         // dequantizeGptqInt4 with the reference's params object, from the parsed file
         const file = q.parseSafetensors(fs.readFileSync(path.join(dir, 'model.safetensors')));

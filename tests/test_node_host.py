@@ -31,7 +31,7 @@ BINDING = {
     "arenaRelease": "ql_arena_release", "arenaSize": "ql_arena_size",
     "arenaWrite": "ql_arena_write", "arenaRead": "ql_arena_read", "gptqSizes": "ql_gptq_sizes",
     "validate": "ql_gptq_validate", "planLinear": "ql_plan_linear", "planBatch": "ql_plan_batch",
-    "unpack": "ql_unpack_f16", "linear": "ql_linear", "linearBatch": "ql_linear_batch",
+    "unpack": "ql_unpack_f16", "unpackBatch": "ql_unpack_f16_batch", "linear": "ql_linear", "linearBatch": "ql_linear_batch",
     "sync": "ql_sync", "timerStart": "ql_timer_start", "timerStop": "ql_timer_stop",
     "graphBegin": "ql_graph_begin", "graphEnd": "ql_graph_end", "graphLaunch": "ql_graph_launch",
     "graphDestroy": "ql_graph_destroy", "seqCreate": "ql_seq_create", "seqRun": "ql_seq_run",
@@ -109,6 +109,9 @@ def test_node_host_matches_oracle(tmp_path, orc):
                     "outs": [f"s{k}.f32" for k in seq_names]}
     K, N = shapes["gateW"]
     cases["unpack"] = {"weight": "L1.gateW", "N": N, "K": K, "out": "u.f16"}
+    ua = ["gateW", "downW", "kW"]
+    cases["unpackAll"] = {"weights": [f"L0.{k}" for k in ua], "N": [shapes[k][1] for k in ua],
+                          "K": [shapes[k][0] for k in ua], "outs": [f"ua_{k}.f16" for k in ua]}
     cases["dequant"] = {"prefix": "model.layers.1.mlp.down_proj", "K": shapes["downW"][0],
                         "N": shapes["downW"][1], "out": "w.f32"}
     (tmp_path / "cases.json").write_text(json.dumps(cases))
@@ -130,6 +133,10 @@ def test_node_host_matches_oracle(tmp_path, orc):
     t, _ = kept[(1, "gateW")]
     u = np.fromfile(tmp_path / "u.f16", dtype=np.uint16).reshape(t.N, t.K)
     assert np.array_equal(u, orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, t.K, t.N, 128))
+    for k in ("gateW", "downW", "kW"):
+        t, _ = kept[(0, k)]
+        u = np.fromfile(tmp_path / f"ua_{k}.f16", dtype=np.uint16).reshape(t.N, t.K)
+        assert np.array_equal(u, orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, t.K, t.N, 128)), k
     for out, (t, _) in (("w.f32", kept[(1, "downW")]), ("kept_qW.f32", kept[(0, "qW")])):
         _, W = orc.dequantize_gptq_int4(t.qweight, t.qzeros, orc.f16_bits_to_f32(t.scales), t.K,
                                         t.N, 128)

@@ -336,10 +336,6 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
             }
             i32x4 c[4][T];
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-#pragma unroll
-                for (int t = 0; t < T; t++) c[u][t] = i32x4{0, 0, 0, 0};
-#pragma unroll
             for (int bb = 0; bb < NB; bb++) {
                 const uint4 w0 = wb[d][b][2 * bb], w1 = wb[d][b][2 * bb + 1];
                 const uint32_t lo[4] = {w0.x, w0.y, w0.z, w0.w};
@@ -348,8 +344,10 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
                 for (int u = 0; u < 4; u++) {
                     const i32x4 bq = i32x4{(int)(lo[u] & 0x0F0F0F0Fu), (int)((lo[u] >> 4) & 0x0F0F0F0Fu),
                                            (int)(hi[u] & 0x0F0F0F0Fu), (int)((hi[u] >> 4) & 0x0F0F0F0Fu)};
+                    // the first 64-k block starts each sum from an inline zero (no register setup)
 #pragma unroll
-                    for (int t = 0; t < T; t++) c[u][t] = mfma_i8(av[bb][t], bq, c[u][t]);
+                    for (int t = 0; t < T; t++)
+                        c[u][t] = mfma_i8(av[bb][t], bq, bb == 0 ? i32x4{0, 0, 0, 0} : c[u][t]);
                 }
             }
             const uint32_t zw = zb[d][b] >> (4 * ((4 * j) & 7));
@@ -444,14 +442,30 @@ struct StripKernel {
     int threads;
 };
 
-// Eight waves of one block each for M <= 8 (two waves per SIMD); four of two blocks each for
-// M 9..16, whose registers take a SIMD per wave.
+// Tunables (compile-time): jobs in flight per wave for M <= 4, <= 8 and <= 16, and the waves of
+// the M 9..16 instance (8: one block each, two waves per SIMD; 4: two blocks each, a SIMD each).
+#ifndef QL_STRIP_P1
+#define QL_STRIP_P1 2
+#endif
+#ifndef QL_STRIP_P2
+#define QL_STRIP_P2 2
+#endif
+#ifndef QL_STRIP_P4
+#define QL_STRIP_P4 2
+#endif
+#ifndef QL_STRIP_W4
+#define QL_STRIP_W4 8
+#endif
+
+// Eight waves of one block each (two waves per SIMD, so one wave's MFMAs overlap the other's
+// epilogue); M 9..16 as QL_STRIP_W4 says (four waves of two blocks measured 20% slower).
 template <int NB>
 StripKernel strip_kernel_for_nb(int M)
 {
-    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, 2>), 64 * 8};
-    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, 2>), 64 * 8};
-    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, 4, 2, 2>), 64 * 4};
+    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, QL_STRIP_P1>), 64 * 8};
+    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, QL_STRIP_P2>), 64 * 8};
+    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, QL_STRIP_W4, 8 / QL_STRIP_W4, QL_STRIP_P4>),
+            64 * QL_STRIP_W4};
 }
 
 StripKernel strip_kernel_for(int M, int group)

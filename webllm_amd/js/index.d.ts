@@ -98,6 +98,8 @@ export class QuantLinearModel {
     gemm(A: Tensor, weight: string, C: Tensor, bias: string | null, M: number, N: number, K: number): void;
     gemmBatch(A: Tensor, weights: string[], Cs: Tensor[], M: number): void;
     unpackF16(name: string, out: Tensor): void;
+    /** fp16 [N,K] copies of many weights in a few launches (ql_unpack_f16_batch). */
+    unpackAllF16(names: string[], outs: Tensor[]): void;
     dequantize(name: string): Float32Array;
     release(): void;
 }

@@ -441,6 +441,21 @@ class QuantLinearModel {
         if (out.dtype !== 'f16' || out.length < lin.N * lin.K) throw new Error('unpackF16: output must be an f16 tensor of N*K elements');
         addon.unpack(this.ctx.handle, lin.desc, this.weights.handle, out.arena.handle, out.offset, false);
     }
+    /**
+     * fp16 [N,K] copies of many weights at once (the loader's whole weight set,
+     * qwen-loader.ts:146-162): names[i] into outs[i], same bits as unpackF16, in a few launches.
+     */
+    unpackAllF16(names, outs) {
+        if (names.length !== outs.length) throw new Error('unpackAllF16: one output tensor per weight');
+        const descs = names.map((n, i) => {
+            const lin = this.linear(n);
+            const out = outs[i];
+            if (out.dtype !== 'f16' || out.length < lin.N * lin.K) throw new Error('unpackAllF16: output must be an f16 tensor of N*K elements');
+            if (out.arena !== outs[0].arena) throw new Error('unpackAllF16: all outputs must share one arena');
+            return lin.desc;
+        });
+        if (descs.length) addon.unpackBatch(this.ctx.handle, descs, this.weights.handle, outs[0].arena.handle, outs.map((o) => o.offset));
+    }
     /** fp32 [N,K] = dequantizeGptqInt4 of the stored tensors (computed on the GPU). */
     dequantize(name) {
         const lin = this.linear(name);

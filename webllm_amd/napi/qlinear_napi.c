@@ -440,6 +440,35 @@ static napi_value js_linear_batch(napi_env env, napi_callback_info info)
     return NULL;
 }
 
+/* unpackBatch(ctx, descs[], w, out, outOffs[]): the whole weight set, ql_unpack_f16_batch */
+static napi_value js_unpack_batch(napi_env env, napi_callback_info info)
+{
+    napi_value argv[5];
+    void *ctx, *w, *o;
+    uint32_t n = 0, m = 0;
+    if (get_args(env, info, 5, argv) || get_ptr(env, argv[0], &ctx) || get_ptr(env, argv[2], &w) ||
+        get_ptr(env, argv[3], &o))
+        return NULL;
+    if (napi_get_array_length(env, argv[1], &n) != napi_ok || napi_get_array_length(env, argv[4], &m) != napi_ok ||
+        n != m) {
+        napi_throw_type_error(env, "QL_E_INVALID", "expected descriptor and offset arrays of one length");
+        return NULL;
+    }
+    ql_gptq_desc* d = (ql_gptq_desc*)calloc(n ? n : 1, sizeof *d);
+    uint64_t* off = (uint64_t*)calloc(n ? n : 1, sizeof *off);
+    int bad = !d || !off;
+    for (uint32_t i = 0; i < n && !bad; i++) {
+        napi_value e;
+        bad = napi_get_element(env, argv[1], i, &e) != napi_ok || get_desc(env, e, &d[i]) ||
+              napi_get_element(env, argv[4], i, &e) != napi_ok || get_u64(env, e, &off[i], 0);
+    }
+    if (!bad) throw_rc(env, ql_unpack_f16_batch((ql_ctx*)ctx, (int32_t)n, d, (ql_arena*)w, (ql_arena*)o, off));
+    else if (!d || !off) napi_throw_error(env, "QL_E_INVALID", "out of host memory");
+    free(d);
+    free(off);
+    return NULL;
+}
+
 static napi_value js_sync(napi_env env, napi_callback_info info)
 {
     napi_value argv[1];
@@ -611,7 +640,7 @@ static napi_value init(napi_env env, napi_value exports)
         {"arenaRelease", js_arena_release}, {"arenaSize", js_arena_size},
         {"arenaWrite", js_arena_write}, {"arenaRead", js_arena_read}, {"gptqSizes", js_gptq_sizes},
         {"validate", js_validate}, {"planLinear", js_plan_linear}, {"planBatch", js_plan_batch},
-        {"unpack", js_unpack}, {"linear", js_linear}, {"linearBatch", js_linear_batch},
+        {"unpack", js_unpack}, {"unpackBatch", js_unpack_batch}, {"linear", js_linear}, {"linearBatch", js_linear_batch},
         {"sync", js_sync}, {"timerStart", js_timer_start}, {"timerStop", js_timer_stop},
         {"graphBegin", js_graph_begin}, {"graphEnd", js_graph_end},
         {"graphLaunch", js_graph_launch}, {"graphDestroy", js_graph_destroy},
