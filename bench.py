@@ -429,8 +429,9 @@ def main():
             f"{gbs:.0f} GB/s; plan {si.as_dict()}")
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "traffic": traffic_from_profiles("seq05_m1_indep"),
-                "kernel": "seq_kernel<1,2,4,2,8,true>",
+                "traffic": traffic_from_profiles("strip05_m1_indep" if si.kernel == ql.SEQ_STRIPS else "seq05_m1_indep"),
+                "kernel": ("strip_kernel<1,2,8,1,2,%d>" % si.split) if si.kernel == ql.SEQ_STRIPS
+                          else "seq_kernel<1,2,4,2,8,true>",
                 "launches_per_step": 1,
                 "bytes_per_launch": step1.bytes,
                 "avg_launch_us": round(kms * 1e3, 3),

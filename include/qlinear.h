@@ -173,6 +173,8 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
  * on the context stream; it allocates nothing and may be captured into a graph and replayed.
  * Runs of one sequence must not overlap (one stream). ql_seq_status waits for the stream and
  * reports whether a run was aborted (a bounded device-side wait ran out: QL_E_STATE). */
+#define QL_SEQ_TILES 0
+#define QL_SEQ_STRIPS 1
 typedef struct ql_seq ql_seq;
 typedef struct ql_seq_info {
     int32_t linears;
@@ -185,6 +187,8 @@ typedef struct ql_seq_info {
     uint64_t device_bytes;/* tables + exchange buffers ql_seq_create allocates */
     uint64_t total_units; /* block-groups (64 columns x one quantization group) of all linears */
     uint64_t busiest_units; /* block-groups of the most loaded workgroup: balance = busiest*grid/total */
+    int32_t kernel;       /* QL_SEQ_TILES: dependency-ordered tiles; QL_SEQ_STRIPS: column strips */
+    int32_t split;        /* strips: waves per 64-column block (1: strips of 8 blocks, 2: of 4) */
 } ql_seq_info;
 /* plan only (host, pure) for a given grid size: validation and the figures above */
 int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,

@@ -281,7 +281,7 @@ def test_strips_7b_independent(ql, ctx, orc, indep7b, M):
     seq = ctx.seq(m.descs, m.weights, act, x_offs, 0, M, y_offs)
     info = seq.info
     say(f"strips 7B x3 M={M}: {info.as_dict()}")
-    assert info.passes == 1 and info.reduces == 0 and info.max_split == 1
+    assert info.kernel == ql.SEQ_STRIPS and info.passes == 1 and info.reduces == 0 and info.max_split == 1
     seq.run()
     seq.status()
     ys = [act.read(yo, (M, L["t"].N), np.float32) for L, yo in zip(m.lin, y_offs)]
@@ -312,3 +312,58 @@ def test_strips_7b_independent(ql, ctx, orc, indep7b, M):
     g.destroy()
     seq.destroy()
     act.release()
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_strips_05b_split_blocks(ql, ctx, orc, M):
+    """Two layers of 0.5B-shaped independent linears: strips of 4 blocks with two waves per block
+    (each wave takes alternate groups of every chunk; part sums added in LDS in part order).
+    Every linear, including the 4864-deep down projection and the biased q/k/v, meets the GEMV
+    bar; repeated runs are bit-identical."""
+    shapes = [(896, 896, True), (896, 128, True), (896, 128, True), (896, 896, False),
+              (896, 4864, False), (896, 4864, False), (4864, 896, False)] * 2
+    wl, al = ql.ArenaLayout(), ql.ArenaLayout()
+    lins = []
+    for i, (K, N, biased) in enumerate(shapes):
+        t = synth.gptq_linear(K, N, 128, seed=0x5B2, key=(i,), stored_zero=7 if i % 2 else None)
+        bias = synth.activations(1, N, seed=0x5B3, key=(i,))[0] if biased else None
+        sym = i % 3 == 2
+        lins.append({"t": t, "bias": bias, "qw": wl.take(t.qweight.nbytes),
+                     "qz": None if sym else wl.take(t.qzeros.nbytes), "sc": wl.take(t.scales.nbytes),
+                     "b": None if bias is None else wl.take(bias.nbytes),
+                     "x": al.take(M * K * 4), "y": al.take(M * N * 4)})
+    w = ctx.arena(wl.used)
+    act = ctx.arena(al.used)
+    xs = []
+    for i, L in enumerate(lins):
+        t = L["t"]
+        w.write(L["qw"], t.qweight)
+        if L["qz"] is not None:
+            w.write(L["qz"], t.qzeros)
+        w.write(L["sc"], t.scales)
+        if L["b"] is not None:
+            w.write(L["b"], L["bias"])
+        x = synth.activations(M, t.K, seed=0x5B4, key=(M, i))
+        act.write(L["x"], x)
+        xs.append(x)
+    descs = [ql.make_desc(L["qw"], L["qz"], L["sc"], L["t"].K, L["t"].N, 128, L["b"]) for L in lins]
+    seq = ctx.seq(descs, w, act, [L["x"] for L in lins], 0, M, [L["y"] for L in lins])
+    info = seq.info
+    say(f"strips 0.5B x2 M={M}: {info.as_dict()}")
+    assert info.kernel == ql.SEQ_STRIPS and info.split == 2 and info.reduces == 0
+    seq.run()
+    seq.status()
+    ys = [act.read(L["y"], (M, L["t"].N), np.float32) for L in lins]
+    for i, (L, x, y) in enumerate(zip(lins, xs, ys)):
+        t = L["t"]
+        qz = None if L["qz"] is None else t.qzeros
+        ref = orc.gptq_linear(t.qweight, qz, t.scales, x, L["bias"], 128)
+        ok, max_abs, max_rel = orc.check_tolerance(y, ref, 1e-5, RTOL)
+        assert ok, f"M={M} linear {i} K={t.K} N={t.N}: maxAbs {max_abs:.3e} maxRel {max_rel:.3e}"
+    seq.run()
+    seq.status()
+    for L, y in zip(lins, ys):
+        assert np.array_equal(act.read(L["y"], (M, L["t"].N), np.float32).view(np.uint32), y.view(np.uint32))
+    seq.destroy()
+    act.release()
+    w.release()

@@ -364,6 +364,8 @@ void fill_strip_info(const ql::StripPlan& p, int n, uint64_t scratch, ql_seq_inf
     info->device_bytes = scratch;
     info->total_units = p.total_units;
     info->busiest_units = p.busiest_units;
+    info->kernel = QL_SEQ_STRIPS;
+    info->split = p.split;
 }
 
 void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info* info)
@@ -378,6 +380,8 @@ void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info
     info->device_bytes = scratch;
     info->total_units = p.total_units;
     info->busiest_units = p.busiest_units;
+    info->kernel = QL_SEQ_TILES;
+    info->split = 1;
 }
 
 int set_device(ql_ctx* ctx)
@@ -437,6 +441,7 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     q->sargs.M = M;
     q->sargs.G = sp.grid;
     q->sargs.group = descs[0].group;
+    q->sargs.split = sp.split;
     fill_strip_info(sp, n, lay.total, &q->info);
     *out = q;
     return QL_OK;

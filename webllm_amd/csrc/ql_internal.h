@@ -200,13 +200,22 @@ int seq_wg_per_cu();
 hipError_t launch_seq(const SeqArgs& a, size_t lds, hipStream_t stream);
 
 // ----------------------------------------------------------------------------------------------
-// Column strips: a sequence of independent linears (no linear reads another's output) at M >= 2
-// whose weights stream from HBM, as one persistent launch, each workgroup owning strips of 4 or 8
-// whole 64-column blocks over all of K (no K splits, no partial sums). Groups of 64 or 128,
-// N % 64 == 0.
+// Column strips: a sequence of independent linears (no linear reads another's output) as one
+// persistent launch, each workgroup owning strips of 8 whole 64-column blocks (or 4, two waves per
+// block) over all of K (no K splits across workgroups). Groups of 64 or 128, N % 64 == 0. Measured
+// against the dependency-ordered tiles: equal on the 0.5B step at M = 1, faster at every M > 1 and
+// on the 7B step (QL_STRIP_MIN_KB_PER_CU can restrict strips to weights streamed from HBM).
 constexpr int kStripMinM = 1;           // fewest rows the strip path serves
-constexpr uint64_t kStripMinBytesPerCU = 1ull << 20;   // weight bytes per CU from which it does
-constexpr int kStripChunkGroups = 4;    // quantization groups staged per chunk
+#ifndef QL_STRIP_MIN_KB_PER_CU
+#define QL_STRIP_MIN_KB_PER_CU 0
+#endif
+constexpr uint64_t kStripMinBytesPerCU = (uint64_t)QL_STRIP_MIN_KB_PER_CU << 10;   // weight bytes per CU from which it does
+#ifndef QL_STRIP_CG
+#define QL_STRIP_CG 4
+#endif
+constexpr int kStripChunkGroups = QL_STRIP_CG;   // quantization groups staged per chunk
+// a plan of 8-block strips more than this far off balance is re-planned with 4-block strips
+constexpr double kStripSplitBalance = 1.06;
 
 struct StripTask {
     int32_t linear, ct, nblk;  // blocks ct .. ct+nblk-1 of the linear, over all of K
@@ -218,10 +227,11 @@ struct StripArgs {
     const StripTask* tasks;
     const int32_t* task_begin; // [G + 1]
     int32_t M, G, group;
+    int32_t split;             // waves per block: 1 (strips of 8 blocks) or 2 (strips of 4)
 };
 
 struct StripPlan {
-    int grid = 0, strips = 0;
+    int grid = 0, strips = 0, split = 1;
     uint64_t lds_bytes = 0;
     uint64_t total_units = 0, busiest_units = 0;   // block-groups: all, most on one workgroup
     std::vector<StripTask> tasks;
@@ -229,7 +239,7 @@ struct StripPlan {
 };
 
 bool strip_eligible(const std::vector<SeqSpec>& lin, int M);
-size_t strip_lds(int M, int group);
+size_t strip_lds(int M, int group, int split);
 void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out);
 hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream);
 

@@ -78,10 +78,15 @@ constexpr int kMaxStripBlocks = 8;       // most blocks in one strip
 //   4. wait for step 1's loads (the kCG positions' loads stay in flight), turn them into digits
 //      in the other LDS buffer, stage the next strip's bias with its first chunk;
 //   5. one barrier.
-template <int T, int NB, int W, int BPW, int P>
+template <int T, int NB, int W, int BPW, int P, int S>
 __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
 {
-    static_assert(kCG % P == 0, "a chunk's positions fill whole ring rounds");
+    // S waves share each block (S > 1: waves take alternate groups of every chunk and add their
+    // sums in LDS at the strip's end, in part order); QP positions per chunk for each wave
+    static_assert(S == 1 || BPW == 1, "split blocks hold one block per wave");
+    constexpr int QP = kCG / S;
+    static_assert(QP * S == kCG && QP % P == 0, "a chunk's positions fill whole ring rounds");
+    constexpr int WB = W / S;                // waves per part = blocks per strip / BPW
     extern __shared__ uint4 dyn_lds[];
     constexpr int GK = NB * 64;              // k per group
     constexpr int CPG = NB * 8;              // lanes per (group, row) when staging
@@ -92,6 +97,8 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
     const int R = 4 * M;
     const int lane = threadIdx.x & 63;
     const int wave = uni(threadIdx.x >> 6);
+    const int bw = wave % WB;                // the wave's block slot in the strip
+    const int sp = wave / WB;                // the wave's part: groups sp, sp + S, ... of a chunk
     const int j = lane & 15;
     const int kq = lane >> 4;
     const int wg = blockIdx.x;
@@ -108,6 +115,8 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
     auto bias_lds = [&](int par) {
         return reinterpret_cast<float*>(reinterpret_cast<char*>(dyn_lds) + 2 * buf_bytes) + par * (kMaxStripBlocks * kCols);
     };
+    // sums of parts 1 .. S-1 at a strip's end: [part - 1][block][row][column]
+    auto part_lds = [&]() { return bias_lds(2); };
 
     // ---- staging cursor: the chunk being staged (task si, chunk sch) ----
     struct Stage {
@@ -226,7 +235,7 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
         uint32_t cq, cz, cs;        // byte offsets of the wave's first block
         uint32_t lq[2 * NB], lz, ls;
     };
-    auto blocks_of = [&](const StripTask& t) { return max(0, min(BPW, t.nblk - wave * BPW)); };
+    auto blocks_of = [&](const StripTask& t) { return max(0, min(BPW, t.nblk - bw * BPW)); };
     auto open = [&](Cur& c, int ti) {
         // every task has kCG positions per chunk for every wave; a wave without blocks in it
         // fetches the task's last block as padding
@@ -244,11 +253,11 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
         c.nch = (c.ngroups + kCG - 1) / kCG;
         c.ch = 0;
         c.pos = 0;
-        c.g = 0;
+        c.g = min(sp, c.ngroups - 1);
         c.Gq = (uint32_t)(NB * 8) * (uint32_t)N * 4u;
         c.Gs = (uint32_t)N * 2u;
         c.Gz = (((uint32_t)N + 7u) >> 3) * 4u;
-        const uint32_t blk0 = (uint32_t)(t.ct + min(wave * BPW, t.nblk - 1));
+        const uint32_t blk0 = (uint32_t)(t.ct + min(bw * BPW, t.nblk - 1));
         c.cq = blk0 * (uint32_t)kCols * 4u;
         c.cs = blk0 * (uint32_t)kCols * 2u;
         c.cz = blk0 * (uint32_t)(kCols / 8) * 4u;
@@ -259,15 +268,16 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
         c.lz = (uint32_t)(j >> 1) * 4u;
         return true;
     };
-    // positions: kCG per chunk; a position past the chunk's groups repeats its last group
+    // positions: QP per chunk, position p on group p * S + sp of the chunk; a position past the
+    // linear's groups re-reads a valid one
     auto advance = [&](Cur& c) {
-        if (c.pos + 1 < kCG) {
+        if (c.pos + 1 < QP) {
             c.pos++;
-            if (c.ch * kCG + c.pos < c.ngroups) c.g++;
+            c.g = min(c.ch * kCG + c.pos * S + sp, c.ngroups - 1);
         } else if (c.ch + 1 < c.nch) {
             c.ch++;
             c.pos = 0;
-            c.g = c.ch * kCG;
+            c.g = min(c.ch * kCG + sp, c.ngroups - 1);
         } else {
             Cur n = c;
             if (open(n, c.ti + 1)) c = n;   // else the stream has ended: stay on the last job
@@ -396,18 +406,49 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
         const int nch = (groups + kCG - 1) / kCG;
         for (int ch = 0; ch < nch; ch++) {
             stage_issue(sg);                 // past the last chunk: repeats it (never finished)
-            const int njobs = nbw > 0 ? min(kCG, groups - ch * kCG) : 0;
+            const int cgc = min(kCG, groups - ch * kCG);
+            const int njobs = nbw > 0 && cgc > sp ? (cgc - sp + S - 1) / S : 0;
 #pragma unroll
-            for (int k = 0; k < kCG; k += P) {
+            for (int k = 0; k < QP; k += P) {
 #pragma unroll
                 for (int d = 0; d < P; d++) {
-                    if (k + d < njobs) consume(d, buf, k + d, nbw);
+                    if (k + d < njobs) consume(d, buf, (k + d) * S + sp, nbw);
                     else touch(d);
                     fetch(d, fc);
                     advance(fc);
                 }
             }
-            if (ch + 1 == nch && nbw > 0) {
+            if (S > 1 && ch + 1 == nch) {
+                // parts 1 .. S-1 hand their sums to part 0 through LDS (one barrier, uniform:
+                // every wave walks the same strips and chunks), which adds them in part order
+                float* pl = part_lds();
+                if (sp > 0 && nbw > 0) {
+#pragma unroll
+                    for (int tt = 0; tt < T; tt++) {
+                        const int m = 4 * tt + kq;
+                        if (m < M)
+                            *reinterpret_cast<f32x4*>(pl + (((sp - 1) * WB + bw) * M + m) * kCols + 4 * j) =
+                                f32x4{acc[0][0][tt], acc[0][1][tt], acc[0][2][tt], acc[0][3][tt]};
+                    }
+                }
+                __syncthreads();
+                if (sp == 0 && nbw > 0) {
+#pragma unroll
+                    for (int q = 1; q < S; q++)
+#pragma unroll
+                        for (int tt = 0; tt < T; tt++) {
+                            const int m = 4 * tt + kq;
+                            if (m < M) {
+                                const f32x4 v = *reinterpret_cast<const f32x4*>(pl + (((q - 1) * WB + bw) * M + m) * kCols + 4 * j);
+                                acc[0][0][tt] += v.x;
+                                acc[0][1][tt] += v.y;
+                                acc[0][2][tt] += v.z;
+                                acc[0][3][tt] += v.w;
+                            }
+                        }
+                }
+            }
+            if (ch + 1 == nch && nbw > 0 && sp == 0) {
                 // the strip's outputs (bias from LDS: no global load on this path)
                 const int N = ld_table(&L->N);
                 float* y = ld_table(&L->y);
@@ -415,7 +456,7 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
 #pragma unroll
                 for (int b = 0; b < BPW; b++) {
                     if (b > 0 && b >= nbw) break;
-                    const int bc = (wave * BPW + b) * kCols + 4 * j;       // column within the strip
+                    const int bc = (bw * BPW + b) * kCols + 4 * j;         // column within the strip
                     const int col = t.ct * kCols + bc;
                     const f32x4 bvv = *reinterpret_cast<const f32x4*>(bl + bc);
 #pragma unroll
@@ -427,8 +468,8 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
                                             acc[b][3][tt] + bvv.w});
                     }
                 }
-                clear();
             }
+            if (ch + 1 == nch) clear();
             if (staging) stage_finish(sg, buf ^ 1);
             __syncthreads();
             buf ^= 1;
@@ -458,20 +499,22 @@ struct StripKernel {
 #endif
 
 // Eight waves of one block each (two waves per SIMD, so one wave's MFMAs overlap the other's
-// epilogue); M 9..16 as QL_STRIP_W4 says (four waves of two blocks measured 20% slower).
-template <int NB>
-StripKernel strip_kernel_for_nb(int M)
+// epilogue); M 9..16 as QL_STRIP_W4 says (four waves of two blocks measured 20% slower). With
+// split 2, two waves share each block of a 4-block strip.
+template <int NB, int S>
+StripKernel strip_kernel_for_ns(int M)
 {
-    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, QL_STRIP_P1>), 64 * 8};
-    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, QL_STRIP_P2>), 64 * 8};
-    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, QL_STRIP_W4, 8 / QL_STRIP_W4, QL_STRIP_P4>),
+    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, QL_STRIP_P1, S>), 64 * 8};
+    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, QL_STRIP_P2, S>), 64 * 8};
+    if (S > 1) return {reinterpret_cast<const void*>(&strip_kernel<4, NB, 8, 1, QL_STRIP_P4, S>), 64 * 8};
+    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, QL_STRIP_W4, 8 / QL_STRIP_W4, QL_STRIP_P4, 1>),
             64 * QL_STRIP_W4};
 }
 
-StripKernel strip_kernel_for(int M, int group)
+StripKernel strip_kernel_for(int M, int group, int split)
 {
-    if (group == 64) return strip_kernel_for_nb<1>(M);
-    if (group == 128) return strip_kernel_for_nb<2>(M);
+    if (group == 64) return split == 2 ? strip_kernel_for_ns<1, 2>(M) : strip_kernel_for_ns<1, 1>(M);
+    if (group == 128) return split == 2 ? strip_kernel_for_ns<2, 2>(M) : strip_kernel_for_ns<2, 1>(M);
     return {nullptr, 0};
 }
 
@@ -490,22 +533,25 @@ bool strip_eligible(const std::vector<SeqSpec>& lin, int M)
             return false;
         bytes += s.weight_bytes;
     }
-    // streamed from HBM: strips of whole K balance well only when every CU gets many of them
-    // (a MALL-resident step is latency-bound and keeps the dependency-ordered tiles)
     return bytes >= kStripMinBytesPerCU * (uint64_t)kPlanCUs;
 }
 
-size_t strip_lds(int M, int group)
+size_t strip_lds(int M, int group, int split)
 {
-    return 2 * strip_buf_bytes(M, group / 64) + 2 * kMaxStripBlocks * kCols * sizeof(float);
+    // two chunk buffers, two bias buffers, and the part sums of a split strip
+    const size_t parts = (size_t)(split - 1) * (kMaxStripBlocks / split) * M * kCols * sizeof(float);
+    return 2 * strip_buf_bytes(M, group / 64) + 2 * kMaxStripBlocks * kCols * sizeof(float) + parts;
 }
 
-void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+namespace {
+
+void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int split, StripPlan* out)
 {
     StripPlan& p = *out;
     p = StripPlan{};
     p.grid = grid;
-    const int SB = strip_blocks(M);
+    p.split = split;
+    const int SB = kMaxStripBlocks / split;   // blocks per strip
     struct Item {
         StripTask t;
         uint64_t cost;
@@ -545,12 +591,27 @@ void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* ou
     }
     p.task_begin[grid] = (int32_t)p.tasks.size();
     p.strips = (int)items.size();
-    p.lds_bytes = lin.empty() ? 0 : strip_lds(M, lin[0].group);
+    p.lds_bytes = lin.empty() ? 0 : strip_lds(M, lin[0].group, split);
+}
+
+}  // namespace
+
+// Strips of 8 blocks, or of 4 with two waves per block when that balances the workgroups
+// better (a strip of 8 blocks of a long-K linear can outweigh a workgroup's mean share).
+void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+{
+    plan_strips_split(lin, M, grid, 1, out);
+    if (out->total_units == 0) return;
+    const double mean = (double)out->total_units / grid;
+    if (out->busiest_units <= mean * kStripSplitBalance) return;
+    StripPlan two;
+    plan_strips_split(lin, M, grid, 2, &two);
+    if (two.busiest_units < out->busiest_units) *out = two;
 }
 
 hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream)
 {
-    const StripKernel k = strip_kernel_for(a.M, a.group);
+    const StripKernel k = strip_kernel_for(a.M, a.group, a.split);
     if (!k.fn) return hipErrorInvalidValue;
     void* args[] = {const_cast<StripArgs*>(&a)};
     return hipLaunchKernel(k.fn, dim3(a.G), dim3(k.threads), args, lds, stream);

@@ -43,6 +43,8 @@ export interface SeqInfo {
     maxSplit: number; ldsBytes: number; deviceBytes: number;
     /** block-groups (64 columns x one group) in total and on the busiest workgroup */
     totalUnits: number; busiestUnits: number;
+    /** 0: dependency-ordered tiles, 1: column strips; split: waves per 64-column block of a strip */
+    kernel: number; split: number;
 }
 /** A forward's decode linears (M <= 16) as one persistent launch; linear i reads linear j's
  *  output when xOffs[i] === yOffs[j]. */

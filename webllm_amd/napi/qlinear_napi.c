@@ -617,6 +617,11 @@ static napi_value js_seq_info(napi_env env, napi_callback_info info)
     napi_set_named_property(env, o, "deviceBytes", make_u64(env, si.device_bytes));
     napi_set_named_property(env, o, "totalUnits", make_u64(env, si.total_units));
     napi_set_named_property(env, o, "busiestUnits", make_u64(env, si.busiest_units));
+    napi_value kv, sv;
+    napi_create_int32(env, si.kernel, &kv);
+    napi_create_int32(env, si.split, &sv);
+    napi_set_named_property(env, o, "kernel", kv);
+    napi_set_named_property(env, o, "split", sv);
     return o;
 }
 

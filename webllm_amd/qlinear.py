@@ -19,6 +19,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libqlinear.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "qlinear.h")
 
+SEQ_TILES, SEQ_STRIPS = 0, 1      # ql_seq_info.kernel
 QL_NONE = (1 << 64) - 1
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -61,7 +62,8 @@ class SeqInfo(ctypes.Structure):
     _fields_ = [("linears", ctypes.c_int32), ("passes", ctypes.c_int32), ("tiles", ctypes.c_int32),
                 ("reduces", ctypes.c_int32), ("grid", ctypes.c_int32), ("max_split", ctypes.c_int32),
                 ("lds_bytes", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64),
-                ("total_units", ctypes.c_uint64), ("busiest_units", ctypes.c_uint64)]
+                ("total_units", ctypes.c_uint64), ("busiest_units", ctypes.c_uint64),
+                ("kernel", ctypes.c_int32), ("split", ctypes.c_int32)]
 
     def as_dict(self) -> dict:
         return {f: getattr(self, f) for f, _ in self._fields_}
