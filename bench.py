@@ -387,7 +387,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    help="all | step05 | headline | step7b | north | sweep | prefill | unpack "
+                    help="all | step05 | headline | step7b | north | sweep | prefill | unpack | lmhead "
                          "(subsets for profiling: headline = the 0.5B step and its MALL-flushed "
                          "timing only; north = the 7B-shaped step at M=1 only)")
     ap.add_argument("--m7b", default="1,2,4,8,16", help="decode batch sizes for the 7B-shaped step")
@@ -494,6 +494,40 @@ def main():
                        "(q,k,v | o | gate,up | down) group (96 launches)")
         extra["prefill05"] = pre
         log(f"prefill: {pre}")
+
+    if only in ("all", "lmhead"):
+        # the tied lm_head / embedding GEMV of the 0.5B model (qwen.ts:488-489): fp16 [151936, 896]
+        V, C = 151936, 896
+        rng = np.random.default_rng(0x1E4D)
+        wl = ctx.arena(V * C * 2)
+        wl.write(0, (rng.standard_normal((V, C), dtype=np.float32) * 0.02).astype(np.float16).view(np.uint16))
+        lm = {}
+        for M in (1, 4):
+            act = ctx.arena(M * C * 4 + M * V * 4 + 256)
+            y_off = (M * C * 4 + 255) // 256 * 256
+            act.write(0, synth.activations(M, C, seed=0x1E4E, key=(M,)))
+            issue = lambda: ctx.gemv_f16w(wl, 0, None, act, 0, M, V, C, y_off)
+            issue()
+            ctx.sync()
+            ctx.graph_begin()
+            issue()
+            g = ctx.graph_end()
+            for _ in range(3):
+                g.launch()
+            ctx.timer_start()
+            reps = max(20, args.steps)
+            for _ in range(reps):
+                g.launch()
+            ms = ctx.timer_stop() / reps
+            nbytes = V * C * 2 + M * C * 4 + M * V * 4
+            lm[str(M)] = {"us": round(ms * 1e3, 1), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                          "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+            g.destroy()
+            act.release()
+        wl.release()
+        lm["note"] = "fp16 W [151936, 896] (272 MB, read once per decode step), fp32 x and y; graph-replayed launches"
+        extra["lmhead05"] = lm
+        log(f"lm_head GEMV: {lm}")
 
     if only in ("all", "unpack"):
         ms, nbytes = unpack_all(ctx, m05, max(5, args.steps // 5))

@@ -153,6 +153,14 @@ int ql_plan_linear(int32_t M, int32_t N, int32_t K, int32_t group, ql_plan* out)
 int ql_linear(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights, ql_arena* act,
               uint64_t x_off, int32_t x_dtype, int32_t M, uint64_t y_off, uint64_t scratch_off);
 
+/* y[M,N] (fp32) = x[M,K] (fp32) . W^T (+ bias) for an fp16 weight W [N,K] row-major at w_off in
+ * `weights` (bias f32 [N] at bias_off or QL_NONE): the tied lm_head / embedding product,
+ * QwenGpt.gemm(lnf, 'embed', logits, null, M, V, C) (qwen.ts:488-489) on gemm_gemv_f16.wgsl's
+ * arithmetic (fp32 x, fp16 weights, fp32 accumulation). M = 1..16 (up to 4 rows per pass over
+ * the weights); x, y, w offsets 16-byte aligned, K % 8 == 0. */
+int ql_gemv_f16w(ql_ctx* ctx, const ql_arena* weights, uint64_t w_off, uint64_t bias_off,
+                 ql_arena* act, uint64_t x_off, int32_t M, int32_t N, int32_t K, uint64_t y_off);
+
 /* several independent linears in one launch (e.g. q/k/v on one input, gate/up on another);
  * linear i reads x_offs[i] and writes y_offs[i]; scratch for all of them starts at scratch_off
  * (ql_plan_batch gives the size). M and x_dtype are shared; at most 8 linears. */

@@ -546,3 +546,47 @@ def test_graph_replay_matches_eager(ql, ctx):
         step()                     # eager work between replays
         ctx.sync()
     g.destroy()
+
+
+# ------------------------------------------------------------------------- fp16-weight GEMV
+
+F16W_CASES = [
+    # (M, N, K, bias, label)
+    (1, 151936, 896, False, "0.5B tied lm_head M=1"),
+    (3, 4100, 896, True, "M=3, ragged N, bias"),
+    (6, 1000, 1024, False, "M=6: two passes over the weights"),
+    (2, 300, 200, True, "K % 128 != 0: one lane per output"),
+]
+
+
+@pytest.mark.parametrize("M,N,K,biased,label", F16W_CASES)
+def test_gemv_f16w_matches_oracle(ql, ctx, orc, M, N, K, biased, label):
+    """The tied lm_head product (qwen.ts:488-489, gemm_gemv_f16.wgsl): fp32 x, fp16 W [N,K],
+    fp32 accumulation, against gemmNTRef on the fp16-decoded weights (double accumulation) at the
+    GEMV bar; repeats are bit-identical."""
+    rng = np.random.default_rng(0xF16 + N)
+    W16 = (rng.standard_normal((N, K), dtype=np.float32) * 0.02).astype(np.float16)
+    bias = synth.activations(1, N, seed=0xF17)[0] if biased else None
+    x = synth.activations(M, K, seed=0xF18, key=(M,))
+    lay = ql.ArenaLayout()
+    w_off = lay.take(W16.nbytes)
+    b_off = lay.take(N * 4) if biased else None
+    w = ctx.arena(lay.used)
+    w.write(w_off, W16.view(np.uint16))
+    if biased:
+        w.write(b_off, bias)
+    alay = ql.ArenaLayout()
+    x_off, y_off = alay.take(x.nbytes), alay.take(M * N * 4)
+    act = ctx.arena(alay.used)
+    act.write(x_off, x)
+    say(f"gemv_f16w {label}: M={M} N={N} K={K}")
+    ctx.gemv_f16w(w, w_off, b_off, act, x_off, M, N, K, y_off)
+    y = act.read(y_off, (M, N), np.float32)
+    ref = orc.gemm_nt(x, W16.astype(np.float32), bias)
+    assert_close(orc, y, ref, GEMV_ATOL, GEMV_RTOL, label)
+    ctx.gemv_f16w(w, w_off, b_off, act, x_off, M, N, K, y_off)
+    assert np.array_equal(act.read(y_off, (M, N), np.float32).view(np.uint32), y.view(np.uint32))
+    with pytest.raises(ql.QlError):
+        ctx.gemv_f16w(w, w_off, b_off, act, x_off, M, N + 1 << 20, K, y_off)
+    act.release()
+    w.release()

@@ -396,7 +396,7 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
                  const std::vector<ql::SeqSpec>& specs, ql_seq** out)
 {
     ql::StripPlan sp;
-    ql::plan_strips(specs, M, ctx->cu_count, &sp);
+    ql::plan_strips(specs, M, ql::strip_grid(ctx->cu_count, specs), &sp);
     const StripLayout lay = strip_layout(specs, sp);
     char* dev = nullptr;
     QL_HIP(hipMalloc(&dev, lay.total));
@@ -817,6 +817,36 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_ar
     g.group = d->group;
     g.x_dtype = x_dtype;
     QL_HIP(ql::launch_gemm_simple(g, ctx->stream));
+    return QL_OK;
+}
+
+int ql_gemv_f16w(ql_ctx* ctx, const ql_arena* weights, uint64_t w_off, uint64_t bias_off,
+                 ql_arena* act, uint64_t x_off, int32_t M, int32_t N, int32_t K, uint64_t y_off)
+{
+    if (!ctx || !weights || !act) return fail(QL_E_INVALID, "null context or arena");
+    if (M < 1 || M > ql::kGemvMaxM) return fail(QL_E_INVALID, "M must be 1..%d", ql::kGemvMaxM);
+    if (N <= 0 || K <= 0) return fail(QL_E_DIMS, "N and K must be positive");
+    if (K % 8) return fail(QL_E_INVALID, "K must be a multiple of 8 (got %d)", K);
+    if (!in_range(w_off, (uint64_t)N * K * 2, weights->size)) return fail(QL_E_RANGE, "fp16 weights [N,K] outside the arena");
+    if (bias_off != QL_NONE && !in_range(bias_off, (uint64_t)N * 4, weights->size))
+        return fail(QL_E_RANGE, "bias [N] outside the weight arena");
+    if (!in_range(x_off, (uint64_t)M * K * 4, act->size)) return fail(QL_E_RANGE, "x [M,K] outside the activation arena");
+    if (!in_range(y_off, (uint64_t)M * N * 4, act->size)) return fail(QL_E_RANGE, "y [M,N] outside the activation arena");
+    if (w_off % 16 || x_off % 16 || y_off % 16 || (bias_off != QL_NONE && bias_off % 4))
+        return fail(QL_E_ALIGN, "w, x and y offsets must be 16-byte aligned (bias 4-byte)");
+    const uint64_t xa = x_off, xb = x_off + (uint64_t)M * K * 4, ya = y_off, yb = y_off + (uint64_t)M * N * 4;
+    if (xa < yb && ya < xb) return fail(QL_E_INVALID, "x and y overlap");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    ql::F16wArgs a;
+    a.w = reinterpret_cast<const uint16_t*>(weights->base + w_off);
+    a.bias = bias_off == QL_NONE ? nullptr : reinterpret_cast<const float*>(weights->base + bias_off);
+    a.x = reinterpret_cast<const float*>(act->base + x_off);
+    a.y = reinterpret_cast<float*>(act->base + y_off);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    QL_HIP(ql::launch_gemv_f16w(a, ql::gemv_f16w_fast_ok(M, N, K), ctx->cu_count, ctx->stream));
     return QL_OK;
 }
 

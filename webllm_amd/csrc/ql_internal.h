@@ -113,6 +113,18 @@ int unpack_tiles(int N, int K);    // 16-packed-row x 64-column tiles of one ten
 hipError_t launch_unpack_batch(const UnpackBatch& b, hipStream_t stream);
 hipError_t launch_unpack_f32(const UnpackArgs& a, hipStream_t stream);
 
+// fp16-weight GEMV (tied lm_head / embedding): y[M,N] = x[M,K] . W[N,K]^T (+ bias), fp32 x/y.
+struct F16wArgs {
+    const uint16_t* w;         // fp16 [N, K] row-major
+    const float* bias;         // [N] or nullptr
+    const float* x;            // [M, K]
+    float* y;                  // [M, N]
+    int M, N, K;
+};
+bool gemv_f16w_fast_ok(int M, int N, int K);
+size_t gemv_f16w_lds(int M, int K);
+hipError_t launch_gemv_f16w(const F16wArgs& a, bool fast, int cu_count, hipStream_t stream);
+
 // ----------------------------------------------------------------------------------------------
 // Linear sequences: many decode linears (M <= 16) in one persistent launch. Linear i may read the
 // output of an earlier linear; the kernel orders them on the device.
@@ -239,6 +251,8 @@ struct StripPlan {
 };
 
 bool strip_eligible(const std::vector<SeqSpec>& lin, int M);
+int strip_grid(int cu_count, const std::vector<SeqSpec>& lin);   // workgroups of a strip launch
+constexpr uint64_t kStripMallBytes = 192ull << 20;   // weights that stay resident in the MALL
 size_t strip_lds(int M, int group, int split);
 void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out);
 hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream);

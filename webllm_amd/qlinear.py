@@ -114,6 +114,7 @@ def lib():
         "ql_unpack_f32": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64]),
         "ql_unpack_f16_batch": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64)]),
         "ql_plan_linear": (I, [I, I, I, I, ctypes.POINTER(Plan)]),
+        "ql_gemv_f16w": (I, [P, P, U64, U64, P, U64, I, I, I, U64]),
         "ql_linear": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64, I, I, U64, U64]),
         "ql_plan_batch": (I, [I, ctypes.POINTER(GptqDesc), I, ctypes.POINTER(U64)]),
         "ql_linear_batch": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64), I, I,
@@ -311,6 +312,13 @@ class Context:
         arr = (GptqDesc * n)(*descs)
         offs = (ctypes.c_uint64 * n)(*out_offs)
         _check(lib().ql_unpack_f16_batch(self.handle, n, arr, weights.handle, out.handle, offs))
+
+    def gemv_f16w(self, weights: Arena, w_off: int, bias_off, act: Arena, x_off: int, M: int, N: int,
+                  K: int, y_off: int):
+        """y[M,N] = x[M,K] . W^T (+ bias) for fp16 W [N,K] (the tied lm_head, qwen.ts:488-489)."""
+        _check(lib().ql_gemv_f16w(self.handle, weights.handle, w_off,
+                                  QL_NONE if bias_off is None else bias_off, act.handle, x_off, M, N,
+                                  K, y_off))
 
     def unpack_f32(self, desc: GptqDesc, weights: Arena, out: Arena, out_off: int):
         _check(lib().ql_unpack_f32(self.handle, ctypes.byref(desc), weights.handle, out.handle,
