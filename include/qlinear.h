@@ -156,8 +156,8 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights, ql
 /* y[M,N] (fp32) = x[M,K] (fp32) . W^T (+ bias) for an fp16 weight W [N,K] row-major at w_off in
  * `weights` (bias f32 [N] at bias_off or QL_NONE): the tied lm_head / embedding product,
  * QwenGpt.gemm(lnf, 'embed', logits, null, M, V, C) (qwen.ts:488-489) on gemm_gemv_f16.wgsl's
- * arithmetic (fp32 x, fp16 weights, fp32 accumulation). M = 1..16 (up to 4 rows per pass over
- * the weights); x, y, w offsets 16-byte aligned, K % 8 == 0. */
+ * arithmetic (fp32 x, fp16 weights, fp32 accumulation). M = 1..65535, up to 4 rows per pass over
+ * the weights (a decode-sized product: prefill rows re-read W once per 4 rows); x, y, w offsets 16-byte aligned, K % 8 == 0. */
 int ql_gemv_f16w(ql_ctx* ctx, const ql_arena* weights, uint64_t w_off, uint64_t bias_off,
                  ql_arena* act, uint64_t x_off, int32_t M, int32_t N, int32_t K, uint64_t y_off);
 

@@ -9,12 +9,13 @@ TINY = gptq.QwenConfig(vocab_size=512, block_size=16, n_layer=2, n_head=4, n_kv_
 
 def write_checkpoint(path, cfg):
     """Writes a Qwen-layout GPTQ checkpoint of config `cfg` (random tensors, half the linears with
-    qzeros nibble 7, half with random zeros) and returns {(layer, key): (GptqTensors, bias f32)}."""
+    qzeros nibble 7, half with random zeros) and returns {(layer, key): (GptqTensors, bias f32)} plus "embed": the fp16 embedding."""
     shapes = gptq.qwen_linear_shapes(cfg)
     tensors, kept = {}, {}
     rng = np.random.default_rng(1)
     emb = (rng.standard_normal((cfg.vocab_size, cfg.n_embd)) * 0.02).astype(np.float16)
     tensors["model.embed_tokens.weight"] = ("F16", emb.shape, emb.tobytes())
+    kept["embed"] = emb
     tensors["model.norm.weight"] = ("F32", (cfg.n_embd,), np.ones(cfg.n_embd, np.float32).tobytes())
     for i in range(cfg.n_layer):
         p = f"model.layers.{i}"

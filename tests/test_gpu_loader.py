@@ -77,6 +77,25 @@ def test_gemm_dispatch_matches_oracle(loaded, orc, ctx):
             pool.reset()
 
 
+def test_gemm_lm_head_over_embed(loaded, orc, ctx):
+    """gemm(lnf, 'embed', logits, null, M, V, C) (qwen.ts:488-489): the tied fp16 embedding as the
+    lm_head weight, f32 in and out, at the GEMV bar; M = 6 takes two passes over the weights."""
+    model, _, kept, _ = loaded
+    emb = kept["embed"]
+    V, C = emb.shape
+    pool = gptq.ActivationArena(ctx, 8 << 20)
+    for M in (1, 6):
+        x = synth.activations(M, C, seed=0x79, key=(M,))
+        A, L = pool.alloc((M, C)), pool.alloc((M, V))
+        A.write(x)
+        model.gemm(A, "embed", L, None, M, V, C)
+        ok, ma, _ = orc.check_tolerance(L.read(), orc.gemm_nt(x, emb.astype(np.float32)), 1e-5, 1e-4)
+        assert ok, (M, ma)
+        with pytest.raises(ValueError, match="embed"):
+            model.gemm(A, "embed", L, None, M, V - 1, C)
+        pool.reset()
+
+
 def test_gemm_batch_qkv(loaded, orc, ctx):
     model, _, kept, _ = loaded
     pool = gptq.ActivationArena(ctx, 8 << 20)

@@ -556,6 +556,7 @@ F16W_CASES = [
     (3, 4100, 896, True, "M=3, ragged N, bias"),
     (6, 1000, 1024, False, "M=6: two passes over the weights"),
     (2, 300, 200, True, "K % 128 != 0: one lane per output"),
+    (21, 2048, 896, True, "M=21: prefill rows, six passes over the weights"),
 ]
 
 

@@ -824,7 +824,7 @@ int ql_gemv_f16w(ql_ctx* ctx, const ql_arena* weights, uint64_t w_off, uint64_t 
                  ql_arena* act, uint64_t x_off, int32_t M, int32_t N, int32_t K, uint64_t y_off)
 {
     if (!ctx || !weights || !act) return fail(QL_E_INVALID, "null context or arena");
-    if (M < 1 || M > ql::kGemvMaxM) return fail(QL_E_INVALID, "M must be 1..%d", ql::kGemvMaxM);
+    if (M < 1 || M > 65535) return fail(QL_E_INVALID, "M must be 1..65535 (got %d)", M);
     if (N <= 0 || K <= 0) return fail(QL_E_DIMS, "N and K must be positive");
     if (K % 8) return fail(QL_E_INVALID, "K must be a multiple of 8 (got %d)", K);
     if (!in_range(w_off, (uint64_t)N * K * 2, weights->size)) return fail(QL_E_RANGE, "fp16 weights [N,K] outside the arena");

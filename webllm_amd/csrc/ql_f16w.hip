@@ -147,7 +147,7 @@ size_t gemv_f16w_lds(int M, int K) { return (size_t)M * K * sizeof(float); }
 
 bool gemv_f16w_fast_ok(int M, int N, int K)
 {
-    return M >= 1 && M <= kGemvMaxM && N > 0 && K > 0 && K % kStepK == 0 && gemv_f16w_lds(4, K) <= (96u << 10);
+    return M >= 1 && N > 0 && K > 0 && K % kStepK == 0 && gemv_f16w_lds(4, K) <= (96u << 10);
 }
 
 hipError_t launch_gemv_f16w(const F16wArgs& a, bool fast, int cu_count, hipStream_t stream)

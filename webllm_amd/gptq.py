@@ -304,6 +304,8 @@ class QuantLinearModel:
         """C[M,N] = A[M,K] @ W^T (+ bias) — qwen.ts:568-618. A is f32 (decode) or f16; C is f32.
         The bias is the linear's own (upload_gptq_linear(bias=...)); passing another name raises,
         as a missing weight does in the reference (qwen.ts:640-645)."""
+        if weight in self.f16 and weight not in self.linears:
+            return self._gemm_f16(A, weight, C, bias, M, N, K)
         lin = self.linear(weight)
         if (lin.K, lin.N) != (K, N):
             raise ValueError(f"gemm: {weight} is [{lin.N},{lin.K}], called with N={N} K={K}")
@@ -323,6 +325,28 @@ class QuantLinearModel:
         scratch = A.pool.scratch_offset(plan.scratch_bytes)
         self.ctx.linear(desc, self.weights, A.arena, A.offset,
                         ql.DTYPE_F32 if A.dtype == "f32" else ql.DTYPE_F16, M, C.offset, scratch)
+
+    def _gemm_f16(self, A: Tensor, weight: str, C: Tensor, bias: str | None, M: int, N: int, K: int):
+        """C[M,N] = A[M,K] @ W^T (+ bias) over an fp16 weight [N,K] (the tied lm_head `embed`,
+        qwen.ts:488-489 with gemm_gemv_f16.wgsl semantics): f32 A and C, fp32 accumulation."""
+        w = self.f16[weight]
+        if w.shape != (N, K):
+            raise ValueError(f"gemm: {weight} is {list(w.shape)}, called with N={N} K={K}")
+        b = None
+        if bias is not None:
+            t = self.f32.get(bias)
+            if t is None:
+                raise ValueError(f"missing f32 weight: {bias}")
+            if t.length != N:
+                raise ValueError(f"gemm: bias {bias} has {t.length} values, N={N}")
+            b = t.offset
+        if A.dtype != "f32" or C.dtype != "f32":
+            raise ValueError("gemm over fp16 weights takes f32 A and C")
+        if A.arena is not C.arena:
+            raise ValueError("gemm: A and C must live in the same activation arena")
+        if A.length < M * K or C.length < M * N:
+            raise ValueError("gemm: tensor too small for [M,K] / [M,N]")
+        self.ctx.gemv_f16w(self.weights, w.offset, b, A.arena, A.offset, M, N, K, C.offset)
 
     def gemm_batch(self, A: Tensor, weights: list, Cs: list, M: int):
         """Several linears on one input in one launch (q/k/v, gate/up; qwen.ts:411-413, :464-465)."""
