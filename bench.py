@@ -387,7 +387,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    help="all | step05 | headline | step7b | north | sweep | prefill | unpack | lmhead "
+                    help="all | step05 | headline | step7b | north | sweep | prefill | unpack | lmhead | attn "
                          "(subsets for profiling: headline = the 0.5B step and its MALL-flushed "
                          "timing only; north = the 7B-shaped step at M=1 only)")
     ap.add_argument("--m7b", default="1,2,4,8,16", help="decode batch sizes for the 7B-shaped step")
@@ -528,6 +528,49 @@ def main():
         lm["note"] = "fp16 W [151936, 896] (272 MB, read once per decode step), fp32 x and y; graph-replayed launches"
         extra["lmhead05"] = lm
         log(f"lm_head GEMV: {lm}")
+
+    if only in ("all", "attn"):
+        # decode attention over the KV cache, every layer of a step (qwen.ts:424-442): the
+        # 0.5B model at its full 128-position cache, the 7B shape at 4096 positions
+        at = {}
+        for name, L, H, KV, D, T in (("05b_t128", 24, 14, 2, 64, 128), ("7b_t4096", 28, 28, 4, 128, 4096)):
+            rng = np.random.default_rng(0xA7)
+            region = T * KV * D * 4
+            cache = ctx.arena(2 * L * region)
+            for i in range(2 * L):
+                cache.write(i * region, rng.standard_normal((T, KV * D)).astype(np.float32))
+            qb = H * D * 4
+            act = ctx.arena(2 * L * qb)
+            act.write(0, rng.standard_normal((L, H * D)).astype(np.float32))
+
+            def issue():
+                for l in range(L):
+                    ctx.attention_decode(act, l * qb, cache, 2 * l * region, (2 * l + 1) * region, T, 1, H, KV,
+                                         D, T - 1, (L + l) * qb)
+            issue()
+            ctx.sync()
+            ctx.graph_begin()
+            issue()
+            g = ctx.graph_end()
+            for _ in range(3):
+                g.launch()
+            ctx.timer_start()
+            reps = max(20, args.steps)
+            for _ in range(reps):
+                g.launch()
+            ms = ctx.timer_stop() / reps
+            nbytes = L * (2 * region + 2 * qb)
+            at[name] = {"us_per_step": round(ms * 1e3, 1), "us_per_layer": round(ms * 1e3 / L, 2),
+                        "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                        "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+                        "layers": L, "heads": H, "kv_heads": KV, "head_dim": D, "positions": T}
+            g.destroy()
+            act.release()
+            cache.release()
+        at["note"] = ("M = 1 at the last position; one launch per layer (grid heads x 1), graph-replayed; "
+                      "bytes = the K and V caches once plus q and out")
+        extra["attn"] = at
+        log(f"decode attention: {at}")
 
     if only in ("all", "unpack"):
         ms, nbytes = unpack_all(ctx, m05, max(5, args.steps // 5))

@@ -161,6 +161,26 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights, ql
 int ql_gemv_f16w(ql_ctx* ctx, const ql_arena* weights, uint64_t w_off, uint64_t bias_off,
                  ql_arena* act, uint64_t x_off, int32_t M, int32_t N, int32_t K, uint64_t y_off);
 
+/* ---- decode attention over the KV cache (qwen.ts:424-442).
+ * Cache: per layer one fp32 K and one fp32 V region of [max_t, n_kv_head * D], row t holding the
+ * vectors of position t (the reference's kCache[i] / vCache[i], qwen.ts:200-205).
+ *
+ * ql_kv_store: cache[(pos0 + r) * row_len + c] = src[r * row_len + c] for r < rows
+ *   (misc/kv_store.wgsl); pos0 + rows > max_t fails with QL_E_RANGE (qwen.ts:352-355 throws).
+ *   row_len % 4 == 0, offsets 16-byte aligned. */
+int ql_kv_store(ql_ctx* ctx, const ql_arena* act, uint64_t src_off, ql_arena* cache, uint64_t cache_off,
+                int32_t max_t, int32_t rows, int32_t row_len, int32_t pos0);
+
+/* ql_attention_decode: out[m, h, :] = softmax_s(q[m, h] . K[s, h / (H / KV)] / sqrt(D)) V[s, ...]
+ *   over s = 0 .. past_len + m (causal; attention/attention_gqa_cache.wgsl, CPU form
+ *   reference/qwen-ref.ts:65-111 attentionGqaRef). q and out are [M, n_head, D] fp32 in `act`;
+ *   D = 4..256 (multiple of 4); past_len + M <= max_t and <= 8192. fp32 throughout. Few rows x heads
+ *   (decode) split the keys over workgroups, with partials in a 4 MiB workspace the context owns:
+ *   calls on one context run in its stream's order, so they never share it at the same time. */
+int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_arena* cache, uint64_t k_off,
+                        uint64_t v_off, int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D,
+                        int32_t past_len, uint64_t out_off);
+
 /* several independent linears in one launch (e.g. q/k/v on one input, gate/up on another);
  * linear i reads x_offs[i] and writes y_offs[i]; scratch for all of them starts at scratch_off
  * (ql_plan_batch gives the size). M and x_dtype are shared; at most 8 linears. */

@@ -296,3 +296,50 @@ uint32_t orc_rng_step(uint32_t* state)
 }
 
 double orc_rng_next(uint32_t* state) { return (double)orc_rng_step(state) / 4294967296.0; }
+
+/* attentionGqaRef (src/reference/qwen-ref.ts:65-111) with the cache's positions
+ * (attention_gqa_cache.wgsl): query row m of q [M, H, D] sits at position past + m and sees keys
+ * 0 .. past + m of the caches kc / vc [>= past + M, KV * D]. JS arithmetic kept: the dot product,
+ * max, exp and sum in double; scores stored in a Float32Array (rounded at each store);
+ * p_s = f32(f32(e_s) / sum); out = f32(sum_s p_s * v_s) accumulated in double. */
+int orc_attention_gqa_cache(const float* q, const float* kc, const float* vc, int M, int H, int KV, int D,
+                            int past, float* out)
+{
+    if (M <= 0 || H <= 0 || KV <= 0 || D <= 0 || past < 0 || H % KV) return ORC_E_DIMS;
+    const double scale = 1.0 / sqrt((double)D);
+    const int group = H / KV, row_len = KV * D;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(past + M));
+    if (!scores) return ORC_E_DIMS;
+    for (int h = 0; h < H; h++) {
+        const int kvh = h / group;
+        for (int m = 0; m < M; m++) {
+            const int t = past + m;
+            const float* qv = q + ((size_t)m * H + h) * D;
+            double max_score = -INFINITY;
+            for (int s = 0; s <= t; s++) {
+                const float* kr = kc + (size_t)s * row_len + (size_t)kvh * D;
+                double dot = 0.0;
+                for (int d = 0; d < D; d++) dot += (double)qv[d] * (double)kr[d];
+                dot *= scale;
+                scores[s] = (float)dot;
+                if (dot > max_score) max_score = dot;
+            }
+            double sum = 0.0;
+            for (int s = 0; s <= t; s++) {
+                const double e = exp((double)scores[s] - max_score);
+                scores[s] = (float)e;
+                sum += e;
+            }
+            for (int s = 0; s <= t; s++) scores[s] = (float)((double)scores[s] / sum);
+            float* o = out + ((size_t)m * H + h) * D;
+            for (int d = 0; d < D; d++) {
+                double acc = 0.0;
+                for (int s = 0; s <= t; s++)
+                    acc += (double)scores[s] * (double)vc[(size_t)s * row_len + (size_t)kvh * D + d];
+                o[d] = (float)acc;
+            }
+        }
+    }
+    free(scores);
+    return 0;
+}

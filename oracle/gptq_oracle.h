@@ -61,6 +61,10 @@ int orc_dequant_gptq_int4_f16(const uint8_t* qweight, size_t qweight_bytes,
 
 void orc_gemm_nt(const float* A, const float* W, int M, int N, int K, const float* bias, float* C);
 
+/* attentionGqaRef (qwen-ref.ts:65-111) over a KV cache: q [M,H,D], caches [past+M, KV*D]. */
+int orc_attention_gqa_cache(const float* q, const float* kc, const float* vc, int M, int H, int KV, int D,
+                            int past, float* out);
+
 /* Fused CPU reference for one GPTQ linear: dequant (as quant.ts) then gemmNTRef, row by row,
  * so memory stays O(K) instead of O(N*K). Bit-identical to orc_dequant + orc_gemm_nt. */
 int orc_gptq_linear(const uint8_t* qweight, const uint8_t* qzeros, const uint16_t* scales_f16,

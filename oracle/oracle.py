@@ -10,6 +10,8 @@ The oracle restates the reference CPU path (intplusplus/webllm):
   gemmNTRef               src/reference/qwen-ref.ts:126-145
   planGemvSplit           src/model/qwen.ts:61-74
   checkTolerance/makeRng  src/reference/cpu-ref.ts:27-67
+  attentionGqaRef         src/reference/qwen-ref.ts:65-111 (over a KV cache, with the positions of
+                          src/gpu/kernels/attention/attention_gqa_cache.wgsl)
 """
 from __future__ import annotations
 
@@ -68,6 +70,8 @@ def lib():
                                       ctypes.c_int, P]
         L.orc_plan_gemv_split.restype = ctypes.c_int
         L.orc_plan_gemv_split.argtypes = [ctypes.c_int, ctypes.c_int]
+        L.orc_attention_gqa_cache.restype = ctypes.c_int
+        L.orc_attention_gqa_cache.argtypes = [P, P, P] + [ctypes.c_int] * 5 + [P]
         L.orc_check_tolerance.restype = ctypes.c_int
         L.orc_check_tolerance.argtypes = [P, P, ctypes.c_size_t, ctypes.c_double, ctypes.c_double,
                                           ctypes.POINTER(ctypes.c_double),
@@ -167,6 +171,21 @@ def gptq_linear(qweight, qzeros, scales_f16, x, bias=None, group: int = 128) -> 
     if rc != 0:
         raise ValueError("oracle gptq_linear: bad arguments")
     return y
+
+
+def attention_gqa_cache(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, H: int, KV: int, D: int,
+                        past: int) -> np.ndarray:
+    """Causal GQA attention of q [M, H, D] over caches [>= past + M, KV * D] (attentionGqaRef)."""
+    q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1, H, D)
+    kc = np.ascontiguousarray(kc, dtype=np.float32).reshape(-1)
+    vc = np.ascontiguousarray(vc, dtype=np.float32).reshape(-1)
+    M = q.shape[0]
+    if kc.size < (past + M) * KV * D or vc.size < (past + M) * KV * D:
+        raise ValueError("oracle attention: cache shorter than past + M rows")
+    out = np.empty((M, H, D), dtype=np.float32)
+    if lib().orc_attention_gqa_cache(_ptr(q), _ptr(kc), _ptr(vc), M, H, KV, D, past, _ptr(out)) != 0:
+        raise ValueError("oracle attention: bad dimensions")
+    return out
 
 
 def plan_gemv_split(wg_n: int, K: int) -> int:

@@ -277,3 +277,57 @@ def test_rng_golden(orc):
         assert [r.step() for _ in d[key]] == d[key]
     r = orc.Rng(1)
     assert r() == 270369 / 2 ** 32
+
+
+def _attention_torch(q, kc, vc, H, KV, D, past):
+    """Textbook causal attention in float64 (torch.softmax), kv head h // (H // KV) repeated per
+    query head: an independent route to the same numbers."""
+    import torch
+    M = q.shape[0]
+    T = past + M
+    Q = torch.from_numpy(q.astype(np.float64)).reshape(M, H, D).transpose(0, 1)           # [H, M, D]
+    Kt = torch.from_numpy(kc[:T].astype(np.float64)).reshape(T, KV, D).transpose(0, 1)    # [KV, T, D]
+    Vt = torch.from_numpy(vc[:T].astype(np.float64)).reshape(T, KV, D).transpose(0, 1)
+    Kt = Kt.repeat_interleave(H // KV, dim=0)
+    Vt = Vt.repeat_interleave(H // KV, dim=0)
+    S = Q @ Kt.transpose(1, 2) / np.sqrt(D)
+    pos = past + torch.arange(M).unsqueeze(1)
+    S = S.masked_fill(torch.arange(T).unsqueeze(0) > pos, float("-inf"))
+    return (torch.softmax(S, dim=-1) @ Vt).transpose(0, 1).numpy()                        # [M, H, D]
+
+
+@pytest.mark.parametrize("M,H,KV,D,past", [(1, 14, 2, 64, 0), (1, 14, 2, 64, 127), (5, 4, 2, 48, 9),
+                                           (3, 8, 8, 16, 30), (1, 28, 4, 128, 300)])
+def test_attention_oracle_vs_textbook(orc, M, H, KV, D, past):
+    """The attention oracle against softmax(QK^T / sqrt(D)) V in float64 with a causal mask
+    and grouped kv heads (a swapped head mapping h % KV, a missing scale or an off-by-one in the
+    visible range all fail this)."""
+    rng = np.random.default_rng(M * 1000 + past)
+    T = past + M
+    q = rng.standard_normal((M, H, D)).astype(np.float32)
+    kc = rng.standard_normal((T, KV * D)).astype(np.float32)
+    vc = rng.standard_normal((T, KV * D)).astype(np.float32)
+    got = orc.attention_gqa_cache(q, kc, vc, H, KV, D, past)
+    ref = _attention_torch(q, kc, vc, H, KV, D, past)
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-6), np.abs(got - ref).max()
+
+
+def test_attention_oracle_special_cases(orc):
+    """One visible key: the output is that key's value, exactly. Equal keys: uniform weights, the
+    mean of the values."""
+    rng = np.random.default_rng(7)
+    H, KV, D = 4, 2, 32
+    q = rng.standard_normal((1, H, D)).astype(np.float32)
+    kc = rng.standard_normal((1, KV * D)).astype(np.float32)
+    vc = rng.standard_normal((1, KV * D)).astype(np.float32)
+    got = orc.attention_gqa_cache(q, kc, vc, H, KV, D, 0)
+    for h in range(H):
+        kvh = h // (H // KV)
+        assert np.array_equal(got[0, h], vc[0, kvh * D:(kvh + 1) * D])
+    T = 9
+    kc = np.tile(rng.standard_normal((1, KV * D)).astype(np.float32), (T, 1))
+    vc = rng.standard_normal((T, KV * D)).astype(np.float32)
+    got = orc.attention_gqa_cache(q, kc, vc, H, KV, D, T - 1)
+    for h in range(H):
+        kvh = h // (H // KV)
+        assert np.allclose(got[0, h], vc[:, kvh * D:(kvh + 1) * D].astype(np.float64).mean(0), atol=1e-6)

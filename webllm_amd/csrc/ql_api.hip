@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -17,6 +18,7 @@ struct ql_ctx {
     int device;
     hipStream_t stream;
     uint32_t* counters;   // split-K arrival counters; every launch leaves them at zero
+    float* attn_ws;       // attention key-split partials (ql::kAttnWsBytes), used in stream order
     hipEvent_t ev_start, ev_stop;
     bool capturing;
     int cu_count;
@@ -475,6 +477,7 @@ int ql_create(int device, ql_ctx** out)
     }
     if ((e = hipMalloc(&c->counters, sizeof(uint32_t) * ql::kCounterCapacity)) != hipSuccess ||
         (e = hipMemset(c->counters, 0, sizeof(uint32_t) * ql::kCounterCapacity)) != hipSuccess ||
+        (e = hipMalloc(&c->attn_ws, ql::kAttnWsBytes)) != hipSuccess ||
         (e = hipEventCreate(&c->ev_start)) != hipSuccess ||
         (e = hipEventCreate(&c->ev_stop)) != hipSuccess) {
         (void)hipStreamDestroy(c->stream);
@@ -493,6 +496,7 @@ int ql_destroy(ql_ctx* ctx)
     (void)hipEventDestroy(ctx->ev_start);
     (void)hipEventDestroy(ctx->ev_stop);
     (void)hipFree(ctx->counters);
+    (void)hipFree(ctx->attn_ws);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return QL_OK;
@@ -847,6 +851,66 @@ int ql_gemv_f16w(ql_ctx* ctx, const ql_arena* weights, uint64_t w_off, uint64_t 
     a.N = N;
     a.K = K;
     QL_HIP(ql::launch_gemv_f16w(a, ql::gemv_f16w_fast_ok(M, N, K), ctx->cu_count, ctx->stream));
+    return QL_OK;
+}
+
+int ql_kv_store(ql_ctx* ctx, const ql_arena* act, uint64_t src_off, ql_arena* cache, uint64_t cache_off,
+                int32_t max_t, int32_t rows, int32_t row_len, int32_t pos0)
+{
+    if (!ctx || !act || !cache) return fail(QL_E_INVALID, "null context or arena");
+    if (max_t <= 0 || rows <= 0 || row_len <= 0 || pos0 < 0)
+        return fail(QL_E_INVALID, "max_t, rows and row_len must be positive, pos0 >= 0");
+    if ((int64_t)pos0 + rows > max_t)
+        return fail(QL_E_RANGE, "context length %lld exceeds the cache's %d positions", (long long)pos0 + rows, max_t);
+    if (row_len % 4) return fail(QL_E_INVALID, "row_len must be a multiple of 4 (got %d)", row_len);
+    if ((int64_t)rows * row_len >= (1ll << 31)) return fail(QL_E_INVALID, "rows x row_len too large");
+    if (!in_range(src_off, (uint64_t)rows * row_len * 4, act->size)) return fail(QL_E_RANGE, "src [rows, row_len] outside the activation arena");
+    if (!in_range(cache_off, (uint64_t)max_t * row_len * 4, cache->size)) return fail(QL_E_RANGE, "cache [max_t, row_len] outside its arena");
+    if (src_off % 16 || cache_off % 16) return fail(QL_E_ALIGN, "src and cache offsets must be 16-byte aligned");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(ql::launch_kv_store(reinterpret_cast<const float*>(act->base + src_off),
+                               reinterpret_cast<float*>(cache->base + cache_off), rows, row_len, pos0, ctx->stream));
+    return QL_OK;
+}
+
+int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_arena* cache, uint64_t k_off,
+                        uint64_t v_off, int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D,
+                        int32_t past_len, uint64_t out_off)
+{
+    if (!ctx || !act || !cache) return fail(QL_E_INVALID, "null context or arena");
+    if (M < 1 || M > 65535 || n_head < 1 || n_head > 65535 || n_kv_head < 1 || past_len < 0 || max_t < 1)
+        return fail(QL_E_INVALID, "bad attention dimensions");
+    if (n_head % n_kv_head) return fail(QL_E_INVALID, "n_head (%d) must be a multiple of n_kv_head (%d)", n_head, n_kv_head);
+    if (D < 4 || D > ql::kAttnMaxD || D % 4) return fail(QL_E_INVALID, "head dim must be 4..%d, a multiple of 4 (got %d)", ql::kAttnMaxD, D);
+    if ((int64_t)past_len + M > max_t)
+        return fail(QL_E_RANGE, "context length %lld exceeds the cache's %d positions", (long long)past_len + M, max_t);
+    if ((int64_t)past_len + M > ql::kAttnMaxT)
+        return fail(QL_E_INVALID, "context length %lld above the supported %d", (long long)past_len + M, ql::kAttnMaxT);
+    const uint64_t qo = (uint64_t)M * n_head * D * 4, cb = (uint64_t)max_t * n_kv_head * D * 4;
+    if (!in_range(q_off, qo, act->size)) return fail(QL_E_RANGE, "q [M, n_head, D] outside the activation arena");
+    if (!in_range(out_off, qo, act->size)) return fail(QL_E_RANGE, "out [M, n_head, D] outside the activation arena");
+    if (!in_range(k_off, cb, cache->size) || !in_range(v_off, cb, cache->size))
+        return fail(QL_E_RANGE, "K/V cache [max_t, n_kv_head * D] outside its arena");
+    if (q_off % 16 || out_off % 16 || k_off % 16 || v_off % 16) return fail(QL_E_ALIGN, "offsets must be 16-byte aligned");
+    if (q_off < out_off + qo && out_off < q_off + qo) return fail(QL_E_INVALID, "q and out overlap");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    ql::AttnArgs a;
+    a.q = reinterpret_cast<const float*>(act->base + q_off);
+    a.k = reinterpret_cast<const float*>(cache->base + k_off);
+    a.v = reinterpret_cast<const float*>(cache->base + v_off);
+    a.out = reinterpret_cast<float*>(act->base + out_off);
+    a.ws = ctx->attn_ws;
+    a.M = M;
+    a.H = n_head;
+    a.KV = n_kv_head;
+    a.G = n_head / n_kv_head;
+    a.D = D;
+    a.past = past_len;
+    a.scale = (float)(1.0 / std::sqrt((double)D));
+    if (ql::plan_attention(&a)) return fail(QL_E_INVALID, "attention shape does not fit the workspace");
+    QL_HIP(ql::launch_attention(a, ctx->stream));
     return QL_OK;
 }
 

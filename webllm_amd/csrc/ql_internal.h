@@ -125,6 +125,26 @@ bool gemv_f16w_fast_ok(int M, int N, int K);
 size_t gemv_f16w_lds(int M, int K);
 hipError_t launch_gemv_f16w(const F16wArgs& a, bool fast, int cu_count, hipStream_t stream);
 
+// Decode attention over an fp32 KV cache [max_t, KV * D] and the cache store.
+constexpr int kAttnMaxT = 8192;        // visible keys per query row
+constexpr int kAttnMaxD = 256;
+constexpr size_t kAttnWsBytes = 4u << 20;   // context workspace for key-split partials
+struct AttnArgs {
+    const float* q;            // [M, H, D]
+    const float* k;            // cache [max_t, KV * D]
+    const float* v;
+    float* out;                // [M, H, D]
+    float* ws;                 // key-split partials: [M, H, nsplit, D] sums, then [.., 2] max/sum
+    int M, H, KV, G, D, past;
+    float scale;               // fp32(1 / sqrt(D))
+    // plan_attention fills these
+    int gm, nj;                // kernel variant: heads per run (template), 64-float pieces of D
+    int heads_per_run, runs_per_group, nsplit, chunk_cap;
+};
+int plan_attention(AttnArgs* a);
+hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+hipError_t launch_kv_store(const float* src, float* dst, int rows, int row_len, int pos0, hipStream_t stream);
+
 // ----------------------------------------------------------------------------------------------
 // Linear sequences: many decode linears (M <= 16) in one persistent launch. Linear i may read the
 // output of an earlier linear; the kernel orders them on the device.

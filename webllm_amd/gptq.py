@@ -234,6 +234,54 @@ class ActivationArena:
 
 
 @dataclass
+class KvCache:
+    """Per-layer fp32 K and V caches [block_size, n_kv_head * D] in one device arena, and the
+    decode attention over them: QwenGpt's kCache/vCache (qwen.ts:140-141, :200-205), kv store
+    (qwen.ts:427-428) and attention_gqa_cache dispatch (qwen.ts:429-440). Stream order replaces
+    the reference's pass breaks."""
+
+    def __init__(self, ctx: ql.Context, config: QwenConfig):
+        self.ctx = ctx
+        self.config = config
+        self.D = qwen_head_dim(config)
+        self.row_len = qwen_kv_dim(config)
+        self.region = -(-config.block_size * self.row_len * 4 // 256) * 256
+        self.arena = ctx.arena(2 * config.n_layer * self.region)
+        self.length = 0                                           # cacheLen (qwen.ts:142)
+
+    def offsets(self, layer: int):
+        if not 0 <= layer < self.config.n_layer:
+            raise ValueError(f"layer {layer} out of range")
+        base = 2 * layer * self.region
+        return base, base + self.region
+
+    def store(self, layer: int, k: Tensor, v: Tensor, rows: int, pos0: int):
+        """cache[pos0 + r] = k[r] / v[r] for r < rows (after RoPE on k, as the reference)."""
+        if k.length < rows * self.row_len or v.length < rows * self.row_len:
+            raise ValueError("kv store: k/v tensors smaller than [rows, n_kv_head * D]")
+        ko, vo = self.offsets(layer)
+        for t, off in ((k, ko), (v, vo)):
+            self.ctx.kv_store(t.arena, t.offset, self.arena, off, self.config.block_size, rows,
+                              self.row_len, pos0)
+
+    def attend(self, layer: int, q: Tensor, out: Tensor, M: int, past_len: int):
+        """out [M, n_head * D] = causal GQA attention of q's M rows at positions past_len + m."""
+        c = self.config
+        if q.length < M * c.n_head * self.D or out.length < M * c.n_head * self.D:
+            raise ValueError("attention: q/out smaller than [M, n_head * D]")
+        if q.arena is not out.arena:
+            raise ValueError("attention: q and out must live in the same activation arena")
+        ko, vo = self.offsets(layer)
+        self.ctx.attention_decode(q.arena, q.offset, self.arena, ko, vo, c.block_size, M, c.n_head,
+                                  c.n_kv_head, self.D, past_len, out.offset)
+
+    def reset(self):
+        self.length = 0
+
+    def release(self):
+        self.arena.release()
+
+
 class _Linear:
     desc: ql.GptqDesc
     K: int

@@ -115,6 +115,8 @@ def lib():
         "ql_unpack_f16_batch": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64)]),
         "ql_plan_linear": (I, [I, I, I, I, ctypes.POINTER(Plan)]),
         "ql_gemv_f16w": (I, [P, P, U64, U64, P, U64, I, I, I, U64]),
+        "ql_kv_store": (I, [P, P, U64, P, U64, I, I, I, I]),
+        "ql_attention_decode": (I, [P, P, U64, P, U64, U64, I, I, I, I, I, I, U64]),
         "ql_linear": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64, I, I, U64, U64]),
         "ql_plan_batch": (I, [I, ctypes.POINTER(GptqDesc), I, ctypes.POINTER(U64)]),
         "ql_linear_batch": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64), I, I,
@@ -319,6 +321,18 @@ class Context:
         _check(lib().ql_gemv_f16w(self.handle, weights.handle, w_off,
                                   QL_NONE if bias_off is None else bias_off, act.handle, x_off, M, N,
                                   K, y_off))
+
+    def kv_store(self, act: Arena, src_off: int, cache: Arena, cache_off: int, max_t: int, rows: int,
+                 row_len: int, pos0: int):
+        """cache[pos0 + r, :] = src[r, :] (misc/kv_store.wgsl; qwen.ts:427-428)."""
+        _check(lib().ql_kv_store(self.handle, act.handle, src_off, cache.handle, cache_off, max_t, rows,
+                                 row_len, pos0))
+
+    def attention_decode(self, act: Arena, q_off: int, cache: Arena, k_off: int, v_off: int, max_t: int,
+                         M: int, n_head: int, n_kv_head: int, D: int, past_len: int, out_off: int):
+        """Causal GQA attention of M new query rows over the KV cache (attention_gqa_cache.wgsl)."""
+        _check(lib().ql_attention_decode(self.handle, act.handle, q_off, cache.handle, k_off, v_off,
+                                         max_t, M, n_head, n_kv_head, D, past_len, out_off))
 
     def unpack_f32(self, desc: GptqDesc, weights: Arena, out: Arena, out_off: int):
         _check(lib().ql_unpack_f32(self.handle, ctypes.byref(desc), weights.handle, out.handle,
