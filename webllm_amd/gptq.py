@@ -233,7 +233,6 @@ class ActivationArena:
         self.layout = ql.ArenaLayout()
 
 
-@dataclass
 class KvCache:
     """Per-layer fp32 K and V caches [block_size, n_kv_head * D] in one device arena, and the
     decode attention over them: QwenGpt's kCache/vCache (qwen.ts:140-141, :200-205), kv store
@@ -282,6 +281,7 @@ class KvCache:
         self.arena.release()
 
 
+@dataclass
 class _Linear:
     desc: ql.GptqDesc
     K: int
