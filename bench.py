@@ -387,7 +387,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    help="all | step05 | headline | step7b | north | sweep | prefill | unpack | lmhead | attn "
+                    help="all | step05 | headline | step7b | north | sweep | prefill | unpack | lmhead | attn | elem "
                          "(subsets for profiling: headline = the 0.5B step and its MALL-flushed "
                          "timing only; north = the 7B-shaped step at M=1 only)")
     ap.add_argument("--m7b", default="1,2,4,8,16", help="decode batch sizes for the 7B-shaped step")
@@ -528,6 +528,49 @@ def main():
         lm["note"] = "fp16 W [151936, 896] (272 MB, read once per decode step), fp32 x and y; graph-replayed launches"
         extra["lmhead05"] = lm
         log(f"lm_head GEMV: {lm}")
+
+    if only in ("all", "elem"):
+        # the elementwise work of a decode layer: residual add + RMSNorm (twice per layer) and
+        # SiLU-mul, at the 0.5B and 7B widths, M = 1, every layer of a step
+        el = {}
+        for name, L, C, I in (("05b", 24, 896, 4864), ("7b", 28, 3584, 18944)):
+            rng = np.random.default_rng(0xE1)
+            wa = ctx.arena(C * 4)
+            wa.write(0, rng.standard_normal(C).astype(np.float32))
+            rb, ib = (C * 4 + 255) // 256 * 256, (I * 4 + 255) // 256 * 256
+            act = ctx.arena(4 * rb + 3 * ib)
+            act.write(0, rng.standard_normal(C).astype(np.float32))
+            act.write(rb, rng.standard_normal(C).astype(np.float32))
+            act.write(4 * rb, rng.standard_normal(I).astype(np.float32))
+            act.write(4 * rb + ib, rng.standard_normal(I).astype(np.float32))
+
+            def issue():
+                for _ in range(L):
+                    ctx.add_rmsnorm(act, 0, rb, wa, 0, 1e-6, 1, C, 3 * rb, 2 * rb)
+                    ctx.add_rmsnorm(act, 0, rb, wa, 0, 1e-6, 1, C, 3 * rb, 2 * rb)
+                    ctx.silu_mul(act, 4 * rb, 4 * rb + ib, I, 4 * rb + 2 * ib)
+            issue()
+            ctx.sync()
+            ctx.graph_begin()
+            issue()
+            g = ctx.graph_end()
+            for _ in range(3):
+                g.launch()
+            ctx.timer_start()
+            reps = max(20, args.steps)
+            for _ in range(reps):
+                g.launch()
+            ms = ctx.timer_stop() / reps
+            nbytes = L * (2 * (5 * C * 4) + 3 * I * 4)
+            el[name] = {"us_per_step": round(ms * 1e3, 1), "us_per_layer": round(ms * 1e3 / L, 2),
+                        "launches_per_layer": 3, "bytes": nbytes}
+            g.destroy()
+            act.release()
+            wa.release()
+        el["note"] = ("per layer: two fused residual-add + RMSNorm launches (x, d, w read; sum, y "
+                      "written) and one SiLU-mul; the reference runs 5 launches for the same work")
+        extra["elem"] = el
+        log(f"elementwise: {el}")
 
     if only in ("all", "attn"):
         # decode attention over the KV cache, every layer of a step (qwen.ts:424-442): the

@@ -181,6 +181,18 @@ int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_are
                         uint64_t v_off, int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D,
                         int32_t past_len, uint64_t out_off);
 
+/* ---- the elementwise work around the linears (qwen.ts:401-405, :447-478).
+ * ql_add_rmsnorm: s = x + d (misc/vec_add.wgsl: the residual add after o_proj / down_proj), stored
+ *   at sum_off unless QL_NONE, then y = s * rstd * w, rstd = 1 / sqrt(mean(s^2) + eps)
+ *   (norm/rmsnorm.wgsl; CPU form reference/qwen-ref.ts:12-28). d_off = QL_NONE: plain RMSNorm of x.
+ *   One launch where the reference runs two; fp32; x, d, sum, y [M, C] in `act`, w [C] in
+ *   `weights`; offsets 4-byte aligned (16-byte and C % 4 == 0 take the vector path). */
+int ql_add_rmsnorm(ql_ctx* ctx, ql_arena* act, uint64_t x_off, uint64_t d_off, const ql_arena* weights,
+                   uint64_t w_off, float eps, int32_t M, int32_t C, uint64_t sum_off, uint64_t y_off);
+/* ql_silu_mul: y[i] = (g / (1 + exp(-g))) * up[i], g = gate[i] (activation/silu_mul.wgsl;
+ *   siluMulRef, qwen-ref.ts:114-121); offsets 16-byte aligned. */
+int ql_silu_mul(ql_ctx* ctx, ql_arena* act, uint64_t gate_off, uint64_t up_off, int64_t n, uint64_t y_off);
+
 /* several independent linears in one launch (e.g. q/k/v on one input, gate/up on another);
  * linear i reads x_offs[i] and writes y_offs[i]; scratch for all of them starts at scratch_off
  * (ql_plan_batch gives the size). M and x_dtype are shared; at most 8 linears. */

@@ -343,3 +343,34 @@ int orc_attention_gqa_cache(const float* q, const float* kc, const float* vc, in
     free(scores);
     return 0;
 }
+
+/* rmsNormRef (src/reference/qwen-ref.ts:12-28) after the residual add of vec_add.wgsl:
+ * s = f32(x + d) (d may be NULL), sum of s^2 in double, rstd = 1 / sqrt(sum / D + eps) in double,
+ * out = f32(s * rstd * w) evaluated left to right in double. */
+void orc_add_rmsnorm(const float* x, const float* d, const float* w, int rows, int D, double eps, float* s_out,
+                     float* out)
+{
+    for (int r = 0; r < rows; r++) {
+        const size_t base = (size_t)r * D;
+        double sum = 0.0;
+        for (int i = 0; i < D; i++) {
+            const float v = d ? x[base + i] + d[base + i] : x[base + i];
+            if (s_out) s_out[base + i] = v;
+            sum += (double)v * (double)v;
+        }
+        const double rstd = 1.0 / sqrt(sum / D + eps);
+        for (int i = 0; i < D; i++) {
+            const float v = d ? x[base + i] + d[base + i] : x[base + i];
+            out[base + i] = (float)((double)v * rstd * (double)w[i]);
+        }
+    }
+}
+
+/* siluMulRef (qwen-ref.ts:114-121): out = f32((g / (1 + exp(-g))) * u) in double. */
+void orc_silu_mul(const float* gate, const float* up, size_t n, float* out)
+{
+    for (size_t i = 0; i < n; i++) {
+        const double g = gate[i];
+        out[i] = (float)((g / (1.0 + exp(-g))) * (double)up[i]);
+    }
+}

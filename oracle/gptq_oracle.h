@@ -61,6 +61,11 @@ int orc_dequant_gptq_int4_f16(const uint8_t* qweight, size_t qweight_bytes,
 
 void orc_gemm_nt(const float* A, const float* W, int M, int N, int K, const float* bias, float* C);
 
+/* rmsNormRef (qwen-ref.ts:12-28) after an optional residual add; siluMulRef (:114-121). */
+void orc_add_rmsnorm(const float* x, const float* d, const float* w, int rows, int D, double eps, float* s_out,
+                     float* out);
+void orc_silu_mul(const float* gate, const float* up, size_t n, float* out);
+
 /* attentionGqaRef (qwen-ref.ts:65-111) over a KV cache: q [M,H,D], caches [past+M, KV*D]. */
 int orc_attention_gqa_cache(const float* q, const float* kc, const float* vc, int M, int H, int KV, int D,
                             int past, float* out);

@@ -10,6 +10,8 @@ The oracle restates the reference CPU path (intplusplus/webllm):
   gemmNTRef               src/reference/qwen-ref.ts:126-145
   planGemvSplit           src/model/qwen.ts:61-74
   checkTolerance/makeRng  src/reference/cpu-ref.ts:27-67
+  rmsNormRef (+ vec_add)  src/reference/qwen-ref.ts:12-28, src/gpu/kernels/misc/vec_add.wgsl
+  siluMulRef              src/reference/qwen-ref.ts:114-121
   attentionGqaRef         src/reference/qwen-ref.ts:65-111 (over a KV cache, with the positions of
                           src/gpu/kernels/attention/attention_gqa_cache.wgsl)
 """
@@ -70,6 +72,10 @@ def lib():
                                       ctypes.c_int, P]
         L.orc_plan_gemv_split.restype = ctypes.c_int
         L.orc_plan_gemv_split.argtypes = [ctypes.c_int, ctypes.c_int]
+        L.orc_add_rmsnorm.restype = None
+        L.orc_add_rmsnorm.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_double, P, P]
+        L.orc_silu_mul.restype = None
+        L.orc_silu_mul.argtypes = [P, P, ctypes.c_size_t, P]
         L.orc_attention_gqa_cache.restype = ctypes.c_int
         L.orc_attention_gqa_cache.argtypes = [P, P, P] + [ctypes.c_int] * 5 + [P]
         L.orc_check_tolerance.restype = ctypes.c_int
@@ -171,6 +177,26 @@ def gptq_linear(qweight, qzeros, scales_f16, x, bias=None, group: int = 128) -> 
     if rc != 0:
         raise ValueError("oracle gptq_linear: bad arguments")
     return y
+
+
+def add_rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, d: np.ndarray | None = None):
+    """(s, y): s = x + d (or x), y = rmsNormRef(s, w, eps) over the rows of [M, C]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, C = x.shape
+    dd = None if d is None else np.ascontiguousarray(d, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    s = np.empty_like(x)
+    y = np.empty_like(x)
+    lib().orc_add_rmsnorm(_ptr(x), _ptr(dd), _ptr(w), M, C, eps, _ptr(s), _ptr(y))
+    return s, y
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(gate, dtype=np.float32).reshape(-1)
+    u = np.ascontiguousarray(up, dtype=np.float32).reshape(-1)
+    out = np.empty_like(g)
+    lib().orc_silu_mul(_ptr(g), _ptr(u), g.size, _ptr(out))
+    return out.reshape(np.shape(gate))
 
 
 def attention_gqa_cache(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, H: int, KV: int, D: int,

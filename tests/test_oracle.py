@@ -331,3 +331,34 @@ def test_attention_oracle_special_cases(orc):
     for h in range(H):
         kvh = h // (H // KV)
         assert np.allclose(got[0, h], vc[:, kvh * D:(kvh + 1) * D].astype(np.float64).mean(0), atol=1e-6)
+
+
+def test_rmsnorm_oracle_vs_textbook(orc):
+    """rmsNormRef restated, against x / sqrt(mean(x^2) + eps) * w in float64 (numpy), with and
+    without the residual add; a constant row c gives c / sqrt(c^2 + eps) * w."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((5, 896)).astype(np.float32)
+    d = rng.standard_normal((5, 896)).astype(np.float32)
+    w = rng.standard_normal(896).astype(np.float32)
+    for dd in (None, d):
+        s, y = orc.add_rmsnorm(x, w, 1e-6, dd)
+        s64 = x.astype(np.float64) + (0 if dd is None else dd.astype(np.float64))
+        assert np.array_equal(s, (x + d) if dd is not None else x)
+        ref = s.astype(np.float64) / np.sqrt((s.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * w
+        assert np.allclose(y, ref, rtol=2e-7, atol=1e-7)
+        assert np.allclose(s, s64, rtol=1e-7)
+    c = np.full((1, 64), 3.0, np.float32)
+    _, y = orc.add_rmsnorm(c, np.ones(64, np.float32), 1e-6)
+    assert np.allclose(y, 3.0 / np.sqrt(9.0 + 1e-6), rtol=1e-7)
+
+
+def test_silu_mul_oracle_vs_expit(orc):
+    """siluMulRef restated, against scipy's logistic function: g * expit(g) * u; silu(0) = 0."""
+    from scipy.special import expit
+    rng = np.random.default_rng(12)
+    g = (rng.standard_normal(4097) * 6).astype(np.float32)
+    u = rng.standard_normal(4097).astype(np.float32)
+    got = orc.silu_mul(g, u)
+    ref = g.astype(np.float64) * expit(g.astype(np.float64)) * u
+    assert np.allclose(got, ref, rtol=2e-7, atol=1e-30)
+    assert orc.silu_mul(np.zeros(3, np.float32), np.ones(3, np.float32)).tolist() == [0.0, 0.0, 0.0]

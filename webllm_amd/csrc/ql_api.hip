@@ -914,6 +914,56 @@ int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_are
     return QL_OK;
 }
 
+int ql_add_rmsnorm(ql_ctx* ctx, ql_arena* act, uint64_t x_off, uint64_t d_off, const ql_arena* weights,
+                   uint64_t w_off, float eps, int32_t M, int32_t C, uint64_t sum_off, uint64_t y_off)
+{
+    if (!ctx || !act || !weights) return fail(QL_E_INVALID, "null context or arena");
+    if (M < 1 || M > 65535 || C < 1 || C > (1 << 24)) return fail(QL_E_INVALID, "M must be 1..65535 and C 1..2^24");
+    if (!(eps >= 0.f)) return fail(QL_E_INVALID, "eps must be >= 0");
+    const uint64_t rb = (uint64_t)M * C * 4;
+    if (!in_range(x_off, rb, act->size) || !in_range(y_off, rb, act->size) ||
+        (d_off != QL_NONE && !in_range(d_off, rb, act->size)) || (sum_off != QL_NONE && !in_range(sum_off, rb, act->size)))
+        return fail(QL_E_RANGE, "x, d, sum or y [M, C] outside the activation arena");
+    if (!in_range(w_off, (uint64_t)C * 4, weights->size)) return fail(QL_E_RANGE, "norm weight [C] outside the weight arena");
+    if (sum_off != QL_NONE && d_off == QL_NONE) return fail(QL_E_INVALID, "sum_off needs d_off (the sum is x + d)");
+    if (x_off % 4 || y_off % 4 || w_off % 4 || (d_off != QL_NONE && d_off % 4) || (sum_off != QL_NONE && sum_off % 4))
+        return fail(QL_E_ALIGN, "offsets must be 4-byte aligned");
+    const uint64_t ya = y_off, yb = y_off + rb;
+    auto overlaps = [&](uint64_t o) { return o != QL_NONE && o < yb && ya < o + rb; };
+    if (overlaps(x_off) || overlaps(d_off) || overlaps(sum_off)) return fail(QL_E_INVALID, "y overlaps an input or the sum");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    ql::ElemArgs a;
+    a.x = reinterpret_cast<const float*>(act->base + x_off);
+    a.d = d_off == QL_NONE ? nullptr : reinterpret_cast<const float*>(act->base + d_off);
+    a.w = reinterpret_cast<const float*>(weights->base + w_off);
+    a.s = sum_off == QL_NONE ? nullptr : reinterpret_cast<float*>(act->base + sum_off);
+    a.y = reinterpret_cast<float*>(act->base + y_off);
+    a.M = M;
+    a.C = C;
+    a.eps = eps;
+    a.vec = C % 4 == 0 && x_off % 16 == 0 && y_off % 16 == 0 && w_off % 16 == 0 &&
+            (d_off == QL_NONE || d_off % 16 == 0) && (sum_off == QL_NONE || sum_off % 16 == 0);
+    QL_HIP(ql::launch_add_rmsnorm(a, ctx->stream));
+    return QL_OK;
+}
+
+int ql_silu_mul(ql_ctx* ctx, ql_arena* act, uint64_t gate_off, uint64_t up_off, int64_t n, uint64_t y_off)
+{
+    if (!ctx || !act) return fail(QL_E_INVALID, "null context or arena");
+    if (n < 1 || n > (1ll << 34)) return fail(QL_E_INVALID, "n out of range");
+    const uint64_t b = (uint64_t)n * 4;
+    if (!in_range(gate_off, b, act->size) || !in_range(up_off, b, act->size) || !in_range(y_off, b, act->size))
+        return fail(QL_E_RANGE, "gate, up or y [n] outside the activation arena");
+    if (gate_off % 16 || up_off % 16 || y_off % 16) return fail(QL_E_ALIGN, "offsets must be 16-byte aligned");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    QL_HIP(ql::launch_silu_mul(reinterpret_cast<const float*>(act->base + gate_off),
+                               reinterpret_cast<const float*>(act->base + up_off),
+                               reinterpret_cast<float*>(act->base + y_off), n, ctx->stream));
+    return QL_OK;
+}
+
 int ql_plan_batch(int32_t count, const ql_gptq_desc* descs, int32_t M, uint64_t* scratch_bytes)
 {
     if (!descs || !scratch_bytes || count <= 0 || count > ql::kMaxBatch)

@@ -142,6 +142,20 @@ struct AttnArgs {
     int heads_per_run, runs_per_group, nsplit, chunk_cap;
 };
 int plan_attention(AttnArgs* a);
+
+// Residual add + RMSNorm, SiLU-mul.
+struct ElemArgs {
+    const float* x;            // [M, C]
+    const float* d;            // [M, C] added to x, or nullptr
+    const float* w;            // [C] norm weight
+    float* s;                  // x + d stored here (nullptr: not stored)
+    float* y;                  // [M, C]
+    int M, C;
+    float eps;
+    int vec;                   // C % 4 == 0 and every pointer 16-byte aligned: f32x4 path
+};
+hipError_t launch_add_rmsnorm(const ElemArgs& a, hipStream_t stream);
+hipError_t launch_silu_mul(const float* gate, const float* up, float* y, long long n, hipStream_t stream);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_kv_store(const float* src, float* dst, int rows, int row_len, int pos0, hipStream_t stream);
 

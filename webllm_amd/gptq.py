@@ -374,6 +374,29 @@ class QuantLinearModel:
         self.ctx.linear(desc, self.weights, A.arena, A.offset,
                         ql.DTYPE_F32 if A.dtype == "f32" else ql.DTYPE_F16, M, C.offset, scratch)
 
+    def rmsnorm(self, x: Tensor, weight: str, y: Tensor, M: int, C: int, eps: float,
+                residual: Tensor | None = None, sum_out: Tensor | None = None):
+        """y = rmsnorm(x (+ residual)) * weight (rmsnorm.wgsl, qwen.ts:403-404, :456-457); with
+        `residual` the add of vec_add.wgsl (qwen.ts:475-476) runs in the same launch and the sum
+        goes to `sum_out` (the next residual stream) when given."""
+        w = self.f32.get(weight)
+        if w is None:
+            raise ValueError(f"missing f32 weight: {weight}")
+        if w.length != C:
+            raise ValueError(f"rmsnorm: {weight} has {w.length} values, C={C}")
+        ts = [t for t in (x, y, residual, sum_out) if t is not None]
+        if any(t.arena is not x.arena for t in ts) or any(t.length < M * C for t in ts):
+            raise ValueError("rmsnorm: tensors must be [M, C] in one activation arena")
+        self.ctx.add_rmsnorm(x.arena, x.offset, None if residual is None else residual.offset, self.weights,
+                             w.offset, eps, M, C, y.offset, None if sum_out is None else sum_out.offset)
+
+    def silu_mul(self, gate: Tensor, up: Tensor, out: Tensor, n: int):
+        """out = silu(gate) * up (silu_mul.wgsl, qwen.ts:468-469)."""
+        ts = (gate, up, out)
+        if any(t.arena is not gate.arena for t in ts) or any(t.length < n for t in ts):
+            raise ValueError("silu_mul: tensors must hold n values in one activation arena")
+        self.ctx.silu_mul(gate.arena, gate.offset, up.offset, n, out.offset)
+
     def _gemm_f16(self, A: Tensor, weight: str, C: Tensor, bias: str | None, M: int, N: int, K: int):
         """C[M,N] = A[M,K] @ W^T (+ bias) over an fp16 weight [N,K] (the tied lm_head `embed`,
         qwen.ts:488-489 with gemm_gemv_f16.wgsl semantics): f32 A and C, fp32 accumulation."""

@@ -116,6 +116,8 @@ def lib():
         "ql_plan_linear": (I, [I, I, I, I, ctypes.POINTER(Plan)]),
         "ql_gemv_f16w": (I, [P, P, U64, U64, P, U64, I, I, I, U64]),
         "ql_kv_store": (I, [P, P, U64, P, U64, I, I, I, I]),
+        "ql_add_rmsnorm": (I, [P, P, U64, U64, P, U64, ctypes.c_float, I, I, U64, U64]),
+        "ql_silu_mul": (I, [P, P, U64, U64, ctypes.c_int64, U64]),
         "ql_attention_decode": (I, [P, P, U64, P, U64, U64, I, I, I, I, I, I, U64]),
         "ql_linear": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64, I, I, U64, U64]),
         "ql_plan_batch": (I, [I, ctypes.POINTER(GptqDesc), I, ctypes.POINTER(U64)]),
@@ -333,6 +335,17 @@ class Context:
         """Causal GQA attention of M new query rows over the KV cache (attention_gqa_cache.wgsl)."""
         _check(lib().ql_attention_decode(self.handle, act.handle, q_off, cache.handle, k_off, v_off,
                                          max_t, M, n_head, n_kv_head, D, past_len, out_off))
+
+    def add_rmsnorm(self, act: Arena, x_off: int, d_off, weights: Arena, w_off: int, eps: float, M: int,
+                    C: int, y_off: int, sum_off=None):
+        """y = rmsnorm(x (+ d)) * w, the sum stored at sum_off (vec_add + rmsnorm.wgsl in one launch)."""
+        _check(lib().ql_add_rmsnorm(self.handle, act.handle, x_off, QL_NONE if d_off is None else d_off,
+                                    weights.handle, w_off, eps, M, C,
+                                    QL_NONE if sum_off is None else sum_off, y_off))
+
+    def silu_mul(self, act: Arena, gate_off: int, up_off: int, n: int, y_off: int):
+        """y = silu(gate) * up (activation/silu_mul.wgsl)."""
+        _check(lib().ql_silu_mul(self.handle, act.handle, gate_off, up_off, n, y_off))
 
     def unpack_f32(self, desc: GptqDesc, weights: Arena, out: Arena, out_off: int):
         _check(lib().ql_unpack_f32(self.handle, ctypes.byref(desc), weights.handle, out.handle,
