@@ -24,7 +24,8 @@ NORM_CASES = [
     # (M, C, residual, store_sum, x offset pad (bytes), label)
     (1, 896, True, True, 0, "0.5B decode: add after o_proj, norm before gate/up"),
     (1, 896, False, False, 0, "0.5B: plain RMSNorm (layer input)"),
-    (16, 3584, True, True, 0, "7B width, 16 rows"),
+    (16, 3584, True, True, 0, "7B width, 16 rows (row kept in registers)"),
+    (2, 8192, True, True, 0, "C = 8192: rows read twice"),
     (3, 900, True, False, 0, "C % 4 != 0: scalar path"),
     (2, 896, True, True, 4, "4-byte aligned offsets: scalar path"),
 ]

@@ -7,6 +7,8 @@
 //                       (the RMSNorm in front of q/k/v, gate/up or lm_head); without d it is the
 //                       plain RMSNorm. One workgroup per row; the row's sum of squares is added
 //                       per thread, then per wave (butterfly), then over the 4 waves in order.
+//                       Rows up to 4096 values stay in registers (one read of x, d and w); longer
+//                       rows read x and d a second time for the output.
 //   silu_mul_kernel     y = (g / (1 + exp(-g))) * u, four values per thread.
 //
 // Both are HBM-bound streams (bytes per row: x, d, s and y once; per element of silu_mul: g, u, y).
@@ -20,6 +22,8 @@ namespace ql {
 
 namespace {
 
+constexpr int kKeep = 4;     // 16-byte pieces of a row kept per thread: rows up to 4096 values
+
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const ElemArgs a)
 {
     __shared__ float red[4];
@@ -29,6 +33,40 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const ElemArgs a)
     float* s_out = a.s ? a.s + (size_t)row * C : nullptr;
     float* y = a.y + (size_t)row * C;
     float ss = 0.f;
+    if (a.vec && C <= 4 * 256 * kKeep) {
+        // one pass over HBM: the row (and the weight) stay in registers across the reduction
+        f32x4 v[kKeep], g[kKeep];
+#pragma unroll
+        for (int k = 0; k < kKeep; k++) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < C / 4) {
+                v[k] = ld_global(reinterpret_cast<const f32x4*>(x) + i);
+                g[k] = ld_global(reinterpret_cast<const f32x4*>(a.w) + i);
+                if (d) {
+                    const f32x4 e = ld_global(reinterpret_cast<const f32x4*>(d) + i);
+                    v[k] = f32x4{v[k].x + e.x, v[k].y + e.y, v[k].z + e.z, v[k].w + e.w};
+                    if (s_out) st_global(reinterpret_cast<f32x4*>(s_out) + i, v[k]);
+                }
+                ss = fmaf(v[k].x, v[k].x, ss);
+                ss = fmaf(v[k].y, v[k].y, ss);
+                ss = fmaf(v[k].z, v[k].z, ss);
+                ss = fmaf(v[k].w, v[k].w, ss);
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        const float rstd = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)C + a.eps);
+#pragma unroll
+        for (int k = 0; k < kKeep; k++) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < C / 4)
+                st_global(reinterpret_cast<f32x4*>(y) + i, f32x4{v[k].x * rstd * g[k].x, v[k].y * rstd * g[k].y,
+                                                                 v[k].z * rstd * g[k].z, v[k].w * rstd * g[k].w});
+        }
+        return;
+    }
     if (a.vec) {
         for (int i = threadIdx.x; i < C / 4; i += 256) {
             f32x4 v = ld_global(reinterpret_cast<const f32x4*>(x) + i);
