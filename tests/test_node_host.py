@@ -36,6 +36,8 @@ BINDING = {
     "graphBegin": "ql_graph_begin", "graphEnd": "ql_graph_end", "graphLaunch": "ql_graph_launch",
     "graphDestroy": "ql_graph_destroy", "seqCreate": "ql_seq_create", "seqRun": "ql_seq_run",
     "seqStatus": "ql_seq_status", "seqInfo": "ql_seq_get_info", "seqDestroy": "ql_seq_destroy",
+    "gemvF16w": "ql_gemv_f16w", "kvStore": "ql_kv_store", "attention": "ql_attention_decode",
+    "addRmsNorm": "ql_add_rmsnorm", "siluMul": "ql_silu_mul",
 }
 
 
@@ -93,6 +95,13 @@ def test_node_host_matches_oracle(tmp_path, orc):
         cases["gemm"].append({"weight": f"L0.{key}", "M": M, "N": N, "K": K, "bias": bias,
                               "f16": f16, "x": f"x{i}", "out": f"y{i}.f32"})
         refs[f"y{i}.f32"] = (orc.gptq_linear(t.qweight, t.qzeros, t.scales, x, b), M >= 17)
+    emb = kept["embed"]                      # the tied lm_head over the fp16 embedding (qwen.ts:488-489)
+    for j, M in enumerate((1, 5)):
+        x = synth.activations(M, TINY.n_embd, seed=0x40E0, key=(M,))
+        x.tofile(tmp_path / f"xe{j}")
+        cases["gemm"].append({"weight": "embed", "M": M, "N": TINY.vocab_size, "K": TINY.n_embd, "bias": None,
+                              "f16": False, "x": f"xe{j}", "out": f"ye{j}.f32"})
+        refs[f"ye{j}.f32"] = (orc.gemm_nt(x, emb.astype(np.float32)), False)
     xb = synth.activations(2, TINY.n_embd, seed=0x40DF)
     xb.tofile(tmp_path / "xb")
     names = ["qW", "kW", "vW"]

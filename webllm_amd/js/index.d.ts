@@ -99,10 +99,25 @@ export class QuantLinearModel {
     /** QwenGpt.gemm: C[M,N] = A[M,K] @ W^T (+ bias). */
     gemm(A: Tensor, weight: string, C: Tensor, bias: string | null, M: number, N: number, K: number): void;
     gemmBatch(A: Tensor, weights: string[], Cs: Tensor[], M: number): void;
+    /** y = rmsnorm(x (+ residual)) * weight, the sum stored in sumOut (one launch: ql_add_rmsnorm). */
+    rmsnorm(x: Tensor, weight: string, y: Tensor, M: number, C: number, eps: number,
+            residual?: Tensor | null, sumOut?: Tensor | null): void;
+    /** out = silu(gate) * up (ql_silu_mul). */
+    siluMul(gate: Tensor, up: Tensor, out: Tensor, n: number): void;
     unpackF16(name: string, out: Tensor): void;
     /** fp16 [N,K] copies of many weights in a few launches (ql_unpack_f16_batch). */
     unpackAllF16(names: string[], outs: Tensor[]): void;
     dequantize(name: string): Float32Array;
+    release(): void;
+}
+
+/** Per-layer fp32 K/V caches and decode attention (qwen.ts:200-205, :427-440). */
+export class KvCache {
+    constructor(ctx: Context, config: QwenConfig);
+    readonly D: number;
+    readonly rowLen: number;
+    store(layer: number, k: Tensor, v: Tensor, rows: number, pos0: number): void;
+    attend(layer: number, q: Tensor, out: Tensor, M: number, pastLen: number): void;
     release(): void;
 }
 

@@ -414,6 +414,7 @@ class QuantLinearModel {
     }
     /** C[M,N] = A[M,K] @ W^T (+ bias) — qwen.ts:568-618. A f32 or f16, C f32. */
     gemm(A, weight, C, bias, M, N, K) {
+        if (this.f16Weights.has(weight) && !this.linears.has(weight)) return this._gemmF16(A, weight, C, bias, M, N, K);
         const lin = this.linear(weight);
         if (lin.K !== K || lin.N !== N) throw new Error(`gemm: ${weight} is [${lin.N},${lin.K}], called with N=${N} K=${K}`);
         if (bias !== null && bias !== undefined && lin.desc.biasOff === null) throw new Error(`missing f32 weight: ${bias}`);
@@ -425,6 +426,34 @@ class QuantLinearModel {
         const scratch = A.pool.scratchOffset(plan.scratchBytes);
         addon.linear(this.ctx.handle, desc, this.weights.handle, A.arena.handle, A.offset,
             A.dtype === 'f16' ? QL_DTYPE_F16 : QL_DTYPE_F32, M, C.offset, scratch);
+    }
+    /** fp16 weights (the tied lm_head `embed`, qwen.ts:488-489): f32 A and C, fp32 accumulation. */
+    _gemmF16(A, weight, C, bias, M, N, K) {
+        const w = this.f16Weights.get(weight);
+        if (w.shape[0] !== N || w.shape[1] !== K) throw new Error(`gemm: ${weight} is [${w.shape}], called with N=${N} K=${K}`);
+        let b = null;
+        if (bias !== null && bias !== undefined) {
+            const t = this.f32Weights.get(bias);
+            if (!t) throw new Error(`missing f32 weight: ${bias}`);
+            b = t.offset;
+        }
+        if (A.dtype !== 'f32' || C.dtype !== 'f32') throw new Error('gemm over fp16 weights takes f32 A and C');
+        if (A.arena !== C.arena) throw new Error('gemm: A and C must live in the same activation arena');
+        if (A.length < M * K || C.length < M * N) throw new Error('gemm: tensor too small for [M,K] / [M,N]');
+        addon.gemvF16w(this.ctx.handle, this.weights.handle, w.offset, b, A.arena.handle, A.offset, M, N, K, C.offset);
+    }
+    /** y = rmsnorm(x (+ residual)) * weight; the sum goes to sumOut (vec_add + rmsnorm.wgsl in one launch). */
+    rmsnorm(x, weight, y, M, C, eps, residual, sumOut) {
+        const w = this.f32Weights.get(weight);
+        if (!w) throw new Error(`missing f32 weight: ${weight}`);
+        if (w.length !== C) throw new Error(`rmsnorm: ${weight} has ${w.length} values, C=${C}`);
+        addon.addRmsNorm(this.ctx.handle, x.arena.handle, x.offset, residual ? residual.offset : null,
+            this.weights.handle, w.offset, eps, M, C, sumOut ? sumOut.offset : null, y.offset);
+    }
+    /** out = silu(gate) * up (silu_mul.wgsl, qwen.ts:468-469). */
+    siluMul(gate, up, out, n) {
+        if (gate.arena !== up.arena || gate.arena !== out.arena) throw new Error('siluMul: tensors must share one arena');
+        addon.siluMul(this.ctx.handle, gate.arena.handle, gate.offset, up.offset, n, out.offset);
     }
     /** Several linears on one input in one launch (q/k/v, gate/up; qwen.ts:411-413, :464-465). */
     gemmBatch(A, weights, Cs, M) {
@@ -533,10 +562,41 @@ function loadQwenWeights(ctx, model, options) {
     return { gpuBytes: model.weightBytes, tensorCount, fileBytes: raw.byteLength, layer: kept };
 }
 
+/**
+ * Per-layer fp32 K and V caches [blockSize, nKvHead * headDim] and the decode attention over them:
+ * QwenGpt's kCache/vCache (qwen.ts:140-141, :200-205), kv_store (:427-428), attention_gqa_cache (:429-440).
+ */
+class KvCache {
+    constructor(ctx, config) {
+        this.ctx = ctx;
+        this.config = config;
+        this.D = qwenHeadDim(config);
+        this.rowLen = qwenKvDim(config);
+        this.region = Math.ceil(config.blockSize * this.rowLen * 4 / 256) * 256;
+        this.arena = ctx.arena(2 * config.nLayer * this.region);
+    }
+    offsets(layer) {
+        if (layer < 0 || layer >= this.config.nLayer) throw new Error(`layer ${layer} out of range`);
+        return [2 * layer * this.region, (2 * layer + 1) * this.region];
+    }
+    store(layer, k, v, rows, pos0) {
+        const [ko, vo] = this.offsets(layer);
+        addon.kvStore(this.ctx.handle, k.arena.handle, k.offset, this.arena.handle, ko, this.config.blockSize, rows, this.rowLen, pos0);
+        addon.kvStore(this.ctx.handle, v.arena.handle, v.offset, this.arena.handle, vo, this.config.blockSize, rows, this.rowLen, pos0);
+    }
+    attend(layer, q, out, M, pastLen) {
+        const c = this.config;
+        const [ko, vo] = this.offsets(layer);
+        addon.attention(this.ctx.handle, q.arena.handle, q.offset, this.arena.handle, ko, vo, c.blockSize, M,
+            c.nHead, c.nKvHead, this.D, pastLen, out.offset);
+    }
+    release() { this.arena.release(); }
+}
+
 module.exports = {
     addon, ADDON_PATH, QL_DTYPE_F32, QL_DTYPE_F16, QWEN25_05B, qwenHeadDim, qwenKvDim, Seq,
     dtypeByteSize, parseSafetensorsHeader, parseSafetensors, tensorCount, requireTensor,
     expectTensor, f16BitsToF32, readTensorBytes, readTensorF32, ArenaLayout, Arena, Context,
     makeDesc, dequantizeGptqInt4, Tensor, ActivationArena, QuantLinearModel,
-    qwenLinearShapes, loadQwenWeights,
+    qwenLinearShapes, loadQwenWeights, KvCache,
 };

@@ -440,6 +440,94 @@ static napi_value js_linear_batch(napi_env env, napi_callback_info info)
     return NULL;
 }
 
+/* gemvF16w(ctx, weights, wOff, biasOff|null, act, xOff, M, N, K, yOff): fp16-weight GEMV (lm_head) */
+static napi_value js_gemv_f16w(napi_env env, napi_callback_info info)
+{
+    napi_value argv[10];
+    void *ctx, *w, *act;
+    uint64_t w_off, b_off, x_off, y_off;
+    int32_t M, N, K;
+    if (get_args(env, info, 10, argv) || get_ptr(env, argv[0], &ctx) || get_ptr(env, argv[1], &w) ||
+        get_u64(env, argv[2], &w_off, 0) || get_u64(env, argv[3], &b_off, 1) || get_ptr(env, argv[4], &act) ||
+        get_u64(env, argv[5], &x_off, 0) || get_i32(env, argv[6], &M) || get_i32(env, argv[7], &N) ||
+        get_i32(env, argv[8], &K) || get_u64(env, argv[9], &y_off, 0))
+        return NULL;
+    throw_rc(env, ql_gemv_f16w((ql_ctx*)ctx, (ql_arena*)w, w_off, b_off, (ql_arena*)act, x_off, M, N, K, y_off));
+    return NULL;
+}
+
+/* kvStore(ctx, act, srcOff, cache, cacheOff, maxT, rows, rowLen, pos0) */
+static napi_value js_kv_store(napi_env env, napi_callback_info info)
+{
+    napi_value argv[9];
+    void *ctx, *act, *cache;
+    uint64_t src_off, c_off;
+    int32_t max_t, rows, row_len, pos0;
+    if (get_args(env, info, 9, argv) || get_ptr(env, argv[0], &ctx) || get_ptr(env, argv[1], &act) ||
+        get_u64(env, argv[2], &src_off, 0) || get_ptr(env, argv[3], &cache) || get_u64(env, argv[4], &c_off, 0) ||
+        get_i32(env, argv[5], &max_t) || get_i32(env, argv[6], &rows) || get_i32(env, argv[7], &row_len) ||
+        get_i32(env, argv[8], &pos0))
+        return NULL;
+    throw_rc(env, ql_kv_store((ql_ctx*)ctx, (ql_arena*)act, src_off, (ql_arena*)cache, c_off, max_t, rows, row_len, pos0));
+    return NULL;
+}
+
+/* attention(ctx, act, qOff, cache, kOff, vOff, maxT, M, nHead, nKvHead, D, pastLen, outOff) */
+static napi_value js_attention(napi_env env, napi_callback_info info)
+{
+    napi_value argv[13];
+    void *ctx, *act, *cache;
+    uint64_t q_off, k_off, v_off, o_off;
+    int32_t max_t, M, H, KV, D, past;
+    if (get_args(env, info, 13, argv) || get_ptr(env, argv[0], &ctx) || get_ptr(env, argv[1], &act) ||
+        get_u64(env, argv[2], &q_off, 0) || get_ptr(env, argv[3], &cache) || get_u64(env, argv[4], &k_off, 0) ||
+        get_u64(env, argv[5], &v_off, 0) || get_i32(env, argv[6], &max_t) || get_i32(env, argv[7], &M) ||
+        get_i32(env, argv[8], &H) || get_i32(env, argv[9], &KV) || get_i32(env, argv[10], &D) ||
+        get_i32(env, argv[11], &past) || get_u64(env, argv[12], &o_off, 0))
+        return NULL;
+    throw_rc(env, ql_attention_decode((ql_ctx*)ctx, (ql_arena*)act, q_off, (ql_arena*)cache, k_off, v_off, max_t,
+                                      M, H, KV, D, past, o_off));
+    return NULL;
+}
+
+/* addRmsNorm(ctx, act, xOff, dOff|null, weights, wOff, eps, M, C, sumOff|null, yOff) */
+static napi_value js_add_rmsnorm(napi_env env, napi_callback_info info)
+{
+    napi_value argv[11];
+    void *ctx, *act, *w;
+    uint64_t x_off, d_off, w_off, s_off, y_off;
+    int32_t M, C;
+    double eps;
+    if (get_args(env, info, 11, argv) || get_ptr(env, argv[0], &ctx) || get_ptr(env, argv[1], &act) ||
+        get_u64(env, argv[2], &x_off, 0) || get_u64(env, argv[3], &d_off, 1) || get_ptr(env, argv[4], &w) ||
+        get_u64(env, argv[5], &w_off, 0))
+        return NULL;
+    if (napi_get_value_double(env, argv[6], &eps) != napi_ok) {
+        napi_throw_type_error(env, "QL_E_INVALID", "eps must be a number");
+        return NULL;
+    }
+    if (get_i32(env, argv[7], &M) || get_i32(env, argv[8], &C) || get_u64(env, argv[9], &s_off, 1) ||
+        get_u64(env, argv[10], &y_off, 0))
+        return NULL;
+    throw_rc(env, ql_add_rmsnorm((ql_ctx*)ctx, (ql_arena*)act, x_off, d_off, (ql_arena*)w, w_off, (float)eps, M, C,
+                                 s_off, y_off));
+    return NULL;
+}
+
+/* siluMul(ctx, act, gateOff, upOff, n, yOff) */
+static napi_value js_silu_mul(napi_env env, napi_callback_info info)
+{
+    napi_value argv[6];
+    void *ctx, *act;
+    uint64_t g_off, u_off, n, y_off;
+    if (get_args(env, info, 6, argv) || get_ptr(env, argv[0], &ctx) || get_ptr(env, argv[1], &act) ||
+        get_u64(env, argv[2], &g_off, 0) || get_u64(env, argv[3], &u_off, 0) || get_u64(env, argv[4], &n, 0) ||
+        get_u64(env, argv[5], &y_off, 0))
+        return NULL;
+    throw_rc(env, ql_silu_mul((ql_ctx*)ctx, (ql_arena*)act, g_off, u_off, (int64_t)n, y_off));
+    return NULL;
+}
+
 /* unpackBatch(ctx, descs[], w, out, outOffs[]): the whole weight set, ql_unpack_f16_batch */
 static napi_value js_unpack_batch(napi_env env, napi_callback_info info)
 {
@@ -651,6 +739,8 @@ static napi_value init(napi_env env, napi_value exports)
         {"graphLaunch", js_graph_launch}, {"graphDestroy", js_graph_destroy},
         {"seqCreate", js_seq_create}, {"seqRun", js_seq_run}, {"seqStatus", js_seq_status},
         {"seqInfo", js_seq_info}, {"seqDestroy", js_seq_destroy},
+        {"gemvF16w", js_gemv_f16w}, {"kvStore", js_kv_store}, {"attention", js_attention},
+        {"addRmsNorm", js_add_rmsnorm}, {"siluMul", js_silu_mul},
     };
     for (size_t i = 0; i < sizeof fns / sizeof fns[0]; i++) {
         napi_value f;
