@@ -518,9 +518,6 @@ StripKernel strip_kernel_for(int M, int group, int split)
     return {nullptr, 0};
 }
 
-// blocks per strip: waves x blocks per wave (8 x 1, or 4 x 2 for M > 8)
-int strip_blocks(int) { return kMaxStripBlocks; }
-
 }  // namespace
 
 // Two workgroups per CU when the weights stay in the 256 MB MALL (the 0.5B step: 39.9 against
