@@ -237,7 +237,8 @@ class KvCache:
     """Per-layer fp32 K and V caches [block_size, n_kv_head * D] in one device arena, and the
     decode attention over them: QwenGpt's kCache/vCache (qwen.ts:140-141, :200-205), kv store
     (qwen.ts:427-428) and attention_gqa_cache dispatch (qwen.ts:429-440). Stream order replaces
-    the reference's pass breaks."""
+    the reference's pass breaks. The caller keeps the context length (the reference's cacheLen,
+    qwen.ts:142, :490) and passes it as pos0 / past_len."""
 
     def __init__(self, ctx: ql.Context, config: QwenConfig):
         self.ctx = ctx
@@ -246,7 +247,6 @@ class KvCache:
         self.row_len = qwen_kv_dim(config)
         self.region = -(-config.block_size * self.row_len * 4 // 256) * 256
         self.arena = ctx.arena(2 * config.n_layer * self.region)
-        self.length = 0                                           # cacheLen (qwen.ts:142)
 
     def offsets(self, layer: int):
         if not 0 <= layer < self.config.n_layer:
@@ -273,9 +273,6 @@ class KvCache:
         ko, vo = self.offsets(layer)
         self.ctx.attention_decode(q.arena, q.offset, self.arena, ko, vo, c.block_size, M, c.n_head,
                                   c.n_kv_head, self.D, past_len, out.offset)
-
-    def reset(self):
-        self.length = 0
 
     def release(self):
         self.arena.release()
