@@ -120,6 +120,38 @@ function gpu(dir) {
         }, ctx);
         writeTyped(path.join(dir, d.out), W);
 
+        // residual add + RMSNorm, SiLU-mul, and the KV cache with decode attention
+        const el = spec.elem;
+        const rd = (f) => Uint8Array.from(fs.readFileSync(path.join(dir, f)));
+        const EX = pool.alloc([el.M, el.C]), ER = pool.alloc([el.M, el.C]);
+        const ES = pool.alloc([el.M, el.C]), EY = pool.alloc([el.M, el.C]);
+        EX.write(rd(el.x));
+        ER.write(rd(el.r));
+        model.rmsnorm(EX, 'L0.inNorm', EY, el.M, el.C, 1e-6, ER, ES);
+        const EG = pool.alloc([el.n]), EU = pool.alloc([el.n]), EO = pool.alloc([el.n]);
+        EG.write(rd(el.g));
+        EU.write(rd(el.u));
+        model.siluMul(EG, EU, EO, el.n);
+        ctx.sync();
+        writeTyped(path.join(dir, 'el_y.f32'), EY.read());
+        writeTyped(path.join(dir, 'el_s.f32'), ES.read());
+        writeTyped(path.join(dir, 'el_o.f32'), EO.read());
+        pool.reset();
+        const kv = new q.KvCache(ctx, spec.config);
+        for (let t = 0; t < spec.kvSteps; t++) {
+            const K = pool.alloc([1, kv.rowLen]), V = pool.alloc([1, kv.rowLen]);
+            const Q = pool.alloc([1, spec.config.nEmbd]), O = pool.alloc([1, spec.config.nEmbd]);
+            K.write(rd(`kv_k${t}`));
+            V.write(rd(`kv_v${t}`));
+            Q.write(rd(`kv_q${t}`));
+            kv.store(1, K, V, 1, t);
+            kv.attend(1, Q, O, 1, t);
+            ctx.sync();
+            writeTyped(path.join(dir, `kv_o${t}.f32`), O.read());
+            pool.reset();
+        }
+        kv.release();
+
         const errors = {};
         const expectThrow = (key, fn) => {
             try { fn(); errors[key] = null; } catch (e) { errors[key] = e.message; }

@@ -123,11 +123,37 @@ def test_node_host_matches_oracle(tmp_path, orc):
                           "K": [shapes[k][0] for k in ua], "outs": [f"ua_{k}.f16" for k in ua]}
     cases["dequant"] = {"prefix": "model.layers.1.mlp.down_proj", "K": shapes["downW"][0],
                         "N": shapes["downW"][1], "out": "w.f32"}
+    # residual add + RMSNorm over the loaded L0.inNorm (ones in the checkpoint), SiLU-mul, and
+    # three decode steps of the KV cache on layer 1
+    ex, er = synth.activations(2, TINY.n_embd, seed=0x40E1), synth.activations(2, TINY.n_embd, seed=0x40E2)
+    eg, eu = synth.activations(1, 2 * TINY.intermediate, seed=0x40E3), synth.activations(1, 2 * TINY.intermediate, seed=0x40E4)
+    for name, arr in (("el_x", ex), ("el_r", er), ("el_g", eg), ("el_u", eu)):
+        arr.tofile(tmp_path / name)
+    cases["elem"] = {"M": 2, "C": TINY.n_embd, "n": 2 * TINY.intermediate, "x": "el_x", "r": "el_r",
+                     "g": "el_g", "u": "el_u"}
+    es, ey = orc.add_rmsnorm(ex, np.ones(TINY.n_embd, np.float32), 1e-6, er)
+    refs["el_y.f32"] = (ey, False)
+    refs["el_o.f32"] = (orc.silu_mul(eg, eu), False)
+    H, KVH = TINY.n_head, TINY.n_kv_head
+    D = TINY.n_embd // H
+    rng = np.random.default_rng(0x40E5)
+    kk, vv = [], []
+    cases["kvSteps"] = 3
+    for t in range(3):
+        k, v = (rng.standard_normal((1, KVH * D)).astype(np.float32) for _ in range(2))
+        qv = rng.standard_normal((1, H * D)).astype(np.float32)
+        for name, arr in (("kv_k", k), ("kv_v", v), ("kv_q", qv)):
+            arr.tofile(tmp_path / f"{name}{t}")
+        kk.append(k)
+        vv.append(v)
+        refs[f"kv_o{t}.f32"] = (orc.attention_gqa_cache(qv.reshape(1, H, D), np.concatenate(kk), np.concatenate(vv),
+                                                        H, KVH, D, t).reshape(1, H * D), False)
     (tmp_path / "cases.json").write_text(json.dumps(cases))
 
     print(f"node host: {len(cases['gemm'])} gemm cases, 1 batch", flush=True)
     res = _node("gpu", tmp_path, 300)
 
+    assert np.array_equal(np.fromfile(tmp_path / "el_s.f32", dtype=np.float32).reshape(es.shape), es)
     assert res["tensorCount"] == 2 + TINY.n_layer * (2 + 7 + 3)
     assert res["progress"] == list(range(1, TINY.n_layer + 1))
     for out, (ref, gemm) in refs.items():
