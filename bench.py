@@ -58,13 +58,16 @@ def linear_bytes(K, N, M):
 class Model:
     """All linears of one model shape packed into a single weight arena."""
 
-    def __init__(self, ctx, shape: str, seed: int):
+    def __init__(self, ctx, shape: str, seed: int, keep_tensors: bool = False):
+        """keep_tensors: keep every linear's host tensors (self.tensors[(layer, proj)]) for a
+        full-size check against the oracle; otherwise only layer 0's are kept."""
         self.shape = shape
         self.linears = synth.model_linears(shape)
         self.layers = synth.QWEN05_LAYERS if shape == "0.5b" else synth.QWEN7_LAYERS
         lay = ql.ArenaLayout()
         self.descs = {}
         self.tensors_for_cpu = {}
+        self.tensors = {}
         plan = []
         for (layer, proj, K, N) in self.linears:
             qw, qz, sc = ql.gptq_sizes(K, N, GROUP)
@@ -81,6 +84,8 @@ class Model:
             self.descs[(layer, proj)] = ql.make_desc(offs[0], offs[1], offs[2], K, N, GROUP)
             if layer == 0:
                 self.tensors_for_cpu[proj] = t
+            if keep_tensors:
+                self.tensors[(layer, proj)] = t
         self.shapes = {(l, p): (K, N) for (l, p, K, N) in self.linears}
 
 

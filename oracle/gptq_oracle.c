@@ -7,6 +7,7 @@
 #include "gptq_oracle.h"
 
 #include <immintrin.h>
+#include <pthread.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -373,4 +374,104 @@ void orc_silu_mul(const float* gate, const float* up, size_t n, float* out)
         const double g = gate[i];
         out[i] = (float)((g / (1.0 + exp(-g))) * (double)up[i]);
     }
+}
+
+/* orc_gptq_linear over a subset of output columns, on several threads: the same arithmetic as
+ * orc_gptq_linear per output (weights dequantized as quant.ts:83-115, dot product accumulated
+ * in double in ascending k as qwen-ref.ts:135-141, one rounding to f32), so every output it
+ * computes is bit-identical to orc_gptq_linear's. Columns are dealt to threads in chunks of 16;
+ * y is [M, ncols], column j holding output cols[j]. */
+typedef struct {
+    const uint8_t* qweight; const uint8_t* qzeros; const uint16_t* scales; const float* bias;
+    const float* x; int M, K, N, group; const int32_t* cols; int ncols; float* y;
+    int next; pthread_mutex_t lock; int rc;
+} cols_job;
+
+static void* cols_worker(void* arg)
+{
+    cols_job* J = (cols_job*)arg;
+    enum { NB = 16 };
+    const int K = J->K, N = J->N, M = J->M;
+    const int pack_cols = (N + 7) / 8;
+    float* w = (float*)malloc(sizeof(float) * (size_t)NB * K);
+    if (!w) { pthread_mutex_lock(&J->lock); J->rc = ORC_E_DIMS; pthread_mutex_unlock(&J->lock); return NULL; }
+    for (;;) {
+        pthread_mutex_lock(&J->lock);
+        const int c0 = J->next;
+        J->next += NB;
+        pthread_mutex_unlock(&J->lock);
+        if (c0 >= J->ncols) break;
+        const int nb = (J->ncols - c0) < NB ? (J->ncols - c0) : NB;
+        for (int j = 0; j < nb; j++) {
+            const int o = J->cols[c0 + j];
+            float* wr = w + (size_t)j * K;
+            for (int pr = 0; pr * 8 < K; pr++) {
+                const uint32_t word = rd_u32le(J->qweight + ((size_t)pr * N + o) * 4);
+                for (int k = 0; k < 8 && pr * 8 + k < K; k++) {
+                    const int i = pr * 8 + k, g = i / J->group;
+                    int zero = 8;
+                    if (J->qzeros) {
+                        const uint32_t zw = rd_u32le(J->qzeros + ((size_t)g * pack_cols + o / 8) * 4);
+                        zero = (int)((zw >> (4 * (o % 8))) & 15u) + 1;
+                    }
+                    const float scale = orc_f16_bits_to_f32(J->scales[(size_t)g * N + o]);
+                    const int q = (int)((word >> (4 * k)) & 15u);
+                    wr[i] = (float)((double)(q - zero) * (double)scale);
+                }
+            }
+        }
+        for (int m = 0; m < M; m++) {
+            const float* a = J->x + (size_t)m * K;
+            int j = 0;
+            for (; j + 4 <= nb; j += 4) {     /* four independent chains, each in ascending k */
+                const float *w0 = w + (size_t)j * K, *w1 = w0 + K, *w2 = w1 + K, *w3 = w2 + K;
+                double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+                for (int i = 0; i < K; i++) {
+                    const double xv = (double)a[i];
+                    a0 += xv * (double)w0[i];
+                    a1 += xv * (double)w1[i];
+                    a2 += xv * (double)w2[i];
+                    a3 += xv * (double)w3[i];
+                }
+                const double acc[4] = {a0, a1, a2, a3};
+                for (int t = 0; t < 4; t++) {
+                    const int o = J->cols[c0 + j + t];
+                    J->y[(size_t)m * J->ncols + c0 + j + t] =
+                        J->bias ? (float)(acc[t] + (double)J->bias[o]) : (float)acc[t];
+                }
+            }
+            for (; j < nb; j++) {
+                const float* wr = w + (size_t)j * K;
+                double acc = 0.0;
+                for (int i = 0; i < K; i++) acc += (double)a[i] * (double)wr[i];
+                const int o = J->cols[c0 + j];
+                J->y[(size_t)m * J->ncols + c0 + j] = J->bias ? (float)(acc + (double)J->bias[o]) : (float)acc;
+            }
+        }
+    }
+    free(w);
+    return NULL;
+}
+
+int orc_gptq_linear_cols(const uint8_t* qweight, const uint8_t* qzeros, const uint16_t* scales_f16,
+                         const float* bias, const float* x, int M, int K, int N, int group_size,
+                         const int32_t* cols, int ncols, int threads, float* y)
+{
+    if (M <= 0 || K <= 0 || N <= 0 || group_size <= 0 || group_size % 8 != 0 || ncols < 0)
+        return ORC_E_DIMS;
+    for (int j = 0; j < ncols; j++)
+        if (cols[j] < 0 || cols[j] >= N) return ORC_E_DIMS;
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    cols_job J = {qweight, qzeros, scales_f16, bias, x, M, K, N, group_size, cols, ncols, y,
+                  0, PTHREAD_MUTEX_INITIALIZER, ORC_OK};
+    pthread_t tid[64];
+    int started = 0;
+    for (int t = 1; t < threads; t++) {
+        if (pthread_create(&tid[started], NULL, cols_worker, &J) != 0) break;
+        started++;
+    }
+    cols_worker(&J);
+    for (int t = 0; t < started; t++) pthread_join(tid[t], NULL);
+    return J.rc;
 }

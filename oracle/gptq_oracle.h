@@ -12,6 +12,7 @@
  *   orc_dequant_gptq_int4 src/weights/quant.ts:42-118     reference KAT (tests/qwen/weights.ts:62-137),
  *                                                         numpy brute force, invariants, error classes
  *   orc_gemm_nt           src/reference/qwen-ref.ts:126   numpy float64 matmul, hand cases
+ *   orc_gptq_linear_cols  (the same, column subset, threaded) bit-identical to orc_gptq_linear
  *   orc_plan_gemv_split   src/model/qwen.ts:61-74         documented table qwen.ts:54-59 + brute force
  *   orc_check_tolerance   src/reference/cpu-ref.ts:27-47  hand cases
  *   orc_rng_*             src/reference/cpu-ref.ts:57-67  xorshift32 closed form in Python ints
@@ -75,6 +76,12 @@ int orc_attention_gqa_cache(const float* q, const float* kc, const float* vc, in
 int orc_gptq_linear(const uint8_t* qweight, const uint8_t* qzeros, const uint16_t* scales_f16,
                     const float* bias, const float* x, int M, int K, int N, int group_size,
                     float* y);
+
+/* orc_gptq_linear for the output columns cols[0..ncols) only (y [M, ncols]), on `threads` threads;
+ * each output bit-identical to orc_gptq_linear's. For checking full-size launches quickly. */
+int orc_gptq_linear_cols(const uint8_t* qweight, const uint8_t* qzeros, const uint16_t* scales_f16,
+                         const float* bias, const float* x, int M, int K, int N, int group_size,
+                         const int32_t* cols, int ncols, int threads, float* y);
 
 int orc_plan_gemv_split(int wg_n, int K);
 

@@ -7,7 +7,8 @@ The oracle restates the reference CPU path (intplusplus/webllm):
   dequantizeGptqInt4      src/weights/quant.ts:42-118
   f32ToF16Bits            src/gpu/buffer.ts:57-100
   f16BitsToF32            src/weights/safetensors.ts:144-152
-  gemmNTRef               src/reference/qwen-ref.ts:126-145
+  gemmNTRef               src/reference/qwen-ref.ts:126-145 (gptq_linear; gptq_linear_cols is the
+                          same per output, on a column subset and several threads)
   planGemvSplit           src/model/qwen.ts:61-74
   checkTolerance/makeRng  src/reference/cpu-ref.ts:27-67
   rmsNormRef (+ vec_add)  src/reference/qwen-ref.ts:12-28, src/gpu/kernels/misc/vec_add.wgsl
@@ -70,6 +71,9 @@ def lib():
         L.orc_gptq_linear.restype = ctypes.c_int
         L.orc_gptq_linear.argtypes = [P, P, P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, P]
+        L.orc_gptq_linear_cols.restype = ctypes.c_int
+        L.orc_gptq_linear_cols.argtypes = [P, P, P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, P, ctypes.c_int, ctypes.c_int, P]
         L.orc_plan_gemv_split.restype = ctypes.c_int
         L.orc_plan_gemv_split.argtypes = [ctypes.c_int, ctypes.c_int]
         L.orc_add_rmsnorm.restype = None
@@ -176,6 +180,31 @@ def gptq_linear(qweight, qzeros, scales_f16, x, bias=None, group: int = 128) -> 
                                _ptr(y))
     if rc != 0:
         raise ValueError("oracle gptq_linear: bad arguments")
+    return y
+
+
+def default_threads() -> int:
+    """Oracle threads: the host's cores, at most 16 (a GPU box's CPU share)."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def gptq_linear_cols(qweight, qzeros, scales_f16, x, cols, bias=None, group: int = 128,
+                     threads: int | None = None) -> np.ndarray:
+    """gptq_linear for the output columns `cols` only: y[M, len(cols)], every value
+    bit-identical to gptq_linear(...)[:, cols]; the columns are shared among threads."""
+    qw = np.ascontiguousarray(qweight, dtype=np.uint32)
+    qz = None if qzeros is None else np.ascontiguousarray(qzeros, dtype=np.uint32)
+    sc = np.ascontiguousarray(scales_f16).view(np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    N = qw.shape[1]
+    c = np.ascontiguousarray(cols, dtype=np.int32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    y = np.empty((M, c.size), dtype=np.float32)
+    rc = lib().orc_gptq_linear_cols(_ptr(qw), _ptr(qz), _ptr(sc), _ptr(b), _ptr(x), M, K, N, group,
+                                    _ptr(c), c.size, threads or default_threads(), _ptr(y))
+    if rc != 0:
+        raise ValueError("oracle gptq_linear_cols: bad arguments")
     return y
 
 

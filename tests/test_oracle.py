@@ -231,6 +231,27 @@ def test_gptq_linear_equals_dequant_then_gemm(orc):
         assert np.array_equal(y, orc.gemm_nt(x, W, bias))
 
 
+@pytest.mark.parametrize("K,N,M,threads", [(256, 40, 3, 1), (1000, 72, 5, 3), (896, 130, 16, 8)])
+def test_gptq_linear_cols_bit_identical(orc, K, N, M, threads):
+    """The threaded column-subset form returns gptq_linear's bits for any column order,
+    repeated columns, ragged K (K % 8 != 0) and a remainder of fewer than 4 columns."""
+    rng = np.random.default_rng(K + N)
+    group = 128 if K % 128 == 0 else 8
+    P, G = (K + 7) // 8, (K + group - 1) // group
+    qweight = rng.integers(0, 1 << 32, size=(P, N), dtype=np.uint64).astype(np.uint32)
+    qzeros = rng.integers(0, 1 << 32, size=(G, (N + 7) // 8), dtype=np.uint64).astype(np.uint32)
+    sf16 = (np.abs(rng.standard_normal((G, N))) * 0.01).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    cols = np.concatenate([rng.permutation(N)[: N - 3], [0, N - 1, 0]]).astype(np.int32)
+    for qz, b in ((qzeros, bias), (None, None)):
+        full = orc.gptq_linear(qweight, qz, sf16, x, b, group)
+        part = orc.gptq_linear_cols(qweight, qz, sf16, x, cols, b, group, threads=threads)
+        assert np.array_equal(part.view(np.uint32), full[:, cols].view(np.uint32))
+    with pytest.raises(ValueError):
+        orc.gptq_linear_cols(qweight, qzeros, sf16, x, [N], None, group)
+
+
 # ---------------------------------------------------------------- planGemvSplit (a7)
 
 def test_plan_gemv_split_documented_table(orc):
