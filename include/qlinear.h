@@ -153,6 +153,21 @@ int ql_plan_linear(int32_t M, int32_t N, int32_t K, int32_t group, ql_plan* out)
 int ql_linear(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights, ql_arena* act,
               uint64_t x_off, int32_t x_dtype, int32_t M, uint64_t y_off, uint64_t scratch_off);
 
+/* ql_linear with no scratch argument and no allocation. No counterpart in the reference: it is
+ * for callers that cannot allocate or carve out a workspace (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same kernels, plan and results as ql_linear.
+ * Split-K partial sums go to a static device array of QL_NOALLOC_SCRATCH_BYTES per GPU, resolved
+ * at ql_create; a plan needing more scratch (ql_plan_linear's scratch_bytes: at most 6.94 MiB for
+ * the Qwen2.5-0.5B and -7B decode shapes at M <= 16) fails with QL_E_RANGE before anything is
+ * enqueued. Nothing in the array must
+ * start at zero (every partial is written before it is read; the arrival counters are the
+ * context's and every launch leaves them at zero). Every call on a GPU shares its array and it
+ * keeps the last call's contents: calls that overlap on one GPU (several streams, contexts or
+ * threads) race. */
+#define QL_NOALLOC_SCRATCH_BYTES (8u << 20)
+int ql_linear_noalloc(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights, ql_arena* act,
+                      uint64_t x_off, int32_t x_dtype, int32_t M, uint64_t y_off);
+
 /* y[M,N] (fp32) = x[M,K] (fp32) . W^T (+ bias) for an fp16 weight W [N,K] row-major at w_off in
  * `weights` (bias f32 [N] at bias_off or QL_NONE): the tied lm_head / embedding product,
  * QwenGpt.gemm(lnf, 'embed', logits, null, M, V, C) (qwen.ts:488-489) on gemm_gemv_f16.wgsl's

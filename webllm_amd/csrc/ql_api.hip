@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "ql_internal.h"
@@ -19,6 +20,7 @@ struct ql_ctx {
     hipStream_t stream;
     uint32_t* counters;   // split-K arrival counters; every launch leaves them at zero
     float* attn_ws;       // attention key-split partials (ql::kAttnWsBytes), used in stream order
+    float* noalloc_scratch;  // this device's address of `scratch` (ql_linear_noalloc)
     hipEvent_t ev_start, ev_stop;
     bool capturing;
     int cu_count;
@@ -47,6 +49,11 @@ struct ql_seq {
     bool strips;            // independent linears at M >= 2: the column-strip kernel (sargs)
     ql::StripArgs sargs;
 };
+
+// Split-K partial sums of ql_linear_noalloc. One copy per GPU, loaded with the code object, so
+// that entry point allocates nothing. Host code never passes this name to a kernel: it is a
+// host-side stand-in there; the device address comes from hipGetSymbolAddress (scratch_address).
+static __device__ __align__(256) char scratch[QL_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -78,6 +85,26 @@ bool in_range(uint64_t off, uint64_t bytes, uint64_t size)
 }
 
 uint64_t align256(uint64_t v) { return (v + 255) & ~(uint64_t)255; }
+
+// Device address of `scratch` on `device` (which must be current), looked up once per device.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_addr[kMaxDevices];
+
+hipError_t scratch_address(int device, float** out)
+{
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if (!g_scratch_addr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_addr[device] = p;
+    }
+    *out = static_cast<float*>(g_scratch_addr[device]);
+    return hipSuccess;
+}
 
 // planGemvSplit of the reference (src/model/qwen.ts:42-44, :61-74), reported in ql_plan.ref_split.
 int ref_plan_gemv_split(int wg_n, int K)
@@ -478,6 +505,7 @@ int ql_create(int device, ql_ctx** out)
     if ((e = hipMalloc(&c->counters, sizeof(uint32_t) * ql::kCounterCapacity)) != hipSuccess ||
         (e = hipMemset(c->counters, 0, sizeof(uint32_t) * ql::kCounterCapacity)) != hipSuccess ||
         (e = hipMalloc(&c->attn_ws, ql::kAttnWsBytes)) != hipSuccess ||
+        (e = scratch_address(device, &c->noalloc_scratch)) != hipSuccess ||
         (e = hipEventCreate(&c->ev_start)) != hipSuccess ||
         (e = hipEventCreate(&c->ev_stop)) != hipSuccess) {
         (void)hipStreamDestroy(c->stream);
@@ -718,7 +746,7 @@ namespace {
 // One GEMM batch entry: pointers, shape, partial sums at scratch_off and arrival counters from
 // counter_base (both used only when the linear splits K).
 int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, uint64_t x_off, int M,
-               uint64_t y_off, uint64_t scratch_off, uint32_t* counters, int counter_base, int wg_begin,
+               uint64_t y_off, float* partial, uint32_t* counters, int counter_base, int wg_begin,
                ql::GemmLinear* out, bool no_split = false)
 {
     ql::GemmShape s = ql::gemm_shape(M, d->N, d->K, d->group, ql::kPlanCUs);
@@ -731,7 +759,7 @@ int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, ui
     L.bias = g.bias;
     L.x = act->base + x_off;
     L.y = reinterpret_cast<float*>(act->base + y_off);
-    L.partial = reinterpret_cast<float*>(act->base + scratch_off);
+    L.partial = partial;
     L.counters = counters + counter_base;
     L.N = d->N;
     L.K = d->K;
@@ -753,31 +781,27 @@ int ql_plan_linear(int32_t M, int32_t N, int32_t K, int32_t group, ql_plan* out)
     return plan_impl(M, N, K, group, out);
 }
 
-int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act,
-              uint64_t x_off, int32_t x_dtype, int32_t M, uint64_t y_off, uint64_t scratch_off)
+namespace {
+
+// ql_linear after its scratch has been resolved: `partial` holds the plan's scratch_bytes (split-K
+// partial sums; unused when the plan does not split K).
+int linear_impl(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act,
+                uint64_t x_off, int32_t x_dtype, int32_t M, uint64_t y_off, const ql_plan& p,
+                float* partial)
 {
-    if (!ctx || !act) return fail(QL_E_INVALID, "null context or activation arena");
-    int rc = check_desc(d, weights);
-    if (rc) return rc;
-    if ((rc = check_io(d, act, x_off, x_dtype, M, y_off))) return rc;
-    ql_plan p;
-    if ((rc = plan_impl(M, d->N, d->K, d->group, &p))) return rc;
+    int rc;
     if ((rc = set_device(ctx))) return rc;
     ql::GemvLinear L = make_linear(d, weights);
     L.x = act->base + x_off;
     L.y = reinterpret_cast<float*>(act->base + y_off);
 
     if (p.kind == QL_KIND_GEMV_MFMA && gemv_aligned(d, x_off, y_off)) {
-        if (!in_range(scratch_off, p.scratch_bytes, act->size))
-            return fail(QL_E_RANGE, "scratch (%llu bytes) outside the activation arena",
-                        (unsigned long long)p.scratch_bytes);
-        if (scratch_off % 16) return fail(QL_E_ALIGN, "scratch offset must be 16-byte aligned");
         const ql::GemvShape s = ql::gemv_shape(M, d->N, d->K, d->group);
         ql::GemvBatch b{};
         L.split = s.split;
         L.strips = s.strips;
         L.wg_begin = 0;
-        L.partial = reinterpret_cast<float*>(act->base + scratch_off);
+        L.partial = partial;
         L.counters = ctx->counters;
         if (s.strips > ql::kCounterCapacity) return fail(QL_E_INVALID, "N too large (%d)", d->N);
         b.L[0] = L;
@@ -793,12 +817,8 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_ar
         return QL_OK;
     }
     if (p.kind == QL_KIND_GEMM_MFMA && gemv_aligned(d, x_off, y_off)) {
-        if (!in_range(scratch_off, p.scratch_bytes, act->size))
-            return fail(QL_E_RANGE, "scratch (%llu bytes) outside the activation arena",
-                        (unsigned long long)p.scratch_bytes);
-        if (scratch_off % 16) return fail(QL_E_ALIGN, "scratch offset must be 16-byte aligned");
         ql::GemmBatch b{};
-        int rc2 = gemm_entry(d, weights, act, x_off, M, y_off, scratch_off, ctx->counters, 0, 0, &b.L[0]);
+        int rc2 = gemm_entry(d, weights, act, x_off, M, y_off, partial, ctx->counters, 0, 0, &b.L[0]);
         if (rc2) return rc2;
         b.count = 1;
         b.M = M;
@@ -822,6 +842,51 @@ int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_ar
     g.x_dtype = x_dtype;
     QL_HIP(ql::launch_gemm_simple(g, ctx->stream));
     return QL_OK;
+}
+
+// true when the plan's MFMA path runs and reads split-K scratch
+bool uses_scratch(const ql_gptq_desc* d, const ql_plan& p, uint64_t x_off, uint64_t y_off)
+{
+    return (p.kind == QL_KIND_GEMV_MFMA || p.kind == QL_KIND_GEMM_MFMA) && gemv_aligned(d, x_off, y_off);
+}
+
+}  // namespace
+
+int ql_linear(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act,
+              uint64_t x_off, int32_t x_dtype, int32_t M, uint64_t y_off, uint64_t scratch_off)
+{
+    if (!ctx || !act) return fail(QL_E_INVALID, "null context or activation arena");
+    int rc = check_desc(d, weights);
+    if (rc) return rc;
+    if ((rc = check_io(d, act, x_off, x_dtype, M, y_off))) return rc;
+    ql_plan p;
+    if ((rc = plan_impl(M, d->N, d->K, d->group, &p))) return rc;
+    if (uses_scratch(d, p, x_off, y_off)) {
+        if (!in_range(scratch_off, p.scratch_bytes, act->size))
+            return fail(QL_E_RANGE, "scratch (%llu bytes) outside the activation arena",
+                        (unsigned long long)p.scratch_bytes);
+        if (scratch_off % 16) return fail(QL_E_ALIGN, "scratch offset must be 16-byte aligned");
+    }
+    return linear_impl(ctx, d, weights, act, x_off, x_dtype, M, y_off, p,
+                       reinterpret_cast<float*>(act->base + scratch_off));
+}
+
+int ql_linear_noalloc(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act,
+                      uint64_t x_off, int32_t x_dtype, int32_t M, uint64_t y_off)
+{
+    if (!ctx || !act) return fail(QL_E_INVALID, "null context or activation arena");
+    int rc = check_desc(d, weights);
+    if (rc) return rc;
+    if ((rc = check_io(d, act, x_off, x_dtype, M, y_off))) return rc;
+    ql_plan p;
+    if ((rc = plan_impl(M, d->N, d->K, d->group, &p))) return rc;
+    if (uses_scratch(d, p, x_off, y_off) && p.scratch_bytes > QL_NOALLOC_SCRATCH_BYTES)
+        return fail(QL_E_RANGE,
+                    "ql_linear_noalloc: this plan needs %llu bytes of split-K scratch, more than the "
+                    "%u-byte static scratch (use ql_linear with a scratch offset)",
+                    (unsigned long long)p.scratch_bytes, (unsigned)QL_NOALLOC_SCRATCH_BYTES);
+    if (!ctx->noalloc_scratch) return fail(QL_E_STATE, "static scratch address not resolved");
+    return linear_impl(ctx, d, weights, act, x_off, x_dtype, M, y_off, p, ctx->noalloc_scratch);
 }
 
 int ql_gemv_f16w(ql_ctx* ctx, const ql_arena* weights, uint64_t w_off, uint64_t bias_off,
@@ -1028,7 +1093,8 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
         uint64_t off = scratch_off;
         int wg = 0, counter_base = 0;
         for (int i = 0; i < count; i++) {
-            if ((rc = gemm_entry(&descs[i], weights, act, x_offs[i], M, y_offs[i], off, ctx->counters,
+            if ((rc = gemm_entry(&descs[i], weights, act, x_offs[i], M, y_offs[i],
+                                 reinterpret_cast<float*>(act->base + off), ctx->counters,
                                  counter_base, wg, &b.L[i], no_split)))
                 return rc;
             const ql::GemmLinear& L = b.L[i];

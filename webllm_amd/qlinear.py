@@ -21,6 +21,7 @@ HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "qlinear.h")
 
 SEQ_TILES, SEQ_STRIPS = 0, 1      # ql_seq_info.kernel
 QL_NONE = (1 << 64) - 1
+NOALLOC_SCRATCH_BYTES = 8 << 20   # QL_NOALLOC_SCRATCH_BYTES
 DTYPE_F32 = 0
 DTYPE_F16 = 1
 KIND_NAMES = {1: "gemv_mfma", 2: "gemv_simple", 3: "gemm_mfma", 4: "gemm_simple"}
@@ -120,6 +121,7 @@ def lib():
         "ql_silu_mul": (I, [P, P, U64, U64, ctypes.c_int64, U64]),
         "ql_attention_decode": (I, [P, P, U64, P, U64, U64, I, I, I, I, I, I, U64]),
         "ql_linear": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64, I, I, U64, U64]),
+        "ql_linear_noalloc": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64, I, I, U64]),
         "ql_plan_batch": (I, [I, ctypes.POINTER(GptqDesc), I, ctypes.POINTER(U64)]),
         "ql_linear_batch": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64), I, I,
                                 ctypes.POINTER(U64), U64]),
@@ -355,6 +357,13 @@ class Context:
                y_off: int, scratch_off: int = 0):
         _check(lib().ql_linear(self.handle, ctypes.byref(desc), weights.handle, act.handle, x_off,
                                x_dtype, M, y_off, scratch_off))
+
+    def linear_noalloc(self, desc: GptqDesc, weights: Arena, act: Arena, x_off: int, x_dtype: int,
+                       M: int, y_off: int):
+        """ql_linear without a scratch argument: split-K partials in the library's static
+        per-GPU array (NOALLOC_SCRATCH_BYTES); calls overlapping on one GPU race."""
+        _check(lib().ql_linear_noalloc(self.handle, ctypes.byref(desc), weights.handle, act.handle,
+                                       x_off, x_dtype, M, y_off))
 
     def linear_batch(self, descs: list[GptqDesc], weights: Arena, act: Arena, x_offs, x_dtype: int,
                      M: int, y_offs, scratch_off: int = 0):
