@@ -14,7 +14,7 @@
  *   ql_gptq_desc / ql_gptq_check  src/weights/quant.ts:16-30 GptqInt4Params, :44-79 validation
  *   ql_unpack_f16                 src/weights/qwen-loader.ts:55-67 dequantGptqLinear +
  *                                 src/model/qwen.ts:262-266 uploadF16 (CPU dequant + f16 encode)
- *   ql_unpack_f32                 src/weights/quant.ts:42-118 dequantizeGptqInt4
+ *   ql_unpack_f32, ql_unpack_f32_ex  src/weights/quant.ts:42-118 dequantizeGptqInt4
  *   ql_plan_linear                src/model/qwen.ts:61-74 planGemvSplit + the branch in :568-618
  *   ql_linear                     src/model/qwen.ts:568-618 QwenGpt.gemm (GEMV / split-K / GEMM)
  *   ql_linear_batch               src/model/qwen.ts:411-413, :464-465 (q/k/v and gate/up issued
@@ -141,6 +141,13 @@ int ql_unpack_f16_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
  * out_off must be 16-byte aligned. */
 int ql_unpack_f32(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights,
                   ql_arena* out, uint64_t out_off);
+/* ql_unpack_f32 with the scales' dtype stated: QL_DTYPE_F16 (as stored in the checkpoint; the same
+ * as ql_unpack_f32) or QL_DTYPE_F32, where desc->scales_off holds f32 scales [ceil(K/group), N]
+ * (4-byte aligned) — GptqInt4Params.scales as the reference takes it, any Float32Array
+ * (quant.ts:22-23, :62 sizes it in values). Each weight is (q - zero) * scale rounded once to f32,
+ * bit-identical to dequantizeGptqInt4 for every f32 scale (quant.ts:111-112). */
+int ql_unpack_f32_ex(ql_ctx* ctx, const ql_gptq_desc* desc, const ql_arena* weights, int32_t scales_dtype,
+                     ql_arena* out, uint64_t out_off);
 
 /* ---- dispatch plan (host only, deterministic, pure). */
 int ql_plan_linear(int32_t M, int32_t N, int32_t K, int32_t group, ql_plan* out);
@@ -201,7 +208,9 @@ int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_are
  *   at sum_off unless QL_NONE, then y = s * rstd * w, rstd = 1 / sqrt(mean(s^2) + eps)
  *   (norm/rmsnorm.wgsl; CPU form reference/qwen-ref.ts:12-28). d_off = QL_NONE: plain RMSNorm of x.
  *   One launch where the reference runs two; fp32; x, d, sum, y [M, C] in `act`, w [C] in
- *   `weights`; offsets 4-byte aligned (16-byte and C % 4 == 0 take the vector path). */
+ *   `weights`; offsets 4-byte aligned (16-byte and C % 4 == 0 take the vector path). The sum may
+ *   be stored in place over x or d (sum_off == x_off or d_off); any other overlap of the sum with
+ *   x or d, or of y with anything, fails with QL_E_INVALID. */
 int ql_add_rmsnorm(ql_ctx* ctx, ql_arena* act, uint64_t x_off, uint64_t d_off, const ql_arena* weights,
                    uint64_t w_off, float eps, int32_t M, int32_t C, uint64_t sum_off, uint64_t y_off);
 /* ql_silu_mul: y[i] = (g / (1 + exp(-g))) * up[i], g = gate[i] (activation/silu_mul.wgsl;

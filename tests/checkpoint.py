@@ -7,9 +7,11 @@ TINY = gptq.QwenConfig(vocab_size=512, block_size=16, n_layer=2, n_head=4, n_kv_
                        n_embd=256, intermediate=640)
 
 
-def write_checkpoint(path, cfg):
+def write_checkpoint(path, cfg, act_order=None, no_g_idx=False):
     """Writes a Qwen-layout GPTQ checkpoint of config `cfg` (random tensors, half the linears with
-    qzeros nibble 7, half with random zeros) and returns {(layer, key): (GptqTensors, bias f32)} plus "embed": the fp16 embedding."""
+    qzeros nibble 7, half with random zeros) and returns {(layer, key): (GptqTensors, bias f32)} plus "embed": the fp16 embedding.
+    act_order=(layer, key): that linear gets a permuted g_idx (a desc_act=true checkpoint);
+    no_g_idx: no g_idx tensors at all."""
     shapes = gptq.qwen_linear_shapes(cfg)
     tensors, kept = {}, {}
     rng = np.random.default_rng(1)
@@ -29,7 +31,10 @@ def write_checkpoint(path, cfg):
             tensors[f"{pre}.qzeros"] = ("I32", t.qzeros.shape, t.qzeros.tobytes())
             tensors[f"{pre}.scales"] = ("F16", t.scales.shape, t.scales.tobytes())
             g_idx = (np.arange(K) // 128).astype(np.int32)
-            tensors[f"{pre}.g_idx"] = ("I32", g_idx.shape, g_idx.tobytes())
+            if act_order == (i, key):
+                g_idx = g_idx[np.random.default_rng(7).permutation(K)]
+            if not no_g_idx:
+                tensors[f"{pre}.g_idx"] = ("I32", g_idx.shape, g_idx.tobytes())
             b = None
             if key in gptq._BIASED:
                 b = rng.standard_normal(N).astype(np.float16)

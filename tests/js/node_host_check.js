@@ -36,6 +36,19 @@ function abi(dir) {
     const file = q.parseSafetensors(fs.readFileSync(path.join(dir, 'model.safetensors')));
     let badParse = null;
     try { q.parseSafetensors(new Uint8Array(4)); } catch (e) { badParse = e.message; }
+    // the loader's format probes (qwen-format.ts:112-130) and readF16Rows (qwen-loader.ts:70-93)
+    const probes = { gIdxOk: null, gIdxActOrder: null, urls: [], badUrl: null };
+    try { q.checkGIdx(file, 'model.layers.1.mlp.gate_proj', 256, 128); } catch (e) { probes.gIdxOk = e.message; }
+    const act = path.join(dir, 'act_order.safetensors');
+    if (fs.existsSync(act)) {
+        const f2 = q.parseSafetensors(fs.readFileSync(act));
+        try { q.checkGIdx(f2, 'model.layers.1.mlp.gate_proj', 256, 128); } catch (e) { probes.gIdxActOrder = e.message; }
+    }
+    writeTyped(path.join(dir, 'rows.f32'), q.readF16Rows(file, 'model.embed_tokens.weight', 5, 3, 256));
+    probes.zerosK = q.countStoredZeros(q.readTensorBytes(file, 'model.layers.0.self_attn.k_proj.qzeros'), 2, 128,
+        new Array(16).fill(0));
+    probes.urls = [q.urlToPath('file:///tmp/a%20b/model.safetensors'), q.urlToPath('rel/model.safetensors')];
+    try { q.urlToPath('https://huggingface.co/m/model.safetensors'); } catch (e) { probes.badUrl = e.message; }
     console.log(JSON.stringify({
         exports: Object.keys(q.addon).sort(),
         plans,
@@ -44,20 +57,31 @@ function abi(dir) {
         tensors: Object.keys(file.header).length,
         embedShape: q.requireTensor(file, 'model.embed_tokens.weight').shape,
         badParse,
+        probes,
     }));
 }
 
-function gpu(dir) {
+async function gpu(dir) {
     const spec = JSON.parse(fs.readFileSync(path.join(dir, 'cases.json'), 'utf8'));
     const ctx = new q.Context(0);
     try {
         const model = new q.QuantLinearModel(ctx, 64 << 20);
         const progress = [];
-        const res = q.loadQwenWeights(ctx, model, {
-            path: path.join(dir, 'model.safetensors'), config: spec.config, keepLayer: 0,
-            onProgress: (i, n) => progress.push(i),
+        const pending = q.loadQwenWeights(ctx, model, {
+            url: 'file://' + path.join(dir, 'model.safetensors'), config: spec.config, keepLayer: 0,
+            keepEmbedRows: { start: 100, rows: 4 }, onProgress: (i, n) => progress.push(i),
         });
+        const isPromise = pending instanceof Promise;
+        const res = await pending;
         writeTyped(path.join(dir, 'kept_qW.f32'), res.layer.qW);
+        writeTyped(path.join(dir, 'embed_rows.f32'), res.embedRows);
+        // an act-order (desc_act) checkpoint is rejected (qwen-format.ts:125-130)
+        let actOrder = null;
+        const m2 = new q.QuantLinearModel(ctx, 64 << 20);
+        try {
+            await q.loadQwenWeights(ctx, m2, { path: path.join(dir, 'act_order.safetensors'), config: spec.config });
+        } catch (e) { actOrder = e.message; }
+        m2.release();
         const pool = new q.ActivationArena(ctx, 32 << 20);
         for (const c of spec.gemm) {
             const A = pool.alloc([c.M, c.K], c.f16 ? 'f16' : 'f32');
@@ -119,6 +143,15 @@ function gpu(dir) {
             inFeatures: d.K, outFeatures: d.N, groupSize: 128,
         }, ctx);
         writeTyped(path.join(dir, d.out), W);
+        // any Float32Array scales (quant.ts:22-23): not fp16 values, tiny, huge
+        const ds = spec.dequantF32;
+        const W2 = q.dequantizeGptqInt4({
+            qweight: Uint8Array.from(fs.readFileSync(path.join(dir, ds.qweight))),
+            qzeros: Uint8Array.from(fs.readFileSync(path.join(dir, ds.qzeros))),
+            scales: readF32(path.join(dir, ds.scales)),
+            inFeatures: ds.K, outFeatures: ds.N, groupSize: ds.group,
+        }, ctx);
+        writeTyped(path.join(dir, ds.out), W2);
 
         // residual add + RMSNorm, SiLU-mul, and the KV cache with decode attention
         const el = spec.elem;
@@ -163,11 +196,21 @@ function gpu(dir) {
         expectThrow('missingBias', () => model.gemm(A, 'L0.oW', C, 'L0.oB', 1, spec.config.nEmbd, spec.config.nEmbd));
         expectThrow('duplicate', () => model.uploadF32('finalNorm', new Float32Array(4)));
         expectThrow('bits', () => q.dequantizeGptqInt4({ qweight: new Uint8Array(4), scales: new Float32Array(1), inFeatures: 8, outFeatures: 1, bits: 8 }, ctx));
+        // tensors of another ActivationArena are refused before any launch
+        const other = new q.ActivationArena(ctx, 1 << 20);
+        const Y2 = other.alloc([1, spec.config.nEmbd]);
+        expectThrow('rmsnormArena', () => model.rmsnorm(A, 'L0.inNorm', Y2, 1, spec.config.nEmbd, 1e-6));
+        expectThrow('rmsnormSumArena', () => model.rmsnorm(A, 'L0.inNorm', C, 1, spec.config.nEmbd, 1e-6, null, Y2));
+        const kv2 = new q.KvCache(ctx, spec.config);
+        expectThrow('attendArena', () => kv2.attend(0, A, Y2, 1, 0));
+        kv2.release();
+        other.release();
         pool.release();
         model.release();
         console.log(JSON.stringify({
             device: ctx.info(), tensorCount: res.tensorCount, gpuBytes: res.gpuBytes,
             fileBytes: res.fileBytes, progress, errors, seqInfo: spec.seqInfo || null,
+            isPromise, storedZeros: res.storedZeros, actOrder,
         }));
     } finally {
         ctx.destroy();
@@ -176,5 +219,5 @@ function gpu(dir) {
 
 const [mode, dir] = process.argv.slice(2);
 if (mode === 'abi') abi(dir);
-else if (mode === 'gpu') gpu(dir);
+else if (mode === 'gpu') gpu(dir).catch((e) => { console.error(e && e.stack ? e.stack : e); process.exit(1); });
 else { console.error('usage: node node_host_check.js abi|gpu <dir>'); process.exit(2); }

@@ -62,6 +62,41 @@ def test_add_rmsnorm_matches_oracle(ql, ctx, orc, M, C, residual, store, pad, la
     wa.release()
 
 
+@pytest.mark.parametrize("M,C,pad,into,label", [
+    (2, 8192, 0, "x", "C = 8192, sum over x: two-pass vector path"),
+    (2, 8192, 0, "d", "C = 8192, sum over d"),
+    (3, 900, 0, "x", "C % 4 != 0, sum over x: scalar two-pass path"),
+    (2, 896, 4, "x", "4-byte aligned, sum over x: scalar path"),
+    (4, 896, 0, "x", "0.5B width, sum over x: rows in registers"),
+])
+def test_add_rmsnorm_sum_in_place(ql, ctx, orc, M, C, pad, into, label):
+    """The residual stream updated in place (sum_off == x_off or d_off): the stored sum is
+    bit-exact and y meets the bar on every path, including the two-pass ones that read the row
+    back; a sum that only partly overlaps x or d is refused."""
+    say(f"add_rmsnorm in place {label}: M={M} C={C}")
+    rng = np.random.default_rng(M * 11 + C)
+    x = rng.standard_normal((M, C)).astype(np.float32)
+    d = rng.standard_normal((M, C)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    lay = ql.ArenaLayout()
+    xo, do, yo = (lay.take(M * C * 4 + 16) + pad for _ in range(3))
+    act = ctx.arena(lay.used)
+    wa = ctx.arena(C * 4)
+    wa.write(0, w)
+    act.write(xo, x)
+    act.write(do, d)
+    so = xo if into == "x" else do
+    ctx.add_rmsnorm(act, xo, do, wa, 0, 1e-6, M, C, yo, so)
+    s_ref, y_ref = orc.add_rmsnorm(x, w, 1e-6, d)
+    ok, ma, mr = orc.check_tolerance(act.read(yo, (M, C), np.float32), y_ref, ATOL, RTOL)
+    assert ok, (label, ma, mr)
+    assert np.array_equal(act.read(so, (M, C), np.float32).view(np.uint32), s_ref.view(np.uint32))
+    with pytest.raises(ql.QlError, match="partly overlaps"):
+        ctx.add_rmsnorm(act, xo, do, wa, 0, 1e-6, M, C, yo, xo + 4 * C if M > 1 else xo + 64)
+    act.release()
+    wa.release()
+
+
 @pytest.mark.parametrize("n", [4864, 18944 * 16, 4863, 3])
 def test_silu_mul_matches_oracle(ql, ctx, orc, n):
     say(f"silu_mul n={n}")

@@ -134,26 +134,76 @@ def test_loader_rejects_wrong_shapes(ctx, tmp_path):
                                gptq.QwenConfig(1000, 16, 2, 4, 2, 256, 640))
 
 
+def test_loader_url_embed_rows_and_zero_counts(ctx, tmp_path):
+    """loadQwenWeights options: url (file://), keepEmbedRows -> embedRows (qwen-loader.ts:134-135,
+    :175), and the stored-zero counts of the format probe (qwen-format.ts:112-123)."""
+    path = tmp_path / "model.safetensors"
+    kept = _checkpoint(str(path), TINY)
+    model = gptq.QuantLinearModel(ctx, 64 << 20)
+    res = gptq.load_qwen_weights(model, url=path.as_uri(), config=TINY,
+                                 keep_embed_rows={"start": 100, "rows": 4})
+    assert np.array_equal(res.embed_rows, kept["embed"][100:104].astype(np.float32).reshape(-1))
+    want = np.zeros(16, np.int64)
+    for (i, key), (t, _) in ((k, v) for k, v in kept.items() if k != "embed"):
+        nib = (t.qzeros[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15
+        want += np.bincount(nib.reshape(t.qzeros.shape[0], -1)[:, :t.N].reshape(-1), minlength=16)
+    assert res.stored_zeros == {v: int(c) for v, c in enumerate(want) if c}
+    assert res.layer is None and res.file_bytes == os.path.getsize(path)
+    model.release()
+
+
+def test_loader_rejects_act_order_checkpoint(ctx, tmp_path):
+    """A desc_act=true checkpoint (permuted g_idx) would load and compute wrong outputs with
+    kernels that assume g = k / group: the loader throws (qwen-format.ts:125-130)."""
+    path = str(tmp_path / "model.safetensors")
+    _checkpoint(path, TINY, act_order=(1, "downW"))
+    model = gptq.QuantLinearModel(ctx, 64 << 20)
+    with pytest.raises(ValueError, match="not the identity"):
+        gptq.load_qwen_weights(model, path, TINY)
+    model.release()
+
+
+def test_dequantize_gptq_int4_any_f32_scales(ctx, orc):
+    """Scales that fp16 cannot represent, subnormal products, overflow to inf and NaN scales,
+    as any Float32Array may hold (quant.ts:22-23): bit-identical to the oracle's dequant."""
+    rng = np.random.default_rng(0x5CA1)
+    K, N, group = 256, 40, 64
+    qw = rng.integers(0, 1 << 32, size=(K // 8, N), dtype=np.uint64).astype(np.uint32)
+    qz = rng.integers(0, 1 << 32, size=(K // group, N // 8), dtype=np.uint64).astype(np.uint32)
+    sc = (rng.standard_normal((K // group, N)) * 0.01).astype(np.float32)
+    sc[0, :8] = np.float32(1e-44)               # products in the f32 subnormal range
+    sc[1, :8] = np.float32(3e38)                # products overflow to +-inf
+    sc[2, 0] = np.float32("nan")
+    sc[3, :8] = -sc[3, :8]
+    for qzeros in (qz, None):
+        rc, want = orc.dequantize_gptq_int4(qw, qzeros, sc, K, N, group)
+        assert rc == 0
+        got = gptq.dequantize_gptq_int4(ctx, qw.tobytes(), None if qzeros is None else qzeros.tobytes(),
+                                        sc, K, N, group)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_dequantize_gptq_int4_reference_kat(ctx):
-    """quant.ts through the GPU drop-in on the reference's own KAT (weights.ts:62-137)."""
+    """quant.ts through the GPU drop-in on the reference's own KAT (weights.ts:62-137), with its
+    f32 scales 0.01*(g+1)*(o+1) (not fp16 values): bit-identical to the KAT's expected weights,
+    and the symmetric fallback (qzeros null -> zero 8) gives the same values here because the KAT
+    stores zero 7."""
     d = json.load(open(os.path.join(GOLDEN, "gptq_kat.json")))
     qw = np.array(d["qweight_u32"], np.uint32).tobytes()
     qz = np.array(d["qzeros_u32"], np.uint32).tobytes()
     sc = np.array(d["scales_f32_bits"], np.uint32).view(np.float32)
     want = np.array(d["want_f32_bits"], np.uint32)
-    # KAT scales 0.01*(g+1)*(o+1) are not fp16 values: the GPU drop-in takes checkpoint (F16)
-    # scales only, so the KAT runs with the scales rounded to fp16 and the expected values
-    # recomputed from the closed form on those scales
+    got = gptq.dequantize_gptq_int4(ctx, qw, qz, sc, 16, 5, 8)
+    assert np.array_equal(got.view(np.uint32).reshape(-1), want)
+    got_sym = gptq.dequantize_gptq_int4(ctx, qw, None, sc, 16, 5, 8)
+    assert np.array_equal(got_sym.view(np.uint32).reshape(-1), want)
+    # fp16-valued scales (what a checkpoint holds) give the closed form on those scales
     s16 = sc.astype(np.float16).astype(np.float32)
     q = [[(o * 7 + i * 3) & 15 for i in range(16)] for o in range(5)]
     want16 = np.array([[(q[o][i] - 8) * s16[(i // 8) * 5 + o] for i in range(16)] for o in range(5)],
                       dtype=np.float32)
-    got = gptq.dequantize_gptq_int4(ctx, qw, qz, s16, 16, 5, 8)
-    assert np.array_equal(got.view(np.uint32), want16.view(np.uint32))
-    got_sym = gptq.dequantize_gptq_int4(ctx, qw, None, s16, 16, 5, 8)
-    assert np.array_equal(got_sym, want16)
-    with pytest.raises(ValueError, match="fp16"):
-        gptq.dequantize_gptq_int4(ctx, qw, qz, sc, 16, 5, 8)
+    got16 = gptq.dequantize_gptq_int4(ctx, qw, qz, s16, 16, 5, 8)
+    assert np.array_equal(got16.view(np.uint32), want16.view(np.uint32))
     for kw, code in [(dict(bits=3), "QL_E_BITS"), (dict(group_size=0), "QL_E_GROUP"),
                      (dict(in_features=0), "QL_E_DIMS"), (dict(group_size=12), "QL_E_GROUP_PACK")]:
         args = dict(in_features=16, out_features=5, group_size=8)

@@ -82,3 +82,48 @@ def test_qwen_config():
     assert shapes["kW"] == (896, 128) and shapes["downW"] == (4864, 896)
     with pytest.raises(ValueError):
         gptq.qwen_head_dim(gptq.QwenConfig(10, 8, 1, 3, 1, 8, 16))
+
+
+def test_loader_format_probes(tmp_path):
+    """qwen-format.ts:112-130 restated on synthetic checkpoints: g_idx must be the identity i/128
+    (an act-order checkpoint is rejected, a missing g_idx accepted); stored-zero nibbles are
+    counted per value; readF16Rows (qwen-loader.ts:70-93) decodes embed rows exactly."""
+    from .checkpoint import TINY, write_checkpoint
+    p = str(tmp_path / "model.safetensors")
+    kept = write_checkpoint(p, TINY)
+    f = gptq.open_safetensors(p)
+    shapes = gptq.qwen_linear_shapes(TINY)
+    for i in range(TINY.n_layer):
+        for key, proj in gptq._PROJ:
+            gptq.check_g_idx(f, f"model.layers.{i}.{proj}", shapes[key][0], 128)
+    t, _ = kept[(0, "qW")]
+    counts = gptq.stored_zero_counts(gptq.read_tensor_bytes(f, "model.layers.0.self_attn.q_proj.qzeros"),
+                                     t.qzeros.shape[0], t.N)
+    assert counts[7] == t.qzeros.shape[0] * t.N and counts.sum() == counts[7]
+    t, _ = kept[(0, "kW")]                       # random stored zeros
+    counts = gptq.stored_zero_counts(gptq.read_tensor_bytes(f, "model.layers.0.self_attn.k_proj.qzeros"),
+                                     t.qzeros.shape[0], t.N)
+    nib = [(int(w) >> (4 * (n % 8))) & 15 for g in range(t.qzeros.shape[0]) for n, w in
+           ((n, t.qzeros[g, n // 8]) for n in range(t.N))]
+    assert counts.tolist() == np.bincount(nib, minlength=16).tolist()
+    rows = gptq.read_f16_rows(f, "model.embed_tokens.weight", 5, 3, TINY.n_embd)
+    assert np.array_equal(rows, kept["embed"][5:8].astype(np.float32).reshape(-1))
+    with pytest.raises(ValueError, match="outside"):
+        gptq.read_f16_rows(f, "model.embed_tokens.weight", TINY.vocab_size - 1, 2, TINY.n_embd)
+    p2 = str(tmp_path / "act_order.safetensors")
+    write_checkpoint(p2, TINY, act_order=(1, "gateW"))
+    f2 = gptq.open_safetensors(p2)
+    gptq.check_g_idx(f2, "model.layers.1.mlp.up_proj", TINY.n_embd, 128)
+    with pytest.raises(ValueError, match="not the identity"):
+        gptq.check_g_idx(f2, "model.layers.1.mlp.gate_proj", TINY.n_embd, 128)
+    p3 = str(tmp_path / "no_g_idx.safetensors")
+    write_checkpoint(p3, TINY, no_g_idx=True)
+    gptq.check_g_idx(gptq.open_safetensors(p3), "model.layers.0.mlp.gate_proj", TINY.n_embd, 128)
+
+
+def test_url_to_path():
+    assert gptq.url_to_path("file:///tmp/a%20b/model.safetensors") == "/tmp/a b/model.safetensors"
+    assert gptq.url_to_path("models/x/model.safetensors") == "models/x/model.safetensors"
+    assert gptq.url_to_path("/abs/model.safetensors") == "/abs/model.safetensors"
+    with pytest.raises(ValueError, match="local path"):
+        gptq.url_to_path("https://huggingface.co/x/model.safetensors")

@@ -57,8 +57,19 @@ def _js_config(c):
 @needs_node
 def test_addon_exports_and_host_logic(tmp_path):
     assert os.path.exists(ADDON), "run __graft_entry__.build() first"
-    write_checkpoint(str(tmp_path / "model.safetensors"), TINY)
+    kept = write_checkpoint(str(tmp_path / "model.safetensors"), TINY)
+    write_checkpoint(str(tmp_path / "act_order.safetensors"), TINY, act_order=(1, "gateW"))
     res = _node("abi", tmp_path, 120)
+    pr = res["probes"]
+    assert pr["gIdxOk"] is None
+    assert "is not the identity map i/128" in pr["gIdxActOrder"]
+    rows = np.fromfile(tmp_path / "rows.f32", dtype=np.float32)
+    assert np.array_equal(rows, kept["embed"][5:8].astype(np.float32).reshape(-1))
+    t, _ = kept[(0, "kW")]
+    nib = (t.qzeros[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15
+    assert pr["zerosK"] == np.bincount(nib.reshape(-1)[: t.qzeros.shape[0] * t.N], minlength=16).tolist()
+    assert pr["urls"] == ["/tmp/a b/model.safetensors", "rel/model.safetensors"]
+    assert "only a local path" in pr["badUrl"]
     assert res["exports"] == sorted(BINDING)
     declared = set(ql.header_functions())
     assert set(BINDING.values()) <= declared
@@ -78,6 +89,7 @@ def test_addon_exports_and_host_logic(tmp_path):
 @pytest.mark.gpu
 def test_node_host_matches_oracle(tmp_path, orc):
     kept = write_checkpoint(str(tmp_path / "model.safetensors"), TINY)
+    write_checkpoint(str(tmp_path / "act_order.safetensors"), TINY, act_order=(1, "downW"))
     shapes = gptq.qwen_linear_shapes(TINY)
     cases = {"config": _js_config(TINY), "gemm": [], "batch": []}
     refs = {}
@@ -123,6 +135,16 @@ def test_node_host_matches_oracle(tmp_path, orc):
                           "K": [shapes[k][0] for k in ua], "outs": [f"ua_{k}.f16" for k in ua]}
     cases["dequant"] = {"prefix": "model.layers.1.mlp.down_proj", "K": shapes["downW"][0],
                         "N": shapes["downW"][1], "out": "w.f32"}
+    rng_s = np.random.default_rng(0x40E6)
+    dK, dN, dG = 256, 48, 64
+    d_qw = rng_s.integers(0, 1 << 32, size=(dK // 8, dN), dtype=np.uint64).astype(np.uint32)
+    d_qz = rng_s.integers(0, 1 << 32, size=(dK // dG, dN // 8), dtype=np.uint64).astype(np.uint32)
+    d_sc = (rng_s.standard_normal((dK // dG, dN)) * 0.01).astype(np.float32)
+    d_sc[0, :8], d_sc[1, :8] = np.float32(1e-44), np.float32(3e38)
+    for name, arr in (("dq_qw", d_qw), ("dq_qz", d_qz), ("dq_sc", d_sc)):
+        arr.tofile(tmp_path / name)
+    cases["dequantF32"] = {"qweight": "dq_qw", "qzeros": "dq_qz", "scales": "dq_sc", "K": dK, "N": dN,
+                           "group": dG, "out": "w32.f32"}
     # residual add + RMSNorm over the loaded L0.inNorm (ones in the checkpoint), SiLU-mul, and
     # three decode steps of the KV cache on layer 1
     ex, er = synth.activations(2, TINY.n_embd, seed=0x40E1), synth.activations(2, TINY.n_embd, seed=0x40E2)
@@ -188,9 +210,23 @@ def test_node_host_matches_oracle(tmp_path, orc):
         ok, max_abs, _ = orc.check_tolerance(y, ref, atol, 1e-4)
         assert ok, f"seq {k}: maxAbs {max_abs:.3e}"
         x_in = y
+    got = np.fromfile(tmp_path / "w32.f32", dtype=np.float32).reshape(dN, dK)
+    _, want = orc.dequantize_gptq_int4(d_qw, d_qz, d_sc, dK, dN, dG)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert res["isPromise"]
+    assert np.array_equal(np.fromfile(tmp_path / "embed_rows.f32", dtype=np.float32),
+                          kept["embed"][100:104].astype(np.float32).reshape(-1))
+    want_z = np.zeros(16, np.int64)
+    for key, (t, _) in ((k, v) for k, v in kept.items() if k != "embed"):
+        nib = (t.qzeros[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15
+        want_z += np.bincount(nib.reshape(t.qzeros.shape[0], -1)[:, :t.N].reshape(-1), minlength=16)
+    assert res["storedZeros"] == {str(v): int(c) for v, c in enumerate(want_z) if c}
+    assert "model.layers.1.mlp.down_proj.g_idx" in res["actOrder"]
     e = res["errors"]
     assert "missing int4 weight: L9.qW" in e["missingWeight"]
     assert "called with N=" in e["wrongShape"]
     assert "missing f32 weight: L0.oB" in e["missingBias"]
     assert "already exists" in e["duplicate"]
     assert "QL_E_BITS" in e["bits"]
+    assert "share one arena" in e["rmsnormArena"] and "share one arena" in e["rmsnormSumArena"]
+    assert "share one arena" in e["attendArena"]

@@ -165,7 +165,8 @@ int plan_impl(int M, int N, int K, int group, ql_plan* p)
     return QL_OK;
 }
 
-int validate_desc(const ql_gptq_desc* d, uint64_t arena_bytes)
+// validate_desc with scales of `scale_bytes` bytes per value (2: fp16 as stored, 4: f32)
+int validate_desc_scales(const ql_gptq_desc* d, uint64_t arena_bytes, int scale_bytes)
 {
     if (!d) return fail(QL_E_INVALID, "null descriptor");
     if (d->bits != 4) return fail(QL_E_BITS, "GPTQ: only 4-bit is supported, got bits=%d", d->bits);
@@ -173,6 +174,7 @@ int validate_desc(const ql_gptq_desc* d, uint64_t arena_bytes)
     if (d->K <= 0 || d->N <= 0) return fail(QL_E_DIMS, "GPTQ: in/out features must be positive");
     uint64_t qw, qz, sc;
     ql_gptq_sizes(d->K, d->N, d->group, &qw, &qz, &sc);
+    sc = sc / 2 * (uint64_t)scale_bytes;
     if (!in_range(d->qweight_off, qw, arena_bytes))
         return fail(QL_E_QWEIGHT_SHORT, "GPTQ: qweight needs %llu bytes at offset %llu, arena has %llu",
                     (unsigned long long)qw, (unsigned long long)d->qweight_off,
@@ -189,11 +191,13 @@ int validate_desc(const ql_gptq_desc* d, uint64_t arena_bytes)
         return fail(QL_E_GROUP_PACK, "GPTQ: group size %d must be a multiple of 8", d->group);
     if (d->bias_off != QL_NONE && !in_range(d->bias_off, (uint64_t)d->N * 4, arena_bytes))
         return fail(QL_E_RANGE, "bias [N] f32 outside the weight arena");
-    if (d->qweight_off % 4 || (d->qzeros_off != QL_NONE && d->qzeros_off % 4) || d->scales_off % 2 ||
-        (d->bias_off != QL_NONE && d->bias_off % 4))
+    if (d->qweight_off % 4 || (d->qzeros_off != QL_NONE && d->qzeros_off % 4) ||
+        d->scales_off % (uint64_t)scale_bytes || (d->bias_off != QL_NONE && d->bias_off % 4))
         return fail(QL_E_ALIGN, "misaligned GPTQ tensor offset (int32/f32: 4 B, f16: 2 B)");
     return QL_OK;
 }
+
+int validate_desc(const ql_gptq_desc* d, uint64_t arena_bytes) { return validate_desc_scales(d, arena_bytes, 2); }
 
 int check_desc(const ql_gptq_desc* d, const ql_arena* w)
 {
@@ -650,7 +654,7 @@ int ql_unpack_f16(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, q
     const int P = (d->K + 7) / 8;
     if (P > 65535) return fail(QL_E_INVALID, "K too large (%d)", d->K);
     if ((rc = set_device(ctx))) return rc;
-    ql::UnpackArgs a;
+    ql::UnpackArgs a{};
     a.qweight = reinterpret_cast<const uint32_t*>(weights->base + d->qweight_off);
     a.qzeros = d->qzeros_off == QL_NONE ? nullptr
                                         : reinterpret_cast<const uint32_t*>(weights->base + d->qzeros_off);
@@ -720,15 +724,24 @@ int ql_unpack_f16_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs, c
 int ql_unpack_f32(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_arena* out,
                   uint64_t out_off)
 {
+    return ql_unpack_f32_ex(ctx, d, weights, QL_DTYPE_F16, out, out_off);
+}
+
+int ql_unpack_f32_ex(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, int32_t scales_dtype,
+                     ql_arena* out, uint64_t out_off)
+{
     if (!ctx || !out) return fail(QL_E_INVALID, "null context or output arena");
-    int rc = check_desc(d, weights);
+    if (scales_dtype != QL_DTYPE_F16 && scales_dtype != QL_DTYPE_F32)
+        return fail(QL_E_INVALID, "scales dtype must be QL_DTYPE_F16 or QL_DTYPE_F32");
+    if (!weights) return fail(QL_E_INVALID, "null descriptor or weight arena");
+    int rc = validate_desc_scales(d, weights->size, scales_dtype == QL_DTYPE_F32 ? 4 : 2);
     if (rc) return rc;
     if (!in_range(out_off, (uint64_t)d->N * d->K * 4, out->size))
         return fail(QL_E_RANGE, "fp32 [N,K] output outside the arena");
     if (out_off % 16) return fail(QL_E_ALIGN, "fp32 output offset must be 16-byte aligned");
     if ((d->K + 7) / 8 > 65535) return fail(QL_E_INVALID, "K too large (%d)", d->K);
     if ((rc = set_device(ctx))) return rc;
-    ql::UnpackArgs a;
+    ql::UnpackArgs a{};
     a.qweight = reinterpret_cast<const uint32_t*>(weights->base + d->qweight_off);
     a.qzeros = d->qzeros_off == QL_NONE ? nullptr
                                         : reinterpret_cast<const uint32_t*>(weights->base + d->qzeros_off);
@@ -737,6 +750,8 @@ int ql_unpack_f32(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, q
     a.N = d->N;
     a.K = d->K;
     a.group = d->group;
+    a.scales_f32 = scales_dtype == QL_DTYPE_F32 ? reinterpret_cast<const float*>(weights->base + d->scales_off)
+                                                : nullptr;
     QL_HIP(ql::launch_unpack_f32(a, ctx->stream));
     return QL_OK;
 }
@@ -996,9 +1011,14 @@ int ql_add_rmsnorm(ql_ctx* ctx, ql_arena* act, uint64_t x_off, uint64_t d_off, c
     const uint64_t ya = y_off, yb = y_off + rb;
     auto overlaps = [&](uint64_t o) { return o != QL_NONE && o < yb && ya < o + rb; };
     if (overlaps(x_off) || overlaps(d_off) || overlaps(sum_off)) return fail(QL_E_INVALID, "y overlaps an input or the sum");
+    // the sum may replace x or d in place (same offset), never overlap them partly: other
+    // threads' elements would change under their reads
+    auto partly = [&](uint64_t o) { return o != QL_NONE && o != sum_off && o < sum_off + rb && sum_off < o + rb; };
+    if (sum_off != QL_NONE && (partly(x_off) || partly(d_off)))
+        return fail(QL_E_INVALID, "the sum partly overlaps x or d (in place it must start at the same offset)");
     int rc = set_device(ctx);
     if (rc) return rc;
-    ql::ElemArgs a;
+    ql::ElemArgs a{};
     a.x = reinterpret_cast<const float*>(act->base + x_off);
     a.d = d_off == QL_NONE ? nullptr : reinterpret_cast<const float*>(act->base + d_off);
     a.w = reinterpret_cast<const float*>(weights->base + w_off);

@@ -8,7 +8,9 @@
 //                       plain RMSNorm. One workgroup per row; the row's sum of squares is added
 //                       per thread, then per wave (butterfly), then over the 4 waves in order.
 //                       Rows up to 4096 values stay in registers (one read of x, d and w); longer
-//                       rows read x and d a second time for the output.
+//                       rows read the stored sum (or x and d) a second time for the output. The
+//                       sum may be stored in place over x or d (the residual stream updated in
+//                       place): every thread reads back only what it wrote.
 //   silu_mul_kernel     y = (g / (1 + exp(-g))) * u, four values per thread.
 //
 // Both are HBM-bound streams (bytes per row: x, d, s and y once; per element of silu_mul: g, u, y).
@@ -96,13 +98,20 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const ElemArgs a)
     __syncthreads();
     const float total = (red[0] + red[1]) + (red[2] + red[3]);
     const float rstd = 1.0f / sqrtf(total / (float)C + a.eps);
-    // second pass: x and d again (L2-resident: this workgroup just read them)
+    // second pass: the stored sum (each thread reads back exactly the elements it wrote, so an
+    // in-place sum over x or d is read correctly), else x and d again (L2-resident: this
+    // workgroup just read them)
     if (a.vec) {
         for (int i = threadIdx.x; i < C / 4; i += 256) {
-            f32x4 v = ld_global(reinterpret_cast<const f32x4*>(x) + i);
-            if (d) {
-                const f32x4 w = ld_global(reinterpret_cast<const f32x4*>(d) + i);
-                v = f32x4{v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w};
+            f32x4 v;
+            if (s_out) {
+                v = ld_global(reinterpret_cast<const f32x4*>(s_out) + i);
+            } else {
+                v = ld_global(reinterpret_cast<const f32x4*>(x) + i);
+                if (d) {
+                    const f32x4 w = ld_global(reinterpret_cast<const f32x4*>(d) + i);
+                    v = f32x4{v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w};
+                }
             }
             const f32x4 g = ld_global(reinterpret_cast<const f32x4*>(a.w) + i);
             st_global(reinterpret_cast<f32x4*>(y) + i,
@@ -110,8 +119,13 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const ElemArgs a)
         }
     } else {
         for (int i = threadIdx.x; i < C; i += 256) {
-            float v = x[i];
-            if (d) v = v + d[i];
+            float v;
+            if (s_out) {
+                v = s_out[i];
+            } else {
+                v = x[i];
+                if (d) v = v + d[i];
+            }
             y[i] = v * rstd * a.w[i];
         }
     }

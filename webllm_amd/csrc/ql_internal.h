@@ -92,6 +92,8 @@ struct UnpackArgs {
     const uint16_t* scales;
     void* out;                 // fp16 [N,K] (launch_unpack) or fp32 [N,K] (launch_unpack_f32)
     int N, K, group;
+    const float* scales_f32;   // launch_unpack_f32 only: f32 scales [K/group, N] used instead of
+                               // `scales` when set
 };
 hipError_t launch_unpack(const UnpackArgs& a, bool fast, hipStream_t stream);
 // Batched fp16 unpack: up to kUnpackBatch tensors (each meeting the tile path's conditions: N % 4 == 0,

@@ -173,7 +173,10 @@ __global__ __launch_bounds__(256) void unpack_f32_kernel(UnpackArgs a)
     const int g = (p * 8) / a.group;
     const uint32_t w = a.qweight[(size_t)p * a.N + n];
     const int z = (int)zero_of(a.qzeros, g, NC, n);
-    const float s = (float)__builtin_bit_cast(_Float16, a.scales[(size_t)g * a.N + n]);
+    // (q - z) * s: one fp32 rounding of the exact product, as the reference's JS-number product
+    // stored into a Float32Array (quant.ts:111-112); exact for fp16 scales
+    const float s = a.scales_f32 ? a.scales_f32[(size_t)g * a.N + n]
+                                 : (float)__builtin_bit_cast(_Float16, a.scales[(size_t)g * a.N + n]);
     float v[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) v[k] = (float)((int)((w >> (4 * k)) & 15u) - z) * s;

@@ -11,6 +11,8 @@ Same names, argument meaning and error behaviour as the reference's TypeScript s
                                             the packed tensors are uploaded as they are
   QuantLinearModel.gemm                     src/model/qwen.ts:568-618 QwenGpt.gemm
   load_qwen_weights                         src/weights/qwen-loader.ts:102-177 loadQwenWeights
+  read_f16_rows                             src/weights/qwen-loader.ts:70-93 readF16Rows
+  check_g_idx / stored_zero_counts          src/tests/qwen/qwen-format.ts:112-130 (format probes)
   QwenConfig / QWEN25_05B / qwen_kv_dim     src/model/qwen-config.ts:1-54
 
 Tensors are slices of device arenas (`Tensor{arena, offset, length, shape}`, buffer.ts:12-18);
@@ -339,6 +341,10 @@ class QuantLinearModel:
         off = self._place(bits)
         self.f16[name] = Tensor(self.weights, off, int(np.prod(shape)), tuple(shape), "f16")
 
+    def release(self):
+        """Frees the weight arena (the reference's QwenGpt.destroy of its weight buffers)."""
+        self.weights.release()
+
     def linear(self, name: str) -> _Linear:
         lin = self.linears.get(name)
         if lin is None:
@@ -447,13 +453,10 @@ class QuantLinearModel:
 
 def dequantize_gptq_int4(ctx: ql.Context, qweight, qzeros, scales, in_features: int,
                          out_features: int, group_size: int = 128, bits: int = 4) -> np.ndarray:
-    """quant.ts:42-118 with the same inputs (raw I32 bytes, f32 scales decoded from F16) and the
-    same output (fp32 [out, in]), computed on the GPU. The f32 scales must be fp16 values, which
-    they are when read from the checkpoint's F16 tensor (readTensorF32)."""
+    """quant.ts:42-118 with the same inputs (raw I32 bytes, any f32 scales — GptqInt4Params.scales
+    is a Float32Array, quant.ts:22-23) and the same output (fp32 [out, in]), computed on the GPU
+    (ql_unpack_f32_ex with f32 scales: bit-identical for every f32 scale)."""
     sc = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
-    s16 = sc.astype(np.float16)
-    if not np.array_equal(s16.astype(np.float32), sc, equal_nan=True):
-        raise ValueError("dequantize_gptq_int4: scales must be fp16-representable (F16 checkpoint)")
     qw = np.frombuffer(bytes(qweight), dtype=np.uint8)
     qz = None if qzeros is None else np.frombuffer(bytes(qzeros), dtype=np.uint8)
     # quant.ts:46-79 order: bits, group, dims, qweight bytes, scales count, qzeros bytes, group % 8
@@ -464,8 +467,8 @@ def dequantize_gptq_int4(ctx: ql.Context, qweight, qzeros, scales, in_features: 
     need_qw, need_qz, need_sc = ql.gptq_sizes(in_features, out_features, group_size)
     if qw.nbytes < need_qw:
         raise ql.QlError(-4, f"GPTQ: qweight needs {need_qw} bytes, got {qw.nbytes}")
-    if s16.nbytes < need_sc:
-        raise ql.QlError(-5, f"GPTQ: scales need {need_sc // 2} values, got {s16.size}")
+    if sc.size < need_sc // 2:
+        raise ql.QlError(-5, f"GPTQ: scales need {need_sc // 2} values, got {sc.size}")
     if qz is not None and qz.nbytes < need_qz:
         raise ql.QlError(-6, f"GPTQ: qzeros need {need_qz} bytes, got {qz.nbytes}")
     if shape_rc == -7:
@@ -473,7 +476,7 @@ def dequantize_gptq_int4(ctx: ql.Context, qweight, qzeros, scales, in_features: 
     lay = ql.ArenaLayout()
     o_qw = lay.take(need_qw)
     o_qz = None if qz is None else lay.take(need_qz)
-    o_sc = lay.take(need_sc)
+    o_sc = lay.take(2 * need_sc)                  # f32 scales
     desc = ql.make_desc(o_qw, o_qz, o_sc, in_features, out_features, group_size, None, bits)
     w = ctx.arena(lay.used + 256)
     out = ctx.arena(max(in_features * out_features * 4, 16))
@@ -481,8 +484,8 @@ def dequantize_gptq_int4(ctx: ql.Context, qweight, qzeros, scales, in_features: 
         w.write(o_qw, qw[:need_qw])
         if qz is not None:
             w.write(o_qz, qz[:need_qz])
-        w.write(o_sc, s16.view(np.uint16)[:need_sc // 2])
-        ctx.unpack_f32(desc, w, out, 0)
+        w.write(o_sc, sc[:need_sc // 2])
+        ctx.unpack_f32(desc, w, out, 0, ql.DTYPE_F32)
         return out.read(0, (out_features, in_features), np.float32)
     finally:
         w.release()
@@ -497,12 +500,75 @@ _PROJ = [("qW", "self_attn.q_proj"), ("kW", "self_attn.k_proj"), ("vW", "self_at
 _BIASED = {"qW", "kW", "vW"}
 
 
+QWEN_LOCAL_DIR = "models/qwen2.5-0.5b-int4/"     # qwen-loader.ts:27 (public/models layout)
+
+
 @dataclass
 class QwenLoadResult:
     gpu_bytes: int
     tensor_count: int
     file_bytes: int
     layer: dict | None = None
+    embed_rows: np.ndarray | None = None      # keep_embed_rows: fp32 [rows * C]
+    # stored qzeros nibbles over every GPTQ linear: {nibble: count}; {7: n} for the symmetric
+    # 4-bit checkpoints tests/qwen/qwen-format.ts:112-123 expects (zero 8 stored as 7)
+    stored_zeros: dict = field(default_factory=dict)
+
+
+def url_to_path(url: str) -> str:
+    """A local file path or a file:// URL (the reference fetches `url`, qwen-loader.ts:113-115;
+    this host reads local files only: there is no network)."""
+    from urllib.parse import unquote, urlparse
+    u = urlparse(url)
+    if u.scheme == "file":
+        return unquote(u.path)
+    if u.scheme in ("", ) or (len(u.scheme) == 1 and url[1:3] in (":\\", ":/")):
+        return url
+    raise ValueError(f"qwen-loader: cannot load {url}: only a local path or a file:// URL")
+
+
+def read_f16_rows(f: SafetensorFile, name: str, row_start: int, row_count: int,
+                  row_length: int) -> np.ndarray:
+    """readF16Rows (qwen-loader.ts:70-93): rows [row_start, row_start + row_count) of a 2-D F16
+    tensor, decoded to fp32 (flat)."""
+    e = require_tensor(f, name)
+    if e.dtype != "F16":
+        raise ValueError(f"qwen-loader: {name} expected F16, got {e.dtype}")
+    if len(e.shape) != 2 or e.shape[0] * row_length != e.shape[0] * e.shape[1]:
+        raise ValueError(f"qwen-loader: {name} shape {e.shape} does not match rowLength={row_length}")
+    if row_start < 0 or row_count < 0 or row_start + row_count > e.shape[0]:
+        raise ValueError(f"qwen-loader: rows [{row_start}, {row_start + row_count}) outside {name} "
+                         f"[{e.shape[0]}, {e.shape[1]}]")
+    start = f.data_start + e.data_offsets[0] + row_start * row_length * 2
+    raw = np.frombuffer(f.buffer[start:start + row_count * row_length * 2], dtype="<u2")
+    return f16_bits_to_f32(raw)
+
+
+def check_g_idx(f: SafetensorFile, prefix: str, in_features: int, group_size: int):
+    """desc_act=false: g_idx, when present, must be the identity map i // group
+    (tests/qwen/qwen-format.ts:125-130); the fused kernels assume it, so any other order
+    (an act-order checkpoint) is rejected instead of loaded wrong."""
+    name = f"{prefix}.g_idx"
+    if name not in f.header:
+        return
+    e = expect_tensor(f, name, "I32", [in_features])
+    g = np.frombuffer(read_tensor_bytes(f, name), dtype="<i4")
+    want = np.arange(in_features, dtype=np.int64) // group_size
+    bad = np.nonzero(g != want)[0]
+    if bad.size:
+        i = int(bad[0])
+        raise ValueError(f"qwen-loader: {name}[{i}] = {int(g[i])} is not the identity map i/{group_size} "
+                         f"(desc_act checkpoints are not supported)")
+    del e
+
+
+def stored_zero_counts(qzeros, groups: int, out_features: int) -> np.ndarray:
+    """Counts of each stored qzeros nibble (0..15) over the real columns of a linear
+    (qwen-format.ts:112-123 collects the same set)."""
+    nc = (out_features + 7) // 8
+    w = np.frombuffer(qzeros, dtype="<u4")[:groups * nc].reshape(groups, nc)
+    nib = (w[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15
+    return np.bincount(nib.reshape(groups, nc * 8)[:, :out_features].reshape(-1), minlength=16)
 
 
 def qwen_linear_shapes(c: QwenConfig) -> dict:
@@ -518,13 +584,22 @@ def open_safetensors(path: str) -> SafetensorFile:
     return parse_safetensors(mm)
 
 
-def load_qwen_weights(model: QuantLinearModel, path: str, config: QwenConfig = QWEN25_05B,
+def load_qwen_weights(model: QuantLinearModel, path: str | None = None, config: QwenConfig = QWEN25_05B,
                       on_progress=None, keep_layer: int | None = None,
-                      group_size: int = 128) -> QwenLoadResult:
+                      group_size: int = 128, url: str | None = None,
+                      keep_embed_rows: tuple | dict | None = None) -> QwenLoadResult:
     """loadQwenWeights (qwen-loader.ts:102-177): embed (F16, tied lm_head), final norm, then per
     layer the 7 GPTQ linears, q/k/v biases and the two norms. The int4 tensors go to the GPU
     packed — no CPU dequant — after the shape checks the reference's format probe makes
-    (tests/qwen/qwen-format.ts:72-80)."""
+    (tests/qwen/qwen-format.ts:72-80) and its g_idx identity check (:125-130); the stored-zero
+    nibbles are counted into the result (:112-123).
+
+    The file is `url` (a path or file:// URL, default QWEN_LOCAL_DIR + "model.safetensors", as
+    qwen-loader.ts:113) or `path`, memory-mapped. keep_layer returns that layer's fp32 weights;
+    keep_embed_rows = (start, rows) or {"start", "rows"} returns those embed rows in fp32
+    (qwen-loader.ts:134-135)."""
+    if path is None:
+        path = url_to_path(url if url is not None else QWEN_LOCAL_DIR + "model.safetensors")
     f = open_safetensors(path)
     count = 0
     C = config.n_embd
@@ -537,10 +612,16 @@ def load_qwen_weights(model: QuantLinearModel, path: str, config: QwenConfig = Q
     model.upload_f16_bits("embed", read_tensor_bytes(f, "model.embed_tokens.weight"),
                           (config.vocab_size, C))
     count += 1
+    embed_rows = None
+    if keep_embed_rows is not None:
+        start, rows = ((keep_embed_rows["start"], keep_embed_rows["rows"])
+                       if isinstance(keep_embed_rows, dict) else keep_embed_rows)
+        embed_rows = read_f16_rows(f, "model.embed_tokens.weight", start, rows, C)
     model.upload_f32("finalNorm", read_tensor_f32(f, "model.norm.weight"))
     count += 1
     shapes = qwen_linear_shapes(config)
     kept = None
+    zeros = np.zeros(16, dtype=np.int64)
     for i in range(config.n_layer):
         p = f"model.layers.{i}"
         model.upload_f32(f"L{i}.inNorm", read_tensor_f32(f, f"{p}.input_layernorm.weight"))
@@ -554,6 +635,8 @@ def load_qwen_weights(model: QuantLinearModel, path: str, config: QwenConfig = Q
             expect_tensor(f, f"{pre}.qweight", "I32", [P, N])
             expect_tensor(f, f"{pre}.qzeros", "I32", [G, NC])
             expect_tensor(f, f"{pre}.scales", "F16", [G, N])
+            check_g_idx(f, pre, K, group_size)
+            zeros += stored_zero_counts(read_tensor_bytes(f, f"{pre}.qzeros"), G, N)
             bias = read_tensor_f32(f, f"{pre}.bias") if key in _BIASED else None
             model.upload_gptq_linear(f"L{i}.{key}", read_tensor_bytes(f, f"{pre}.qweight"),
                                      read_tensor_bytes(f, f"{pre}.qzeros"),
@@ -565,7 +648,8 @@ def load_qwen_weights(model: QuantLinearModel, path: str, config: QwenConfig = Q
             kept = layer
         if on_progress:
             on_progress(i + 1, config.n_layer, f"layer {i + 1}/{config.n_layer}")
-    return QwenLoadResult(model.weight_bytes, count, f.buffer.nbytes, kept)
+    return QwenLoadResult(model.weight_bytes, count, f.buffer.nbytes, kept, embed_rows,
+                          {int(v): int(c) for v, c in enumerate(zeros) if c})
 
 
 def write_safetensors(path: str, tensors: dict, metadata: dict | None = None):

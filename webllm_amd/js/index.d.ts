@@ -70,7 +70,7 @@ export interface GptqInt4Params {
     qweight: Uint8Array; qzeros?: Uint8Array | null; scales: Float32Array;
     inFeatures: number; outFeatures: number; groupSize?: number; bits?: number;
 }
-/** quant.ts dequantizeGptqInt4, computed on the GPU: fp32 [outFeatures, inFeatures]. */
+/** quant.ts dequantizeGptqInt4, computed on the GPU: fp32 [outFeatures, inFeatures], for any f32 scales. */
 export function dequantizeGptqInt4(params: GptqInt4Params, ctx?: Context): Float32Array;
 
 export class Tensor {
@@ -121,13 +121,27 @@ export class KvCache {
     release(): void;
 }
 
+/** qwen-loader.ts:29-38, plus this host's config / groupSize and path / buffer alternatives to url. */
 export interface QwenLoadOptions {
+    /** a local path or file:// URL; default QWEN_LOCAL_DIR + 'model.safetensors' */
+    url?: string;
+    onProgress?: (done: number, total: number, label: string) => void;
+    keepLayer?: number;
+    keepEmbedRows?: { start: number; rows: number };
     path?: string; buffer?: ArrayBuffer | Uint8Array; config?: QwenConfig; groupSize?: number;
-    keepLayer?: number; onProgress?: (done: number, total: number, label: string) => void;
 }
+/** qwen-loader.ts:40-52, plus storedZeros: {nibble: count} of the stored qzeros (qwen-format.ts:112-123). */
 export interface QwenLoadResult {
     gpuBytes: number; tensorCount: number; fileBytes: number;
     layer?: Record<'qW' | 'kW' | 'vW' | 'oW' | 'gateW' | 'upW' | 'downW', Float32Array>;
+    embedRows?: Float32Array;
+    storedZeros: Record<number, number>;
 }
+export const QWEN_LOCAL_DIR: string;
 export function qwenLinearShapes(c: QwenConfig): Record<string, [number, number]>;
-export function loadQwenWeights(ctx: Context | null, model: QuantLinearModel, options: QwenLoadOptions): QwenLoadResult;
+/** Rejects (throws asynchronously) on a malformed file, wrong shapes or a non-identity g_idx. */
+export function loadQwenWeights(ctx: Context | null, model: QuantLinearModel, options?: QwenLoadOptions): Promise<QwenLoadResult>;
+export function urlToPath(url: string): string;
+export function readF16Rows(file: SafetensorFile, name: string, rowStart: number, rowCount: number, rowLength: number): Float32Array;
+export function checkGIdx(file: SafetensorFile, prefix: string, inFeatures: number, group: number): void;
+export function countStoredZeros(qzeros: Uint8Array, groups: number, outFeatures: number, counts: number[]): number[];

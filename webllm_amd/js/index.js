@@ -11,8 +11,10 @@
  *   dequantizeGptqInt4(params)                   src/weights/quant.ts:42-118 (exact, on the GPU)
  *   QuantLinearModel.gemm(A, weight, C, bias,    src/model/qwen.ts:568-618 QwenGpt.gemm
  *     M, N, K)
- *   loadQwenWeights(ctx, model, options)         src/weights/qwen-loader.ts:102-177, with the
- *                                                packed int4 tensors uploaded as they are
+ *   loadQwenWeights(ctx, model, options)         src/weights/qwen-loader.ts:102-177 (async), with
+ *                                                the packed int4 tensors uploaded as they are
+ *   readF16Rows                                  src/weights/qwen-loader.ts:70-93
+ *   checkGIdx, countStoredZeros                  src/tests/qwen/qwen-format.ts:112-130 probes
  *   QWEN25_05B, qwenKvDim                        src/model/qwen-config.ts:1-54
  *
  * Errors are thrown as Error (the reference's `throw new Error(msg)`); library status codes carry
@@ -258,34 +260,12 @@ function libError(code, message) {
 
 // ------------------------------------------------------------------ quant.ts
 
-function toF16Bits(scales) {
-    const f32 = Float32Array.from(scales);
-    const out = new Uint16Array(f32.length);
-    const u = new Uint32Array(f32.buffer);
-    for (let i = 0; i < f32.length; i++) {
-        // fp16-representable inputs only (checked below): exact re-encode, no rounding needed
-        const x = u[i];
-        const sign = (x >>> 16) & 0x8000;
-        const e = (x >>> 23) & 0xff;
-        const m = x & 0x7fffff;
-        let h;
-        if (e === 0xff) h = sign | 0x7c00 | (m ? 0x200 | (m >>> 13) : 0);
-        else if (e === 0 && m === 0) h = sign;
-        else if (e >= 113) h = sign | ((e - 112) << 10) | (m >>> 13);
-        else h = sign | ((0x800000 | m) >>> (126 - e));
-        out[i] = h;
-        if (!(f16BitsToF32(h) === f32[i] || (Number.isNaN(f32[i]) && Number.isNaN(f16BitsToF32(h))))) {
-            throw new Error('dequantizeGptqInt4: scales must be fp16-representable (F16 checkpoint)');
-        }
-    }
-    return out;
-}
-
 let defaultCtx = null;
 
 /**
  * quant.ts:42-118: GptqInt4Params -> fp32 [outFeatures, inFeatures], computed on the GPU
- * (ql_unpack_f32, bit-identical to the reference's loop). `ctx` defaults to device 0.
+ * (ql_unpack_f32_ex with the f32 scales as given: any Float32Array, quant.ts:22-23; bit-identical
+ * to the reference's loop). `ctx` defaults to device 0.
  */
 function dequantizeGptqInt4(params, ctx) {
     const groupSize = params.groupSize === undefined || params.groupSize === null ? 128 : params.groupSize;
@@ -307,20 +287,20 @@ function dequantizeGptqInt4(params, ctx) {
         throw libError('QL_E_QZEROS_SHORT', `GPTQ: qzeros need ${need.qzerosBytes} bytes, got ${qz.byteLength}`);
     }
     if (shapeRc === -7) throw libError('QL_E_GROUP_PACK', `GPTQ: groupSize=${groupSize} must be a multiple of 8`);
-    const s16 = toF16Bits(params.scales.subarray(0, need.scalesBytes / 2));
+    const s32 = Float32Array.from(params.scales.subarray(0, need.scalesBytes / 2));
     if (!ctx) { if (!defaultCtx) defaultCtx = new Context(0); ctx = defaultCtx; }
     const lay = new ArenaLayout();
     const oQw = lay.take(need.qweightBytes);
     const oQz = qz ? lay.take(need.qzerosBytes) : null;
-    const oSc = lay.take(need.scalesBytes);
+    const oSc = lay.take(s32.byteLength);
     const w = ctx.arena(lay.used + 256);
     const out = ctx.arena(Math.max(inF * outF * 4, 16));
     try {
         w.write(oQw, params.qweight.subarray(0, need.qweightBytes));
         if (qz) w.write(oQz, qz.subarray(0, need.qzerosBytes));
-        w.write(oSc, s16);
+        w.write(oSc, s32);
         addon.unpack(ctx.handle, makeDesc(oQw, oQz, oSc, inF, outF, groupSize, null, bits), w.handle,
-            out.handle, 0, true);
+            out.handle, 0, true, QL_DTYPE_F32);
         return out.read(0, new Float32Array(outF * inF));
     } finally {
         w.release();
@@ -447,6 +427,9 @@ class QuantLinearModel {
         const w = this.f32Weights.get(weight);
         if (!w) throw new Error(`missing f32 weight: ${weight}`);
         if (w.length !== C) throw new Error(`rmsnorm: ${weight} has ${w.length} values, C=${C}`);
+        for (const t of [y, residual, sumOut]) {
+            if (t && t.arena !== x.arena) throw new Error('rmsnorm: x, y, residual and sumOut must share one arena');
+        }
         addon.addRmsNorm(this.ctx.handle, x.arena.handle, x.offset, residual ? residual.offset : null,
             this.weights.handle, w.offset, eps, M, C, sumOut ? sumOut.offset : null, y.offset);
     }
@@ -510,17 +493,82 @@ function qwenLinearShapes(c) {
     return { qW: [C, C], kW: [C, HI], vW: [C, HI], oW: [C, C], gateW: [C, I], upW: [C, I], downW: [I, C] };
 }
 
+const QWEN_LOCAL_DIR = 'models/qwen2.5-0.5b-int4/';   // qwen-loader.ts:27 (public/models layout)
+
+/** A local path or file:// URL -> path (the reference fetches `url`; this host has no network). */
+function urlToPath(url) {
+    if (/^file:/i.test(url)) return decodeURIComponent(new URL(url).pathname);
+    if (/^[a-z][a-z0-9+.-]*:\/\//i.test(url)) throw new Error(`qwen-loader: cannot load ${url}: only a local path or a file:// URL`);
+    return url;
+}
+
+/** readF16Rows (qwen-loader.ts:70-93): rows [rowStart, rowStart+rowCount) of an F16 tensor as fp32. */
+function readF16Rows(file, name, rowStart, rowCount, rowLength) {
+    const entry = requireTensor(file, name);
+    if (entry.dtype !== 'F16') throw new Error(`qwen-loader: ${name} expected F16, got ${entry.dtype}`);
+    if (entry.shape.length !== 2 || entry.shape[0] * rowLength !== entry.shape[0] * entry.shape[1]) {
+        throw new Error(`qwen-loader: ${name} shape ${entry.shape} does not match rowLength=${rowLength}`);
+    }
+    if (rowStart < 0 || rowCount < 0 || rowStart + rowCount > entry.shape[0]) {
+        throw new Error(`qwen-loader: rows [${rowStart}, ${rowStart + rowCount}) outside ${name} [${entry.shape}]`);
+    }
+    const byteStart = file.dataStart + entry.data_offsets[0] + rowStart * rowLength * 2;
+    const view = new DataView(file.buffer.buffer, file.buffer.byteOffset + byteStart, rowCount * rowLength * 2);
+    const out = new Float32Array(rowCount * rowLength);
+    for (let i = 0; i < out.length; i++) out[i] = f16BitsToF32(view.getUint16(i * 2, true));
+    return out;
+}
+
 /**
- * loadQwenWeights (qwen-loader.ts:102-177) for a QuantLinearModel; `ctx` is unused (the model holds
- * its context), as the reference's `_gpu` is. options: {path | buffer,
- * config, keepLayer, onProgress, groupSize}. The int4 tensors go to the GPU packed after the
- * shape checks of tests/qwen/qwen-format.ts:72-80; a kept layer is returned dequantized (fp32).
+ * desc_act=false: g_idx, when present, must be the identity map i / group (qwen-format.ts:125-130).
+ * The fused kernels assume it, so an act-order checkpoint is rejected rather than loaded wrong.
  */
-function loadQwenWeights(ctx, model, options) {
+function checkGIdx(file, prefix, inFeatures, group) {
+    const name = `${prefix}.g_idx`;
+    if (!Object.prototype.hasOwnProperty.call(file.header, name)) return;
+    expectTensor(file, name, 'I32', [inFeatures]);
+    const b = readTensorBytes(file, name);
+    const view = new DataView(b.buffer, b.byteOffset, b.byteLength);
+    for (let i = 0; i < inFeatures; i++) {
+        const g = view.getInt32(i * 4, true);
+        if (g !== Math.floor(i / group)) {
+            throw new Error(`qwen-loader: ${name}[${i}] = ${g} is not the identity map i/${group} (desc_act checkpoints are not supported)`);
+        }
+    }
+}
+
+/** Adds the stored qzeros nibbles of a linear's real columns into counts[0..15] (qwen-format.ts:112-123). */
+function countStoredZeros(qzeros, groups, outFeatures, counts) {
+    const nc = Math.ceil(outFeatures / 8);
+    const view = new DataView(qzeros.buffer, qzeros.byteOffset, qzeros.byteLength);
+    for (let g = 0; g < groups; g++) {
+        for (let n = 0; n < outFeatures; n++) {
+            const word = view.getUint32((g * nc + (n >> 3)) * 4, true);
+            counts[(word >>> (4 * (n & 7))) & 15]++;
+        }
+    }
+    return counts;
+}
+
+/**
+ * loadQwenWeights (qwen-loader.ts:102-177) for a QuantLinearModel: async, like the reference
+ * (`ctx` is unused, as the reference's `_gpu` is; the model holds its context). options (the
+ * reference's QwenLoadOptions, qwen-loader.ts:29-38): url (a local path or file:// URL, default
+ * QWEN_LOCAL_DIR + 'model.safetensors'), onProgress(done, total, label), keepLayer,
+ * keepEmbedRows {start, rows}; and this host's config, groupSize, and path / buffer (a path or an
+ * already-read file instead of url). The int4 tensors go to the GPU packed after the shape checks
+ * of qwen-format.ts:72-80 and its g_idx identity check; the result (QwenLoadResult, :40-52) adds
+ * storedZeros {nibble: count} over every linear (the format probe's stored-zero set, :112-123).
+ */
+async function loadQwenWeights(ctx, model, options) {
     const opt = options || {};
     const config = opt.config || QWEN25_05B;
     const group = opt.groupSize || 128;
-    const raw = opt.buffer || fs.readFileSync(opt.path);
+    let raw = opt.buffer;
+    if (!raw) {
+        const file = opt.path || urlToPath(opt.url !== undefined ? opt.url : `${QWEN_LOCAL_DIR}model.safetensors`);
+        raw = await fs.promises.readFile(file);
+    }
     const file = parseSafetensors(raw);
     const C = config.nEmbd;
     let tensorCount = 0;
@@ -531,9 +579,13 @@ function loadQwenWeights(ctx, model, options) {
     if (emb.dtype !== 'F16') throw new Error(`qwen-loader: model.embed_tokens.weight expected F16, got ${emb.dtype}`);
     model.uploadF16Bits('embed', readTensorBytes(file, 'model.embed_tokens.weight'), [config.vocabSize, C]);
     tensorCount += 1;
+    const embedRows = opt.keepEmbedRows
+        ? readF16Rows(file, 'model.embed_tokens.weight', opt.keepEmbedRows.start, opt.keepEmbedRows.rows, C)
+        : undefined;
     model.uploadF32('finalNorm', readTensorF32(file, 'model.norm.weight'));
     tensorCount += 1;
     const shapes = qwenLinearShapes(config);
+    const zeros = new Array(16).fill(0);
     let kept;
     for (let i = 0; i < config.nLayer; i++) {
         const p = `model.layers.${i}`;
@@ -544,12 +596,16 @@ function loadQwenWeights(ctx, model, options) {
         for (const [key, proj] of PROJ) {
             const [K, N] = shapes[key];
             const pre = `${p}.${proj}`;
+            const G = Math.ceil(K / group);
             expectTensor(file, `${pre}.qweight`, 'I32', [Math.ceil(K / 8), N]);
-            expectTensor(file, `${pre}.qzeros`, 'I32', [Math.ceil(K / group), Math.ceil(N / 8)]);
-            expectTensor(file, `${pre}.scales`, 'F16', [Math.ceil(K / group), N]);
+            expectTensor(file, `${pre}.qzeros`, 'I32', [G, Math.ceil(N / 8)]);
+            expectTensor(file, `${pre}.scales`, 'F16', [G, N]);
+            checkGIdx(file, pre, K, group);
+            const qzeros = readTensorBytes(file, `${pre}.qzeros`);
+            countStoredZeros(qzeros, G, N, zeros);
             const bias = BIASED.has(key) ? readTensorF32(file, `${pre}.bias`) : null;
             model.uploadGptqLinear(`L${i}.${key}`, {
-                qweight: readTensorBytes(file, `${pre}.qweight`), qzeros: readTensorBytes(file, `${pre}.qzeros`),
+                qweight: readTensorBytes(file, `${pre}.qweight`), qzeros,
                 scalesF16: readTensorBytes(file, `${pre}.scales`), inFeatures: K, outFeatures: N,
                 groupSize: group, bias,
             });
@@ -559,7 +615,9 @@ function loadQwenWeights(ctx, model, options) {
         if (opt.keepLayer === i) kept = layer;
         if (opt.onProgress) opt.onProgress(i + 1, config.nLayer, `layer ${i + 1}/${config.nLayer}`);
     }
-    return { gpuBytes: model.weightBytes, tensorCount, fileBytes: raw.byteLength, layer: kept };
+    const storedZeros = {};
+    zeros.forEach((c, v) => { if (c) storedZeros[v] = c; });
+    return { gpuBytes: model.weightBytes, tensorCount, fileBytes: raw.byteLength, layer: kept, embedRows, storedZeros };
 }
 
 /**
@@ -581,11 +639,13 @@ class KvCache {
     }
     store(layer, k, v, rows, pos0) {
         const [ko, vo] = this.offsets(layer);
+        if (k.arena !== v.arena) throw new Error('store: k and v must share one arena');
         addon.kvStore(this.ctx.handle, k.arena.handle, k.offset, this.arena.handle, ko, this.config.blockSize, rows, this.rowLen, pos0);
         addon.kvStore(this.ctx.handle, v.arena.handle, v.offset, this.arena.handle, vo, this.config.blockSize, rows, this.rowLen, pos0);
     }
     attend(layer, q, out, M, pastLen) {
         const c = this.config;
+        if (q.arena !== out.arena) throw new Error('attend: q and out must share one arena');
         const [ko, vo] = this.offsets(layer);
         addon.attention(this.ctx.handle, q.arena.handle, q.offset, this.arena.handle, ko, vo, c.blockSize, M,
             c.nHead, c.nKvHead, this.D, pastLen, out.offset);
@@ -598,5 +658,6 @@ module.exports = {
     dtypeByteSize, parseSafetensorsHeader, parseSafetensors, tensorCount, requireTensor,
     expectTensor, f16BitsToF32, readTensorBytes, readTensorF32, ArenaLayout, Arena, Context,
     makeDesc, dequantizeGptqInt4, Tensor, ActivationArena, QuantLinearModel,
-    qwenLinearShapes, loadQwenWeights, KvCache,
+    qwenLinearShapes, loadQwenWeights, KvCache, QWEN_LOCAL_DIR, urlToPath, readF16Rows, checkGIdx,
+    countStoredZeros,
 };

@@ -387,7 +387,7 @@ static napi_value js_plan_batch(napi_env env, napi_callback_info info)
 
 /* ------------------------------------------------------------------------------------- work */
 
-/* unpack(ctx, desc, weights, out, outOff, f32) */
+/* unpack(ctx, desc, weights, out, outOff, f32[, scalesDtype]) */
 static napi_value js_unpack(napi_env env, napi_callback_info info)
 {
     napi_value argv[6];
@@ -399,7 +399,16 @@ static napi_value js_unpack(napi_env env, napi_callback_info info)
         get_ptr(env, argv[2], &w) || get_ptr(env, argv[3], &o) || get_u64(env, argv[4], &off, 0))
         return NULL;
     napi_get_value_bool(env, argv[5], &f32);
-    throw_rc(env, f32 ? ql_unpack_f32((ql_ctx*)ctx, &d, (ql_arena*)w, (ql_arena*)o, off)
+    /* optional 7th argument: the scales' dtype for the fp32 form (QL_DTYPE_F32: f32 scales) */
+    size_t argc = 7;
+    napi_value all[7];
+    int32_t sdt = QL_DTYPE_F16;
+    if (napi_get_cb_info(env, info, &argc, all, NULL, NULL) == napi_ok && argc >= 7) {
+        napi_valuetype t;
+        if (napi_typeof(env, all[6], &t) == napi_ok && t != napi_undefined && get_i32(env, all[6], &sdt))
+            return NULL;
+    }
+    throw_rc(env, f32 ? ql_unpack_f32_ex((ql_ctx*)ctx, &d, (ql_arena*)w, sdt, (ql_arena*)o, off)
                       : ql_unpack_f16((ql_ctx*)ctx, &d, (ql_arena*)w, (ql_arena*)o, off));
     return NULL;
 }

@@ -113,6 +113,7 @@ def lib():
         "ql_gptq_check": (I, [ctypes.POINTER(GptqDesc), P]),
         "ql_unpack_f16": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64]),
         "ql_unpack_f32": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64]),
+        "ql_unpack_f32_ex": (I, [P, ctypes.POINTER(GptqDesc), P, I, P, U64]),
         "ql_unpack_f16_batch": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64)]),
         "ql_plan_linear": (I, [I, I, I, I, ctypes.POINTER(Plan)]),
         "ql_gemv_f16w": (I, [P, P, U64, U64, P, U64, I, I, I, U64]),
@@ -349,9 +350,11 @@ class Context:
         """y = silu(gate) * up (activation/silu_mul.wgsl)."""
         _check(lib().ql_silu_mul(self.handle, act.handle, gate_off, up_off, n, y_off))
 
-    def unpack_f32(self, desc: GptqDesc, weights: Arena, out: Arena, out_off: int):
-        _check(lib().ql_unpack_f32(self.handle, ctypes.byref(desc), weights.handle, out.handle,
-                                   out_off))
+    def unpack_f32(self, desc: GptqDesc, weights: Arena, out: Arena, out_off: int,
+                   scales_dtype: int = DTYPE_F16):
+        """fp32 [N,K] dequant; scales_dtype DTYPE_F32 reads f32 scales at desc.scales_off."""
+        _check(lib().ql_unpack_f32_ex(self.handle, ctypes.byref(desc), weights.handle, scales_dtype,
+                                      out.handle, out_off))
 
     def linear(self, desc: GptqDesc, weights: Arena, act: Arena, x_off: int, x_dtype: int, M: int,
                y_off: int, scratch_off: int = 0):
