@@ -298,6 +298,32 @@ uint32_t orc_rng_step(uint32_t* state)
 
 double orc_rng_next(uint32_t* state) { return (double)orc_rng_step(state) / 4294967296.0; }
 
+/* src/reference/cpu-ref.ts:50-54 randomF32 with makeRng: out[i] = f32(rng() * 2 - 1), the double
+ * rng() * 2 - 1 being exact and rounded to f32 by the Float32Array store. */
+void orc_random_f32(uint32_t* state, size_t n, float* out)
+{
+    for (size_t i = 0; i < n; i++) out[i] = (float)(orc_rng_next(state) * 2.0 - 1.0);
+}
+
+/* src/model/init.ts:36-52 makeNormal (Box-Muller over makeRng): draws u, v in (0, 1) skipping
+ * zeros, returns r*cos(2*pi*v) and keeps r*sin(2*pi*v) as the next value, r = sqrt(-2 ln u).
+ * double throughout, as JS numbers; Math.log/sin/cos may differ from libm in the last ulp. */
+double orc_normal_next(uint32_t* state, double* spare, int* has_spare)
+{
+    if (*has_spare) {
+        *has_spare = 0;
+        return *spare;
+    }
+    double u = 0.0, v = 0.0;
+    while (u == 0.0) u = orc_rng_next(state);
+    while (v == 0.0) v = orc_rng_next(state);
+    const double r = sqrt(-2.0 * log(u));
+    const double angle = 2.0 * 3.141592653589793 * v;     /* Math.PI */
+    *spare = r * sin(angle);
+    *has_spare = 1;
+    return r * cos(angle);
+}
+
 /* attentionGqaRef (src/reference/qwen-ref.ts:65-111) with the cache's positions
  * (attention_gqa_cache.wgsl): query row m of q [M, H, D] sits at position past + m and sees keys
  * 0 .. past + m of the caches kc / vc [>= past + M, KV * D]. JS arithmetic kept: the dot product,

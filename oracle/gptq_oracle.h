@@ -16,6 +16,8 @@
  *   orc_plan_gemv_split   src/model/qwen.ts:61-74         documented table qwen.ts:54-59 + brute force
  *   orc_check_tolerance   src/reference/cpu-ref.ts:27-47  hand cases
  *   orc_rng_*             src/reference/cpu-ref.ts:57-67  xorshift32 closed form in Python ints
+ *   orc_random_f32        src/reference/cpu-ref.ts:50-54  closed form over Python-int xorshift + numpy f32
+ *   orc_normal_next       src/model/init.ts:36-52         numpy float64 Box-Muller (1 ulp), moments
  */
 #ifndef GPTQ_ORACLE_H
 #define GPTQ_ORACLE_H
@@ -91,6 +93,9 @@ int orc_check_tolerance(const float* got, const float* ref, size_t n, double ato
 uint32_t orc_rng_step(uint32_t* state);
 double orc_rng_next(uint32_t* state);
 void orc_rng_seed(uint32_t* state, uint32_t seed);
+/* randomF32 (cpu-ref.ts:50-54) and makeNormal's Box-Muller (model/init.ts:36-52) over makeRng */
+void orc_random_f32(uint32_t* state, size_t n, float* out);
+double orc_normal_next(uint32_t* state, double* spare, int* has_spare);
 
 #ifdef __cplusplus
 }

@@ -10,7 +10,8 @@ The oracle restates the reference CPU path (intplusplus/webllm):
   gemmNTRef               src/reference/qwen-ref.ts:126-145 (gptq_linear; gptq_linear_cols is the
                           same per output, on a column subset and several threads)
   planGemvSplit           src/model/qwen.ts:61-74
-  checkTolerance/makeRng  src/reference/cpu-ref.ts:27-67
+  checkTolerance/makeRng  src/reference/cpu-ref.ts:27-67 (with randomF32)
+  makeNormal              src/model/init.ts:36-52
   rmsNormRef (+ vec_add)  src/reference/qwen-ref.ts:12-28, src/gpu/kernels/misc/vec_add.wgsl
   siluMulRef              src/reference/qwen-ref.ts:114-121
   attentionGqaRef         src/reference/qwen-ref.ts:65-111 (over a KV cache, with the positions of
@@ -91,6 +92,11 @@ def lib():
         L.orc_rng_next.restype = ctypes.c_double
         L.orc_rng_next.argtypes = [ctypes.POINTER(ctypes.c_uint32)]
         L.orc_rng_seed.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint32]
+        L.orc_random_f32.restype = None
+        L.orc_random_f32.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_size_t, P]
+        L.orc_normal_next.restype = ctypes.c_double
+        L.orc_normal_next.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_int)]
         _lib = L
     return _lib
 
@@ -271,3 +277,22 @@ class Rng:
 
     def __call__(self) -> float:
         return lib().orc_rng_next(ctypes.byref(self.state))
+
+    def random_f32(self, n: int) -> np.ndarray:
+        """randomF32(n, rng) (cpu-ref.ts:50-54): n values f32(rng() * 2 - 1) in [-1, 1)."""
+        out = np.empty(n, dtype=np.float32)
+        lib().orc_random_f32(ctypes.byref(self.state), n, _ptr(out))
+        return out
+
+
+class Normal:
+    """makeNormal(rng) (model/init.ts:36-52): Box-Muller pairs over a makeRng stream."""
+
+    def __init__(self, seed: int):
+        self.rng = Rng(seed)
+        self.spare = ctypes.c_double()
+        self.has = ctypes.c_int(0)
+
+    def __call__(self) -> float:
+        return lib().orc_normal_next(ctypes.byref(self.rng.state), ctypes.byref(self.spare),
+                                     ctypes.byref(self.has))

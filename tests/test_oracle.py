@@ -300,6 +300,48 @@ def test_rng_golden(orc):
     assert r() == 270369 / 2 ** 32
 
 
+def _xorshift_py(seed, n):
+    """makeRng in Python ints (cpu-ref.ts:57-67), independent of the C oracle."""
+    s = (seed & 0xFFFFFFFF) or 1
+    out = []
+    for _ in range(n):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        out.append(s)
+    return out
+
+
+def test_random_f32_closed_form(orc):
+    """randomF32 (cpu-ref.ts:50-54): f32(s/2^32 * 2 - 1) = f32((s - 2^31) / 2^31); the double is
+    exact, numpy rounds it to f32 (RNE) independently; values lie in [-1, 1)."""
+    for seed in (0x9EF0, 0x5E11, 1):
+        got = orc.Rng(seed).random_f32(4096)
+        want = np.array([(s - 2 ** 31) / 2 ** 31 for s in _xorshift_py(seed, 4096)], np.float64).astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        assert got.min() >= -1.0 and got.max() < 1.0
+    # a value that needs rounding: s = 2^31 + 1 gives 2^-31, exact; s = 1 gives -1 + 2^-31 -> -1 in f32
+    assert np.float32((1 - 2 ** 31) / 2 ** 31) == np.float32(-1.0)
+
+
+def test_make_normal_box_muller(orc):
+    """makeNormal (init.ts:36-52): values in pairs (cos first, then the kept sin), zero draws
+    skipped; against a float64 numpy Box-Muller over the Python-int stream to 1e-15 relative
+    (libm vs V8 transcendental last-ulp differences stay within that), and N(0,1) moments."""
+    seed, n = 0x1234, 20000
+    nrm = orc.Normal(seed)
+    got = np.array([nrm() for _ in range(n)])
+    u = np.array(_xorshift_py(seed, n), np.float64) / 2 ** 32      # no zero draws for this seed
+    assert np.all(u > 0)
+    uu, vv = u[0::2], u[1::2]
+    r = np.sqrt(-2.0 * np.log(uu))
+    want = np.empty(n)
+    want[0::2] = r * np.cos(2 * np.pi * vv)
+    want[1::2] = r * np.sin(2 * np.pi * vv)
+    assert np.allclose(got, want, rtol=1e-15, atol=1e-15)
+    assert abs(got.mean()) < 0.03 and abs(got.std() - 1) < 0.02
+
+
 def _attention_torch(q, kc, vc, H, KV, D, past):
     """Textbook causal attention in float64 (torch.softmax), kv head h // (H // KV) repeated per
     query head: an independent route to the same numbers."""
