@@ -257,6 +257,38 @@ class SeqStep:
         self.act.release()
 
 
+class PrefillStep:
+    """The prefill step as configured (config 3): all linears of the model, each on its own fp16
+    activations [M, K] ~ N(0,1), as ONE persistent prefill GEMM launch (ql_seq_* at M > 16: tasks
+    of 128 x 256 output tiles over all of K, planned longest first onto one workgroup per CU)."""
+
+    def __init__(self, ctx, model: Model, M: int, seed: int = 0x5EED):
+        self.ctx, self.model, self.M = ctx, model, M
+        lay = ql.ArenaLayout()
+        descs, xs, ys = [], [], []
+        self.order = []
+        for (layer, proj, K, N) in model.linears:
+            descs.append(model.descs[(layer, proj)])
+            xs.append(lay.take(M * K * 2))
+            ys.append(lay.take(M * N * 4))
+            self.order.append((layer, proj))
+        self.act = ctx.arena(lay.used)
+        for i, (layer, proj) in enumerate(self.order):
+            K = model.shapes[(layer, proj)][0]
+            x = synth.activations(M, K, seed=seed, key=(layer, synth.PROJ_INDEX[proj], M))
+            self.act.write(xs[i], x.astype(np.float16).view(np.uint16))
+        self.x_offs, self.y_offs = xs, ys
+        self.seq = ctx.seq(descs, model.arena, self.act, xs, ql.DTYPE_F16, M, ys)
+        self.info = self.seq.info
+        self.flops = sum(2 * M * model.shapes[lp][0] * model.shapes[lp][1] for lp in self.order)
+        self.graph = None
+
+    capture = SeqStep.capture
+    kernel_ms = SeqStep.kernel_ms
+    run = SeqStep.run
+    release = SeqStep.release
+
+
 def timed(step, steps: int, warmup: int) -> float:
     if step.graph is None:
         step.capture()
@@ -392,10 +424,12 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    help="all | step05 | headline | step7b | north | sweep | prefill | unpack | lmhead | attn | elem "
+                    help="all | step05 | headline | step7b | north | sweep | prefill | prefill_one | unpack | lmhead | "
+                         "attn | elem "
                          "(subsets for profiling: headline = the 0.5B step and its MALL-flushed "
                          "timing only; north = the 7B-shaped step at M=1 only)")
     ap.add_argument("--m7b", default="1,2,4,8,16", help="decode batch sizes for the 7B-shaped step")
+    ap.add_argument("--prefill-m", default="128,512", help="prefill rows for the one-launch prefill step")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-flush", action="store_true",
@@ -413,7 +447,7 @@ def main():
     only = args.only
 
     m05 = None
-    if only in ("all", "step05", "headline", "sweep", "prefill", "unpack"):
+    if only in ("all", "step05", "headline", "sweep", "prefill", "prefill_one", "unpack"):
         t0 = time.time()
         m05 = Model(ctx, "0.5b", seed=0x9EF0)
         log(f"0.5B weights: {m05.weight_bytes/1e6:.1f} MB uploaded in {time.time()-t0:.1f}s")
@@ -483,9 +517,20 @@ def main():
         extra["step05_m_sweep"] = sweep
         log(f"M sweep: {sweep}")
 
-    if only in ("all", "prefill"):
+    if only in ("all", "prefill", "prefill_one"):
         pre = {}
-        for layered in (False, True):
+        for M in [int(v) for v in args.prefill_m.split(",")]:
+            st = PrefillStep(ctx, m05, M)
+            ms = timed(st, max(5, args.steps // 5), 2)
+            kms = st.kernel_ms(max(10, args.steps // 2))
+            tf = st.flops / (kms * 1e-3) / 1e12
+            pre[f"{M}_one_launch"] = {
+                "us": round(ms * 1e3, 1), "kernel_us": round(kms * 1e3, 1), "tflops": round(tf, 2),
+                "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "launches": 1, "tasks": st.info.tiles,
+                "balance": round(st.info.balance, 4)}
+            log(f"prefill M={M} one launch: {pre[f'{M}_one_launch']}")
+            st.release()
+        for layered in ((False, True) if only != "prefill_one" else ()):
             for M in (128, 512):
                 st = Step(ctx, m05, M, x_dtype=ql.DTYPE_F16, layered=layered)
                 ms = timed(st, max(5, args.steps // 5), 2)
@@ -494,8 +539,10 @@ def main():
                     "us": round(ms * 1e3, 1), "tflops": round(tf, 2),
                     "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "launches": len(st.launches)}
                 st.release()
-        pre["note"] = ("M x 168 linears, fp16 x, fp32 y. As written (each linear on its own input): "
-                       "8 linears per launch. _layered: the model's dependency order, one launch per "
+        pre["note"] = ("M x 168 linears, fp16 x, fp32 y. _one_launch: the config as written (each linear "
+                       "on its own input) as one persistent prefill launch (tflops from the kernel "
+                       "time: graphs of 10 launches, HIP events). Plain M: the same as ql_linear_batch "
+                       "launches of 8 linears. _layered: the model's dependency order, one launch per "
                        "(q,k,v | o | gate,up | down) group (96 launches)")
         extra["prefill05"] = pre
         log(f"prefill: {pre}")

@@ -236,9 +236,14 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
  * buffers (the arenas are bound by address and must outlive it). ql_seq_run enqueues one launch
  * on the context stream; it allocates nothing and may be captured into a graph and replayed.
  * Runs of one sequence must not overlap (one stream). ql_seq_status waits for the stream and
- * reports whether a run was aborted (a bounded device-side wait ran out: QL_E_STATE). */
+ * reports whether a run was aborted (a bounded device-side wait ran out: QL_E_STATE).
+ * Prefill (M = 17..65536): a sequence of independent linears (no linear reads another's output)
+ * with fp16 x, N % 4 == 0 and groups a multiple of 128 runs as ONE persistent prefill GEMM
+ * launch (kernel QL_SEQ_PREFILL): tasks of 128 rows x 256 columns over all of K, planned longest
+ * first onto one workgroup per CU; y = f16(x) . f16(W)^T in fp32, as ql_linear's MFMA GEMM. */
 #define QL_SEQ_TILES 0
 #define QL_SEQ_STRIPS 1
+#define QL_SEQ_PREFILL 2
 typedef struct ql_seq ql_seq;
 typedef struct ql_seq_info {
     int32_t linears;
@@ -251,7 +256,8 @@ typedef struct ql_seq_info {
     uint64_t device_bytes;/* tables + exchange buffers ql_seq_create allocates */
     uint64_t total_units; /* block-groups (64 columns x one quantization group) of all linears */
     uint64_t busiest_units; /* block-groups of the most loaded workgroup: balance = busiest*grid/total */
-    int32_t kernel;       /* QL_SEQ_TILES: dependency-ordered tiles; QL_SEQ_STRIPS: column strips */
+    int32_t kernel;       /* QL_SEQ_TILES: dependency-ordered tiles; QL_SEQ_STRIPS: column strips;
+                             QL_SEQ_PREFILL: prefill GEMM tiles (units: 128-k chunks) */
     int32_t split;        /* strips: waves per 64-column block (1: strips of 8 blocks, 2: of 4) */
 } ql_seq_info;
 /* plan only (host, pure) for a given grid size: validation and the figures above */

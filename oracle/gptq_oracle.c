@@ -410,6 +410,7 @@ void orc_silu_mul(const float* gate, const float* up, size_t n, float* out)
 typedef struct {
     const uint8_t* qweight; const uint8_t* qzeros; const uint16_t* scales; const float* bias;
     const float* x; int M, K, N, group; const int32_t* cols; int ncols; float* y;
+    int w_f16;    /* weights rounded to fp16 as the uploaded arena (f32ToF16Bits), the GEMM's operand */
     int next; pthread_mutex_t lock; int rc;
 } cols_job;
 
@@ -443,6 +444,7 @@ static void* cols_worker(void* arg)
                     const float scale = orc_f16_bits_to_f32(J->scales[(size_t)g * N + o]);
                     const int q = (int)((word >> (4 * k)) & 15u);
                     wr[i] = (float)((double)(q - zero) * (double)scale);
+                    if (J->w_f16) wr[i] = orc_f16_bits_to_f32(orc_f32_to_f16_bits(wr[i]));
                 }
             }
         }
@@ -481,7 +483,7 @@ static void* cols_worker(void* arg)
 
 int orc_gptq_linear_cols(const uint8_t* qweight, const uint8_t* qzeros, const uint16_t* scales_f16,
                          const float* bias, const float* x, int M, int K, int N, int group_size,
-                         const int32_t* cols, int ncols, int threads, float* y)
+                         const int32_t* cols, int ncols, int threads, int w_f16, float* y)
 {
     if (M <= 0 || K <= 0 || N <= 0 || group_size <= 0 || group_size % 8 != 0 || ncols < 0)
         return ORC_E_DIMS;
@@ -489,7 +491,7 @@ int orc_gptq_linear_cols(const uint8_t* qweight, const uint8_t* qzeros, const ui
         if (cols[j] < 0 || cols[j] >= N) return ORC_E_DIMS;
     if (threads < 1) threads = 1;
     if (threads > 64) threads = 64;
-    cols_job J = {qweight, qzeros, scales_f16, bias, x, M, K, N, group_size, cols, ncols, y,
+    cols_job J = {qweight, qzeros, scales_f16, bias, x, M, K, N, group_size, cols, ncols, y, w_f16,
                   0, PTHREAD_MUTEX_INITIALIZER, ORC_OK};
     pthread_t tid[64];
     int started = 0;

@@ -80,10 +80,12 @@ int orc_gptq_linear(const uint8_t* qweight, const uint8_t* qzeros, const uint16_
                     float* y);
 
 /* orc_gptq_linear for the output columns cols[0..ncols) only (y [M, ncols]), on `threads` threads;
- * each output bit-identical to orc_gptq_linear's. For checking full-size launches quickly. */
+ * each output bit-identical to orc_gptq_linear's. For checking full-size launches quickly.
+ * w_f16: each weight rounded to fp16 first (f32ToF16Bits, the uploaded arena), so the result is
+ * gemmNTRef over the fp16 weights, the operand of the reference's M > 1 GEMM. */
 int orc_gptq_linear_cols(const uint8_t* qweight, const uint8_t* qzeros, const uint16_t* scales_f16,
                          const float* bias, const float* x, int M, int K, int N, int group_size,
-                         const int32_t* cols, int ncols, int threads, float* y);
+                         const int32_t* cols, int ncols, int threads, int w_f16, float* y);
 
 int orc_plan_gemv_split(int wg_n, int K);
 

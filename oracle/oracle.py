@@ -74,7 +74,7 @@ def lib():
                                       ctypes.c_int, P]
         L.orc_gptq_linear_cols.restype = ctypes.c_int
         L.orc_gptq_linear_cols.argtypes = [P, P, P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                           ctypes.c_int, P, ctypes.c_int, ctypes.c_int, P]
+                                           ctypes.c_int, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P]
         L.orc_plan_gemv_split.restype = ctypes.c_int
         L.orc_plan_gemv_split.argtypes = [ctypes.c_int, ctypes.c_int]
         L.orc_add_rmsnorm.restype = None
@@ -195,9 +195,11 @@ def default_threads() -> int:
 
 
 def gptq_linear_cols(qweight, qzeros, scales_f16, x, cols, bias=None, group: int = 128,
-                     threads: int | None = None) -> np.ndarray:
+                     threads: int | None = None, w_f16: bool = False) -> np.ndarray:
     """gptq_linear for the output columns `cols` only: y[M, len(cols)], every value
-    bit-identical to gptq_linear(...)[:, cols]; the columns are shared among threads."""
+    bit-identical to gptq_linear(...)[:, cols]; the columns are shared among threads.
+    w_f16: the weights rounded to fp16 first (the GEMM path's operand: gemm_nt over
+    dequantize_gptq_int4_f16)."""
     qw = np.ascontiguousarray(qweight, dtype=np.uint32)
     qz = None if qzeros is None else np.ascontiguousarray(qzeros, dtype=np.uint32)
     sc = np.ascontiguousarray(scales_f16).view(np.uint16)
@@ -208,7 +210,7 @@ def gptq_linear_cols(qweight, qzeros, scales_f16, x, cols, bias=None, group: int
     b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
     y = np.empty((M, c.size), dtype=np.float32)
     rc = lib().orc_gptq_linear_cols(_ptr(qw), _ptr(qz), _ptr(sc), _ptr(b), _ptr(x), M, K, N, group,
-                                    _ptr(c), c.size, threads or default_threads(), _ptr(y))
+                                    _ptr(c), c.size, threads or default_threads(), int(w_f16), _ptr(y))
     if rc != 0:
         raise ValueError("oracle gptq_linear_cols: bad arguments")
     return y

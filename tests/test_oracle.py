@@ -250,6 +250,11 @@ def test_gptq_linear_cols_bit_identical(orc, K, N, M, threads):
         assert np.array_equal(part.view(np.uint32), full[:, cols].view(np.uint32))
     with pytest.raises(ValueError):
         orc.gptq_linear_cols(qweight, qzeros, sf16, x, [N], None, group)
+    # fp16 weights: gemmNTRef over the uploaded fp16 arena, bit for bit
+    if K % 8 == 0:
+        W16 = orc.f16_bits_to_f32(orc.dequantize_gptq_int4_f16(qweight, qzeros, sf16, K, N, group))
+        part = orc.gptq_linear_cols(qweight, qzeros, sf16, x, cols, bias, group, threads=threads, w_f16=True)
+        assert np.array_equal(part.view(np.uint32), orc.gemm_nt(x, W16, bias)[:, cols].view(np.uint32))
 
 
 # ---------------------------------------------------------------- planGemvSplit (a7)

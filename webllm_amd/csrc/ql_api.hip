@@ -48,6 +48,8 @@ struct ql_seq {
     ql_seq_info info;
     bool strips;            // independent linears at M >= 2: the column-strip kernel (sargs)
     ql::StripArgs sargs;
+    bool prefill;           // independent linears at M > 16: the prefill GEMM (pargs)
+    ql::PrefillArgs pargs;
 };
 
 // Split-K partial sums of ql_linear_noalloc. One copy per GPU, loaded with the code object, so
@@ -258,16 +260,21 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
     if (!descs || !x_offs || !y_offs) return fail(QL_E_INVALID, "null sequence arrays");
     if (n <= 0 || n > ql::kSeqMaxLinears)
         return fail(QL_E_INVALID, "a sequence holds 1..%d linears, got %d", ql::kSeqMaxLinears, n);
-    if (M < 1 || M > ql::kGemvMaxM) return fail(QL_E_INVALID, "sequences run decode rows M = 1..%d", ql::kGemvMaxM);
+    if (M < 1 || M > ql::kSeqMaxRows) return fail(QL_E_INVALID, "sequences run M = 1..%d rows", ql::kSeqMaxRows);
     if (x_dtype != QL_DTYPE_F32 && x_dtype != QL_DTYPE_F16)
         return fail(QL_E_INVALID, "x_dtype must be QL_DTYPE_F32 or QL_DTYPE_F16");
+    const bool prefill = M > ql::kGemvMaxM;
     const uint64_t es = x_dtype == QL_DTYPE_F32 ? 4 : 2;
     std::vector<std::pair<uint64_t, int>> ys(n);
     for (int i = 0; i < n; i++) {
         const ql_gptq_desc* d = &descs[i];
         int rc = validate_desc(d, w_bytes);
         if (rc) return rc;
-        if (!ql::gemv_fast_ok(M, d->N, d->K, d->group) || d->group != descs[0].group)
+        if (prefill && !ql::prefill_ok(M, d->N, d->K, d->group, x_dtype))
+            return fail(QL_E_INVALID,
+                        "linear %d: a prefill sequence (M > %d) needs fp16 x, N %% 4 == 0 and groups a "
+                        "multiple of 128 dividing K", i, ql::kGemvMaxM);
+        if (!prefill && (!ql::gemv_fast_ok(M, d->N, d->K, d->group) || d->group != descs[0].group))
             return fail(QL_E_INVALID,
                         "linear %d: a sequence needs N %% 4 == 0, K %% group == 0 and one group size "
                         "(64, 128 or 256) for all linears", i);
@@ -303,6 +310,10 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
             if (descs[j].N != d->K)
                 return fail(QL_E_INVALID, "linear %d reads linear %d's output, but K=%d != N=%d", i, j, d->K,
                             descs[j].N);
+            if (prefill)
+                return fail(QL_E_INVALID, "linear %d reads linear %d's output: prefill sequences (M > %d) "
+                            "take independent linears (run each dependent pass as its own sequence)", i, j,
+                            ql::kGemvMaxM);
             s.src = j;
             continue;
         }
@@ -476,6 +487,103 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     q->sargs.group = descs[0].group;
     q->sargs.split = sp.split;
     fill_strip_info(sp, n, lay.total, &q->info);
+    *out = q;
+    return QL_OK;
+}
+
+struct PrefillLayout {
+    uint64_t lin, tasks, task_begin, total;
+};
+
+PrefillLayout prefill_layout(int n, const ql::PrefillPlan& p)
+{
+    PrefillLayout L;
+    uint64_t off = 0;
+    auto take = [&](uint64_t bytes) {
+        const uint64_t o = off;
+        off = align256(off + bytes);
+        return o;
+    };
+    L.lin = take(sizeof(ql::PrefillLinear) * n);
+    L.tasks = take(sizeof(ql::PrefillTask) * std::max<size_t>(1, p.tasks.size()));
+    L.task_begin = take(sizeof(int32_t) * (p.grid + 1));
+    L.total = off;
+    return L;
+}
+
+std::vector<ql::PrefillSpec> prefill_specs(const std::vector<ql::SeqSpec>& specs)
+{
+    std::vector<ql::PrefillSpec> v(specs.size());
+    for (size_t i = 0; i < specs.size(); i++) v[i] = ql::PrefillSpec{specs[i].N, specs[i].K};
+    return v;
+}
+
+void fill_prefill_info(const ql::PrefillPlan& p, int n, int M, const std::vector<ql::SeqSpec>& specs,
+                       uint64_t bytes, ql_seq_info* info)
+{
+    memset(info, 0, sizeof *info);
+    info->linears = n;
+    info->passes = 1;
+    info->tiles = (int32_t)p.tasks.size();
+    info->grid = p.grid;
+    info->max_split = 1;
+    info->device_bytes = bytes;
+    info->total_units = p.total_units;
+    info->busiest_units = p.busiest_units;
+    info->kernel = QL_SEQ_PREFILL;
+    info->split = 1;
+    (void)M;
+    (void)specs;
+}
+
+// Independent linears at M > 16: one prefill GEMM launch over a planned task table.
+int prefill_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights, ql_arena* act,
+                   const uint64_t* x_offs, int32_t M, const uint64_t* y_offs,
+                   const std::vector<ql::SeqSpec>& specs, ql_seq** out)
+{
+    ql::PrefillPlan pp;
+    ql::plan_prefill(prefill_specs(specs), M, ctx->cu_count, &pp);
+    const PrefillLayout lay = prefill_layout(n, pp);
+    char* dev = nullptr;
+    QL_HIP(hipMalloc(&dev, lay.total));
+    std::vector<ql::PrefillLinear> lin(n);
+    for (int i = 0; i < n; i++) {
+        const ql_gptq_desc* d = &descs[i];
+        const ql::GemvLinear g = make_linear(d, weights);
+        ql::PrefillLinear& L = lin[i];
+        L = ql::PrefillLinear{};
+        L.qweight = g.qweight;
+        L.qzeros = g.qzeros;
+        L.scales = g.scales;
+        L.bias = g.bias;
+        L.x = reinterpret_cast<const uint16_t*>(act->base + x_offs[i]);
+        L.y = reinterpret_cast<float*>(act->base + y_offs[i]);
+        L.N = d->N;
+        L.K = d->K;
+        L.group = d->group;
+    }
+    hipError_t e = hipMemcpy(dev + lay.lin, lin.data(), sizeof(ql::PrefillLinear) * n, hipMemcpyHostToDevice);
+    if (e == hipSuccess && !pp.tasks.empty())
+        e = hipMemcpy(dev + lay.tasks, pp.tasks.data(), sizeof(ql::PrefillTask) * pp.tasks.size(),
+                      hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(dev + lay.task_begin, pp.task_begin.data(), sizeof(int32_t) * pp.task_begin.size(),
+                      hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(e, "ql_seq_create upload");
+    }
+    ql_seq* q = new ql_seq();
+    q->device = ctx->device;
+    q->dev = dev;
+    q->prefill = true;
+    q->pargs = ql::PrefillArgs{};
+    q->pargs.lin = reinterpret_cast<const ql::PrefillLinear*>(dev + lay.lin);
+    q->pargs.tasks = reinterpret_cast<const ql::PrefillTask*>(dev + lay.tasks);
+    q->pargs.task_begin = reinterpret_cast<const int32_t*>(dev + lay.task_begin);
+    q->pargs.M = M;
+    q->pargs.G = pp.grid;
+    fill_prefill_info(pp, n, M, specs, lay.total, &q->info);
     *out = q;
     return QL_OK;
 }
@@ -790,6 +898,53 @@ int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, ui
 
 }  // namespace
 
+namespace {
+
+// A batch of linears (x offsets, dtype and alignment already checked) as one prefill GEMM launch,
+// when every linear qualifies, all share K (the batch form deals tiles round robin, which balances
+// only equal tiles) and the tiles fill at least half the device (fewer tiles run faster split
+// along K by the chunked GEMM). Returns false when it does not apply.
+bool prefill_batch(ql_ctx* ctx, int count, const ql_gptq_desc* descs, const ql_arena* weights, ql_arena* act,
+                   const uint64_t* x_offs, int x_dtype, int M, const uint64_t* y_offs, int* rc)
+{
+    int tiles = 0;
+    for (int i = 0; i < count; i++) {
+        if (!ql::prefill_ok(M, descs[i].N, descs[i].K, descs[i].group, x_dtype) ||
+            !gemv_aligned(&descs[i], x_offs[i], y_offs[i]) || descs[i].K != descs[0].K)
+            return false;
+        tiles += ql::prefill_tiles(M, descs[i].N);
+    }
+    if (tiles < ql::kPrefillMinTiles) return false;
+    ql::PrefillArgs a{};
+    a.count = count;
+    a.M = M;
+    int begin = 0;
+    for (int i = 0; i < count; i++) {
+        const ql::GemvLinear g = make_linear(&descs[i], weights);
+        ql::PrefillLinear& L = a.L[i];
+        L.qweight = g.qweight;
+        L.qzeros = g.qzeros;
+        L.scales = g.scales;
+        L.bias = g.bias;
+        L.x = reinterpret_cast<const uint16_t*>(act->base + x_offs[i]);
+        L.y = reinterpret_cast<float*>(act->base + y_offs[i]);
+        L.N = descs[i].N;
+        L.K = descs[i].K;
+        L.group = descs[i].group;
+        L.tiles_m = (M + ql::kPrefillRows - 1) / ql::kPrefillRows;
+        L.tile_begin = begin;
+        begin += ql::prefill_tiles(M, descs[i].N);
+    }
+    a.total_tiles = begin;
+    a.G = std::min(begin, ctx->cu_count);
+    if ((*rc = set_device(ctx))) return true;
+    const hipError_t e = ql::launch_prefill(a, false, ctx->stream);
+    *rc = e == hipSuccess ? QL_OK : hip_fail(e, "launch_prefill");
+    return true;
+}
+
+}  // namespace
+
 int ql_plan_linear(int32_t M, int32_t N, int32_t K, int32_t group, ql_plan* out)
 {
     if (!out) return fail(QL_E_INVALID, "null plan pointer");
@@ -832,6 +987,7 @@ int linear_impl(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_
         return QL_OK;
     }
     if (p.kind == QL_KIND_GEMM_MFMA && gemv_aligned(d, x_off, y_off)) {
+        if (prefill_batch(ctx, 1, d, weights, act, &x_off, x_dtype, M, &y_off, &rc)) return rc;
         ql::GemmBatch b{};
         int rc2 = gemm_entry(d, weights, act, x_off, M, y_off, partial, ctx->counters, 0, 0, &b.L[0]);
         if (rc2) return rc2;
@@ -1093,6 +1249,7 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
             bm = b;
         }
     }
+    if (gemm && prefill_batch(ctx, count, descs, weights, act, x_offs, x_dtype, M, y_offs, &rc)) return rc;
     if (gemm) {
         // one launch; each linear's partial sums at its own offset, as ql_plan_batch sized them
         if ((rc = set_device(ctx))) return rc;
@@ -1174,6 +1331,12 @@ int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
     std::vector<ql::SeqSpec> specs;
     int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, UINT64_MAX, UINT64_MAX, &specs);
     if (rc) return rc;
+    if (M > ql::kGemvMaxM) {
+        ql::PrefillPlan pp;
+        ql::plan_prefill(prefill_specs(specs), M, grid, &pp);
+        fill_prefill_info(pp, n, M, specs, prefill_layout(n, pp).total, info);
+        return QL_OK;
+    }
     if (ql::strip_eligible(specs, M)) {
         ql::StripPlan sp;
         ql::plan_strips(specs, M, grid, &sp);
@@ -1201,6 +1364,7 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
     int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, weights->size, act->size, &specs);
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
+    if (M > ql::kGemvMaxM) return prefill_create(ctx, n, descs, weights, act, x_offs, M, y_offs, specs, out);
     if (ql::strip_eligible(specs, M)) return strip_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs,
                                                           specs, out);
     int per_cu = 0;
@@ -1287,7 +1451,8 @@ int ql_seq_run(ql_ctx* ctx, ql_seq* seq)
     if (seq->device != ctx->device) return fail(QL_E_INVALID, "sequence belongs to another device");
     int rc = set_device(ctx);
     if (rc) return rc;
-    if (seq->strips) QL_HIP(ql::launch_strips(seq->sargs, seq->lds, ctx->stream));
+    if (seq->prefill) QL_HIP(ql::launch_prefill(seq->pargs, true, ctx->stream));
+    else if (seq->strips) QL_HIP(ql::launch_strips(seq->sargs, seq->lds, ctx->stream));
     else QL_HIP(ql::launch_seq(seq->args, seq->lds, ctx->stream));
     return QL_OK;
 }
@@ -1299,7 +1464,7 @@ int ql_seq_status(ql_ctx* ctx, ql_seq* seq)
     int rc = set_device(ctx);
     if (rc) return rc;
     QL_HIP(hipStreamSynchronize(ctx->stream));
-    if (seq->strips) return QL_OK;          // no device-side waits: nothing can abort
+    if (seq->strips || seq->prefill) return QL_OK;   // no device-side waits: nothing can abort
     uint32_t words[2] = {0, 0};
     QL_HIP(hipMemcpy(words, seq->args.abort, sizeof words, hipMemcpyDeviceToHost));
     if (words[0] == 0 && words[1] == 0) return QL_OK;

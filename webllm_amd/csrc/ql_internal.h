@@ -85,6 +85,52 @@ GemmShape gemm_shape(int M, int N, int K, int group, int cu_count);
 uint64_t gemm_partial_bytes(int M, int N, int split);
 hipError_t launch_gemm_batch(const GemmBatch& b, hipStream_t stream);
 
+// Prefill GEMM over many linears in one persistent launch (M > 16, fp16 x, groups a multiple of
+// 128): tasks of one 128 x 256 output tile over all of K, from a host plan (table) or from the
+// tile numbering of a batch of up to kMaxBatch linears.
+constexpr int kPrefillRows = 128;
+constexpr int kPrefillCols = 256;
+#ifndef QL_PREFILL_MIN_TILES
+#define QL_PREFILL_MIN_TILES 128
+#endif
+constexpr int kPrefillMinTiles = QL_PREFILL_MIN_TILES;   // fewest tiles a ql_linear(_batch) launch takes it for
+struct PrefillLinear {
+    const uint32_t* qweight;   // [K/8, N]
+    const uint32_t* qzeros;    // [K/group, ceil(N/8)] or nullptr (zero 8)
+    const uint16_t* scales;    // [K/group, N] fp16 bits
+    const float* bias;         // [N] or nullptr
+    const uint16_t* x;         // [M, K] fp16
+    float* y;                  // [M, N]
+    int32_t N, K, group;
+    int32_t tiles_m;           // batch mode: row tiles, and the linear's first tile number
+    int32_t tile_begin;
+    int32_t pad;
+};
+struct PrefillTask {
+    int32_t linear, mt, nt, pad;
+};
+struct PrefillArgs {
+    const PrefillLinear* lin;  // table mode: linears, tasks, and each workgroup's first task [G + 1]
+    const PrefillTask* tasks;
+    const int32_t* task_begin;
+    PrefillLinear L[kMaxBatch];// batch mode: the linears; workgroup w takes tiles w, w + G, ...
+    int32_t count, total_tiles;
+    int32_t M, G;
+};
+struct PrefillSpec {
+    int N, K;
+};
+struct PrefillPlan {
+    int grid = 0;
+    uint64_t total_units = 0, busiest_units = 0;   // 128-k chunks: all, most on one workgroup
+    std::vector<PrefillTask> tasks;
+    std::vector<int32_t> task_begin;
+};
+bool prefill_ok(int M, int N, int K, int group, int x_dtype);
+int prefill_tiles(int M, int N);
+void plan_prefill(const std::vector<PrefillSpec>& lin, int M, int grid, PrefillPlan* out);
+hipError_t launch_prefill(const PrefillArgs& a, bool table, hipStream_t stream);
+
 // load-time unpack to fp16 [N, K]
 struct UnpackArgs {
     const uint32_t* qweight;
@@ -166,6 +212,7 @@ hipError_t launch_kv_store(const float* src, float* dst, int rows, int row_len, 
 // output of an earlier linear; the kernel orders them on the device.
 
 constexpr int kSeqMaxLinears = 4096;
+constexpr int kSeqMaxRows = 65536;     // rows of a sequence (above kGemvMaxM: prefill GEMM)
 constexpr int kSeqTileCols = 64;       // output columns per sequence tile (one wave's width)
 constexpr int kSeqMaxSplit = 4096;     // parts (K pieces) of one 64-column block, at most
 constexpr int kSeqTickets = 32;        // per-run ticket sub-counters (epoch), 64 B apart
