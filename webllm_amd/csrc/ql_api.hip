@@ -272,8 +272,9 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
         if (rc) return rc;
         if (prefill && !ql::prefill_ok(M, d->N, d->K, d->group, x_dtype))
             return fail(QL_E_INVALID,
-                        "linear %d: a prefill sequence (M > %d) needs fp16 x, N %% 4 == 0 and groups a "
-                        "multiple of 128 dividing K", i, ql::kGemvMaxM);
+                        "linear %d: a prefill sequence (M > %d) needs fp16 x, N %% 4 == 0, groups a "
+                        "multiple of 128 dividing K, and M*N*4, M*K*2 and K*N/2 below 2^31 bytes", i,
+                        ql::kGemvMaxM);
         if (!prefill && (!ql::gemv_fast_ok(M, d->N, d->K, d->group) || d->group != descs[0].group))
             return fail(QL_E_INVALID,
                         "linear %d: a sequence needs N %% 4 == 0, K %% group == 0 and one group size "

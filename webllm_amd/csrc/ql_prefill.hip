@@ -295,8 +295,11 @@ void prefill_kernel(const PrefillArgs a)
 
 bool prefill_ok(int M, int N, int K, int group, int x_dtype)
 {
+    // every buffer offset of the launch (activations, outputs, packed weights) stays below 2^31
+    const int64_t lim = INT64_C(1) << 31;
     return M > kGemvMaxM && x_dtype == 1 && N > 0 && N % 4 == 0 && group > 0 && group % 128 == 0 &&
-           K > 0 && K % group == 0;
+           K > 0 && K % group == 0 && (int64_t)M * N * 4 < lim && (int64_t)M * K * 2 < lim &&
+           (int64_t)K * N / 2 < lim;
 }
 
 int prefill_tiles(int M, int N) { return ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN); }
