@@ -1,18 +1,22 @@
 #!/usr/bin/env python3
 """Benchmark of the GPTQ int4 quantized-linear hot path on one MI355X.
 
-Headline (BASELINE.json metric): microseconds per Qwen2.5-0.5B-shaped decode step — 168 GPTQ
-int4 linears (24 layers x q,k,v,o,gate,up,down; group 128), M = 1, fp32 activations, weights
-resident in HBM. The step is issued the way the model's data dependencies allow: per layer
-{q,k,v} on one input, {o}, {gate,up} on one input, {down} — 96 launches, captured once into a
-HIP graph; one step = one graph replay. Inputs are synthetic (random nibbles, zero 8, fp16 scales
-|N(0,1)|*0.01, x ~ N(0,1)); no checkpoint is available offline.
+Headline (BASELINE.json metric): microseconds per Qwen2.5-0.5B-shaped decode step - the 168 GPTQ
+int4 linears (24 layers x q,k,v,o,gate,up,down; group 128) at M = 1, each on its own fp32
+activations ~N(0,1) as the benchmark config states them, weights resident in HBM, issued as ONE
+persistent launch (ql_seq_create over a strip plan), captured into a HIP graph; one step = one
+graph replay. Inputs are synthetic (random nibbles, zero 8, fp16 scales |N(0,1)|*0.01,
+x ~ N(0,1)); no checkpoint is available offline.
 
-Also measured (reported under "extra"): the same step with the 256 MB MALL flushed before each
-step; the 7B-shaped step (140 linears, 3.34 GB, HBM-bound) at M = 1, 4, 16; the M sweep
-{1,2,4,8,16}; prefill GEMM at M = 128, 512 (TFLOP/s); the load-time unpack of all 168 tensors.
-The CPU baseline is the reference CPU path (dequantizeGptqInt4 + gemmNTRef) restated for Node,
-run single-threaded on this host on layer 0 of the same inputs and scaled to a whole step.
+Also measured (reported under "extra"): the same step after a read-only pass over 1 GiB has
+evicted the 256 MB MALL; the linears chained through their outputs (one launch, device-ordered
+passes) and as per-linear launches; the 7B-shaped step (140 linears, 3.34 GB, HBM-bound) at
+M = 1, 2, 4, 8, 16; the M sweep {1,2,4,8,16}; prefill GEMM at M = 128, 512 (TFLOP/s); the
+load-time unpack of all 168 tensors; the lm_head GEMV, elementwise ops and decode attention.
+The CPU baseline is the reference CPU path (dequantizeGptqInt4 + gemmNTRef) restated for Node and
+run single-threaded on this host over all 168 linears of the timed step on the same inputs, every
+output checked against the GPU's; --only cpu runs the rest of the CPU plan (config 1 with the GPU
+beside it, variant (ii), config 4 as one 7B layer x28, config 5's fp16 unpack).
 """
 from __future__ import annotations
 
@@ -62,6 +66,7 @@ class Model:
         """keep_tensors: keep every linear's host tensors (self.tensors[(layer, proj)]) for a
         full-size check against the oracle; otherwise only layer 0's are kept."""
         self.shape = shape
+        self.seed = seed
         self.linears = synth.model_linears(shape)
         self.layers = synth.QWEN05_LAYERS if shape == "0.5b" else synth.QWEN7_LAYERS
         lay = ql.ArenaLayout()
@@ -298,13 +303,20 @@ def timed(step, steps: int, warmup: int) -> float:
 
 
 def flushed_step_ms(ctx, step: Step, reps: int = 5) -> float:
-    """Step time with the MALL (256 MB) evicted first: a 1 GiB device copy precedes each step."""
-    flush = ctx.arena(1 << 30)
+    """Step time with the MALL (256 MB) evicted first by a read-only pass: an fp16 GEMV over a
+    1 GiB matrix (1 GiB read, 512 KB written) precedes each step, so the step starts with none of
+    its weights cached and no dirty lines left to write back while it runs."""
+    N, K = 131072, 4096
+    flush = ctx.arena(N * K * 2)
+    fx = ctx.arena(K * 4 + N * 4 + 256)
+    y_off = (K * 4 + 255) // 256 * 256
+    fx.write(0, np.zeros(K, np.float32))
     times = []
     for _ in range(reps):
-        ctx.copy(flush, 0, flush, 1 << 29, 1 << 29)
+        ctx.gemv_f16w(flush, 0, None, fx, 0, 1, N, K, y_off)
         ctx.sync()
         times.append(step.run(1))
+    fx.release()
     flush.release()
     return float(np.median(times))
 
@@ -340,75 +352,156 @@ def unpack_all(ctx, model: Model, steps: int):
     return ms, read + write
 
 
-def cpu_baseline(model: Model, step: Step, min_seconds: float):
-    """Reference CPU path (Node restatement, oracle/js) on layer 0 of the same inputs."""
+def node_run(items, min_seconds: float, plan=None):
+    """The reference CPU path (oracle/js/gptq_ref.js, Node, one thread) over the linears in
+    items [(tensors, x [M, K] f32)]: returns its timing record and the outputs y [M, N]."""
     node = shutil.which("node")
-    t0_layer = [l for l in step.launches if l[0] == 0]
+    if not node:
+        raise RuntimeError("node not found: the CPU baseline runs the reference path under Node")
     with tempfile.TemporaryDirectory() as d:
-        meta = {"linears": []}
-        gpu_y = []
-        atols_x = []
-        for (layer, gi, projs, descs, x_off, y_offs, s_off) in t0_layer:
-            x = step.act.read(x_off, (step.M, descs[0].K), np.float32)
-            for p, desc, yo in zip(projs, descs, y_offs):
-                t = model.tensors_for_cpu[p]
-                i = len(meta["linears"])
-                t.qweight.tofile(os.path.join(d, f"qw_{i}"))
-                t.qzeros.tofile(os.path.join(d, f"qz_{i}"))
-                t.scales.tofile(os.path.join(d, f"sc_{i}"))
-                x.tofile(os.path.join(d, f"x_{i}"))
-                meta["linears"].append({"K": t.K, "N": t.N, "group": GROUP, "M": step.M,
-                                        "qweight": f"qw_{i}", "qzeros": f"qz_{i}",
-                                        "scales": f"sc_{i}", "x": f"x_{i}"})
-                gpu_y.append(step.act.read(yo, (step.M, desc.N), np.float32))
-                atols_x.append(1e-5 * max(1.0, float(np.sqrt(np.mean(x.astype(np.float64) ** 2)))))
+        meta = {"linears": [], "plan": plan or {}}
+        for i, (t, x) in enumerate(items):
+            t.qweight.tofile(os.path.join(d, f"qw_{i}"))
+            t.qzeros.tofile(os.path.join(d, f"qz_{i}"))
+            t.scales.tofile(os.path.join(d, f"sc_{i}"))
+            np.ascontiguousarray(x, dtype=np.float32).tofile(os.path.join(d, f"x_{i}"))
+            meta["linears"].append({"K": t.K, "N": t.N, "group": GROUP, "M": x.shape[0],
+                                    "qweight": f"qw_{i}", "qzeros": f"qz_{i}", "scales": f"sc_{i}",
+                                    "x": f"x_{i}"})
         json.dump(meta, open(os.path.join(d, "meta.json"), "w"))
-        macs = sum(l["M"] * l["K"] * l["N"] for l in meta["linears"])
-        if node:
-            r = subprocess.run([node, os.path.join(ROOT, "oracle", "js", "gptq_ref.js"), d,
-                                str(min_seconds)], capture_output=True, text=True, timeout=600)
-            if r.returncode != 0:
-                raise RuntimeError(f"node baseline failed: {r.stderr[-2000:]}")
-            res = json.loads(r.stdout.strip().splitlines()[-1])
-            cpu_y = [np.fromfile(os.path.join(d, f"y_{i}.f32"), dtype=np.float32)
-                     for i in range(len(gpu_y))]
-            kind_note = f"Node {res['node']} restatement of quant.ts dequantizeGptqInt4 + qwen-ref.ts gemmNTRef"
-        else:   # no Node on this host: the C oracle restatement of the same CPU path
-            from oracle import oracle as orc
-            t1 = time.perf_counter()
-            reps = 0
-            while True:
-                cpu_y = []
-                for l in meta["linears"]:
-                    t = model.tensors_for_cpu[[p for p in model.tensors_for_cpu
-                                               if model.tensors_for_cpu[p].K == l["K"] and
-                                               model.tensors_for_cpu[p].N == l["N"]][0]]
-                    x = np.fromfile(os.path.join(d, l["x"]), dtype=np.float32).reshape(l["M"], l["K"])
-                    cpu_y.append(orc.gptq_linear(t.qweight, t.qzeros, t.scales, x).reshape(-1))
-                reps += 1
-                if time.perf_counter() - t1 > min_seconds:
-                    break
-            res = {"matvec_ms": (time.perf_counter() - t1) * 1e3 / reps, "dequant_ms": None,
-                   "reps": reps, "cpu": "", "cpus": os.cpu_count()}
-            kind_note = "C oracle (node not found)"
-    # |d| <= atol + 1e-4|ref| with atol = 1e-5 * rms(x): the reference's 1e-5 for N(0,1) inputs,
-    # scaled for the larger inputs of chained linears
-    atols = atols_x
-    rel = max(float(np.max(np.abs(g.reshape(-1) - c) / (a / 1e-4 + np.abs(c))))
-              for g, c, a in zip(gpu_y, cpu_y, atols))
-    ok = all(np.all(np.abs(g.reshape(-1) - c) <= a + 1e-4 * np.abs(c))
-             for g, c, a in zip(gpu_y, cpu_y, atols))
-    per_step_us = res["matvec_ms"] * model.layers * 1e3
+        r = subprocess.run([node, os.path.join(ROOT, "oracle", "js", "gptq_ref.js"), d, str(min_seconds)],
+                           capture_output=True, text=True, timeout=1200)
+        if r.returncode != 0:
+            raise RuntimeError(f"node baseline failed: {r.stderr[-2000:]}")
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+        ys = [np.fromfile(os.path.join(d, f"y_{i}.f32"), dtype=np.float32).reshape(x.shape[0], t.N)
+              for i, (t, x) in enumerate(items)]
+    return res, ys
+
+
+def gpu_cpu_check(gpu_y, cpu_y, xs):
+    """|d| <= atol + 1e-4 |ref| with atol = 1e-5 * rms(x) (the reference's 1e-5 for N(0,1)
+    inputs); returns (ok, the largest |d| / (atol / 1e-4 + |ref|))."""
+    ok, worst = True, 0.0
+    for g, c, x in zip(gpu_y, cpu_y, xs):
+        a = 1e-5 * max(1.0, float(np.sqrt(np.mean(x.astype(np.float64) ** 2))))
+        d = np.abs(g - c)
+        ok = ok and bool(np.all(d <= a + 1e-4 * np.abs(c)))
+        worst = max(worst, float(np.max(d / (a / 1e-4 + np.abs(c)))))
+    return ok, worst
+
+
+def step_items(model: Model, step):
+    """(tensors, x) of every linear of a step, the tensors regenerated from the model's seed."""
+    items = []
+    for i, (layer, proj) in enumerate(step.order):
+        K, N = model.shapes[(layer, proj)]
+        t = synth.gptq_linear(K, N, GROUP, seed=model.seed, key=(layer, synth.PROJ_INDEX[proj]))
+        items.append((t, step.act.read(step.x_offs[i], (step.M, K), np.float32)))
+    return items
+
+
+def cpu_baseline(model: Model, step, min_seconds: float):
+    """The reference CPU path on config 2 in full: all 168 linears of the timed step on the same
+    inputs (weights dequantized once, as the reference loads them; the matvecs timed), every
+    output checked against the GPU's."""
+    items = step_items(model, step)
+    res, cpu_y = node_run(items, min_seconds)
+    gpu_y = [step.act.read(step.y_offs[i], (step.M, t.N), np.float32) for i, (t, _) in enumerate(items)]
+    ok, rel = gpu_cpu_check(gpu_y, cpu_y, [x for _, x in items])
+    macs = res["macs"]
     return {
-        "value": round(per_step_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
-        "sample": (f"layer 0 (7 linears, {macs/1e6:.1f} M MACs) matvec x {res['reps']} reps, "
-                   f"scaled x{model.layers} layers; dequant at load {res['dequant_ms']:.0f} ms "
-                   f"for layer 0 ({kind_note})" if res.get("dequant_ms") is not None else
-                   f"layer 0 matvec x {res['reps']} reps, scaled x{model.layers} ({kind_note})"),
+        "value": round(res["matvec_median_ms"] * 1e3, 1), "unit": "us/step", "cores": 1, "kind": "port",
+        "sample": (f"config 2 in full: all {len(items)} linears ({macs/1e6:.1f} M MACs) of the timed step "
+                   f"on its inputs, variant (i) (weights dequantized once, {res['dequant_ms']:.0f} ms, as "
+                   f"the reference loads them; matvecs timed): median of {res['reps']} steps; Node "
+                   f"{res['node']} restatement of quant.ts dequantizeGptqInt4 + qwen-ref.ts gemmNTRef"),
+        "mean_us": round(res["matvec_ms"] * 1e3, 1),
         "host_cpu": res.get("cpu", ""), "host_threads": res.get("cpus"),
-        "dequant_ms_layer0": None if res.get("dequant_ms") is None else round(res["dequant_ms"], 1),
-        "gpu_vs_cpu_ok": bool(ok), "gpu_vs_cpu_max_rel_atol": rel,
+        "dequant_ms": round(res["dequant_ms"], 1),
+        "gpu_vs_cpu_ok": bool(ok), "gpu_vs_cpu_max_rel_atol": rel, "linears_checked": len(items),
     }
+
+
+def cpu_plan(ctx, min_seconds: float):
+    """The CPU baseline plan beyond the headline: config 1 in full with the GPU beside it,
+    config 2 variant (ii), config 4 (one 7B layer, extrapolated x28) and config 5 (the fp16
+    unpack of all 168 tensors)."""
+    out = {}
+    # config 1: the 0.5B gate_proj shape alone, M = 1
+    K, N = 896, 4864
+    t = synth.gptq_linear(K, N, GROUP, seed=0xC0F1, key=(0,))
+    x = synth.activations(1, K, seed=0xC0F2, key=(0,))
+    res, cpu_y = node_run([(t, x)], min(min_seconds, 3.0), {"fused_reps": 9})
+    wl, al = ql.ArenaLayout(), ql.ArenaLayout()
+    offs = (wl.take(t.qweight.nbytes), wl.take(t.qzeros.nbytes), wl.take(t.scales.nbytes))
+    xo, yo = al.take(K * 4), al.take(N * 4)
+    so = al.take(max(ql.plan_linear(1, N, K, GROUP).scratch_bytes, 16))
+    w = ctx.arena(wl.used)
+    act = ctx.arena(al.used)
+    w.write(offs[0], t.qweight)
+    w.write(offs[1], t.qzeros)
+    w.write(offs[2], t.scales)
+    act.write(xo, x)
+    desc = ql.make_desc(offs[0], offs[1], offs[2], K, N, GROUP)
+    ctx.linear(desc, w, act, xo, ql.DTYPE_F32, 1, yo, so)
+    ctx.sync()
+    ctx.graph_begin()
+    ctx.linear(desc, w, act, xo, ql.DTYPE_F32, 1, yo, so)
+    g = ctx.graph_end()
+    for _ in range(5):
+        g.launch()
+    ctx.timer_start()
+    for _ in range(200):
+        g.launch()
+    gpu_us = ctx.timer_stop() / 200 * 1e3
+    gy = act.read(yo, (1, N), np.float32)
+    g.destroy()
+    w.release()
+    act.release()
+    ok, rel = gpu_cpu_check([gy], cpu_y, [x])
+    nbytes = linear_bytes(K, N, 1)
+    out["config1"] = {"gpu_us": round(gpu_us, 2), "gpu_gbs": round(nbytes / (gpu_us * 1e-6) / 1e9, 1),
+                      "cpu_matvec_us": round(res["matvec_median_ms"] * 1e3, 1),
+                      "cpu_dequant_ms": round(res["dequant_ms"], 2),
+                      "cpu_fused_us": round(res["fused_ms"] * 1e3, 1), "gpu_vs_cpu_ok": ok,
+                      "gpu_vs_cpu_max_rel_atol": rel,
+                      "note": "gate 896->4864, M=1, one ql_linear launch (graph-replayed, 200 reps); CPU "
+                              "variant (i) matvec median and variant (ii) dequant+matvec median of 9"}
+    # config 2 variant (ii) and config 5: the 168 linears of the 0.5B step
+    m05 = Model(ctx, "0.5b", seed=0x9EF0)
+    items = []
+    for (layer, proj, K, N) in m05.linears:
+        items.append((synth.gptq_linear(K, N, GROUP, seed=m05.seed, key=(layer, synth.PROJ_INDEX[proj])),
+                      synth.activations(1, K, seed=0x5EED, key=(layer, synth.PROJ_INDEX[proj], 1))))
+    m05.arena.release()
+    res, _ = node_run(items, 1.0, {"fused_reps": 3, "f16_reps": 3})
+    out["config2_variant_ii"] = {"us": round(res["fused_ms"] * 1e3, 1),
+                                 "variant_i_us": round(res["matvec_median_ms"] * 1e3, 1),
+                                 "dequant_ms": round(res["dequant_ms"], 1),
+                                 "note": "all 168 linears, dequant + matvec per call, median of 3"}
+    out["config5"] = {"cpu_ms": round(res["f16_ms"], 1),
+                      "note": "dequantizeGptqInt4 + f32ToF16Bits of all 168 tensors ([N,K] fp16), median of 3"}
+    del items
+    # config 4: one 7B-shaped layer (q, o 3584->3584; gate, up 3584->18944; down 18944->3584)
+    items = []
+    for (layer, proj, K, N) in synth.model_linears("7b"):
+        if layer == 0:
+            items.append((synth.gptq_linear(K, N, GROUP, seed=0x7B, key=(0, synth.PROJ_INDEX[proj])),
+                          synth.activations(1, K, seed=0x5EED, key=(0, synth.PROJ_INDEX[proj], 1))))
+    L7 = synth.QWEN7_LAYERS
+    res, _ = node_run(items, min(min_seconds, 5.0), {"fused_reps": 3})
+    out["config4_m1_extrapolated"] = {
+        "us": round(res["matvec_median_ms"] * 1e3 * L7, 1),
+        "variant_ii_us": round(res["fused_ms"] * 1e3 * L7, 1),
+        "dequant_ms": round(res["dequant_ms"] * L7, 1),
+        "layer_us": round(res["matvec_median_ms"] * 1e3, 1), "layers": L7,
+        "note": f"one layer's {len(items)} linears timed in full (variant (i) median, variant (ii) median of 3), "
+                f"x{L7} layers: extrapolated"}
+    out["host_cpu"] = res.get("cpu", "")
+    out["cores"] = 1
+    out["node"] = res.get("node", "")
+    return out
 
 
 def traffic_from_profiles(workload: str):
@@ -425,7 +518,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
                     help="all | step05 | headline | step7b | north | sweep | prefill | prefill_one | unpack | lmhead | "
-                         "attn | elem "
+                         "attn | elem | cpu "
                          "(subsets for profiling: headline = the 0.5B step and its MALL-flushed "
                          "timing only; north = the 7B-shaped step at M=1 only)")
     ap.add_argument("--m7b", default="1,2,4,8,16", help="decode batch sizes for the 7B-shaped step")
@@ -466,6 +559,7 @@ def main():
         gbs = step1.bytes / (kms * 1e-3) / 1e9
         log(f"0.5B step M=1 (one launch): {value:.1f} us/step, kernel {kms*1e3:.1f} us, "
             f"{gbs:.0f} GB/s; plan {si.as_dict()}")
+        flushed = None if args.no_flush else flushed_step_ms(ctx, step1)
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
                 "traffic": traffic_from_profiles("strip05_m1_indep" if si.kernel == ql.SEQ_STRIPS else "seq05_m1_indep"),
@@ -476,13 +570,19 @@ def main():
                 "avg_launch_us": round(kms * 1e3, 3),
                 "tiles": si.tiles, "reduces": si.reduces, "grid": si.grid,
                 "balance": round(si.balance, 4),
+                "mall_resident": True,
+                "flushed": None if flushed is None else {
+                    "us": round(flushed * 1e3, 1),
+                    "achieved": round(step1.bytes / (flushed * 1e-3) / 1e9, 1),
+                    "frac": round(step1.bytes / (flushed * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
                 "note": "one persistent launch per step (168 linears, each on its own input); "
                         "launch duration = HIP-event time of graphs of 10 consecutive launches on "
                         "the context stream / launches (value = one launch per graph replay, so "
-                        "it also carries the replay gap); the 0.5B weights (186 MB) fit the "
-                        "256 MB MALL"}
-        if not args.no_flush:
-            flushed = flushed_step_ms(ctx, step1)
+                        "it also carries the replay gap). The 0.5B weights (186 MB) stay in the "
+                        "256 MB MALL across replays, so achieved/frac are HBM+MALL bandwidth over "
+                        "the HBM peak; 'flushed' is one step after a read-only pass over 1 GiB has "
+                        "evicted them (HBM-fed, includes launch latency)"}
+        if flushed is not None:
             extra["step05_m1_flushed_us"] = round(flushed * 1e3, 1)
             extra["step05_m1_flushed_gbs"] = round(step1.bytes / (flushed * 1e-3) / 1e9, 1)
             log(f"0.5B step M=1 MALL-flushed: {flushed*1e3:.1f} us")
@@ -666,6 +766,10 @@ def main():
                       "bytes = the K and V caches once plus q and out")
         extra["attn"] = at
         log(f"decode attention: {at}")
+
+    if only == "cpu":
+        extra["cpu_plan"] = cpu_plan(ctx, args.cpu_seconds)
+        log(f"cpu plan: {extra['cpu_plan']}")
 
     if only in ("all", "unpack"):
         ms, nbytes = unpack_all(ctx, m05, max(5, args.steps // 5))
