@@ -527,6 +527,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-flush", action="store_true",
                     help="skip the MALL-flushed timing (profiling runs of the headline kernel)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="end with one 512 MiB device-to-device copy: the known-size kernel that "
+                         "scales FETCH_SIZE / WRITE_SIZE counter passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus "
@@ -563,8 +566,8 @@ def main():
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
                 "traffic": traffic_from_profiles("strip05_m1_indep" if si.kernel == ql.SEQ_STRIPS else "seq05_m1_indep"),
-                "kernel": ("strip_kernel<1,2,8,1,2,%d>" % si.split) if si.kernel == ql.SEQ_STRIPS
-                          else "seq_kernel<1,2,4,2,8,true>",
+                "kernel": ("strip_kernel<1,2,8,1,2,%d,%s>" % (si.split, "true" if si.stream else "false")
+                           if si.kernel == ql.SEQ_STRIPS else "seq_kernel<1,2,4,2,8,true>"),
                 "launches_per_step": 1,
                 "bytes_per_launch": step1.bytes,
                 "avg_launch_us": round(kms * 1e3, 3),
@@ -612,8 +615,19 @@ def main():
         for M in (1, 2, 4, 8, 16):
             st = SeqStep(ctx, m05, M, chained=False)
             ms = timed(st, max(10, args.steps // 2), 2)
-            sweep[str(M)] = {"us": round(ms * 1e3, 1), "gbs": round(st.bytes / (ms * 1e-3) / 1e9, 1)}
+            sweep[str(M)] = {"us": round(ms * 1e3, 1), "gbs": round(st.bytes / (ms * 1e-3) / 1e9, 1),
+                             "kernel": "strip"}
             st.release()
+        # past 16 rows the MFMA GEMM takes over (fp16 activations, one persistent launch)
+        for M in (32, 64):
+            st = PrefillStep(ctx, m05, M)
+            ms = timed(st, max(10, args.steps // 2), 2)
+            sweep[str(M)] = {"us": round(ms * 1e3, 1), "tflops": round(st.flops / (ms * 1e-3) / 1e12, 1),
+                             "kernel": "prefill"}
+            st.release()
+        sweep["note"] = ("M <= 16: the decode sequence (strip_kernel, fp32 x); M = 32, 64: the prefill "
+                         "GEMM launch (fp16 x, 128-row tiles). Two 16-row decode steps against one "
+                         "32-row prefill step place the crossover")
         extra["step05_m_sweep"] = sweep
         log(f"M sweep: {sweep}")
 
@@ -837,6 +851,12 @@ def main():
                                       for M in s7 if M.isdigit()}
         log(f"7B step: {s7}")
         m7.arena.release()
+
+    if args.calib_copy:
+        flush = ctx.arena(1 << 30)
+        ctx.copy(flush, 0, flush, 1 << 29, 1 << 29)
+        ctx.sync()
+        flush.release()
 
     ctx.destroy()
     if value is None:

@@ -259,6 +259,9 @@ typedef struct ql_seq_info {
     int32_t kernel;       /* QL_SEQ_TILES: dependency-ordered tiles; QL_SEQ_STRIPS: column strips;
                              QL_SEQ_PREFILL: prefill GEMM tiles (units: 128-k chunks) */
     int32_t split;        /* strips: waves per 64-column block (1: strips of 8 blocks, 2: of 4) */
+    int32_t stream;       /* strips: 1 when the packed weights are read with streaming loads (the
+                             weights exceed what the 256 MB MALL keeps between steps) */
+    int32_t reserved;
 } ql_seq_info;
 /* plan only (host, pure) for a given grid size: validation and the figures above */
 int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,

@@ -290,3 +290,36 @@ def test_gptq_validation_applies_per_linear():
     c.add(896, 896, c.ext(896))
     c.descs[0].bits = 3
     assert _err(c).name == "QL_E_BITS"
+
+
+def test_strips_stream_weights_the_mall_cannot_keep():
+    """Strips read the packed weights with streaming loads when the launch's weights exceed what
+    the MALL keeps between steps (the 7B step, 3.3 GB), and with ordinary loads when they fit
+    (the 0.5B step, 186 MB, which the next step then finds in the MALL)."""
+    c = Chain(M=1)
+    for _ in range(24):
+        for K, N in ((896, 896), (896, 128), (896, 128), (896, 896), (896, 4864), (896, 4864), (4864, 896)):
+            c.add(K, N, c.ext(K))
+    small = c.plan(grid=512)
+    assert small.kernel == ql.SEQ_STRIPS and small.stream == 0
+    big = qwen7b(Chain(M=1), 28, chained=False).plan(grid=256)
+    assert big.kernel == ql.SEQ_STRIPS and big.stream == 1
+    # chained sequences (dependency-ordered tiles) report no streaming
+    assert qwen7b(Chain(M=1), 2, chained=True).plan(grid=256).stream == 0
+
+
+def test_seq_info_struct_matches_the_library():
+    """ql_plan_seq writes exactly sizeof(SeqInfo) bytes: a guard area after the ctypes struct stays
+    untouched and the struct's last field (reserved) comes back zeroed."""
+    import ctypes
+    c = Chain(M=1)
+    c.add(896, 896, c.ext(896))
+    n = len(c.descs)
+    size = ctypes.sizeof(ql.SeqInfo)
+    buf = (ctypes.c_uint8 * (size + 64))(*([0xAA] * (size + 64)))
+    rc = ql.lib().ql_plan_seq(n, (ql.GptqDesc * n)(*c.descs), 1, (ctypes.c_uint64 * n)(*c.x), ql.DTYPE_F32,
+                              (ctypes.c_uint64 * n)(*c.y), 256, ctypes.cast(buf, ctypes.POINTER(ql.SeqInfo)))
+    assert rc == 0
+    assert bytes(buf[size:]) == b"\xaa" * 64
+    info = ql.SeqInfo.from_buffer_copy(bytes(buf[:size]))
+    assert info.reserved == 0 and info.linears == 1

@@ -411,6 +411,8 @@ void fill_strip_info(const ql::StripPlan& p, int n, uint64_t scratch, ql_seq_inf
     info->busiest_units = p.busiest_units;
     info->kernel = QL_SEQ_STRIPS;
     info->split = p.split;
+    info->stream = p.stream ? 1 : 0;
+    info->reserved = 0;
 }
 
 void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info* info)
@@ -427,6 +429,8 @@ void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info
     info->busiest_units = p.busiest_units;
     info->kernel = QL_SEQ_TILES;
     info->split = 1;
+    info->stream = 0;
+    info->reserved = 0;
 }
 
 int set_device(ql_ctx* ctx)
@@ -487,6 +491,7 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     q->sargs.G = sp.grid;
     q->sargs.group = descs[0].group;
     q->sargs.split = sp.split;
+    q->sargs.stream = sp.stream ? 1 : 0;
     fill_strip_info(sp, n, lay.total, &q->info);
     *out = q;
     return QL_OK;

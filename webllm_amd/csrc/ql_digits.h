@@ -26,6 +26,16 @@ __device__ __forceinline__ T ld_global(const T* p)
     return *p;   // host pass: never executed
 #endif
 }
+// a streaming load (nontemporal: the line is not kept for reuse)
+template <typename T>
+__device__ __forceinline__ T ld_stream(const T* p)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) T*)(p));
+#else
+    return *p;   // host pass: never executed
+#endif
+}
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 

@@ -323,10 +323,12 @@ struct StripArgs {
     const int32_t* task_begin; // [G + 1]
     int32_t M, G, group;
     int32_t split;             // waves per block: 1 (strips of 8 blocks) or 2 (strips of 4)
+    int32_t stream;            // 1: packed weights by streaming (nontemporal) loads
 };
 
 struct StripPlan {
     int grid = 0, strips = 0, split = 1;
+    bool stream = false;       // the weights exceed what the MALL keeps between steps
     uint64_t lds_bytes = 0;
     uint64_t total_units = 0, busiest_units = 0;   // block-groups: all, most on one workgroup
     std::vector<StripTask> tasks;

@@ -78,7 +78,7 @@ constexpr int kMaxStripBlocks = 8;       // most blocks in one strip
 //   4. wait for step 1's loads (the kCG positions' loads stay in flight), turn them into digits
 //      in the other LDS buffer, stage the next strip's bias with its first chunk;
 //   5. one barrier.
-template <int T, int NB, int W, int BPW, int P, int S>
+template <int T, int NB, int W, int BPW, int P, int S, bool NT>
 __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
 {
     // S waves share each block (S > 1: waves take alternate groups of every chunk and add their
@@ -291,7 +291,8 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
             const char* q = c.qw + g * c.Gq + c.cq + bb * (uint32_t)kCols * 4u;
 #pragma unroll
             for (int r = 0; r < 2 * NB; r++)
-                wb[d][b][r] = __builtin_bit_cast(uint4, ld_global(reinterpret_cast<const u32x4*>(q + c.lq[r])));
+                wb[d][b][r] = __builtin_bit_cast(uint4, NT ? ld_stream(reinterpret_cast<const u32x4*>(q + c.lq[r]))
+                                                           : ld_global(reinterpret_cast<const u32x4*>(q + c.lq[r])));
             zb[d][b] = ld_global(reinterpret_cast<const uint32_t*>(c.qz + g * c.Gz + c.cz + bb * (uint32_t)(kCols / 8) * 4u + c.lz));
             sb[d][b] = __builtin_bit_cast(uint2, ld_global(reinterpret_cast<const u32x2*>(c.sc + g * c.Gs + c.cs + bb * (uint32_t)kCols * 2u + c.ls)));
         }
@@ -501,21 +502,32 @@ struct StripKernel {
 // Eight waves of one block each (two waves per SIMD, so one wave's MFMAs overlap the other's
 // epilogue); M 9..16 as QL_STRIP_W4 says (four waves of two blocks measured 20% slower). With
 // split 2, two waves share each block of a 4-block strip.
-template <int NB, int S>
+template <int NB, int S, bool NT>
 StripKernel strip_kernel_for_ns(int M)
 {
-    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, QL_STRIP_P1, S>), 64 * 8};
-    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, QL_STRIP_P2, S>), 64 * 8};
-    if (S > 1) return {reinterpret_cast<const void*>(&strip_kernel<4, NB, 8, 1, QL_STRIP_P4, S>), 64 * 8};
-    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, QL_STRIP_W4, 8 / QL_STRIP_W4, QL_STRIP_P4, 1>),
+    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, QL_STRIP_P1, S, NT>), 64 * 8};
+    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, QL_STRIP_P2, S, NT>), 64 * 8};
+    if (S > 1) return {reinterpret_cast<const void*>(&strip_kernel<4, NB, 8, 1, QL_STRIP_P4, S, NT>), 64 * 8};
+    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, QL_STRIP_W4, 8 / QL_STRIP_W4, QL_STRIP_P4, 1, NT>),
             64 * QL_STRIP_W4};
 }
 
-StripKernel strip_kernel_for(int M, int group, int split)
+template <bool NT>
+StripKernel strip_kernel_for_nt(int M, int group, int split)
 {
-    if (group == 64) return split == 2 ? strip_kernel_for_ns<1, 2>(M) : strip_kernel_for_ns<1, 1>(M);
-    if (group == 128) return split == 2 ? strip_kernel_for_ns<2, 2>(M) : strip_kernel_for_ns<2, 1>(M);
+    if (group == 64) return split == 2 ? strip_kernel_for_ns<1, 2, NT>(M) : strip_kernel_for_ns<1, 1, NT>(M);
+    if (group == 128) return split == 2 ? strip_kernel_for_ns<2, 2, NT>(M) : strip_kernel_for_ns<2, 1, NT>(M);
     return {nullptr, 0};
+}
+
+// Packed weights that the MALL cannot keep until the next step are read with streaming
+// (nontemporal) loads: the 7B step at M = 1 takes 503 us against 561 us with ordinary loads.
+// Weights that it keeps (the 0.5B step) are read with ordinary loads, so that the next step
+// finds them there (34.8 us against 38.6 us). Zeros and scales always use ordinary loads
+// (streaming them too measured 2% slower on the 7B step).
+StripKernel strip_kernel_for(int M, int group, int split, bool stream)
+{
+    return stream ? strip_kernel_for_nt<true>(M, group, split) : strip_kernel_for_nt<false>(M, group, split);
 }
 
 }  // namespace
@@ -606,18 +618,22 @@ void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int spl
 // better (a strip of 8 blocks of a long-K linear can outweigh a workgroup's mean share).
 void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
 {
+    uint64_t bytes = 0;
+    for (const SeqSpec& s : lin) bytes += s.weight_bytes;
     plan_strips_split(lin, M, grid, 1, out);
+    out->stream = bytes > kStripMallBytes;
     if (out->total_units == 0) return;
     const double mean = (double)out->total_units / grid;
     if (out->busiest_units <= mean * kStripSplitBalance) return;
     StripPlan two;
     plan_strips_split(lin, M, grid, 2, &two);
+    two.stream = out->stream;
     if (two.busiest_units < out->busiest_units) *out = two;
 }
 
 hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream)
 {
-    const StripKernel k = strip_kernel_for(a.M, a.group, a.split);
+    const StripKernel k = strip_kernel_for(a.M, a.group, a.split, a.stream != 0);
     if (!k.fn) return hipErrorInvalidValue;
     void* args[] = {const_cast<StripArgs*>(&a)};
     return hipLaunchKernel(k.fn, dim3(a.G), dim3(k.threads), args, lds, stream);

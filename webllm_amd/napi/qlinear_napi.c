@@ -719,6 +719,7 @@ static napi_value js_seq_info(napi_env env, napi_callback_info info)
     napi_create_int32(env, si.split, &sv);
     napi_set_named_property(env, o, "kernel", kv);
     napi_set_named_property(env, o, "split", sv);
+    napi_set_named_property(env, o, "stream", make_i32(env, si.stream));
     return o;
 }
 

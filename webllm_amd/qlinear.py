@@ -64,7 +64,8 @@ class SeqInfo(ctypes.Structure):
                 ("reduces", ctypes.c_int32), ("grid", ctypes.c_int32), ("max_split", ctypes.c_int32),
                 ("lds_bytes", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64),
                 ("total_units", ctypes.c_uint64), ("busiest_units", ctypes.c_uint64),
-                ("kernel", ctypes.c_int32), ("split", ctypes.c_int32)]
+                ("kernel", ctypes.c_int32), ("split", ctypes.c_int32), ("stream", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
 
     def as_dict(self) -> dict:
         return {f: getattr(self, f) for f, _ in self._fields_}
