@@ -498,6 +498,13 @@ struct StripKernel {
 #ifndef QL_STRIP_W4
 #define QL_STRIP_W4 8
 #endif
+// The planner starts each CU's second workgroup (workgroups kPlanCUs and up) this many
+// block-groups behind: its waves issue after the first workgroup's and stream at about half its
+// rate until that one's first strip ends. Measured on the 0.5B step (grid 512): 33.1 us per step
+// at 48 or 80 against 34.6 at 0 and 36.3 or more at 112 and up.
+#ifndef QL_STRIP_SECOND_OFFSET
+#define QL_STRIP_SECOND_OFFSET 64
+#endif
 
 // Eight waves of one block each (two waves per SIMD, so one wave's MFMAs overlap the other's
 // epilogue); M 9..16 as QL_STRIP_W4 says (four waves of two blocks measured 20% slower). With
@@ -592,7 +599,11 @@ void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int spl
     std::vector<uint64_t> load(grid, 0), units(grid, 0);
     typedef std::pair<uint64_t, int> Slot;
     std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>> q;
-    for (int w = 0; w < grid; w++) q.push({0, w});
+    // a CU's second workgroup starts behind its first (the first one's waves issue first)
+    for (int w = 0; w < grid; w++) {
+        load[w] = w >= kPlanCUs ? (uint64_t)QL_STRIP_SECOND_OFFSET : 0;
+        q.push({load[w], w});
+    }
     for (const Item& it : items) {
         const Slot s = q.top();
         q.pop();
