@@ -625,7 +625,7 @@ def main():
         # past 16 rows the MFMA GEMM takes over (fp16 activations, one persistent launch)
         for M in (32, 64):
             st = PrefillStep(ctx, m05, M)
-            ms = timed(st, max(10, args.steps // 2), 2)
+            ms = timed(st, max(10, args.steps // 2), 10)
             sweep[str(M)] = {"us": round(ms * 1e3, 1), "tflops": round(st.flops / (ms * 1e-3) / 1e12, 1),
                              "kernel": "prefill"}
             st.release()
@@ -639,7 +639,8 @@ def main():
         pre = {}
         for M in [int(v) for v in args.prefill_m.split(",")]:
             st = PrefillStep(ctx, m05, M)
-            ms = timed(st, max(5, args.steps // 5), 2)
+            # the first launches after an idle period run up to 20% slow (clock ramp): warm up longer
+            ms = timed(st, max(20, args.steps // 2), 30)
             kms = st.kernel_ms(max(10, args.steps // 2))
             tf = st.flops / (kms * 1e-3) / 1e12
             pre[f"{M}_one_launch"] = {

@@ -509,13 +509,17 @@ struct StripKernel {
 // Eight waves of one block each (two waves per SIMD, so one wave's MFMAs overlap the other's
 // epilogue); M 9..16 as QL_STRIP_W4 says (four waves of two blocks measured 20% slower). With
 // split 2, two waves share each block of a 4-block strip.
+// jobs in flight: as asked when they fill a chunk's positions (kCG / S) in whole rounds, else 2
+constexpr int ring_depth(int p, int S) { return (kCG / S) % p == 0 ? p : 2; }
+
 template <int NB, int S, bool NT>
 StripKernel strip_kernel_for_ns(int M)
 {
-    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, QL_STRIP_P1, S, NT>), 64 * 8};
-    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, QL_STRIP_P2, S, NT>), 64 * 8};
-    if (S > 1) return {reinterpret_cast<const void*>(&strip_kernel<4, NB, 8, 1, QL_STRIP_P4, S, NT>), 64 * 8};
-    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, QL_STRIP_W4, 8 / QL_STRIP_W4, QL_STRIP_P4, 1, NT>),
+    constexpr int P1 = ring_depth(QL_STRIP_P1, S), P2 = ring_depth(QL_STRIP_P2, S), P4 = ring_depth(QL_STRIP_P4, S);
+    if (M <= 4) return {reinterpret_cast<const void*>(&strip_kernel<1, NB, 8, 1, P1, S, NT>), 64 * 8};
+    if (M <= 8) return {reinterpret_cast<const void*>(&strip_kernel<2, NB, 8, 1, P2, S, NT>), 64 * 8};
+    if (S > 1) return {reinterpret_cast<const void*>(&strip_kernel<4, NB, 8, 1, P4, S, NT>), 64 * 8};
+    return {reinterpret_cast<const void*>(&strip_kernel<4, NB, QL_STRIP_W4, 8 / QL_STRIP_W4, P4, 1, NT>),
             64 * QL_STRIP_W4};
 }
 
