@@ -26,6 +26,14 @@
  *                                 with src/model/qwen.ts:556-559 passBreak, as runForward uses
  *                                 them (qwen.ts:382-387, :411-473): a forward's linears recorded
  *                                 once, then submitted as one unit per step
+ *   ql_seq_fuse, ql_plan_seq_fused, ql_seq_create_fused
+ *                                 the same, with the layer's elementwise dispatches around the
+ *                                 linears folded in: rmsnorm before q/k/v and gate/up
+ *                                 (qwen.ts:403-405, :458-460, src/gpu/kernels/norm/rmsnorm.wgsl),
+ *                                 the residual vec_add after o and down (qwen.ts:453-455,
+ *                                 :476-478, src/gpu/kernels/misc/vec_add.wgsl) and silu_mul
+ *                                 before down (qwen.ts:468-470,
+ *                                 src/gpu/kernels/activation/silu_mul.wgsl)
  */
 #ifndef QLINEAR_H
 #define QLINEAR_H
@@ -272,6 +280,32 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
 int ql_seq_get_info(const ql_seq* seq, ql_seq_info* info);
 int ql_seq_run(ql_ctx* ctx, ql_seq* seq);
 int ql_seq_status(ql_ctx* ctx, ql_seq* seq);
+/* Fused sequences (M = 1..16, fp32 x): per linear, elementwise work folded into the launch.
+ *   norm_w_off  QL_NONE, or the weights-arena offset of an fp32 [K] RMSNorm weight: the linear
+ *               reads rmsnorm(x) = x * rsqrt(mean(x^2) + norm_eps) * w per row (rmsNormRef)
+ *               instead of x;
+ *   x2_off      QL_NONE, or the activation-arena offset of an fp32 [M, K] second operand: the
+ *               linear reads silu(x) * x2 (siluMulRef) instead of x; like x_offs it is another
+ *               linear's output when it equals that linear's y offset, else external;
+ *   res_off     QL_NONE, or the activation-arena offset of an fp32 [M, N] residual added to the
+ *               linear's output (y = W.x + bias + res); another linear's output when it equals
+ *               that linear's y offset, else external.
+ * norm and x2 exclude each other. A fused sequence always runs as dependency-ordered tiles
+ * (QL_SEQ_TILES); a linear runs after every producer it reads (x, x2 or res). ql_plan_seq_fused
+ * and ql_seq_create_fused with fuse == NULL behave as ql_plan_seq and ql_seq_create. */
+typedef struct ql_seq_fuse {
+    uint64_t norm_w_off;
+    uint64_t x2_off;
+    uint64_t res_off;
+    float norm_eps;
+    int32_t reserved;
+} ql_seq_fuse;
+int ql_plan_seq_fused(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,
+                      int32_t x_dtype, const uint64_t* y_offs, const ql_seq_fuse* fuse, int32_t grid,
+                      ql_seq_info* info);
+int ql_seq_create_fused(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights,
+                        ql_arena* act, const uint64_t* x_offs, int32_t x_dtype, int32_t M,
+                        const uint64_t* y_offs, const ql_seq_fuse* fuse, ql_seq** out);
 /* diagnostic: polls a device-side wait makes before aborting the run (default 4M, min 64) */
 int ql_seq_set_spin_limit(ql_seq* seq, uint32_t polls);
 int ql_seq_destroy(ql_seq* seq);

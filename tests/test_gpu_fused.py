@@ -1,0 +1,182 @@
+"""GPU parity of fused sequences (ql_seq_create_fused): the Qwen layer's elementwise work folded
+into one persistent launch of its linears, as the reference's layer runs it
+(src/model/qwen.ts:403-478: rmsnorm -> q/k/v, o -> vec_add, rmsnorm -> gate/up -> silu_mul ->
+down -> vec_add; o reads q in attention's place).
+
+Every linear is checked on the inputs the GPU actually used (its producers' GPU outputs), against
+the oracle's composition: rmsNormRef (orc_add_rmsnorm) or siluMulRef (orc_silu_mul) of those
+inputs, then gemmNTRef over the quant.ts weights, plus the residual (vec_add in fp32), with the
+single-GEMV bar |d| <= atol + 1e-4 |ref|, atol = 1e-5 * max(1, rms(input))."""
+import sys
+
+import numpy as np
+import pytest
+
+from webllm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-4
+EPS = 1e-6
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+class FusedModel:
+    """`layers` Qwen-shaped layers as one fused sequence: q/k/v <- rmsnorm(h, ln1);
+    h1 = h + o(q); gate/up <- rmsnorm(h1, ln2); h2 = h1 + down(silu(gate) * up)."""
+
+    def __init__(self, ql, ctx, M, layers, C, I, KV, seed=0xF05E, group=128):
+        self.ql, self.M, self.group = ql, M, group
+        wl, al = ql.ArenaLayout(), ql.ArenaLayout()
+        self.h0 = synth.activations(M, C, seed=seed, key=(M,))
+        self.h0_off = al.take(self.h0.nbytes)
+        self.lin, self.norms = [], []
+        fuse = []
+        h = (self.h0_off, -1)
+        for layer in range(layers):
+            ln = []
+            for k in range(2):
+                w = 1.0 + 0.1 * synth.activations(1, C, seed=seed + 7, key=(layer, k))[0]
+                ln.append((wl.take(w.nbytes), w))
+            self.norms.extend(ln)
+            for key, N in (("q", C), ("k", KV), ("v", KV)):
+                self._add(wl, al, layer, key, C, N, h, {"norm": ln[0]}, biased=True)
+                fuse.append(ql.make_fuse(norm_w_off=ln[0][0], norm_eps=EPS))
+            q = self._ref(-3)
+            self._add(wl, al, layer, "o", C, C, q, {"res": h})
+            fuse.append(ql.make_fuse(res_off=h[0]))
+            h1 = self._ref(-1)
+            for key in ("gate", "up"):
+                self._add(wl, al, layer, key, C, I, h1, {"norm": ln[1]})
+                fuse.append(ql.make_fuse(norm_w_off=ln[1][0], norm_eps=EPS))
+            g, u = self._ref(-2), self._ref(-1)
+            self._add(wl, al, layer, "down", I, C, g, {"x2": u, "res": h1})
+            fuse.append(ql.make_fuse(x2_off=u[0], res_off=h1[0]))
+            h = self._ref(-1)
+        self.weights = ctx.arena(wl.used)
+        self.act = ctx.arena(al.used)
+        for L in self.lin:
+            t = L["t"]
+            self.weights.write(L["qw"], t.qweight)
+            if L["qz"] is not None:
+                self.weights.write(L["qz"], t.qzeros)
+            self.weights.write(L["sc"], t.scales)
+            if L["bias"] is not None:
+                self.weights.write(L["b"], L["bias"])
+        for off, w in self.norms:
+            self.weights.write(off, w.astype(np.float32))
+        self.act.write(self.h0_off, self.h0)
+        self.descs = [ql.make_desc(L["qw"], L["qz"], L["sc"], L["t"].K, L["t"].N, group, L["b"])
+                      for L in self.lin]
+        self.fuse = fuse
+        self.seq = ctx.seq(self.descs, self.weights, self.act, [L["x"][0] for L in self.lin], 0, M,
+                           [L["y_off"] for L in self.lin], fuse=fuse)
+
+    def _ref(self, i):
+        return (self.lin[i]["y_off"], len(self.lin) + i)
+
+    def _add(self, wl, al, layer, key, K, N, x, extra, biased=False):
+        idx = len(self.lin)
+        sym = idx % 3 == 1
+        t = synth.gptq_linear(K, N, self.group, seed=0xF05F, key=(layer, idx), stored_zero=7 if idx % 2 else None)
+        bias = synth.activations(1, N, seed=0xF060, key=(layer, idx))[0] if biased else None
+        L = {"t": t, "bias": bias, "qw": wl.take(t.qweight.nbytes),
+             "qz": None if sym else wl.take(t.qzeros.nbytes), "sc": wl.take(t.scales.nbytes),
+             "b": None if bias is None else wl.take(bias.nbytes), "x": x,
+             "y_off": al.take(self.M * N * 4), "name": f"L{layer}.{key}", **extra}
+        L["qzeros"] = None if sym else t.qzeros
+        self.lin.append(L)
+
+    def outputs(self):
+        return [self.act.read(L["y_off"], (self.M, L["t"].N), np.float32) for L in self.lin]
+
+    def value(self, ref, ys):
+        off, src = ref
+        return self.h0 if src < 0 else ys[src]
+
+    def release(self):
+        self.seq.destroy()
+        self.weights.release()
+        self.act.release()
+
+
+def check_fused(orc, m: FusedModel, ys, label, cols_for=None):
+    worst = 0.0
+    for L, y in zip(m.lin, ys):
+        t = L["t"]
+        x = m.value(L["x"], ys)
+        if "norm" in L:
+            x = orc.add_rmsnorm(x, L["norm"][1], EPS)[1]
+        if "x2" in L:
+            x = orc.silu_mul(x, m.value(L["x2"], ys))
+        if cols_for is None:
+            cols = np.arange(t.N, dtype=np.int32)
+            ref = orc.gptq_linear(t.qweight, L["qzeros"], t.scales, x, L["bias"], m.group)
+        else:
+            cols = cols_for(t.N)
+            ref = orc.gptq_linear_cols(t.qweight, L["qzeros"], t.scales, x, cols, L["bias"], m.group)
+        if "res" in L:
+            ref = ref + m.value(L["res"], ys)[:, cols]        # vec_add in fp32
+        got = np.ascontiguousarray(y[:, cols])
+        atol = 1e-5 * max(1.0, float(np.sqrt(np.mean(x.astype(np.float64) ** 2))))
+        ok, max_abs, max_rel = orc.check_tolerance(got, ref, atol, RTOL)
+        assert np.isfinite(y).all(), f"{label} {L['name']}: non-finite output"
+        worst = max(worst, float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)))
+        assert ok, f"{label} {L['name']}: maxAbs {max_abs:.3e} (atol {atol:.2e}) maxRel {max_rel:.3e}"
+    say(f"  {label}: {len(ys)} linears within bar, worst normwise {worst:.3e}")
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_fused_layers_05b(ql, ctx, orc, M):
+    """Two 0.5B-shaped layers (14 linears, 8 dependent passes) in one fused launch; repeated runs
+    and graph replays are bit-identical (fixed reduction orders, epochs instead of clears)."""
+    m = FusedModel(ql, ctx, M, 2, 896, 4864, 128)
+    info = m.seq.info
+    say(f"fused 0.5B x2 M={M}: {info.as_dict()}")
+    assert info.kernel == ql.SEQ_TILES and info.passes == 8 and info.linears == 14
+    m.seq.run()
+    m.seq.status()
+    ys = m.outputs()
+    check_fused(orc, m, ys, f"fused 0.5B M={M}")
+    last = m.lin[-1]
+    zero = np.zeros((M, last["t"].N), np.float32)
+    m.act.write(last["y_off"], zero)
+    m.seq.run()
+    m.seq.status()
+    for a, b in zip(ys, m.outputs()):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    ctx.graph_begin()
+    m.seq.run()
+    g = ctx.graph_end()
+    for r in range(3):
+        m.act.write(last["y_off"], zero)
+        g.launch()
+        m.seq.status()
+        for a, b in zip(ys, m.outputs()):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"graph replay {r}"
+    g.destroy()
+    m.release()
+
+
+def _sample(N, count=4):
+    nb = N // 64
+    picks = sorted(set([0, nb - 1] + [int(round(i * (nb - 1) / (count - 1))) for i in range(count)]))
+    return np.concatenate([np.arange(b * 64, b * 64 + 64) for b in picks]).astype(np.int32)
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_fused_layer_7b(ql, ctx, orc, M):
+    """One 7B-shaped layer (q/o 3584, gate/up 18944, down 18944 -> 3584, 4 KV heads of 128 for
+    k/v): RMSNorm over 3584-wide rows, SiLU-mul over 18944, both residuals; sampled columns."""
+    m = FusedModel(ql, ctx, M, 1, 3584, 18944, 512)
+    info = m.seq.info
+    say(f"fused 7B x1 M={M}: {info.as_dict()}")
+    assert info.kernel == ql.SEQ_TILES and info.passes == 4
+    m.seq.run()
+    m.seq.status()
+    check_fused(orc, m, m.outputs(), f"fused 7B M={M}", cols_for=_sample)
+    m.release()

@@ -323,3 +323,99 @@ def test_seq_info_struct_matches_the_library():
     assert bytes(buf[size:]) == b"\xaa" * 64
     info = ql.SeqInfo.from_buffer_copy(bytes(buf[:size]))
     assert info.reserved == 0 and info.linears == 1
+
+
+def fused_layers(c: Chain, layers: int, C=896, I=4864, KV=128):
+    """The Qwen layer's data flow as a fused sequence (o reads q in attention's place):
+    q/k/v <- rmsnorm(h); h1 = h + o(q); gate/up <- rmsnorm(h1); h2 = h1 + down(silu(gate) * up)."""
+    fuse = []
+    h = c.ext(C)
+    for _ in range(layers):
+        ln1, ln2 = c.w.take(C * 4), c.w.take(C * 4)
+        q = c.add(C, C, h)
+        fuse.append(ql.make_fuse(norm_w_off=ln1))
+        c.add(C, KV, h)
+        fuse.append(ql.make_fuse(norm_w_off=ln1))
+        c.add(C, KV, h)
+        fuse.append(ql.make_fuse(norm_w_off=ln1))
+        h1 = c.add(C, C, q)
+        fuse.append(ql.make_fuse(res_off=h))
+        g = c.add(C, I, h1)
+        fuse.append(ql.make_fuse(norm_w_off=ln2))
+        u = c.add(C, I, h1)
+        fuse.append(ql.make_fuse(norm_w_off=ln2))
+        h = c.add(I, C, g)
+        fuse.append(ql.make_fuse(x2_off=u, res_off=h1))
+    return c, fuse
+
+
+def test_fused_layers_plan_as_chained_tiles():
+    """Norms, residuals and SiLU-mul folded in: the layer's 4 dependent passes (q/k/v, o,
+    gate/up, down), every linear's producers (input, GLU operand, residual) in earlier passes;
+    a fused sequence never takes strips, even when no linear reads another's input."""
+    c, fuse = fused_layers(Chain(), 2)
+    info = ql.plan_seq(c.descs, c.M, c.x, c.y, 256, fuse=fuse)
+    assert info.kernel == ql.SEQ_TILES and info.linears == 14 and info.passes == 8
+    # independent linears with a norm on their external inputs: still tiles
+    c2 = Chain()
+    w = c2.w.take(896 * 4)
+    f2 = []
+    for _ in range(4):
+        c2.add(896, 896, c2.ext(896))
+        f2.append(ql.make_fuse(norm_w_off=w))
+    assert ql.plan_seq(c2.descs, 1, c2.x, c2.y, 256).kernel == ql.SEQ_STRIPS
+    i2 = ql.plan_seq(c2.descs, 1, c2.x, c2.y, 256, fuse=f2)
+    assert i2.kernel == ql.SEQ_TILES and i2.passes == 1
+    # no fusion at all through the fused entry point: the same plan as ql_plan_seq
+    none = [ql.make_fuse() for _ in c2.descs]
+    assert ql.plan_seq(c2.descs, 1, c2.x, c2.y, 256, fuse=none).kernel == ql.SEQ_STRIPS
+
+
+def test_fused_residual_counts_as_a_dependency():
+    """A linear whose only link to an earlier one is its residual runs in a later pass."""
+    c = Chain()
+    y0 = c.add(896, 896, c.ext(896))
+    c.add(896, 896, c.ext(896))
+    fuse = [ql.make_fuse(), ql.make_fuse(res_off=y0)]
+    info = ql.plan_seq(c.descs, 1, c.x, c.y, 256, fuse=fuse)
+    assert info.kernel == ql.SEQ_TILES and info.passes == 2
+
+
+def test_fused_validation():
+    """Norm and GLU exclude each other; producers must run earlier and have the operand's width;
+    norm weights are 16-byte aligned with eps in [0, 1]; an external residual must not overlap an
+    output; fusion is refused for prefill sequences."""
+    c = Chain()
+    h = c.ext(896)
+    w = c.w.take(896 * 4)
+    y0 = c.add(896, 896, h)
+    c.add(896, 896, y0)
+
+    def code(fuse, M=1, descs=None):
+        d = descs or c.descs
+        with pytest.raises(ql.QlError) as e:
+            ql.plan_seq(d, M, c.x[:len(d)], c.y[:len(d)], 256, fuse=fuse)
+        return e.value.name
+
+    f = ql.make_fuse
+    assert code([f(norm_w_off=w, x2_off=y0), f()]) == "QL_E_INVALID"          # norm and GLU both
+    assert code([f(res_off=c.y[1]), f()]) == "QL_E_INVALID"                      # residual from a later linear
+    assert code([f(), f(norm_w_off=w + 4)]) == "QL_E_ALIGN"                      # norm weight alignment
+    assert code([f(), f(norm_w_off=w, norm_eps=-1.0)]) == "QL_E_INVALID"
+    # an external residual that overlaps an output
+    assert code([f(), f(res_off=y0 + 64)]) == "QL_E_INVALID"
+    # a GLU operand from a producer of the wrong width
+    c2 = Chain()
+    hh = c2.ext(896)
+    a = c2.add(896, 128, hh)
+    c2.add(896, 896, hh)
+    with pytest.raises(ql.QlError) as e:
+        ql.plan_seq(c2.descs, 1, c2.x, c2.y, 256, fuse=[f(), f(x2_off=a)])
+    assert e.value.name == "QL_E_INVALID"
+    # fusion is a decode feature (M <= 16)
+    c3 = Chain(M=32)
+    ww = c3.w.take(896 * 4)
+    c3.add(896, 896, c3.ext(896, es=2))
+    with pytest.raises(ql.QlError) as e:
+        ql.plan_seq(c3.descs, 32, c3.x, c3.y, 256, x_dtype=ql.DTYPE_F16, fuse=[f(norm_w_off=ww)])
+    assert e.value.name == "QL_E_INVALID"

@@ -255,7 +255,7 @@ uint64_t gptq_weight_bytes(const ql_gptq_desc* d)
 // any output of the sequence; outputs must not overlap each other.
 int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,
                 int32_t x_dtype, const uint64_t* y_offs, uint64_t w_bytes, uint64_t act_bytes,
-                std::vector<ql::SeqSpec>* specs)
+                std::vector<ql::SeqSpec>* specs, const ql_seq_fuse* fuse = nullptr)
 {
     if (!descs || !x_offs || !y_offs) return fail(QL_E_INVALID, "null sequence arrays");
     if (n <= 0 || n > ql::kSeqMaxLinears)
@@ -330,7 +330,70 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
                 return fail(QL_E_INVALID, "linear %d: input overlaps the output of linear %d", i, pv.second);
         }
     }
+    if (!fuse) return QL_OK;
+    // Fused operands: a producer when the offset starts another linear's output (earlier in the
+    // sequence, of the operand's width), else an external f32 range that overlaps no output.
+    auto operand = [&](int i, uint64_t off, int width, const char* what, int* src) -> int {
+        auto it = std::lower_bound(ys.begin(), ys.end(), std::make_pair(off, -1));
+        if (it != ys.end() && it->first == off) {
+            const int j = it->second;
+            if (j >= i) return fail(QL_E_INVALID, "linear %d: its %s is the output of linear %d, which runs later", i, what, j);
+            if (descs[j].N != width)
+                return fail(QL_E_INVALID, "linear %d: its %s is linear %d's output, width %d != %d", i, what, j,
+                            descs[j].N, width);
+            *src = j;
+            return QL_OK;
+        }
+        const uint64_t b = (uint64_t)M * width * 4;
+        if (off % 16) return fail(QL_E_ALIGN, "linear %d: the %s offset must be 16-byte aligned", i, what);
+        if (!in_range(off, b, act_bytes)) return fail(QL_E_RANGE, "linear %d: the %s lies outside the activation arena", i, what);
+        if (it != ys.end() && it->first < off + b)
+            return fail(QL_E_INVALID, "linear %d: the %s overlaps the output of linear %d", i, what, it->second);
+        if (it != ys.begin()) {
+            const auto pv = *(it - 1);
+            if (pv.first + (uint64_t)M * descs[pv.second].N * 4 > off)
+                return fail(QL_E_INVALID, "linear %d: the %s overlaps the output of linear %d", i, what, pv.second);
+        }
+        *src = -1;
+        return QL_OK;
+    };
+    bool any = false;
+    for (int i = 0; i < n; i++) {
+        const ql_seq_fuse& f = fuse[i];
+        ql::SeqSpec& s = (*specs)[i];
+        const int K = descs[i].K, N = descs[i].N;
+        if (f.norm_w_off != QL_NONE && f.x2_off != QL_NONE)
+            return fail(QL_E_INVALID, "linear %d: a fused RMSNorm and a fused SiLU-mul exclude each other", i);
+        if (f.norm_w_off != QL_NONE) {
+            if (f.norm_w_off % 16) return fail(QL_E_ALIGN, "linear %d: the norm weight offset must be 16-byte aligned", i);
+            if (!in_range(f.norm_w_off, (uint64_t)K * 4, w_bytes))
+                return fail(QL_E_RANGE, "linear %d: norm weight [K] outside the weight arena", i);
+            if (!(f.norm_eps >= 0.f) || f.norm_eps > 1.f)
+                return fail(QL_E_INVALID, "linear %d: norm_eps must be in [0, 1]", i);
+            s.fuse |= ql::kFuseNorm;
+        }
+        if (f.x2_off != QL_NONE) {
+            int rc = operand(i, f.x2_off, K, "SiLU-mul operand", &s.src2);
+            if (rc) return rc;
+            s.fuse |= ql::kFuseGlu;
+        }
+        if (f.res_off != QL_NONE) {
+            int rc = operand(i, f.res_off, N, "residual", &s.res_src);
+            if (rc) return rc;
+            s.fuse |= ql::kFuseRes;
+        }
+        any = any || s.fuse != 0;
+    }
+    if (any && prefill)
+        return fail(QL_E_INVALID, "fused elementwise work runs in decode sequences (M = 1..%d)", ql::kGemvMaxM);
     return QL_OK;
+}
+
+bool seq_fused(const std::vector<ql::SeqSpec>& specs)
+{
+    for (const ql::SeqSpec& s : specs)
+        if (s.fuse) return true;
+    return false;
 }
 
 // Device memory of a planned sequence, laid out in one allocation.
@@ -1329,13 +1392,15 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
     return QL_OK;
 }
 
-int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,
-                int32_t x_dtype, const uint64_t* y_offs, int32_t grid, ql_seq_info* info)
+namespace {
+
+int plan_seq_impl(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs, int32_t x_dtype,
+                  const uint64_t* y_offs, const ql_seq_fuse* fuse, int32_t grid, ql_seq_info* info)
 {
     if (!info) return fail(QL_E_INVALID, "null info pointer");
     if (grid < 1 || grid > (1 << 16)) return fail(QL_E_INVALID, "grid must be 1..65536");
     std::vector<ql::SeqSpec> specs;
-    int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, UINT64_MAX, UINT64_MAX, &specs);
+    int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, UINT64_MAX, UINT64_MAX, &specs, fuse);
     if (rc) return rc;
     if (M > ql::kGemvMaxM) {
         ql::PrefillPlan pp;
@@ -1343,7 +1408,7 @@ int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
         fill_prefill_info(pp, n, M, specs, prefill_layout(n, pp).total, info);
         return QL_OK;
     }
-    if (ql::strip_eligible(specs, M)) {
+    if (!seq_fused(specs) && ql::strip_eligible(specs, M)) {
         ql::StripPlan sp;
         ql::plan_strips(specs, M, grid, &sp);
         fill_strip_info(sp, n, strip_layout(specs, sp).total, info);
@@ -1357,9 +1422,26 @@ int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
     return QL_OK;
 }
 
-int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights,
-                  ql_arena* act, const uint64_t* x_offs, int32_t x_dtype, int32_t M,
-                  const uint64_t* y_offs, ql_seq** out)
+}  // namespace
+
+int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,
+                int32_t x_dtype, const uint64_t* y_offs, int32_t grid, ql_seq_info* info)
+{
+    return plan_seq_impl(n, descs, M, x_offs, x_dtype, y_offs, nullptr, grid, info);
+}
+
+int ql_plan_seq_fused(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,
+                      int32_t x_dtype, const uint64_t* y_offs, const ql_seq_fuse* fuse, int32_t grid,
+                      ql_seq_info* info)
+{
+    return plan_seq_impl(n, descs, M, x_offs, x_dtype, y_offs, fuse, grid, info);
+}
+
+namespace {
+
+int seq_create_impl(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights, ql_arena* act,
+                    const uint64_t* x_offs, int32_t x_dtype, int32_t M, const uint64_t* y_offs,
+                    const ql_seq_fuse* fuse, ql_seq** out)
 {
     if (!ctx || !weights || !act || !out) return fail(QL_E_INVALID, "null context, arena or output");
     *out = nullptr;
@@ -1367,14 +1449,15 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
     if (weights->device != ctx->device || act->device != ctx->device)
         return fail(QL_E_INVALID, "arenas belong to another device");
     std::vector<ql::SeqSpec> specs;
-    int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, weights->size, act->size, &specs);
+    int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, weights->size, act->size, &specs, fuse);
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
+    const bool fused = seq_fused(specs);
     if (M > ql::kGemvMaxM) return prefill_create(ctx, n, descs, weights, act, x_offs, M, y_offs, specs, out);
-    if (ql::strip_eligible(specs, M)) return strip_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs,
-                                                          specs, out);
+    if (!fused && ql::strip_eligible(specs, M))
+        return strip_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, specs, out);
     int per_cu = 0;
-    QL_HIP(ql::seq_blocks_per_cu(M, descs[0].group, &per_cu));
+    QL_HIP(ql::seq_blocks_per_cu(M, descs[0].group, fused, &per_cu));
     if (per_cu < 1) return fail(QL_E_INVALID, "sequence kernel does not fit on a CU");
     const int grid = std::min(per_cu, ql::seq_wg_per_cu()) * ctx->cu_count;
     ql::SeqPlanOut p;
@@ -1403,6 +1486,19 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
         L.N = d->N;
         L.K = d->K;
         L.x_dtype = x_dtype;
+        L.fuse = specs[i].fuse;
+        L.src2 = specs[i].src2;
+        L.res_src = specs[i].res_src;
+        L.norm_w = nullptr;
+        L.x2 = nullptr;
+        L.res = nullptr;
+        L.norm_eps = 0.f;
+        if (L.fuse & ql::kFuseNorm) {
+            L.norm_w = reinterpret_cast<const float*>(weights->base + fuse[i].norm_w_off);
+            L.norm_eps = fuse[i].norm_eps;
+        }
+        if ((L.fuse & ql::kFuseGlu) && L.src2 < 0) L.x2 = reinterpret_cast<const float*>(act->base + fuse[i].x2_off);
+        if ((L.fuse & ql::kFuseRes) && L.res_src < 0) L.res = reinterpret_cast<const float*>(act->base + fuse[i].res_off);
     }
     hipError_t e = hipMemset(dev, 0, lay.total);
     if (e == hipSuccess && lay.sym_words)
@@ -1439,9 +1535,26 @@ int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
     a.group = descs[0].group;
     a.spin_limit = 1u << 22;
     a.block_mode = p.block_mode ? 1 : 0;
+    a.fused = fused ? 1 : 0;
     fill_seq_info(p, n, lay.total, &q->info);
     *out = q;
     return QL_OK;
+}
+
+}  // namespace
+
+int ql_seq_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights,
+                  ql_arena* act, const uint64_t* x_offs, int32_t x_dtype, int32_t M,
+                  const uint64_t* y_offs, ql_seq** out)
+{
+    return seq_create_impl(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, nullptr, out);
+}
+
+int ql_seq_create_fused(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights,
+                        ql_arena* act, const uint64_t* x_offs, int32_t x_dtype, int32_t M,
+                        const uint64_t* y_offs, const ql_seq_fuse* fuse, ql_seq** out)
+{
+    return seq_create_impl(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, fuse, out);
 }
 
 int ql_seq_get_info(const ql_seq* seq, ql_seq_info* info)

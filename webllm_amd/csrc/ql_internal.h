@@ -222,6 +222,11 @@ constexpr uint32_t kSeqErrTimeout = 1;
 constexpr int kSeqBiasBlocks = 64;    // most blocks of a tile that adds a bias (staged in LDS)
 
 // Device table entry per linear (read-only in the kernel).
+// Elementwise work folded into a sequence linear (SeqLinear::fuse bits).
+constexpr int kFuseNorm = 1;   // x -> rmsnorm(x) * norm_w at staging
+constexpr int kFuseGlu = 2;    // x -> silu(x) * x2 at staging
+constexpr int kFuseRes = 4;    // y -> y + res in the epilogue
+
 struct SeqLinear {
     const uint32_t* qweight;
     const uint32_t* qzeros;    // never null: symmetric linears point at stored-7 words
@@ -232,6 +237,13 @@ struct SeqLinear {
     uint64_t* y_ll;            // output again as (value bits | epoch << 32) for consumers
     int32_t src;               // producer linear (its y is this linear's x), or -1
     int32_t N, K, x_dtype;
+    // fused elementwise work (fuse == 0: none)
+    const float* norm_w;       // RMSNorm weight [K] (kFuseNorm)
+    const float* x2;           // external second GLU operand [M, K], f32 (kFuseGlu, src2 < 0)
+    const float* res;          // external residual [M, N], f32 (kFuseRes, res_src < 0)
+    int32_t src2, res_src;     // producer linears of x2 and res, or -1
+    int32_t fuse;
+    float norm_eps;
 };
 
 // One unit of work, run by one workgroup in list order.
@@ -260,6 +272,7 @@ struct SeqArgs {
     int32_t M, G, group;
     uint32_t spin_limit;
     int32_t block_mode;             // some tile runs in block mode: launch the instance with it
+    int32_t fused;                  // some linear has fused elementwise work: the instance with it
 };
 
 // Host description of one linear of a sequence, for planning.
@@ -267,6 +280,8 @@ struct SeqSpec {
     int N, K, group, src;
     bool has_qzeros, has_bias;
     uint64_t weight_bytes;
+    int src2 = -1, res_src = -1;    // producers of the GLU operand and the residual, or -1
+    int fuse = 0;                   // kFuse* bits
 };
 
 struct SeqPlanOut {
@@ -290,7 +305,7 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
 std::string verify_seq_plan(const std::vector<SeqSpec>& lin, int M, const SeqPlanOut& p);
 size_t seq_lds_budget(int M, int group);   // dynamic LDS a sequence may use per workgroup
 // Workgroups of the sequence kernel that fit on one CU at once.
-hipError_t seq_blocks_per_cu(int M, int group, int* blocks);
+hipError_t seq_blocks_per_cu(int M, int group, bool fused, int* blocks);
 int seq_wg_per_cu();
 hipError_t launch_seq(const SeqArgs& a, size_t lds, hipStream_t stream);
 

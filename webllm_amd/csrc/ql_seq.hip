@@ -255,7 +255,7 @@ struct FetchSrc {
     int b0, bs;                 // the wave's first block of the tile and its block step
 };
 
-template <int T, int NB, int RG, int kP, int W, bool BMODE>
+template <int T, int NB, int RG, int kP, int W, bool BMODE, bool FU>
 __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
 {
     constexpr int kThreads = 64 * W;
@@ -273,6 +273,9 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
     __shared__ float bias_lds[kSeqBiasBlocks * kCols];
     __shared__ uint32_t sh_epoch;
     __shared__ int sh_bad;
+    // fused RMSNorm: the rows' sums of squares by wave, then 1/rms per row
+    __shared__ float sh_ss[FU ? W : 1][FU ? 4 * T : 1];
+    __shared__ float sh_rstd[FU ? 4 * T : 1];
 
     const int wg = blockIdx.x;
     const int lane = threadIdx.x & 63;
@@ -327,6 +330,20 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         f.ct = t.ct;
         f.nblk = t.nblk;
         return f;
+    };
+
+    // Fused residual of output (m, n) of linear L: an external input or a producer's output word
+    // (waited for like any input; the producer ran in an earlier pass).
+    auto residual = [&](const SeqLinear& L, int m, int n, int N, uint32_t e, bool& ok) -> float {
+        if (L.res_src < 0) return ld_global(L.res + (size_t)m * N + n);
+        const uint64_t* w = uniform_ptr(ld_const(&a.lin[L.res_src].y_ll)) + (size_t)m * N + n;
+        uint64_t v = ld_ll(w);
+        uint32_t polls = 0;
+        while ((uint32_t)(v >> 32) != e && ok) {
+            if (!keep_waiting(a, polls)) ok = false;
+            else v = ld_ll(w);
+        }
+        return __uint_as_float((uint32_t)v);
     };
 
     // Software pipeline over each wave's job stream. In a tile, the wave's job k is block
@@ -475,6 +492,8 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                                            e, a, &sum);
                 if (!ok) continue;
                 if (L.bias) sum += ld_global(L.bias + nn);
+                if constexpr (FU)
+                    if (L.fuse & kFuseRes) sum += residual(L, m, nn, N, e, ok);
                 st_global(L.y + (size_t)m * N + nn, sum);
                 st_ll(L.y_ll + (size_t)m * N + nn, sum, e);
             }
@@ -493,6 +512,11 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         const int nbw = !bmode ? task.nblk : wave < task.nblk ? (task.nblk - 1 - wave) / W + 1 : 0;
         const bool P = L.src >= 0;
         const uint64_t* p_ll = P ? ld_const(&a.lin[L.src].y_ll) : nullptr;
+        // fused staging: x -> rmsnorm(x) * w (NORM) or silu(x) * x2 (GLU)
+        const bool NORM = FU && (L.fuse & kFuseNorm);
+        const bool GLU = FU && (L.fuse & kFuseGlu);
+        const bool P2 = GLU && L.src2 >= 0;
+        const uint64_t* p2_ll = P2 ? ld_const(&a.lin[L.src2].y_ll) : nullptr;
         // this tile's and the next tile's views, read now so that their table loads overlap the
         // prologue (without a next tile the stream's tail re-reads this tile)
         const FetchSrc cs = src_of(ti);
@@ -501,15 +525,53 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         // the segment's activation digits (shared by all blocks of the tile), from the external
         // input or from the producer's output words: wave 0 first waits for one word of each
         // 64-value chunk of the segment (one producer block's columns)
-        if (P && QL_SEQ_SENTINEL) {
+        if ((P || P2) && QL_SEQ_SENTINEL) {
             if (wave == 0) {
-                const int c0 = task.g0 * GK / kCols;
-                const int c1 = task.g1 * GK / kCols;
-                ok = wait_words(p_ll + (size_t)c0 * kCols, kCols, c1 - c0, lane, e, a);
+                // a normalized input needs its whole row (the sum of squares)
+                const int c0 = NORM ? 0 : task.g0 * GK / kCols;
+                const int c1 = NORM ? L.K / kCols : task.g1 * GK / kCols;
+                if (P) ok = wait_words(p_ll + (size_t)c0 * kCols, kCols, c1 - c0, lane, e, a);
+                if (P2 && ok) ok = wait_words(p2_ll + (size_t)c0 * kCols, kCols, c1 - c0, lane, e, a);
             }
             if (!ok) sh_bad = 1;
             __syncthreads();
             if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
+        }
+        if constexpr (FU) {
+            if (NORM) {
+                // rows' sums of squares: thread t takes 8-value chunks t, t + kThreads, ... of each
+                // row; lanes, then waves, add in a fixed order (runs repeat bit for bit)
+                const int cpr = L.K / 8;
+                for (int m = 0; m < M; m++) {
+                    float ss = 0.f;
+                    for (int c = threadIdx.x; c < cpr; c += kThreads) {
+                        const size_t xo = (size_t)m * L.K + (size_t)c * 8;
+                        float v[8];
+                        if (P) {
+                            uint64_t w[8];
+                            issue8_ll(p_ll + xo, w);
+                            if (ok) ok = finish8_ll(p_ll + xo, e, w, v, a);
+                            if (!ok) break;
+                        } else {
+                            load8(L.x, L.x_dtype, xo, v);
+                        }
+#pragma unroll
+                        for (int k = 0; k < 8; k++) ss = fmaf(v[k], v[k], ss);
+                    }
+#pragma unroll
+                    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+                    if (lane == 0) sh_ss[wave][m] = ss;
+                }
+                if (!ok) sh_bad = 1;
+                __syncthreads();
+                if (threadIdx.x < M) {
+                    double t = 0.0;
+                    for (int w = 0; w < W; w++) t += (double)sh_ss[w][threadIdx.x];
+                    sh_rstd[threadIdx.x] = (float)(1.0 / sqrt(t / (double)L.K + (double)L.norm_eps));
+                }
+                __syncthreads();
+                if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
+            }
         }
         uint4* xd = dyn_lds;
         float2* gst = reinterpret_cast<float2*>(dyn_lds + gseg * NB * 4 * R);
@@ -541,6 +603,24 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                         else load8(L.x, L.x_dtype, xo[h], v[h]);
                     }
                 }
+                // the fused second operand (GLU) and norm weights of the same chunks
+                uint64_t w2[FU ? H : 1][8];
+                float v2[FU ? H : 1][8];
+                if constexpr (FU) {
+#pragma unroll
+                    for (int h = 0; h < H; h++) {
+                        if (!live[h]) continue;
+                        if (P2) issue8_ll(p2_ll + xo[h], w2[h]);
+                        else if (GLU) load8(L.x2, 0, xo[h], v2[h]);
+                        else if (NORM) {
+                            const int idx = base + kThreads * h + threadIdx.x;
+                            const int item = idx / CPG;
+                            const int c = idx - item * CPG;
+                            const int gg = item / M;
+                            load8(L.norm_w, 0, (size_t)(task.g0 + gg) * GK + (size_t)c * 8, v2[h]);
+                        }
+                    }
+                }
 #pragma unroll
                 for (int h = 0; h < H; h++) {
                     const int idx = base + kThreads * h + threadIdx.x;
@@ -554,6 +634,24 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                         if (!ok) {
 #pragma unroll
                             for (int k = 0; k < 8; k++) v[h][k] = 0.f;
+                        }
+                    }
+                    if constexpr (FU) {
+                        if (P2) {
+                            if (ok) ok = finish8_ll(p2_ll + xo[h], e, w2[h], v2[h], a);
+                            if (!ok) {
+#pragma unroll
+                                for (int k = 0; k < 8; k++) v2[h][k] = 0.f;
+                            }
+                        }
+                        if (GLU) {
+                            // siluMulRef: silu(g) * u = g / (1 + exp(-g)) * u
+#pragma unroll
+                            for (int k = 0; k < 8; k++) v[h][k] = v[h][k] / (1.f + expf(-v[h][k])) * v2[h][k];
+                        } else if (NORM) {
+                            const float r = sh_rstd[m];
+#pragma unroll
+                            for (int k = 0; k < 8; k++) v[h][k] = v[h][k] * r * v2[h][k];
                         }
                     }
                     const int blk = gg * NB + (c >> 3);
@@ -659,6 +757,8 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                         for (int w = 1; w < W; w++) v += red[rs][w][m][lane];
                         if (task.slot < 0) {
                             if (L.bias) v += bias_lds[b * kCols + lane];
+                            if constexpr (FU)
+                                if (L.fuse & kFuseRes) v += residual(L, m, ncol, N, e, ok);
                             st_global(L.y + (size_t)m * N + ncol, v);
                             st_ll(L.y_ll + (size_t)m * N + ncol, v, e);
                         } else {
@@ -695,6 +795,8 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                     if (nc >= N) continue;
                     if (task.slot < 0) {
                         if (L.bias) v += bias_lds[b * kCols + lane];
+                        if constexpr (FU)
+                            if (L.fuse & kFuseRes) v += residual(L, m, nc, N, e, ok);
                         st_global(L.y + (size_t)m * N + nc, v);
                         st_ll(L.y_ll + (size_t)m * N + nc, v, e);
                     } else {
@@ -762,7 +864,7 @@ struct SeqKernel {
 // Eight waves per workgroup (one workgroup per CU) where two waves per SIMD fit the registers:
 // a single workgroup keeps its waves in step through the per-block barriers, where two
 // co-resident workgroups drift apart (the older one's waves win issue). Otherwise four waves.
-template <int T, bool BM>
+template <int T, bool BM, bool FU>
 SeqKernel kernel_for(int nb)
 {
     constexpr int RG = T == 1 ? 4 : 2;      // reduction ring slots (32 KB of LDS with 8 waves)
@@ -770,19 +872,25 @@ SeqKernel kernel_for(int nb)
     constexpr int P = T == 4 ? QL_SEQ_PREFETCH_WIDE : QL_SEQ_PREFETCH;
     constexpr int W = T <= 2 ? QL_SEQ_WAVES : 4;
     switch (nb) {
-    case 1: return {reinterpret_cast<const void*>(&seq_kernel<T, 1, RG, P, W, BM>), 64 * W};
-    case 2: return {reinterpret_cast<const void*>(&seq_kernel<T, 2, RG, P, W, BM>), 64 * W};
-    case 4: return {reinterpret_cast<const void*>(&seq_kernel<T, 4, RG, QL_SEQ_PREFETCH, 4, BM>), 256};
+    case 1: return {reinterpret_cast<const void*>(&seq_kernel<T, 1, RG, P, W, BM, FU>), 64 * W};
+    case 2: return {reinterpret_cast<const void*>(&seq_kernel<T, 2, RG, P, W, BM, FU>), 64 * W};
+    case 4: return {reinterpret_cast<const void*>(&seq_kernel<T, 4, RG, QL_SEQ_PREFETCH, 4, BM, FU>), 256};
     default: return {nullptr, 0};
     }
 }
 
-SeqKernel seq_kernel_for(int M, int group, bool bmode = false)
+template <bool FU>
+SeqKernel seq_kernel_for_fu(int M, int group, bool bmode)
 {
     const int nb = group / 64;
-    if (M <= 4) return bmode ? kernel_for<1, true>(nb) : kernel_for<1, false>(nb);
-    if (M <= 8) return bmode ? kernel_for<2, true>(nb) : kernel_for<2, false>(nb);
-    return bmode ? kernel_for<4, true>(nb) : kernel_for<4, false>(nb);
+    if (M <= 4) return bmode ? kernel_for<1, true, FU>(nb) : kernel_for<1, false, FU>(nb);
+    if (M <= 8) return bmode ? kernel_for<2, true, FU>(nb) : kernel_for<2, false, FU>(nb);
+    return bmode ? kernel_for<4, true, FU>(nb) : kernel_for<4, false, FU>(nb);
+}
+
+SeqKernel seq_kernel_for(int M, int group, bool bmode = false, bool fused = false)
+{
+    return fused ? seq_kernel_for_fu<true>(M, group, bmode) : seq_kernel_for_fu<false>(M, group, bmode);
 }
 
 }  // namespace
@@ -938,7 +1046,11 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
     const int n = (int)lin.size();
     p.pass_of.assign(n, 0);
     for (int i = 0; i < n; i++) {
-        p.pass_of[i] = lin[i].src >= 0 ? p.pass_of[lin[i].src] + 1 : 0;
+        // after every producer the linear reads: its input, the GLU operand, the residual
+        int pass = 0;
+        for (const int src : {lin[i].src, lin[i].src2, lin[i].res_src})
+            if (src >= 0) pass = std::max(pass, p.pass_of[src] + 1);
+        p.pass_of[i] = pass;
         p.passes = std::max(p.passes, p.pass_of[i] + 1);
     }
     std::vector<std::vector<SeqTask>> per_wg(grid);
@@ -1330,12 +1442,12 @@ std::string verify_seq_plan(const std::vector<SeqSpec>& lin, int M, const SeqPla
     return "";
 }
 
-hipError_t seq_blocks_per_cu(int M, int group, int* blocks)
+hipError_t seq_blocks_per_cu(int M, int group, bool fused, int* blocks)
 {
     // the smaller occupancy of the two instances (with and without block mode)
     int b[2] = {0, 0};
     for (int i = 0; i < 2; i++) {
-        const SeqKernel k = seq_kernel_for(M, group, i == 1);
+        const SeqKernel k = seq_kernel_for(M, group, i == 1, fused);
         if (!k.fn) return hipErrorInvalidValue;
         const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b[i], k.fn, k.threads, lds_budget(M, group));
         if (e != hipSuccess) return e;
@@ -1348,7 +1460,7 @@ int seq_wg_per_cu() { return QL_SEQ_WG_PER_CU; }
 
 hipError_t launch_seq(const SeqArgs& a, size_t lds, hipStream_t stream)
 {
-    const SeqKernel k = seq_kernel_for(a.M, a.group, a.block_mode != 0);
+    const SeqKernel k = seq_kernel_for(a.M, a.group, a.block_mode != 0, a.fused != 0);
     if (!k.fn) return hipErrorInvalidValue;
     void* args[] = {const_cast<SeqArgs*>(&a)};
     return hipLaunchKernel(k.fn, dim3(a.G), dim3(k.threads), args, lds, stream);

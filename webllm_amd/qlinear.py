@@ -48,6 +48,21 @@ class GptqDesc(ctypes.Structure):
                 ("bits", ctypes.c_int32)]
 
 
+class SeqFuse(ctypes.Structure):
+    """Elementwise work folded into one linear of a fused sequence (ql_seq_fuse): RMSNorm of x
+    (norm weight in the weights arena), silu(x) * x2, and a residual added to y; offsets of
+    another linear's output make that linear a producer."""
+    _fields_ = [("norm_w_off", ctypes.c_uint64), ("x2_off", ctypes.c_uint64),
+                ("res_off", ctypes.c_uint64), ("norm_eps", ctypes.c_float),
+                ("reserved", ctypes.c_int32)]
+
+
+def make_fuse(norm_w_off: int | None = None, norm_eps: float = 1e-6, x2_off: int | None = None,
+              res_off: int | None = None) -> SeqFuse:
+    return SeqFuse(QL_NONE if norm_w_off is None else norm_w_off, QL_NONE if x2_off is None else x2_off,
+                   QL_NONE if res_off is None else res_off, norm_eps, 0)
+
+
 class Plan(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_int32), ("split", ctypes.c_int32), ("waves", ctypes.c_int32),
                 ("grid_x", ctypes.c_int32), ("grid_y", ctypes.c_int32), ("block", ctypes.c_int32),
@@ -138,6 +153,10 @@ def lib():
                             ctypes.POINTER(U64), I, ctypes.POINTER(SeqInfo)]),
         "ql_seq_create": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64), I, I,
                               ctypes.POINTER(U64), pp]),
+        "ql_plan_seq_fused": (I, [I, ctypes.POINTER(GptqDesc), I, ctypes.POINTER(U64), I,
+                                  ctypes.POINTER(U64), ctypes.POINTER(SeqFuse), I, ctypes.POINTER(SeqInfo)]),
+        "ql_seq_create_fused": (I, [P, I, ctypes.POINTER(GptqDesc), P, P, ctypes.POINTER(U64), I, I,
+                                    ctypes.POINTER(U64), ctypes.POINTER(SeqFuse), pp]),
         "ql_seq_get_info": (I, [P, ctypes.POINTER(SeqInfo)]),
         "ql_seq_run": (I, [P, P]),
         "ql_seq_status": (I, [P, P]),
@@ -177,12 +196,19 @@ def plan_batch(descs: list[GptqDesc], M: int) -> int:
 
 
 def plan_seq(descs: list[GptqDesc], M: int, x_offs, y_offs, grid: int,
-             x_dtype: int = DTYPE_F32) -> SeqInfo:
+             x_dtype: int = DTYPE_F32, fuse: list[SeqFuse] | None = None) -> SeqInfo:
     """Validation and plan figures of a linear sequence for `grid` workgroups (host only)."""
     n = len(descs)
     info = SeqInfo()
-    _check(lib().ql_plan_seq(n, (GptqDesc * n)(*descs), M, (ctypes.c_uint64 * n)(*x_offs), x_dtype,
-                             (ctypes.c_uint64 * n)(*y_offs), grid, ctypes.byref(info)))
+    if fuse is None:
+        _check(lib().ql_plan_seq(n, (GptqDesc * n)(*descs), M, (ctypes.c_uint64 * n)(*x_offs), x_dtype,
+                                 (ctypes.c_uint64 * n)(*y_offs), grid, ctypes.byref(info)))
+    else:
+        if len(fuse) != n:
+            raise ValueError(f"fuse has {len(fuse)} entries for {n} linears")
+        _check(lib().ql_plan_seq_fused(n, (GptqDesc * n)(*descs), M, (ctypes.c_uint64 * n)(*x_offs), x_dtype,
+                                       (ctypes.c_uint64 * n)(*y_offs), (SeqFuse * n)(*fuse), grid,
+                                       ctypes.byref(info)))
     return info
 
 
@@ -254,12 +280,20 @@ class Seq:
     x_offs[i] == y_offs[j] (src/gpu/pipeline.ts:71-116 CommandBatch with passBreak)."""
 
     def __init__(self, ctx: "Context", descs: list[GptqDesc], weights: Arena, act: Arena, x_offs,
-                 x_dtype: int, M: int, y_offs):
+                 x_dtype: int, M: int, y_offs, fuse: list[SeqFuse] | None = None):
         n = len(descs)
         h = ctypes.c_void_p()
-        _check(lib().ql_seq_create(ctx.handle, n, (GptqDesc * n)(*descs), weights.handle,
-                                   act.handle, (ctypes.c_uint64 * n)(*x_offs), x_dtype, M,
-                                   (ctypes.c_uint64 * n)(*y_offs), ctypes.byref(h)))
+        if fuse is None:
+            _check(lib().ql_seq_create(ctx.handle, n, (GptqDesc * n)(*descs), weights.handle,
+                                       act.handle, (ctypes.c_uint64 * n)(*x_offs), x_dtype, M,
+                                       (ctypes.c_uint64 * n)(*y_offs), ctypes.byref(h)))
+        else:
+            if len(fuse) != n:
+                raise ValueError(f"fuse has {len(fuse)} entries for {n} linears")
+            _check(lib().ql_seq_create_fused(ctx.handle, n, (GptqDesc * n)(*descs), weights.handle,
+                                             act.handle, (ctypes.c_uint64 * n)(*x_offs), x_dtype, M,
+                                             (ctypes.c_uint64 * n)(*y_offs), (SeqFuse * n)(*fuse),
+                                             ctypes.byref(h)))
         self.ctx = ctx
         self.handle = h
         ctx._owned.add(self)
@@ -379,8 +413,8 @@ class Context:
                                      M, yo, scratch_off))
 
     def seq(self, descs: list[GptqDesc], weights: Arena, act: Arena, x_offs, x_dtype: int, M: int,
-            y_offs) -> Seq:
-        return Seq(self, descs, weights, act, x_offs, x_dtype, M, y_offs)
+            y_offs, fuse: list[SeqFuse] | None = None) -> Seq:
+        return Seq(self, descs, weights, act, x_offs, x_dtype, M, y_offs, fuse)
 
     def sync(self):
         _check(lib().ql_sync(self.handle))
