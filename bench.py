@@ -49,6 +49,7 @@ LAYER_LAUNCHES_7B = [("q",), ("o",), ("gate", "up"), ("down",)]
 SEQ_LAYER_05B = [("q", None), ("k", None), ("v", None), ("o", "q"), ("gate", "o"), ("up", "o"),
                  ("down", "gate")]
 SEQ_LAYER_7B = [("q", None), ("o", "q"), ("gate", "o"), ("up", "o"), ("down", "gate")]
+NORM_EPS = 1e-6          # Qwen2.5's rms_norm_eps
 
 
 def log(*a):
@@ -79,7 +80,14 @@ class Model:
             qw, qz, sc = ql.gptq_sizes(K, N, GROUP)
             offs = (lay.take(qw), lay.take(qz), lay.take(sc))
             plan.append((layer, proj, K, N, offs))
+        # the layers' RMSNorm weights (before q/k/v and before gate/up), fp32 [C] each:
+        # 1 + 0.1 N(0,1) stands in for trained values near 1
+        C = self.linears[0][2]
+        self.norm_offs = {(layer, k): lay.take(C * 4) for layer in range(self.layers) for k in range(2)}
         self.arena = ctx.arena(lay.used)
+        for (layer, k), off in self.norm_offs.items():
+            w = 1.0 + 0.1 * synth.activations(1, C, seed=seed + 3, key=(layer, k))[0]
+            self.arena.write(off, w.astype(np.float32))
         self.weight_bytes = 0
         for (layer, proj, K, N, offs) in plan:
             t = synth.gptq_linear(K, N, GROUP, seed=seed, key=(layer, synth.PROJ_INDEX[proj]))
@@ -172,12 +180,14 @@ class Step:
 
 
 class SeqStep:
-    """The decode step as ONE persistent launch (ql_seq_*): the linears chained through their
-    outputs the way a layer consumes them — (q,k,v) <- h, o <- q, (gate,up) <- o, down <- gate,
-    next layer's h <- down — so each linear waits on the device for the one it reads, as after a
-    pass break in the reference (src/model/qwen.ts:556-559). Attention and the elementwise ops
-    between linears are outside the sequence (o reads q in attention's place, down reads gate in
-    SiLU(gate)*up's place); every one of the model's linears runs, with its real dependency."""
+    """The decode step as ONE persistent launch (ql_seq_*).
+
+    chained=False: the benchmark config as written, every linear on its own input (strips).
+    chained=True: the layer's data flow (src/model/qwen.ts:398-482) with its elementwise work
+    folded into the launch (ql_seq_create_fused): q/k/v <- rmsnorm(h); h1 = h + o(q) (o reads q
+    in attention's place); gate/up <- rmsnorm(h1); h2 = h1 + down(silu(gate) * up); the next
+    layer's h = h2. Each linear waits on the device for what it reads, as after a pass break in
+    the reference (qwen.ts:556-559)."""
 
     def __init__(self, ctx, model: Model, M: int, seed: int = 0x5EED, chained: bool = True):
         self.ctx, self.model, self.M, self.x_dtype = ctx, model, M, ql.DTYPE_F32
@@ -190,12 +200,24 @@ class SeqStep:
         h0 = lay.take(M * C * 4)
         inputs.append((h0, C, (0, 0, M)))
         h = h0
+        fuse = []
         for layer in range(model.layers):
             y = {}
             for i, (proj, src) in enumerate(SEQ_LAYER_05B if model.shape == "0.5b" else SEQ_LAYER_7B):
                 d = model.descs[(layer, proj)]
                 if chained:
-                    x_off = h if src is None else y[src]
+                    if proj in ("q", "k", "v"):
+                        x_off = h
+                        fuse.append(ql.make_fuse(norm_w_off=model.norm_offs[(layer, 0)], norm_eps=NORM_EPS))
+                    elif proj == "o":
+                        x_off = y["q"]
+                        fuse.append(ql.make_fuse(res_off=h))
+                    elif proj in ("gate", "up"):
+                        x_off = y["o"]
+                        fuse.append(ql.make_fuse(norm_w_off=model.norm_offs[(layer, 1)], norm_eps=NORM_EPS))
+                    else:
+                        x_off = y["gate"]
+                        fuse.append(ql.make_fuse(x2_off=y["up"], res_off=y["o"]))
                 else:
                     # the benchmark configs as written: every linear has its own x ~ N(0,1)
                     x_off = h0 if layer == 0 and i == 0 else lay.take(M * d.K * 4)
@@ -211,7 +233,8 @@ class SeqStep:
         for off, K, key in inputs:
             self.act.write(off, synth.activations(M, K, seed=seed, key=key))
         self.x_offs, self.y_offs = xs, ys
-        self.seq = ctx.seq(descs, model.arena, self.act, xs, ql.DTYPE_F32, M, ys)
+        self.fuse = fuse if chained else None
+        self.seq = ctx.seq(descs, model.arena, self.act, xs, ql.DTYPE_F32, M, ys, fuse=self.fuse)
         self.info = self.seq.info
         self.bytes = sum(linear_bytes(model.shapes[lp][0], model.shapes[lp][1], M) for lp in self.order)
         self.flops = sum(2 * M * model.shapes[lp][0] * model.shapes[lp][1] for lp in self.order)
@@ -228,6 +251,13 @@ class SeqStep:
         self.ctx.graph_begin()
         self.seq.run()
         self.graph = self.ctx.graph_end()
+
+    def finite(self) -> bool:
+        """Every output of the last run is finite (a chained step carries its values across all
+        layers)."""
+        self.ctx.sync()
+        return all(bool(np.isfinite(self.act.read(yo, (self.M, self.model.shapes[lp][1]), np.float32)).all())
+                   for yo, lp in zip(self.y_offs, self.order))
 
     def kernel_ms(self, reps: int, per_graph: int = 10) -> float:
         """Device time per launch with the replay gap amortized: a graph of `per_graph`
@@ -599,9 +629,11 @@ def main():
         extra["step05_m1_chained"] = {
             "us": round(ms * 1e3, 1), "gbs": round(ch.bytes / (ms * 1e-3) / 1e9, 1),
             "passes": ch.info.passes, "tiles": ch.info.tiles, "reduces": ch.info.reduces,
-            "note": "the same 168 linears chained through their outputs as a layer consumes "
-                    "them ((q,k,v) <- h, o <- q, (gate,up) <- o, down <- gate): 96 dependent "
-                    "passes ordered on the device in one launch"}
+            "finite": ch.finite(),
+            "note": "the same 168 linears as a layer consumes them, with the layer's elementwise "
+                    "work folded into the one launch: (q,k,v) <- rmsnorm(h), h1 = h + o(q), "
+                    "(gate,up) <- rmsnorm(h1), h2 = h1 + down(silu(gate) * up); 96 dependent "
+                    "passes ordered on the device (o reads q in attention's place)"}
         log(f"0.5B step M=1 chained: {ms*1e3:.1f} us")
         ch.release()
         st = Step(ctx, m05, 1)
@@ -841,6 +873,8 @@ def main():
                     "roofline_us": round(roof_us, 1), "target_us_70pct": round(roof_us / 0.7, 1),
                     "launches": 1, "passes": st.info.passes, "tiles": st.info.tiles,
                     "reduces": st.info.reduces}
+                if chained:
+                    s7[f"{M}_chained"]["finite"] = st.finite()
                 st.release()
         st = Step(ctx, m7, 1)
         ms = timed(st, max(10, args.steps // 2), 2)

@@ -180,3 +180,71 @@ def test_fused_layer_7b(ql, ctx, orc, M):
     m.seq.status()
     check_fused(orc, m, m.outputs(), f"fused 7B M={M}", cols_for=_sample)
     m.release()
+
+
+def check_step(orc, model, st, cols_for, label):
+    """A chained bench step (bench.SeqStep(chained=True)): every linear against the oracle's
+    composition on the inputs the GPU used, its fusion read from the step's own fuse list."""
+    ql_none = (1 << 64) - 1
+    y_of = {yo: i for i, yo in enumerate(st.y_offs)}
+    ys = [st.act.read(yo, (st.M, model.shapes[lp][1]), np.float32) for yo, lp in zip(st.y_offs, st.order)]
+
+    def value(off, width):
+        return ys[y_of[off]] if off in y_of else st.act.read(off, (st.M, width), np.float32)
+
+    worst = 0.0
+    for i, (lp, f) in enumerate(zip(st.order, st.fuse)):
+        K, N = model.shapes[lp]
+        t = model.tensors[lp]
+        x = value(st.x_offs[i], K)
+        if f.norm_w_off != ql_none:
+            w = model.arena.read(f.norm_w_off, (K,), np.float32)
+            x = orc.add_rmsnorm(x, w, f.norm_eps)[1]
+        if f.x2_off != ql_none:
+            x = orc.silu_mul(x, value(f.x2_off, K))
+        cols = cols_for(N)
+        ref = orc.gptq_linear_cols(t.qweight, t.qzeros, t.scales, x, cols, None, 128)
+        if f.res_off != ql_none:
+            ref = ref + value(f.res_off, N)[:, cols]
+        got = np.ascontiguousarray(ys[i][:, cols])
+        atol = 1e-5 * max(1.0, float(np.sqrt(np.mean(x.astype(np.float64) ** 2))))
+        ok, max_abs, max_rel = orc.check_tolerance(got, ref, atol, RTOL)
+        assert np.isfinite(ys[i]).all(), f"{label} linear {i} {lp}: non-finite output"
+        worst = max(worst, float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)))
+        assert ok, f"{label} linear {i} {lp}: maxAbs {max_abs:.3e} (atol {atol:.2e}) maxRel {max_rel:.3e}"
+    say(f"  {label}: {len(ys)} linears within bar, worst normwise {worst:.3e}")
+
+
+@pytest.fixture(scope="module")
+def bench_mod():
+    import bench
+    return bench
+
+
+def test_chained_step_05b_full_size(ql, ctx, orc, bench_mod):
+    """The bench's chained 0.5B step (24 fused layers, 96 passes, one launch) at M=1: every
+    linear's every column against the oracle; the values stay finite to the last layer."""
+    model = bench_mod.Model(ctx, "0.5b", seed=0x9EF0, keep_tensors=True)
+    st = bench_mod.SeqStep(ctx, model, 1, chained=True)
+    say(f"chained 0.5B step: {st.info.as_dict()}")
+    assert st.info.kernel == ql.SEQ_TILES and st.info.passes == 96 and st.info.linears == 168
+    st.run(2)
+    assert st.finite()
+    check_step(orc, model, st, lambda N: np.arange(N, dtype=np.int32), "chained 0.5B M=1")
+    st.release()
+    model.arena.release()
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_chained_step_7b_full_size(ql, ctx, orc, bench_mod, M):
+    """The bench's chained 7B step (28 fused layers, 112 passes, 3.35 GB, one launch): every
+    linear on a sample of 64-column blocks; finite to the last layer."""
+    model = bench_mod.Model(ctx, "7b", seed=0x7B, keep_tensors=True)
+    st = bench_mod.SeqStep(ctx, model, M, chained=True)
+    say(f"chained 7B step M={M}: {st.info.as_dict()}")
+    assert st.info.kernel == ql.SEQ_TILES and st.info.passes == 112
+    st.run(2)
+    assert st.finite()
+    check_step(orc, model, st, _sample, f"chained 7B M={M}")
+    st.release()
+    model.arena.release()

@@ -399,7 +399,8 @@ bool seq_fused(const std::vector<ql::SeqSpec>& specs)
 // Device memory of a planned sequence, laid out in one allocation.
 struct SeqLayout {
     std::vector<uint64_t> y_ll;
-    uint64_t lin, tasks, task_begin, first_tile, tickets, words, sym_zeros, sym_words, part, total;
+    std::vector<uint64_t> ssq;      // per linear, or UINT64_MAX when no consumer normalizes it
+    uint64_t lin, fl, tasks, task_begin, first_tile, tickets, words, sym_zeros, sym_words, part, total;
 };
 
 SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut& p, int M)
@@ -413,6 +414,7 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
     };
     const int n = (int)specs.size();
     L.lin = take(sizeof(ql::SeqLinear) * n);
+    L.fl = seq_fused(specs) ? take(sizeof(ql::SeqFuseLin) * n) : UINT64_MAX;
     L.tasks = take(sizeof(ql::SeqTask) * std::max<size_t>(1, p.tasks.size()));
     L.task_begin = take(sizeof(int32_t) * (p.grid + 1));
     L.first_tile = take(sizeof(int32_t) * p.grid);
@@ -426,6 +428,13 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
                                                               ((specs[i].N + 7) / 8));
     L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
     for (int i = 0; i < n; i++) L.y_ll.push_back(take((uint64_t)M * specs[i].N * 8));
+    // block sums of squares of every output that a fused RMSNorm reads
+    L.ssq.assign(n, UINT64_MAX);
+    for (int c = 0; c < n; c++)
+        if ((specs[c].fuse & ql::kFuseNorm) && specs[c].src >= 0 && L.ssq[specs[c].src] == UINT64_MAX) {
+            const int i = specs[c].src;
+            L.ssq[i] = take((uint64_t)M * ((specs[i].N + ql::kSeqTileCols - 1) / ql::kSeqTileCols) * 8);
+        }
     L.part = take(std::max<uint64_t>(1, p.slots) * (uint64_t)M * ql::kSeqTileCols * 8);
     L.total = off;
     return L;
@@ -1471,9 +1480,11 @@ int seq_create_impl(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_
     char* dev = nullptr;
     QL_HIP(hipMalloc(&dev, lay.total));
     std::vector<ql::SeqLinear> lin(n);
+    std::vector<ql::SeqFuseLin> fl(n);
     for (int i = 0; i < n; i++) {
         const ql_gptq_desc* d = &descs[i];
         ql::SeqLinear& L = lin[i];
+        ql::SeqFuseLin& F = fl[i];
         const ql::GemvLinear g = make_linear(d, weights);
         L.qweight = g.qweight;
         L.qzeros = g.qzeros ? g.qzeros : reinterpret_cast<const uint32_t*>(dev + lay.sym_zeros);
@@ -1486,25 +1497,28 @@ int seq_create_impl(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_
         L.N = d->N;
         L.K = d->K;
         L.x_dtype = x_dtype;
-        L.fuse = specs[i].fuse;
-        L.src2 = specs[i].src2;
-        L.res_src = specs[i].res_src;
-        L.norm_w = nullptr;
-        L.x2 = nullptr;
-        L.res = nullptr;
-        L.norm_eps = 0.f;
-        if (L.fuse & ql::kFuseNorm) {
-            L.norm_w = reinterpret_cast<const float*>(weights->base + fuse[i].norm_w_off);
-            L.norm_eps = fuse[i].norm_eps;
+        F.fuse = specs[i].fuse;
+        F.src2 = specs[i].src2;
+        F.res_src = specs[i].res_src;
+        F.norm_w = nullptr;
+        F.x2 = nullptr;
+        F.res = nullptr;
+        F.norm_eps = 0.f;
+        if (F.fuse & ql::kFuseNorm) {
+            F.norm_w = reinterpret_cast<const float*>(weights->base + fuse[i].norm_w_off);
+            F.norm_eps = fuse[i].norm_eps;
         }
-        if ((L.fuse & ql::kFuseGlu) && L.src2 < 0) L.x2 = reinterpret_cast<const float*>(act->base + fuse[i].x2_off);
-        if ((L.fuse & ql::kFuseRes) && L.res_src < 0) L.res = reinterpret_cast<const float*>(act->base + fuse[i].res_off);
+        if ((F.fuse & ql::kFuseGlu) && F.src2 < 0) F.x2 = reinterpret_cast<const float*>(act->base + fuse[i].x2_off);
+        if ((F.fuse & ql::kFuseRes) && F.res_src < 0) F.res = reinterpret_cast<const float*>(act->base + fuse[i].res_off);
+        F.ssq = lay.ssq[i] == UINT64_MAX ? nullptr : reinterpret_cast<uint64_t*>(dev + lay.ssq[i]);
     }
     hipError_t e = hipMemset(dev, 0, lay.total);
     if (e == hipSuccess && lay.sym_words)
         e = hipMemsetD32(reinterpret_cast<hipDeviceptr_t>(dev + lay.sym_zeros), 0x77777777,
                          lay.sym_words);
     if (e == hipSuccess) e = hipMemcpy(dev + lay.lin, lin.data(), sizeof(ql::SeqLinear) * n, hipMemcpyHostToDevice);
+    if (e == hipSuccess && fused)
+        e = hipMemcpy(dev + lay.fl, fl.data(), sizeof(ql::SeqFuseLin) * n, hipMemcpyHostToDevice);
     if (e == hipSuccess && !p.tasks.empty())
         e = hipMemcpy(dev + lay.tasks, p.tasks.data(), sizeof(ql::SeqTask) * p.tasks.size(), hipMemcpyHostToDevice);
     if (e == hipSuccess)
@@ -1536,6 +1550,7 @@ int seq_create_impl(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_
     a.spin_limit = 1u << 22;
     a.block_mode = p.block_mode ? 1 : 0;
     a.fused = fused ? 1 : 0;
+    a.fl = fused ? reinterpret_cast<const ql::SeqFuseLin*>(dev + lay.fl) : nullptr;
     fill_seq_info(p, n, lay.total, &q->info);
     *out = q;
     return QL_OK;

@@ -237,12 +237,18 @@ struct SeqLinear {
     uint64_t* y_ll;            // output again as (value bits | epoch << 32) for consumers
     int32_t src;               // producer linear (its y is this linear's x), or -1
     int32_t N, K, x_dtype;
-    // fused elementwise work (fuse == 0: none)
+};
+
+// A fused sequence linear's elementwise work, in a table of its own beside SeqLinear (read only
+// by the fused kernel instance, where it is needed).
+struct SeqFuseLin {
     const float* norm_w;       // RMSNorm weight [K] (kFuseNorm)
     const float* x2;           // external second GLU operand [M, K], f32 (kFuseGlu, src2 < 0)
     const float* res;          // external residual [M, N], f32 (kFuseRes, res_src < 0)
+    uint64_t* ssq;             // [M][ceil(N/64)] epoch words: sums of squares of the output's
+                               // rows by 64-column block, for a consumer that normalizes it
     int32_t src2, res_src;     // producer linears of x2 and res, or -1
-    int32_t fuse;
+    int32_t fuse;              // kFuse* bits
     float norm_eps;
 };
 
@@ -273,6 +279,7 @@ struct SeqArgs {
     uint32_t spin_limit;
     int32_t block_mode;             // some tile runs in block mode: launch the instance with it
     int32_t fused;                  // some linear has fused elementwise work: the instance with it
+    const SeqFuseLin* fl;           // [n] when fused
 };
 
 // Host description of one linear of a sequence, for planning.

@@ -273,9 +273,8 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
     __shared__ float bias_lds[kSeqBiasBlocks * kCols];
     __shared__ uint32_t sh_epoch;
     __shared__ int sh_bad;
-    // fused RMSNorm: the rows' sums of squares by wave, then 1/rms per row
-    __shared__ float sh_ss[FU ? W : 1][FU ? 4 * T : 1];
-    __shared__ float sh_rstd[FU ? 4 * T : 1];
+    // fused RMSNorm: each wave's 1/rms per row of the current linear's input
+    __shared__ float sh_rstd[FU ? W : 1][FU ? 4 * T : 1];
 
     const int wg = blockIdx.x;
     const int lane = threadIdx.x & 63;
@@ -334,9 +333,10 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
 
     // Fused residual of output (m, n) of linear L: an external input or a producer's output word
     // (waited for like any input; the producer ran in an earlier pass).
-    auto residual = [&](const SeqLinear& L, int m, int n, int N, uint32_t e, bool& ok) -> float {
-        if (L.res_src < 0) return ld_global(L.res + (size_t)m * N + n);
-        const uint64_t* w = uniform_ptr(ld_const(&a.lin[L.res_src].y_ll)) + (size_t)m * N + n;
+    auto residual = [&](const SeqFuseLin* F, int m, int n, int N, uint32_t e, bool& ok) -> float {
+        const int rs = ld_const(&F->res_src);
+        if (rs < 0) return ld_global(uniform_ptr(ld_const(&F->res)) + (size_t)m * N + n);
+        const uint64_t* w = uniform_ptr(ld_const(&a.lin[rs].y_ll)) + (size_t)m * N + n;
         uint64_t v = ld_ll(w);
         uint32_t polls = 0;
         while ((uint32_t)(v >> 32) != e && ok) {
@@ -344,6 +344,71 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             else v = ld_ll(w);
         }
         return __uint_as_float((uint32_t)v);
+    };
+
+    // The sum of squares of one stored row of a 64-column block (lane = column, 0 past N), for a
+    // consumer that normalizes this output: one epoch word per (row, block), added over the
+    // wave's lanes in a fixed order.
+    auto emit_ssq = [&](uint64_t* ssq, int N, int m, int blk, float v, uint32_t e) {
+        float q = v * v;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) q += __shfl_xor(q, o);
+        if (lane == 0) st_ll(ssq + (size_t)m * ((N + kCols - 1) / kCols) + blk, q, e);
+    };
+
+    // Fused RMSNorm: 1/rms of each input row of linear L, computed by the calling wave alone into
+    // sh_rstd[wave] (lane l takes the row's 8-value chunks l, l + 64, ...; the xor butterfly adds
+    // them in a fixed order, so every wave and every run gets the same values). The input is an
+    // external x or the producer's output words, waited for (its pass is an earlier one).
+    auto wave_rstd = [&](const SeqLinear& L, const SeqFuseLin* F, uint32_t e, bool& ok) {
+        const float eps = ld_const(&F->norm_eps);
+        const uint64_t* pss = L.src >= 0 ? ld_const(&a.fl[L.src].ssq) : nullptr;
+        if (pss) {
+            // the producer's sums of squares, one word per (row, 64-column block), in block order
+            pss = uniform_ptr(pss);
+            const int nbk = L.K / kCols;
+            for (int m = 0; m < M; m++) {
+                float ss = 0.f;
+                for (int c = lane; c < nbk && ok; c += 64) {
+                    const uint64_t* w = pss + (size_t)m * nbk + c;
+                    uint64_t v = ld_ll(w);
+                    uint32_t polls = 0;
+                    while ((uint32_t)(v >> 32) != e && ok) {
+                        if (!keep_waiting(a, polls)) ok = false;
+                        else v = ld_ll(w);
+                    }
+                    ss += __uint_as_float((uint32_t)v);
+                }
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+                if (lane == 0) sh_rstd[wave][m] = (float)(1.0 / sqrt((double)ss / (double)L.K + (double)eps));
+            }
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            return;
+        }
+        const uint64_t* pll = L.src >= 0 ? uniform_ptr(ld_const(&a.lin[L.src].y_ll)) : nullptr;
+        const int cpr = L.K / 8;
+        for (int m = 0; m < M; m++) {
+            float ss = 0.f;
+            for (int c = lane; c < cpr && ok; c += 64) {
+                const size_t xo = (size_t)m * L.K + (size_t)c * 8;
+                float v[8];
+                if (pll) {
+                    uint64_t w[8];
+                    issue8_ll(pll + xo, w);
+                    ok = finish8_ll(pll + xo, e, w, v, a);
+                } else {
+                    load8(L.x, L.x_dtype, xo, v);
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++) ss = fmaf(v[k], v[k], ss);
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+            if (lane == 0) sh_rstd[wave][m] = (float)(1.0 / sqrt((double)ss / (double)L.K + (double)eps));
+        }
+        // the wave's own LDS writes precede its reads (in order per wave); keep the compiler too
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
     };
 
     // Software pipeline over each wave's job stream. In a tile, the wave's job k is block
@@ -479,23 +544,43 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             if (!ok) sh_bad = 1;
             __syncthreads();
             if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
-            for (int idx = threadIdx.x; idx < task.nblk * M * kCols; idx += kThreads) {
-                const int b = idx / (M * kCols);
-                const int r = idx - b * (M * kCols);
-                const int m = r / kCols;
-                const int nn = (task.ct + b) * kCols + (r - m * kCols);
-                if (nn >= N || !ok) continue;
+            const SeqFuseLin* F = FU ? a.fl + task.linear : nullptr;
+            const int fz = FU ? ld_const(&F->fuse) : 0;
+            uint64_t* const fssq = FU ? ld_const(&F->ssq) : nullptr;
+            if constexpr (FU)
+                if (fz & kFuseNorm) wave_rstd(L, F, e, ok);
+            // output (m, nn) of block b: its parts added in K order, then the epilogue; stored, and
+            // returned for the block's sum of squares
+            auto reduce_one = [&](int b, int r, int m, int nn) -> float {
                 const uint64_t* src = a.part + (size_t)(task.slot + b * task.stride) * slot_words + r;
                 float sum = 0.f;
                 for (int s0 = 0; s0 < np && ok; s0 += kSumBatch)
                     ok = sum_ll<kSumBatch>(src + (size_t)s0 * slot_words, slot_words, min(kSumBatch, np - s0),
                                            e, a, &sum);
-                if (!ok) continue;
+                if (!ok) return 0.f;
+                if constexpr (FU)
+                    if (fz & kFuseNorm) sum *= sh_rstd[wave][m];
                 if (L.bias) sum += ld_global(L.bias + nn);
                 if constexpr (FU)
-                    if (L.fuse & kFuseRes) sum += residual(L, m, nn, N, e, ok);
+                    if (fz & kFuseRes) sum += residual(F, m, nn, N, e, ok);
                 st_global(L.y + (size_t)m * N + nn, sum);
                 st_ll(L.y_ll + (size_t)m * N + nn, sum, e);
+                return sum;
+            };
+            for (int idx = threadIdx.x; idx < task.nblk * M * kCols; idx += kThreads) {
+                const int b = idx / (M * kCols);
+                const int r = idx - b * (M * kCols);
+                const int m = r / kCols;
+                const int nn = (task.ct + b) * kCols + (r - m * kCols);
+                if constexpr (FU)
+                    if (fssq) {
+                        // one wave holds one (block, row): its 64 lanes are the block's columns
+                        const float v = nn < N && ok ? reduce_one(b, r, m, nn) : 0.f;
+                        emit_ssq(fssq, N, m, task.ct + b, v, e);
+                        continue;
+                    }
+                if (nn >= N || !ok) continue;
+                reduce_one(b, r, m, nn);
             }
             if (!ok) sh_bad = 1;
             __syncthreads();
@@ -513,10 +598,13 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         const bool P = L.src >= 0;
         const uint64_t* p_ll = P ? ld_const(&a.lin[L.src].y_ll) : nullptr;
         // fused staging: x -> rmsnorm(x) * w (NORM) or silu(x) * x2 (GLU)
-        const bool NORM = FU && (L.fuse & kFuseNorm);
-        const bool GLU = FU && (L.fuse & kFuseGlu);
-        const bool P2 = GLU && L.src2 >= 0;
-        const uint64_t* p2_ll = P2 ? ld_const(&a.lin[L.src2].y_ll) : nullptr;
+        const SeqFuseLin* F = FU ? a.fl + task.linear : nullptr;
+        const int fz = FU ? ld_const(&F->fuse) : 0;
+        const bool NORM = FU && (fz & kFuseNorm);
+        const bool GLU = FU && (fz & kFuseGlu);
+        const int src2 = GLU ? ld_const(&F->src2) : -1;
+        const bool P2 = GLU && src2 >= 0;
+        const uint64_t* p2_ll = P2 ? ld_const(&a.lin[src2].y_ll) : nullptr;
         // this tile's and the next tile's views, read now so that their table loads overlap the
         // prologue (without a next tile the stream's tail re-reads this tile)
         const FetchSrc cs = src_of(ti);
@@ -527,51 +615,14 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         // 64-value chunk of the segment (one producer block's columns)
         if ((P || P2) && QL_SEQ_SENTINEL) {
             if (wave == 0) {
-                // a normalized input needs its whole row (the sum of squares)
-                const int c0 = NORM ? 0 : task.g0 * GK / kCols;
-                const int c1 = NORM ? L.K / kCols : task.g1 * GK / kCols;
+                const int c0 = task.g0 * GK / kCols;
+                const int c1 = task.g1 * GK / kCols;
                 if (P) ok = wait_words(p_ll + (size_t)c0 * kCols, kCols, c1 - c0, lane, e, a);
                 if (P2 && ok) ok = wait_words(p2_ll + (size_t)c0 * kCols, kCols, c1 - c0, lane, e, a);
             }
             if (!ok) sh_bad = 1;
             __syncthreads();
             if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
-        }
-        if constexpr (FU) {
-            if (NORM) {
-                // rows' sums of squares: thread t takes 8-value chunks t, t + kThreads, ... of each
-                // row; lanes, then waves, add in a fixed order (runs repeat bit for bit)
-                const int cpr = L.K / 8;
-                for (int m = 0; m < M; m++) {
-                    float ss = 0.f;
-                    for (int c = threadIdx.x; c < cpr; c += kThreads) {
-                        const size_t xo = (size_t)m * L.K + (size_t)c * 8;
-                        float v[8];
-                        if (P) {
-                            uint64_t w[8];
-                            issue8_ll(p_ll + xo, w);
-                            if (ok) ok = finish8_ll(p_ll + xo, e, w, v, a);
-                            if (!ok) break;
-                        } else {
-                            load8(L.x, L.x_dtype, xo, v);
-                        }
-#pragma unroll
-                        for (int k = 0; k < 8; k++) ss = fmaf(v[k], v[k], ss);
-                    }
-#pragma unroll
-                    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-                    if (lane == 0) sh_ss[wave][m] = ss;
-                }
-                if (!ok) sh_bad = 1;
-                __syncthreads();
-                if (threadIdx.x < M) {
-                    double t = 0.0;
-                    for (int w = 0; w < W; w++) t += (double)sh_ss[w][threadIdx.x];
-                    sh_rstd[threadIdx.x] = (float)(1.0 / sqrt(t / (double)L.K + (double)L.norm_eps));
-                }
-                __syncthreads();
-                if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
-            }
         }
         uint4* xd = dyn_lds;
         float2* gst = reinterpret_cast<float2*>(dyn_lds + gseg * NB * 4 * R);
@@ -611,13 +662,13 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                     for (int h = 0; h < H; h++) {
                         if (!live[h]) continue;
                         if (P2) issue8_ll(p2_ll + xo[h], w2[h]);
-                        else if (GLU) load8(L.x2, 0, xo[h], v2[h]);
+                        else if (GLU) load8(uniform_ptr(ld_const(&F->x2)), 0, xo[h], v2[h]);
                         else if (NORM) {
                             const int idx = base + kThreads * h + threadIdx.x;
                             const int item = idx / CPG;
                             const int c = idx - item * CPG;
                             const int gg = item / M;
-                            load8(L.norm_w, 0, (size_t)(task.g0 + gg) * GK + (size_t)c * 8, v2[h]);
+                            load8(uniform_ptr(ld_const(&F->norm_w)), 0, (size_t)(task.g0 + gg) * GK + (size_t)c * 8, v2[h]);
                         }
                     }
                 }
@@ -649,9 +700,11 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
 #pragma unroll
                             for (int k = 0; k < 8; k++) v[h][k] = v[h][k] / (1.f + expf(-v[h][k])) * v2[h][k];
                         } else if (NORM) {
-                            const float r = sh_rstd[m];
+                            // x * w here; the row's 1/rms, a scalar, multiplies the dot products
+                            // when the outputs are stored (the linear commutes with it), so the
+                            // tile need not wait for the whole row before it starts
 #pragma unroll
-                            for (int k = 0; k < 8; k++) v[h][k] = v[h][k] * r * v2[h][k];
+                            for (int k = 0; k < 8; k++) v[h][k] = v[h][k] * v2[h][k];
                         }
                     }
                     const int blk = gg * NB + (c >> 3);
@@ -665,6 +718,10 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         if (!ok) sh_bad = 1;
         __syncthreads();
         if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
+        // A tile with fused output work (RMSNorm scale, residual, sums of squares for a consumer)
+        // stores its raw sums to y in the job loop and finishes them after it, so the job loop
+        // keeps the plain instance's code: no extra loads or waits between weight jobs.
+        const bool deferred = FU && task.slot < 0 && (NORM || (fz & kFuseRes) || ld_const(&F->ssq) != nullptr);
 
         float acc[4][T];
 #pragma unroll
@@ -755,10 +812,10 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                         float v = red[rs][0][m][lane];
 #pragma unroll
                         for (int w = 1; w < W; w++) v += red[rs][w][m][lane];
-                        if (task.slot < 0) {
+                        if (deferred) {
+                            st_global(L.y + (size_t)m * N + ncol, v);   // finished after the loop
+                        } else if (task.slot < 0) {
                             if (L.bias) v += bias_lds[b * kCols + lane];
-                            if constexpr (FU)
-                                if (L.fuse & kFuseRes) v += residual(L, m, ncol, N, e, ok);
                             st_global(L.y + (size_t)m * N + ncol, v);
                             st_ll(L.y_ll + (size_t)m * N + ncol, v, e);
                         } else {
@@ -793,10 +850,10 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                     const float s2 = __shfl(acc[2][t], src), s3 = __shfl(acc[3][t], src);
                     float v = u == 0 ? s0 : u == 1 ? s1 : u == 2 ? s2 : s3;
                     if (nc >= N) continue;
-                    if (task.slot < 0) {
+                    if (deferred) {
+                        st_global(L.y + (size_t)m * N + nc, v);   // finished after the loop
+                    } else if (task.slot < 0) {
                         if (L.bias) v += bias_lds[b * kCols + lane];
-                        if constexpr (FU)
-                            if (L.fuse & kFuseRes) v += residual(L, m, nc, N, e, ok);
                         st_global(L.y + (size_t)m * N + nc, v);
                         st_ll(L.y_ll + (size_t)m * N + nc, v, e);
                     } else {
@@ -851,8 +908,40 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         if (!bmode && wcount == 0)
             for (int b = 0; b < task.nblk; b++) publish(b);
         if (!ok) sh_bad = 1;
+        // the raw sums of a deferred tile are complete before the barrier (read back after it)
+        if constexpr (FU)
+            if (deferred) __builtin_amdgcn_s_waitcnt(0);
         // the next tile's prologue rewrites the digits
         __syncthreads();
+        if constexpr (FU) {
+            if (deferred) {
+                // the fused output work: y = raw * (1/rms) + bias + residual, then the sums of
+                // squares of the final rows by block. Wave w takes (block, row) pairs w, w + W,
+                // ...; a wave's 64 lanes are the pair's 64 columns. The raw sums were stored by
+                // this workgroup's waves before the barrier; agent-scope loads read them back.
+                if (NORM) wave_rstd(L, F, e, ok);
+                uint64_t* const fssq = ld_const(&F->ssq);
+                for (int pr = wave; pr < task.nblk * M && ok; pr += W) {
+                    const int b = pr / M, m = pr - b * M;
+                    const int nc = (task.ct + b) * kCols + lane;
+                    float v = 0.f;
+                    if (nc < N) {
+                        v = __hip_atomic_load(QL_GLOBAL(const float, L.y + (size_t)m * N + nc), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                        if (NORM) v *= sh_rstd[wave][m];
+                        if (L.bias) v += bias_lds[b * kCols + lane];
+                        if (fz & kFuseRes) v += residual(F, m, nc, N, e, ok);
+                        st_global(L.y + (size_t)m * N + nc, v);
+                        st_ll(L.y_ll + (size_t)m * N + nc, v, e);
+                    }
+                    if (fssq) emit_ssq(fssq, N, m, task.ct + b, v, e);
+                }
+                if (!ok) sh_bad = 1;
+                // the next tile's prologue rewrites the staged bias
+                __syncthreads();
+            }
+        }
+        if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
     }
 }
 
