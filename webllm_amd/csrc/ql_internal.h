@@ -219,7 +219,7 @@ constexpr int kSeqTickets = 32;        // per-run ticket sub-counters (epoch), 6
 constexpr int kSeqTile = 0;
 constexpr int kSeqReduce = 1;
 constexpr uint32_t kSeqErrTimeout = 1;
-constexpr int kSeqBiasBlocks = 64;    // most blocks of a tile that adds a bias (staged in LDS)
+constexpr int kSeqBiasBlocks = 64;    // most (block, row) pairs whose bias (+ residual) a tile stages in LDS
 
 // Device table entry per linear (read-only in the kernel).
 // Elementwise work folded into a sequence linear (SeqLinear::fuse bits).

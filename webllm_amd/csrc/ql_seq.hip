@@ -46,7 +46,8 @@ namespace {
 //   QL_SEQ_WG_PER_CU     resident workgroups per CU the grid is sized for
 //   QL_SEQ_PRO_CHUNKS    8-value input chunks per lane whose loads a tile's prologue issues together
 //   QL_SEQ_SENTINEL      1: a tile first polls one word per 64-value input chunk (wave 0), then
-//                        loads its input; 0: every lane polls its own input words
+//                        loads its input; 0: every lane polls its own input words (one round trip
+//                        less per dependent pass; measured faster on 0.5B- and 7B-shaped chains)
 //   QL_SEQ_BLOCK_MODE    1: tiles of fewer groups than waves may run in block mode (below)
 //   QL_SEQ_TILE_COST_MALL block-groups a tile's fixed work (prologue, pipeline drain) is priced
 //                        at when a streaming pass whose weights fit the MALL is cut into runs
@@ -62,7 +63,7 @@ namespace {
 #define QL_SEQ_TILE_COST 48
 #endif
 #ifndef QL_SEQ_SENTINEL
-#define QL_SEQ_SENTINEL 1
+#define QL_SEQ_SENTINEL 0
 #endif
 #ifndef QL_SEQ_PREFETCH
 #define QL_SEQ_PREFETCH 2
@@ -273,8 +274,9 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
     __shared__ float bias_lds[kSeqBiasBlocks * kCols];
     __shared__ uint32_t sh_epoch;
     __shared__ int sh_bad;
-    // fused RMSNorm: each wave's 1/rms per row of the current linear's input
-    __shared__ float sh_rstd[FU ? W : 1][FU ? 4 * T : 1];
+    // fused RMSNorm: 1/rms of each input row of the current task's linear (written by the last
+    // wave before a barrier, read by every wave after it)
+    __shared__ float sh_rstd[FU ? 4 * T : 1];
 
     const int wg = blockIdx.x;
     const int lane = threadIdx.x & 63;
@@ -356,59 +358,70 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         if (lane == 0) st_ll(ssq + (size_t)m * ((N + kCols - 1) / kCols) + blk, q, e);
     };
 
-    // Fused RMSNorm: 1/rms of each input row of linear L, computed by the calling wave alone into
-    // sh_rstd[wave] (lane l takes the row's 8-value chunks l, l + 64, ...; the xor butterfly adds
-    // them in a fixed order, so every wave and every run gets the same values). The input is an
-    // external x or the producer's output words, waited for (its pass is an earlier one).
-    auto wave_rstd = [&](const SeqLinear& L, const SeqFuseLin* F, uint32_t e, bool& ok) {
+    // Fused RMSNorm: 1/rms of each input row of linear L into sh_rstd, computed by the calling wave
+    // alone (before a barrier that publishes it). With a producer that emits sums of squares (one
+    // word per row and 64-column block), lane l adds the row's words l, l + 64, ... and an xor
+    // butterfly adds the lanes; all rows' loads go out together, so this costs one round trip.
+    // Otherwise (an external input) the row itself is read. The order of additions is fixed, so
+    // every task and every run gets the same values.
+    auto rows_rstd = [&](const SeqLinear& L, const SeqFuseLin* F, uint32_t e, bool& ok) {
         const float eps = ld_const(&F->norm_eps);
         const uint64_t* pss = L.src >= 0 ? ld_const(&a.fl[L.src].ssq) : nullptr;
+        float ss[4 * T];
+#pragma unroll
+        for (int m = 0; m < 4 * T; m++) ss[m] = 0.f;
         if (pss) {
-            // the producer's sums of squares, one word per (row, 64-column block), in block order
             pss = uniform_ptr(pss);
             const int nbk = L.K / kCols;
-            for (int m = 0; m < M; m++) {
-                float ss = 0.f;
-                for (int c = lane; c < nbk && ok; c += 64) {
-                    const uint64_t* w = pss + (size_t)m * nbk + c;
-                    uint64_t v = ld_ll(w);
-                    uint32_t polls = 0;
-                    while ((uint32_t)(v >> 32) != e && ok) {
-                        if (!keep_waiting(a, polls)) ok = false;
-                        else v = ld_ll(w);
+            for (int c0 = 0; c0 < nbk && ok; c0 += 64) {
+                const int c = c0 + lane;
+                uint64_t w[4 * T];
+#pragma unroll
+                for (int m = 0; m < 4 * T; m++)
+                    w[m] = m < M && c < nbk ? ld_ll(pss + (size_t)m * nbk + c) : (uint64_t)e << 32;
+                uint32_t polls = 0;
+                for (;;) {
+                    bool ready = true;
+#pragma unroll
+                    for (int m = 0; m < 4 * T; m++) ready = ready && (uint32_t)(w[m] >> 32) == e;
+                    if (ready) break;
+                    if (!keep_waiting(a, polls)) {
+                        ok = false;
+                        break;
                     }
-                    ss += __uint_as_float((uint32_t)v);
+#pragma unroll
+                    for (int m = 0; m < 4 * T; m++)
+                        if ((uint32_t)(w[m] >> 32) != e) w[m] = ld_ll(pss + (size_t)m * nbk + c);
                 }
 #pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-                if (lane == 0) sh_rstd[wave][m] = (float)(1.0 / sqrt((double)ss / (double)L.K + (double)eps));
+                for (int m = 0; m < 4 * T; m++)
+                    if (m < M && c < nbk) ss[m] += __uint_as_float((uint32_t)w[m]);
             }
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            return;
-        }
-        const uint64_t* pll = L.src >= 0 ? uniform_ptr(ld_const(&a.lin[L.src].y_ll)) : nullptr;
-        const int cpr = L.K / 8;
-        for (int m = 0; m < M; m++) {
-            float ss = 0.f;
-            for (int c = lane; c < cpr && ok; c += 64) {
-                const size_t xo = (size_t)m * L.K + (size_t)c * 8;
-                float v[8];
-                if (pll) {
-                    uint64_t w[8];
-                    issue8_ll(pll + xo, w);
-                    ok = finish8_ll(pll + xo, e, w, v, a);
-                } else {
-                    load8(L.x, L.x_dtype, xo, v);
+        } else {
+            const uint64_t* pll = L.src >= 0 ? uniform_ptr(ld_const(&a.lin[L.src].y_ll)) : nullptr;
+            const int cpr = L.K / 8;
+            for (int m = 0; m < M; m++)
+                for (int c = lane; c < cpr && ok; c += 64) {
+                    const size_t xo = (size_t)m * L.K + (size_t)c * 8;
+                    float v[8];
+                    if (pll) {
+                        uint64_t w[8];
+                        issue8_ll(pll + xo, w);
+                        ok = finish8_ll(pll + xo, e, w, v, a);
+                    } else {
+                        load8(L.x, L.x_dtype, xo, v);
+                    }
+#pragma unroll
+                    for (int k = 0; k < 8; k++) ss[m] = fmaf(v[k], v[k], ss[m]);
                 }
-#pragma unroll
-                for (int k = 0; k < 8; k++) ss = fmaf(v[k], v[k], ss);
-            }
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-            if (lane == 0) sh_rstd[wave][m] = (float)(1.0 / sqrt((double)ss / (double)L.K + (double)eps));
         }
-        // the wave's own LDS writes precede its reads (in order per wave); keep the compiler too
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+        for (int m = 0; m < 4 * T; m++) {
+            float q = ss[m];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) q += __shfl_xor(q, o);
+            if (lane == 0 && m < M) sh_rstd[m] = (float)(1.0 / sqrt((double)q / (double)L.K + (double)eps));
+        }
     };
 
     // Software pipeline over each wave's job stream. In a tile, the wave's job k is block
@@ -529,6 +542,11 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             // K order), plus bias. Wave 0 first waits for one word of every slot.
             const int np = task.parts;
             const size_t slot_words = (size_t)M * kCols;
+            const SeqFuseLin* F = FU ? a.fl + task.linear : nullptr;
+            const int fz = FU ? ld_const(&F->fuse) : 0;
+            uint64_t* const fssq = FU ? ld_const(&F->ssq) : nullptr;
+            if constexpr (FU)
+                if ((fz & kFuseNorm) && wave == W - 1) rows_rstd(L, F, e, ok);
             if (wave == 0) {
                 for (int l = lane; l < task.nblk * np && ok; l += 64) {
                     const int b = l / np;
@@ -544,25 +562,40 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             if (!ok) sh_bad = 1;
             __syncthreads();
             if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
-            const SeqFuseLin* F = FU ? a.fl + task.linear : nullptr;
-            const int fz = FU ? ld_const(&F->fuse) : 0;
-            uint64_t* const fssq = FU ? ld_const(&F->ssq) : nullptr;
-            if constexpr (FU)
-                if (fz & kFuseNorm) wave_rstd(L, F, e, ok);
-            // output (m, nn) of block b: its parts added in K order, then the epilogue; stored, and
-            // returned for the block's sum of squares
+            // output (m, nn) of block b: its parts added in K order, then the epilogue
+            // rstd * sum + (bias + residual); stored, and returned for the block's sum of squares
             auto reduce_one = [&](int b, int r, int m, int nn) -> float {
                 const uint64_t* src = a.part + (size_t)(task.slot + b * task.stride) * slot_words + r;
+                // the residual's load goes out with the parts' (its producer ran passes earlier)
+                float add = L.bias ? ld_global(L.bias + nn) : 0.f;
+                uint64_t rw = 0;
+                const uint64_t* rp = nullptr;
+                if constexpr (FU)
+                    if (fz & kFuseRes) {
+                        const int rs = ld_const(&F->res_src);
+                        if (rs < 0) add += ld_global(uniform_ptr(ld_const(&F->res)) + (size_t)m * N + nn);
+                        else {
+                            rp = uniform_ptr(ld_const(&a.lin[rs].y_ll)) + (size_t)m * N + nn;
+                            rw = ld_ll(rp);
+                        }
+                    }
                 float sum = 0.f;
                 for (int s0 = 0; s0 < np && ok; s0 += kSumBatch)
                     ok = sum_ll<kSumBatch>(src + (size_t)s0 * slot_words, slot_words, min(kSumBatch, np - s0),
                                            e, a, &sum);
+                if constexpr (FU)
+                    if (rp) {
+                        uint32_t polls = 0;
+                        while ((uint32_t)(rw >> 32) != e && ok) {
+                            if (!keep_waiting(a, polls)) ok = false;
+                            else rw = ld_ll(rp);
+                        }
+                        add += __uint_as_float((uint32_t)rw);
+                    }
                 if (!ok) return 0.f;
                 if constexpr (FU)
-                    if (fz & kFuseNorm) sum *= sh_rstd[wave][m];
-                if (L.bias) sum += ld_global(L.bias + nn);
-                if constexpr (FU)
-                    if (fz & kFuseRes) sum += residual(F, m, nn, N, e, ok);
+                    if (fz & kFuseNorm) sum *= sh_rstd[m];
+                sum += add;
                 st_global(L.y + (size_t)m * N + nn, sum);
                 st_ll(L.y_ll + (size_t)m * N + nn, sum, e);
                 return sum;
@@ -626,12 +659,29 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         }
         uint4* xd = dyn_lds;
         float2* gst = reinterpret_cast<float2*>(dyn_lds + gseg * NB * 4 * R);
+        // A tile that writes whole outputs finishes them where it stores them:
+        // y = rstd * sum + (bias + residual) (rstd with a fused RMSNorm, the residual with a fused
+        // add), then the block sums of squares for a consumer that normalizes y. The prologue
+        // stages what that needs, in the round trip of the tile's own input: bias + residual
+        // per (block, row, column) in bias_lds (rows only with a residual; the planner keeps
+        // nblk * rows within kSeqBiasBlocks), taken from the highest threads down because the
+        // input chunks occupy the lowest; and 1/rms per row in sh_rstd, from the last wave.
+        const bool RES = FU && task.slot < 0 && (fz & kFuseRes);
+        const int Mr = RES ? M : 1;
         {
-            if (task.slot < 0 && L.bias)
-                for (int idx = threadIdx.x; idx < task.nblk * kCols; idx += kThreads) {
-                    const int col = task.ct * kCols + idx;
-                    bias_lds[idx] = col < N ? ld_global(L.bias + col) : 0.f;
+            if (task.slot < 0 && (L.bias || RES))
+                for (int idx = kThreads - 1 - (int)threadIdx.x; idx < task.nblk * Mr * kCols; idx += kThreads) {
+                    const int b = idx / (Mr * kCols);
+                    const int r = idx - b * (Mr * kCols);
+                    const int m = r / kCols;
+                    const int col = (task.ct + b) * kCols + (r - m * kCols);
+                    float v = col < N && L.bias ? ld_global(L.bias + col) : 0.f;
+                    if constexpr (FU)
+                        if (RES && col < N) v += residual(F, m, col, N, e, ok);
+                    bias_lds[idx] = v;
                 }
+            if constexpr (FU)
+                if (NORM && task.slot < 0 && wave == W - 1) rows_rstd(L, F, e, ok);
             // QL_SEQ_PRO_CHUNKS chunks per trip: their input loads are all issued before any is used
             const int items = gseg * M;
             constexpr int H = QL_SEQ_PRO_CHUNKS;
@@ -718,10 +768,16 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         if (!ok) sh_bad = 1;
         __syncthreads();
         if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
-        // A tile with fused output work (RMSNorm scale, residual, sums of squares for a consumer)
-        // stores its raw sums to y in the job loop and finishes them after it, so the job loop
-        // keeps the plain instance's code: no extra loads or waits between weight jobs.
-        const bool deferred = FU && task.slot < 0 && (NORM || (fz & kFuseRes) || ld_const(&F->ssq) != nullptr);
+        uint64_t* const fssq = FU && task.slot < 0 ? ld_const(&F->ssq) : nullptr;
+        // one finished output: rstd * sum + staged (bias + residual), stored as value and word
+        auto finish = [&](int b, int m, int nc, float v) -> float {
+            if constexpr (FU)
+                if (NORM) v *= sh_rstd[m];
+            if (L.bias || RES) v += bias_lds[(b * Mr + (RES ? m : 0)) * kCols + lane];
+            st_global(L.y + (size_t)m * N + nc, v);
+            st_ll(L.y_ll + (size_t)m * N + nc, v, e);
+            return v;
+        };
 
         float acc[4][T];
 #pragma unroll
@@ -808,20 +864,16 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             if (arrived == W - 1) {
                 const int ncol = (task.ct + b) * kCols + lane;
                 for (int m = 0; m < M; m++) {
+                    float v = 0.f;
                     if (ncol < N) {
-                        float v = red[rs][0][m][lane];
+                        v = red[rs][0][m][lane];
 #pragma unroll
                         for (int w = 1; w < W; w++) v += red[rs][w][m][lane];
-                        if (deferred) {
-                            st_global(L.y + (size_t)m * N + ncol, v);   // finished after the loop
-                        } else if (task.slot < 0) {
-                            if (L.bias) v += bias_lds[b * kCols + lane];
-                            st_global(L.y + (size_t)m * N + ncol, v);
-                            st_ll(L.y_ll + (size_t)m * N + ncol, v, e);
-                        } else {
-                            st_ll(a.part + ((size_t)(task.slot + b * task.stride) * M + m) * kCols + lane, v, e);
-                        }
+                        if (task.slot < 0) v = finish(b, m, ncol, v);
+                        else st_ll(a.part + ((size_t)(task.slot + b * task.stride) * M + m) * kCols + lane, v, e);
                     }
+                    if constexpr (FU)
+                        if (fssq) emit_ssq(fssq, N, m, task.ct + b, v, e);
                 }
                 __atomic_signal_fence(__ATOMIC_SEQ_CST);
                 if (lane == 0) {
@@ -849,16 +901,14 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                     const float s0 = __shfl(acc[0][t], src), s1 = __shfl(acc[1][t], src);
                     const float s2 = __shfl(acc[2][t], src), s3 = __shfl(acc[3][t], src);
                     float v = u == 0 ? s0 : u == 1 ? s1 : u == 2 ? s2 : s3;
-                    if (nc >= N) continue;
-                    if (deferred) {
-                        st_global(L.y + (size_t)m * N + nc, v);   // finished after the loop
-                    } else if (task.slot < 0) {
-                        if (L.bias) v += bias_lds[b * kCols + lane];
-                        st_global(L.y + (size_t)m * N + nc, v);
-                        st_ll(L.y_ll + (size_t)m * N + nc, v, e);
+                    if (nc < N) {
+                        if (task.slot < 0) v = finish(b, m, nc, v);
+                        else st_ll(a.part + ((size_t)(task.slot + b * task.stride) * M + m) * kCols + lane, v, e);
                     } else {
-                        st_ll(a.part + ((size_t)(task.slot + b * task.stride) * M + m) * kCols + lane, v, e);
+                        v = 0.f;
                     }
+                    if constexpr (FU)
+                        if (fssq) emit_ssq(fssq, N, m, task.ct + b, v, e);
                 }
             }
         };
@@ -908,39 +958,8 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         if (!bmode && wcount == 0)
             for (int b = 0; b < task.nblk; b++) publish(b);
         if (!ok) sh_bad = 1;
-        // the raw sums of a deferred tile are complete before the barrier (read back after it)
-        if constexpr (FU)
-            if (deferred) __builtin_amdgcn_s_waitcnt(0);
-        // the next tile's prologue rewrites the digits
+        // the next tile's prologue rewrites the digits and the staged epilogue
         __syncthreads();
-        if constexpr (FU) {
-            if (deferred) {
-                // the fused output work: y = raw * (1/rms) + bias + residual, then the sums of
-                // squares of the final rows by block. Wave w takes (block, row) pairs w, w + W,
-                // ...; a wave's 64 lanes are the pair's 64 columns. The raw sums were stored by
-                // this workgroup's waves before the barrier; agent-scope loads read them back.
-                if (NORM) wave_rstd(L, F, e, ok);
-                uint64_t* const fssq = ld_const(&F->ssq);
-                for (int pr = wave; pr < task.nblk * M && ok; pr += W) {
-                    const int b = pr / M, m = pr - b * M;
-                    const int nc = (task.ct + b) * kCols + lane;
-                    float v = 0.f;
-                    if (nc < N) {
-                        v = __hip_atomic_load(QL_GLOBAL(const float, L.y + (size_t)m * N + nc), __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-                        if (NORM) v *= sh_rstd[wave][m];
-                        if (L.bias) v += bias_lds[b * kCols + lane];
-                        if (fz & kFuseRes) v += residual(F, m, nc, N, e, ok);
-                        st_global(L.y + (size_t)m * N + nc, v);
-                        st_ll(L.y_ll + (size_t)m * N + nc, v, e);
-                    }
-                    if (fssq) emit_ssq(fssq, N, m, task.ct + b, v, e);
-                }
-                if (!ok) sh_bad = 1;
-                // the next tile's prologue rewrites the staged bias
-                __syncthreads();
-            }
-        }
         if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
     }
 }
@@ -1010,6 +1029,13 @@ static int latency_split(const SeqSpec& s, int M, double units)
     const int mg = max_tile_groups(s, M, true);
     S = std::max({S, 1, (groups + mg - 1) / mg});
     return std::min({S, groups, kSeqMaxSplit});
+}
+
+// Rows per block a tile writing whole outputs of this linear stages in LDS for its epilogue: one
+// (the bias) or M (bias + residual of a fused add); none without either.
+static int staged_rows(const SeqSpec& s, int M)
+{
+    return (s.fuse & kFuseRes) ? M : s.has_bias ? 1 : 0;
 }
 
 namespace {
@@ -1346,7 +1372,7 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
                     if (b.lin != a.lin || b.c != a.c + (int)(e - k) || b.g0 != a.g0 || b.g1 != a.g1) break;
                     const int64_t sb = slot_of(b);
                     if ((s0 < 0) != (sb < 0)) break;
-                    if (s0 < 0 && lin[a.lin].has_bias && e - k == (size_t)kSeqBiasBlocks) break;
+                    if (s0 < 0 && (e - k + 1) * (size_t)staged_rows(lin[a.lin], M) > (size_t)kSeqBiasBlocks) break;
                     if (s0 >= 0) {
                         const int64_t d = sb - slot_of(v[e - 1]);
                         if (e == k + 1) stride = d;
@@ -1445,7 +1471,8 @@ std::string verify_seq_plan(const std::vector<SeqSpec>& lin, int M, const SeqPla
             prev_tile = t;
             if (k.g0 < 0 || k.g1 > groups || k.g0 >= k.g1) return "tile groups outside K";
             if ((uint64_t)(k.g1 - k.g0) * lds_per_group(M, s.group) > p.lds_bytes) return "tile exceeds the LDS plan";
-            if (k.slot < 0 && s.has_bias && k.nblk > kSeqBiasBlocks) return "tile with bias exceeds the staged blocks";
+            if (k.slot < 0 && k.nblk * staged_rows(s, M) > kSeqBiasBlocks)
+                return "tile with a staged epilogue exceeds the staged blocks";
             for (int b = 0; b < k.nblk; b++) {
                 for (int g = k.g0; g < k.g1; g++) {
                     int& cv = cover[k.linear][(size_t)(k.ct + b) * groups + g];
