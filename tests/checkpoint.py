@@ -7,6 +7,12 @@ TINY = gptq.QwenConfig(vocab_size=512, block_size=16, n_layer=2, n_head=4, n_kv_
                        n_embd=256, intermediate=640)
 
 
+def post_norm_weight(cfg, layer):
+    """The post-attention RMSNorm weight of `layer` in these checkpoints: 1 + 0.1 N(0,1) per channel
+    (the input norms are ones)."""
+    return (1.0 + 0.1 * synth.activations(1, cfg.n_embd, seed=0x10AE, key=(layer,))[0]).astype(np.float32)
+
+
 def write_checkpoint(path, cfg, act_order=None, no_g_idx=False):
     """Writes a Qwen-layout GPTQ checkpoint of config `cfg` (random tensors, half the linears with
     qzeros nibble 7, half with random zeros) and returns {(layer, key): (GptqTensors, bias f32)} plus "embed": the fp16 embedding.
@@ -22,7 +28,7 @@ def write_checkpoint(path, cfg, act_order=None, no_g_idx=False):
     for i in range(cfg.n_layer):
         p = f"model.layers.{i}"
         tensors[f"{p}.input_layernorm.weight"] = ("F32", (cfg.n_embd,), np.ones(cfg.n_embd, np.float32).tobytes())
-        tensors[f"{p}.post_attention_layernorm.weight"] = ("F32", (cfg.n_embd,), np.ones(cfg.n_embd, np.float32).tobytes())
+        tensors[f"{p}.post_attention_layernorm.weight"] = ("F32", (cfg.n_embd,), post_norm_weight(cfg, i).tobytes())
         for j, (key, proj) in enumerate(gptq._PROJ):
             K, N = shapes[key]
             t = synth.gptq_linear(K, N, 128, seed=0x10AD, key=(i, j), stored_zero=None if j % 2 else 7)

@@ -119,6 +119,35 @@ async function gpu(dir) {
             pool.reset();
             spec.seqInfo = info;
         }
+        // a fused layer run from JavaScript (ql_seq_create_fused): q/k/v <- rmsnorm(h, inNorm),
+        // h1 = h + o(q), gate/up <- rmsnorm(h1, postNorm), h2 = h1 + down(silu(gate) * up)
+        if (spec.fused) {
+            const fz = spec.fused;
+            const names = ['qW', 'kW', 'vW', 'oW', 'gateW', 'upW', 'downW'];
+            const descs = names.map((k) => model.linear(`L0.${k}`).desc);
+            const H = pool.alloc([fz.M, descs[0].K]);
+            H.write(readF32(path.join(dir, fz.x)));
+            const Y = descs.map((d) => pool.alloc([fz.M, d.N]));
+            const ln1 = model.f32Weights.get('L0.inNorm').offset;
+            const ln2 = model.f32Weights.get('L0.postNorm').offset;
+            const norm = (off) => ({ normWOff: off, normEps: fz.eps });
+            const xOffs = [H, H, H, Y[0], Y[3], Y[3], Y[4]].map((t) => t.offset);
+            const fuse = [norm(ln1), norm(ln1), norm(ln1), { resOff: H.offset }, norm(ln2), norm(ln2),
+                { x2Off: Y[5].offset, resOff: Y[3].offset }];
+            const seq = ctx.seq(descs, model.weights, pool.arena, xOffs, q.QL_DTYPE_F32, fz.M,
+                Y.map((y) => y.offset), fuse);
+            spec.fusedInfo = seq.info;
+            seq.run();
+            seq.status();
+            Y.forEach((y, i) => writeTyped(path.join(dir, fz.outs[i]), y.read()));
+            seq.destroy();
+            pool.reset();
+            // both fused operands at once are refused (norm and x2 exclude each other)
+            try {
+                ctx.seq([descs[0]], model.weights, pool.arena, [H.offset], q.QL_DTYPE_F32, fz.M, [Y[0].offset],
+                    [{ normWOff: ln1, x2Off: Y[5].offset }]);
+            } catch (e) { spec.fusedBoth = e.message; }
+        }
         const u = spec.unpack;
         const U = pool.alloc([u.N, u.K], 'f16');
         model.unpackF16(u.weight, U);
@@ -210,6 +239,7 @@ async function gpu(dir) {
         console.log(JSON.stringify({
             device: ctx.info(), tensorCount: res.tensorCount, gpuBytes: res.gpuBytes,
             fileBytes: res.fileBytes, progress, errors, seqInfo: spec.seqInfo || null,
+            fusedInfo: spec.fusedInfo || null, fusedBoth: spec.fusedBoth || null,
             isPromise, storedZeros: res.storedZeros, actOrder,
         }));
     } finally {

@@ -15,7 +15,7 @@ import pytest
 from webllm_amd import gptq, synth
 from webllm_amd import qlinear as ql
 
-from .checkpoint import TINY, write_checkpoint
+from .checkpoint import TINY, post_norm_weight, write_checkpoint
 
 NODE = shutil.which("node")
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -128,6 +128,10 @@ def test_node_host_matches_oracle(tmp_path, orc):
     xs.tofile(tmp_path / "xs")
     cases["seq"] = {"weights": [f"L0.{k}" for k in seq_names], "M": 1, "x": "xs",
                     "outs": [f"s{k}.f32" for k in seq_names]}
+    fz = ["qW", "kW", "vW", "oW", "gateW", "upW", "downW"]
+    xf = synth.activations(1, TINY.n_embd, seed=0x40E7)
+    xf.tofile(tmp_path / "xf")
+    cases["fused"] = {"x": "xf", "M": 1, "eps": 1e-6, "outs": [f"f{k}.f32" for k in fz]}
     K, N = shapes["gateW"]
     cases["unpack"] = {"weight": "L1.gateW", "N": N, "K": K, "out": "u.f16"}
     ua = ["gateW", "downW", "kW"]
@@ -210,6 +214,27 @@ def test_node_host_matches_oracle(tmp_path, orc):
         ok, max_abs, _ = orc.check_tolerance(y, ref, atol, 1e-4)
         assert ok, f"seq {k}: maxAbs {max_abs:.3e}"
         x_in = y
+    # the JavaScript-built fused layer: each linear against the oracle's composition on the inputs
+    # the GPU used (rmsNormRef / siluMulRef, gemmNTRef, vec_add)
+    assert res["fusedInfo"]["passes"] == 4 and res["fusedInfo"]["linears"] == 7
+    assert res["fusedInfo"]["kernel"] == 0          # QL_SEQ_TILES
+    assert res["fusedBoth"] and "QL_E_INVALID" in res["fusedBoth"]
+    ys = {k: np.fromfile(tmp_path / f"f{k}.f32", dtype=np.float32).reshape(1, -1) for k in fz}
+    ln1, ln2 = np.ones(TINY.n_embd, np.float32), post_norm_weight(TINY, 0)
+    n1 = orc.add_rmsnorm(xf, ln1, 1e-6)[1]
+    n2 = orc.add_rmsnorm(ys["oW"], ln2, 1e-6)[1]
+    plan = {"qW": (n1, None), "kW": (n1, None), "vW": (n1, None), "oW": (ys["qW"], xf),
+            "gateW": (n2, None), "upW": (n2, None),
+            "downW": (orc.silu_mul(ys["gateW"], ys["upW"]), ys["oW"])}
+    for k in fz:
+        t, b = kept[(0, k)]
+        x_in, res_in = plan[k]
+        ref = orc.gptq_linear(t.qweight, t.qzeros, t.scales, x_in, b)
+        if res_in is not None:
+            ref = ref + res_in
+        atol = 1e-5 * max(1.0, float(np.sqrt(np.mean(x_in.astype(np.float64) ** 2))))
+        ok, max_abs, _ = orc.check_tolerance(ys[k], ref, atol, 1e-4)
+        assert ok, f"fused {k}: maxAbs {max_abs:.3e}"
     got = np.fromfile(tmp_path / "w32.f32", dtype=np.float32).reshape(dN, dK)
     _, want = orc.dequantize_gptq_int4(d_qw, d_qz, d_sc, dK, dN, dG)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -54,10 +54,14 @@ export class Seq {
     status(): void;
     destroy(): void;
 }
+/** Elementwise work folded into one linear of a fused sequence (ql_seq_fuse). */
+export interface SeqFuse {
+    normWOff?: number | null; normEps?: number; x2Off?: number | null; resOff?: number | null;
+}
 export class Context {
     constructor(device?: number);
     seq(descs: GptqDesc[], weights: Arena, act: Arena, xOffs: number[], xDtype: number, M: number,
-        yOffs: number[]): Seq;
+        yOffs: number[], fuse?: (SeqFuse | null)[]): Seq;
     info(): { name: string; cuCount: number; hbmBytes: number };
     arena(bytes: number): Arena;
     sync(): void;

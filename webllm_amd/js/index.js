@@ -197,11 +197,18 @@ class Arena {
  * A forward's decode linears as one persistent launch (ql_seq_*; the CommandBatch of
  * src/gpu/pipeline.ts:71-116 with passBreak, qwen.ts:556-559): linear i consumes linear j's
  * output when xOffs[i] === yOffs[j], and the kernel orders the two on the device.
+ * `fuse` (optional, one entry per linear, null for none) folds the layer's elementwise work in
+ * (ql_seq_create_fused; qwen.ts:401-405, :445-478): {normWOff, normEps} normalizes the linear's
+ * input (RMSNorm weights at normWOff in `weights`), {x2Off} multiplies silu(x) by a second input,
+ * {resOff} adds a residual to the output. An offset equal to another linear's yOffs entry makes
+ * that linear the producer.
  */
 class Seq {
-    constructor(ctx, descs, weights, act, xOffs, xDtype, M, yOffs) {
+    constructor(ctx, descs, weights, act, xOffs, xDtype, M, yOffs, fuse) {
         this.ctx = ctx;
-        this.handle = addon.seqCreate(ctx.handle, descs, weights.handle, act.handle, xOffs, xDtype, M, yOffs);
+        this.handle = fuse
+            ? addon.seqCreate(ctx.handle, descs, weights.handle, act.handle, xOffs, xDtype, M, yOffs, fuse)
+            : addon.seqCreate(ctx.handle, descs, weights.handle, act.handle, xOffs, xDtype, M, yOffs);
         ctx._seqs.add(this);
     }
     get info() { return addon.seqInfo(this.handle); }
@@ -224,8 +231,8 @@ class Context {
         this._arenas = new Set();
         this._seqs = new Set();
     }
-    seq(descs, weights, act, xOffs, xDtype, M, yOffs) {
-        return new Seq(this, descs, weights, act, xOffs, xDtype, M, yOffs);
+    seq(descs, weights, act, xOffs, xDtype, M, yOffs, fuse) {
+        return new Seq(this, descs, weights, act, xOffs, xDtype, M, yOffs, fuse);
     }
     info() { return addon.deviceInfo(this.handle); }
     arena(bytes) { return new Arena(this, bytes); }

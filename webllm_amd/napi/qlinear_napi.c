@@ -635,14 +635,57 @@ static napi_value js_graph_destroy(napi_env env, napi_callback_info info)
     return NULL;
 }
 
-/* seqCreate(ctx, descs[], weights, act, xOffs[], xDtype, M, yOffs[]) -> sequence handle */
+/* {normWOff|null, normEps, x2Off|null, resOff|null} (any may be absent; null/undefined = no fusion)
+   -> ql_seq_fuse */
+static int get_fuse(napi_env env, napi_value obj, ql_seq_fuse* f)
+{
+    napi_valuetype t;
+    memset(f, 0, sizeof *f);
+    f->norm_w_off = f->x2_off = f->res_off = QL_NONE;
+    f->norm_eps = 1e-6f;
+    if (napi_typeof(env, obj, &t) != napi_ok) return 1;
+    if (t == napi_null || t == napi_undefined) return 0;
+    if (t != napi_object) {
+        napi_throw_type_error(env, "QL_E_INVALID", "expected a fusion object or null");
+        return 1;
+    }
+    static const char* const names[3] = {"normWOff", "x2Off", "resOff"};
+    uint64_t* const dst[3] = {&f->norm_w_off, &f->x2_off, &f->res_off};
+    for (int k = 0; k < 3; k++) {
+        bool has = false;
+        napi_value v;
+        if (napi_has_named_property(env, obj, names[k], &has) != napi_ok) return 1;
+        if (has && (prop(env, obj, names[k], &v) || get_u64(env, v, dst[k], 1))) return 1;
+    }
+    bool has = false;
+    if (napi_has_named_property(env, obj, "normEps", &has) != napi_ok) return 1;
+    if (has) {
+        napi_value v;
+        double eps;
+        if (prop(env, obj, "normEps", &v)) return 1;
+        if (napi_get_value_double(env, v, &eps) != napi_ok) {
+            napi_throw_type_error(env, "QL_E_INVALID", "normEps must be a number");
+            return 1;
+        }
+        f->norm_eps = (float)eps;
+    }
+    return 0;
+}
+
+/* seqCreate(ctx, descs[], weights, act, xOffs[], xDtype, M, yOffs[], fuse[]?) -> sequence handle;
+   with fuse (one entry per linear) the sequence is created by ql_seq_create_fused */
 static napi_value js_seq_create(napi_env env, napi_callback_info info)
 {
-    napi_value argv[8];
+    napi_value argv[9];
     void *ctx, *w, *act;
     int32_t xdt, M;
     uint32_t n, m;
-    if (get_args(env, info, 8, argv) || get_ptr(env, argv[0], &ctx)) return NULL;
+    size_t argc = 9;
+    if (napi_get_cb_info(env, info, &argc, argv, NULL, NULL) != napi_ok || argc < 8) {
+        napi_throw_type_error(env, "QL_E_INVALID", "too few arguments");
+        return NULL;
+    }
+    if (get_ptr(env, argv[0], &ctx)) return NULL;
     if (napi_get_array_length(env, argv[1], &n) != napi_ok || n == 0 || n > 4096) {
         napi_throw_type_error(env, "QL_E_INVALID", "expected an array of 1..4096 descriptors");
         return NULL;
@@ -655,11 +698,23 @@ static napi_value js_seq_create(napi_env env, napi_callback_info info)
         napi_throw_type_error(env, "QL_E_INVALID", "offset arrays must match the descriptors");
         return NULL;
     }
+    napi_valuetype ft = napi_undefined;
+    if (argc > 8) napi_typeof(env, argv[8], &ft);
+    const int fused = ft != napi_undefined && ft != napi_null;
+    if (fused && (napi_get_array_length(env, argv[8], &m) != napi_ok || m != n)) {
+        napi_throw_type_error(env, "QL_E_INVALID", "fuse must be an array with one entry per descriptor");
+        return NULL;
+    }
     ql_gptq_desc* d = (ql_gptq_desc*)calloc(n, sizeof(ql_gptq_desc));
     uint64_t* xo = (uint64_t*)calloc(n, sizeof(uint64_t));
     uint64_t* yo = (uint64_t*)calloc(n, sizeof(uint64_t));
+    ql_seq_fuse* fz = fused ? (ql_seq_fuse*)calloc(n, sizeof(ql_seq_fuse)) : NULL;
     napi_value result = NULL;
-    int bad = !d || !xo || !yo;
+    int bad = !d || !xo || !yo || (fused && !fz);
+    for (uint32_t i = 0; i < n && fused && !bad; i++) {
+        napi_value e;
+        bad = napi_get_element(env, argv[8], i, &e) != napi_ok || get_fuse(env, e, &fz[i]);
+    }
     for (uint32_t i = 0; i < n && !bad; i++) {
         napi_value e;
         bad = napi_get_element(env, argv[1], i, &e) != napi_ok || get_desc(env, e, &d[i]);
@@ -667,10 +722,13 @@ static napi_value js_seq_create(napi_env env, napi_callback_info info)
     if (!bad) bad = get_u64_array(env, argv[4], xo, n) || get_u64_array(env, argv[7], yo, n);
     if (!bad) {
         ql_seq* seq = NULL;
-        if (!throw_rc(env, ql_seq_create((ql_ctx*)ctx, (int32_t)n, d, (ql_arena*)w, (ql_arena*)act, xo,
-                                         xdt, M, yo, &seq)))
-            napi_create_external(env, seq, NULL, NULL, &result);
+        const int rc = fused ? ql_seq_create_fused((ql_ctx*)ctx, (int32_t)n, d, (ql_arena*)w, (ql_arena*)act, xo,
+                                                   xdt, M, yo, fz, &seq)
+                             : ql_seq_create((ql_ctx*)ctx, (int32_t)n, d, (ql_arena*)w, (ql_arena*)act, xo,
+                                             xdt, M, yo, &seq);
+        if (!throw_rc(env, rc)) napi_create_external(env, seq, NULL, NULL, &result);
     }
+    free(fz);
     free(d);
     free(xo);
     free(yo);
