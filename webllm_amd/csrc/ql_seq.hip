@@ -539,7 +539,8 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
 
         if (task.kind == kSeqReduce) {
             // blocks ct .. ct+nblk-1: each the sum of its parts (consecutive pool slots, ascending
-            // K order), plus bias. Wave 0 first waits for one word of every slot.
+            // K order), plus bias. Each lane polls the parts of its own outputs as it loads them
+            // (with QL_SEQ_SENTINEL, wave 0 first waits for one word of every slot).
             const int np = task.parts;
             const size_t slot_words = (size_t)M * kCols;
             const SeqFuseLin* F = FU ? a.fl + task.linear : nullptr;
@@ -547,7 +548,7 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             uint64_t* const fssq = FU ? ld_const(&F->ssq) : nullptr;
             if constexpr (FU)
                 if ((fz & kFuseNorm) && wave == W - 1) rows_rstd(L, F, e, ok);
-            if (wave == 0) {
+            if (QL_SEQ_SENTINEL && wave == 0) {
                 for (int l = lane; l < task.nblk * np && ok; l += 64) {
                     const int b = l / np;
                     const uint64_t* w0 = a.part + (size_t)(task.slot + b * task.stride + (l - b * np)) * slot_words;
