@@ -117,8 +117,11 @@ template <bool TABLE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 void prefill_kernel(const PrefillArgs a)
 {
-    // [buffer][k block][k quarter][row]: 8 fp16 in dequant order; the spare row staggers banks
-    __shared__ u32x4 As[2][4][4][kBM + 1];
+    // [buffer][k block][k quarter][row ^ (4 k block + k quarter)]: 8 fp16 in dequant order. The
+    // xor spreads both the staging writes (16 lanes: one row, 16 planes) and the fragment reads
+    // (16 lanes: 16 rows, one plane) over distinct banks: SQ_LDS_BANK_CONFLICT reads 0 (a spare row
+    // per plane instead left 40 % of the LDS cycles in conflicts)
+    __shared__ u32x4 As[2][4][4][kBM];
     __shared__ f32x4 Bs[2][kBN / 4];      // bias of the current task, alternating by task parity
 
     const int w = blockIdx.x;
@@ -223,7 +226,7 @@ void prefill_kernel(const PrefillArgs a)
             // 1. this chunk's activations (and, at the task's first chunk, its bias) into LDS
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int e = 0; e < kAC; e++) As[slot][apc[e] >> 2][apc[e] & 3][arow[e]] = perm_k8(xa[e]);
+            for (int e = 0; e < kAC; e++) As[slot][apc[e] >> 2][apc[e] & 3][arow[e] ^ apc[e]] = perm_k8(xa[e]);
             if (c == 0 && threadIdx.x < 64) Bs[q & 1][threadIdx.x] = bv;
             uint32_t zz[4], ss[4];
             {
@@ -247,7 +250,7 @@ void prefill_kernel(const PrefillArgs a)
             u32x4 af[2][kMT];
             f16x8 bf[2][4];
 #pragma unroll
-            for (int tm = 0; tm < kMT; tm++) af[0][tm] = As[slot][0][kq][16 * tm + j];
+            for (int tm = 0; tm < kMT; tm++) af[0][tm] = As[slot][0][kq][(16 * tm + j) ^ kq];
 #pragma unroll
             for (int t = 0; t < 4; t++) bf[0][t] = dequant_word_perm(wq[0][t], zz[t], ss[t]);
             load_w(nx.c, 0);
@@ -256,7 +259,7 @@ void prefill_kernel(const PrefillArgs a)
             for (int kb = 0; kb < 4; kb++) {
                 if (kb < 3) {
 #pragma unroll
-                    for (int tm = 0; tm < kMT; tm++) af[(kb + 1) & 1][tm] = As[slot][kb + 1][kq][16 * tm + j];
+                    for (int tm = 0; tm < kMT; tm++) af[(kb + 1) & 1][tm] = As[slot][kb + 1][kq][(16 * tm + j) ^ (4 * (kb + 1) + kq)];
 #pragma unroll
                     for (int t = 0; t < 4; t++) bf[(kb + 1) & 1][t] = dequant_word_perm(wq[kb + 1][t], zz[t], ss[t]);
                     load_w(nx.c, kb + 1);
