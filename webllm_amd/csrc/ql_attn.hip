@@ -8,18 +8,18 @@
 // h / G, G = H / KV (grouped-query attention).
 //
 // attn_kernel<GM, NJ>: one workgroup (4 waves) per (query row m, run of up to GM heads of one kv
-// group, key split). K and V rows are read once for all the heads of the run.
-//   scores   16 lanes per key, each holding NJ 16-byte pieces of the row (4 floats per 64 of D:
-//            coalesced reads), 4 keys per wave per step, dot products with the GM query vectors
-//            kept in registers, butterfly over the 16 lanes; scores in LDS
-//   softmax  per head: max, e = exp(score - max), sum over the split's keys
-//   output   thread (chunk c of 4 values of D, part q) sums p_s * V[s] over keys s = q mod parts;
-//            the parts are added in ascending order (deterministic)
-// Without a key split (one split) p = e / sum, normalized before weighting V as the reference's
-// CPU attention does, and the workgroup writes the output. With splits (enough workgroups for
-// the chip when rows x heads are few, as in decode) each split writes its max, sum and the
-// unnormalized e-weighted V sums to the context's workspace and attn_combine_kernel merges the
-// splits in ascending order: out = sum_i acc_i exp(max_i - max) / sum_i sum_i exp(max_i - max).
+// group, key split). K and V rows are read once for all the heads of the run, in one pass:
+//   16 lanes per key, each holding NJ 16-byte pieces of the K and V rows (4 floats per 64 of D:
+//   coalesced reads); a wave takes 4 keys per step, every lane two steps' rows in flight. A lane
+//   keeps, per head, the running max, the sum of exp(score - max) and the e-weighted V sums of
+//   its own keys (online softmax: a new max rescales the sums), so no phase waits for another.
+//   The four key lanes of a wave then merge their states (xor 16, xor 32), the four waves merge
+//   through LDS in wave order: state (m, l, acc) and (m', l', acc') give m* = max(m, m'),
+//   l* = l e^(m - m*) + l' e^(m' - m*), acc* likewise.
+// Without a key split the workgroup writes acc / l. With splits (enough workgroups for the chip
+// when rows x heads are few, as in decode) each split writes its max, sum and acc to the
+// context's workspace and attn_combine_kernel merges the splits in ascending order:
+// out = sum_i acc_i exp(max_i - max) / sum_i sum_i exp(max_i - max).
 // Bytes per call: the visible K and V rows once (plus q and out); HBM-bound at long contexts.
 #include <algorithm>
 #include <cmath>
@@ -33,41 +33,36 @@ namespace ql {
 namespace {
 
 constexpr int kAttnThreads = 256;
-constexpr int kAttnLdsFloats = 16384;    // 64 KiB of LDS per workgroup: scores, reductions, parts
 constexpr int kAttnWantBlocks = 512;     // workgroups to aim for (two per CU)
 constexpr int kAttnMinKeys = 64;         // keys per split, at least
 constexpr int kAttnSplitMinT = 512;      // shorter contexts: no key split (the merge launch costs more)
 constexpr int kAttnMinBlocks = 256;      // fewer workgroups: give up sharing K/V rows over heads
-constexpr int kU = 4;                    // K row loads in flight per lane before use
-constexpr int kUV = 8;                   // V row loads in flight per lane before use
+constexpr int kKB = 4;                   // wave steps (4 keys each) whose K and V rows a lane holds
 
-// per-head max or sum over the workgroup; red holds 4 * GM floats; all threads call it
-template <int GM, bool MAX>
-__device__ __forceinline__ void block_reduce(float (&v)[GM], float* red)
+// online-softmax state (m, l, acc) merged with another: the larger max wins, both sides rescaled;
+// a side without keys (m = -inf) contributes nothing
+template <int NJ>
+__device__ __forceinline__ void merge_state(float& m, float& l, f32x4 (&acc)[NJ], float mo, float lo,
+                                            const f32x4 (&ao)[NJ])
 {
-    const int wave = threadIdx.x >> 6;
+    const float mn = fmaxf(m, mo);
+    const float sa = m == -INFINITY ? 0.f : expf(m - mn);
+    const float sb = mo == -INFINITY ? 0.f : expf(mo - mn);
+    l = l * sa + lo * sb;
 #pragma unroll
-    for (int g = 0; g < GM; g++) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float w = __shfl_xor(v[g], o);
-            v[g] = MAX ? fmaxf(v[g], w) : v[g] + w;
-        }
-        if ((threadIdx.x & 63) == 0) red[g * 4 + wave] = v[g];
+    for (int j = 0; j < NJ; j++) {
+        acc[j].x = acc[j].x * sa + ao[j].x * sb;
+        acc[j].y = acc[j].y * sa + ao[j].y * sb;
+        acc[j].z = acc[j].z * sa + ao[j].z * sb;
+        acc[j].w = acc[j].w * sa + ao[j].w * sb;
     }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < GM; g++) {
-        const float* r = red + g * 4;
-        v[g] = MAX ? fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3])) : (r[0] + r[1]) + (r[2] + r[3]);
-    }
-    __syncthreads();
+    m = mn;
 }
 
 template <int GM, int NJ>
 __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a)
 {
-    extern __shared__ float lds[];
+    extern __shared__ float lds[];                                  // [4 waves][GM][D + 4]
     const int run = blockIdx.x, split = blockIdx.y, m = blockIdx.z;
     const int D = a.D, H = a.H, G = a.G;
     const int kvh = run / a.runs_per_group;
@@ -77,10 +72,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a)
     const int T = a.past + m + 1;                                   // visible keys
     const int chunk = (T + a.nsplit - 1) / a.nsplit;
     const int s_lo = min(T, split * chunk), n = min(T, s_lo + chunk) - s_lo;
-    const int cap = a.chunk_cap;
-    float* scores = lds;                                            // [GM][cap]
-    float* red = lds + GM * cap;                                    // [GM][4]
-    float* parts = red + 4 * GM;                                    // [P][GM][D]
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, kq = lane >> 4;
@@ -93,161 +84,193 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a)
             qv[g][j] = (g < ng && d < D) ? *reinterpret_cast<const f32x4*>(a.q + ((size_t)m * H + h0 + g) * D + d)
                                          : f32x4{0.f, 0.f, 0.f, 0.f};
         }
-    const float* kbase = a.k + (size_t)s_lo * row_len + (size_t)kvh * D;
-    // kU steps of 16 keys: every row load of the round is issued before the first dot product
-    for (int i0 = 0; i0 < n; i0 += 16 * kU) {
-        f32x4 kv[kU][NJ];
+    float mr[GM], lr[GM];
+    f32x4 acc[GM][NJ];
 #pragma unroll
-        for (int u = 0; u < kU; u++) {
+    for (int g = 0; g < GM; g++) {
+        mr[g] = -INFINITY;
+        lr[g] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[g][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float* kbase = a.k + (size_t)s_lo * row_len + (size_t)kvh * D;
+    const float* vbase = a.v + (size_t)s_lo * row_len + (size_t)kvh * D;
+    // kKB steps of 16 keys: every K and V row load of the round is issued before the first use
+    for (int i0 = 0; i0 < n; i0 += 16 * kKB) {
+        f32x4 kr[kKB][NJ], vr[kKB][NJ];
+#pragma unroll
+        for (int u = 0; u < kKB; u++) {
             const int i = i0 + 16 * u + wave * 4 + kq;
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
                 const int d = 64 * j + 4 * l16;
-                kv[u][j] = (i < n && d < D) ? *reinterpret_cast<const f32x4*>(kbase + (size_t)i * row_len + d)
-                                            : f32x4{0.f, 0.f, 0.f, 0.f};
+                const bool ok = i < n && d < D;
+                kr[u][j] = ok ? *reinterpret_cast<const f32x4*>(kbase + (size_t)i * row_len + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+                vr[u][j] = ok ? *reinterpret_cast<const f32x4*>(vbase + (size_t)i * row_len + d) : f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
 #pragma unroll
-        for (int u = 0; u < kU; u++) {
-            const int i = i0 + 16 * u + wave * 4 + kq;
+        for (int g = 0; g < GM; g++) {
+            float sc[kKB];
 #pragma unroll
-            for (int g = 0; g < GM; g++) {
+            for (int u = 0; u < kKB; u++) {
                 float dot = 0.f;
 #pragma unroll
                 for (int j = 0; j < NJ; j++) {
-                    dot = fmaf(qv[g][j].x, kv[u][j].x, dot);
-                    dot = fmaf(qv[g][j].y, kv[u][j].y, dot);
-                    dot = fmaf(qv[g][j].z, kv[u][j].z, dot);
-                    dot = fmaf(qv[g][j].w, kv[u][j].w, dot);
+                    dot = fmaf(qv[g][j].x, kr[u][j].x, dot);
+                    dot = fmaf(qv[g][j].y, kr[u][j].y, dot);
+                    dot = fmaf(qv[g][j].z, kr[u][j].z, dot);
+                    dot = fmaf(qv[g][j].w, kr[u][j].w, dot);
                 }
                 dot += __shfl_xor(dot, 8);
                 dot += __shfl_xor(dot, 4);
                 dot += __shfl_xor(dot, 2);
                 dot += __shfl_xor(dot, 1);
-                if (i < n && l16 == 0) scores[g * cap + i] = dot * a.scale;
+                sc[u] = i0 + 16 * u + wave * 4 + kq < n ? dot * a.scale : -INFINITY;
             }
-        }
-    }
-    __syncthreads();
-
-    float mx[GM], sum[GM];
+            float bm = sc[0];
 #pragma unroll
-    for (int g = 0; g < GM; g++) {
-        mx[g] = -INFINITY;
-        for (int i = threadIdx.x; i < n; i += kAttnThreads) mx[g] = fmaxf(mx[g], scores[g * cap + i]);
-    }
-    block_reduce<GM, true>(mx, red);
+            for (int u = 1; u < kKB; u++) bm = fmaxf(bm, sc[u]);
+            const float mn = fmaxf(mr[g], bm);
+            if (mn == -INFINITY) continue;                          // no key of this lane yet
+            const float r = expf(mr[g] - mn);                       // 0 while the state is empty
+            lr[g] *= r;
 #pragma unroll
-    for (int g = 0; g < GM; g++) {
-        sum[g] = 0.f;
-        for (int i = threadIdx.x; i < n; i += kAttnThreads) {
-            const float e = expf(scores[g * cap + i] - mx[g]);
-            scores[g * cap + i] = e;
-            sum[g] += e;
-        }
-    }
-    block_reduce<GM, false>(sum, red);        // its barriers also order the e stores
-    const bool whole = a.nsplit == 1;
-    if (whole) {
-#pragma unroll
-        for (int g = 0; g < GM; g++)
-            for (int i = threadIdx.x; i < n; i += kAttnThreads) scores[g * cap + i] = scores[g * cap + i] / sum[g];
-        __syncthreads();
-    }
-
-    const int nc = D / 4;                     // 4-value chunks of D
-    const int P = kAttnThreads / nc;          // parts over the keys
-    const int c = threadIdx.x % nc, part = threadIdx.x / nc;
-    if (part < P) {
-        f32x4 acc[GM];
-#pragma unroll
-        for (int g = 0; g < GM; g++) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const float* vbase = a.v + (size_t)s_lo * row_len + (size_t)kvh * D + 4 * c;
-        for (int i0 = part; i0 < n; i0 += P * kUV) {
-            f32x4 vv[kUV];
-#pragma unroll
-            for (int u = 0; u < kUV; u++) {
-                const int i = i0 + P * u;
-                vv[u] = i < n ? *reinterpret_cast<const f32x4*>(vbase + (size_t)i * row_len) : f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < NJ; j++) {
+                acc[g][j].x *= r;
+                acc[g][j].y *= r;
+                acc[g][j].z *= r;
+                acc[g][j].w *= r;
             }
 #pragma unroll
-            for (int u = 0; u < kUV; u++) {
-                const int i = i0 + P * u;
-                if (i < n) {
+            for (int u = 0; u < kKB; u++) {
+                const float p = expf(sc[u] - mn);                   // 0 past the split's keys
+                lr[g] += p;
 #pragma unroll
-                    for (int g = 0; g < GM; g++) {
-                        const float p = scores[g * cap + i];
-                        acc[g].x = fmaf(p, vv[u].x, acc[g].x);
-                        acc[g].y = fmaf(p, vv[u].y, acc[g].y);
-                        acc[g].z = fmaf(p, vv[u].z, acc[g].z);
-                        acc[g].w = fmaf(p, vv[u].w, acc[g].w);
-                    }
+                for (int j = 0; j < NJ; j++) {
+                    acc[g][j].x = fmaf(p, vr[u][j].x, acc[g][j].x);
+                    acc[g][j].y = fmaf(p, vr[u][j].y, acc[g][j].y);
+                    acc[g][j].z = fmaf(p, vr[u][j].z, acc[g][j].z);
+                    acc[g][j].w = fmaf(p, vr[u][j].w, acc[g][j].w);
                 }
             }
+            mr[g] = mn;
         }
-#pragma unroll
-        for (int g = 0; g < GM; g++) *reinterpret_cast<f32x4*>(parts + (part * GM + g) * D + 4 * c) = acc[g];
     }
+    // the four key lanes of the wave (kq): merged pairwise; both partners compute the same sums
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1)
+#pragma unroll
+        for (int g = 0; g < GM; g++) {
+            const float mo = __shfl_xor(mr[g], o), lo = __shfl_xor(lr[g], o);
+            f32x4 ao[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                ao[j].x = __shfl_xor(acc[g][j].x, o);
+                ao[j].y = __shfl_xor(acc[g][j].y, o);
+                ao[j].z = __shfl_xor(acc[g][j].z, o);
+                ao[j].w = __shfl_xor(acc[g][j].w, o);
+            }
+            merge_state<NJ>(mr[g], lr[g], acc[g], mo, lo, ao);
+        }
+    // the waves' states through LDS, merged in wave order
+    const int stride = D + 4;
+    if (kq == 0)
+#pragma unroll
+        for (int g = 0; g < GM; g++) {
+            float* st = lds + (size_t)(wave * GM + g) * stride;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int d = 64 * j + 4 * l16;
+                if (d < D) *reinterpret_cast<f32x4*>(st + d) = acc[g][j];
+            }
+            if (l16 == 0) {
+                st[D] = mr[g];
+                st[D + 1] = lr[g];
+            }
+        }
     __syncthreads();
+    const int nc = D / 4;
+    const bool whole = a.nsplit == 1;
     for (int t = threadIdx.x; t < ng * nc; t += kAttnThreads) {
-        const int g = t / nc, cc = t - g * nc;
-        f32x4 o = *reinterpret_cast<const f32x4*>(parts + g * D + 4 * cc);
-        for (int q2 = 1; q2 < P; q2++) {
-            const f32x4 w = *reinterpret_cast<const f32x4*>(parts + (q2 * GM + g) * D + 4 * cc);
-            o.x += w.x;
-            o.y += w.y;
-            o.z += w.z;
-            o.w += w.w;
+        const int g = t / nc, c = t - g * nc;
+        const float* st0 = lds + (size_t)g * stride;
+        float mw = st0[D], lw = st0[D + 1];
+        f32x4 o[1] = {*reinterpret_cast<const f32x4*>(st0 + 4 * c)};
+        for (int w = 1; w < 4; w++) {
+            const float* st = lds + (size_t)(w * GM + g) * stride;
+            const f32x4 ow[1] = {*reinterpret_cast<const f32x4*>(st + 4 * c)};
+            merge_state<1>(mw, lw, o, st[D], st[D + 1], ow);
         }
         const size_t row = (size_t)m * H + h0 + g;                  // (m, h)
         if (whole) {
-            st_global(reinterpret_cast<f32x4*>(a.out + row * D + 4 * cc), o);
+            const float inv = 1.f / lw;
+            st_global(reinterpret_cast<f32x4*>(a.out + row * D + 4 * c),
+                      f32x4{o[0].x * inv, o[0].y * inv, o[0].z * inv, o[0].w * inv});
         } else {
             const size_t slot = row * a.nsplit + split;
-            st_global(reinterpret_cast<f32x4*>(a.ws + slot * D + 4 * cc), o);
-            if (cc == 0) {
-                float* st = a.ws + (size_t)a.M * H * a.nsplit * D + 2 * slot;
-                st_global(st, mx[g]);
-                st_global(st + 1, sum[g]);
+            st_global(reinterpret_cast<f32x4*>(a.ws + slot * D + 4 * c), o[0]);
+            if (c == 0) {
+                float* stt = a.ws + (size_t)a.M * H * a.nsplit * D + 2 * slot;
+                st_global(stt, mw);
+                st_global(stt + 1, lw);
             }
         }
     }
 }
 
-// one wave per (h, m): lane i < S reads split i's max and sum (S <= 64), the wave forms the
-// weights exp(max_i - max) / sum_j sum_j exp(max_j - max) in LDS, then lanes take 4-value chunks
-// of D and add the splits in ascending order
-__global__ __launch_bounds__(64) void attn_combine_kernel(const AttnArgs a)
+// one workgroup per (h, m): wave 0 lane i < S reads split i's max and sum (S <= 64) and forms the
+// weights exp(max_i - max) / sum_j sum_j exp(max_j - max) in LDS; thread (part p, 4-value chunk c)
+// then adds splits p, p + P, ... in ascending order, and the P parts are added in order
+__global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a)
 {
     __shared__ float wgt[64];
-    const int h = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+    __shared__ f32x4 part[256];
+    const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
     const size_t row = (size_t)m * a.H + h;
     const int S = a.nsplit, D = a.D;
-    const float* st = a.ws + (size_t)a.M * a.H * S * D + 2 * row * S;
-    const float mi = lane < S ? ld_global(st + 2 * lane) : -INFINITY;
-    const float li = lane < S ? ld_global(st + 2 * lane + 1) : 0.f;
-    float mx = mi;
+    if (t < 64) {
+        const float* st = a.ws + (size_t)a.M * a.H * S * D + 2 * row * S;
+        const float mi = t < S ? ld_global(st + 2 * t) : -INFINITY;
+        const float li = t < S ? ld_global(st + 2 * t + 1) : 0.f;
+        float mx = mi;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    const float e = lane < S ? expf(mi - mx) : 0.f;
-    float l = li * e;
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float e = t < S && mi != -INFINITY ? expf(mi - mx) : 0.f;
+        float l = li * e;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-    wgt[lane] = e / l;
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+        wgt[t] = e / l;
+    }
     __syncthreads();
-    for (int cc = lane; cc < D / 4; cc += 64) {
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
-        const f32x4* src = reinterpret_cast<const f32x4*>(a.ws + row * S * D) + cc;
-#pragma unroll 8
-        for (int i = 0; i < S; i++) {
+    const int nc = D / 4;
+    const int P = 256 / nc;
+    const int c = t % nc, p = t / nc;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    if (p < P) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(a.ws + row * S * D) + c;
+#pragma unroll 4
+        for (int i = p; i < S; i += P) {
             const float w = wgt[i];
-            const f32x4 v = ld_global(src + (size_t)i * (D / 4));
+            const f32x4 v = ld_global(src + (size_t)i * nc);
             o.x = fmaf(w, v.x, o.x);
             o.y = fmaf(w, v.y, o.y);
             o.z = fmaf(w, v.z, o.z);
             o.w = fmaf(w, v.w, o.w);
         }
-        st_global(reinterpret_cast<f32x4*>(a.out + row * D) + cc, o);
+    }
+    part[t] = o;
+    __syncthreads();
+    if (t < nc) {
+        f32x4 r = part[t];
+        for (int q = 1; q < P; q++) {
+            const f32x4 w = part[q * nc + t];
+            r.x += w.x;
+            r.y += w.y;
+            r.z += w.z;
+            r.w += w.w;
+        }
+        st_global(reinterpret_cast<f32x4*>(a.out + row * D) + t, r);
     }
 }
 
@@ -283,14 +306,14 @@ AttnFn attn_fn(int gm, int nj)
 
 size_t attn_lds_bytes(int gm, int cap, int D)
 {
-    const int P = kAttnThreads / (D / 4);
-    return ((size_t)gm * cap + 4 * gm + (size_t)P * gm * D) * sizeof(float);
+    (void)cap;
+    return (size_t)4 * gm * (D + 4) * sizeof(float);
 }
 
 }  // namespace
 
 // Heads per run (GM: 1, 2, 4 or 8, at most 16 f32x4 of query registers), key splits (enough
-// workgroups, scores within LDS, workspace within its capacity) and the LDS size. Runs of several
+// workgroups, workspace within its capacity) and the LDS size. Runs of several
 // heads read each K/V row once for all of them; while the grid would still be short of
 // kAttnMinBlocks workgroups, fewer heads per run buy parallelism (the rows then come from L2).
 int plan_attention(AttnArgs* a)
@@ -302,11 +325,8 @@ int plan_attention(AttnArgs* a)
     for (;; gm /= 2) {
         const int hpr = std::min(gm, a->G);
         const int runs = a->KV * ((a->G + hpr - 1) / hpr);
-        // scores of gm heads x the split's keys in what the reductions and V parts leave of LDS
-        // (less 4 * gm: the split's key count is rounded up to a multiple of 4, which keeps the
-        // parts after the scores 16-byte aligned)
-        const int budget = kAttnLdsFloats - 8 * gm - (kAttnThreads / (a->D / 4)) * gm * a->D;
-        const int min_split = (int)(((long long)gm * tcap + budget - 1) / budget);
+        // one pass keeps no per-key state in LDS, so any split length fits
+        const int min_split = 1;
         const long long blocks = (long long)runs * a->M;
         int want = (int)std::min<long long>(64, (kAttnWantBlocks + blocks - 1) / blocks);
         want = tcap < kAttnSplitMinT ? 1 : std::min(want, (tcap + kAttnMinKeys - 1) / kAttnMinKeys);
@@ -336,7 +356,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t stream)
     hipLaunchKernelGGL(fn, dim3(a.KV * a.runs_per_group, a.nsplit, a.M), dim3(kAttnThreads), lds, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.H, a.M), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.H, a.M), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
