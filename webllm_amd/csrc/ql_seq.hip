@@ -43,6 +43,9 @@ namespace {
 //   QL_SEQ_STREAM_KB     weight KiB per workgroup from which a pass is planned for streaming
 //                        (several evenly split blocks per workgroup) instead of one block each
 //   QL_SEQ_MIN_GROUPS    fewest groups per K segment when a linear is split across workgroups
+//   QL_SEQ_WHOLE_GROUPS  a latency-bound linear of at most this many groups is not split along K
+//                        (walking its groups costs less than the reduction's round trip: 7B o,
+//                        28 groups, measured faster whole; 0.5B down, 38 groups, split)
 //   QL_SEQ_WG_PER_CU     resident workgroups per CU the grid is sized for
 //   QL_SEQ_PRO_CHUNKS    8-value input chunks per lane whose loads a tile's prologue issues together
 //   QL_SEQ_SENTINEL      1: a tile first polls one word per 64-value input chunk (wave 0), then
@@ -85,6 +88,9 @@ namespace {
 #endif
 #ifndef QL_SEQ_MIN_GROUPS
 #define QL_SEQ_MIN_GROUPS 4
+#endif
+#ifndef QL_SEQ_WHOLE_GROUPS
+#define QL_SEQ_WHOLE_GROUPS 32
 #endif
 #ifndef QL_SEQ_WG_PER_CU
 #define QL_SEQ_WG_PER_CU 2
@@ -1027,6 +1033,7 @@ static int latency_split(const SeqSpec& s, int M, double units)
     const int groups = s.K / s.group;
     int S = (int)(units / ct + 0.5);
     S = std::min(S, std::max(1, groups / kMinGroups));
+    if (groups <= QL_SEQ_WHOLE_GROUPS) S = 1;
     const int mg = max_tile_groups(s, M, true);
     S = std::max({S, 1, (groups + mg - 1) / mg});
     return std::min({S, groups, kSeqMaxSplit});
