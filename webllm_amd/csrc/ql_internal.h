@@ -226,6 +226,7 @@ constexpr int kSeqBiasBlocks = 64;    // most (block, row) pairs whose bias (+ r
 constexpr int kFuseNorm = 1;   // x -> rmsnorm(x) * norm_w at staging
 constexpr int kFuseGlu = 2;    // x -> silu(x) * x2 at staging
 constexpr int kFuseRes = 4;    // y -> y + res in the epilogue
+constexpr int kFuseSsq = 8;    // (tasks only) a consumer normalizes this output: emit its sums of squares
 
 struct SeqLinear {
     const uint32_t* qweight;
@@ -263,7 +264,8 @@ struct SeqTask {
     int32_t g0, g1, slot, stride;
     int32_t parts;
     int32_t next_tile;         // index of the same workgroup's next tile task, or -1
-    int32_t pad[2];
+    int32_t fuse;              // the linear's kFuse* bits (| kFuseSsq), read with the task
+    int32_t pad;
 };
 
 struct SeqArgs {

@@ -550,8 +550,8 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
             const int np = task.parts;
             const size_t slot_words = (size_t)M * kCols;
             const SeqFuseLin* F = FU ? a.fl + task.linear : nullptr;
-            const int fz = FU ? ld_const(&F->fuse) : 0;
-            uint64_t* const fssq = FU ? ld_const(&F->ssq) : nullptr;
+            const int fz = FU ? task.fuse : 0;                  // carried by the task: no table read
+            uint64_t* const fssq = FU && (fz & kFuseSsq) ? ld_const(&F->ssq) : nullptr;
             if constexpr (FU)
                 if ((fz & kFuseNorm) && wave == W - 1) rows_rstd(L, F, e, ok);
             if (QL_SEQ_SENTINEL && wave == 0) {
@@ -639,7 +639,7 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         const uint64_t* p_ll = P ? ld_const(&a.lin[L.src].y_ll) : nullptr;
         // fused staging: x -> rmsnorm(x) * w (NORM) or silu(x) * x2 (GLU)
         const SeqFuseLin* F = FU ? a.fl + task.linear : nullptr;
-        const int fz = FU ? ld_const(&F->fuse) : 0;
+        const int fz = FU ? task.fuse : 0;                      // carried by the task: no table read
         const bool NORM = FU && (fz & kFuseNorm);
         const bool GLU = FU && (fz & kFuseGlu);
         const int src2 = GLU ? ld_const(&F->src2) : -1;
@@ -775,7 +775,7 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         if (!ok) sh_bad = 1;
         __syncthreads();
         if (__builtin_amdgcn_readfirstlane(sh_bad)) return;
-        uint64_t* const fssq = FU && task.slot < 0 ? ld_const(&F->ssq) : nullptr;
+        uint64_t* const fssq = FU && task.slot < 0 && (fz & kFuseSsq) ? ld_const(&F->ssq) : nullptr;
         // one finished output: rstd * sum + staged (bias + residual), stored as value and word
         auto finish = [&](int b, int m, int nc, float v) -> float {
             if constexpr (FU)
@@ -1167,6 +1167,12 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
     p = SeqPlanOut{};
     p.grid = grid;
     const int n = (int)lin.size();
+    // the fuse bits every task of a linear carries: its own, and kFuseSsq when a consumer
+    // normalizes its output (the same rule that gives it a sums-of-squares buffer)
+    std::vector<int32_t> task_fuse(n);
+    for (int i = 0; i < n; i++) task_fuse[i] = lin[i].fuse;
+    for (int c = 0; c < n; c++)
+        if ((lin[c].fuse & kFuseNorm) && lin[c].src >= 0) task_fuse[lin[c].src] |= kFuseSsq;
     p.pass_of.assign(n, 0);
     for (int i = 0; i < n; i++) {
         // after every producer the linear reads: its input, the GLU operand, the residual
@@ -1361,7 +1367,7 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
                 while (e < blocks.size() && e - k < 8 && blocks[e] == blocks[e - 1] + 1 &&
                        (int)parts[i][blocks[e]].size() == np && base[i][blocks[e]] == base[i][blocks[e - 1]] + np)
                     e++;
-                per_wg[w].push_back(SeqTask{i, kSeqReduce, c, (int)(e - k), 0, 0, (int32_t)base[i][c], np, np, -1, {0, 0}});
+                per_wg[w].push_back(SeqTask{i, kSeqReduce, c, (int)(e - k), 0, 0, (int32_t)base[i][c], np, np, -1, task_fuse[i], 0});
                 p.reduces++;
                 k = e;
             }
@@ -1389,7 +1395,7 @@ void plan_seq(const std::vector<SeqSpec>& lin, int M, int grid, SeqPlanOut* out)
                     e++;
                 }
                 per_wg[w].push_back(SeqTask{a.lin, kSeqTile, a.c, (int)(e - k), a.g0, a.g1, (int32_t)s0,
-                                            (int32_t)stride, 0, -1, {0, 0}});
+                                            (int32_t)stride, 0, -1, task_fuse[a.lin], 0});
                 p.tiles++;
                 p.max_gseg = std::max(p.max_gseg, a.g1 - a.g0);
                 // blocks whose parts all sit in this run and end with this tile
