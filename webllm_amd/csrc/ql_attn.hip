@@ -34,9 +34,10 @@ namespace {
 
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWantBlocks = 512;     // workgroups to aim for (two per CU)
-constexpr int kAttnMinKeys = 64;         // keys per split, at least
+constexpr int kAttnMinKeys = 64;         // keys per split, at least (32 measured slower at 7B, 4096 positions)
 constexpr int kAttnSplitMinT = 512;      // shorter contexts: no key split (the merge launch costs more)
 constexpr int kAttnMinBlocks = 256;      // fewer workgroups: give up sharing K/V rows over heads
+constexpr int kAttnMaxSplit = 128;      // key splits at most (the merge takes up to 256)
 constexpr int kKB = 4;                   // wave steps (4 keys each) whose K and V rows a lane holds
 
 // online-softmax state (m, l, acc) merged with another: the larger max wins, both sides rescaled;
@@ -219,28 +220,39 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a)
     }
 }
 
-// one workgroup per (h, m): wave 0 lane i < S reads split i's max and sum (S <= 64) and forms the
-// weights exp(max_i - max) / sum_j sum_j exp(max_j - max) in LDS; thread (part p, 4-value chunk c)
-// then adds splits p, p + P, ... in ascending order, and the P parts are added in order
+// one workgroup per (h, m): wave 0 reads the splits' max and sum (lane i: splits i, i + 64, ...;
+// S <= 256) and forms the weights exp(max_i - max) / sum_j sum_j exp(max_j - max) in LDS (sums
+// in a fixed order); thread (part p, 4-value chunk c) then adds splits p, p + P, ... in ascending
+// order, and the P parts are added in order
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a)
 {
-    __shared__ float wgt[64];
+    __shared__ float wgt[256];
     __shared__ f32x4 part[256];
     const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
     const size_t row = (size_t)m * a.H + h;
     const int S = a.nsplit, D = a.D;
     if (t < 64) {
         const float* st = a.ws + (size_t)a.M * a.H * S * D + 2 * row * S;
-        const float mi = t < S ? ld_global(st + 2 * t) : -INFINITY;
-        const float li = t < S ? ld_global(st + 2 * t + 1) : 0.f;
-        float mx = mi;
+        float mi[4], li[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int i = t + 64 * r;
+            mi[r] = i < S ? ld_global(st + 2 * i) : -INFINITY;
+            li[r] = i < S ? ld_global(st + 2 * i + 1) : 0.f;
+        }
+        float mx = fmaxf(fmaxf(mi[0], mi[1]), fmaxf(mi[2], mi[3]));
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        const float e = t < S && mi != -INFINITY ? expf(mi - mx) : 0.f;
-        float l = li * e;
+        float e[4], l = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            e[r] = mi[r] != -INFINITY ? expf(mi[r] - mx) : 0.f;
+            l += li[r] * e[r];
+        }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-        wgt[t] = e / l;
+#pragma unroll
+        for (int r = 0; r < 4; r++) wgt[t + 64 * r] = e[r] / l;
     }
     __syncthreads();
     const int nc = D / 4;
@@ -328,11 +340,12 @@ int plan_attention(AttnArgs* a)
         // one pass keeps no per-key state in LDS, so any split length fits
         const int min_split = 1;
         const long long blocks = (long long)runs * a->M;
-        int want = (int)std::min<long long>(64, (kAttnWantBlocks + blocks - 1) / blocks);
+        int want = (int)std::min<long long>(kAttnMaxSplit, (kAttnWantBlocks + blocks - 1) / blocks);
         want = tcap < kAttnSplitMinT ? 1 : std::min(want, (tcap + kAttnMinKeys - 1) / kAttnMinKeys);
         int ns = std::max(min_split, std::max(want, 1));
-        const size_t ws = (size_t)a->M * a->H * ns * (a->D + 2) * sizeof(float);
-        if (ns > 1 && ws > kAttnWsBytes) ns = min_split;
+        // as many splits as the workspace holds
+        const int fit = (int)std::min<size_t>(kAttnMaxSplit, kAttnWsBytes / ((size_t)a->M * a->H * (a->D + 2) * sizeof(float)));
+        if (ns > fit) ns = std::max(1, fit);
         const size_t ws2 = (size_t)a->M * a->H * ns * (a->D + 2) * sizeof(float);
         const bool few = (long long)runs * a->M * ns < kAttnMinBlocks && gm > 1;
         if (!few && (ns == 1 || ws2 <= kAttnWsBytes)) {
