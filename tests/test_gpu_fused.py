@@ -130,7 +130,7 @@ def check_fused(orc, m: FusedModel, ys, label, cols_for=None):
     say(f"  {label}: {len(ys)} linears within bar, worst normwise {worst:.3e}")
 
 
-@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
 def test_fused_layers_05b(ql, ctx, orc, M):
     """Two 0.5B-shaped layers (14 linears, 8 dependent passes) in one fused launch; repeated runs
     and graph replays are bit-identical (fixed reduction orders, epochs instead of clears)."""
