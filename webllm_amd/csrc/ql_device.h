@@ -25,6 +25,24 @@ __device__ __forceinline__ uint32_t magic_pair(uint32_t w, int shift)
     return ((w >> shift) & 0x000F000Fu) | 0x64006400u;
 }
 
+// The same with the mask and the fp16 1024 pair in registers (mask uniform, magic per lane), so
+// the and + or is one v_and_or_b32 (three-operand instructions take no literals on gfx950).
+__device__ __forceinline__ uint32_t magic_pair_r(uint32_t w, int shift, uint32_t mask, uint32_t magic)
+{
+    return ((w >> shift) & mask) | magic;
+}
+
+__device__ __forceinline__ f16x8 dequant_word_perm_r(uint32_t w, uint32_t zz, uint32_t ss, uint32_t mask, uint32_t magic)
+{
+    const f16x2 z = as_f16x2(zz);
+    const f16x2 s = as_f16x2(ss);
+    const f16x2 p0 = (as_f16x2(magic_pair_r(w, 0, mask, magic)) - z) * s;
+    const f16x2 p1 = (as_f16x2(magic_pair_r(w, 4, mask, magic)) - z) * s;
+    const f16x2 p2 = (as_f16x2(magic_pair_r(w, 8, mask, magic)) - z) * s;
+    const f16x2 p3 = (as_f16x2(magic_pair_r(w, 12, mask, magic)) - z) * s;
+    return f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
 // fp16 pair (1024 + z, 1024 + z) for a true zero point z in [1, 16].
 __device__ __forceinline__ uint32_t zero_pair(uint32_t z) { return (0x6400u + z) * 0x00010001u; }
 

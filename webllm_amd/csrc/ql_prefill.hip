@@ -131,6 +131,10 @@ void prefill_kernel(const PrefillArgs a)
     const int M = a.M;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, kq = lane >> 4;
+    // dequantization constants held in registers (see magic_pair_r)
+    uint32_t kmask = 0x000F000Fu, kmagic = 0x64006400u;
+    asm volatile("" : "+s"(kmask));
+    asm volatile("" : "+v"(kmagic));
 
     // activation piece e = threadIdx.x + 256 a: row e / 16, 8-k piece e % 16 of the chunk
     int arow[kAC], apc[kAC];
@@ -252,7 +256,7 @@ void prefill_kernel(const PrefillArgs a)
 #pragma unroll
             for (int tm = 0; tm < kMT; tm++) af[0][tm] = As[slot][0][kq][(16 * tm + j) ^ kq];
 #pragma unroll
-            for (int t = 0; t < 4; t++) bf[0][t] = dequant_word_perm(wq[0][t], zz[t], ss[t]);
+            for (int t = 0; t < 4; t++) bf[0][t] = dequant_word_perm_r(wq[0][t], zz[t], ss[t], kmask, kmagic);
             load_w(nx.c, 0);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -261,7 +265,7 @@ void prefill_kernel(const PrefillArgs a)
 #pragma unroll
                     for (int tm = 0; tm < kMT; tm++) af[(kb + 1) & 1][tm] = As[slot][kb + 1][kq][(16 * tm + j) ^ (4 * (kb + 1) + kq)];
 #pragma unroll
-                    for (int t = 0; t < 4; t++) bf[(kb + 1) & 1][t] = dequant_word_perm(wq[kb + 1][t], zz[t], ss[t]);
+                    for (int t = 0; t < 4; t++) bf[(kb + 1) & 1][t] = dequant_word_perm_r(wq[kb + 1][t], zz[t], ss[t], kmask, kmagic);
                     load_w(nx.c, kb + 1);
                 }
 #pragma unroll
