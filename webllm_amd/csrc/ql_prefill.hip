@@ -298,7 +298,7 @@ void prefill_kernel(const PrefillArgs a)
         for (int c = 1; c < cu.nch; c++) chunk(c);
 
         // 4. the tile's outputs, bias added: lane (j, kq) holds rows 16 tm + 4 kq + r of its 4
-        //    adjacent columns
+        //    adjacent columns; streaming stores (the outputs are not read back by the launch)
         const PrefillLinear cl = lin_at<TABLE>(a, cu.li);
         const int ncol = cu.n0 + wave * 64 + 4 * j;
         if (ncol < cl.N) {
@@ -309,18 +309,18 @@ void prefill_kernel(const PrefillArgs a)
                 for (int tm = 0; tm < kMT; tm++)
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        st_global(reinterpret_cast<f32x4*>(yb + (size_t)(16 * tm + r) * cl.N),
-                                  f32x4{acc[tm][0][r] + bias.x, acc[tm][1][r] + bias.y, acc[tm][2][r] + bias.z,
-                                        acc[tm][3][r] + bias.w});
+                        __builtin_nontemporal_store(f32x4{acc[tm][0][r] + bias.x, acc[tm][1][r] + bias.y, acc[tm][2][r] + bias.z,
+                                        acc[tm][3][r] + bias.w}, reinterpret_cast<f32x4*>(yb + (size_t)(16 * tm + r) * cl.N));
             } else {
 #pragma unroll
                 for (int tm = 0; tm < kMT; tm++)
 #pragma unroll
                     for (int r = 0; r < 4; r++)
                         if (cu.m0 + 16 * tm + 4 * kq + r < M)
-                            st_global(reinterpret_cast<f32x4*>(yb + (size_t)(16 * tm + r) * cl.N),
+                            __builtin_nontemporal_store(
                                       f32x4{acc[tm][0][r] + bias.x, acc[tm][1][r] + bias.y,
-                                            acc[tm][2][r] + bias.z, acc[tm][3][r] + bias.w});
+                                            acc[tm][2][r] + bias.z, acc[tm][3][r] + bias.w},
+                                      reinterpret_cast<f32x4*>(yb + (size_t)(16 * tm + r) * cl.N));
             }
         }
     }
