@@ -517,7 +517,7 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
                  const std::vector<ql::SeqSpec>& specs, ql_seq** out)
 {
     ql::StripPlan sp;
-    ql::plan_strips(specs, M, ql::strip_grid(ctx->cu_count, specs), &sp);
+    ql::plan_strips(specs, M, ql::strip_grid(ctx->cu_count, specs, M), &sp);
     const StripLayout lay = strip_layout(specs, sp);
     char* dev = nullptr;
     QL_HIP(hipMalloc(&dev, lay.total));

@@ -360,7 +360,7 @@ struct StripPlan {
 };
 
 bool strip_eligible(const std::vector<SeqSpec>& lin, int M);
-int strip_grid(int cu_count, const std::vector<SeqSpec>& lin);   // workgroups of a strip launch
+int strip_grid(int cu_count, const std::vector<SeqSpec>& lin, int M);   // workgroups of a strip launch
 constexpr uint64_t kStripMallBytes = 192ull << 20;   // weights that stay resident in the MALL
 size_t strip_lds(int M, int group, int split);
 void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out);

@@ -78,8 +78,15 @@ constexpr int kMaxStripBlocks = 8;       // most blocks in one strip
 //   4. wait for step 1's loads (the kCG positions' loads stay in flight), turn them into digits
 //      in the other LDS buffer, stage the next strip's bias with its first chunk;
 //   5. one barrier.
+// Waves per SIMD that the M 5..8 instance reading MALL-resident weights is compiled for (at most
+// 128 VGPRs): 4 lets a CU hold both of its workgroups (the 0.5B step at M=8: 48.7 against
+// 53.6 us). The streaming instance keeps the compiler's choice (143 VGPRs): capped at 128 it
+// spills and the 7B step at M=8 takes 773 against 664 us (711 with two workgroups per CU).
+#ifndef QL_STRIP_OCC2
+#define QL_STRIP_OCC2 4
+#endif
 template <int T, int NB, int W, int BPW, int P, int S, bool NT>
-__global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
+__global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void strip_kernel(const StripArgs a)
 {
     // S waves share each block (S > 1: waves take alternate groups of every chunk and add their
     // sums in LDS at the strip's end, in part order); QP positions per chunk for each wave
@@ -323,20 +330,19 @@ __global__ __launch_bounds__(64 * W) void strip_kernel(const StripArgs a)
     auto consume = [&](int d, int buf, int gg, int nbw) {
         const uint4* xd = digits(buf);
         const float2* gst = gstat(buf);
+        // Digit rows past the last (R and up) and group statistics of rows past M read the last
+        // valid ones instead of zeros: they only feed output rows m >= M, which are never stored,
+        // and the loads need no lane masking.
         i32x4 av[NB][T];
 #pragma unroll
         for (int bb = 0; bb < NB; bb++)
 #pragma unroll
-            for (int t = 0; t < T; t++) {
-                const int row = 16 * t + j;
-                av[bb][t] = row < R ? __builtin_bit_cast(i32x4, xd[((gg * NB + bb) * 4 + kq) * R + row])
-                                    : i32x4{0, 0, 0, 0};
-            }
+            for (int t = 0; t < T; t++)
+                av[bb][t] = __builtin_bit_cast(i32x4, xd[((gg * NB + bb) * 4 + kq) * R + min(16 * t + j, R - 1)]);
         float2 st[T];
 #pragma unroll
         for (int t = 0; t < T; t++) {
-            const int m = 4 * t + kq;
-            st[t] = m < M ? gst[gg * M + m] : float2{0.f, 0.f};
+            st[t] = gst[gg * M + min(4 * t + kq, M - 1)];
             st[t].x *= 0x1p-8f;       // the digit pairs below carry a factor 2^8
         }
 #pragma unroll
@@ -545,11 +551,17 @@ StripKernel strip_kernel_for(int M, int group, int split, bool stream)
 
 // Two workgroups per CU when the weights stay in the 256 MB MALL (the 0.5B step: 39.9 against
 // 41.6 us per step), one when they stream from HBM (the 7B step: 557 against 566 us).
-int strip_grid(int cu_count, const std::vector<SeqSpec>& lin)
+// A CU holds two workgroups of the M <= 8 instances only (the M 9..16 instance takes 215 VGPRs,
+// two waves per SIMD), so MALL-resident plans for M 9..16 use one workgroup per CU (the 0.5B step
+// at M=16: 81.2 against 83.8 us with a second workgroup that waits for the first).
+#ifndef QL_STRIP_MALL2_MAX_M
+#define QL_STRIP_MALL2_MAX_M 8
+#endif
+int strip_grid(int cu_count, const std::vector<SeqSpec>& lin, int M)
 {
     uint64_t bytes = 0;
     for (const SeqSpec& s : lin) bytes += s.weight_bytes;
-    return cu_count * (bytes <= kStripMallBytes ? 2 : 1);
+    return cu_count * (bytes <= kStripMallBytes && M <= QL_STRIP_MALL2_MAX_M ? 2 : 1);
 }
 
 bool strip_eligible(const std::vector<SeqSpec>& lin, int M)
