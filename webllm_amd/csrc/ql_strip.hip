@@ -94,6 +94,12 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
     constexpr int QP = kCG / S;
     static_assert(QP * S == kCG && QP % P == 0, "a chunk's positions fill whole ring rounds");
     constexpr int WB = W / S;                // waves per part = blocks per strip / BPW
+    // The M 5..8 instance on MALL-resident weights is compiled for four waves per SIMD (at most
+    // 128 VGPRs). It computes one column quarter's sums at a time and keeps one lane offset for
+    // its weight loads, which frees the registers it would otherwise spill (the 0.5B step at M=8:
+    // 42.3 against 48.3 us). The other instances keep all quarters' sums and per-row offsets,
+    // which measured 1-2 % faster for them (the 7B step at M = 1, 8, 16).
+    constexpr bool kLean = T == 2 && !NT;
     extern __shared__ uint4 dyn_lds[];
     constexpr int GK = NB * 64;              // k per group
     constexpr int CPG = NB * 8;              // lanes per (group, row) when staging
@@ -240,7 +246,9 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
         const char* sc;
         uint32_t Gq, Gz, Gs;        // bytes from one group to the next
         uint32_t cq, cz, cs;        // byte offsets of the wave's first block
-        uint32_t lq[2 * NB], lz, ls;
+        uint32_t Rq;                // bytes of one packed row (N words)
+        // the lane's byte offsets: of each packed row it loads, or (kLean) of the first only
+        uint32_t lq[kLean ? 1 : 2 * NB], lz, ls;
     };
     auto blocks_of = [&](const StripTask& t) { return max(0, min(BPW, t.nblk - bw * BPW)); };
     auto open = [&](Cur& c, int ti) {
@@ -268,8 +276,9 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
         c.cq = blk0 * (uint32_t)kCols * 4u;
         c.cs = blk0 * (uint32_t)kCols * 2u;
         c.cz = blk0 * (uint32_t)(kCols / 8) * 4u;
+        c.Rq = (uint32_t)N * 4u;
 #pragma unroll
-        for (int r = 0; r < 2 * NB; r++)
+        for (int r = 0; r < (kLean ? 1 : 2 * NB); r++)
             c.lq[r] = ((uint32_t)(2 * kq + (r >> 1) * 8 + (r & 1)) * (uint32_t)N + 4u * (uint32_t)j) * 4u;
         c.ls = 8u * (uint32_t)j;
         c.lz = (uint32_t)(j >> 1) * 4u;
@@ -297,9 +306,13 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
             const uint32_t bb = (uint32_t)min(b, max(c.nbw, 1) - 1);   // extra blocks re-read the first
             const char* q = c.qw + g * c.Gq + c.cq + bb * (uint32_t)kCols * 4u;
 #pragma unroll
-            for (int r = 0; r < 2 * NB; r++)
-                wb[d][b][r] = __builtin_bit_cast(uint4, NT ? ld_stream(reinterpret_cast<const u32x4*>(q + c.lq[r]))
-                                                           : ld_global(reinterpret_cast<const u32x4*>(q + c.lq[r])));
+            for (int r = 0; r < 2 * NB; r++) {
+                // packed row 2 kq + 8 (r / 2) + r % 2 of the group (kLean: a uniform row offset on
+                // top of the lane's one)
+                const char* qr = kLean ? q + (uint32_t)((r >> 1) * 8 + (r & 1)) * c.Rq + c.lq[0] : q + c.lq[kLean ? 0 : r];
+                wb[d][b][r] = __builtin_bit_cast(uint4, NT ? ld_stream(reinterpret_cast<const u32x4*>(qr))
+                                                           : ld_global(reinterpret_cast<const u32x4*>(qr)));
+            }
             zb[d][b] = ld_global(reinterpret_cast<const uint32_t*>(c.qz + g * c.Gz + c.cz + bb * (uint32_t)(kCols / 8) * 4u + c.lz));
             sb[d][b] = __builtin_bit_cast(uint2, ld_global(reinterpret_cast<const u32x2*>(c.sc + g * c.Gs + c.cs + bb * (uint32_t)kCols * 2u + c.ls)));
         }
@@ -351,39 +364,57 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
                 touch_block(d, b);
                 continue;
             }
-            i32x4 c[4][T];
-#pragma unroll
-            for (int bb = 0; bb < NB; bb++) {
-                const uint4 w0 = wb[d][b][2 * bb], w1 = wb[d][b][2 * bb + 1];
-                const uint32_t lo[4] = {w0.x, w0.y, w0.z, w0.w};
-                const uint32_t hi[4] = {w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const i32x4 bq = i32x4{(int)(lo[u] & 0x0F0F0F0Fu), (int)((lo[u] >> 4) & 0x0F0F0F0Fu),
-                                           (int)(hi[u] & 0x0F0F0F0Fu), (int)((hi[u] >> 4) & 0x0F0F0F0Fu)};
-                    // the first 64-k block starts each sum from an inline zero (no register setup)
-#pragma unroll
-                    for (int t = 0; t < T; t++)
-                        c[u][t] = mfma_i8(av[bb][t], bq, bb == 0 ? i32x4{0, 0, 0, 0} : c[u][t]);
-                }
-            }
             const uint32_t zw = zb[d][b] >> (4 * ((4 * j) & 7));
             const uint2 sv = sb[d][b];
             const uint32_t sw[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
+            // the weight nibbles of 64-k block bb, column quarter u, as bytes
+            auto bq_of = [&](int bb, int u) {
+                const uint4 w0 = wb[d][b][2 * bb], w1 = wb[d][b][2 * bb + 1];
+                const uint32_t lo[4] = {w0.x, w0.y, w0.z, w0.w};
+                const uint32_t hi[4] = {w1.x, w1.y, w1.z, w1.w};
+                return i32x4{(int)(lo[u] & 0x0F0F0F0Fu), (int)((lo[u] >> 4) & 0x0F0F0F0Fu),
+                             (int)(hi[u] & 0x0F0F0F0Fu), (int)((hi[u] >> 4) & 0x0F0F0F0Fu)};
+            };
+            // the group epilogue of column quarter u from its T digit sums
+            auto quarter = [&](int u, const i32x4* cu) {
                 const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
                 const float sz = s * (float)(((zw >> (4 * u)) & 15u) + 1u);
 #pragma unroll
                 for (int t = 0; t < T; t++) {
                     // digit products (|c| < 2^18, digit 3 most significant) in two exact integer
                     // pairs: 2^8 * sum_d c_d 2^(8d-24) = (c0 + 2^8 c1) 2^-16 + (c2 + 2^8 c3)
-                    const int lo2 = c[u][t][0] + c[u][t][1] * 256;
-                    const int hi2 = c[u][t][2] + c[u][t][3] * 256;
+                    const int lo2 = cu[t][0] + cu[t][1] * 256;
+                    const int hi2 = cu[t][2] + cu[t][3] * 256;
                     const float v = fmaf((float)lo2, 0x1p-16f, (float)hi2);
                     acc[b][u][t] = fmaf(s * st[t].x, v, acc[b][u][t]);
                     acc[b][u][t] = fmaf(-sz, st[t].y, acc[b][u][t]);
                 }
+            };
+            // the first 64-k block starts each sum from an inline zero (no register setup)
+            if constexpr (kLean) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    i32x4 c[T];
+#pragma unroll
+                    for (int bb = 0; bb < NB; bb++) {
+                        const i32x4 bq = bq_of(bb, u);
+#pragma unroll
+                        for (int t = 0; t < T; t++) c[t] = mfma_i8(av[bb][t], bq, bb == 0 ? i32x4{0, 0, 0, 0} : c[t]);
+                    }
+                    quarter(u, c);
+                }
+            } else {
+                i32x4 c[4][T];
+#pragma unroll
+                for (int bb = 0; bb < NB; bb++)
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const i32x4 bq = bq_of(bb, u);
+#pragma unroll
+                        for (int t = 0; t < T; t++) c[u][t] = mfma_i8(av[bb][t], bq, bb == 0 ? i32x4{0, 0, 0, 0} : c[u][t]);
+                    }
+#pragma unroll
+                for (int u = 0; u < 4; u++) quarter(u, c[u]);
             }
         }
     };
