@@ -262,7 +262,8 @@ def indep7b(ql, ctx):
     m.weights.release()
 
 
-@pytest.mark.parametrize("M", [1, 2, 8, 16])
+# M = 5 and 11 leave the last 16-row digit tile partly past the rows (those rows' loads clamp)
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 11, 16])
 def test_strips_7b_independent(ql, ctx, orc, indep7b, M):
     """Fifteen independent 7B-shaped linears (360 MB, each on its own fp32 input) at M rows run
     as column strips (no K split, nothing reduced): linears with bias, without qzeros and the
@@ -314,7 +315,7 @@ def test_strips_7b_independent(ql, ctx, orc, indep7b, M):
     act.release()
 
 
-@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("M", [1, 4, 6, 13, 16])
 def test_strips_05b_split_blocks(ql, ctx, orc, M):
     """Two layers of 0.5B-shaped independent linears: strips of 4 blocks with two waves per block
     (each wave takes alternate groups of every chunk; part sums added in LDS in part order).
