@@ -210,6 +210,18 @@ int ql_kv_store(ql_ctx* ctx, const ql_arena* act, uint64_t src_off, ql_arena* ca
 int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_arena* cache, uint64_t k_off,
                         uint64_t v_off, int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D,
                         int32_t past_len, uint64_t out_off);
+/* ql_plan_attention (diagnostic, host only): the launch shape ql_attention_decode picks for these
+ *   dimensions, with the same checks (no counterpart in the reference, whose attention is one
+ *   dispatch per layer, qwen.ts:430-442). heads_per_run query heads share each K/V row read;
+ *   nsplit key splits (1 = no merge launch); workgroups of the attention launch. */
+typedef struct ql_attn_info {
+    int32_t heads_per_run;
+    int32_t nsplit;
+    int32_t workgroups;
+    int32_t keys_per_split;
+} ql_attn_info;
+int ql_plan_attention(int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D, int32_t past_len,
+                      ql_attn_info* info);
 
 /* ---- the elementwise work around the linears (qwen.ts:401-405, :447-478).
  * ql_add_rmsnorm: s = x + d (misc/vec_add.wgsl: the residual add after o_proj / down_proj), stored
@@ -269,7 +281,9 @@ typedef struct ql_seq_info {
     int32_t split;        /* strips: waves per 64-column block (1: strips of 8 blocks, 2: of 4) */
     int32_t stream;       /* strips: 1 when the packed weights are read with streaming loads (the
                              weights exceed what the 256 MB MALL keeps between steps) */
-    int32_t reserved;
+    int32_t variant;      /* strips: 1 when the launch is the no-padding kernel for M = 5..16 on
+                             streamed weights (every linear: group 128, K a multiple of 512, N a
+                             multiple of 512); 0 otherwise */
 } ql_seq_info;
 /* plan only (host, pure) for a given grid size: validation and the figures above */
 int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,

@@ -134,3 +134,18 @@ def test_null_handles_are_errors_not_crashes(ql):
     assert L.ql_graph_destroy(None) == -10
     assert L.ql_arena_size(None) == 0
     assert b"null" in L.ql_last_error()
+
+
+def test_attention_plans(ql):
+    """ql_plan_attention (host only): each GPU attention case's heads per run and key splits, as
+    the GPU test asserts them before its launch, including 128 splits and the workspace cap."""
+    from tests.test_gpu_attn import CASES
+
+    for M, H, KV, D, past, max_t, hpr, nsplit, label in CASES:
+        plan = ql.plan_attention(max_t, M, H, KV, D, past)
+        assert (plan.heads_per_run, plan.nsplit) == (hpr, nsplit), label
+        assert plan.workgroups >= 1 and plan.keys_per_split * plan.nsplit >= past + M
+    with pytest.raises(ql.QlError):
+        ql.plan_attention(8192, 2, 28, 4, 128, 8191)      # past + M beyond the cache
+    with pytest.raises(ql.QlError):
+        ql.plan_attention(64, 1, 6, 4, 64, 0)             # H not a multiple of KV

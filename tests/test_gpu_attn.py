@@ -1,8 +1,8 @@
 """GPU parity of the decode attention over the KV cache and of the cache store (qwen.ts:424-442,
 attention/attention_gqa_cache.wgsl, misc/kv_store.wgsl) against the oracle's attentionGqaRef
 restatement (reference/qwen-ref.ts:65-111). Decode shapes (few rows x heads) split the keys over
-workgroups and merge the splits in a second kernel; the cases cover one split and 2 to 64, runs
-of 1 to 8 heads sharing a kv head and head dims 16 to 256. Bar: the reference's own attention
+workgroups and merge the splits in a second kernel; the cases cover one split and 10 to 128, runs
+of 1 to 8 heads sharing a kv head, head dims 16 to 256 and a plan that the split workspace caps. Bar: the reference's own attention
 tolerance, 1e-4
 (tests/kernels.ts:1115), applied here as |got - ref| <= 1e-5 + 1e-4 |ref|; the cache store is a
 copy and is bit-exact."""
@@ -24,18 +24,20 @@ def say(*a):
 
 
 CASES = [
-    # (M, H, KV, D, past, max_t, label)
-    (1, 14, 2, 64, 0, 128, "0.5B decode, first position"),
-    (1, 14, 2, 64, 127, 128, "0.5B decode, full 128-position cache"),
-    (16, 14, 2, 64, 100, 128, "16 rows over a cache (prefill continuation), causal"),
-    (1, 28, 4, 128, 4095, 4096, "7B decode, 4096 positions"),
-    (3, 6, 3, 48, 20, 64, "D = 48 (not a multiple of 64), group 2"),
-    (2, 8, 8, 16, 5, 8, "no grouping (H = KV), past + M = max_t"),
-    (1, 14, 2, 64, 1000, 1024, "0.5B heads over 1001 positions: 8 key splits"),
-    (2, 4, 1, 64, 600, 1024, "4 heads on one kv head: 10 key splits"),
-    (520, 1, 1, 16, 0, 1024, "520 rows from position 0: enough workgroups, one split"),
-    (600, 8, 1, 64, 500, 1100, "8 heads on one kv head, 1100 positions: LDS forces 2 key splits"),
-    (1, 8, 2, 256, 700, 1024, "D = 256: runs of 4 heads, key splits"),
+    # (M, H, KV, D, past, max_t, heads per run, key splits, label): the plan is asserted
+    (1, 14, 2, 64, 0, 128, 1, 1, "0.5B decode, first position"),
+    (1, 14, 2, 64, 127, 128, 1, 1, "0.5B decode, full 128-position cache"),
+    (16, 14, 2, 64, 100, 128, 1, 1, "16 rows over a cache (prefill continuation), causal"),
+    (1, 28, 4, 128, 4095, 4096, 7, 64, "7B decode, 4096 positions: 64 key splits"),
+    (1, 28, 4, 128, 8191, 8192, 7, 128, "7B decode, 8192 positions: 128 key splits (merge reads splits 65-128)"),
+    (3, 6, 3, 48, 20, 64, 1, 1, "D = 48 (not a multiple of 64), group 2"),
+    (2, 8, 8, 16, 5, 8, 1, 1, "no grouping (H = KV), past + M = max_t"),
+    (1, 14, 2, 64, 1000, 1024, 1, 16, "0.5B heads over 1001 positions: 16 key splits"),
+    (2, 4, 1, 64, 600, 1024, 1, 10, "4 heads on one kv head: 10 key splits"),
+    (520, 1, 1, 16, 0, 1024, 1, 1, "520 rows from position 0: enough workgroups, one split"),
+    (600, 8, 1, 64, 500, 1100, 8, 1, "8 heads on one kv head, 1100 positions: runs of 8 heads, one split"),
+    (1, 8, 2, 256, 700, 1024, 1, 11, "D = 256: one head per run, 11 key splits"),
+    (32, 128, 8, 256, 600, 640, 4, 1, "workspace cap: 32 rows x 128 heads of 256 leave room for one split"),
 ]
 
 
@@ -57,9 +59,12 @@ def _setup(ql, ctx, M, H, KV, D, past, max_t, seed):
     return rows, q, act, src, q_off, o_off, cache, k_off, v_off
 
 
-@pytest.mark.parametrize("M,H,KV,D,past,max_t,label", CASES)
-def test_attention_matches_oracle(ql, ctx, orc, M, H, KV, D, past, max_t, label):
-    say(f"attention {label}: M={M} H={H} KV={KV} D={D} past={past} max_t={max_t}")
+@pytest.mark.parametrize("M,H,KV,D,past,max_t,hpr,nsplit,label", CASES)
+def test_attention_matches_oracle(ql, ctx, orc, M, H, KV, D, past, max_t, hpr, nsplit, label):
+    plan = ql.plan_attention(max_t, M, H, KV, D, past)
+    say(f"attention {label}: M={M} H={H} KV={KV} D={D} past={past} max_t={max_t}: heads per run "
+        f"{plan.heads_per_run}, {plan.nsplit} key splits, {plan.workgroups} workgroups")
+    assert (plan.heads_per_run, plan.nsplit) == (hpr, nsplit)
     rows, q, act, src, q_off, o_off, cache, k_off, v_off = _setup(ql, ctx, M, H, KV, D, past, max_t, 0xA77 + past)
     T = past + M
     # the cache filled the way a step does it: earlier positions, then this call's rows

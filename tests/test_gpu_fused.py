@@ -235,11 +235,42 @@ def test_chained_step_05b_full_size(ql, ctx, orc, bench_mod):
     model.arena.release()
 
 
-@pytest.mark.parametrize("M", [1, 4])
-def test_chained_step_7b_full_size(ql, ctx, orc, bench_mod, M):
-    """The bench's chained 7B step (28 fused layers, 112 passes, 3.35 GB, one launch): every
-    linear on a sample of 64-column blocks; finite to the last layer."""
-    model = bench_mod.Model(ctx, "7b", seed=0x7B, keep_tensors=True)
+def test_chained_step_05b_bounded_waits_abort(ql, ctx, orc, bench_mod):
+    """The pass-break contract (qwen.ts:556-559) made safe: with a spin limit of 64 polls the
+    kernel's own bounded waits give up on the chained 0.5B step (96 dependent passes), every
+    workgroup exits, and ql_seq_status reports QL_E_STATE; after the default limit is restored the
+    next run completes and matches the oracle."""
+    model = bench_mod.Model(ctx, "0.5b", seed=0x9EF0, keep_tensors=True)
+    st = bench_mod.SeqStep(ctx, model, 1, chained=True)
+    assert st.info.kernel == ql.SEQ_TILES and st.info.passes == 96
+    st.seq.set_spin_limit(64)
+    say("chained 0.5B step, spin limit 64: expecting an abort")
+    st.seq.run()
+    with pytest.raises(ql.QlError) as exc:
+        st.seq.status()
+    assert exc.value.name == "QL_E_STATE", exc.value
+    say(f"  aborted as expected: {exc.value}")
+    st.seq.set_spin_limit(1 << 22)
+    st.seq.run()
+    st.seq.status()
+    assert st.finite()
+    check_step(orc, model, st, lambda N: np.arange(N, dtype=np.int32), "chained 0.5B M=1 after abort")
+    st.release()
+    model.arena.release()
+
+
+@pytest.fixture(scope="module")
+def model7b_chained(ctx, bench_mod):
+    m = bench_mod.Model(ctx, "7b", seed=0x7B, keep_tensors=True)
+    yield m
+    m.arena.release()
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_chained_step_7b_full_size(ql, ctx, orc, bench_mod, model7b_chained, M):
+    """The bench's chained 7B step (28 fused layers, 112 passes, 3.35 GB, one launch) at every M
+    bench times it: every linear on a sample of 64-column blocks; finite to the last layer."""
+    model = model7b_chained
     st = bench_mod.SeqStep(ctx, model, M, chained=True)
     say(f"chained 7B step M={M}: {st.info.as_dict()}")
     assert st.info.kernel == ql.SEQ_TILES and st.info.passes == 112
@@ -247,4 +278,3 @@ def test_chained_step_7b_full_size(ql, ctx, orc, bench_mod, M):
     assert st.finite()
     check_step(orc, model, st, _sample, f"chained 7B M={M}")
     st.release()
-    model.arena.release()

@@ -303,14 +303,21 @@ def test_strips_stream_weights_the_mall_cannot_keep():
     small = c.plan(grid=512)
     assert small.kernel == ql.SEQ_STRIPS and small.stream == 0
     big = qwen7b(Chain(M=1), 28, chained=False).plan(grid=256)
-    assert big.kernel == ql.SEQ_STRIPS and big.stream == 1
+    assert big.kernel == ql.SEQ_STRIPS and big.stream == 1 and big.variant == 0
+    # M 5..16 on the streamed 7B shapes: the no-padding strip kernel; the 0.5B step (MALL-resident,
+    # K = 896 is 7 groups) keeps the general one
+    for M in (5, 8, 9, 16):
+        wide = qwen7b(Chain(M=M), 28, chained=False).plan(grid=256)
+        assert wide.kernel == ql.SEQ_STRIPS and wide.stream == 1 and wide.variant == 1, M
+    for M in (1, 4):
+        assert qwen7b(Chain(M=M), 28, chained=False).plan(grid=256).variant == 0
     # chained sequences (dependency-ordered tiles) report no streaming
     assert qwen7b(Chain(M=1), 2, chained=True).plan(grid=256).stream == 0
 
 
 def test_seq_info_struct_matches_the_library():
     """ql_plan_seq writes exactly sizeof(SeqInfo) bytes: a guard area after the ctypes struct stays
-    untouched and the struct's last field (reserved) comes back zeroed."""
+    untouched and the struct's last field (variant) comes back zeroed."""
     import ctypes
     c = Chain(M=1)
     c.add(896, 896, c.ext(896))
@@ -322,7 +329,7 @@ def test_seq_info_struct_matches_the_library():
     assert rc == 0
     assert bytes(buf[size:]) == b"\xaa" * 64
     info = ql.SeqInfo.from_buffer_copy(bytes(buf[:size]))
-    assert info.reserved == 0 and info.linears == 1
+    assert info.variant == 0 and info.linears == 1
 
 
 def fused_layers(c: Chain, layers: int, C=896, I=4864, KV=128):

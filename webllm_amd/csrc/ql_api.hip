@@ -484,7 +484,7 @@ void fill_strip_info(const ql::StripPlan& p, int n, uint64_t scratch, ql_seq_inf
     info->kernel = QL_SEQ_STRIPS;
     info->split = p.split;
     info->stream = p.stream ? 1 : 0;
-    info->reserved = 0;
+    info->variant = p.wide ? 1 : 0;
 }
 
 void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info* info)
@@ -502,7 +502,7 @@ void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info
     info->kernel = QL_SEQ_TILES;
     info->split = 1;
     info->stream = 0;
-    info->reserved = 0;
+    info->variant = 0;
 }
 
 int set_device(ql_ctx* ctx)
@@ -564,6 +564,7 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     q->sargs.group = descs[0].group;
     q->sargs.split = sp.split;
     q->sargs.stream = sp.stream ? 1 : 0;
+    q->sargs.wide = sp.wide ? 1 : 0;
     fill_strip_info(sp, n, lay.total, &q->info);
     *out = q;
     return QL_OK;
@@ -1188,11 +1189,11 @@ int ql_kv_store(ql_ctx* ctx, const ql_arena* act, uint64_t src_off, ql_arena* ca
     return QL_OK;
 }
 
-int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_arena* cache, uint64_t k_off,
-                        uint64_t v_off, int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D,
-                        int32_t past_len, uint64_t out_off)
+namespace {
+
+// The dimension checks shared by ql_attention_decode and ql_plan_attention.
+int check_attention_dims(int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D, int32_t past_len)
 {
-    if (!ctx || !act || !cache) return fail(QL_E_INVALID, "null context or arena");
     if (M < 1 || M > 65535 || n_head < 1 || n_head > 65535 || n_kv_head < 1 || past_len < 0 || max_t < 1)
         return fail(QL_E_INVALID, "bad attention dimensions");
     if (n_head % n_kv_head) return fail(QL_E_INVALID, "n_head (%d) must be a multiple of n_kv_head (%d)", n_head, n_kv_head);
@@ -1201,6 +1202,39 @@ int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_are
         return fail(QL_E_RANGE, "context length %lld exceeds the cache's %d positions", (long long)past_len + M, max_t);
     if ((int64_t)past_len + M > ql::kAttnMaxT)
         return fail(QL_E_INVALID, "context length %lld above the supported %d", (long long)past_len + M, ql::kAttnMaxT);
+    return QL_OK;
+}
+
+}  // namespace
+
+int ql_plan_attention(int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D, int32_t past_len,
+                      ql_attn_info* info)
+{
+    if (!info) return fail(QL_E_INVALID, "null info");
+    int rc = check_attention_dims(max_t, M, n_head, n_kv_head, D, past_len);
+    if (rc) return rc;
+    ql::AttnArgs a{};
+    a.M = M;
+    a.H = n_head;
+    a.KV = n_kv_head;
+    a.G = n_head / n_kv_head;
+    a.D = D;
+    a.past = past_len;
+    if (ql::plan_attention(&a)) return fail(QL_E_INVALID, "attention shape does not fit the workspace");
+    info->heads_per_run = a.heads_per_run;
+    info->nsplit = a.nsplit;
+    info->workgroups = a.KV * a.runs_per_group * a.nsplit * a.M;
+    info->keys_per_split = a.chunk_cap;
+    return QL_OK;
+}
+
+int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_arena* cache, uint64_t k_off,
+                        uint64_t v_off, int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D,
+                        int32_t past_len, uint64_t out_off)
+{
+    if (!ctx || !act || !cache) return fail(QL_E_INVALID, "null context or arena");
+    int rc = check_attention_dims(max_t, M, n_head, n_kv_head, D, past_len);
+    if (rc) return rc;
     const uint64_t qo = (uint64_t)M * n_head * D * 4, cb = (uint64_t)max_t * n_kv_head * D * 4;
     if (!in_range(q_off, qo, act->size)) return fail(QL_E_RANGE, "q [M, n_head, D] outside the activation arena");
     if (!in_range(out_off, qo, act->size)) return fail(QL_E_RANGE, "out [M, n_head, D] outside the activation arena");
@@ -1208,7 +1242,7 @@ int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_are
         return fail(QL_E_RANGE, "K/V cache [max_t, n_kv_head * D] outside its arena");
     if (q_off % 16 || out_off % 16 || k_off % 16 || v_off % 16) return fail(QL_E_ALIGN, "offsets must be 16-byte aligned");
     if (q_off < out_off + qo && out_off < q_off + qo) return fail(QL_E_INVALID, "q and out overlap");
-    int rc = set_device(ctx);
+    rc = set_device(ctx);
     if (rc) return rc;
     ql::AttnArgs a;
     a.q = reinterpret_cast<const float*>(act->base + q_off);

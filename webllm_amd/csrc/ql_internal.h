@@ -348,11 +348,13 @@ struct StripArgs {
     int32_t M, G, group;
     int32_t split;             // waves per block: 1 (strips of 8 blocks) or 2 (strips of 4)
     int32_t stream;            // 1: packed weights by streaming (nontemporal) loads
+    int32_t wide;              // 1: strip_wide_kernel (no padding, M 5..16, streamed weights)
 };
 
 struct StripPlan {
     int grid = 0, strips = 0, split = 1;
     bool stream = false;       // the weights exceed what the MALL keeps between steps
+    bool wide = false;         // strip_wide_kernel: streamed, split 1, M 5..16, no padding
     uint64_t lds_bytes = 0;
     uint64_t total_units = 0, busiest_units = 0;   // block-groups: all, most on one workgroup
     std::vector<StripTask> tasks;
@@ -365,5 +367,10 @@ constexpr uint64_t kStripMallBytes = 192ull << 20;   // weights that stay reside
 size_t strip_lds(int M, int group, int split);
 void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out);
 hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream);
+// The strip launch without padding (ql_strip_wide.hip): every linear group 128, K a multiple of
+// 4 groups, N a multiple of 512, weights streamed, strips of 8 blocks, M 5..16.
+bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan& p);
+size_t strip_wide_lds(int M);
+hipError_t launch_strips_wide(const StripArgs& a, size_t lds, hipStream_t stream);
 
 }  // namespace ql

@@ -19,6 +19,7 @@
 // Arithmetic is the decode kernels' exact int8-digit MFMA product and fp32 group epilogue, so
 // outputs equal the sequence kernel's bit for bit.
 #include <algorithm>
+#include <cstdlib>
 #include <functional>
 #include <queue>
 #include <vector>
@@ -674,7 +675,7 @@ void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int spl
 
 // Strips of 8 blocks, or of 4 with two waves per block when that balances the workgroups
 // better (a strip of 8 blocks of a long-K linear can outweigh a workgroup's mean share).
-void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+static void plan_strips_base(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
 {
     uint64_t bytes = 0;
     for (const SeqSpec& s : lin) bytes += s.weight_bytes;
@@ -689,8 +690,26 @@ void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* ou
     if (two.busiest_units < out->busiest_units) *out = two;
 }
 
+// The plan, then the no-padding kernel where it applies (QL_STRIP_WIDE=0 in the environment
+// keeps strip_kernel, for comparisons).
+static void plan_strips_final(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+{
+    plan_strips_base(lin, M, grid, out);
+    const char* env = getenv("QL_STRIP_WIDE");
+    if ((!env || atoi(env) != 0) && strip_wide_eligible(lin, M, *out)) {
+        out->wide = true;
+        out->lds_bytes = strip_wide_lds(M);
+    }
+}
+
+void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+{
+    plan_strips_final(lin, M, grid, out);
+}
+
 hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream)
 {
+    if (a.wide) return launch_strips_wide(a, lds, stream);
     const StripKernel k = strip_kernel_for(a.M, a.group, a.split, a.stream != 0);
     if (!k.fn) return hipErrorInvalidValue;
     void* args[] = {const_cast<StripArgs*>(&a)};

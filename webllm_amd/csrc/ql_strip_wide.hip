@@ -1,0 +1,507 @@
+// Column strips for decode batches of M = 5..16 rows on weights streamed from HBM: the strip
+// launch of ql_strip.hip for plans without padding, with an arithmetic laid out for few vector
+// instructions per job.
+//
+// Same work split as strip_kernel (a workgroup owns strips of 8 whole 64-column blocks over all
+// of K, one block per wave; K in chunks of 4 quantization groups staged as activation digits in
+// double-buffered LDS; a 2-deep register ring of packed weights per wave), restricted to plans in
+// which every linear has a multiple of 4 groups of 128 and a multiple of 512 columns, so every
+// chunk has 4 jobs for every wave and no position is padding. What differs:
+// * M 9..16 (L = 1): the four base-256 digits of every activation laid out digit-major: tile d
+//   holds digit d of rows 0..15, so a lane holds the four digit sums of its 4 rows x 4 columns and
+//   recombines them in its own registers; M 5..8 (L = 0): rows 4m + d in two 16-row tiles, as
+//   strip_kernel. (Three digits, 24 bits of each group's range, measured 1.9e-5 against the
+//   1e-5 + 1e-4 |ref| bar on the 7B down projections (K = 18944), so four are kept.)
+// * the zero-point term -s*z*sum(x) goes through one v_mfma_f32_16x16x4_f32 per column quarter
+//   and chunk (k = the chunk's 4 groups: A = the groups' row sums, B = -s*z of the lane's
+//   columns, loaded per lane for group chunk + kq), added to the sums once per chunk, instead of
+//   one FMA per output and job;
+// * every LDS address is a lane constant plus a compile-time offset, and positions never branch.
+// Each job's epilogue is then, per output, two integer recombinations, two conversions, one FMA
+// for the digit value and one multiply-add with scale * 2^-E.
+#include "ql_device.h"
+#include "ql_digits.h"
+#include "ql_internal.h"
+
+namespace ql {
+
+namespace {
+
+constexpr int kCG = kStripChunkGroups;   // quantization groups per chunk (4)
+constexpr int kCols = kSeqTileCols;      // 64 output columns per block
+constexpr int kW = 8;                    // waves: one block each
+constexpr int kThreads = 64 * kW;
+constexpr int kP = 2;                    // jobs in flight per wave
+constexpr int kNB = 2;                   // 64-k blocks per 128-k group
+constexpr int kBlocks = 8;               // blocks per strip
+static_assert(kCG == 4 && kCG % kP == 0, "chunks of 4 groups, whole ring rounds");
+
+template <typename T>
+__device__ __forceinline__ T tab(const T* p)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    // tables are written once before any launch: constant address space, scalar loads
+    return *(const __attribute__((address_space(4))) T*)(reinterpret_cast<uintptr_t>(p));
+#else
+    return *p;
+#endif
+}
+
+__device__ __forceinline__ int sreg(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <typename T>
+__device__ __forceinline__ const T* sptr(const T* p)
+{
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<const T*>((hi << 32) | lo);
+}
+
+// Buffer loads: a scalar resource per tensor, a 32-bit lane offset and a scalar offset, so no
+// lane computes a 64-bit address. kNT: the streaming (nontemporal) policy.
+constexpr int kNT = 2;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7FFFFFFF, 0x00020000);
+}
+
+__device__ __forceinline__ f32x4 mfma_f32_4(float a, float b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Four digits per activation. L = 0: digit row 4m + d (m < 8) in tile m / 4 at row 4 (m % 4) + d;
+// L = 1: tile d, row m (m < 16).
+template <int L>
+struct WideLayout {
+    static constexpr int kDigits = 4;
+    static constexpr int kTiles = L == 0 ? 2 : 4;       // 16-row tiles per (64-k block, quarter)
+    static constexpr int kMaxM = L == 0 ? 8 : 16;
+    static constexpr int kTileB = 16 * 16;              // 16 rows of 16 bytes
+    static constexpr int kKqB = kTiles * kTileB;        // per lane group kq (16 k of the block)
+    static constexpr int kBbB = 4 * kKqB;               // per 64-k block
+    static constexpr int kGB = kNB * kBbB;              // per group
+    static constexpr int kDigB = kCG * kGB;             // digits of one chunk
+    static constexpr int kGstB = kCG * 16 * 8;          // {2^-E, sum x} per (group, row < 16)
+    static constexpr int kBufB = kDigB + kGstB;         // one chunk buffer
+    static constexpr int kBiasB = 2 * kBlocks * kCols * 4;   // two strips' bias
+    static constexpr int kZB = L == 0 ? kW * 16 * kCols * 4 : 0;   // zero-term transposition (L = 0)
+    static constexpr int kLds = 2 * kBufB + kBiasB + kZB;
+    // 8-value staging items per thread and chunk: kCG groups x kMaxM rows x 16 pieces of 8 k
+    static constexpr int kH = (kCG * kMaxM * 16 + kThreads - 1) / kThreads;
+};
+
+// Digits of one 8-k piece owned by one of 16 consecutive lanes that hold one (group, row):
+// writes its 16-byte-row halves (k order {0,2,4,6,1,3,5,7}) for each of the four digits, rows
+// digit_stride_u2 uint2 apart, and returns the group's {2^-E, sum x} (identical bits in all 16
+// lanes: butterfly reductions).
+__device__ __forceinline__ float2 stage_piece(const float v[8], uint2* row0, int digit_stride_u2)
+{
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off));
+        sum += __shfl_xor(sum, off);
+    }
+    const int E = group_exponent(amax);          // max|x| * 2^E < 64
+    const float scale = ldexpf(1.f, E + 24);
+    uint32_t ev[4], od[4];
+    byte_transpose(digits_of(v[0], scale), digits_of(v[2], scale), digits_of(v[4], scale),
+                   digits_of(v[6], scale), ev);
+    byte_transpose(digits_of(v[1], scale), digits_of(v[3], scale), digits_of(v[5], scale),
+                   digits_of(v[7], scale), od);
+#pragma unroll
+    for (int i = 0; i < 4; i++) row0[i * digit_stride_u2] = uint2{ev[i], od[i]};
+    return float2{ldexpf(1.f, -E), sum};
+}
+
+template <int L>
+__global__ __launch_bounds__(kThreads, 1) void strip_wide_kernel(const StripArgs a)
+{
+    using Lay = WideLayout<L>;
+    constexpr int H = Lay::kH;
+    constexpr int KT = Lay::kTiles;
+    extern __shared__ uint4 dyn_lds[];
+    char* const lds = reinterpret_cast<char*>(dyn_lds);
+    const int M = a.M;
+    const int lane = threadIdx.x & 63;
+    const int wave = sreg(threadIdx.x >> 6);
+    const int j = lane & 15;
+    const int kq = lane >> 4;
+    const int wg = blockIdx.x;
+    const int tb = tab(a.task_begin + wg);
+    const int te = tab(a.task_begin + wg + 1);
+    if (tb >= te) return;
+
+    // chunk buffers (digits, then {2^-E, sum x}), the strips' bias, the zero-term transposition
+    auto gst = [&](int buf) { return reinterpret_cast<float2*>(lds + buf * Lay::kBufB + Lay::kDigB); };
+    float* const bias_base = reinterpret_cast<float*>(lds + 2 * Lay::kBufB);
+    auto bias_lds = [&](int par) { return bias_base + par * (kBlocks * kCols); };
+
+    // digits of rows >= M stay zero: clear both chunk buffers once
+    for (int o = threadIdx.x * 16; o < 2 * Lay::kBufB; o += kThreads * 16)
+        *reinterpret_cast<uint4*>(lds + o) = uint4{0u, 0u, 0u, 0u};
+    __syncthreads();
+
+    // ---- staging: the chunk being staged (task si, chunk sch) ----
+    struct Stage {
+        int si, sch, ngroups, K, xdt, ct, has_bias;
+        __amdgpu_buffer_rsrc_t rx, rb, rz, rs;   // x, bias (x without one), the wave block's zeros, scales
+        uint32_t Gz, Gs;
+    };
+    auto stage_open = [&](Stage& st, int ti) {
+        const StripTask t = tab(a.tasks + ti);
+        const SeqLinear* Lp = a.lin + t.linear;
+        st.si = ti;
+        st.sch = 0;
+        const void* x = sptr(tab(&Lp->x));
+        const float* b = tab(&Lp->bias);
+        st.has_bias = b != nullptr;
+        st.rx = rsrc(x);
+        st.rb = rsrc(b ? static_cast<const void*>(sptr(b) + t.ct * kCols) : x);
+        st.K = tab(&Lp->K);
+        st.xdt = tab(&Lp->x_dtype);
+        st.ngroups = st.K / 128;
+        st.ct = t.ct;
+        const int N = tab(&Lp->N);
+        const uint32_t blk = (uint32_t)(t.ct + wave);
+        st.rz = rsrc(reinterpret_cast<const char*>(sptr(tab(&Lp->qzeros))) + blk * (uint32_t)(kCols / 8) * 4u);
+        st.rs = rsrc(reinterpret_cast<const char*>(sptr(tab(&Lp->scales))) + blk * (uint32_t)kCols * 2u);
+        st.Gz = (((uint32_t)N + 7u) >> 3) * 4u;
+        st.Gs = (uint32_t)N * 2u;
+    };
+    u32x4 xr[H][2];                         // raw activation bits: f32 (both) or f16 ([0])
+    float bv;                               // one bias value per thread (512 = a strip's columns)
+    uint32_t zq;                            // zero word of group (chunk + kq), the lane's columns
+    u32x2 sq;                               // scales of group (chunk + kq), the lane's 4 columns
+    // step 1: unconditional loads (threads past the chunk's items re-read its last item)
+    auto stage_issue = [&](const Stage& st) {
+        const int g0 = st.sch * kCG;
+        const int items = kCG * M * 16;
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            const int idx = min((int)threadIdx.x + kThreads * h, items - 1);
+            const int item = idx >> 4, c = idx & 15;
+            const int gg = item / M, m = item - gg * M;
+            const uint32_t e = (uint32_t)m * (uint32_t)st.K + (uint32_t)((g0 + gg) * 128 + c * 8);
+            if (st.xdt == 0) {
+                xr[h][0] = __builtin_amdgcn_raw_buffer_load_b128(st.rx, e * 4u, 0, 0);
+                xr[h][1] = __builtin_amdgcn_raw_buffer_load_b128(st.rx, e * 4u + 16u, 0, 0);
+            } else {
+                // the same number of loads on both paths keeps the step-5 wait exact
+                uint32_t e2 = e * 2u;
+                asm volatile("" : "+v"(e2));        // a second load, not merged with the first
+                xr[h][0] = __builtin_amdgcn_raw_buffer_load_b128(st.rx, e * 2u, 0, 0);
+                xr[h][1] = __builtin_amdgcn_raw_buffer_load_b128(st.rx, e2, 0, 0);
+            }
+        }
+        bv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(st.rb, st.has_bias ? threadIdx.x * 4u : 0u, 0, 0));
+        zq = __builtin_amdgcn_raw_buffer_load_b32(st.rz, (uint32_t)kq * st.Gz + (uint32_t)(j >> 1) * 4u, (uint32_t)g0 * st.Gz, 0);
+        sq = __builtin_amdgcn_raw_buffer_load_b64(st.rs, (uint32_t)kq * st.Gs + (uint32_t)j * 8u, (uint32_t)g0 * st.Gs, 0);
+    };
+    float nsz[4];                           // -s * z of group (chunk + kq), the lane's columns
+    // step 5: digits of the staged chunk into buffer `buf`, its -s*z, the strip's bias
+    auto stage_finish = [&](const Stage& st, int buf) {
+        const int items = kCG * M * 16;
+        char* const dig = lds + buf * Lay::kBufB;
+        float2* const gs = gst(buf);
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            const int idx = (int)threadIdx.x + kThreads * h;
+            if (idx < items) {                    // whole 16-lane groups: items is a multiple of 16
+                const int item = idx >> 4, c = idx & 15;
+                const int gg = item / M, m = item - gg * M;
+                float v[8];
+                if (st.xdt == 0) {
+                    const f32x4 lo = __builtin_bit_cast(f32x4, xr[h][0]), hi = __builtin_bit_cast(f32x4, xr[h][1]);
+                    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+                    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+                } else {
+                    const f16x8 hv = __builtin_bit_cast(f16x8, xr[h][0]);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = (float)hv[e];
+                }
+                // piece c covers k 8c .. 8c+7 of the group: 64-k block c / 8, lane group
+                // (c % 8) / 2 of its B operand, 8-byte half c % 2 of the 16-byte row
+                const int row = L == 0 ? (m >> 2) * 16 + 4 * (m & 3) : m;
+                char* const r0 = dig + gg * Lay::kGB + (c >> 3) * Lay::kBbB + ((c & 7) >> 1) * Lay::kKqB +
+                                 row * 16 + (c & 1) * 8;
+                const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8);
+                if (c == 0) gs[gg * 16 + m] = s2;
+            }
+        }
+        // -s * z of the lane's columns 4j .. 4j+3 for group (chunk + kq), zero = stored + 1
+        const uint32_t zw = zq >> (16 * (j & 1));
+        const uint32_t sw[4] = {sq.x & 0xffffu, sq.x >> 16, sq.y & 0xffffu, sq.y >> 16};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
+            nsz[u] = -s * (float)(((zw >> (4 * u)) & 15u) + 1u);
+        }
+        if (st.sch == 0) bias_lds((st.si - tb) & 1)[threadIdx.x] = st.has_bias ? bv : 0.f;
+    };
+    auto stage_next = [&](Stage& st) {    // false past the last chunk of the last task
+        if ((st.sch + 1) * kCG < st.ngroups) {
+            st.sch++;
+            return true;
+        }
+        if (st.si + 1 >= te) return false;
+        stage_open(st, st.si + 1);
+        return true;
+    };
+
+    // ---- job stream: one job per group of each strip (the wave's block) ----
+    uint4 wb[kP][2 * kNB];
+    uint2 sb[kP];
+    struct Cur {
+        int ti, g, ngroups;
+        __amdgpu_buffer_rsrc_t rq, rs;   // the wave block's packed weights and scales
+        uint32_t Gq, Gs;
+        uint32_t lq[2 * kNB];       // the lane's packed rows 2kq, 2kq+1, 2kq+8, 2kq+9 of a group
+    };
+    const uint32_t ls = 8u * (uint32_t)j;
+    auto open = [&](Cur& c, int ti) {
+        const StripTask t = tab(a.tasks + ti);
+        const SeqLinear* Lp = a.lin + t.linear;
+        c.ti = ti;
+        c.g = 0;
+        const int N = sreg(tab(&Lp->N));
+        c.ngroups = sreg(tab(&Lp->K)) / 128;
+        const uint32_t blk = (uint32_t)(t.ct + wave);
+        c.rq = rsrc(reinterpret_cast<const char*>(sptr(tab(&Lp->qweight))) + blk * (uint32_t)kCols * 4u);
+        c.rs = rsrc(reinterpret_cast<const char*>(sptr(tab(&Lp->scales))) + blk * (uint32_t)kCols * 2u);
+        c.Gq = 16u * (uint32_t)N * 4u;
+        c.Gs = (uint32_t)N * 2u;
+#pragma unroll
+        for (int r = 0; r < 2 * kNB; r++)
+            c.lq[r] = ((uint32_t)(2 * kq + (r >> 1) * 8 + (r & 1)) * (uint32_t)N + 4u * (uint32_t)j) * 4u;
+    };
+    auto advance = [&](Cur& c) {
+        if (c.g + 1 < c.ngroups) c.g++;
+        else if (c.ti + 1 < te) open(c, c.ti + 1);
+        // else: the stream has ended; stay on the last job (its reloads are never consumed)
+    };
+    auto fetch = [&](int d, const Cur& c) {
+        const uint32_t gq = (uint32_t)c.g * c.Gq;
+#pragma unroll
+        for (int r = 0; r < 2 * kNB; r++)
+            wb[d][r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(c.rq, c.lq[r], gq, kNT));
+        sb[d] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(c.rs, ls, (uint32_t)c.g * c.Gs, 0));
+    };
+
+    // accumulators: L = 1 rows 4kq + r of column 4j + u: acc[u][r]; L = 0 rows 4t + kq: acc[u][t],
+    // and the zero term in the MFMA layout (rows 4kq + r) in zacc, folded in at a strip's end
+    f32x4 acc[4];
+    f32x4 zacc[L == 0 ? 4 : 1];
+    auto clear = [&]() {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (L == 0) zacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+
+    // lane-constant LDS offsets: the A operand row of this lane (row j of each tile, lane group kq)
+    const int a_lane = kq * Lay::kKqB + j * 16;
+
+    // one job: local group gg of the chunk in buffer `buf`, ring slot d
+    auto consume = [&](int d, int buf, int gg) {
+        const char* const dig = lds + buf * Lay::kBufB + gg * Lay::kGB + a_lane;
+        i32x4 av[kNB][KT];
+#pragma unroll
+        for (int bb = 0; bb < kNB; bb++)
+#pragma unroll
+            for (int t = 0; t < KT; t++)
+                av[bb][t] = *reinterpret_cast<const i32x4*>(dig + bb * Lay::kBbB + t * Lay::kTileB);
+        const float2* const gs = gst(buf) + gg * 16;
+        const uint2 sv = sb[d];
+        float s[4];
+        s[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv.x & 0xffffu));
+        s[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv.x >> 16));
+        s[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv.y & 0xffffu));
+        s[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv.y >> 16));
+        // the weight nibbles of 64-k block bb, column quarter u, as bytes
+        auto bq_of = [&](int bb, int u) {
+            const uint4 w0 = wb[d][2 * bb], w1 = wb[d][2 * bb + 1];
+            const uint32_t lo[4] = {w0.x, w0.y, w0.z, w0.w};
+            const uint32_t hi[4] = {w1.x, w1.y, w1.z, w1.w};
+            return i32x4{(int)(lo[u] & 0x0F0F0F0Fu), (int)((lo[u] >> 4) & 0x0F0F0F0Fu),
+                         (int)(hi[u] & 0x0F0F0F0Fu), (int)((hi[u] >> 4) & 0x0F0F0F0Fu)};
+        };
+        if constexpr (L == 1) {
+            // e[r] = 2^-E of row 4kq + r, times 2^-8 (the digit pairs below carry 2^8)
+            const f32x4 g01 = *reinterpret_cast<const f32x4*>(gs + 4 * kq);
+            const f32x4 g23 = *reinterpret_cast<const f32x4*>(gs + 4 * kq + 2);
+            const float e[4] = {g01.x * 0x1p-8f, g01.z * 0x1p-8f, g23.x * 0x1p-8f, g23.z * 0x1p-8f};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                i32x4 c[4];
+#pragma unroll
+                for (int bb = 0; bb < kNB; bb++) {
+                    const i32x4 bq = bq_of(bb, u);
+#pragma unroll
+                    for (int t = 0; t < 4; t++) c[t] = mfma_i8(av[bb][t], bq, bb == 0 ? i32x4{0, 0, 0, 0} : c[t]);
+                }
+                // tile t holds digit t: 2^8 * sum_d c_d 2^(8d-24) = (c0 + 2^8 c1) 2^-16 + (c2 + 2^8 c3)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int lo2 = c[0][r] + c[1][r] * 256;
+                    const int hi2 = c[2][r] + c[3][r] * 256;
+                    const float v = fmaf((float)lo2, 0x1p-16f, (float)hi2);
+                    acc[u][r] = fmaf(s[u] * e[r], v, acc[u][r]);
+                }
+            }
+            // keep this job's epilogue here: without a use, the compiler sinks every job's
+            // epilogue to the end of the chunk and keeps all four jobs' MFMA results live
+#pragma unroll
+            for (int u = 0; u < 4; u++) asm volatile("" : "+v"(acc[u]));
+        } else {
+            // e[t] = 2^-E of row 4t + kq, times 2^-8 (the digit pairs below carry 2^8)
+            float e[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) e[t] = gs[4 * t + kq].x * 0x1p-8f;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                i32x4 c[2];
+#pragma unroll
+                for (int bb = 0; bb < kNB; bb++) {
+                    const i32x4 bq = bq_of(bb, u);
+#pragma unroll
+                    for (int t = 0; t < 2; t++) c[t] = mfma_i8(av[bb][t], bq, bb == 0 ? i32x4{0, 0, 0, 0} : c[t]);
+                }
+                // digit products (|c| < 2^18, digit 3 most significant) in two exact integer
+                // pairs: 2^8 * sum_d c_d 2^(8d-24) = (c0 + 2^8 c1) 2^-16 + (c2 + 2^8 c3)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const int lo2 = c[t][0] + c[t][1] * 256;
+                    const int hi2 = c[t][2] + c[t][3] * 256;
+                    const float v = fmaf((float)lo2, 0x1p-16f, (float)hi2);
+                    acc[u][t] = fmaf(s[u] * e[t], v, acc[u][t]);
+                }
+            }
+            // keep this job's epilogue here: without a use, the compiler sinks every job's
+            // epilogue to the end of the chunk and keeps all four jobs' MFMA results live
+#pragma unroll
+            for (int u = 0; u < 4; u++) asm volatile("" : "+v"(acc[u]));
+        }
+    };
+
+    // the zero-point term of a chunk: rows i, columns 4j + u: sum over its 4 groups g of
+    // sum_x[g][i] * (-s z)[g][col] (lane (kq, i) holds A = sum_x of group kq, row i; lane (kq, j)
+    // holds B = -s z of group kq, its column of quarter u). The MFMA starts from zero and its
+    // result is added with ordinary adds: its internal sum is not one IEEE rounding, and fed the
+    // running sum as C it lost up to 2.8e-5 over the 148 groups of a 7B down projection.
+    auto zero_term = [&](int buf) {
+        const float sx = gst(buf)[kq * 16 + j].y;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const f32x4 z = mfma_f32_4(sx, nsz[u], f32x4{0.f, 0.f, 0.f, 0.f});
+            if constexpr (L == 1) acc[u] += z;
+            else zacc[u] += z;
+        }
+    };
+
+    // the first chunk, then the ring's first kP positions
+    Stage sg;
+    stage_open(sg, tb);
+    stage_issue(sg);
+    stage_finish(sg, 0);
+    __syncthreads();
+    bool staging = stage_next(sg);
+    Cur fc;
+    open(fc, tb);
+#pragma unroll
+    for (int d = 0; d < kP; d++) {
+        fetch(d, fc);
+        advance(fc);
+    }
+    clear();
+
+    int buf = 0;
+    for (int ti = tb; ti < te; ti++) {
+        const StripTask t = tab(a.tasks + ti);
+        const SeqLinear* Lp = a.lin + t.linear;
+        const int nch = tab(&Lp->K) / (128 * kCG);
+        for (int ch = 0; ch < nch; ch++) {
+            stage_issue(sg);                 // past the last chunk: repeats it (never finished)
+#pragma unroll
+            for (int gg = 0; gg < kCG; gg++) {
+                consume(gg % kP, buf, gg);
+                fetch(gg % kP, fc);
+                advance(fc);
+            }
+            zero_term(buf);
+            if (ch + 1 == nch) {
+                const int N = tab(&Lp->N);
+                float* y = tab(&Lp->y);
+                const int col = (t.ct + wave) * kCols + 4 * j;
+                const f32x4 bvv = *reinterpret_cast<const f32x4*>(bias_lds((ti - tb) & 1) + wave * kCols + 4 * j);
+                if constexpr (L == 1) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int m = 4 * kq + r;
+                        if (m < M)
+                            st_global(reinterpret_cast<f32x4*>(y + (size_t)m * N + col),
+                                      f32x4{acc[0][r] + bvv.x, acc[1][r] + bvv.y, acc[2][r] + bvv.z, acc[3][r] + bvv.w});
+                    }
+                } else {
+                    // the zero term from the MFMA layout (row 4kq + r) to the digit layout (row
+                    // 4t + kq) through this wave's own LDS rows
+                    float* const zl = reinterpret_cast<float*>(lds + 2 * Lay::kBufB + Lay::kBiasB) + wave * 16 * kCols;
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        *reinterpret_cast<f32x4*>(zl + (4 * kq + r) * kCols + 4 * j) =
+                            f32x4{zacc[0][r], zacc[1][r], zacc[2][r], zacc[3][r]};
+                    // a wave's LDS operations complete in order: the reads below see every lane's
+                    // writes (the fences only keep the compiler from moving them)
+                    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                    __builtin_amdgcn_wave_barrier();
+                    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+                    for (int tt = 0; tt < 2; tt++) {
+                        const int m = 4 * tt + kq;
+                        const f32x4 z = *reinterpret_cast<const f32x4*>(zl + m * kCols + 4 * j);
+                        if (m < M)
+                            st_global(reinterpret_cast<f32x4*>(y + (size_t)m * N + col),
+                                      f32x4{acc[0][tt] + z.x + bvv.x, acc[1][tt] + z.y + bvv.y,
+                                            acc[2][tt] + z.z + bvv.z, acc[3][tt] + z.w + bvv.w});
+                    }
+                }
+                clear();
+            }
+            if (staging) stage_finish(sg, buf ^ 1);
+            __syncthreads();
+            buf ^= 1;
+            if (staging) staging = stage_next(sg);
+        }
+    }
+}
+
+}  // namespace
+
+bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan& p)
+{
+    if (!p.stream || p.split != 1 || M < 5 || M > kGemvMaxM) return false;
+    for (const SeqSpec& s : lin)
+        if (s.group != 128 || s.K % (128 * kCG) != 0 || s.N % (kBlocks * kCols) != 0) return false;
+    return true;
+}
+
+size_t strip_wide_lds(int M)
+{
+    return M <= 8 ? (size_t)WideLayout<0>::kLds : (size_t)WideLayout<1>::kLds;
+}
+
+hipError_t launch_strips_wide(const StripArgs& a, size_t lds, hipStream_t stream)
+{
+    const void* fn = a.M <= 8 ? reinterpret_cast<const void*>(&strip_wide_kernel<0>)
+                              : reinterpret_cast<const void*>(&strip_wide_kernel<1>);
+    void* args[] = {const_cast<StripArgs*>(&a)};
+    return hipLaunchKernel(fn, dim3(a.G), dim3(kThreads), args, lds, stream);
+}
+
+}  // namespace ql

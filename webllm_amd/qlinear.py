@@ -80,7 +80,7 @@ class SeqInfo(ctypes.Structure):
                 ("lds_bytes", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64),
                 ("total_units", ctypes.c_uint64), ("busiest_units", ctypes.c_uint64),
                 ("kernel", ctypes.c_int32), ("split", ctypes.c_int32), ("stream", ctypes.c_int32),
-                ("reserved", ctypes.c_int32)]
+                ("variant", ctypes.c_int32)]
 
     def as_dict(self) -> dict:
         return {f: getattr(self, f) for f, _ in self._fields_}
@@ -89,6 +89,12 @@ class SeqInfo(ctypes.Structure):
     def balance(self) -> float:
         """Block-groups of the busiest workgroup over the mean (1.0 = perfectly even)."""
         return self.busiest_units * self.grid / max(1, self.total_units)
+
+
+class AttnInfo(ctypes.Structure):
+    """The launch shape ql_attention_decode picks (ql_attn_info)."""
+    _fields_ = [("heads_per_run", ctypes.c_int32), ("nsplit", ctypes.c_int32),
+                ("workgroups", ctypes.c_int32), ("keys_per_split", ctypes.c_int32)]
 
 
 _lib = None
@@ -137,6 +143,7 @@ def lib():
         "ql_add_rmsnorm": (I, [P, P, U64, U64, P, U64, ctypes.c_float, I, I, U64, U64]),
         "ql_silu_mul": (I, [P, P, U64, U64, ctypes.c_int64, U64]),
         "ql_attention_decode": (I, [P, P, U64, P, U64, U64, I, I, I, I, I, I, U64]),
+        "ql_plan_attention": (I, [I, I, I, I, I, I, ctypes.POINTER(AttnInfo)]),
         "ql_linear": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64, I, I, U64, U64]),
         "ql_linear_noalloc": (I, [P, ctypes.POINTER(GptqDesc), P, P, U64, I, I, U64]),
         "ql_plan_batch": (I, [I, ctypes.POINTER(GptqDesc), I, ctypes.POINTER(U64)]),
@@ -186,6 +193,13 @@ def plan_linear(M: int, N: int, K: int, group: int = 128) -> Plan:
     p = Plan()
     _check(lib().ql_plan_linear(M, N, K, group, ctypes.byref(p)))
     return p
+
+
+def plan_attention(max_t: int, M: int, n_head: int, n_kv_head: int, D: int, past_len: int) -> AttnInfo:
+    """The launch shape of ql_attention_decode for these dimensions (host only)."""
+    info = AttnInfo()
+    _check(lib().ql_plan_attention(max_t, M, n_head, n_kv_head, D, past_len, ctypes.byref(info)))
+    return info
 
 
 def plan_batch(descs: list[GptqDesc], M: int) -> int:
