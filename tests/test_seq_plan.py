@@ -309,6 +309,10 @@ def test_strips_stream_weights_the_mall_cannot_keep():
     for M in (5, 8, 9, 16):
         wide = qwen7b(Chain(M=M), 28, chained=False).plan(grid=256)
         assert wide.kernel == ql.SEQ_STRIPS and wide.stream == 1 and wide.variant == 1, M
+        # the wide kernel has one block per wave: every strip is 8 whole 64-column blocks
+        # (140 linears' 21,280 blocks), never the 4-block strips of split 2
+        assert wide.split == 1 and wide.tiles == 21280 // 8, (M, wide.split, wide.tiles)
+        assert wide.grid == 256, (M, wide.grid)
     for M in (1, 4):
         assert qwen7b(Chain(M=M), 28, chained=False).plan(grid=256).variant == 0
     # chained sequences (dependency-ordered tiles) report no streaming

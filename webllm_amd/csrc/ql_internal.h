@@ -371,6 +371,7 @@ hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream);
 // 4 groups, N a multiple of 512, weights streamed, strips of 8 blocks, M 5..16.
 bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan& p);
 size_t strip_wide_lds(int M);
+int strip_wide_per_cu(int M);          // workgroups per CU of the wide kernel at M rows
 hipError_t launch_strips_wide(const StripArgs& a, size_t lds, hipStream_t stream);
 
 }  // namespace ql

@@ -697,8 +697,24 @@ static void plan_strips_final(const std::vector<SeqSpec>& lin, int M, int grid, 
     plan_strips_base(lin, M, grid, out);
     const char* env = getenv("QL_STRIP_WIDE");
     if ((!env || atoi(env) != 0) && strip_wide_eligible(lin, M, *out)) {
-        out->wide = true;
-        out->lds_bytes = strip_wide_lds(M);
+        // the M 5..8 instance runs two workgroups per CU: plan for that many, with strips of 8
+        // blocks (the kernel's one block per wave) whatever the balance
+        const int per_cu = strip_wide_per_cu(M);
+        if (per_cu > 1 && grid <= kPlanCUs) {
+            StripPlan two;
+            plan_strips_split(lin, M, grid * per_cu, 1, &two);
+            two.stream = out->stream;
+            *out = two;
+        }
+        // every strip must be 8 whole blocks: the kernel has no path for a shorter one
+        bool whole = out->split == 1;
+        for (const StripTask& t : out->tasks) whole = whole && t.nblk == kMaxStripBlocks;
+        if (whole) {
+            out->wide = true;
+            out->lds_bytes = strip_wide_lds(M);
+        } else {
+            plan_strips_base(lin, M, grid, out);
+        }
     }
 }
 

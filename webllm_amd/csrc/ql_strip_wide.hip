@@ -19,6 +19,8 @@
 // * every LDS address is a lane constant plus a compile-time offset, and positions never branch.
 // Each job's epilogue is then, per output, two integer recombinations, two conversions, one FMA
 // for the digit value and one multiply-add with scale * 2^-E.
+#include <type_traits>
+
 #include "ql_device.h"
 #include "ql_digits.h"
 #include "ql_internal.h"
@@ -31,7 +33,10 @@ constexpr int kCG = kStripChunkGroups;   // quantization groups per chunk (4)
 constexpr int kCols = kSeqTileCols;      // 64 output columns per block
 constexpr int kW = 8;                    // waves: one block each
 constexpr int kThreads = 64 * kW;
-constexpr int kP = 2;                    // jobs in flight per wave
+#ifndef QL_WIDE_P
+#define QL_WIDE_P 2
+#endif
+constexpr int kP = QL_WIDE_P;            // jobs in flight per wave
 constexpr int kNB = 2;                   // 64-k blocks per 128-k group
 constexpr int kBlocks = 8;               // blocks per strip
 static_assert(kCG == 4 && kCG % kP == 0, "chunks of 4 groups, whole ring rounds");
@@ -83,7 +88,7 @@ struct WideLayout {
     static constexpr int kBbB = 4 * kKqB;               // per 64-k block
     static constexpr int kGB = kNB * kBbB;              // per group
     static constexpr int kDigB = kCG * kGB;             // digits of one chunk
-    static constexpr int kGstB = kCG * 16 * 8;          // {2^-E, sum x} per (group, row < 16)
+    static constexpr int kGstB = kCG * 16 * 8;          // {2^-(E+8), sum x} per (group, row < 16)
     static constexpr int kBufB = kDigB + kGstB;         // one chunk buffer
     static constexpr int kBiasB = 2 * kBlocks * kCols * 4;   // two strips' bias
     static constexpr int kZB = L == 0 ? kW * 16 * kCols * 4 : 0;   // zero-term transposition (L = 0)
@@ -92,35 +97,66 @@ struct WideLayout {
     static constexpr int kH = (kCG * kMaxM * 16 + kThreads - 1) / kThreads;
 };
 
-// Digits of one 8-k piece owned by one of 16 consecutive lanes that hold one (group, row):
-// writes its 16-byte-row halves (k order {0,2,4,6,1,3,5,7}) for each of the four digits, rows
-// digit_stride_u2 uint2 apart, and returns the group's {2^-E, sum x} (identical bits in all 16
-// lanes: butterfly reductions).
+// Reductions over the 16 lanes of a row by DPP row rotations (every lane ends with the combined
+// value; the max is exact, and the sum's order is fixed per lane, so each run gives the same bits).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ void row_max_sum(float& amax, float& sum)
+{
+    // row_ror:8, row_ror:4, quad_perm [2,3,0,1], quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dpp<0x128>(amax)); sum += dpp<0x128>(sum);
+    amax = fmaxf(amax, dpp<0x124>(amax)); sum += dpp<0x124>(sum);
+    amax = fmaxf(amax, dpp<0x4E>(amax));  sum += dpp<0x4E>(sum);
+    amax = fmaxf(amax, dpp<0xB1>(amax));  sum += dpp<0xB1>(sum);
+}
+
+// round(v) as an integer, halves rounded up (v_cvt_rpi_i32_f32: one instruction)
+__device__ __forceinline__ int round_int(float v)
+{
+    int r;
+    asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// Signed base-256 digits of round(v * scale): byte i of the result is digit i.
+__device__ __forceinline__ uint32_t digits4_of(float v, float scale)
+{
+    return ((uint32_t)round_int(v * scale) + 0x00808080u) ^ 0x00808080u;
+}
+
+// Digits of one 8-k piece owned by one of 16 consecutive lanes (one DPP row) that hold one
+// (group, row): writes its 16-byte-row halves (k order {0,2,4,6,1,3,5,7}) for each of the four
+// digits, rows digit_stride_u2 uint2 apart, and returns the group's {2^-(E+8), sum x} (2^-8:
+// the digit pairs of the epilogue carry 2^8).
 __device__ __forceinline__ float2 stage_piece(const float v[8], uint2* row0, int digit_stride_u2)
 {
-    float amax = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
+                       fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
     float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off));
-        sum += __shfl_xor(sum, off);
-    }
+    row_max_sum(amax, sum);
     const int E = group_exponent(amax);          // max|x| * 2^E < 64
     const float scale = ldexpf(1.f, E + 24);
     uint32_t ev[4], od[4];
-    byte_transpose(digits_of(v[0], scale), digits_of(v[2], scale), digits_of(v[4], scale),
-                   digits_of(v[6], scale), ev);
-    byte_transpose(digits_of(v[1], scale), digits_of(v[3], scale), digits_of(v[5], scale),
-                   digits_of(v[7], scale), od);
+    byte_transpose(digits4_of(v[0], scale), digits4_of(v[2], scale), digits4_of(v[4], scale),
+                   digits4_of(v[6], scale), ev);
+    byte_transpose(digits4_of(v[1], scale), digits4_of(v[3], scale), digits4_of(v[5], scale),
+                   digits4_of(v[7], scale), od);
 #pragma unroll
     for (int i = 0; i < 4; i++) row0[i * digit_stride_u2] = uint2{ev[i], od[i]};
-    return float2{ldexpf(1.f, -E), sum};
+    return float2{ldexpf(1.f, -E - 8), sum};
 }
 
+// Waves per SIMD the M 5..8 instance is compiled for. At 4 it fits 128 VGPRs (some spilled) and
+// a CU holds two of its workgroups, planned as 512: the 7B step at M=8 measured 653 against
+// 603-610 us with one workgroup per CU (2), so 2 is kept.
+#ifndef QL_WIDE_OCC0
+#define QL_WIDE_OCC0 2
+#endif
 template <int L>
-__global__ __launch_bounds__(kThreads, 1) void strip_wide_kernel(const StripArgs a)
+__global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wide_kernel(const StripArgs a)
 {
     using Lay = WideLayout<L>;
     constexpr int H = Lay::kH;
@@ -137,7 +173,7 @@ __global__ __launch_bounds__(kThreads, 1) void strip_wide_kernel(const StripArgs
     const int te = tab(a.task_begin + wg + 1);
     if (tb >= te) return;
 
-    // chunk buffers (digits, then {2^-E, sum x}), the strips' bias, the zero-term transposition
+    // chunk buffers (digits, then {2^-(E+8), sum x}), the strips' bias, the zero-term transposition
     auto gst = [&](int buf) { return reinterpret_cast<float2*>(lds + buf * Lay::kBufB + Lay::kDigB); };
     float* const bias_base = reinterpret_cast<float*>(lds + 2 * Lay::kBufB);
     auto bias_lds = [&](int par) { return bias_base + par * (kBlocks * kCols); };
@@ -295,12 +331,14 @@ __global__ __launch_bounds__(kThreads, 1) void strip_wide_kernel(const StripArgs
 
     // accumulators: L = 1 rows 4kq + r of column 4j + u: acc[u][r]; L = 0 rows 4t + kq: acc[u][t],
     // and the zero term in the MFMA layout (rows 4kq + r) in zacc, folded in at a strip's end
-    f32x4 acc[4];
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef typename std::conditional<L == 0, f32x2, f32x4>::type Acc;
+    Acc acc[4];
     f32x4 zacc[L == 0 ? 4 : 1];
     auto clear = [&]() {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            acc[u] = Acc{};
             if constexpr (L == 0) zacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     };
@@ -333,10 +371,10 @@ __global__ __launch_bounds__(kThreads, 1) void strip_wide_kernel(const StripArgs
                          (int)(hi[u] & 0x0F0F0F0Fu), (int)((hi[u] >> 4) & 0x0F0F0F0Fu)};
         };
         if constexpr (L == 1) {
-            // e[r] = 2^-E of row 4kq + r, times 2^-8 (the digit pairs below carry 2^8)
+            // e[r] = 2^-(E+8) of row 4kq + r (the digit pairs below carry 2^8)
             const f32x4 g01 = *reinterpret_cast<const f32x4*>(gs + 4 * kq);
             const f32x4 g23 = *reinterpret_cast<const f32x4*>(gs + 4 * kq + 2);
-            const float e[4] = {g01.x * 0x1p-8f, g01.z * 0x1p-8f, g23.x * 0x1p-8f, g23.z * 0x1p-8f};
+            const float e[4] = {g01.x, g01.z, g23.x, g23.z};
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 i32x4 c[4];
@@ -360,10 +398,10 @@ __global__ __launch_bounds__(kThreads, 1) void strip_wide_kernel(const StripArgs
 #pragma unroll
             for (int u = 0; u < 4; u++) asm volatile("" : "+v"(acc[u]));
         } else {
-            // e[t] = 2^-E of row 4t + kq, times 2^-8 (the digit pairs below carry 2^8)
+            // e[t] = 2^-(E+8) of row 4t + kq (the digit pairs below carry 2^8)
             float e[2];
 #pragma unroll
-            for (int t = 0; t < 2; t++) e[t] = gs[4 * t + kq].x * 0x1p-8f;
+            for (int t = 0; t < 2; t++) e[t] = gs[4 * t + kq].x;
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 i32x4 c[2];
@@ -489,6 +527,11 @@ bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan
     for (const SeqSpec& s : lin)
         if (s.group != 128 || s.K % (128 * kCG) != 0 || s.N % (kBlocks * kCols) != 0) return false;
     return true;
+}
+
+int strip_wide_per_cu(int M)
+{
+    return M <= 8 && QL_WIDE_OCC0 >= 4 ? 2 : 1;
 }
 
 size_t strip_wide_lds(int M)
