@@ -33,6 +33,11 @@ constexpr int kCG = kStripChunkGroups;   // quantization groups per chunk (4)
 constexpr int kCols = kSeqTileCols;      // 64 output columns per block
 constexpr int kW = 8;                    // waves: one block each
 constexpr int kThreads = 64 * kW;
+// M 9..16: each column quarter's MFMAs and epilogue form a scheduling region of their own (the
+// 7B step at M=16 826-831 against 839-846 us with one region per job; 192 against 208 VGPRs)
+#ifndef QL_WIDE_QREGION
+#define QL_WIDE_QREGION 1
+#endif
 #ifndef QL_WIDE_P
 #define QL_WIDE_P 2
 #endif
@@ -392,6 +397,10 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
                     const float v = fmaf((float)lo2, 0x1p-16f, (float)hi2);
                     acc[u][r] = fmaf(s[u] * e[r], v, acc[u][r]);
                 }
+#if QL_WIDE_QREGION
+                asm volatile("" : "+v"(acc[u]));
+                __builtin_amdgcn_sched_barrier(0);
+#endif
             }
             // keep this job's epilogue here: without a use, the compiler sinks every job's
             // epilogue to the end of the chunk and keeps all four jobs' MFMA results live
