@@ -223,6 +223,17 @@ typedef struct ql_attn_info {
 int ql_plan_attention(int32_t max_t, int32_t M, int32_t n_head, int32_t n_kv_head, int32_t D, int32_t past_len,
                       ql_attn_info* info);
 
+/* ql_embed_f16: out[r, :] = f32(embed[tokens[r], :]) for r < rows: the embedding lookup that
+ *   starts a forward (embedding_f16.wgsl, dispatched at qwen.ts:392), over the fp16 [vocab, D]
+ *   table at embed_off in `weights` (the tied table ql_gemv_f16w reads as lm_head), with uint32
+ *   token ids [rows] at tokens_off and the fp32 [rows, D] output at out_off in `act`. Exact
+ *   (binary16 -> binary32, as f16BitsToF32, safetensors.ts:144-152). A token id >= vocab writes a
+ *   row of zeros (the WGSL reads past the table there; WebGPU's robust access makes that read
+ *   implementation-defined). rows 1..65535; embed 2-byte, tokens and out 4-byte aligned (D % 8 == 0
+ *   with 16-byte embed/out offsets takes the 16-byte path). */
+int ql_embed_f16(ql_ctx* ctx, const ql_arena* weights, uint64_t embed_off, int32_t vocab, int32_t D,
+                 ql_arena* act, uint64_t tokens_off, int32_t rows, uint64_t out_off);
+
 /* ---- the elementwise work around the linears (qwen.ts:401-405, :447-478).
  * ql_add_rmsnorm: s = x + d (misc/vec_add.wgsl: the residual add after o_proj / down_proj), stored
  *   at sum_off unless QL_NONE, then y = s * rstd * w, rstd = 1 / sqrt(mean(s^2) + eps)

@@ -162,6 +162,49 @@ def test_fused_layers_05b(ql, ctx, orc, M):
     m.release()
 
 
+@pytest.mark.parametrize("M", [1, 16])
+def test_fused_silu_mul_external_operand(ql, ctx, orc, M):
+    """The SiLU-mul second operand from an external [M, I] buffer (x2_off not another linear's
+    output): gate and up run as one pass, down reads silu(gate) * up_ext where up_ext was written
+    by the host; every output against siluMulRef + gemmNTRef on the GPU's gate output."""
+    C, I = 896, 4864
+    wl, al = ql.ArenaLayout(), ql.ArenaLayout()
+    tg = synth.gptq_linear(C, I, 128, seed=0xE2A, key=(0,))
+    td = synth.gptq_linear(I, C, 128, seed=0xE2A, key=(1,))
+    offs = []
+    for t in (tg, td):
+        offs.append((wl.take(t.qweight.nbytes), wl.take(t.qzeros.nbytes), wl.take(t.scales.nbytes)))
+    x = synth.activations(M, C, seed=0xE2B, key=(M,))
+    up = synth.activations(M, I, seed=0xE2C, key=(M,))
+    x_off, g_off, u_off, y_off = al.take(x.nbytes), al.take(M * I * 4), al.take(up.nbytes), al.take(M * C * 4)
+    w = ctx.arena(wl.used)
+    for t, (a, b, c) in zip((tg, td), offs):
+        w.write(a, t.qweight)
+        w.write(b, t.qzeros)
+        w.write(c, t.scales)
+    act = ctx.arena(al.used)
+    act.write(x_off, x)
+    act.write(u_off, up)
+    descs = [ql.make_desc(*offs[0], C, I, 128), ql.make_desc(*offs[1], I, C, 128)]
+    fuse = [ql.make_fuse(), ql.make_fuse(x2_off=u_off)]
+    seq = ctx.seq(descs, w, act, [x_off, g_off], 0, M, [g_off, y_off], fuse=fuse)
+    assert seq.info.kernel == ql.SEQ_TILES and seq.info.passes == 2
+    seq.run()
+    seq.status()
+    g = act.read(g_off, (M, I), np.float32)
+    y = act.read(y_off, (M, C), np.float32)
+    ok, ma, mr = orc.check_tolerance(g, orc.gptq_linear(tg.qweight, tg.qzeros, tg.scales, x), 1e-5, RTOL)
+    assert ok, ("gate", ma, mr)
+    h = orc.silu_mul(g, up)
+    ref = orc.gptq_linear(td.qweight, td.qzeros, td.scales, h)
+    atol = 1e-5 * max(1.0, float(np.sqrt(np.mean(h.astype(np.float64) ** 2))))
+    ok, ma, mr = orc.check_tolerance(y, ref, atol, RTOL)
+    assert ok, ("down", ma, mr)
+    seq.destroy()
+    w.release()
+    act.release()
+
+
 def _sample(N, count=4):
     nb = N // 64
     picks = sorted(set([0, nb - 1] + [int(round(i * (nb - 1) / (count - 1))) for i in range(count)]))

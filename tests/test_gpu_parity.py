@@ -591,3 +591,77 @@ def test_gemv_f16w_matches_oracle(ql, ctx, orc, M, N, K, biased, label):
         ctx.gemv_f16w(w, w_off, b_off, act, x_off, M, N + 1 << 20, K, y_off)
     act.release()
     w.release()
+
+
+# ------------------------------------------------------------------------- embedding lookup
+
+EMBED_CASES = [
+    # (vocab, D, rows, out offset pad, label)
+    (151936, 896, 5, 0, "0.5B table (151936 x 896), 5 tokens incl. the first and last id"),
+    (4096, 3584, 16, 0, "7B row width, 16 rows"),
+    (65536, 16, 300, 0, "all 2^16 fp16 patterns as rows of 16, 300 rows"),
+    (1000, 20, 7, 4, "D % 8 != 0 and a 4-byte output offset: one value per load"),
+]
+
+
+@pytest.mark.parametrize("vocab,D,rows,pad,label", EMBED_CASES)
+def test_embed_f16_bit_exact(ql, ctx, orc, vocab, D, rows, pad, label):
+    """The embedding lookup (embedding_f16.wgsl, dispatched at qwen.ts:392): out[r, :] =
+    f16BitsToF32(W[tokens[r], :]) bit for bit (the oracle's decode is pinned over all 2^16
+    patterns); a token id >= vocab gives a zero row."""
+    rng = np.random.default_rng(0xE3B + vocab + D)
+    if vocab * D == 1 << 20:
+        table = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16).repeat(16).reshape(vocab, D)
+    else:
+        table = rng.integers(0, 1 << 16, size=(vocab, D), dtype=np.uint32).astype(np.uint16)
+    tokens = rng.integers(0, vocab, size=rows, dtype=np.uint32)
+    tokens[0] = 0
+    tokens[-1] = vocab - 1
+    if rows > 2:
+        tokens[1] = vocab            # out of range: zeros
+    lay = ql.ArenaLayout()
+    e_off = lay.take(table.nbytes)
+    w = ctx.arena(lay.used)
+    w.write(e_off, table)
+    alay = ql.ArenaLayout()
+    t_off = alay.take(rows * 4)
+    o_off = alay.take(rows * D * 4 + pad) + pad
+    act = ctx.arena(alay.used)
+    act.write(t_off, tokens)
+    say(f"embed {label}: vocab={vocab} D={D} rows={rows}")
+    ctx.embed_f16(w, e_off, vocab, D, act, t_off, rows, o_off)
+    got = act.read(o_off, (rows, D), np.float32)
+    want = np.zeros((rows, D), np.float32)
+    ok = tokens < vocab
+    want[ok] = orc.f16_bits_to_f32(table[tokens[ok]].reshape(-1)).reshape(-1, D)
+    g, r = got.view(np.uint32), want.view(np.uint32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan), label
+    assert np.array_equal(g[~nan], r[~nan]), label
+    with pytest.raises(ql.QlError):          # table past the arena
+        ctx.embed_f16(w, e_off, vocab + 1, D, act, t_off, rows, o_off)
+    with pytest.raises(ql.QlError):          # tokens and out overlap
+        ctx.embed_f16(w, e_off, vocab, D, act, t_off, rows, t_off)
+    act.release()
+    w.release()
+
+
+def test_embed_through_host(ql, ctx, orc):
+    """QuantLinearModel.embed over an fp16 table uploaded as the loader does (upload_f16_bits)."""
+    from webllm_amd import gptq
+    vocab, C, M = 512, 896, 3
+    rng = np.random.default_rng(0xE3C)
+    table = (rng.standard_normal((vocab, C), dtype=np.float32) * 0.02).astype(np.float16)
+    model = gptq.QuantLinearModel(ctx, table.nbytes + 4096, scratch_capacity=4096)
+    model.upload_f16_bits("embed", table.view(np.uint16), (vocab, C))
+    pool = gptq.ActivationArena(ctx, 1 << 20)
+    toks = pool.alloc((M,), "u32")
+    out = pool.alloc((M, C))
+    ids = np.array([7, 0, vocab - 1], np.uint32)
+    toks.write(ids)
+    model.embed(toks, out, M)
+    assert np.array_equal(out.read(), table[ids].astype(np.float32))
+    with pytest.raises(ValueError):
+        model.embed(out, out, M)
+    pool.arena.release()
+    model.release()

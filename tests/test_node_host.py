@@ -36,7 +36,7 @@ BINDING = {
     "graphBegin": "ql_graph_begin", "graphEnd": "ql_graph_end", "graphLaunch": "ql_graph_launch",
     "graphDestroy": "ql_graph_destroy", "seqCreate": "ql_seq_create", "seqRun": "ql_seq_run",
     "seqStatus": "ql_seq_status", "seqInfo": "ql_seq_get_info", "seqDestroy": "ql_seq_destroy",
-    "gemvF16w": "ql_gemv_f16w", "kvStore": "ql_kv_store", "attention": "ql_attention_decode",
+    "gemvF16w": "ql_gemv_f16w", "embedF16": "ql_embed_f16", "kvStore": "ql_kv_store", "attention": "ql_attention_decode",
     "addRmsNorm": "ql_add_rmsnorm", "siluMul": "ql_silu_mul",
 }
 

@@ -410,6 +410,10 @@ def test_fused_validation():
 
     f = ql.make_fuse
     assert code([f(norm_w_off=w, x2_off=y0), f()]) == "QL_E_INVALID"          # norm and GLU both
+    # fused staging reads fp32 words: fp16 x is refused
+    with pytest.raises(ql.QlError) as e16:
+        ql.plan_seq(c.descs, 1, c.x, c.y, 256, ql.DTYPE_F16, fuse=[f(norm_w_off=w), f()])
+    assert e16.value.name == "QL_E_INVALID" and "fp32 x" in str(e16.value)
     assert code([f(res_off=c.y[1]), f()]) == "QL_E_INVALID"                      # residual from a later linear
     assert code([f(), f(norm_w_off=w + 4)]) == "QL_E_ALIGN"                      # norm weight alignment
     assert code([f(), f(norm_w_off=w, norm_eps=-1.0)]) == "QL_E_INVALID"

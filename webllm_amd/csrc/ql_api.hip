@@ -386,6 +386,9 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
     }
     if (any && prefill)
         return fail(QL_E_INVALID, "fused elementwise work runs in decode sequences (M = 1..%d)", ql::kGemvMaxM);
+    // the fused staging reads fp32 words (norm weight, x2 and residual products are fp32)
+    if (any && x_dtype != QL_DTYPE_F32)
+        return fail(QL_E_INVALID, "fused sequences take fp32 x (x_dtype QL_DTYPE_F32)");
     return QL_OK;
 }
 
@@ -1166,6 +1169,33 @@ int ql_gemv_f16w(ql_ctx* ctx, const ql_arena* weights, uint64_t w_off, uint64_t 
     a.N = N;
     a.K = K;
     QL_HIP(ql::launch_gemv_f16w(a, ql::gemv_f16w_fast_ok(M, N, K), ctx->cu_count, ctx->stream));
+    return QL_OK;
+}
+
+int ql_embed_f16(ql_ctx* ctx, const ql_arena* weights, uint64_t embed_off, int32_t vocab, int32_t D,
+                 ql_arena* act, uint64_t tokens_off, int32_t rows, uint64_t out_off)
+{
+    if (!ctx || !weights || !act) return fail(QL_E_INVALID, "null context or arena");
+    if (rows < 1 || rows > 65535) return fail(QL_E_INVALID, "rows must be 1..65535 (got %d)", rows);
+    if (vocab < 1 || D < 1 || D > (1 << 24)) return fail(QL_E_DIMS, "vocab and D must be positive (D <= 2^24)");
+    if (!in_range(embed_off, (uint64_t)vocab * D * 2, weights->size))
+        return fail(QL_E_RANGE, "fp16 embedding [vocab, D] outside the weight arena");
+    if (!in_range(tokens_off, (uint64_t)rows * 4, act->size)) return fail(QL_E_RANGE, "tokens [rows] outside the activation arena");
+    if (!in_range(out_off, (uint64_t)rows * D * 4, act->size)) return fail(QL_E_RANGE, "out [rows, D] outside the activation arena");
+    if (embed_off % 2 || tokens_off % 4 || out_off % 4) return fail(QL_E_ALIGN, "embed 2-byte, tokens and out 4-byte aligned");
+    if (tokens_off < out_off + (uint64_t)rows * D * 4 && out_off < tokens_off + (uint64_t)rows * 4)
+        return fail(QL_E_INVALID, "tokens and out overlap");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    ql::EmbedArgs a;
+    a.w = reinterpret_cast<const uint16_t*>(weights->base + embed_off);
+    a.tokens = reinterpret_cast<const uint32_t*>(act->base + tokens_off);
+    a.out = reinterpret_cast<float*>(act->base + out_off);
+    a.vocab = vocab;
+    a.D = D;
+    a.rows = rows;
+    a.vec = D % 8 == 0 && embed_off % 16 == 0 && out_off % 16 == 0;
+    QL_HIP(ql::launch_embed_rows(a, ctx->stream));
     return QL_OK;
 }
 

@@ -150,6 +150,43 @@ bool gemv_f16w_fast_ok(int M, int N, int K)
     return M >= 1 && N > 0 && K > 0 && K % kStepK == 0 && gemv_f16w_lds(4, K) <= (96u << 10);
 }
 
+// The embedding lookup (embedding_f16.wgsl): out[r, :] = f32(W[tokens[r], :]). A workgroup covers
+// 2048 values of one row, 8 per lane (one 16-byte load, two 16-byte stores) where the row length
+// and offsets allow, else one value per load. A token id >= vocab writes zeros.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const EmbedArgs a)
+{
+    const int r = blockIdx.y;
+    const uint32_t tok = __builtin_amdgcn_readfirstlane(a.tokens[r]);
+    const bool ok = tok < (uint32_t)a.vocab;
+    const uint16_t* src = a.w + (size_t)(ok ? tok : 0u) * a.D;
+    float* dst = a.out + (size_t)r * a.D;
+    if (a.vec) {
+        const int i = (blockIdx.x * 256 + threadIdx.x) * 8;
+        if (i < a.D) {
+            f32x4 lo = f32x4{0.f, 0.f, 0.f, 0.f}, hi = lo;
+            if (ok) {
+                const f16x8 h = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(src + i));
+                lo = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+                hi = f32x4{(float)h[4], (float)h[5], (float)h[6], (float)h[7]};
+            }
+            *reinterpret_cast<f32x4*>(dst + i) = lo;
+            *reinterpret_cast<f32x4*>(dst + i + 4) = hi;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int i = blockIdx.x * 2048 + e * 256 + threadIdx.x;
+            if (i < a.D) dst[i] = ok ? (float)__builtin_bit_cast(_Float16, src[i]) : 0.f;
+        }
+    }
+}
+
+hipError_t launch_embed_rows(const EmbedArgs& a, hipStream_t stream)
+{
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((a.D + 2047) / 2048, a.rows), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv_f16w(const F16wArgs& a, bool fast, int cu_count, hipStream_t stream)
 {
     if (!fast) {

@@ -173,6 +173,16 @@ bool gemv_f16w_fast_ok(int M, int N, int K);
 size_t gemv_f16w_lds(int M, int K);
 hipError_t launch_gemv_f16w(const F16wArgs& a, bool fast, int cu_count, hipStream_t stream);
 
+// The embedding lookup over the fp16 table: out[r, :] = f32(w[tokens[r], :]).
+struct EmbedArgs {
+    const uint16_t* w;         // fp16 [vocab, D]
+    const uint32_t* tokens;    // [rows]
+    float* out;                // [rows, D]
+    int vocab, D, rows;
+    int vec;                   // D % 8 == 0 and w, out 16-byte aligned: 8 values per lane
+};
+hipError_t launch_embed_rows(const EmbedArgs& a, hipStream_t stream);
+
 // Decode attention over an fp32 KV cache [max_t, KV * D] and the cache store.
 constexpr int kAttnMaxT = 8192;        // visible keys per query row
 constexpr int kAttnMaxD = 256;

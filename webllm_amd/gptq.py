@@ -199,7 +199,7 @@ class Tensor:
     pool: "ActivationArena | None" = None
 
     def read(self) -> np.ndarray:
-        dt = {"f32": np.float32, "f16": np.float16, "u8": np.uint8}[self.dtype]
+        dt = {"f32": np.float32, "f16": np.float16, "u8": np.uint8, "u32": np.uint32}[self.dtype]
         return self.arena.read(self.offset, self.shape, dt)
 
     def write(self, data: np.ndarray):
@@ -215,7 +215,7 @@ class ActivationArena:
 
     def alloc(self, shape, dtype: str = "f32") -> Tensor:
         n = int(np.prod(shape))
-        size = n * (2 if dtype == "f16" else (1 if dtype == "u8" else 4))
+        size = n * {"f16": 2, "u8": 1}.get(dtype, 4)
         off = self.layout.take(size)
         if self.layout.used > self.arena.size:
             raise ValueError(f"activation arena exhausted ({self.layout.used} > {self.arena.size})")
@@ -376,6 +376,19 @@ class QuantLinearModel:
         scratch = A.pool.scratch_offset(plan.scratch_bytes)
         self.ctx.linear(desc, self.weights, A.arena, A.offset,
                         ql.DTYPE_F32 if A.dtype == "f32" else ql.DTYPE_F16, M, C.offset, scratch)
+
+    def embed(self, tokens: Tensor, out: Tensor, M: int, weight: str = "embed"):
+        """out[M, C] = the fp16 table's rows tokens[0..M) as f32: the forward's first dispatch
+        (embedding_f16.wgsl, qwen.ts:391-392). Token ids >= vocab give zero rows."""
+        w = self.f16.get(weight)
+        if w is None:
+            raise ValueError(f"missing f16 weight: {weight}")
+        vocab, C = w.shape
+        if tokens.dtype != "u32" or tokens.length < M:
+            raise ValueError("embed: tokens must be a u32 tensor of at least M ids")
+        if out.dtype != "f32" or out.length < M * C or out.arena is not tokens.arena:
+            raise ValueError("embed: out must be an f32 [M, C] tensor in the tokens' arena")
+        self.ctx.embed_f16(self.weights, w.offset, vocab, C, tokens.arena, tokens.offset, M, out.offset)
 
     def rmsnorm(self, x: Tensor, weight: str, y: Tensor, M: int, C: int, eps: float,
                 residual: Tensor | None = None, sum_out: Tensor | None = None):

@@ -79,13 +79,13 @@ export function dequantizeGptqInt4(params: GptqInt4Params, ctx?: Context): Float
 
 export class Tensor {
     readonly arena: Arena; readonly offset: number; readonly length: number;
-    readonly shape: number[]; readonly dtype: 'f32' | 'f16';
-    read(): Float32Array | Uint16Array;
+    readonly shape: number[]; readonly dtype: 'f32' | 'f16' | 'u32';
+    read(): Float32Array | Uint16Array | Uint32Array;
     write(data: ArrayBufferView): void;
 }
 export class ActivationArena {
     constructor(ctx: Context, bytes: number);
-    alloc(shape: number[], dtype?: 'f32' | 'f16'): Tensor;
+    alloc(shape: number[], dtype?: 'f32' | 'f16' | 'u32'): Tensor;
     scratchOffset(nbytes: number): number;
     reset(): void;
     release(): void;
@@ -103,6 +103,8 @@ export class QuantLinearModel {
     /** QwenGpt.gemm: C[M,N] = A[M,K] @ W^T (+ bias). */
     gemm(A: Tensor, weight: string, C: Tensor, bias: string | null, M: number, N: number, K: number): void;
     gemmBatch(A: Tensor, weights: string[], Cs: Tensor[], M: number): void;
+    /** out[M, C] = the fp16 table's rows tokens[0..M) as f32 (ql_embed_f16); ids >= vocab give zeros. */
+    embed(tokens: Tensor, out: Tensor, M: number, weight?: string): void;
     /** y = rmsnorm(x (+ residual)) * weight, the sum stored in sumOut (one launch: ql_add_rmsnorm). */
     rmsnorm(x: Tensor, weight: string, y: Tensor, M: number, C: number, eps: number,
             residual?: Tensor | null, sumOut?: Tensor | null): void;

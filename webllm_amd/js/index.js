@@ -324,7 +324,7 @@ class Tensor {
         this.dtype = dtype; this.pool = pool || null;
     }
     read() {
-        const T = this.dtype === 'f16' ? Uint16Array : Float32Array;
+        const T = this.dtype === 'f16' ? Uint16Array : (this.dtype === 'u32' ? Uint32Array : Float32Array);
         return this.arena.read(this.offset, new T(this.length));
     }
     write(data) { this.arena.write(this.offset, data); }
@@ -428,6 +428,18 @@ class QuantLinearModel {
         if (A.arena !== C.arena) throw new Error('gemm: A and C must live in the same activation arena');
         if (A.length < M * K || C.length < M * N) throw new Error('gemm: tensor too small for [M,K] / [M,N]');
         addon.gemvF16w(this.ctx.handle, this.weights.handle, w.offset, b, A.arena.handle, A.offset, M, N, K, C.offset);
+    }
+    /** out[M, C] = rows tokens[0..M) of the fp16 table as f32 (embedding_f16.wgsl, qwen.ts:391-392);
+     *  token ids >= vocab give zero rows. */
+    embed(tokens, out, M, weight) {
+        const name = weight || 'embed';
+        const w = this.f16Weights.get(name);
+        if (!w) throw new Error(`missing f16 weight: ${name}`);
+        const vocab = w.shape[0], C = w.shape[1];
+        if (tokens.dtype !== 'u32' || tokens.length < M) throw new Error('embed: tokens must be a u32 tensor of at least M ids');
+        if (out.dtype !== 'f32' || out.length < M * C || out.arena !== tokens.arena)
+            throw new Error("embed: out must be an f32 [M, C] tensor in the tokens' arena");
+        addon.embedF16(this.ctx.handle, this.weights.handle, w.offset, vocab, C, tokens.arena.handle, tokens.offset, M, out.offset);
     }
     /** y = rmsnorm(x (+ residual)) * weight; the sum goes to sumOut (vec_add + rmsnorm.wgsl in one launch). */
     rmsnorm(x, weight, y, M, C, eps, residual, sumOut) {

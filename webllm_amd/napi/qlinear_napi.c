@@ -465,6 +465,22 @@ static napi_value js_gemv_f16w(napi_env env, napi_callback_info info)
     return NULL;
 }
 
+/* embedF16(ctx, weights, embedOff, vocab, D, act, tokensOff, rows, outOff): embedding lookup */
+static napi_value js_embed_f16(napi_env env, napi_callback_info info)
+{
+    napi_value argv[9];
+    void *ctx, *w, *act;
+    uint64_t e_off, t_off, o_off;
+    int32_t vocab, D, rows;
+    if (get_args(env, info, 9, argv) || get_ptr(env, argv[0], &ctx) || get_ptr(env, argv[1], &w) ||
+        get_u64(env, argv[2], &e_off, 0) || get_i32(env, argv[3], &vocab) || get_i32(env, argv[4], &D) ||
+        get_ptr(env, argv[5], &act) || get_u64(env, argv[6], &t_off, 0) || get_i32(env, argv[7], &rows) ||
+        get_u64(env, argv[8], &o_off, 0))
+        return NULL;
+    throw_rc(env, ql_embed_f16((ql_ctx*)ctx, (ql_arena*)w, e_off, vocab, D, (ql_arena*)act, t_off, rows, o_off));
+    return NULL;
+}
+
 /* kvStore(ctx, act, srcOff, cache, cacheOff, maxT, rows, rowLen, pos0) */
 static napi_value js_kv_store(napi_env env, napi_callback_info info)
 {
@@ -807,7 +823,7 @@ static napi_value init(napi_env env, napi_value exports)
         {"graphLaunch", js_graph_launch}, {"graphDestroy", js_graph_destroy},
         {"seqCreate", js_seq_create}, {"seqRun", js_seq_run}, {"seqStatus", js_seq_status},
         {"seqInfo", js_seq_info}, {"seqDestroy", js_seq_destroy},
-        {"gemvF16w", js_gemv_f16w}, {"kvStore", js_kv_store}, {"attention", js_attention},
+        {"gemvF16w", js_gemv_f16w}, {"embedF16", js_embed_f16}, {"kvStore", js_kv_store}, {"attention", js_attention},
         {"addRmsNorm", js_add_rmsnorm}, {"siluMul", js_silu_mul},
     };
     for (size_t i = 0; i < sizeof fns / sizeof fns[0]; i++) {

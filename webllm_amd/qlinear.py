@@ -140,6 +140,7 @@ def lib():
         "ql_plan_linear": (I, [I, I, I, I, ctypes.POINTER(Plan)]),
         "ql_gemv_f16w": (I, [P, P, U64, U64, P, U64, I, I, I, U64]),
         "ql_kv_store": (I, [P, P, U64, P, U64, I, I, I, I]),
+        "ql_embed_f16": (I, [P, P, U64, I, I, P, U64, I, U64]),
         "ql_add_rmsnorm": (I, [P, P, U64, U64, P, U64, ctypes.c_float, I, I, U64, U64]),
         "ql_silu_mul": (I, [P, P, U64, U64, ctypes.c_int64, U64]),
         "ql_attention_decode": (I, [P, P, U64, P, U64, U64, I, I, I, I, I, I, U64]),
@@ -375,6 +376,13 @@ class Context:
         _check(lib().ql_gemv_f16w(self.handle, weights.handle, w_off,
                                   QL_NONE if bias_off is None else bias_off, act.handle, x_off, M, N,
                                   K, y_off))
+
+    def embed_f16(self, weights: Arena, embed_off: int, vocab: int, D: int, act: Arena, tokens_off: int,
+                  rows: int, out_off: int):
+        """out[r, :] = f32(embed[tokens[r], :]) (embedding_f16.wgsl; qwen.ts:392); token ids >= vocab
+        give zero rows."""
+        _check(lib().ql_embed_f16(self.handle, weights.handle, embed_off, vocab, D, act.handle, tokens_off,
+                                  rows, out_off))
 
     def kv_store(self, act: Arena, src_off: int, cache: Arena, cache_off: int, max_t: int, rows: int,
                  row_len: int, pos0: int):
