@@ -52,6 +52,24 @@ SEQ_LAYER_7B = [("q", None), ("o", "q"), ("gate", "o"), ("up", "o"), ("down", "g
 NORM_EPS = 1e-6          # Qwen2.5's rms_norm_eps
 
 
+def step_inputs(shape: str, M: int, chained: bool) -> list[tuple[int, int, tuple]]:
+    """The external inputs SeqStep writes, in its order, as (linear index, K, synth key): the
+    first linear's input (the layer-0 residual stream when chained) has key (0, 0, M); in the step
+    as written (chained=False) every further linear has an input of its own, key (layer + 1, i, M)
+    for linear i of each layer. Host only; tests/golden/make_digests.py hashes the same list."""
+    seq = SEQ_LAYER_05B if shape == "0.5b" else SEQ_LAYER_7B
+    K = {p: k for p, k, _ in (synth.PROJ_05B if shape == "0.5b" else synth.PROJ_7B)}
+    layers = synth.QWEN05_LAYERS if shape == "0.5b" else synth.QWEN7_LAYERS
+    out = [(0, K[seq[0][0]], (0, 0, M))]
+    if not chained:
+        for layer in range(layers):
+            for i, (proj, _) in enumerate(seq):
+                n = layer * len(seq) + i
+                if n > 0:
+                    out.append((n, K[proj], (layer + 1, i, M)))
+    return out
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -195,10 +213,11 @@ class SeqStep:
         lay = ql.ArenaLayout()
         descs, xs, ys = [], [], []
         self.order = []
-        inputs = []          # (offset, K, key) of every externally written input
+        ext = {n: (K, key) for n, K, key in step_inputs(model.shape, M, chained)}
+        inputs = []          # (offset, K, key) of every externally written input, in ext's order
         C = model.shapes[(0, "q")][0]
         h0 = lay.take(M * C * 4)
-        inputs.append((h0, C, (0, 0, M)))
+        inputs.append((h0,) + ext[0])
         h = h0
         fuse = []
         for layer in range(model.layers):
@@ -220,9 +239,11 @@ class SeqStep:
                         fuse.append(ql.make_fuse(x2_off=y["up"], res_off=y["o"]))
                 else:
                     # the benchmark configs as written: every linear has its own x ~ N(0,1)
-                    x_off = h0 if layer == 0 and i == 0 else lay.take(M * d.K * 4)
-                    if x_off != h0:
-                        inputs.append((x_off, d.K, (layer + 1, i, M)))
+                    n = len(self.order)
+                    x_off = h0 if n == 0 else lay.take(M * d.K * 4)
+                    if n > 0:
+                        assert ext[n][0] == d.K
+                        inputs.append((x_off,) + ext[n])
                 y[proj] = lay.take(M * d.N * 4)
                 descs.append(d)
                 xs.append(x_off)

@@ -41,13 +41,11 @@ def weights_digest(shape: str, seed: int, layers=None) -> str:
 
 
 def step_inputs_digest(shape: str, M: int, seed: int = 0x5EED) -> str:
-    """The external inputs of bench.SeqStep(model, M, chained=False), in the order it writes them."""
+    """The external inputs of bench.SeqStep(model, M, chained=False), from the list SeqStep itself
+    writes (bench.step_inputs), in its order."""
+    import bench
     h = hashlib.sha256()
-    first = True
-    for (layer, proj, K, N) in synth.model_linears(shape):
-        i = PROJS[shape].index(proj)
-        key = (0, 0, M) if first else (layer + 1, i, M)
-        first = False
+    for _, K, key in bench.step_inputs(shape, M, chained=False):
         h.update(synth.activations(M, K, seed=seed, key=key).tobytes())
     return h.hexdigest()
 

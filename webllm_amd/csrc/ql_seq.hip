@@ -406,7 +406,10 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
         } else {
             const uint64_t* pll = L.src >= 0 ? uniform_ptr(ld_const(&a.lin[L.src].y_ll)) : nullptr;
             const int cpr = L.K / 8;
-            for (int m = 0; m < M; m++)
+            for (int m = 0; m < M; m++) {
+                // the row's sum in a scalar, then into ss[m] by compile-time indices (a runtime
+                // index into a register array would put ss in scratch memory)
+                float rs = 0.f;
                 for (int c = lane; c < cpr && ok; c += 64) {
                     const size_t xo = (size_t)m * L.K + (size_t)c * 8;
                     float v[8];
@@ -418,8 +421,12 @@ __global__ __launch_bounds__(64 * W) void seq_kernel(const SeqArgs a)
                         load8(L.x, L.x_dtype, xo, v);
                     }
 #pragma unroll
-                    for (int k = 0; k < 8; k++) ss[m] = fmaf(v[k], v[k], ss[m]);
+                    for (int k = 0; k < 8; k++) rs = fmaf(v[k], v[k], rs);
                 }
+#pragma unroll
+                for (int mm = 0; mm < 4 * T; mm++)
+                    if (mm == m) ss[mm] += rs;
+            }
         }
 #pragma unroll
         for (int m = 0; m < 4 * T; m++) {

@@ -536,7 +536,7 @@ struct StripKernel {
 #ifndef QL_STRIP_W4
 #define QL_STRIP_W4 8
 #endif
-// The planner starts each CU's second workgroup (workgroups kPlanCUs and up) this many
+// The planner starts each CU's second workgroup (the second half of a two-per-CU grid) this many
 // block-groups behind: its waves issue after the first workgroup's and stream at about half its
 // rate until that one's first strip ends. Measured on the 0.5B step (grid 512): 33.1 us per step
 // at 48 or 80 against 34.6 at 0 and 36.3 or more at 112 and up.
@@ -647,9 +647,14 @@ void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int spl
     std::vector<uint64_t> load(grid, 0), units(grid, 0);
     typedef std::pair<uint64_t, int> Slot;
     std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>> q;
-    // a CU's second workgroup starts behind its first (the first one's waves issue first)
+    // a CU's second workgroup starts behind its first (the first one's waves issue first). The
+    // dispatcher fills the CUs with workgroups 0 .. CUs-1 first, so with two per CU (strip_grid's
+    // rule: weights the MALL keeps, M <= QL_STRIP_MALL2_MAX_M) the second ones are grid/2 and up.
+    uint64_t bytes = 0;
+    for (const SeqSpec& s : lin) bytes += s.weight_bytes;
+    const int second = bytes <= kStripMallBytes && M <= QL_STRIP_MALL2_MAX_M ? grid / 2 : grid;
     for (int w = 0; w < grid; w++) {
-        load[w] = w >= kPlanCUs ? (uint64_t)QL_STRIP_SECOND_OFFSET : 0;
+        load[w] = w >= second ? (uint64_t)QL_STRIP_SECOND_OFFSET : 0;
         q.push({load[w], w});
     }
     for (const Item& it : items) {
