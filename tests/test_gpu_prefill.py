@@ -29,9 +29,10 @@ def x16(x):
 
 
 class PrefillSet:
-    """Independent linears in one weight arena, each with its own fp16 input."""
+    """Independent linears in one weight arena, each with its own fp16 input (x32: fp32 input,
+    which the launch rounds to fp16; the oracle reads the fp16-rounded values)."""
 
-    def __init__(self, ql, ctx, shapes, M, seed, group=128):
+    def __init__(self, ql, ctx, shapes, M, seed, group=128, x32=False):
         wl, al = ql.ArenaLayout(), ql.ArenaLayout()
         self.lin = []
         for i, (K, N, biased, g) in enumerate(shapes):
@@ -39,11 +40,12 @@ class PrefillSet:
             t = synth.gptq_linear(K, N, gs, seed=seed, key=(i,), stored_zero=7 if i % 2 else None)
             bias = synth.activations(1, N, seed=seed + 1, key=(i,))[0] if biased else None
             sym = i % 3 == 2
-            x = x16(synth.activations(M, K, seed=seed + 2, key=(i, M)))
-            self.lin.append({"t": t, "bias": bias, "group": gs, "x": x,
+            x_in = synth.activations(M, K, seed=seed + 2, key=(i, M))
+            x = x16(x_in)
+            self.lin.append({"t": t, "bias": bias, "group": gs, "x": x, "x_in": x_in,
                              "qw": wl.take(t.qweight.nbytes), "qz": None if sym else wl.take(t.qzeros.nbytes),
                              "sc": wl.take(t.scales.nbytes), "b": None if bias is None else wl.take(bias.nbytes),
-                             "xo": al.take(M * K * 2), "yo": al.take(M * N * 4),
+                             "xo": al.take(M * K * (4 if x32 else 2)), "yo": al.take(M * N * 4),
                              "qzeros": None if sym else t.qzeros})
         self.w = ctx.arena(wl.used)
         self.act = ctx.arena(al.used)
@@ -55,7 +57,7 @@ class PrefillSet:
             self.w.write(L["sc"], t.scales)
             if L["b"] is not None:
                 self.w.write(L["b"], L["bias"])
-            self.act.write(L["xo"], L["x"].astype(np.float16).view(np.uint16))
+            self.act.write(L["xo"], L["x_in"] if x32 else L["x"].astype(np.float16).view(np.uint16))
         self.descs = [ql.make_desc(L["qw"], L["qz"], L["sc"], L["t"].K, L["t"].N, L["group"], L["b"])
                       for L in self.lin]
         self.M = M
@@ -113,6 +115,43 @@ def test_prefill_seq_layers(ql, ctx, orc, M):
         for a, b in zip(ys, s.outputs()):
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"graph replay {r}"
     g.destroy()
+    seq.destroy()
+    s.release()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [128, 300])
+def test_prefill_seq_f32_input(ql, ctx, orc, M):
+    """fp32 x into the prefill launch, rounded to fp16 (nearest even) as it is staged, as the
+    reference's tile load does (gemm_nt_f16_from_f32.wgsl:60); the oracle reads the same
+    fp16-rounded x. Also the single-linear entry (QuantLinearModel.gemm's ql_linear) on a batch
+    that fills the device."""
+    s = PrefillSet(ql, ctx, LAYER * 2, M, seed=0x9F20, x32=True)
+    seq = ctx.seq(s.descs, s.w, s.act, [L["xo"] for L in s.lin], ql.DTYPE_F32, M, [L["yo"] for L in s.lin])
+    assert seq.info.kernel == ql.SEQ_PREFILL
+    seq.run()
+    seq.status()
+    ys = s.outputs()
+    s.check(orc, ys, f"prefill f32 x M={M}")
+    # gate and up (K = 896) through ql_linear_batch on fp32 x, against the oracle
+    pick = (4, 5)
+    lay = ql.ArenaLayout()
+    xo = [lay.take(M * 896 * 4) for _ in pick]
+    yo = [lay.take(M * s.lin[i]["t"].N * 4) for i in pick]
+    so = lay.take(max(256, ql.plan_batch([s.descs[i] for i in pick], M)))
+    act2 = ctx.arena(lay.used)
+    for o, i in zip(xo, pick):
+        act2.write(o, s.lin[i]["x_in"])
+    ctx.linear_batch([s.descs[i] for i in pick], s.w, act2, xo, ql.DTYPE_F32, M, yo, so)
+    ctx.sync()
+    for o, i in zip(yo, pick):
+        y = act2.read(o, (M, s.lin[i]["t"].N), np.float32)
+        t = s.lin[i]["t"]
+        ref = orc.gptq_linear_cols(t.qweight, s.lin[i]["qzeros"], t.scales, s.lin[i]["x"], np.arange(t.N),
+                                   s.lin[i]["bias"], s.lin[i]["group"], w_f16=True)
+        ok, ma, mr = orc.check_tolerance(y, ref, ATOL, RTOL)
+        assert ok, (i, ma, mr)
+    act2.release()
     seq.destroy()
     s.release()
 

@@ -254,8 +254,13 @@ def test_reject_width_mismatch():
 
 
 def test_reject_shapes_outside_the_sequence_kernel():
+    # M > 16 is the prefill launch, for fp32 x (rounded to fp16 as staged) as for fp16 x
     c = Chain(M=17)
     c.add(896, 896, c.ext(896))
+    assert c.plan().kernel == ql.SEQ_PREFILL
+    assert c.plan(x_dtype=ql.DTYPE_F16).kernel == ql.SEQ_PREFILL
+    c = Chain(M=17)
+    c.add(896, 898, c.ext(896))       # N % 4 != 0: no prefill tile form
     assert _err(c).name == "QL_E_INVALID"
     c = Chain()
     x = c.ext(896)

@@ -272,8 +272,8 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
         if (rc) return rc;
         if (prefill && !ql::prefill_ok(M, d->N, d->K, d->group, x_dtype))
             return fail(QL_E_INVALID,
-                        "linear %d: a prefill sequence (M > %d) needs fp16 x, N %% 4 == 0, groups a "
-                        "multiple of 128 dividing K, and M*N*4, M*K*2 and K*N/2 below 2^31 bytes", i,
+                        "linear %d: a prefill sequence (M > %d) needs N %% 4 == 0, groups a multiple of "
+                        "128 dividing K, and M*N*4, M*K*(x bytes) and K*N/2 below 2^31 bytes", i,
                         ql::kGemvMaxM);
         if (!prefill && (!ql::gemv_fast_ok(M, d->N, d->K, d->group) || d->group != descs[0].group))
             return fail(QL_E_INVALID,
@@ -620,7 +620,7 @@ void fill_prefill_info(const ql::PrefillPlan& p, int n, int M, const std::vector
 
 // Independent linears at M > 16: one prefill GEMM launch over a planned task table.
 int prefill_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights, ql_arena* act,
-                   const uint64_t* x_offs, int32_t M, const uint64_t* y_offs,
+                   const uint64_t* x_offs, int32_t x_dtype, int32_t M, const uint64_t* y_offs,
                    const std::vector<ql::SeqSpec>& specs, ql_seq** out)
 {
     ql::PrefillPlan pp;
@@ -638,7 +638,7 @@ int prefill_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_a
         L.qzeros = g.qzeros;
         L.scales = g.scales;
         L.bias = g.bias;
-        L.x = reinterpret_cast<const uint16_t*>(act->base + x_offs[i]);
+        L.x = act->base + x_offs[i];
         L.y = reinterpret_cast<float*>(act->base + y_offs[i]);
         L.N = d->N;
         L.K = d->K;
@@ -665,6 +665,7 @@ int prefill_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_a
     q->pargs.task_begin = reinterpret_cast<const int32_t*>(dev + lay.task_begin);
     q->pargs.M = M;
     q->pargs.G = pp.grid;
+    q->pargs.x_f32 = x_dtype == QL_DTYPE_F32 ? 1 : 0;
     fill_prefill_info(pp, n, M, specs, lay.total, &q->info);
     *out = q;
     return QL_OK;
@@ -1008,7 +1009,7 @@ bool prefill_batch(ql_ctx* ctx, int count, const ql_gptq_desc* descs, const ql_a
         L.qzeros = g.qzeros;
         L.scales = g.scales;
         L.bias = g.bias;
-        L.x = reinterpret_cast<const uint16_t*>(act->base + x_offs[i]);
+        L.x = act->base + x_offs[i];
         L.y = reinterpret_cast<float*>(act->base + y_offs[i]);
         L.N = descs[i].N;
         L.K = descs[i].K;
@@ -1019,6 +1020,7 @@ bool prefill_batch(ql_ctx* ctx, int count, const ql_gptq_desc* descs, const ql_a
     }
     a.total_tiles = begin;
     a.G = std::min(begin, ctx->cu_count);
+    a.x_f32 = x_dtype == QL_DTYPE_F32 ? 1 : 0;
     if ((*rc = set_device(ctx))) return true;
     const hipError_t e = ql::launch_prefill(a, false, ctx->stream);
     *rc = e == hipSuccess ? QL_OK : hip_fail(e, "launch_prefill");
@@ -1526,7 +1528,7 @@ int seq_create_impl(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
     const bool fused = seq_fused(specs);
-    if (M > ql::kGemvMaxM) return prefill_create(ctx, n, descs, weights, act, x_offs, M, y_offs, specs, out);
+    if (M > ql::kGemvMaxM) return prefill_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, specs, out);
     if (!fused && ql::strip_eligible(specs, M))
         return strip_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, specs, out);
     int per_cu = 0;

@@ -99,7 +99,7 @@ struct PrefillLinear {
     const uint32_t* qzeros;    // [K/group, ceil(N/8)] or nullptr (zero 8)
     const uint16_t* scales;    // [K/group, N] fp16 bits
     const float* bias;         // [N] or nullptr
-    const uint16_t* x;         // [M, K] fp16
+    const void* x;             // [M, K] fp16, or fp32 (PrefillArgs::x_f32)
     float* y;                  // [M, N]
     int32_t N, K, group;
     int32_t tiles_m;           // batch mode: row tiles, and the linear's first tile number
@@ -116,6 +116,7 @@ struct PrefillArgs {
     PrefillLinear L[kMaxBatch];// batch mode: the linears; workgroup w takes tiles w, w + G, ...
     int32_t count, total_tiles;
     int32_t M, G;
+    int32_t x_f32;             // 1: x is fp32, rounded to fp16 (RNE) as it is staged
 };
 struct PrefillSpec {
     int N, K;

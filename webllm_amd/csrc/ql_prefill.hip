@@ -1,5 +1,6 @@
 // Prefill GEMM over many GPTQ int4 linears in one persistent launch, M > 16:
-// y[M,N] = f16(x)[M,K] * f16(W)[N,K]^T (+ bias), fp32 accumulation, x fp16. The arithmetic of
+// y[M,N] = f16(x)[M,K] * f16(W)[N,K]^T (+ bias), fp32 accumulation, x fp16 or fp32 (rounded to
+// fp16 as it is staged, as gemm_nt_f16_from_f32.wgsl:60 does in its tile load). The arithmetic of
 // the reference's M > 1 path (gemm_nt_f16_from_f32.wgsl: fp16 operands, fp32 sums), with W
 // dequantized from the packed int4 words inside the kernel, bit-identical to the load-time fp16
 // arena (dequant_word_perm, ql_device.h).
@@ -74,6 +75,24 @@ __device__ __forceinline__ u32x4 perm_k8(u32x4 nat)
     return r;
 }
 
+// 8 activations (natural k order) as fp16 bits: fp16 as loaded, or fp32 rounded to nearest even
+template <bool XF32>
+__device__ __forceinline__ u32x4 to_f16x8(const u32x4* x)
+{
+    if constexpr (!XF32) {
+        return x[0];
+    } else {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const f32x4 lo = __builtin_bit_cast(f32x4, x[0]), hi = __builtin_bit_cast(f32x4, x[1]);
+        u32x4 r;
+        r.x = as_u32(__builtin_convertvector(f32x2{lo.x, lo.y}, f16x2));
+        r.y = as_u32(__builtin_convertvector(f32x2{lo.z, lo.w}, f16x2));
+        r.z = as_u32(__builtin_convertvector(f32x2{hi.x, hi.y}, f16x2));
+        r.w = as_u32(__builtin_convertvector(f32x2{hi.z, hi.w}, f16x2));
+        return r;
+    }
+}
+
 // One task's coordinates (uniform across the workgroup).
 struct Pos {
     int q;       // task ordinal in this workgroup's list
@@ -113,7 +132,9 @@ __device__ __forceinline__ PrefillLinear lin_at(const PrefillArgs& a, int li)
     return TABLE ? ld_tab(a.lin + li) : a.L[li];
 }
 
-template <bool TABLE>
+// XF32: fp32 activations, loaded as 32 bytes per 8-k piece and rounded to fp16 (round to
+// nearest even, v_cvt_pk_f16_f32) when the piece is written to LDS
+template <bool TABLE, bool XF32>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 void prefill_kernel(const PrefillArgs a)
 {
@@ -150,13 +171,15 @@ void prefill_kernel(const PrefillArgs a)
     nx.q = 0;
     nx.c = 0;
     task_at<TABLE>(a, w, 0, nx);
-    u32x4 xa[kAC];
+    constexpr int XS = XF32 ? 2 : 1;      // 16-byte loads per 8-k activation piece
+    constexpr uint32_t XE = XF32 ? 4 : 2;  // bytes per activation
+    u32x4 xa[kAC][XS];
     u32x4 wq[4];
     u32x2 sv;
     uint32_t zv;
     f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
     // lane-side pointers of the load position (recomputed when it enters a new task)
-    const uint16_t* xp[kAC];
+    const char* xp[kAC];
     const uint32_t* qwp;
     const uint16_t* scp;
     const uint32_t* qzp;
@@ -168,7 +191,7 @@ void prefill_kernel(const PrefillArgs a)
         const int nc = ncol < L.N ? ncol : 0;
 #pragma unroll
         for (int e = 0; e < kAC; e++)
-            xp[e] = L.x + (size_t)min(p.m0 + arow[e], M - 1) * L.K + 8 * apc[e];
+            xp[e] = static_cast<const char*>(L.x) + ((size_t)min(p.m0 + arow[e], M - 1) * L.K + 8 * apc[e]) * XE;
         qwp = L.qweight + nc + (size_t)kq * L.N;
         scp = L.scales + nc;
         qzp = L.qzeros ? L.qzeros + (nc >> 3) : &kPrefillSymZeros;
@@ -184,7 +207,10 @@ void prefill_kernel(const PrefillArgs a)
     // for them is one and the same), though only a task's first chunk stages it
     auto load_x = [&](int c) {
 #pragma unroll
-        for (int e = 0; e < kAC; e++) xa[e] = ld_global(reinterpret_cast<const u32x4*>(xp[e] + (size_t)c * 128));
+        for (int e = 0; e < kAC; e++)
+#pragma unroll
+            for (int h = 0; h < XS; h++)
+                xa[e][h] = ld_global(reinterpret_cast<const u32x4*>(xp[e] + (size_t)c * 128 * XE) + h);
         bv = ld_global(reinterpret_cast<const f32x4*>(bp));
     };
     auto load_sz = [&](int c) {
@@ -230,7 +256,7 @@ void prefill_kernel(const PrefillArgs a)
             // 1. this chunk's activations (and, at the task's first chunk, its bias) into LDS
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int e = 0; e < kAC; e++) As[slot][apc[e] >> 2][apc[e] & 3][arow[e] ^ apc[e]] = perm_k8(xa[e]);
+            for (int e = 0; e < kAC; e++) As[slot][apc[e] >> 2][apc[e] & 3][arow[e] ^ apc[e]] = perm_k8(to_f16x8<XF32>(xa[e]));
             if (c == 0 && threadIdx.x < 64) Bs[q & 1][threadIdx.x] = bv;
             uint32_t zz[4], ss[4];
             {
@@ -332,9 +358,9 @@ bool prefill_ok(int M, int N, int K, int group, int x_dtype)
 {
     // every buffer offset of the launch (activations, outputs, packed weights) stays below 2^31
     const int64_t lim = INT64_C(1) << 31;
-    return M > kGemvMaxM && x_dtype == 1 && N > 0 && N % 4 == 0 && group > 0 && group % 128 == 0 &&
-           K > 0 && K % group == 0 && (int64_t)M * N * 4 < lim && (int64_t)M * K * 2 < lim &&
-           (int64_t)K * N / 2 < lim;
+    return M > kGemvMaxM && (x_dtype == 0 || x_dtype == 1) && N > 0 && N % 4 == 0 && group > 0 &&
+           group % 128 == 0 && K > 0 && K % group == 0 && (int64_t)M * N * 4 < lim &&
+           (int64_t)M * K * (x_dtype == 0 ? 4 : 2) < lim && (int64_t)K * N / 2 < lim;
 }
 
 int prefill_tiles(int M, int N) { return ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN); }
@@ -392,10 +418,13 @@ void plan_prefill(const std::vector<PrefillSpec>& lin, int M, int grid, PrefillP
 hipError_t launch_prefill(const PrefillArgs& a, bool table, hipStream_t stream)
 {
     if (a.G < 1) return hipErrorInvalidValue;
-    if (table)
-        hipLaunchKernelGGL(prefill_kernel<true>, dim3(a.G), dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL(prefill_kernel<false>, dim3(a.G), dim3(256), 0, stream, a);
+    if (table) {
+        if (a.x_f32) hipLaunchKernelGGL((prefill_kernel<true, true>), dim3(a.G), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((prefill_kernel<true, false>), dim3(a.G), dim3(256), 0, stream, a);
+    } else {
+        if (a.x_f32) hipLaunchKernelGGL((prefill_kernel<false, true>), dim3(a.G), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((prefill_kernel<false, false>), dim3(a.G), dim3(256), 0, stream, a);
+    }
     return hipGetLastError();
 }
 
