@@ -320,25 +320,28 @@ class SeqStep:
 class PrefillStep:
     """The prefill step as configured (config 3): all linears of the model, each on its own fp16
     activations [M, K] ~ N(0,1), as ONE persistent prefill GEMM launch (ql_seq_* at M > 16: tasks
-    of 128 x 256 output tiles over all of K, planned longest first onto one workgroup per CU)."""
+    of 128 x 256 output tiles over all of K, planned longest first onto one workgroup per CU).
+    x_dtype=DTYPE_F32: the same activations as fp32, rounded to fp16 inside the launch as the
+    reference's gemm_nt_f16_from_f32.wgsl does."""
 
-    def __init__(self, ctx, model: Model, M: int, seed: int = 0x5EED):
+    def __init__(self, ctx, model: Model, M: int, seed: int = 0x5EED, x_dtype: int = ql.DTYPE_F16):
         self.ctx, self.model, self.M = ctx, model, M
         lay = ql.ArenaLayout()
         descs, xs, ys = [], [], []
         self.order = []
+        es = 4 if x_dtype == ql.DTYPE_F32 else 2
         for (layer, proj, K, N) in model.linears:
             descs.append(model.descs[(layer, proj)])
-            xs.append(lay.take(M * K * 2))
+            xs.append(lay.take(M * K * es))
             ys.append(lay.take(M * N * 4))
             self.order.append((layer, proj))
         self.act = ctx.arena(lay.used)
         for i, (layer, proj) in enumerate(self.order):
             K = model.shapes[(layer, proj)][0]
             x = synth.activations(M, K, seed=seed, key=(layer, synth.PROJ_INDEX[proj], M))
-            self.act.write(xs[i], x.astype(np.float16).view(np.uint16))
+            self.act.write(xs[i], x if es == 4 else x.astype(np.float16).view(np.uint16))
         self.x_offs, self.y_offs = xs, ys
-        self.seq = ctx.seq(descs, model.arena, self.act, xs, ql.DTYPE_F16, M, ys)
+        self.seq = ctx.seq(descs, model.arena, self.act, xs, x_dtype, M, ys)
         self.info = self.seq.info
         self.flops = sum(2 * M * model.shapes[lp][0] * model.shapes[lp][1] for lp in self.order)
         self.graph = None
@@ -702,6 +705,13 @@ def main():
                 "balance": round(st.info.balance, 4)}
             log(f"prefill M={M} one launch: {pre[f'{M}_one_launch']}")
             st.release()
+            # fp32 activations into the same launch (rounded to fp16 as staged)
+            st = PrefillStep(ctx, m05, M, x_dtype=ql.DTYPE_F32)
+            kms = st.kernel_ms(max(10, args.steps // 2))
+            tf = st.flops / (kms * 1e-3) / 1e12
+            pre[f"{M}_one_launch_f32x"] = {"kernel_us": round(kms * 1e3, 1), "tflops": round(tf, 2),
+                                          "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4)}
+            st.release()
         for layered in ((False, True) if only != "prefill_one" else ()):
             for M in (128, 512):
                 st = Step(ctx, m05, M, x_dtype=ql.DTYPE_F16, layered=layered)
@@ -713,7 +723,8 @@ def main():
                 st.release()
         pre["note"] = ("M x 168 linears, fp16 x, fp32 y. _one_launch: the config as written (each linear "
                        "on its own input) as one persistent prefill launch (tflops from the kernel "
-                       "time: graphs of 10 launches, HIP events). Plain M: the same as ql_linear_batch "
+                       "time: graphs of 10 launches, HIP events); _one_launch_f32x: the same launch fed "
+                       "fp32 x, rounded to fp16 as staged. Plain M: the same as ql_linear_batch "
                        "launches of 8 linears. _layered: the model's dependency order, one launch per "
                        "(q,k,v | o | gate,up | down) group (96 launches)")
         extra["prefill05"] = pre
