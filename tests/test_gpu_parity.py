@@ -551,24 +551,47 @@ def test_graph_replay_matches_eager(ql, ctx):
 # ------------------------------------------------------------------------- fp16-weight GEMV
 
 F16W_CASES = [
-    # (M, N, K, bias, label)
-    (1, 151936, 896, False, "0.5B tied lm_head M=1"),
-    (3, 4100, 896, True, "M=3, ragged N, bias"),
-    (6, 1000, 1024, False, "M=6: two passes over the weights"),
-    (2, 300, 200, True, "K % 128 != 0: one lane per output"),
-    (21, 2048, 896, True, "M=21: prefill rows, six passes over the weights"),
+    # (M, N, K, bias, subnormal share of W, x spread, label)
+    (1, 151936, 896, False, 0, False, "0.5B tied lm_head M=1 (fp32-FMA kernel)"),
+    (4, 151936, 896, False, 0, False, "0.5B tied lm_head M=4 (matrix cores)"),
+    (16, 20000, 896, True, 0, False, "M=16: one pass, bias"),
+    (3, 4100, 896, True, 0, False, "M=3, ragged N, bias"),
+    (6, 1000, 1024, False, 0, False, "M=6"),
+    (2, 300, 200, True, 0, False, "K % 32 != 0, bias"),
+    (21, 2048, 896, True, 0, False, "M=21: prefill rows, two passes over the weights"),
+    (16, 8192, 896, False, 0.1, False, "10% subnormal weights"),
+    (3, 4100, 896, True, 0.02, True, "x past fp16's range and in its subnormals, 2% subnormal W"),
+    (5, 777, 3584, True, 0.01, True, "K=3584 (7B width), x past fp16's range and in its subnormals"),
 ]
 
 
-@pytest.mark.parametrize("M,N,K,biased,label", F16W_CASES)
-def test_gemv_f16w_matches_oracle(ql, ctx, orc, M, N, K, biased, label):
-    """The tied lm_head product (qwen.ts:488-489, gemm_gemv_f16.wgsl): fp32 x, fp16 W [N,K],
-    fp32 accumulation, against gemmNTRef on the fp16-decoded weights (double accumulation) at the
-    GEMV bar; repeats are bit-identical."""
+def f16w_case(M, N, K, biased, sub, spread):
+    """W ~ 0.02 N(0,1) in fp16 (about 0.24% of it subnormal by itself), with a share `sub` set to
+    uniform subnormals; x ~ N(0,1) per row, with `spread` setting x[0, 5] = 1e5 (past fp16's range,
+    so unscaled fp16 parts of x would overflow) and scaling row 1 by 1e-6 (into fp16's
+    subnormals)."""
     rng = np.random.default_rng(0xF16 + N)
-    W16 = (rng.standard_normal((N, K), dtype=np.float32) * 0.02).astype(np.float16)
+    W = rng.standard_normal((N, K), dtype=np.float32) * 0.02
+    if sub:
+        mask = rng.random((N, K)) < sub
+        W[mask] = (rng.random(int(mask.sum())) * 2 - 1).astype(np.float32) * 6.0e-5
+    W16 = W.astype(np.float16)
     bias = synth.activations(1, N, seed=0xF17)[0] if biased else None
     x = synth.activations(M, K, seed=0xF18, key=(M,))
+    if spread:
+        x[0, 5] = 1e5
+        if M > 1:
+            x[1] *= 1e-6
+    return W16, bias, x
+
+
+@pytest.mark.parametrize("M,N,K,biased,sub,spread,label", F16W_CASES)
+def test_gemv_f16w_matches_oracle(ql, ctx, orc, M, N, K, biased, sub, spread, label):
+    """The tied lm_head product (qwen.ts:488-489, gemm_gemv_f16.wgsl): fp32 x, fp16 W [N,K],
+    fp32 accumulation, against gemmNTRef on the fp16-decoded weights (double accumulation) at the
+    GEMV bar; repeats are bit-identical. The spread cases exercise the matrix-core kernel's per-row,
+    per-step scaling of x into fp16 parts."""
+    W16, bias, x = f16w_case(M, N, K, biased, sub, spread)
     lay = ql.ArenaLayout()
     w_off = lay.take(W16.nbytes)
     b_off = lay.take(N * 4) if biased else None
