@@ -446,10 +446,10 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
 // Device tables of a column-strip sequence: linears, strips, per-workgroup strip ranges, and
 // stored-7 qzeros words for linears without qzeros.
 struct StripLayout {
-    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, total;
+    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, partial, total;
 };
 
-StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripPlan& p)
+StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripPlan& p, int M)
 {
     StripLayout L;
     uint64_t off = 0;
@@ -468,6 +468,8 @@ StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripP
             L.sym_words = std::max<uint64_t>(L.sym_words, (uint64_t)(specs[i].K / specs[i].group) *
                                                               ((specs[i].N + 7) / 8));
     L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
+    // K-split strips' partial sums: [slot][part][M][strip columns]
+    L.partial = take(sizeof(float) * (uint64_t)p.kslots * ql::kStripMaxKParts * M * ql::kStripMaxCols);
     L.total = off;
     return L;
 }
@@ -477,9 +479,9 @@ void fill_strip_info(const ql::StripPlan& p, int n, uint64_t scratch, ql_seq_inf
     info->linears = n;
     info->passes = 1;
     info->tiles = p.strips;
-    info->reduces = 0;
+    info->reduces = p.kslots;
     info->grid = p.grid;
-    info->max_split = 1;
+    info->max_split = p.max_parts;
     info->lds_bytes = p.lds_bytes;
     info->device_bytes = scratch;
     info->total_units = p.total_units;
@@ -521,7 +523,8 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
 {
     ql::StripPlan sp;
     ql::plan_strips(specs, M, ql::strip_grid(ctx->cu_count, specs, M), &sp);
-    const StripLayout lay = strip_layout(specs, sp);
+    if (sp.kslots > ql::kCounterCapacity) return fail(QL_E_INVALID, "too many K-split strips (%d)", sp.kslots);
+    const StripLayout lay = strip_layout(specs, sp, M);
     char* dev = nullptr;
     QL_HIP(hipMalloc(&dev, lay.total));
     std::vector<ql::SeqLinear> lin(n);
@@ -568,6 +571,8 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     q->sargs.split = sp.split;
     q->sargs.stream = sp.stream ? 1 : 0;
     q->sargs.wide = sp.wide ? 1 : 0;
+    q->sargs.partial = reinterpret_cast<float*>(dev + lay.partial);
+    q->sargs.counters = ctx->counters;
     fill_strip_info(sp, n, lay.total, &q->info);
     *out = q;
     return QL_OK;
@@ -1486,7 +1491,7 @@ int plan_seq_impl(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_
     if (!seq_fused(specs) && ql::strip_eligible(specs, M)) {
         ql::StripPlan sp;
         ql::plan_strips(specs, M, grid, &sp);
-        fill_strip_info(sp, n, strip_layout(specs, sp).total, info);
+        fill_strip_info(sp, n, strip_layout(specs, sp, M).total, info);
         return QL_OK;
     }
     ql::SeqPlanOut p;
