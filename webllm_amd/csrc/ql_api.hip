@@ -446,7 +446,10 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
 // Device tables of a column-strip sequence: linears, strips, per-workgroup strip ranges, and
 // stored-7 qzeros words for linears without qzeros.
 struct StripLayout {
-    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, partial, total;
+    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, partial;
+    uint64_t dimg, dimg_base, dimg_lin;   // the wide kernel's digit images and their tables
+    int32_t dimg_count;
+    uint64_t total;
 };
 
 StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripPlan& p, int M)
@@ -470,6 +473,13 @@ StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripP
     L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
     // K-split strips' partial sums: [slot][part][M][strip columns]
     L.partial = take(sizeof(float) * (uint64_t)p.kslots * ql::kStripMaxKParts * M * ql::kStripMaxCols);
+    // strip_wide_kernel: one digit image per 512-k chunk of every linear
+    L.dimg_count = 0;
+    if (p.wide)
+        for (int i = 0; i < n; i++) L.dimg_count += specs[i].K / 512;
+    L.dimg_base = take(sizeof(int32_t) * std::max(1, n));
+    L.dimg_lin = take(sizeof(int32_t) * std::max(1, L.dimg_count));
+    L.dimg = take(p.wide ? ql::strip_wide_image_bytes(M) * (uint64_t)L.dimg_count : 16);
     L.total = off;
     return L;
 }
@@ -553,6 +563,16 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     if (e == hipSuccess)
         e = hipMemcpy(dev + lay.task_begin, sp.task_begin.data(), sizeof(int32_t) * sp.task_begin.size(),
                       hipMemcpyHostToDevice);
+    if (e == hipSuccess && sp.wide) {
+        std::vector<int32_t> base(n), owner;
+        for (int i = 0; i < n; i++) {
+            base[i] = (int32_t)owner.size();
+            owner.insert(owner.end(), specs[i].K / 512, i);
+        }
+        e = hipMemcpy(dev + lay.dimg_base, base.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy(dev + lay.dimg_lin, owner.data(), sizeof(int32_t) * owner.size(), hipMemcpyHostToDevice);
+    }
     if (e != hipSuccess) {
         (void)hipFree(dev);
         return hip_fail(e, "ql_seq_create upload");
@@ -573,6 +593,10 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     q->sargs.wide = sp.wide ? 1 : 0;
     q->sargs.partial = reinterpret_cast<float*>(dev + lay.partial);
     q->sargs.counters = ctx->counters;
+    q->sargs.dimg = sp.wide ? dev + lay.dimg : nullptr;
+    q->sargs.dimg_base = reinterpret_cast<const int32_t*>(dev + lay.dimg_base);
+    q->sargs.dimg_lin = reinterpret_cast<const int32_t*>(dev + lay.dimg_lin);
+    q->sargs.dimg_count = lay.dimg_count;
     fill_strip_info(sp, n, lay.total, &q->info);
     *out = q;
     return QL_OK;

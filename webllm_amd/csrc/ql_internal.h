@@ -370,6 +370,14 @@ struct StripArgs {
     // counter per slot (zero before every launch; the last arrival leaves it at zero)
     float* partial;
     uint32_t* counters;
+    // strip_wide_kernel: each linear's activation digits, precomputed by wide_digits_kernel (one
+    // workgroup per chunk, launched first) as images of the kernel's LDS chunk buffer: linear i's
+    // chunk c at dimg + (dimg_base[i] + c) * strip_wide_image_bytes(M); dimg_lin[j] is the linear
+    // of image j, dimg_count the images
+    char* dimg;
+    const int32_t* dimg_base;
+    const int32_t* dimg_lin;
+    int32_t dimg_count;
 };
 
 struct StripPlan {
@@ -394,6 +402,7 @@ hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream);
 bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan& p);
 size_t strip_wide_lds(int M);
 int strip_wide_per_cu(int M);          // workgroups per CU of the wide kernel at M rows
+size_t strip_wide_image_bytes(int M);   // one chunk's digit image
 hipError_t launch_strips_wide(const StripArgs& a, size_t lds, hipStream_t stream);
 
 }  // namespace ql

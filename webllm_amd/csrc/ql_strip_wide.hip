@@ -16,7 +16,12 @@
 //   and chunk (k = the chunk's 4 groups: A = the groups' row sums, B = -s*z of the lane's
 //   columns, loaded per lane for group chunk + kq), added to the sums once per chunk, instead of
 //   one FMA per output and job;
-// * every LDS address is a lane constant plus a compile-time offset, and positions never branch.
+// * every LDS address is a lane constant plus a compile-time offset, and positions never branch;
+// * the activation digits are computed once per (linear, chunk) by wide_digits_kernel, launched
+//   just before, as images of the LDS chunk buffer; each strip's workgroup copies the image
+//   instead of computing the digits itself (every strip of a linear used to recompute them: about
+//   46 of the 7B step's 255 vector instructions per job at M=16). The 7B step at M=16: 792-799
+//   against 827-832 us (the digits launch itself 24.7 us); M=8 unchanged within noise.
 // Each job's epilogue is then, per output, two integer recombinations, two conversions, one FMA
 // for the digit value and one multiply-add with scale * 2^-E.
 #include <type_traits>
@@ -100,6 +105,10 @@ struct WideLayout {
     static constexpr int kLds = 2 * kBufB + kBiasB + kZB;
     // 8-value staging items per thread and chunk: kCG groups x kMaxM rows x 16 pieces of 8 k
     static constexpr int kH = (kCG * kMaxM * 16 + kThreads - 1) / kThreads;
+    // a chunk buffer as 16-byte units, and the units each thread copies from its digit image
+    static constexpr int kUnits = kBufB / 16;
+    static constexpr int kHI = (kUnits + kThreads - 1) / kThreads;
+    static_assert(kBufB % 16 == 0, "whole 16-byte units");
 };
 
 // Reductions over the 16 lanes of a row by DPP row rotations (every lane ends with the combined
@@ -154,6 +163,62 @@ __device__ __forceinline__ float2 stage_piece(const float v[8], uint2* row0, int
     return float2{ldexpf(1.f, -E - 8), sum};
 }
 
+// The activation digits of one chunk of one linear (workgroup j: image j), laid out as
+// strip_wide_kernel's LDS chunk buffer: digits of every (group, row < M, 8-k piece) by
+// stage_piece, zeros for rows M and up, then {2^-(E+8), sum x} per (group, row). Built in LDS, then
+// copied out whole. Each strip of the linear copies the image instead of computing it.
+template <int L>
+__global__ __launch_bounds__(kThreads) void wide_digits_kernel(const StripArgs a)
+{
+    using Lay = WideLayout<L>;
+    extern __shared__ uint4 dyn_lds[];
+    char* const lds = reinterpret_cast<char*>(dyn_lds);
+    const int M = a.M;
+    const int j = blockIdx.x;
+    const int li = tab(a.dimg_lin + j);
+    const int ch = j - tab(a.dimg_base + li);
+    const SeqLinear* Lp = a.lin + li;
+    const __amdgpu_buffer_rsrc_t rx = rsrc(sptr(tab(&Lp->x)));
+    const int K = tab(&Lp->K);
+    const int xdt = tab(&Lp->x_dtype);
+    for (int o = threadIdx.x * 16; o < Lay::kBufB; o += kThreads * 16)
+        *reinterpret_cast<uint4*>(lds + o) = uint4{0u, 0u, 0u, 0u};
+    __syncthreads();
+    const int items = kCG * M * 16;
+    const int g0 = ch * kCG;
+    float2* const gs = reinterpret_cast<float2*>(lds + Lay::kDigB);
+#pragma unroll
+    for (int h = 0; h < Lay::kH; h++) {
+        const int idx = (int)threadIdx.x + kThreads * h;
+        if (idx < items) {                        // whole 16-lane groups: items is a multiple of 16
+            const int item = idx >> 4, c = idx & 15;
+            const int gg = item / M, m = item - gg * M;
+            const uint32_t e = (uint32_t)m * (uint32_t)K + (uint32_t)((g0 + gg) * 128 + c * 8);
+            float v[8];
+            if (xdt == 0) {
+                const f32x4 lo = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, e * 4u, 0, 0));
+                const f32x4 hi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, e * 4u + 16u, 0, 0));
+                v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+                v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+            } else {
+                const f16x8 hv = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, e * 2u, 0, 0));
+#pragma unroll
+                for (int q = 0; q < 8; q++) v[q] = (float)hv[q];
+            }
+            // piece c covers k 8c .. 8c+7 of the group: 64-k block c / 8, lane group
+            // (c % 8) / 2 of its B operand, 8-byte half c % 2 of the 16-byte row
+            const int row = L == 0 ? (m >> 2) * 16 + 4 * (m & 3) : m;
+            char* const r0 = lds + gg * Lay::kGB + (c >> 3) * Lay::kBbB + ((c & 7) >> 1) * Lay::kKqB + row * 16 + (c & 1) * 8;
+            const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8);
+            if (c == 0) gs[gg * 16 + m] = s2;
+        }
+    }
+    __syncthreads();
+    char* const dst = a.dimg + (size_t)j * Lay::kBufB;
+    for (int o = threadIdx.x * 16; o < Lay::kBufB; o += kThreads * 16)
+        st_global(reinterpret_cast<u32x4*>(dst + o), *reinterpret_cast<const u32x4*>(lds + o));
+}
+
 // Waves per SIMD the M 5..8 instance is compiled for. At 4 it fits 128 VGPRs (some spilled) and
 // a CU holds two of its workgroups, planned as 512: the 7B step at M=8 measured 653 against
 // 603-610 us with one workgroup per CU (2), so 2 is kept.
@@ -183,15 +248,11 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     float* const bias_base = reinterpret_cast<float*>(lds + 2 * Lay::kBufB);
     auto bias_lds = [&](int par) { return bias_base + par * (kBlocks * kCols); };
 
-    // digits of rows >= M stay zero: clear both chunk buffers once
-    for (int o = threadIdx.x * 16; o < 2 * Lay::kBufB; o += kThreads * 16)
-        *reinterpret_cast<uint4*>(lds + o) = uint4{0u, 0u, 0u, 0u};
-    __syncthreads();
 
-    // ---- staging: the chunk being staged (task si, chunk sch) ----
+    // ---- staging: the chunk being staged (task si, chunk sch): its digit image into LDS ----
     struct Stage {
-        int si, sch, ngroups, K, xdt, ct, has_bias;
-        __amdgpu_buffer_rsrc_t rx, rb, rz, rs;   // x, bias (x without one), the wave block's zeros, scales
+        int si, sch, ngroups, ct, has_bias;
+        __amdgpu_buffer_rsrc_t ri, rb, rz, rs;   // the linear's digit images, bias (x without one), the wave block's zeros, scales
         uint32_t Gz, Gs;
     };
     auto stage_open = [&](Stage& st, int ti) {
@@ -199,14 +260,11 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         const SeqLinear* Lp = a.lin + t.linear;
         st.si = ti;
         st.sch = 0;
-        const void* x = sptr(tab(&Lp->x));
         const float* b = tab(&Lp->bias);
         st.has_bias = b != nullptr;
-        st.rx = rsrc(x);
-        st.rb = rsrc(b ? static_cast<const void*>(sptr(b) + t.ct * kCols) : x);
-        st.K = tab(&Lp->K);
-        st.xdt = tab(&Lp->x_dtype);
-        st.ngroups = st.K / 128;
+        st.ri = rsrc(a.dimg + (size_t)tab(a.dimg_base + t.linear) * Lay::kBufB);
+        st.rb = rsrc(b ? static_cast<const void*>(sptr(b) + t.ct * kCols) : static_cast<const void*>(a.dimg));
+        st.ngroups = tab(&Lp->K) / 128;
         st.ct = t.ct;
         const int N = tab(&Lp->N);
         const uint32_t blk = (uint32_t)(t.ct + wave);
@@ -215,65 +273,31 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         st.Gz = (((uint32_t)N + 7u) >> 3) * 4u;
         st.Gs = (uint32_t)N * 2u;
     };
-    u32x4 xr[H][2];                         // raw activation bits: f32 (both) or f16 ([0])
+    u32x4 xr[Lay::kHI];                     // the chunk's image units of this thread
     float bv;                               // one bias value per thread (512 = a strip's columns)
     uint32_t zq;                            // zero word of group (chunk + kq), the lane's columns
     u32x2 sq;                               // scales of group (chunk + kq), the lane's 4 columns
-    // step 1: unconditional loads (threads past the chunk's items re-read its last item)
+    // step 1: unconditional loads (threads past the image's units re-read its last one)
     auto stage_issue = [&](const Stage& st) {
         const int g0 = st.sch * kCG;
-        const int items = kCG * M * 16;
+        const uint32_t img = (uint32_t)st.sch * (uint32_t)Lay::kBufB;
 #pragma unroll
-        for (int h = 0; h < H; h++) {
-            const int idx = min((int)threadIdx.x + kThreads * h, items - 1);
-            const int item = idx >> 4, c = idx & 15;
-            const int gg = item / M, m = item - gg * M;
-            const uint32_t e = (uint32_t)m * (uint32_t)st.K + (uint32_t)((g0 + gg) * 128 + c * 8);
-            if (st.xdt == 0) {
-                xr[h][0] = __builtin_amdgcn_raw_buffer_load_b128(st.rx, e * 4u, 0, 0);
-                xr[h][1] = __builtin_amdgcn_raw_buffer_load_b128(st.rx, e * 4u + 16u, 0, 0);
-            } else {
-                // the same number of loads on both paths keeps the step-5 wait exact
-                uint32_t e2 = e * 2u;
-                asm volatile("" : "+v"(e2));        // a second load, not merged with the first
-                xr[h][0] = __builtin_amdgcn_raw_buffer_load_b128(st.rx, e * 2u, 0, 0);
-                xr[h][1] = __builtin_amdgcn_raw_buffer_load_b128(st.rx, e2, 0, 0);
-            }
+        for (int h = 0; h < Lay::kHI; h++) {
+            const int u = min((int)threadIdx.x + kThreads * h, Lay::kUnits - 1);
+            xr[h] = __builtin_amdgcn_raw_buffer_load_b128(st.ri, (uint32_t)u * 16u, img, 0);
         }
         bv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(st.rb, st.has_bias ? threadIdx.x * 4u : 0u, 0, 0));
         zq = __builtin_amdgcn_raw_buffer_load_b32(st.rz, (uint32_t)kq * st.Gz + (uint32_t)(j >> 1) * 4u, (uint32_t)g0 * st.Gz, 0);
         sq = __builtin_amdgcn_raw_buffer_load_b64(st.rs, (uint32_t)kq * st.Gs + (uint32_t)j * 8u, (uint32_t)g0 * st.Gs, 0);
     };
     float nsz[4];                           // -s * z of group (chunk + kq), the lane's columns
-    // step 5: digits of the staged chunk into buffer `buf`, its -s*z, the strip's bias
+    // step 5: the staged image into buffer `buf`, its -s*z, the strip's bias
     auto stage_finish = [&](const Stage& st, int buf) {
-        const int items = kCG * M * 16;
         char* const dig = lds + buf * Lay::kBufB;
-        float2* const gs = gst(buf);
 #pragma unroll
-        for (int h = 0; h < H; h++) {
-            const int idx = (int)threadIdx.x + kThreads * h;
-            if (idx < items) {                    // whole 16-lane groups: items is a multiple of 16
-                const int item = idx >> 4, c = idx & 15;
-                const int gg = item / M, m = item - gg * M;
-                float v[8];
-                if (st.xdt == 0) {
-                    const f32x4 lo = __builtin_bit_cast(f32x4, xr[h][0]), hi = __builtin_bit_cast(f32x4, xr[h][1]);
-                    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-                    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-                } else {
-                    const f16x8 hv = __builtin_bit_cast(f16x8, xr[h][0]);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = (float)hv[e];
-                }
-                // piece c covers k 8c .. 8c+7 of the group: 64-k block c / 8, lane group
-                // (c % 8) / 2 of its B operand, 8-byte half c % 2 of the 16-byte row
-                const int row = L == 0 ? (m >> 2) * 16 + 4 * (m & 3) : m;
-                char* const r0 = dig + gg * Lay::kGB + (c >> 3) * Lay::kBbB + ((c & 7) >> 1) * Lay::kKqB +
-                                 row * 16 + (c & 1) * 8;
-                const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8);
-                if (c == 0) gs[gg * 16 + m] = s2;
-            }
+        for (int h = 0; h < Lay::kHI; h++) {
+            const int u = (int)threadIdx.x + kThreads * h;
+            if (u < Lay::kUnits) *reinterpret_cast<u32x4*>(dig + u * 16) = xr[h];
         }
         // -s * z of the lane's columns 4j .. 4j+3 for group (chunk + kq), zero = stored + 1
         const uint32_t zw = zq >> (16 * (j & 1));
@@ -548,11 +572,21 @@ size_t strip_wide_lds(int M)
     return M <= 8 ? (size_t)WideLayout<0>::kLds : (size_t)WideLayout<1>::kLds;
 }
 
+size_t strip_wide_image_bytes(int M)
+{
+    return M <= 8 ? (size_t)WideLayout<0>::kBufB : (size_t)WideLayout<1>::kBufB;
+}
+
 hipError_t launch_strips_wide(const StripArgs& a, size_t lds, hipStream_t stream)
 {
+    if (!a.dimg || a.dimg_count < 1) return hipErrorInvalidValue;
+    void* args[] = {const_cast<StripArgs*>(&a)};
+    const void* dfn = a.M <= 8 ? reinterpret_cast<const void*>(&wide_digits_kernel<0>)
+                               : reinterpret_cast<const void*>(&wide_digits_kernel<1>);
+    hipError_t e = hipLaunchKernel(dfn, dim3(a.dimg_count), dim3(kThreads), args, strip_wide_image_bytes(a.M), stream);
+    if (e != hipSuccess) return e;
     const void* fn = a.M <= 8 ? reinterpret_cast<const void*>(&strip_wide_kernel<0>)
                               : reinterpret_cast<const void*>(&strip_wide_kernel<1>);
-    void* args[] = {const_cast<StripArgs*>(&a)};
     return hipLaunchKernel(fn, dim3(a.G), dim3(kThreads), args, lds, stream);
 }
 
