@@ -75,12 +75,11 @@ def model05(ql, ctx):
 @pytest.mark.gpu
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_headline_step_05b_full_size(ql, ctx, orc, model05, M):
-    """The headline launch: 24 layers x 7 linears, each on its own input, one strip launch (the
-    down projections' strips in K parts)."""
+    """The headline launch: 24 layers x 7 linears, each on its own input, one strip launch."""
     st = bench.SeqStep(ctx, model05, M, chained=False)
     info = st.info
     say(f"0.5B step M={M}: {info.as_dict()}")
-    assert info.linears == 168 and info.passes == 1
+    assert info.linears == 168 and info.passes == 1 and info.reduces == 0
     assert info.kernel == ql.SEQ_STRIPS
     run_as_benched(st)
     check_step(orc, model05, st, lambda N: np.arange(N, dtype=np.int32), f"0.5B M={M}")

@@ -446,7 +446,7 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
 // Device tables of a column-strip sequence: linears, strips, per-workgroup strip ranges, and
 // stored-7 qzeros words for linears without qzeros.
 struct StripLayout {
-    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, partial;
+    uint64_t lin, tasks, task_begin, sym_zeros, sym_words;
     uint64_t dimg, dimg_base, dimg_lin;   // the wide kernel's digit images and their tables
     int32_t dimg_count;
     uint64_t total;
@@ -471,8 +471,6 @@ StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripP
             L.sym_words = std::max<uint64_t>(L.sym_words, (uint64_t)(specs[i].K / specs[i].group) *
                                                               ((specs[i].N + 7) / 8));
     L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
-    // K-split strips' partial sums: [slot][part][M][strip columns]
-    L.partial = take(sizeof(float) * (uint64_t)p.kslots * ql::kStripMaxKParts * M * ql::kStripMaxCols);
     // strip_wide_kernel: one digit image per 512-k chunk of every linear
     L.dimg_count = 0;
     if (p.wide)
@@ -489,9 +487,9 @@ void fill_strip_info(const ql::StripPlan& p, int n, uint64_t scratch, ql_seq_inf
     info->linears = n;
     info->passes = 1;
     info->tiles = p.strips;
-    info->reduces = p.kslots;
+    info->reduces = 0;
     info->grid = p.grid;
-    info->max_split = p.max_parts;
+    info->max_split = 1;
     info->lds_bytes = p.lds_bytes;
     info->device_bytes = scratch;
     info->total_units = p.total_units;
@@ -533,7 +531,6 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
 {
     ql::StripPlan sp;
     ql::plan_strips(specs, M, ql::strip_grid(ctx->cu_count, specs, M), &sp);
-    if (sp.kslots > ql::kCounterCapacity) return fail(QL_E_INVALID, "too many K-split strips (%d)", sp.kslots);
     const StripLayout lay = strip_layout(specs, sp, M);
     char* dev = nullptr;
     QL_HIP(hipMalloc(&dev, lay.total));
@@ -591,8 +588,6 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     q->sargs.split = sp.split;
     q->sargs.stream = sp.stream ? 1 : 0;
     q->sargs.wide = sp.wide ? 1 : 0;
-    q->sargs.partial = reinterpret_cast<float*>(dev + lay.partial);
-    q->sargs.counters = ctx->counters;
     q->sargs.dimg = sp.wide ? dev + lay.dimg : nullptr;
     q->sargs.dimg_base = reinterpret_cast<const int32_t*>(dev + lay.dimg_base);
     q->sargs.dimg_lin = reinterpret_cast<const int32_t*>(dev + lay.dimg_lin);

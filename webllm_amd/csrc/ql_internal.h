@@ -332,9 +332,7 @@ hipError_t launch_seq(const SeqArgs& a, size_t lds, hipStream_t stream);
 // ----------------------------------------------------------------------------------------------
 // Column strips: a sequence of independent linears (no linear reads another's output) as one
 // persistent launch, each workgroup owning strips of 8 whole 64-column blocks (or 4, two waves per
-// block) over all of K, or over a range of K chunks when a whole strip would outweigh a
-// workgroup's share (its K parts then meet in a partial-sum slot: the last part to arrive adds
-// them in part order). Groups of 64 or 128, N % 64 == 0. Measured
+// block) over all of K (no K splits across workgroups). Groups of 64 or 128, N % 64 == 0. Measured
 // against the dependency-ordered tiles: equal on the 0.5B step at M = 1, faster at every M > 1 and
 // on the 7B step (QL_STRIP_MIN_KB_PER_CU can restrict strips to weights streamed from HBM).
 constexpr int kStripMinM = 1;           // fewest rows the strip path serves
@@ -350,13 +348,9 @@ constexpr int kStripChunkGroups = QL_STRIP_CG;   // quantization groups staged p
 constexpr double kStripSplitBalance = 1.06;
 
 struct StripTask {
-    int32_t linear, ct, nblk;  // blocks ct .. ct+nblk-1 of the linear
-    int32_t ch0, chunks;       // its chunks (of kStripChunkGroups groups) ch0 .. ch0+chunks-1
-    int32_t part, parts;       // K part `part` of `parts`; parts > 1: sums go to partial slot `slot`
-    int32_t slot;
+    int32_t linear, ct, nblk;  // blocks ct .. ct+nblk-1 of the linear, over all of K
+    int32_t chunks;            // chunks of kStripChunkGroups groups
 };
-constexpr int kStripMaxKParts = 8;      // most K parts of one strip
-constexpr int kStripMaxCols = 8 * kSeqTileCols;   // columns of the widest strip (8 blocks)
 
 struct StripArgs {
     const SeqLinear* lin;      // y_ll unused
@@ -366,10 +360,6 @@ struct StripArgs {
     int32_t split;             // waves per block: 1 (strips of 8 blocks) or 2 (strips of 4)
     int32_t stream;            // 1: packed weights by streaming (nontemporal) loads
     int32_t wide;              // 1: strip_wide_kernel (no padding, M 5..16, streamed weights)
-    // K-split strips: partial sums [slot][part][M][kStripMaxCols] and one arrival
-    // counter per slot (zero before every launch; the last arrival leaves it at zero)
-    float* partial;
-    uint32_t* counters;
     // strip_wide_kernel: each linear's activation digits, precomputed by wide_digits_kernel (one
     // workgroup per chunk, launched first) as images of the kernel's LDS chunk buffer: linear i's
     // chunk c at dimg + (dimg_base[i] + c) * strip_wide_image_bytes(M); dimg_lin[j] is the linear
@@ -386,7 +376,6 @@ struct StripPlan {
     bool wide = false;         // strip_wide_kernel: streamed, split 1, M 5..16, no padding
     uint64_t lds_bytes = 0;
     uint64_t total_units = 0, busiest_units = 0;   // block-groups: all, most on one workgroup
-    int kslots = 0, max_parts = 1;   // strips split along K, most parts of one
     std::vector<StripTask> tasks;
     std::vector<int32_t> task_begin;
 };

@@ -134,7 +134,7 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
 
     // ---- staging cursor: the chunk being staged (task si, chunk sch) ----
     struct Stage {
-        int si, sch, ch0, chend, ngroups;
+        int si, sch, ngroups;
         const void* x;
         const float* bias;       // the task's bias, or any valid float pointer when it has none
         int K, xdt, ct, nblk, has_bias;
@@ -143,8 +143,7 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
         const StripTask t = ld_table(a.tasks + ti);
         const SeqLinear* L = a.lin + t.linear;
         st.si = ti;
-        st.ch0 = st.sch = t.ch0;
-        st.chend = t.ch0 + t.chunks;
+        st.sch = 0;
         st.x = uni_ptr(ld_table(&L->x));
         const float* b = ld_table(&L->bias);
         st.has_bias = b != nullptr;
@@ -219,7 +218,7 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
                 if (c == 0) gst[gg * M + m] = s2;
             }
         }
-        if (st.sch == st.ch0) {
+        if (st.sch == 0) {
 #pragma unroll
             for (int v = 0; v < BV; v++) {
                 const int bi = (int)threadIdx.x + kThreads * v;
@@ -228,7 +227,7 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
         }
     };
     auto stage_next = [&](Stage& st) {    // false past the last chunk of the last task
-        if (st.sch + 1 < st.chend) {
+        if ((st.sch + 1) * kCG < st.ngroups) {
             st.sch++;
             return true;
         }
@@ -267,10 +266,10 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
         const int N = uni(ld_table(&L->N));
         const int K = uni(ld_table(&L->K));
         c.ngroups = K / GK;
-        c.ch = t.ch0;
-        c.nch = t.ch0 + t.chunks;             // end of the task's chunks
+        c.nch = (c.ngroups + kCG - 1) / kCG;
+        c.ch = 0;
         c.pos = 0;
-        c.g = min(c.ch * kCG + sp, c.ngroups - 1);
+        c.g = min(sp, c.ngroups - 1);
         c.Gq = (uint32_t)(NB * 8) * (uint32_t)N * 4u;
         c.Gs = (uint32_t)N * 2u;
         c.Gz = (((uint32_t)N + 7u) >> 3) * 4u;
@@ -437,15 +436,14 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
     }
     clear();
 
-    __shared__ uint32_t last_part;           // this workgroup brought a K-split strip's last part
     int buf = 0;
     for (int ti = tb; ti < te; ti++) {
         const StripTask t = ld_table(a.tasks + ti);
         const SeqLinear* L = a.lin + t.linear;
         const int groups = ld_table(&L->K) / GK;
         const int nbw = blocks_of(t);
-        const int nch = t.ch0 + t.chunks;    // end of the task's chunks
-        for (int ch = t.ch0; ch < nch; ch++) {
+        const int nch = (groups + kCG - 1) / kCG;
+        for (int ch = 0; ch < nch; ch++) {
             stage_issue(sg);                 // past the last chunk: repeats it (never finished)
             const int cgc = min(kCG, groups - ch * kCG);
             const int njobs = nbw > 0 && cgc > sp ? (cgc - sp + S - 1) / S : 0;
@@ -490,12 +488,10 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
                 }
             }
             if (ch + 1 == nch && nbw > 0 && sp == 0) {
-                // the strip's outputs (bias from LDS: no global load on this path), or a K part's
-                // sums into its partial slot (coherent stores: another workgroup reads them)
+                // the strip's outputs (bias from LDS: no global load on this path)
                 const int N = ld_table(&L->N);
                 float* y = ld_table(&L->y);
                 const float* bl = bias_lds((ti - tb) & 1);
-                float* pp = a.partial + (size_t)(t.slot * kStripMaxKParts + t.part) * M * kStripMaxCols;
 #pragma unroll
                 for (int b = 0; b < BPW; b++) {
                     if (b > 0 && b >= nbw) break;
@@ -505,49 +501,10 @@ __global__ __launch_bounds__(64 * W, (T == 2 && !NT) ? QL_STRIP_OCC2 : 1) void s
 #pragma unroll
                     for (int tt = 0; tt < T; tt++) {
                         const int m = 4 * tt + kq;
-                        if (m < M) {
-                            if (t.parts == 1) {
-                                st_global(reinterpret_cast<f32x4*>(y + (size_t)m * N + col),
-                                          f32x4{acc[b][0][tt] + bvv.x, acc[b][1][tt] + bvv.y,
-                                                acc[b][2][tt] + bvv.z, acc[b][3][tt] + bvv.w});
-                            } else {
-#pragma unroll
-                                for (int u = 0; u < 4; u++)
-                                    __hip_atomic_store(pp + (size_t)m * kStripMaxCols + bc + u, acc[b][u][tt],
-                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            }
-                        }
-                    }
-                }
-            }
-            if (ch + 1 == nch && t.parts > 1) {
-                // arrival: every wave's partial stores are complete before the count; the last
-                // part to arrive adds the parts in part order, with the bias, into y
-                __builtin_amdgcn_s_waitcnt(0);
-                __syncthreads();
-                if (threadIdx.x == 0) {
-                    const uint32_t prev = __hip_atomic_fetch_add(a.counters + t.slot, 1u, __ATOMIC_RELAXED,
-                                                                 __HIP_MEMORY_SCOPE_AGENT);
-                    const uint32_t last = prev == (uint32_t)(t.parts - 1);
-                    if (last) __hip_atomic_store(a.counters + t.slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    last_part = last;
-                }
-                __syncthreads();
-                if (last_part) {
-                    const int N = ld_table(&L->N);
-                    float* y = ld_table(&L->y);
-                    const float* bias = ld_table(&L->bias);
-                    const int cols = t.nblk * kCols;
-                    const float* p0 = a.partial + (size_t)t.slot * kStripMaxKParts * M * kStripMaxCols;
-                    for (int idx = threadIdx.x; idx < M * cols; idx += kThreads) {
-                        const int m = idx / cols, c = idx - m * cols;
-                        const float* pq = p0 + (size_t)m * kStripMaxCols + c;
-                        float sum = __hip_atomic_load(pq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        for (int q = 1; q < t.parts; q++)
-                            sum += __hip_atomic_load(pq + (size_t)q * M * kStripMaxCols, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-                        const int col = t.ct * kCols + c;
-                        y[(size_t)m * N + col] = bias ? sum + bias[col] : sum;
+                        if (m < M)
+                            st_global(reinterpret_cast<f32x4*>(y + (size_t)m * N + col),
+                                      f32x4{acc[b][0][tt] + bvv.x, acc[b][1][tt] + bvv.y, acc[b][2][tt] + bvv.z,
+                                            acc[b][3][tt] + bvv.w});
                     }
                 }
             }
@@ -661,14 +618,7 @@ size_t strip_lds(int M, int group, int split)
 
 namespace {
 
-// kparts: a strip of more block-groups than kStripKPartShare percent of a workgroup's mean share
-// is cut along K into parts of whole chunks (at most kStripMaxKParts), each priced and dealt on
-// its own (QL_STRIP_KPART_SHARE in the environment overrides the percentage, for comparisons)
-#ifndef QL_STRIP_KPART_SHARE
-#define QL_STRIP_KPART_SHARE 125
-#endif
-constexpr int kStripKPartShare = QL_STRIP_KPART_SHARE;
-void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int split, bool kparts, StripPlan* out)
+void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int split, StripPlan* out)
 {
     StripPlan& p = *out;
     p = StripPlan{};
@@ -679,45 +629,17 @@ void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int spl
         StripTask t;
         uint64_t cost;
     };
-    // weight bytes in block-groups, plus a chunk of a full strip for the pipeline's start
-    auto cost_of = [&](int nb, int groups) { return (uint64_t)nb * groups + (uint64_t)kCG * SB; };
-    std::vector<Item> strips;
+    std::vector<Item> items;
     for (int i = 0; i < (int)lin.size(); i++) {
         const int ct = lin[i].N / kCols;
         const int groups = lin[i].K / lin[i].group;
         const int chunks = (groups + kCG - 1) / kCG;
         for (int c = 0; c < ct; c += SB) {
             const int nb = std::min(SB, ct - c);
-            strips.push_back(Item{StripTask{i, c, nb, 0, chunks, 0, 1, 0}, cost_of(nb, groups)});
+            // weight bytes in block-groups, plus a chunk of a full strip for the pipeline's start
+            items.push_back(Item{StripTask{i, c, nb, chunks}, (uint64_t)nb * groups + (uint64_t)kCG * SB});
             p.total_units += (uint64_t)nb * groups;
         }
-    }
-    // a part's block-groups: at most kStripKPartShare percent of a workgroup's mean share
-    const char* env = getenv("QL_STRIP_KPART_SHARE");
-    const uint64_t share = env ? (uint64_t)std::max(1, atoi(env)) : (uint64_t)kStripKPartShare;
-    const uint64_t target = std::max<uint64_t>(1, p.total_units * share / (100 * (uint64_t)grid));
-    std::vector<Item> items;
-    for (const Item& it : strips) {
-        const int groups = lin[it.t.linear].K / lin[it.t.linear].group;
-        const uint64_t units = (uint64_t)it.t.nblk * groups;
-        const int parts = kparts ? (int)std::min<uint64_t>({(uint64_t)kStripMaxKParts, (uint64_t)it.t.chunks,
-                                                            (units + target - 1) / target})
-                                 : 1;
-        if (parts <= 1) {
-            items.push_back(it);
-            continue;
-        }
-        // chunks dealt as evenly as possible, the longer parts first
-        int c0 = 0;
-        for (int q = 0; q < parts; q++) {
-            const int nc = it.t.chunks / parts + (q < it.t.chunks % parts ? 1 : 0);
-            const int g = std::min(groups, (c0 + nc) * kCG) - c0 * kCG;
-            items.push_back(Item{StripTask{it.t.linear, it.t.ct, it.t.nblk, c0, nc, q, parts, p.kslots},
-                                 cost_of(it.t.nblk, g)});
-            c0 += nc;
-        }
-        p.kslots++;
-        p.max_parts = std::max(p.max_parts, parts);
     }
     // longest first onto the least loaded workgroup
     std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
@@ -740,8 +662,7 @@ void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int spl
         q.pop();
         per[s.second].push_back(it.t);
         load[s.second] = s.first + it.cost;
-        const int groups = lin[it.t.linear].K / lin[it.t.linear].group;
-        units[s.second] += (uint64_t)it.t.nblk * (std::min(groups, (it.t.ch0 + it.t.chunks) * kCG) - it.t.ch0 * kCG);
+        units[s.second] += (uint64_t)it.t.nblk * (lin[it.t.linear].K / lin[it.t.linear].group);
         q.push({load[s.second], s.second});
     }
     p.task_begin.assign(grid + 1, 0);
@@ -751,58 +672,55 @@ void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int spl
         p.busiest_units = std::max(p.busiest_units, units[w]);
     }
     p.task_begin[grid] = (int32_t)p.tasks.size();
-    p.strips = (int)strips.size();
+    p.strips = (int)items.size();
     p.lds_bytes = lin.empty() ? 0 : strip_lds(M, lin[0].group, split);
 }
 
 }  // namespace
 
 // Strips of 8 blocks, or of 4 with two waves per block when that balances the workgroups
-// better (a strip of 8 blocks of a long-K linear can outweigh a workgroup's mean share); with
-// kparts, such a strip is cut along K instead.
-static void plan_strips_base(const std::vector<SeqSpec>& lin, int M, int grid, bool kparts, StripPlan* out)
+// better (a strip of 8 blocks of a long-K linear can outweigh a workgroup's mean share).
+static void plan_strips_base(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
 {
     uint64_t bytes = 0;
     for (const SeqSpec& s : lin) bytes += s.weight_bytes;
-    plan_strips_split(lin, M, grid, 1, kparts, out);
+    plan_strips_split(lin, M, grid, 1, out);
     out->stream = bytes > kStripMallBytes;
-    if (out->total_units == 0 || kparts) return;
+    if (out->total_units == 0) return;
     const double mean = (double)out->total_units / grid;
     if (out->busiest_units <= mean * kStripSplitBalance) return;
     StripPlan two;
-    plan_strips_split(lin, M, grid, 2, kparts, &two);
+    plan_strips_split(lin, M, grid, 2, &two);
     two.stream = out->stream;
     if (two.busiest_units < out->busiest_units) *out = two;
 }
 
-// The no-padding kernel where it applies (QL_STRIP_WIDE=0 in the environment keeps strip_kernel,
-// for comparisons), else strip_kernel's plan with K parts. QL_STRIP_KPARTS=0 plans strip_kernel
-// without K parts (whole-K strips), for comparisons.
+// The plan, then the no-padding kernel where it applies (QL_STRIP_WIDE=0 in the environment
+// keeps strip_kernel, for comparisons).
 static void plan_strips_final(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
 {
-    plan_strips_base(lin, M, grid, false, out);
+    plan_strips_base(lin, M, grid, out);
     const char* env = getenv("QL_STRIP_WIDE");
     if ((!env || atoi(env) != 0) && strip_wide_eligible(lin, M, *out)) {
         // the M 5..8 instance runs two workgroups per CU: plan for that many, with strips of 8
         // blocks (the kernel's one block per wave) whatever the balance
         const int per_cu = strip_wide_per_cu(M);
-        StripPlan w = *out;
         if (per_cu > 1 && grid <= kPlanCUs) {
-            plan_strips_split(lin, M, grid * per_cu, 1, false, &w);
-            w.stream = out->stream;
+            StripPlan two;
+            plan_strips_split(lin, M, grid * per_cu, 1, &two);
+            two.stream = out->stream;
+            *out = two;
         }
         // every strip must be 8 whole blocks: the kernel has no path for a shorter one
-        bool whole = w.split == 1;
-        for (const StripTask& t : w.tasks) whole = whole && t.nblk == kMaxStripBlocks;
+        bool whole = out->split == 1;
+        for (const StripTask& t : out->tasks) whole = whole && t.nblk == kMaxStripBlocks;
         if (whole) {
-            *out = w;
             out->wide = true;
             out->lds_bytes = strip_wide_lds(M);
-            return;
+        } else {
+            plan_strips_base(lin, M, grid, out);
         }
     }
-    const char* kp = getenv("QL_STRIP_KPARTS");
-    if (!kp || atoi(kp) != 0) plan_strips_base(lin, M, grid, true, out);
 }
 
 void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
