@@ -642,7 +642,10 @@ def main():
                         "back, so it also carries the gap between launches). The 0.5B weights (186 MB) stay in the "
                         "256 MB MALL across replays, so achieved/frac are HBM+MALL bandwidth over "
                         "the HBM peak; 'flushed' is one step after a read-only pass over 1 GiB has "
-                        "evicted them (HBM-fed, includes launch latency)"}
+                        "evicted them (HBM-fed, includes launch latency). 'traffic' is not measured "
+                        "in this run: it is the calibrated FETCH_SIZE + WRITE_SIZE bytes per launch of "
+                        "this kernel on this step from separate rocprofv3 counter passes, read from "
+                        "profiles/traffic.json"}
         if flushed is not None:
             extra["step05_m1_flushed_us"] = round(flushed * 1e3, 1)
             extra["step05_m1_flushed_gbs"] = round(step1.bytes / (flushed * 1e-3) / 1e9, 1)
