@@ -264,8 +264,9 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
  * share one group size (64, 128 or 256), need N % 4 == 0, and 16-byte aligned qweight, bias, x
  * and y offsets (scales 8-byte).
  * ql_seq_create validates, plans and allocates the sequence's device tables and exchange
- * buffers (the arenas are bound by address and must outlive it). ql_seq_run enqueues one launch
- * on the context stream; it allocates nothing and may be captured into a graph and replayed.
+ * buffers (the arenas are bound by address and must outlive it). ql_seq_run enqueues its launch
+ * (one, except pass-by-pass sequences, below) on the context stream; it allocates nothing and
+ * may be captured into a graph and replayed.
  * Runs of one sequence must not overlap (one stream). ql_seq_status waits for the stream and
  * reports whether a run was aborted (a bounded device-side wait ran out: QL_E_STATE).
  * Prefill (M = 17..65536): a sequence of independent linears (no linear reads another's output)
@@ -275,6 +276,7 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
 #define QL_SEQ_TILES 0
 #define QL_SEQ_STRIPS 1
 #define QL_SEQ_PREFILL 2
+#define QL_SEQ_STRIP_PASSES 3
 typedef struct ql_seq ql_seq;
 typedef struct ql_seq_info {
     int32_t linears;
@@ -288,7 +290,9 @@ typedef struct ql_seq_info {
     uint64_t total_units; /* block-groups (64 columns x one quantization group) of all linears */
     uint64_t busiest_units; /* block-groups of the most loaded workgroup: balance = busiest*grid/total */
     int32_t kernel;       /* QL_SEQ_TILES: dependency-ordered tiles; QL_SEQ_STRIPS: column strips;
-                             QL_SEQ_PREFILL: prefill GEMM tiles (units: 128-k chunks) */
+                             QL_SEQ_PREFILL: prefill GEMM tiles (units: 128-k chunks);
+                             QL_SEQ_STRIP_PASSES: one strip launch per pass (figures summed over
+                             the passes) */
     int32_t split;        /* strips: waves per 64-column block (1: strips of 8 blocks, 2: of 4) */
     int32_t stream;       /* strips: 1 when the packed weights are read with streaming loads (the
                              weights exceed what the 256 MB MALL keeps between steps) */
@@ -315,9 +319,18 @@ int ql_seq_status(ql_ctx* ctx, ql_seq* seq);
  *   res_off     QL_NONE, or the activation-arena offset of an fp32 [M, N] residual added to the
  *               linear's output (y = W.x + bias + res); another linear's output when it equals
  *               that linear's y offset, else external.
- * norm and x2 exclude each other. A fused sequence always runs as dependency-ordered tiles
- * (QL_SEQ_TILES); a linear runs after every producer it reads (x, x2 or res). ql_plan_seq_fused
- * and ql_seq_create_fused with fuse == NULL behave as ql_plan_seq and ql_seq_create. */
+ * norm and x2 exclude each other. A linear runs after every producer it reads (x, x2 or res).
+ * A fused sequence runs as dependency-ordered tiles (QL_SEQ_TILES) in one launch, except as
+ * below. ql_plan_seq_fused and ql_seq_create_fused with fuse == NULL behave as ql_plan_seq and
+ * ql_seq_create.
+ * Chained sequences (fused or not) at M = 5..16 whose weights exceed what the MALL keeps (192 MiB)
+ * and whose linears all have groups of 128, K % 512 == 0, K >= 1024 and N % 512 == 0 run pass by
+ * pass instead (QL_SEQ_STRIP_PASSES): ql_seq_run enqueues, per pass, one launch per distinct
+ * RMSNorm or SiLU-mul input (into buffers of the sequence), the pass's digit-image and
+ * column-strip launches (every strip cut into K parts of whole 512-k chunks, each part's sums
+ * stored apart), and one launch that adds each linear's parts in part order with its bias and
+ * residual; stream order replaces the device-side waits (nothing can abort). QL_SEQ_PASSES=0 in
+ * the environment keeps the tiles. */
 typedef struct ql_seq_fuse {
     uint64_t norm_w_off;
     uint64_t x2_off;

@@ -311,12 +311,14 @@ def model7b_chained(ctx, bench_mod):
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_chained_step_7b_full_size(ql, ctx, orc, bench_mod, model7b_chained, M):
-    """The bench's chained 7B step (28 fused layers, 112 passes, 3.35 GB, one launch) at every M
-    bench times it: every linear on a sample of 64-column blocks; finite to the last layer."""
+    """The bench's chained 7B step (28 fused layers, 112 passes, 3.35 GB) at every M bench times
+    it: one launch of dependency-ordered tiles at M <= 4, pass by pass (norm or SiLU-mul, K-part
+    strips, part sums) at M >= 5; every linear on a sample of 64-column blocks; finite to the last
+    layer."""
     model = model7b_chained
     st = bench_mod.SeqStep(ctx, model, M, chained=True)
     say(f"chained 7B step M={M}: {st.info.as_dict()}")
-    assert st.info.kernel == ql.SEQ_TILES and st.info.passes == 112
+    assert st.info.kernel == (ql.SEQ_STRIP_PASSES if M >= 5 else ql.SEQ_TILES) and st.info.passes == 112
     st.run(2)
     assert st.finite()
     check_step(orc, model, st, _sample, f"chained 7B M={M}")

@@ -136,13 +136,16 @@ def test_balance_7b_independent(M, grid):
     assert info.balance < 1.07
 
 
-def test_strips_for_independent_sequences_only():
+def test_strips_for_independent_sequences_only(monkeypatch):
     """Independent linears run as column strips (nothing reduced, no K split across workgroups):
     the 0.5B step at M = 1 is planned as strips of 4 blocks with two waves per block (8-block
-    strips of the 4864-deep down projection would outweigh a workgroup's share); any chained
-    sequence keeps the dependency-ordered tiles."""
+    strips of the 4864-deep down projection would outweigh a workgroup's share); a chained
+    sequence keeps the dependency-ordered tiles (a streamed one at M >= 2 only with the
+    pass-by-pass form switched off)."""
+    monkeypatch.setenv("QL_SEQ_PASSES", "0")
     info = qwen7b(Chain(M=16), 28, chained=True).plan(grid=256)
-    assert info.passes == 28 * 4 and info.reduces > 0
+    assert info.kernel == ql.SEQ_TILES and info.passes == 28 * 4 and info.reduces > 0
+    monkeypatch.delenv("QL_SEQ_PASSES")
     c = Chain(M=1)
     for _ in range(24):
         for K, N in ((896, 896), (896, 128), (896, 128), (896, 896), (896, 4864), (896, 4864), (4864, 896)):
@@ -151,6 +154,31 @@ def test_strips_for_independent_sequences_only():
     # 4-block strips per layer: q 4, k 1, v 1, o 4, gate 19, up 19, down 4
     assert info.passes == 1 and info.reduces == 0 and info.max_split == 1
     assert info.tiles == 24 * (4 + 1 + 1 + 4 + 19 + 19 + 4)
+
+
+@pytest.mark.parametrize("M", [5, 8, 16])
+def test_chained_streamed_runs_pass_by_pass(M):
+    """A chained sequence of streamed weights (the 7B shape, 3.35 GB) at M = 5..16 runs one strip
+    launch per pass: 112 passes (q; o; gate, up; down per layer), the independent step's 2660
+    strips of 8 blocks, each cut into K parts of whole 512-k chunks that a part-sum launch adds, so
+    nothing is reduced across workgroups inside a launch. At M <= 4, or on weights the MALL keeps (two 0.5B layers), it keeps the
+    dependency-ordered tiles."""
+    info = qwen7b(Chain(M=M), 28, chained=True).plan(grid=256)
+    assert info.kernel == ql.SEQ_STRIP_PASSES and info.passes == 112 and info.linears == 140
+    assert info.tiles == 28 * (7 + 7 + 37 + 37 + 7) and info.reduces == 0 and info.max_split == 1
+    assert info.stream == 1 and info.variant == 1 and info.grid == 256
+    # every 8-block strip of every linear over all of K: 8 blocks x K/128 groups
+    assert info.total_units == 28 * 8 * (7 * 28 + 7 * 28 + 74 * 28 + 7 * 148)
+    for m in (1, 2, 4):
+        assert qwen7b(Chain(M=m), 28, chained=True).plan(grid=256).kernel == ql.SEQ_TILES
+    c = Chain(M=M)
+    h = c.ext(896)
+    for _ in range(2):
+        q = c.add(896, 896, h)
+        o = c.add(896, 896, q)
+        g = c.add(896, 4864, o)
+        h = c.add(4864, 896, g)
+    assert c.plan(grid=256).kernel == ql.SEQ_TILES
 
 
 def test_05b_independent_prices_tiles():

@@ -40,6 +40,21 @@ struct ql_graph {
     hipGraphExec_t exec;
 };
 
+// One launch of a pass-by-pass sequence: an RMSNorm of an input (e), a SiLU-mul (o = silu(g) * u
+// over n values), a pass's strips (s, lds), or the pass's part sums (sums).
+struct SeqStep {
+    enum Kind { kNorm, kGlu, kStrips, kPartSums } kind;
+    const ql::PartSum* sums = nullptr;   // kPartSums: the device table, count entries
+    int count = 0, M = 0, max_n = 0;
+    ql::ElemArgs e{};
+    const float* g = nullptr;
+    const float* u = nullptr;
+    float* o = nullptr;
+    long long n = 0;
+    ql::StripArgs s{};
+    uint64_t lds = 0;
+};
+
 struct ql_seq {
     int device;
     char* dev;              // one allocation: tables, exchange buffers, tickets, abort/error words
@@ -50,6 +65,9 @@ struct ql_seq {
     ql::StripArgs sargs;
     bool prefill;           // independent linears at M > 16: the prefill GEMM (pargs)
     ql::PrefillArgs pargs;
+    bool passes = false;    // chained, streamed weights, M >= 2: one strip launch per pass (steps)
+    std::vector<SeqStep> steps;
+    std::vector<char*> bufs;   // the steps' device allocations (dev holds the input buffers)
 };
 
 // Split-K partial sums of ql_linear_noalloc. One copy per GPU, loaded with the code object, so
@@ -446,7 +464,7 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
 // Device tables of a column-strip sequence: linears, strips, per-workgroup strip ranges, and
 // stored-7 qzeros words for linears without qzeros.
 struct StripLayout {
-    uint64_t lin, tasks, task_begin, sym_zeros, sym_words;
+    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, poff;
     uint64_t dimg, dimg_base, dimg_lin;   // the wide kernel's digit images and their tables
     int32_t dimg_count;
     uint64_t total;
@@ -471,6 +489,7 @@ StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripP
             L.sym_words = std::max<uint64_t>(L.sym_words, (uint64_t)(specs[i].K / specs[i].group) *
                                                               ((specs[i].N + 7) / 8));
     L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
+    L.poff = take(sizeof(int64_t) * std::max(1, n));
     // strip_wide_kernel: one digit image per 512-k chunk of every linear
     L.dimg_count = 0;
     if (p.wide)
@@ -524,33 +543,27 @@ int set_device(ql_ctx* ctx)
     return QL_OK;
 }
 
-// ql_seq_create for independent linears at M >= 2: one workgroup per CU walking its strips.
-int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights, ql_arena* act,
-                 const uint64_t* x_offs, int32_t x_dtype, int32_t M, const uint64_t* y_offs,
-                 const std::vector<ql::SeqSpec>& specs, ql_seq** out)
+// One strip launch's device tables over `lin` (x, y and weight pointers filled in, except the
+// symmetric zeros of linears without qzeros, which point into the new allocation), planned on
+// `grid` workgroups (force_stream as plan_strips). The caller owns *dev.
+struct StripBuild {
+    char* dev = nullptr;
+    ql::StripArgs a{};
+    ql::StripPlan plan;
+    uint64_t lds = 0, bytes = 0;
+};
+
+int strip_build(const std::vector<ql::SeqSpec>& specs, std::vector<ql::SeqLinear> lin, int M, int group,
+                const ql::StripPlan& plan, const std::vector<int64_t>* poff, float* partial, StripBuild* out)
 {
-    ql::StripPlan sp;
-    ql::plan_strips(specs, M, ql::strip_grid(ctx->cu_count, specs, M), &sp);
+    out->plan = plan;
+    const ql::StripPlan& sp = out->plan;
     const StripLayout lay = strip_layout(specs, sp, M);
+    const int n = (int)specs.size();
     char* dev = nullptr;
     QL_HIP(hipMalloc(&dev, lay.total));
-    std::vector<ql::SeqLinear> lin(n);
-    for (int i = 0; i < n; i++) {
-        const ql_gptq_desc* d = &descs[i];
-        ql::SeqLinear& L = lin[i];
-        const ql::GemvLinear g = make_linear(d, weights);
-        L.qweight = g.qweight;
-        L.qzeros = g.qzeros ? g.qzeros : reinterpret_cast<const uint32_t*>(dev + lay.sym_zeros);
-        L.scales = g.scales;
-        L.bias = g.bias;
-        L.x = act->base + x_offs[i];
-        L.y = reinterpret_cast<float*>(act->base + y_offs[i]);
-        L.y_ll = nullptr;
-        L.src = -1;
-        L.N = d->N;
-        L.K = d->K;
-        L.x_dtype = x_dtype;
-    }
+    for (int i = 0; i < n; i++)
+        if (!lin[i].qzeros) lin[i].qzeros = reinterpret_cast<const uint32_t*>(dev + lay.sym_zeros);
     hipError_t e = hipMemset(dev, 0, lay.total);
     if (e == hipSuccess && lay.sym_words)
         e = hipMemsetD32(reinterpret_cast<hipDeviceptr_t>(dev + lay.sym_zeros), 0x77777777, lay.sym_words);
@@ -560,6 +573,8 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     if (e == hipSuccess)
         e = hipMemcpy(dev + lay.task_begin, sp.task_begin.data(), sizeof(int32_t) * sp.task_begin.size(),
                       hipMemcpyHostToDevice);
+    if (e == hipSuccess && poff)
+        e = hipMemcpy(dev + lay.poff, poff->data(), sizeof(int64_t) * n, hipMemcpyHostToDevice);
     if (e == hipSuccess && sp.wide) {
         std::vector<int32_t> base(n), owner;
         for (int i = 0; i < n; i++) {
@@ -574,25 +589,326 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
         (void)hipFree(dev);
         return hip_fail(e, "ql_seq_create upload");
     }
+    ql::StripArgs& a = out->a;
+    a.lin = reinterpret_cast<const ql::SeqLinear*>(dev + lay.lin);
+    a.tasks = reinterpret_cast<const ql::StripTask*>(dev + lay.tasks);
+    a.task_begin = reinterpret_cast<const int32_t*>(dev + lay.task_begin);
+    a.M = M;
+    a.G = sp.grid;
+    a.group = group;
+    a.split = sp.split;
+    a.stream = sp.stream ? 1 : 0;
+    a.wide = sp.wide ? 1 : 0;
+    a.dimg = sp.wide ? dev + lay.dimg : nullptr;
+    a.dimg_base = reinterpret_cast<const int32_t*>(dev + lay.dimg_base);
+    a.dimg_lin = reinterpret_cast<const int32_t*>(dev + lay.dimg_lin);
+    a.dimg_count = lay.dimg_count;
+    a.partial = partial;
+    a.poff = reinterpret_cast<const int64_t*>(dev + lay.poff);
+    out->dev = dev;
+    out->lds = sp.lds_bytes;
+    out->bytes = lay.total;
+    return QL_OK;
+}
+
+// A linear's table entry with its weights bound (qzeros null when it has none).
+ql::SeqLinear seq_linear_of(const ql_gptq_desc* d, const ql_arena* weights, const void* x, int32_t x_dtype, float* y)
+{
+    ql::SeqLinear L{};
+    const ql::GemvLinear g = make_linear(d, weights);
+    L.qweight = g.qweight;
+    L.qzeros = g.qzeros;
+    L.scales = g.scales;
+    L.bias = g.bias;
+    L.x = x;
+    L.y = y;
+    L.y_ll = nullptr;
+    L.src = -1;
+    L.N = d->N;
+    L.K = d->K;
+    L.x_dtype = x_dtype;
+    return L;
+}
+
+// ql_seq_create for independent linears at M >= 2: one workgroup per CU walking its strips.
+int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights, ql_arena* act,
+                 const uint64_t* x_offs, int32_t x_dtype, int32_t M, const uint64_t* y_offs,
+                 const std::vector<ql::SeqSpec>& specs, ql_seq** out)
+{
+    std::vector<ql::SeqLinear> lin(n);
+    for (int i = 0; i < n; i++)
+        lin[i] = seq_linear_of(&descs[i], weights, act->base + x_offs[i], x_dtype,
+                               reinterpret_cast<float*>(act->base + y_offs[i]));
+    ql::StripPlan plan;
+    ql::plan_strips(specs, M, ql::strip_grid(ctx->cu_count, specs, M), &plan);
+    StripBuild b;
+    int rc = strip_build(specs, lin, M, descs[0].group, plan, nullptr, nullptr, &b);
+    if (rc) return rc;
     ql_seq* q = new ql_seq();
     q->device = ctx->device;
-    q->dev = dev;
-    q->lds = sp.lds_bytes;
+    q->dev = b.dev;
+    q->lds = b.lds;
     q->strips = true;
-    q->sargs.lin = reinterpret_cast<const ql::SeqLinear*>(dev + lay.lin);
-    q->sargs.tasks = reinterpret_cast<const ql::StripTask*>(dev + lay.tasks);
-    q->sargs.task_begin = reinterpret_cast<const int32_t*>(dev + lay.task_begin);
-    q->sargs.M = M;
-    q->sargs.G = sp.grid;
-    q->sargs.group = descs[0].group;
-    q->sargs.split = sp.split;
-    q->sargs.stream = sp.stream ? 1 : 0;
-    q->sargs.wide = sp.wide ? 1 : 0;
-    q->sargs.dimg = sp.wide ? dev + lay.dimg : nullptr;
-    q->sargs.dimg_base = reinterpret_cast<const int32_t*>(dev + lay.dimg_base);
-    q->sargs.dimg_lin = reinterpret_cast<const int32_t*>(dev + lay.dimg_lin);
-    q->sargs.dimg_count = lay.dimg_count;
-    fill_strip_info(sp, n, lay.total, &q->info);
+    q->sargs = b.a;
+    fill_strip_info(b.plan, n, b.bytes, &q->info);
+    *out = q;
+    return QL_OK;
+}
+
+// ---- chained sequences of streamed weights at M = 5..16: one strip launch per pass ----
+//
+// The dependency-ordered tiles at M > 1 cut K into short segments (the digits of a tile's whole
+// segment sit in LDS) and reduce them across workgroups. For a model whose weights stream from
+// HBM anyway, each pass (the linears whose producers all ran in earlier passes) runs instead as
+// the no-padding strip launch with every strip cut into K parts of whole 512-k chunks (about one
+// task per workgroup), then one launch that adds each linear's parts in part order with its bias
+// and residual. The fused RMSNorm or SiLU-mul of a pass's inputs runs before it, one launch per
+// distinct input, into a buffer of the sequence. Stream order replaces the device-side waits.
+int seq_pass_of(const std::vector<ql::SeqSpec>& specs, std::vector<int>* pass)
+{
+    const int n = (int)specs.size();
+    pass->assign(n, 0);
+    int depth = 0;
+    for (int i = 0; i < n; i++) {
+        int p = 0;
+        for (int j : {specs[i].src, specs[i].src2, specs[i].res_src})
+            if (j >= 0) p = std::max(p, (*pass)[j] + 1);
+        (*pass)[i] = p;
+        depth = std::max(depth, p + 1);
+    }
+    return depth;
+}
+
+bool passes_ok(const std::vector<ql::SeqSpec>& specs, int M)
+{
+    const char* env = getenv("QL_SEQ_PASSES");
+    if (env && atoi(env) == 0) return false;
+    if (M < 5 || M > ql::kGemvMaxM) return false;
+    uint64_t bytes = 0;
+    bool chained = false;
+    for (const ql::SeqSpec& s : specs) {
+        bytes += s.weight_bytes;
+        chained = chained || s.src >= 0 || s.src2 >= 0 || s.res_src >= 0;
+        // the no-padding strips, at least two K parts per strip
+        if (s.group != 128 || s.K % 512 || s.K < 1024 || s.N % 512) return false;
+    }
+    return chained && bytes > ql::kStripMallBytes;
+}
+
+// The pass-by-pass form's plan: per pass the linears and their strip plan, the distinct
+// transformed inputs and their buffer offsets.
+struct PassInput {
+    bool glu;
+    int x_src, x2_src;           // producers, or -1 (then the offsets below)
+    uint64_t x_off, x2_off, w_off;
+    float eps;
+    int K;
+    uint64_t buf_off;            // in the sequence's input buffers
+};
+struct PassesPlan {
+    std::vector<int> pass;       // per linear
+    int depth = 0;
+    std::vector<PassInput> inputs;
+    std::vector<int> input_of;   // per linear: index into inputs, or -1
+    std::vector<std::vector<int>> members;      // per pass: its linears
+    std::vector<std::vector<ql::SeqSpec>> specs; // per pass: the strip launch's specs
+    std::vector<ql::StripPlan> plans;
+    std::vector<std::vector<int64_t>> poff;      // per pass: partial-sum offsets (floats) per member
+    std::vector<std::vector<int>> parts;         // per pass: K parts per member
+    uint64_t input_bytes = 0, partial_bytes = 0; // the partial buffer serves every pass in turn
+};
+
+void plan_passes(const std::vector<ql::SeqSpec>& specs, const ql_seq_fuse* fuse, const uint64_t* x_offs,
+                 int M, int grid, PassesPlan* P)
+{
+    const int n = (int)specs.size();
+    P->depth = seq_pass_of(specs, &P->pass);
+    P->input_of.assign(n, -1);
+    for (int i = 0; i < n; i++) {
+        const ql::SeqSpec& sp = specs[i];
+        if (!(sp.fuse & (ql::kFuseNorm | ql::kFuseGlu))) continue;
+        PassInput in{};
+        in.glu = (sp.fuse & ql::kFuseGlu) != 0;
+        in.x_src = sp.src;
+        in.x_off = sp.src >= 0 ? 0 : x_offs[i];
+        in.x2_src = in.glu ? sp.src2 : -1;
+        in.x2_off = in.glu && sp.src2 < 0 ? fuse[i].x2_off : 0;
+        in.w_off = in.glu ? 0 : fuse[i].norm_w_off;
+        in.eps = in.glu ? 0.f : fuse[i].norm_eps;
+        in.K = sp.K;
+        int k = -1;
+        for (int q = 0; q < (int)P->inputs.size() && k < 0; q++) {
+            const PassInput& o = P->inputs[q];
+            if (o.glu == in.glu && o.x_src == in.x_src && o.x_off == in.x_off && o.x2_src == in.x2_src &&
+                o.x2_off == in.x2_off && o.w_off == in.w_off && o.eps == in.eps && o.K == in.K)
+                k = q;
+        }
+        if (k < 0) {
+            in.buf_off = P->input_bytes;
+            P->input_bytes += align256((uint64_t)M * in.K * 4);
+            k = (int)P->inputs.size();
+            P->inputs.push_back(in);
+        }
+        P->input_of[i] = k;
+    }
+    P->members.assign(P->depth, {});
+    for (int i = 0; i < n; i++) P->members[P->pass[i]].push_back(i);
+    P->specs.assign(P->depth, {});
+    P->plans.assign(P->depth, ql::StripPlan{});
+    P->poff.assign(P->depth, {});
+    P->parts.assign(P->depth, {});
+    for (int p = 0; p < P->depth; p++) {
+        for (int i : P->members[p]) {
+            ql::SeqSpec s = specs[i];
+            s.src = s.src2 = s.res_src = -1;
+            s.fuse = 0;
+            P->specs[p].push_back(s);
+        }
+        ql::plan_strips_kparts(P->specs[p], M, grid, &P->plans[p]);
+        if (!P->plans[p].wide) {
+            P->depth = 0;  // a shape the K-part strips cannot run: the caller keeps the tiles
+            return;
+        }
+        std::vector<int>& parts = P->parts[p];
+        parts.assign(P->members[p].size(), 1);
+        for (const ql::StripTask& t : P->plans[p].tasks) parts[t.linear] = std::max(parts[t.linear], t.parts);
+        int64_t off = 0;
+        for (size_t k = 0; k < parts.size(); k++) {
+            P->poff[p].push_back(off);
+            off += (int64_t)parts[k] * M * P->specs[p][k].N;
+            off = (off + 63) & ~(int64_t)63;
+        }
+        P->partial_bytes = std::max<uint64_t>(P->partial_bytes, (uint64_t)off * 4);
+    }
+}
+
+void fill_passes_info(const PassesPlan& P, int n, uint64_t bytes, int grid, ql_seq_info* info)
+{
+    *info = ql_seq_info{};
+    info->linears = n;
+    info->passes = P.depth;
+    info->grid = grid;
+    for (const ql::StripPlan& sp : P.plans) info->grid = std::max(info->grid, sp.grid);
+    info->max_split = 1;
+    info->device_bytes = bytes;
+    info->kernel = QL_SEQ_STRIP_PASSES;
+    info->split = 1;
+    info->stream = 1;
+    for (const ql::StripPlan& sp : P.plans) {
+        info->tiles += sp.strips;
+        info->lds_bytes = std::max<uint64_t>(info->lds_bytes, sp.lds_bytes);
+        info->total_units += sp.total_units;
+        info->busiest_units += sp.busiest_units;
+        info->split = std::max(info->split, sp.split);
+        info->variant = info->variant || sp.wide ? 1 : 0;
+    }
+}
+
+int passes_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights, ql_arena* act,
+                  const uint64_t* x_offs, int32_t x_dtype, int32_t M, const uint64_t* y_offs,
+                  const ql_seq_fuse* fuse, const std::vector<ql::SeqSpec>& specs, ql_seq** out)
+{
+    PassesPlan P;
+    const int grid = ctx->cu_count;
+    plan_passes(specs, fuse, x_offs, M, grid, &P);
+    if (P.depth < 1) return fail(QL_E_INVALID, "sequence shapes do not fit the K-part strips");
+    ql_seq* q = new ql_seq();
+    q->device = ctx->device;
+    q->passes = true;
+    auto cleanup = [&](int rc) {
+        for (char* b : q->bufs) (void)hipFree(b);
+        (void)hipFree(q->dev);
+        delete q;
+        return rc;
+    };
+    {
+        hipError_t e = hipMalloc(&q->dev, P.input_bytes + P.partial_bytes);
+        if (e != hipSuccess) return cleanup(hip_fail(e, "ql_seq_create input and partial-sum buffers"));
+    }
+    float* const partial = reinterpret_cast<float*>(q->dev + P.input_bytes);
+    auto y_ptr = [&](int j) { return reinterpret_cast<float*>(act->base + y_offs[j]); };
+    auto ext_ptr = [&](int src, uint64_t off) -> const float* {
+        return src >= 0 ? y_ptr(src) : reinterpret_cast<const float*>(act->base + off);
+    };
+    std::vector<bool> made(P.inputs.size(), false);
+    uint64_t bytes = P.input_bytes + P.partial_bytes;
+    for (int p = 0; p < P.depth; p++) {
+        // the pass's transformed inputs
+        for (int i : P.members[p]) {
+            const int k = P.input_of[i];
+            if (k < 0 || made[k]) continue;
+            made[k] = true;
+            const PassInput& in = P.inputs[k];
+            SeqStep st{};
+            float* buf = reinterpret_cast<float*>(q->dev + in.buf_off);
+            if (in.glu) {
+                st.kind = SeqStep::kGlu;
+                st.g = ext_ptr(in.x_src, in.x_off);
+                st.u = ext_ptr(in.x2_src, in.x2_off);
+                st.o = buf;
+                st.n = (long long)M * in.K;
+            } else {
+                st.kind = SeqStep::kNorm;
+                st.e.x = ext_ptr(in.x_src, in.x_off);
+                st.e.d = nullptr;
+                st.e.w = reinterpret_cast<const float*>(weights->base + in.w_off);
+                st.e.s = nullptr;
+                st.e.y = buf;
+                st.e.M = M;
+                st.e.C = in.K;
+                st.e.eps = in.eps;
+                st.e.vec = in.K % 4 == 0 && reinterpret_cast<uintptr_t>(st.e.x) % 16 == 0 && in.w_off % 16 == 0;
+            }
+            q->steps.push_back(st);
+        }
+        // the pass's strips, then its part sums (bias and residual)
+        std::vector<ql::SeqLinear> lin;
+        for (int i : P.members[p]) {
+            const int k = P.input_of[i];
+            const void* x = k >= 0 ? static_cast<const void*>(q->dev + P.inputs[k].buf_off)
+                                   : static_cast<const void*>(ext_ptr(specs[i].src, x_offs[i]));
+            const int32_t xd = k >= 0 || specs[i].src >= 0 ? QL_DTYPE_F32 : x_dtype;
+            lin.push_back(seq_linear_of(&descs[i], weights, x, xd, y_ptr(i)));
+        }
+        StripBuild b;
+        int rc = strip_build(P.specs[p], lin, M, descs[0].group, P.plans[p], &P.poff[p], partial, &b);
+        if (rc) return cleanup(rc);
+        q->bufs.push_back(b.dev);
+        bytes += b.bytes;
+        SeqStep st{};
+        st.kind = SeqStep::kStrips;
+        st.s = b.a;
+        st.lds = b.lds;
+        q->steps.push_back(st);
+        std::vector<ql::PartSum> sums;
+        int max_n = 0;
+        for (size_t k = 0; k < P.members[p].size(); k++) {
+            const int i = P.members[p][k];
+            ql::PartSum e{};
+            e.part0 = partial + P.poff[p][k];
+            e.bias = lin[k].bias;
+            e.res = specs[i].fuse & ql::kFuseRes ? ext_ptr(specs[i].res_src, fuse[i].res_off) : nullptr;
+            e.y = y_ptr(i);
+            e.parts = P.parts[p][k];
+            e.N = descs[i].N;
+            max_n = std::max(max_n, e.N);
+            sums.push_back(e);
+        }
+        char* tab = nullptr;
+        hipError_t e = hipMalloc(&tab, sizeof(ql::PartSum) * sums.size());
+        if (e == hipSuccess) q->bufs.push_back(tab);
+        if (e == hipSuccess) e = hipMemcpy(tab, sums.data(), sizeof(ql::PartSum) * sums.size(), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return cleanup(hip_fail(e, "ql_seq_create part sums"));
+        bytes += sizeof(ql::PartSum) * sums.size();
+        SeqStep ps{};
+        ps.kind = SeqStep::kPartSums;
+        ps.sums = reinterpret_cast<const ql::PartSum*>(tab);
+        ps.count = (int)sums.size();
+        ps.M = M;
+        ps.max_n = max_n;
+        q->steps.push_back(ps);
+    }
+    fill_passes_info(P, n, bytes, grid, &q->info);
     *out = q;
     return QL_OK;
 }
@@ -1513,6 +1829,16 @@ int plan_seq_impl(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_
         fill_strip_info(sp, n, strip_layout(specs, sp, M).total, info);
         return QL_OK;
     }
+    if (passes_ok(specs, M)) {
+        PassesPlan P;
+        plan_passes(specs, fuse, x_offs, M, grid, &P);
+        if (P.depth < 1) return fail(QL_E_INVALID, "sequence shapes do not fit the K-part strips");
+        uint64_t bytes = P.input_bytes + P.partial_bytes;
+        for (int p = 0; p < P.depth; p++)
+            bytes += strip_layout(P.specs[p], P.plans[p], M).total + sizeof(ql::PartSum) * P.members[p].size();
+        fill_passes_info(P, n, bytes, grid, info);
+        return QL_OK;
+    }
     ql::SeqPlanOut p;
     ql::plan_seq(specs, M, grid, &p);
     const std::string bad = ql::verify_seq_plan(specs, M, p);
@@ -1555,6 +1881,8 @@ int seq_create_impl(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_
     if (M > ql::kGemvMaxM) return prefill_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, specs, out);
     if (!fused && ql::strip_eligible(specs, M))
         return strip_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, specs, out);
+    if (passes_ok(specs, M))
+        return passes_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, fuse, specs, out);
     int per_cu = 0;
     QL_HIP(ql::seq_blocks_per_cu(M, descs[0].group, fused, &per_cu));
     if (per_cu < 1) return fail(QL_E_INVALID, "sequence kernel does not fit on a CU");
@@ -1675,7 +2003,16 @@ int ql_seq_run(ql_ctx* ctx, ql_seq* seq)
     if (seq->device != ctx->device) return fail(QL_E_INVALID, "sequence belongs to another device");
     int rc = set_device(ctx);
     if (rc) return rc;
-    if (seq->prefill) QL_HIP(ql::launch_prefill(seq->pargs, true, ctx->stream));
+    if (seq->passes) {
+        for (const SeqStep& st : seq->steps) {
+            switch (st.kind) {
+            case SeqStep::kNorm: QL_HIP(ql::launch_add_rmsnorm(st.e, ctx->stream)); break;
+            case SeqStep::kGlu: QL_HIP(ql::launch_silu_mul(st.g, st.u, st.o, st.n, ctx->stream)); break;
+            case SeqStep::kStrips: QL_HIP(ql::launch_strips(st.s, st.lds, ctx->stream)); break;
+            case SeqStep::kPartSums: QL_HIP(ql::launch_part_sums(st.sums, st.count, st.M, st.max_n, ctx->stream)); break;
+            }
+        }
+    } else if (seq->prefill) QL_HIP(ql::launch_prefill(seq->pargs, true, ctx->stream));
     else if (seq->strips) QL_HIP(ql::launch_strips(seq->sargs, seq->lds, ctx->stream));
     else QL_HIP(ql::launch_seq(seq->args, seq->lds, ctx->stream));
     return QL_OK;
@@ -1688,7 +2025,7 @@ int ql_seq_status(ql_ctx* ctx, ql_seq* seq)
     int rc = set_device(ctx);
     if (rc) return rc;
     QL_HIP(hipStreamSynchronize(ctx->stream));
-    if (seq->strips || seq->prefill) return QL_OK;   // no device-side waits: nothing can abort
+    if (seq->strips || seq->prefill || seq->passes) return QL_OK;   // no device-side waits: nothing can abort
     uint32_t words[2] = {0, 0};
     QL_HIP(hipMemcpy(words, seq->args.abort, sizeof words, hipMemcpyDeviceToHost));
     if (words[0] == 0 && words[1] == 0) return QL_OK;
@@ -1709,6 +2046,7 @@ int ql_seq_destroy(ql_seq* seq)
 {
     if (!seq) return fail(QL_E_INVALID, "null sequence");
     (void)hipSetDevice(seq->device);
+    for (char* b : seq->bufs) (void)hipFree(b);
     (void)hipFree(seq->dev);
     delete seq;
     return QL_OK;

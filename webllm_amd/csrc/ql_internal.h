@@ -348,8 +348,11 @@ constexpr int kStripChunkGroups = QL_STRIP_CG;   // quantization groups staged p
 constexpr double kStripSplitBalance = 1.06;
 
 struct StripTask {
-    int32_t linear, ct, nblk;  // blocks ct .. ct+nblk-1 of the linear, over all of K
-    int32_t chunks;            // chunks of kStripChunkGroups groups
+    int32_t linear, ct, nblk;  // blocks ct .. ct+nblk-1 of the linear
+    int32_t chunks;            // chunks of kStripChunkGroups groups: all of K (ch0 = 0), or
+    int32_t ch0;               // (strip_wide_kernel only) chunks ch0 .. ch0+chunks-1 of
+    int32_t part, parts;       // K part `part` of `parts` > 1, whose sums (no bias) go to
+                               // partial + poff[linear] + part * M * N, row stride N
 };
 
 struct StripArgs {
@@ -368,7 +371,21 @@ struct StripArgs {
     const int32_t* dimg_base;
     const int32_t* dimg_lin;
     int32_t dimg_count;
+    // K parts (tasks with parts > 1): partial sums [part][M][N] of linear i at partial + poff[i]
+    float* partial;
+    const int64_t* poff;
 };
+
+// Sums the K parts of strip tasks in part order, with bias and an optional residual, into y:
+// one entry per linear, y[m][n] = sum_p part_p[m][n] + bias[n] + res[m][n].
+struct PartSum {
+    const float* part0;        // parts x [M][N], part p at part0 + p * M * N
+    const float* bias;         // [N] or null
+    const float* res;          // [M][N] or null
+    float* y;                  // [M][N]
+    int32_t parts, N;
+};
+hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, hipStream_t stream);
 
 struct StripPlan {
     int grid = 0, strips = 0, split = 1;
@@ -384,7 +401,13 @@ bool strip_eligible(const std::vector<SeqSpec>& lin, int M);
 int strip_grid(int cu_count, const std::vector<SeqSpec>& lin, int M);   // workgroups of a strip launch
 constexpr uint64_t kStripMallBytes = 192ull << 20;   // weights that stay resident in the MALL
 size_t strip_lds(int M, int group, int split);
-void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out);
+// force_stream 1: plan as streamed from HBM whatever the launch's own bytes (a pass of a model
+// whose weights do not stay in the MALL); -1: by the launch's bytes
+void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out, int force_stream = -1);
+// The wide strips with every strip cut into K parts, for one pass of a pass-by-pass sequence:
+// strips of 8 blocks, each cut into about grid / strips parts of whole 512-k chunks, dealt
+// longest first. Empty when the linears are not wide-eligible at M.
+void plan_strips_kparts(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out);
 hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream);
 // The strip launch without padding (ql_strip_wide.hip): every linear group 128, K a multiple of
 // 4 groups, N a multiple of 512, weights streamed, strips of 8 blocks, M 5..16.

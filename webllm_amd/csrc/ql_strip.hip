@@ -618,7 +618,9 @@ size_t strip_lds(int M, int group, int split)
 
 namespace {
 
-void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int split, StripPlan* out)
+// force_stream: 1 plans the launch as streamed from HBM whatever its own bytes (one pass of a
+// model whose weights do not stay in the MALL), -1 decides by the launch's bytes
+void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int split, int force_stream, StripPlan* out)
 {
     StripPlan& p = *out;
     p = StripPlan{};
@@ -652,7 +654,8 @@ void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int spl
     // rule: weights the MALL keeps, M <= QL_STRIP_MALL2_MAX_M) the second ones are grid/2 and up.
     uint64_t bytes = 0;
     for (const SeqSpec& s : lin) bytes += s.weight_bytes;
-    const int second = bytes <= kStripMallBytes && M <= QL_STRIP_MALL2_MAX_M ? grid / 2 : grid;
+    const bool mall = force_stream >= 0 ? force_stream == 0 : bytes <= kStripMallBytes;
+    const int second = mall && M <= QL_STRIP_MALL2_MAX_M ? grid / 2 : grid;
     for (int w = 0; w < grid; w++) {
         load[w] = w >= second ? (uint64_t)QL_STRIP_SECOND_OFFSET : 0;
         q.push({load[w], w});
@@ -680,26 +683,26 @@ void plan_strips_split(const std::vector<SeqSpec>& lin, int M, int grid, int spl
 
 // Strips of 8 blocks, or of 4 with two waves per block when that balances the workgroups
 // better (a strip of 8 blocks of a long-K linear can outweigh a workgroup's mean share).
-static void plan_strips_base(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+static void plan_strips_base(const std::vector<SeqSpec>& lin, int M, int grid, int force_stream, StripPlan* out)
 {
     uint64_t bytes = 0;
     for (const SeqSpec& s : lin) bytes += s.weight_bytes;
-    plan_strips_split(lin, M, grid, 1, out);
-    out->stream = bytes > kStripMallBytes;
+    plan_strips_split(lin, M, grid, 1, force_stream, out);
+    out->stream = force_stream >= 0 ? force_stream != 0 : bytes > kStripMallBytes;
     if (out->total_units == 0) return;
     const double mean = (double)out->total_units / grid;
     if (out->busiest_units <= mean * kStripSplitBalance) return;
     StripPlan two;
-    plan_strips_split(lin, M, grid, 2, &two);
+    plan_strips_split(lin, M, grid, 2, force_stream, &two);
     two.stream = out->stream;
     if (two.busiest_units < out->busiest_units) *out = two;
 }
 
 // The plan, then the no-padding kernel where it applies (QL_STRIP_WIDE=0 in the environment
 // keeps strip_kernel, for comparisons).
-static void plan_strips_final(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+static void plan_strips_final(const std::vector<SeqSpec>& lin, int M, int grid, int force_stream, StripPlan* out)
 {
-    plan_strips_base(lin, M, grid, out);
+    plan_strips_base(lin, M, grid, force_stream, out);
     const char* env = getenv("QL_STRIP_WIDE");
     if ((!env || atoi(env) != 0) && strip_wide_eligible(lin, M, *out)) {
         // the M 5..8 instance runs two workgroups per CU: plan for that many, with strips of 8
@@ -707,7 +710,7 @@ static void plan_strips_final(const std::vector<SeqSpec>& lin, int M, int grid, 
         const int per_cu = strip_wide_per_cu(M);
         if (per_cu > 1 && grid <= kPlanCUs) {
             StripPlan two;
-            plan_strips_split(lin, M, grid * per_cu, 1, &two);
+            plan_strips_split(lin, M, grid * per_cu, 1, force_stream, &two);
             two.stream = out->stream;
             *out = two;
         }
@@ -718,14 +721,73 @@ static void plan_strips_final(const std::vector<SeqSpec>& lin, int M, int grid, 
             out->wide = true;
             out->lds_bytes = strip_wide_lds(M);
         } else {
-            plan_strips_base(lin, M, grid, out);
+            plan_strips_base(lin, M, grid, force_stream, out);
         }
     }
 }
 
-void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out, int force_stream)
 {
-    plan_strips_final(lin, M, grid, out);
+    plan_strips_final(lin, M, grid, force_stream, out);
+}
+
+void plan_strips_kparts(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out)
+{
+    StripPlan& p = *out;
+    p = StripPlan{};
+    p.split = 1;
+    p.stream = true;
+    if (!strip_wide_eligible(lin, M, p)) return;
+    // the M 5..8 instance runs two workgroups per CU
+    if (grid <= kPlanCUs) grid *= strip_wide_per_cu(M);
+    p.grid = grid;
+    int nstrips = 0;
+    for (const SeqSpec& s : lin) nstrips += s.N / (kMaxStripBlocks * kCols);
+    // at least two parts (every output goes through the part sums), about one task per workgroup
+    const int target = std::max(2, (grid + nstrips - 1) / std::max(1, nstrips));
+    struct Item {
+        StripTask t;
+        uint64_t cost;
+    };
+    std::vector<Item> items;
+    for (int i = 0; i < (int)lin.size(); i++) {
+        const int groups = lin[i].K / lin[i].group;
+        const int chunks = groups / kCG;
+        const int parts = std::min(chunks, target);
+        for (int c = 0; c < lin[i].N / kCols; c += kMaxStripBlocks) {
+            int c0 = 0;
+            for (int q = 0; q < parts; q++) {
+                const int nc = chunks / parts + (q < chunks % parts ? 1 : 0);
+                items.push_back(Item{StripTask{i, c, kMaxStripBlocks, nc, c0, q, parts},
+                                     (uint64_t)kMaxStripBlocks * nc * kCG + (uint64_t)kCG * kMaxStripBlocks});
+                c0 += nc;
+            }
+            p.total_units += (uint64_t)kMaxStripBlocks * groups;
+        }
+    }
+    std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
+    std::vector<std::vector<StripTask>> per(grid);
+    std::vector<uint64_t> units(grid, 0);
+    typedef std::pair<uint64_t, int> Slot;
+    std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>> q;
+    for (int w = 0; w < grid; w++) q.push({0, w});
+    for (const Item& it : items) {
+        const Slot s = q.top();
+        q.pop();
+        per[s.second].push_back(it.t);
+        units[s.second] += (uint64_t)it.t.nblk * it.t.chunks * kCG;
+        q.push({s.first + it.cost, s.second});
+    }
+    p.task_begin.assign(grid + 1, 0);
+    for (int w = 0; w < grid; w++) {
+        p.task_begin[w] = (int32_t)p.tasks.size();
+        p.tasks.insert(p.tasks.end(), per[w].begin(), per[w].end());
+        p.busiest_units = std::max(p.busiest_units, units[w]);
+    }
+    p.task_begin[grid] = (int32_t)p.tasks.size();
+    p.strips = nstrips;
+    p.wide = true;
+    p.lds_bytes = strip_wide_lds(M);
 }
 
 hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream)

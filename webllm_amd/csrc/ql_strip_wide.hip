@@ -229,7 +229,6 @@ template <int L>
 __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wide_kernel(const StripArgs a)
 {
     using Lay = WideLayout<L>;
-    constexpr int H = Lay::kH;
     constexpr int KT = Lay::kTiles;
     extern __shared__ uint4 dyn_lds[];
     char* const lds = reinterpret_cast<char*>(dyn_lds);
@@ -251,7 +250,7 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
 
     // ---- staging: the chunk being staged (task si, chunk sch): its digit image into LDS ----
     struct Stage {
-        int si, sch, ngroups, ct, has_bias;
+        int si, sch, ch0, chend, ngroups, ct, has_bias;
         __amdgpu_buffer_rsrc_t ri, rb, rz, rs;   // the linear's digit images, bias (x without one), the wave block's zeros, scales
         uint32_t Gz, Gs;
     };
@@ -259,7 +258,8 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         const StripTask t = tab(a.tasks + ti);
         const SeqLinear* Lp = a.lin + t.linear;
         st.si = ti;
-        st.sch = 0;
+        st.sch = st.ch0 = t.ch0;
+        st.chend = t.ch0 + t.chunks;
         const float* b = tab(&Lp->bias);
         st.has_bias = b != nullptr;
         st.ri = rsrc(a.dimg + (size_t)tab(a.dimg_base + t.linear) * Lay::kBufB);
@@ -307,10 +307,10 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
             const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
             nsz[u] = -s * (float)(((zw >> (4 * u)) & 15u) + 1u);
         }
-        if (st.sch == 0) bias_lds((st.si - tb) & 1)[threadIdx.x] = st.has_bias ? bv : 0.f;
+        if (st.sch == st.ch0) bias_lds((st.si - tb) & 1)[threadIdx.x] = st.has_bias ? bv : 0.f;
     };
     auto stage_next = [&](Stage& st) {    // false past the last chunk of the last task
-        if ((st.sch + 1) * kCG < st.ngroups) {
+        if (st.sch + 1 < st.chend) {
             st.sch++;
             return true;
         }
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     uint4 wb[kP][2 * kNB];
     uint2 sb[kP];
     struct Cur {
-        int ti, g, ngroups;
+        int ti, g, gend;            // the task's groups end at gend
         __amdgpu_buffer_rsrc_t rq, rs;   // the wave block's packed weights and scales
         uint32_t Gq, Gs;
         uint32_t lq[2 * kNB];       // the lane's packed rows 2kq, 2kq+1, 2kq+8, 2kq+9 of a group
@@ -333,9 +333,9 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         const StripTask t = tab(a.tasks + ti);
         const SeqLinear* Lp = a.lin + t.linear;
         c.ti = ti;
-        c.g = 0;
+        c.g = t.ch0 * kCG;
         const int N = sreg(tab(&Lp->N));
-        c.ngroups = sreg(tab(&Lp->K)) / 128;
+        c.gend = (t.ch0 + t.chunks) * kCG;
         const uint32_t blk = (uint32_t)(t.ct + wave);
         c.rq = rsrc(reinterpret_cast<const char*>(sptr(tab(&Lp->qweight))) + blk * (uint32_t)kCols * 4u);
         c.rs = rsrc(reinterpret_cast<const char*>(sptr(tab(&Lp->scales))) + blk * (uint32_t)kCols * 2u);
@@ -346,7 +346,7 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
             c.lq[r] = ((uint32_t)(2 * kq + (r >> 1) * 8 + (r & 1)) * (uint32_t)N + 4u * (uint32_t)j) * 4u;
     };
     auto advance = [&](Cur& c) {
-        if (c.g + 1 < c.ngroups) c.g++;
+        if (c.g + 1 < c.gend) c.g++;
         else if (c.ti + 1 < te) open(c, c.ti + 1);
         // else: the stream has ended; stay on the last job (its reloads are never consumed)
     };
@@ -496,8 +496,8 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     for (int ti = tb; ti < te; ti++) {
         const StripTask t = tab(a.tasks + ti);
         const SeqLinear* Lp = a.lin + t.linear;
-        const int nch = tab(&Lp->K) / (128 * kCG);
-        for (int ch = 0; ch < nch; ch++) {
+        const int nch = t.ch0 + t.chunks;   // end of the task's chunks
+        for (int ch = t.ch0; ch < nch; ch++) {
             stage_issue(sg);                 // past the last chunk: repeats it (never finished)
 #pragma unroll
             for (int gg = 0; gg < kCG; gg++) {
@@ -507,10 +507,13 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
             }
             zero_term(buf);
             if (ch + 1 == nch) {
+                // a whole task's outputs with the bias, or a K part's sums into its partial block
+                const bool whole = t.parts <= 1;
                 const int N = tab(&Lp->N);
-                float* y = tab(&Lp->y);
+                float* const y = whole ? tab(&Lp->y) : a.partial + tab(a.poff + t.linear) + (size_t)t.part * M * N;
                 const int col = (t.ct + wave) * kCols + 4 * j;
-                const f32x4 bvv = *reinterpret_cast<const f32x4*>(bias_lds((ti - tb) & 1) + wave * kCols + 4 * j);
+                const f32x4 bvv = whole ? *reinterpret_cast<const f32x4*>(bias_lds((ti - tb) & 1) + wave * kCols + 4 * j)
+                                        : f32x4{0.f, 0.f, 0.f, 0.f};
                 if constexpr (L == 1) {
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
@@ -552,7 +555,33 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     }
 }
 
+// The K parts of every split linear of a pass, added in part order with bias and residual:
+// blockIdx.y is the entry, 4 consecutive outputs per lane (N % 4 == 0).
+__global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, int M)
+{
+    const PartSum e = entries[blockIdx.y];
+    const int n4 = e.N / 4;
+    const int i = blockIdx.x * 256 + threadIdx.x;          // 4-value group over [M][N]
+    if (i >= M * n4) return;
+    const int m = i / n4, c = (i - m * n4) * 4;
+    const size_t stride = (size_t)M * e.N;
+    const float* p = e.part0 + (size_t)m * e.N + c;
+    f32x4 v = ld_global(reinterpret_cast<const f32x4*>(p));
+    for (int q = 1; q < e.parts; q++) v += ld_global(reinterpret_cast<const f32x4*>(p + (size_t)q * stride));
+    if (e.bias) v += ld_global(reinterpret_cast<const f32x4*>(e.bias + c));
+    if (e.res) v += ld_global(reinterpret_cast<const f32x4*>(e.res + (size_t)m * e.N + c));
+    st_global(reinterpret_cast<f32x4*>(e.y + (size_t)m * e.N + c), v);
+}
+
 }  // namespace
+
+hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, hipStream_t stream)
+{
+    if (count < 1) return hipSuccess;
+    const int groups = M * (max_n / 4);
+    hipLaunchKernelGGL(part_sum_kernel, dim3((groups + 255) / 256, count), dim3(256), 0, stream, entries_dev, M);
+    return hipGetLastError();
+}
 
 bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan& p)
 {
