@@ -599,6 +599,7 @@ int strip_build(const std::vector<ql::SeqSpec>& specs, std::vector<ql::SeqLinear
     a.split = sp.split;
     a.stream = sp.stream ? 1 : 0;
     a.wide = sp.wide ? 1 : 0;
+    a.ring = sp.ring;
     a.dimg = sp.wide ? dev + lay.dimg : nullptr;
     a.dimg_base = reinterpret_cast<const int32_t*>(dev + lay.dimg_base);
     a.dimg_lin = reinterpret_cast<const int32_t*>(dev + lay.dimg_lin);

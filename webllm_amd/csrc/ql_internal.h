@@ -363,6 +363,7 @@ struct StripArgs {
     int32_t split;             // waves per block: 1 (strips of 8 blocks) or 2 (strips of 4)
     int32_t stream;            // 1: packed weights by streaming (nontemporal) loads
     int32_t wide;              // 1: strip_wide_kernel (no padding, M 5..16, streamed weights)
+    int32_t ring;              // strip_wide_kernel: jobs in flight per wave, 2 or 4
     // strip_wide_kernel: each linear's activation digits, precomputed by wide_digits_kernel (one
     // workgroup per chunk, launched first) as images of the kernel's LDS chunk buffer: linear i's
     // chunk c at dimg + (dimg_base[i] + c) * strip_wide_image_bytes(M); dimg_lin[j] is the linear
@@ -391,6 +392,7 @@ struct StripPlan {
     int grid = 0, strips = 0, split = 1;
     bool stream = false;       // the weights exceed what the MALL keeps between steps
     bool wide = false;         // strip_wide_kernel: streamed, split 1, M 5..16, no padding
+    int ring = 2;              // strip_wide_kernel's jobs in flight per wave (4: K-part tasks)
     uint64_t lds_bytes = 0;
     uint64_t total_units = 0, busiest_units = 0;   // block-groups: all, most on one workgroup
     std::vector<StripTask> tasks;

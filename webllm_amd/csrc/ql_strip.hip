@@ -787,6 +787,7 @@ void plan_strips_kparts(const std::vector<SeqSpec>& lin, int M, int grid, StripP
     p.task_begin[grid] = (int32_t)p.tasks.size();
     p.strips = nstrips;
     p.wide = true;
+    p.ring = 4;
     p.lds_bytes = strip_wide_lds(M);
 }
 

@@ -43,13 +43,9 @@ constexpr int kThreads = 64 * kW;
 #ifndef QL_WIDE_QREGION
 #define QL_WIDE_QREGION 1
 #endif
-#ifndef QL_WIDE_P
-#define QL_WIDE_P 2
-#endif
-constexpr int kP = QL_WIDE_P;            // jobs in flight per wave
 constexpr int kNB = 2;                   // 64-k blocks per 128-k group
 constexpr int kBlocks = 8;               // blocks per strip
-static_assert(kCG == 4 && kCG % kP == 0, "chunks of 4 groups, whole ring rounds");
+static_assert(kCG == 4, "chunks of 4 groups");
 
 template <typename T>
 __device__ __forceinline__ T tab(const T* p)
@@ -225,9 +221,12 @@ __global__ __launch_bounds__(kThreads) void wide_digits_kernel(const StripArgs a
 #ifndef QL_WIDE_OCC0
 #define QL_WIDE_OCC0 2
 #endif
-template <int L>
+// P: jobs in flight per wave (the register ring's depth): 2 for long strips over all of K, 4 (a
+// chunk's every job) for the short K-part tasks, whose time is mostly round trips to HBM.
+template <int L, int P>
 __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wide_kernel(const StripArgs a)
 {
+    static_assert(kCG % P == 0, "whole ring rounds per chunk");
     using Lay = WideLayout<L>;
     constexpr int KT = Lay::kTiles;
     extern __shared__ uint4 dyn_lds[];
@@ -320,8 +319,8 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     };
 
     // ---- job stream: one job per group of each strip (the wave's block) ----
-    uint4 wb[kP][2 * kNB];
-    uint2 sb[kP];
+    uint4 wb[P][2 * kNB];
+    uint2 sb[P];
     struct Cur {
         int ti, g, gend;            // the task's groups end at gend
         __amdgpu_buffer_rsrc_t rq, rs;   // the wave block's packed weights and scales
@@ -476,20 +475,20 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         }
     };
 
-    // the first chunk, then the ring's first kP positions
+    // the first chunk's image, then the ring's first P positions, in flight together
     Stage sg;
     stage_open(sg, tb);
     stage_issue(sg);
-    stage_finish(sg, 0);
-    __syncthreads();
-    bool staging = stage_next(sg);
     Cur fc;
     open(fc, tb);
 #pragma unroll
-    for (int d = 0; d < kP; d++) {
+    for (int d = 0; d < P; d++) {
         fetch(d, fc);
         advance(fc);
     }
+    stage_finish(sg, 0);
+    __syncthreads();
+    bool staging = stage_next(sg);
     clear();
 
     int buf = 0;
@@ -501,8 +500,8 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
             stage_issue(sg);                 // past the last chunk: repeats it (never finished)
 #pragma unroll
             for (int gg = 0; gg < kCG; gg++) {
-                consume(gg % kP, buf, gg);
-                fetch(gg % kP, fc);
+                consume(gg % P, buf, gg);
+                fetch(gg % P, fc);
                 advance(fc);
             }
             zero_term(buf);
@@ -555,22 +554,48 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     }
 }
 
-// The K parts of every split linear of a pass, added in part order with bias and residual:
-// blockIdx.y is the entry, 4 consecutive outputs per lane (N % 4 == 0).
+// The K parts of every split linear of a pass, summed with bias and residual: blockIdx.y is the
+// entry; 4 lanes (a DPP quad) per 4 consecutive outputs (N % 4 == 0), lane r summing parts
+// r, r + 4, ... in order, the quad's four sums then combined as (s0 + s1) + (s2 + s3), so every
+// run adds in the same order. Up to 4 loads per lane are issued before their adds.
 __global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, int M)
 {
     const PartSum e = entries[blockIdx.y];
     const int n4 = e.N / 4;
-    const int i = blockIdx.x * 256 + threadIdx.x;          // 4-value group over [M][N]
-    if (i >= M * n4) return;
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x) >> 2;   // 4-value group over [M][N]
+    const int r = threadIdx.x & 3;
+    if (i >= M * n4) return;                                 // whole quads leave together
     const int m = i / n4, c = (i - m * n4) * 4;
     const size_t stride = (size_t)M * e.N;
     const float* p = e.part0 + (size_t)m * e.N + c;
-    f32x4 v = ld_global(reinterpret_cast<const f32x4*>(p));
-    for (int q = 1; q < e.parts; q++) v += ld_global(reinterpret_cast<const f32x4*>(p + (size_t)q * stride));
-    if (e.bias) v += ld_global(reinterpret_cast<const f32x4*>(e.bias + c));
-    if (e.res) v += ld_global(reinterpret_cast<const f32x4*>(e.res + (size_t)m * e.N + c));
-    st_global(reinterpret_cast<f32x4*>(e.y + (size_t)m * e.N + c), v);
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    int q = r;
+    for (; q + 12 < e.parts; q += 16) {
+        const f32x4 a0 = ld_global(reinterpret_cast<const f32x4*>(p + (size_t)q * stride));
+        const f32x4 a1 = ld_global(reinterpret_cast<const f32x4*>(p + (size_t)(q + 4) * stride));
+        const f32x4 a2 = ld_global(reinterpret_cast<const f32x4*>(p + (size_t)(q + 8) * stride));
+        const f32x4 a3 = ld_global(reinterpret_cast<const f32x4*>(p + (size_t)(q + 12) * stride));
+        v += a0;
+        v += a1;
+        v += a2;
+        v += a3;
+    }
+    for (; q < e.parts; q += 4) v += ld_global(reinterpret_cast<const f32x4*>(p + (size_t)q * stride));
+    // quad_perm [1,0,3,2] then [2,3,0,1]: lane 0 ends with (s0 + s1) + (s2 + s3) (an add's two
+    // operands commute exactly, so which lane reads which does not matter). Each component is
+    // copied to a scalar first: __builtin_bit_cast of a vector element subscript (v[k]) read
+    // element 0 whatever k.
+    f32x4 t;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float sk = v[k];
+        const float w = sk + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sk), 0xB1, 0xF, 0xF, false));
+        t[k] = w + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, w), 0x4E, 0xF, 0xF, false));
+    }
+    if (r != 0) return;
+    if (e.bias) t += ld_global(reinterpret_cast<const f32x4*>(e.bias + c));
+    if (e.res) t += ld_global(reinterpret_cast<const f32x4*>(e.res + (size_t)m * e.N + c));
+    st_global(reinterpret_cast<f32x4*>(e.y + (size_t)m * e.N + c), t);
 }
 
 }  // namespace
@@ -578,8 +603,8 @@ __global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, i
 hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, hipStream_t stream)
 {
     if (count < 1) return hipSuccess;
-    const int groups = M * (max_n / 4);
-    hipLaunchKernelGGL(part_sum_kernel, dim3((groups + 255) / 256, count), dim3(256), 0, stream, entries_dev, M);
+    const int threads = M * (max_n / 4) * 4;
+    hipLaunchKernelGGL(part_sum_kernel, dim3((threads + 255) / 256, count), dim3(256), 0, stream, entries_dev, M);
     return hipGetLastError();
 }
 
@@ -614,8 +639,11 @@ hipError_t launch_strips_wide(const StripArgs& a, size_t lds, hipStream_t stream
                                : reinterpret_cast<const void*>(&wide_digits_kernel<1>);
     hipError_t e = hipLaunchKernel(dfn, dim3(a.dimg_count), dim3(kThreads), args, strip_wide_image_bytes(a.M), stream);
     if (e != hipSuccess) return e;
-    const void* fn = a.M <= 8 ? reinterpret_cast<const void*>(&strip_wide_kernel<0>)
-                              : reinterpret_cast<const void*>(&strip_wide_kernel<1>);
+    const bool deep = a.ring == 4;
+    const void* fn = a.M <= 8 ? (deep ? reinterpret_cast<const void*>(&strip_wide_kernel<0, 4>)
+                                      : reinterpret_cast<const void*>(&strip_wide_kernel<0, 2>))
+                              : (deep ? reinterpret_cast<const void*>(&strip_wide_kernel<1, 4>)
+                                      : reinterpret_cast<const void*>(&strip_wide_kernel<1, 2>));
     return hipLaunchKernel(fn, dim3(a.G), dim3(kThreads), args, lds, stream);
 }
 
