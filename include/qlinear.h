@@ -323,14 +323,16 @@ int ql_seq_status(ql_ctx* ctx, ql_seq* seq);
  * A fused sequence runs as dependency-ordered tiles (QL_SEQ_TILES) in one launch, except as
  * below. ql_plan_seq_fused and ql_seq_create_fused with fuse == NULL behave as ql_plan_seq and
  * ql_seq_create.
- * Chained sequences (fused or not) at M = 5..16 whose weights exceed what the MALL keeps (192 MiB)
- * and whose linears all have groups of 128, K % 512 == 0, K >= 1024 and N % 512 == 0 run pass by
- * pass instead (QL_SEQ_STRIP_PASSES): ql_seq_run enqueues, per pass, one launch per distinct
- * RMSNorm or SiLU-mul input (into buffers of the sequence), the pass's digit-image and
- * column-strip launches (every strip cut into K parts of whole 512-k chunks, each part's sums
- * stored apart), and one launch that adds each linear's parts in part order with its bias and
- * residual; stream order replaces the device-side waits (nothing can abort). QL_SEQ_PASSES=0 in
- * the environment keeps the tiles. */
+ * Chained sequences (fused or not) at M = 5..16 with fp32 x whose weights exceed what the MALL
+ * keeps (192 MiB) and whose linears all have groups of 128, K % 512 == 0, K >= 1024 and
+ * N % 512 == 0 run pass by pass instead (QL_SEQ_STRIP_PASSES): ql_seq_run enqueues, per pass,
+ * the pass's column-strip launch (every strip cut into K parts of whole 512-k chunks, each part's
+ * sums stored apart; each linear's activations formed as they are staged: as is, times an
+ * RMSNorm weight, or SiLU-mul of two producers) and one launch that adds each linear's parts in a
+ * fixed order, times the row's 1/rms for an RMSNorm'd input, with bias and residual (and the row
+ * sums of squares of outputs a later linear RMSNorms); an external input that is RMSNorm'd adds
+ * one launch before its pass. Stream order replaces the device-side waits (nothing can abort).
+ * QL_SEQ_PASSES=0 in the environment keeps the tiles. */
 typedef struct ql_seq_fuse {
     uint64_t norm_w_off;
     uint64_t x2_off;

@@ -40,17 +40,13 @@ struct ql_graph {
     hipGraphExec_t exec;
 };
 
-// One launch of a pass-by-pass sequence: an RMSNorm of an input (e), a SiLU-mul (o = silu(g) * u
-// over n values), a pass's strips (s, lds), or the pass's part sums (sums).
+// One launch of a pass-by-pass sequence: the RMSNorm of an external input (e), a pass's strips
+// (s, lds), or the pass's part sums (sums).
 struct SeqStep {
-    enum Kind { kNorm, kGlu, kStrips, kPartSums } kind;
+    enum Kind { kNorm, kStrips, kPartSums } kind;
     const ql::PartSum* sums = nullptr;   // kPartSums: the device table, count entries
     int count = 0, M = 0, max_n = 0;
     ql::ElemArgs e{};
-    const float* g = nullptr;
-    const float* u = nullptr;
-    float* o = nullptr;
-    long long n = 0;
     ql::StripArgs s{};
     uint64_t lds = 0;
 };
@@ -464,7 +460,7 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
 // Device tables of a column-strip sequence: linears, strips, per-workgroup strip ranges, and
 // stored-7 qzeros words for linears without qzeros.
 struct StripLayout {
-    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, poff;
+    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, poff, in;
     uint64_t dimg, dimg_base, dimg_lin;   // the wide kernel's digit images and their tables
     int32_t dimg_count;
     uint64_t total;
@@ -490,13 +486,16 @@ StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripP
                                                               ((specs[i].N + 7) / 8));
     L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
     L.poff = take(sizeof(int64_t) * std::max(1, n));
-    // strip_wide_kernel: one digit image per 512-k chunk of every linear
+    L.in = take(sizeof(ql::StripIn) * std::max(1, n));
+    // strip_wide_kernel: one digit image per 512-k chunk of every linear (unless the activations
+    // are staged through StripIn)
+    const bool images = p.wide && !p.staged;
     L.dimg_count = 0;
-    if (p.wide)
+    if (images)
         for (int i = 0; i < n; i++) L.dimg_count += specs[i].K / 512;
     L.dimg_base = take(sizeof(int32_t) * std::max(1, n));
     L.dimg_lin = take(sizeof(int32_t) * std::max(1, L.dimg_count));
-    L.dimg = take(p.wide ? ql::strip_wide_image_bytes(M) * (uint64_t)L.dimg_count : 16);
+    L.dimg = take(images ? ql::strip_wide_image_bytes(M) * (uint64_t)L.dimg_count : 16);
     L.total = off;
     return L;
 }
@@ -554,7 +553,8 @@ struct StripBuild {
 };
 
 int strip_build(const std::vector<ql::SeqSpec>& specs, std::vector<ql::SeqLinear> lin, int M, int group,
-                const ql::StripPlan& plan, const std::vector<int64_t>* poff, float* partial, StripBuild* out)
+                const ql::StripPlan& plan, const std::vector<int64_t>* poff, float* partial,
+                const std::vector<ql::StripIn>* ins, StripBuild* out)
 {
     out->plan = plan;
     const ql::StripPlan& sp = out->plan;
@@ -575,7 +575,10 @@ int strip_build(const std::vector<ql::SeqSpec>& specs, std::vector<ql::SeqLinear
                       hipMemcpyHostToDevice);
     if (e == hipSuccess && poff)
         e = hipMemcpy(dev + lay.poff, poff->data(), sizeof(int64_t) * n, hipMemcpyHostToDevice);
-    if (e == hipSuccess && sp.wide) {
+    if (e == hipSuccess && sp.staged)
+        e = ins ? hipMemcpy(dev + lay.in, ins->data(), sizeof(ql::StripIn) * n, hipMemcpyHostToDevice)
+                : hipErrorInvalidValue;
+    if (e == hipSuccess && sp.wide && !sp.staged) {
         std::vector<int32_t> base(n), owner;
         for (int i = 0; i < n; i++) {
             base[i] = (int32_t)owner.size();
@@ -600,7 +603,8 @@ int strip_build(const std::vector<ql::SeqSpec>& specs, std::vector<ql::SeqLinear
     a.stream = sp.stream ? 1 : 0;
     a.wide = sp.wide ? 1 : 0;
     a.ring = sp.ring;
-    a.dimg = sp.wide ? dev + lay.dimg : nullptr;
+    a.dimg = sp.wide && !sp.staged ? dev + lay.dimg : nullptr;
+    a.in = sp.staged ? reinterpret_cast<const ql::StripIn*>(dev + lay.in) : nullptr;
     a.dimg_base = reinterpret_cast<const int32_t*>(dev + lay.dimg_base);
     a.dimg_lin = reinterpret_cast<const int32_t*>(dev + lay.dimg_lin);
     a.dimg_count = lay.dimg_count;
@@ -643,7 +647,7 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     ql::StripPlan plan;
     ql::plan_strips(specs, M, ql::strip_grid(ctx->cu_count, specs, M), &plan);
     StripBuild b;
-    int rc = strip_build(specs, lin, M, descs[0].group, plan, nullptr, nullptr, &b);
+    int rc = strip_build(specs, lin, M, descs[0].group, plan, nullptr, nullptr, nullptr, &b);
     if (rc) return rc;
     ql_seq* q = new ql_seq();
     q->device = ctx->device;
@@ -680,11 +684,11 @@ int seq_pass_of(const std::vector<ql::SeqSpec>& specs, std::vector<int>* pass)
     return depth;
 }
 
-bool passes_ok(const std::vector<ql::SeqSpec>& specs, int M)
+bool passes_ok(const std::vector<ql::SeqSpec>& specs, int M, int32_t x_dtype)
 {
     const char* env = getenv("QL_SEQ_PASSES");
     if (env && atoi(env) == 0) return false;
-    if (M < 5 || M > ql::kGemvMaxM) return false;
+    if (M < 5 || M > ql::kGemvMaxM || x_dtype != QL_DTYPE_F32) return false;
     uint64_t bytes = 0;
     bool chained = false;
     for (const ql::SeqSpec& s : specs) {
@@ -696,27 +700,30 @@ bool passes_ok(const std::vector<ql::SeqSpec>& specs, int M)
     return chained && bytes > ql::kStripMallBytes;
 }
 
-// The pass-by-pass form's plan: per pass the linears and their strip plan, the distinct
-// transformed inputs and their buffer offsets.
+// The pass-by-pass form's plan: per pass the linears and their strip plan; the external inputs
+// that are RMSNorm'd (one launch each, into a buffer of the sequence); the producers whose output
+// a consumer RMSNorms (their part sums also write its row sums of squares).
 struct PassInput {
-    bool glu;
-    int x_src, x2_src;           // producers, or -1 (then the offsets below)
-    uint64_t x_off, x2_off, w_off;
+    uint64_t x_off, w_off;       // external x in the activation arena, norm weight in the weights'
     float eps;
     int K;
-    uint64_t buf_off;            // in the sequence's input buffers
+    uint64_t buf_off;            // in the sequence's buffers
 };
 struct PassesPlan {
     std::vector<int> pass;       // per linear
     int depth = 0;
     std::vector<PassInput> inputs;
     std::vector<int> input_of;   // per linear: index into inputs, or -1
+    std::vector<int64_t> ssq_off;  // per linear: its output's row sums of squares (bytes), or -1
     std::vector<std::vector<int>> members;      // per pass: its linears
     std::vector<std::vector<ql::SeqSpec>> specs; // per pass: the strip launch's specs
     std::vector<ql::StripPlan> plans;
     std::vector<std::vector<int64_t>> poff;      // per pass: partial-sum offsets (floats) per member
     std::vector<std::vector<int>> parts;         // per pass: K parts per member
-    uint64_t input_bytes = 0, partial_bytes = 0; // the partial buffer serves every pass in turn
+    // the sequence's buffers: normed inputs, then sums of squares, then the partial sums (which
+    // serve every pass in turn)
+    uint64_t input_bytes = 0, ssq_bytes = 0, partial_bytes = 0;
+    uint64_t buffer_bytes() const { return input_bytes + ssq_bytes + partial_bytes; }
 };
 
 void plan_passes(const std::vector<ql::SeqSpec>& specs, const ql_seq_fuse* fuse, const uint64_t* x_offs,
@@ -725,24 +732,28 @@ void plan_passes(const std::vector<ql::SeqSpec>& specs, const ql_seq_fuse* fuse,
     const int n = (int)specs.size();
     P->depth = seq_pass_of(specs, &P->pass);
     P->input_of.assign(n, -1);
+    P->ssq_off.assign(n, -1);
     for (int i = 0; i < n; i++) {
         const ql::SeqSpec& sp = specs[i];
-        if (!(sp.fuse & (ql::kFuseNorm | ql::kFuseGlu))) continue;
+        if (!(sp.fuse & ql::kFuseNorm)) continue;
+        if (sp.src >= 0) {
+            // the producer's part sums give the row sums of squares; the strips stage x * w
+            int64_t& o = P->ssq_off[sp.src];
+            if (o < 0) {
+                o = (int64_t)P->ssq_bytes;
+                P->ssq_bytes += align256((uint64_t)M * (sp.K / 256) * 4);
+            }
+            continue;
+        }
         PassInput in{};
-        in.glu = (sp.fuse & ql::kFuseGlu) != 0;
-        in.x_src = sp.src;
-        in.x_off = sp.src >= 0 ? 0 : x_offs[i];
-        in.x2_src = in.glu ? sp.src2 : -1;
-        in.x2_off = in.glu && sp.src2 < 0 ? fuse[i].x2_off : 0;
-        in.w_off = in.glu ? 0 : fuse[i].norm_w_off;
-        in.eps = in.glu ? 0.f : fuse[i].norm_eps;
+        in.x_off = x_offs[i];
+        in.w_off = fuse[i].norm_w_off;
+        in.eps = fuse[i].norm_eps;
         in.K = sp.K;
         int k = -1;
         for (int q = 0; q < (int)P->inputs.size() && k < 0; q++) {
             const PassInput& o = P->inputs[q];
-            if (o.glu == in.glu && o.x_src == in.x_src && o.x_off == in.x_off && o.x2_src == in.x2_src &&
-                o.x2_off == in.x2_off && o.w_off == in.w_off && o.eps == in.eps && o.K == in.K)
-                k = q;
+            if (o.x_off == in.x_off && o.w_off == in.w_off && o.eps == in.eps && o.K == in.K) k = q;
         }
         if (k < 0) {
             in.buf_off = P->input_bytes;
@@ -823,56 +834,66 @@ int passes_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
         return rc;
     };
     {
-        hipError_t e = hipMalloc(&q->dev, P.input_bytes + P.partial_bytes);
-        if (e != hipSuccess) return cleanup(hip_fail(e, "ql_seq_create input and partial-sum buffers"));
+        hipError_t e = hipMalloc(&q->dev, P.buffer_bytes());
+        if (e != hipSuccess) return cleanup(hip_fail(e, "ql_seq_create pass buffers"));
     }
-    float* const partial = reinterpret_cast<float*>(q->dev + P.input_bytes);
+    float* const ssq = reinterpret_cast<float*>(q->dev + P.input_bytes);
+    float* const partial = reinterpret_cast<float*>(q->dev + P.input_bytes + P.ssq_bytes);
+    auto ssq_of = [&](int j) {
+        return P.ssq_off[j] < 0 ? nullptr : ssq + P.ssq_off[j] / 4;
+    };
     auto y_ptr = [&](int j) { return reinterpret_cast<float*>(act->base + y_offs[j]); };
     auto ext_ptr = [&](int src, uint64_t off) -> const float* {
         return src >= 0 ? y_ptr(src) : reinterpret_cast<const float*>(act->base + off);
     };
     std::vector<bool> made(P.inputs.size(), false);
-    uint64_t bytes = P.input_bytes + P.partial_bytes;
+    uint64_t bytes = P.buffer_bytes();
     for (int p = 0; p < P.depth; p++) {
-        // the pass's transformed inputs
+        // the pass's RMSNorm'd external inputs
         for (int i : P.members[p]) {
             const int k = P.input_of[i];
             if (k < 0 || made[k]) continue;
             made[k] = true;
             const PassInput& in = P.inputs[k];
             SeqStep st{};
-            float* buf = reinterpret_cast<float*>(q->dev + in.buf_off);
-            if (in.glu) {
-                st.kind = SeqStep::kGlu;
-                st.g = ext_ptr(in.x_src, in.x_off);
-                st.u = ext_ptr(in.x2_src, in.x2_off);
-                st.o = buf;
-                st.n = (long long)M * in.K;
-            } else {
-                st.kind = SeqStep::kNorm;
-                st.e.x = ext_ptr(in.x_src, in.x_off);
-                st.e.d = nullptr;
-                st.e.w = reinterpret_cast<const float*>(weights->base + in.w_off);
-                st.e.s = nullptr;
-                st.e.y = buf;
-                st.e.M = M;
-                st.e.C = in.K;
-                st.e.eps = in.eps;
-                st.e.vec = in.K % 4 == 0 && reinterpret_cast<uintptr_t>(st.e.x) % 16 == 0 && in.w_off % 16 == 0;
-            }
+            st.kind = SeqStep::kNorm;
+            st.e.x = ext_ptr(-1, in.x_off);
+            st.e.d = nullptr;
+            st.e.w = reinterpret_cast<const float*>(weights->base + in.w_off);
+            st.e.s = nullptr;
+            st.e.y = reinterpret_cast<float*>(q->dev + in.buf_off);
+            st.e.M = M;
+            st.e.C = in.K;
+            st.e.eps = in.eps;
+            st.e.vec = in.K % 4 == 0 && reinterpret_cast<uintptr_t>(st.e.x) % 16 == 0 && in.w_off % 16 == 0;
             q->steps.push_back(st);
         }
-        // the pass's strips, then its part sums (bias and residual)
+        // the pass's strips (each linear's activations formed as they are staged)
         std::vector<ql::SeqLinear> lin;
+        std::vector<ql::StripIn> ins;
         for (int i : P.members[p]) {
             const int k = P.input_of[i];
-            const void* x = k >= 0 ? static_cast<const void*>(q->dev + P.inputs[k].buf_off)
-                                   : static_cast<const void*>(ext_ptr(specs[i].src, x_offs[i]));
-            const int32_t xd = k >= 0 || specs[i].src >= 0 ? QL_DTYPE_F32 : x_dtype;
-            lin.push_back(seq_linear_of(&descs[i], weights, x, xd, y_ptr(i)));
+            const uint32_t fz = specs[i].fuse;
+            ql::StripIn in{};
+            const float* x;
+            if (k >= 0) {
+                x = reinterpret_cast<const float*>(q->dev + P.inputs[k].buf_off);
+            } else if (fz & ql::kFuseGlu) {
+                x = ext_ptr(specs[i].src, x_offs[i]);
+                in.kind = 2;
+                in.x2 = ext_ptr(specs[i].src2, fuse[i].x2_off);
+            } else if (fz & ql::kFuseNorm) {
+                x = y_ptr(specs[i].src);
+                in.kind = 1;
+                in.x2 = reinterpret_cast<const float*>(weights->base + fuse[i].norm_w_off);
+            } else {
+                x = ext_ptr(specs[i].src, x_offs[i]);
+            }
+            lin.push_back(seq_linear_of(&descs[i], weights, x, QL_DTYPE_F32, y_ptr(i)));
+            ins.push_back(in);
         }
         StripBuild b;
-        int rc = strip_build(P.specs[p], lin, M, descs[0].group, P.plans[p], &P.poff[p], partial, &b);
+        int rc = strip_build(P.specs[p], lin, M, descs[0].group, P.plans[p], &P.poff[p], partial, &ins, &b);
         if (rc) return cleanup(rc);
         q->bufs.push_back(b.dev);
         bytes += b.bytes;
@@ -881,6 +902,8 @@ int passes_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
         st.s = b.a;
         st.lds = b.lds;
         q->steps.push_back(st);
+        // then its part sums: the row scale of an RMSNorm'd input, bias, residual, and the row
+        // sums of squares of outputs that a consumer RMSNorms
         std::vector<ql::PartSum> sums;
         int max_n = 0;
         for (size_t k = 0; k < P.members[p].size(); k++) {
@@ -890,8 +913,14 @@ int passes_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_ar
             e.bias = lin[k].bias;
             e.res = specs[i].fuse & ql::kFuseRes ? ext_ptr(specs[i].res_src, fuse[i].res_off) : nullptr;
             e.y = y_ptr(i);
+            e.ssq = ssq_of(i);
+            if (ins[k].kind == 1) {
+                e.in_ssq = ssq_of(specs[i].src);
+                e.eps = fuse[i].norm_eps;
+            }
             e.parts = P.parts[p][k];
             e.N = descs[i].N;
+            e.K = descs[i].K;
             max_n = std::max(max_n, e.N);
             sums.push_back(e);
         }
@@ -1830,11 +1859,11 @@ int plan_seq_impl(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_
         fill_strip_info(sp, n, strip_layout(specs, sp, M).total, info);
         return QL_OK;
     }
-    if (passes_ok(specs, M)) {
+    if (passes_ok(specs, M, x_dtype)) {
         PassesPlan P;
         plan_passes(specs, fuse, x_offs, M, grid, &P);
         if (P.depth < 1) return fail(QL_E_INVALID, "sequence shapes do not fit the K-part strips");
-        uint64_t bytes = P.input_bytes + P.partial_bytes;
+        uint64_t bytes = P.buffer_bytes();
         for (int p = 0; p < P.depth; p++)
             bytes += strip_layout(P.specs[p], P.plans[p], M).total + sizeof(ql::PartSum) * P.members[p].size();
         fill_passes_info(P, n, bytes, grid, info);
@@ -1882,7 +1911,7 @@ int seq_create_impl(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_
     if (M > ql::kGemvMaxM) return prefill_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, specs, out);
     if (!fused && ql::strip_eligible(specs, M))
         return strip_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, specs, out);
-    if (passes_ok(specs, M))
+    if (passes_ok(specs, M, x_dtype))
         return passes_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, fuse, specs, out);
     int per_cu = 0;
     QL_HIP(ql::seq_blocks_per_cu(M, descs[0].group, fused, &per_cu));
@@ -2008,7 +2037,6 @@ int ql_seq_run(ql_ctx* ctx, ql_seq* seq)
         for (const SeqStep& st : seq->steps) {
             switch (st.kind) {
             case SeqStep::kNorm: QL_HIP(ql::launch_add_rmsnorm(st.e, ctx->stream)); break;
-            case SeqStep::kGlu: QL_HIP(ql::launch_silu_mul(st.g, st.u, st.o, st.n, ctx->stream)); break;
             case SeqStep::kStrips: QL_HIP(ql::launch_strips(st.s, st.lds, ctx->stream)); break;
             case SeqStep::kPartSums: QL_HIP(ql::launch_part_sums(st.sums, st.count, st.M, st.max_n, ctx->stream)); break;
             }

@@ -375,16 +375,32 @@ struct StripArgs {
     // K parts (tasks with parts > 1): partial sums [part][M][N] of linear i at partial + poff[i]
     float* partial;
     const int64_t* poff;
+    // strip_wide_kernel, K-part plans: non-null to stage each linear's activations from its fp32
+    // x through in[i] (no digit images)
+    const struct StripIn* in;
 };
 
-// Sums the K parts of strip tasks in part order, with bias and an optional residual, into y:
-// one entry per linear, y[m][n] = sum_p part_p[m][n] + bias[n] + res[m][n].
+// How a pass-by-pass linear's activations are formed while its strips stage them (x is the
+// linear's fp32 SeqLinear::x, [M][K]): kind 0 x as is; 1 x * x2[k] (an RMSNorm's weight; the
+// row's 1 / rms is applied by the part sums); 2 SiLU-mul, silu(x) * x2[m][k].
+struct StripIn {
+    const float* x2;           // kind 1: [K]; kind 2: [M][K]
+    int32_t kind;
+};
+
+// Sums the K parts of strip tasks in a fixed order, with bias and an optional residual, into y:
+// one entry per linear.
+// y[m][n] = rstd[m] * sum_p part_p[m][n] + bias[n] + res[m][n], rstd[m] = 1 / sqrt(sum_b
+// in_ssq[m][b] / K + eps) when the linear's input is an RMSNorm (else 1).
 struct PartSum {
     const float* part0;        // parts x [M][N], part p at part0 + p * M * N
     const float* bias;         // [N] or null
     const float* res;          // [M][N] or null
     float* y;                  // [M][N]
-    int32_t parts, N;
+    float* ssq;                // null, or [M][N / 256]: sums of squares of y's rows by 256 columns
+    const float* in_ssq;       // null, or the input's [M][K / 256] (its producer's ssq)
+    float eps;
+    int32_t parts, N, K;       // N % 256 == 0 when ssq is set, K % 256 == 0 when in_ssq is
 };
 hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, hipStream_t stream);
 
@@ -393,6 +409,7 @@ struct StripPlan {
     bool stream = false;       // the weights exceed what the MALL keeps between steps
     bool wide = false;         // strip_wide_kernel: streamed, split 1, M 5..16, no padding
     int ring = 2;              // strip_wide_kernel's jobs in flight per wave (4: K-part tasks)
+    bool staged = false;       // K-part plans: activations staged through StripIn, no digit images
     uint64_t lds_bytes = 0;
     uint64_t total_units = 0, busiest_units = 0;   // block-groups: all, most on one workgroup
     std::vector<StripTask> tasks;

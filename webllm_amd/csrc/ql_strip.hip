@@ -788,6 +788,7 @@ void plan_strips_kparts(const std::vector<SeqSpec>& lin, int M, int grid, StripP
     p.strips = nstrips;
     p.wide = true;
     p.ring = 4;
+    p.staged = true;
     p.lds_bytes = strip_wide_lds(M);
 }
 

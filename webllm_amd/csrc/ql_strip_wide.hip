@@ -223,7 +223,12 @@ __global__ __launch_bounds__(kThreads) void wide_digits_kernel(const StripArgs a
 #endif
 // P: jobs in flight per wave (the register ring's depth): 2 for long strips over all of K, 4 (a
 // chunk's every job) for the short K-part tasks, whose time is mostly round trips to HBM.
-template <int L, int P>
+// S: where a chunk's activation digits come from. 0: the digit images of wide_digits_kernel;
+// 1: computed while staging from fp32 activations formed through the linear's StripIn (as is,
+// times the RMSNorm weight, or SiLU-mul of two producers), so a pass of a pass-by-pass sequence
+// needs neither an elementwise launch nor a digits launch (an RMSNorm's 1/rms, one scalar per
+// row, multiplies the sums in the part-sum launch: the linear commutes with it).
+template <int L, int P, int S>
 __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wide_kernel(const StripArgs a)
 {
     static_assert(kCG % P == 0, "whole ring rounds per chunk");
@@ -247,11 +252,23 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     auto bias_lds = [&](int par) { return bias_base + par * (kBlocks * kCols); };
 
 
-    // ---- staging: the chunk being staged (task si, chunk sch): its digit image into LDS ----
+    if constexpr (S == 1) {
+        // rows M and up of both chunk buffers stay zero (staging writes rows below M only)
+        if (M < Lay::kMaxM) {
+            for (int o = threadIdx.x * 16; o < 2 * Lay::kBufB; o += kThreads * 16)
+                *reinterpret_cast<uint4*>(lds + o) = uint4{0u, 0u, 0u, 0u};
+            __syncthreads();
+        }
+    }
+
+    // ---- staging: the chunk being staged (task si, chunk sch): its digits into LDS ----
     struct Stage {
         int si, sch, ch0, chend, ngroups, ct, has_bias;
-        __amdgpu_buffer_rsrc_t ri, rb, rz, rs;   // the linear's digit images, bias (x without one), the wave block's zeros, scales
+        __amdgpu_buffer_rsrc_t ri, rb, rz, rs;   // the linear's digit images (S = 1: x), bias (x without one), the wave block's zeros, scales
         uint32_t Gz, Gs;
+        // S = 1: the second operand (SiLU-mul's up, RMSNorm's weight; x otherwise)
+        __amdgpu_buffer_rsrc_t r2;
+        int K, kind;
     };
     auto stage_open = [&](Stage& st, int ti) {
         const StripTask t = tab(a.tasks + ti);
@@ -261,8 +278,19 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         st.chend = t.ch0 + t.chunks;
         const float* b = tab(&Lp->bias);
         st.has_bias = b != nullptr;
-        st.ri = rsrc(a.dimg + (size_t)tab(a.dimg_base + t.linear) * Lay::kBufB);
-        st.rb = rsrc(b ? static_cast<const void*>(sptr(b) + t.ct * kCols) : static_cast<const void*>(a.dimg));
+        const void* dummy = a.dimg;                     // a global address for unused loads
+        if constexpr (S == 0) {
+            st.ri = rsrc(a.dimg + (size_t)tab(a.dimg_base + t.linear) * Lay::kBufB);
+        } else {
+            const StripIn in = tab(a.in + t.linear);
+            const float* x = sptr(static_cast<const float*>(tab(&Lp->x)));
+            st.ri = rsrc(x);
+            st.K = tab(&Lp->K);
+            st.kind = in.kind;
+            st.r2 = rsrc(in.kind != 0 ? sptr(in.x2) : x);
+            dummy = x;
+        }
+        st.rb = rsrc(b ? static_cast<const void*>(sptr(b) + t.ct * kCols) : dummy);
         st.ngroups = tab(&Lp->K) / 128;
         st.ct = t.ct;
         const int N = tab(&Lp->N);
@@ -272,18 +300,37 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         st.Gz = (((uint32_t)N + 7u) >> 3) * 4u;
         st.Gs = (uint32_t)N * 2u;
     };
-    u32x4 xr[Lay::kHI];                     // the chunk's image units of this thread
+    u32x4 xr[Lay::kHI];                     // S = 0: the chunk's image units of this thread
+    u32x4 xs[Lay::kH][4];                   // S = 1: per item, x then the second operand (8 k each)
     float bv;                               // one bias value per thread (512 = a strip's columns)
     uint32_t zq;                            // zero word of group (chunk + kq), the lane's columns
     u32x2 sq;                               // scales of group (chunk + kq), the lane's 4 columns
-    // step 1: unconditional loads (threads past the image's units re-read its last one)
+    // step 1: unconditional loads, the same number on every path (threads past the image's units
+    // or the chunk's items re-read the last one), so the wait before step 5 is exact
     auto stage_issue = [&](const Stage& st) {
         const int g0 = st.sch * kCG;
-        const uint32_t img = (uint32_t)st.sch * (uint32_t)Lay::kBufB;
+        if constexpr (S == 0) {
+            const uint32_t img = (uint32_t)st.sch * (uint32_t)Lay::kBufB;
 #pragma unroll
-        for (int h = 0; h < Lay::kHI; h++) {
-            const int u = min((int)threadIdx.x + kThreads * h, Lay::kUnits - 1);
-            xr[h] = __builtin_amdgcn_raw_buffer_load_b128(st.ri, (uint32_t)u * 16u, img, 0);
+            for (int h = 0; h < Lay::kHI; h++) {
+                const int u = min((int)threadIdx.x + kThreads * h, Lay::kUnits - 1);
+                xr[h] = __builtin_amdgcn_raw_buffer_load_b128(st.ri, (uint32_t)u * 16u, img, 0);
+            }
+        } else {
+            const int items = kCG * M * 16;
+#pragma unroll
+            for (int h = 0; h < Lay::kH; h++) {
+                const int idx = min((int)threadIdx.x + kThreads * h, items - 1);
+                const int item = idx >> 4, c = idx & 15;
+                const int gg = item / M, m = item - gg * M;
+                const uint32_t k = (uint32_t)((g0 + gg) * 128 + c * 8);
+                const uint32_t e = (uint32_t)m * (uint32_t)st.K + k;
+                xs[h][0] = __builtin_amdgcn_raw_buffer_load_b128(st.ri, e * 4u, 0, 0);
+                xs[h][1] = __builtin_amdgcn_raw_buffer_load_b128(st.ri, e * 4u + 16u, 0, 0);
+                const uint32_t e2 = st.kind == 1 ? k : e;       // the norm weight has no rows
+                xs[h][2] = __builtin_amdgcn_raw_buffer_load_b128(st.r2, e2 * 4u, 0, 0);
+                xs[h][3] = __builtin_amdgcn_raw_buffer_load_b128(st.r2, e2 * 4u + 16u, 0, 0);
+            }
         }
         bv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(st.rb, st.has_bias ? threadIdx.x * 4u : 0u, 0, 0));
         zq = __builtin_amdgcn_raw_buffer_load_b32(st.rz, (uint32_t)kq * st.Gz + (uint32_t)(j >> 1) * 4u, (uint32_t)g0 * st.Gz, 0);
@@ -293,10 +340,41 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     // step 5: the staged image into buffer `buf`, its -s*z, the strip's bias
     auto stage_finish = [&](const Stage& st, int buf) {
         char* const dig = lds + buf * Lay::kBufB;
+        if constexpr (S == 0) {
 #pragma unroll
-        for (int h = 0; h < Lay::kHI; h++) {
-            const int u = (int)threadIdx.x + kThreads * h;
-            if (u < Lay::kUnits) *reinterpret_cast<u32x4*>(dig + u * 16) = xr[h];
+            for (int h = 0; h < Lay::kHI; h++) {
+                const int u = (int)threadIdx.x + kThreads * h;
+                if (u < Lay::kUnits) *reinterpret_cast<u32x4*>(dig + u * 16) = xr[h];
+            }
+        } else {
+            const int items = kCG * M * 16;
+            float2* const gs = gst(buf);
+#pragma unroll
+            for (int h = 0; h < Lay::kH; h++) {
+                const int idx = (int)threadIdx.x + kThreads * h;
+                if (idx < items) {                // whole 16-lane groups: items is a multiple of 16
+                    const int item = idx >> 4, c = idx & 15;
+                    const int gg = item / M, m = item - gg * M;
+                    const f32x4 x0 = __builtin_bit_cast(f32x4, xs[h][0]), x1 = __builtin_bit_cast(f32x4, xs[h][1]);
+                    const f32x4 y0 = __builtin_bit_cast(f32x4, xs[h][2]), y1 = __builtin_bit_cast(f32x4, xs[h][3]);
+                    float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                    const float w2[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+                    if (st.kind == 2) {
+                        // silu(g) * u = g / (1 + exp(-g)) * u
+#pragma unroll
+                        for (int q = 0; q < 8; q++) v[q] = v[q] / (1.f + expf(-v[q])) * w2[q];
+                    } else if (st.kind == 1) {
+#pragma unroll
+                        for (int q = 0; q < 8; q++) v[q] = v[q] * w2[q];
+                    }
+                    // piece c covers k 8c .. 8c+7 of the group: 64-k block c / 8, lane group
+                    // (c % 8) / 2 of its B operand, 8-byte half c % 2 of the 16-byte row
+                    const int row = L == 0 ? (m >> 2) * 16 + 4 * (m & 3) : m;
+                    char* const r0 = dig + gg * Lay::kGB + (c >> 3) * Lay::kBbB + ((c & 7) >> 1) * Lay::kKqB + row * 16 + (c & 1) * 8;
+                    const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8);
+                    if (c == 0) gs[gg * 16 + m] = s2;
+                }
+            }
         }
         // -s * z of the lane's columns 4j .. 4j+3 for group (chunk + kq), zero = stored + 1
         const uint32_t zw = zq >> (16 * (j & 1));
@@ -557,14 +635,19 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
 // The K parts of every split linear of a pass, summed with bias and residual: blockIdx.y is the
 // entry; 4 lanes (a DPP quad) per 4 consecutive outputs (N % 4 == 0), lane r summing parts
 // r, r + 4, ... in order, the quad's four sums then combined as (s0 + s1) + (s2 + s3), so every
-// run adds in the same order. Up to 4 loads per lane are issued before their adds.
+// run adds in the same order. Up to 4 loads per lane are issued before their adds. With in_ssq
+// set (the linear's input is RMSNorm'd: its strips staged x * w), the sum is multiplied by the
+// row's 1 / rms before bias and residual. With ssq set (N % 256 == 0: a workgroup's 64 quads are
+// 256 columns of one row), the workgroup also writes the sum of squares of its 256 outputs, in a
+// fixed order, for a consumer that RMSNorms y.
 __global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, int M)
 {
+    __shared__ float red[4];
     const PartSum e = entries[blockIdx.y];
     const int n4 = e.N / 4;
     const int i = (int)(blockIdx.x * 256 + threadIdx.x) >> 2;   // 4-value group over [M][N]
     const int r = threadIdx.x & 3;
-    if (i >= M * n4) return;                                 // whole quads leave together
+    if (i >= M * n4) return;                  // whole quads (with ssq: whole workgroups) leave
     const int m = i / n4, c = (i - m * n4) * 4;
     const size_t stride = (size_t)M * e.N;
     const float* p = e.part0 + (size_t)m * e.N + c;
@@ -581,10 +664,9 @@ __global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, i
         v += a3;
     }
     for (; q < e.parts; q += 4) v += ld_global(reinterpret_cast<const f32x4*>(p + (size_t)q * stride));
-    // quad_perm [1,0,3,2] then [2,3,0,1]: lane 0 ends with (s0 + s1) + (s2 + s3) (an add's two
-    // operands commute exactly, so which lane reads which does not matter). Each component is
-    // copied to a scalar first: __builtin_bit_cast of a vector element subscript (v[k]) read
-    // element 0 whatever k.
+    // quad_perm [1,0,3,2] then [2,3,0,1]: every lane of the quad ends with (s0 + s1) + (s2 + s3)
+    // (an add's two operands commute exactly). Each component is copied to a scalar first:
+    // __builtin_bit_cast of a vector element subscript (v[k]) read element 0 whatever k.
     f32x4 t;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -592,10 +674,31 @@ __global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, i
         const float w = sk + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sk), 0xB1, 0xF, 0xF, false));
         t[k] = w + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, w), 0x4E, 0xF, 0xF, false));
     }
-    if (r != 0) return;
+    if (e.in_ssq) {
+        // the input row's sum of squares: lane r adds its 256-column blocks r, r + 4, ... in
+        // order, then the quad as above (the same bits in every quad of the row)
+        const int nb = e.K / 256;
+        const float* sp = e.in_ssq + (size_t)m * nb;
+        float ss = 0.f;
+        for (int b = r; b < nb; b += 4) ss += ld_global(sp + b);
+        const float w = ss + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, ss), 0xB1, 0xF, 0xF, false));
+        const float tot = w + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, w), 0x4E, 0xF, 0xF, false));
+        const float rstd = 1.0f / sqrtf(tot / (float)e.K + e.eps);
+        t *= rstd;
+    }
     if (e.bias) t += ld_global(reinterpret_cast<const f32x4*>(e.bias + c));
     if (e.res) t += ld_global(reinterpret_cast<const f32x4*>(e.res + (size_t)m * e.N + c));
-    st_global(reinterpret_cast<f32x4*>(e.y + (size_t)m * e.N + c), t);
+    if (r == 0) st_global(reinterpret_cast<f32x4*>(e.y + (size_t)m * e.N + c), t);
+    if (e.ssq) {
+        // the quad's lanes hold the same t: the xor 1 and 2 steps double it exactly, so the
+        // wave's butterfly ends with 4 x (the sum over its 16 quads), the same in every lane
+        float s2 = fmaf(t.w, t.w, fmaf(t.z, t.z, fmaf(t.y, t.y, t.x * t.x)));
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) s2 += __shfl_xor(s2, o);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s2;
+        __syncthreads();
+        if (threadIdx.x == 0) e.ssq[(size_t)m * (e.N / 256) + c / 256] = ((red[0] + red[1]) + (red[2] + red[3])) * 0.25f;
+    }
 }
 
 }  // namespace
@@ -633,17 +736,24 @@ size_t strip_wide_image_bytes(int M)
 
 hipError_t launch_strips_wide(const StripArgs& a, size_t lds, hipStream_t stream)
 {
-    if (!a.dimg || a.dimg_count < 1) return hipErrorInvalidValue;
     void* args[] = {const_cast<StripArgs*>(&a)};
+    if (a.in) {
+        // activations staged through StripIn: no digit images (K-part plans only)
+        if (a.ring != 4) return hipErrorInvalidValue;
+        const void* fn = a.M <= 8 ? reinterpret_cast<const void*>(&strip_wide_kernel<0, 4, 1>)
+                                  : reinterpret_cast<const void*>(&strip_wide_kernel<1, 4, 1>);
+        return hipLaunchKernel(fn, dim3(a.G), dim3(kThreads), args, lds, stream);
+    }
+    if (!a.dimg || a.dimg_count < 1) return hipErrorInvalidValue;
     const void* dfn = a.M <= 8 ? reinterpret_cast<const void*>(&wide_digits_kernel<0>)
                                : reinterpret_cast<const void*>(&wide_digits_kernel<1>);
     hipError_t e = hipLaunchKernel(dfn, dim3(a.dimg_count), dim3(kThreads), args, strip_wide_image_bytes(a.M), stream);
     if (e != hipSuccess) return e;
     const bool deep = a.ring == 4;
-    const void* fn = a.M <= 8 ? (deep ? reinterpret_cast<const void*>(&strip_wide_kernel<0, 4>)
-                                      : reinterpret_cast<const void*>(&strip_wide_kernel<0, 2>))
-                              : (deep ? reinterpret_cast<const void*>(&strip_wide_kernel<1, 4>)
-                                      : reinterpret_cast<const void*>(&strip_wide_kernel<1, 2>));
+    const void* fn = a.M <= 8 ? (deep ? reinterpret_cast<const void*>(&strip_wide_kernel<0, 4, 0>)
+                                      : reinterpret_cast<const void*>(&strip_wide_kernel<0, 2, 0>))
+                              : (deep ? reinterpret_cast<const void*>(&strip_wide_kernel<1, 4, 0>)
+                                      : reinterpret_cast<const void*>(&strip_wide_kernel<1, 2, 0>));
     return hipLaunchKernel(fn, dim3(a.G), dim3(kThreads), args, lds, stream);
 }
 
