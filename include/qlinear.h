@@ -296,9 +296,9 @@ typedef struct ql_seq_info {
     int32_t split;        /* strips: waves per 64-column block (1: strips of 8 blocks, 2: of 4) */
     int32_t stream;       /* strips: 1 when the packed weights are read with streaming loads (the
                              weights exceed what the 256 MB MALL keeps between steps) */
-    int32_t variant;      /* strips: 1 when the launch is the no-padding kernel for M = 5..16 on
-                             streamed weights (every linear: group 128, K a multiple of 512, N a
-                             multiple of 512); 0 otherwise */
+    int32_t variant;      /* strips: 1 when the launch is the no-padding kernel on streamed
+                             weights (every linear: group 128, K a multiple of 512, N a multiple
+                             of 512; M = 5..16, or 2..16 pass by pass); 0 otherwise */
 } ql_seq_info;
 /* plan only (host, pure) for a given grid size: validation and the figures above */
 int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,
@@ -323,7 +323,7 @@ int ql_seq_status(ql_ctx* ctx, ql_seq* seq);
  * A fused sequence runs as dependency-ordered tiles (QL_SEQ_TILES) in one launch, except as
  * below. ql_plan_seq_fused and ql_seq_create_fused with fuse == NULL behave as ql_plan_seq and
  * ql_seq_create.
- * Chained sequences (fused or not) at M = 5..16 with fp32 x whose weights exceed what the MALL
+ * Chained sequences (fused or not) at M = 2..16 with fp32 x whose weights exceed what the MALL
  * keeps (192 MiB) and whose linears all have groups of 128, K % 512 == 0, K >= 1024 and
  * N % 512 == 0 run pass by pass instead (QL_SEQ_STRIP_PASSES): ql_seq_run enqueues, per pass,
  * the pass's column-strip launch (every strip cut into K parts of whole 512-k chunks, each part's

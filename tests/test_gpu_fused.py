@@ -312,14 +312,14 @@ def model7b_chained(ctx, bench_mod):
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_chained_step_7b_full_size(ql, ctx, orc, bench_mod, model7b_chained, M):
     """The bench's chained 7B step (28 fused layers, 112 passes, 3.35 GB) at every M bench times
-    it: one launch of dependency-ordered tiles at M <= 4, pass by pass at M >= 5 (K-part strips
+    it: one launch of dependency-ordered tiles at M = 1, pass by pass at M >= 2 (K-part strips
     that RMSNorm-weight or SiLU-mul their activations as they stage them, then part sums with the
     row's 1/rms, bias, residual and the next norm's row sums of squares); every linear on a sample
     of 64-column blocks; finite to the last layer."""
     model = model7b_chained
     st = bench_mod.SeqStep(ctx, model, M, chained=True)
     say(f"chained 7B step M={M}: {st.info.as_dict()}")
-    assert st.info.kernel == (ql.SEQ_STRIP_PASSES if M >= 5 else ql.SEQ_TILES) and st.info.passes == 112
+    assert st.info.kernel == (ql.SEQ_STRIP_PASSES if M >= 2 else ql.SEQ_TILES) and st.info.passes == 112
     st.run(2)
     assert st.finite()
     check_step(orc, model, st, _sample, f"chained 7B M={M}")

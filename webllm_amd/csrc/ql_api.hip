@@ -660,15 +660,18 @@ int strip_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_are
     return QL_OK;
 }
 
-// ---- chained sequences of streamed weights at M = 5..16: one strip launch per pass ----
+// ---- chained sequences of streamed weights at M = 2..16: one strip launch per pass ----
 //
 // The dependency-ordered tiles at M > 1 cut K into short segments (the digits of a tile's whole
 // segment sit in LDS) and reduce them across workgroups. For a model whose weights stream from
 // HBM anyway, each pass (the linears whose producers all ran in earlier passes) runs instead as
 // the no-padding strip launch with every strip cut into K parts of whole 512-k chunks (about one
-// task per workgroup), then one launch that adds each linear's parts in part order with its bias
-// and residual. The fused RMSNorm or SiLU-mul of a pass's inputs runs before it, one launch per
-// distinct input, into a buffer of the sequence. Stream order replaces the device-side waits.
+// task per workgroup), then one launch that adds each linear's parts in a fixed order with its
+// bias and residual. The strips form each linear's activations as they stage them (an RMSNorm's
+// weight, or SiLU-mul of two producers); an RMSNorm's 1/rms scales the summed parts, from row
+// sums of squares that the producer's part sums write. Only an external input that is RMSNorm'd
+// has a launch of its own, into a buffer of the sequence. Stream order replaces the device-side
+// waits.
 int seq_pass_of(const std::vector<ql::SeqSpec>& specs, std::vector<int>* pass)
 {
     const int n = (int)specs.size();
@@ -688,7 +691,7 @@ bool passes_ok(const std::vector<ql::SeqSpec>& specs, int M, int32_t x_dtype)
 {
     const char* env = getenv("QL_SEQ_PASSES");
     if (env && atoi(env) == 0) return false;
-    if (M < 5 || M > ql::kGemvMaxM || x_dtype != QL_DTYPE_F32) return false;
+    if (M < ql::kPassMinM || M > ql::kGemvMaxM || x_dtype != QL_DTYPE_F32) return false;
     uint64_t bytes = 0;
     bool chained = false;
     for (const ql::SeqSpec& s : specs) {

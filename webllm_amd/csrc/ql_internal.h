@@ -429,8 +429,10 @@ void plan_strips(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* ou
 void plan_strips_kparts(const std::vector<SeqSpec>& lin, int M, int grid, StripPlan* out);
 hipError_t launch_strips(const StripArgs& a, size_t lds, hipStream_t stream);
 // The strip launch without padding (ql_strip_wide.hip): every linear group 128, K a multiple of
-// 4 groups, N a multiple of 512, weights streamed, strips of 8 blocks, M 5..16.
-bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan& p);
+// 4 groups, N a multiple of 512, weights streamed, strips of 8 blocks, M min_m..16 (the kernel
+// runs any M from 1; below 5 the padded strip kernel is faster over all of K).
+bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan& p, int min_m = 5);
+constexpr int kPassMinM = 2;   // pass-by-pass sequences: the K-part strips from this M
 size_t strip_wide_lds(int M);
 int strip_wide_per_cu(int M);          // workgroups per CU of the wide kernel at M rows
 size_t strip_wide_image_bytes(int M);   // one chunk's digit image

@@ -737,8 +737,8 @@ void plan_strips_kparts(const std::vector<SeqSpec>& lin, int M, int grid, StripP
     p = StripPlan{};
     p.split = 1;
     p.stream = true;
-    if (!strip_wide_eligible(lin, M, p)) return;
-    // the M 5..8 instance runs two workgroups per CU
+    if (!strip_wide_eligible(lin, M, p, kPassMinM)) return;
+    // the M <= 8 instance runs two workgroups per CU
     if (grid <= kPlanCUs) grid *= strip_wide_per_cu(M);
     p.grid = grid;
     int nstrips = 0;

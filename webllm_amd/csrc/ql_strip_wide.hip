@@ -711,9 +711,9 @@ hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int ma
     return hipGetLastError();
 }
 
-bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan& p)
+bool strip_wide_eligible(const std::vector<SeqSpec>& lin, int M, const StripPlan& p, int min_m)
 {
-    if (!p.stream || p.split != 1 || M < 5 || M > kGemvMaxM) return false;
+    if (!p.stream || p.split != 1 || M < min_m || M > kGemvMaxM) return false;
     for (const SeqSpec& s : lin)
         if (s.group != 128 || s.K % (128 * kCG) != 0 || s.N % (kBlocks * kCols) != 0) return false;
     return true;
