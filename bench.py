@@ -724,12 +724,26 @@ def main():
                     "us": round(ms * 1e3, 1), "tflops": round(tf, 2),
                     "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "launches": len(st.launches)}
                 st.release()
+        if only != "prefill_one":
+            # the model's dependency order with the layer's elementwise work, as one sequence
+            # (runForward(M = T)): pass by pass, one prefill launch per pass
+            for M in (128, 512):
+                st = SeqStep(ctx, m05, M, chained=True)
+                ms = timed(st, max(5, args.steps // 5), 2)
+                tf = st.flops / (ms * 1e-3) / 1e12
+                pre[f"{M}_chained"] = {
+                    "us": round(ms * 1e3, 1), "tflops": round(tf, 2), "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4),
+                    "passes": st.info.passes, "tasks": st.info.tiles, "finite": st.finite()}
+                st.release()
         pre["note"] = ("M x 168 linears, fp16 x, fp32 y. _one_launch: the config as written (each linear "
                        "on its own input) as one persistent prefill launch (tflops from the kernel "
                        "time: graphs of 10 launches, HIP events); _one_launch_f32x: the same launch fed "
                        "fp32 x, rounded to fp16 as staged. Plain M: the same as ql_linear_batch "
                        "launches of 8 linears. _layered: the model's dependency order, one launch per "
-                       "(q,k,v | o | gate,up | down) group (96 launches)")
+                       "(q,k,v | o | gate,up | down) group (96 launches). _chained: the model's "
+                       "dependency order as one sequence with the layer's RMSNorms, SiLU-mul and "
+                       "residuals (ql_seq_create_fused, fp32 x): per pass one prefill launch (96), "
+                       "plus one launch per RMSNorm or SiLU-mul input (72)")
         extra["prefill05"] = pre
         log(f"prefill: {pre}")
 

@@ -277,6 +277,7 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
 #define QL_SEQ_STRIPS 1
 #define QL_SEQ_PREFILL 2
 #define QL_SEQ_STRIP_PASSES 3
+#define QL_SEQ_PREFILL_PASSES 4
 typedef struct ql_seq ql_seq;
 typedef struct ql_seq_info {
     int32_t linears;
@@ -298,7 +299,8 @@ typedef struct ql_seq_info {
                              weights exceed what the 256 MB MALL keeps between steps) */
     int32_t variant;      /* strips: 1 when the launch is the no-padding kernel on streamed
                              weights (every linear: group 128, K a multiple of 512, N a multiple
-                             of 512; M = 5..16, or 2..16 pass by pass); 0 otherwise */
+                             of 512; M = 5..16, or 2..16 pass by pass); QL_SEQ_PREFILL_PASSES: the
+                             passes that run the chunked split-K GEMM; 0 otherwise */
 } ql_seq_info;
 /* plan only (host, pure) for a given grid size: validation and the figures above */
 int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,

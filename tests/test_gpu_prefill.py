@@ -233,3 +233,82 @@ def test_prefill_config3_full_step(ql, ctx, orc, model05, M):
         worst = max(worst, float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)))
     say(f"  config 3 M={M}: 168 linears within bar, worst normwise {worst:.3e}")
     st.release()
+
+
+def flip_bound(x, w_cols):
+    """Per output [M, len(cols)]: the most that fp16 rounding of an fp32 activation computed
+    slightly differently (within 16 fp32 ulps) can move y = f16(x) . W^T: sum over the
+    activations within that distance of an fp16 rounding midpoint of one fp16 ulp times |w|."""
+    x = np.asarray(x, dtype=np.float32)
+    h = x.astype(np.float16)
+    ulp16 = np.spacing(np.abs(h)).astype(np.float32)
+    slack = ulp16 / 2 - np.abs(x - h.astype(np.float32))
+    amb = slack <= 16 * np.spacing(np.abs(x))
+    d = np.where(amb, ulp16, 0.0).astype(np.float64)
+    return d @ np.abs(np.asarray(w_cols, dtype=np.float64)).T
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [128, 300])
+def test_prefill_chained_step(ql, ctx, orc, model05, M):
+    """The 0.5B step in the model's dependency order at M > 16 (runForward(M = T),
+    qwen.ts:398-482) as one sequence: q/k/v <- rmsnorm(h), h1 = h + o(q), gate/up <- rmsnorm(h1),
+    h2 = h1 + down(silu(gate) * up), 24 layers, run pass by pass (96 prefill launches with the
+    RMSNorm and SiLU-mul launches between them, the residuals added at the stores). Every linear
+    on sampled blocks against the oracle on the inputs the GPU produced: its RMSNorm or SiLU-mul
+    in fp32, rounded to fp16 as the launch stages it, fp16 weights, the bar 1e-5 x the input's rms
+    + 2e-3 |ref| plus the rounding ambiguity: the GPU's fp32 RMSNorm or SiLU-mul can differ from
+    the oracle's in the last bits, and an activation within 16 fp32 ulps of an fp16 midpoint can
+    round either way, moving each output by up to one fp16 ulp of that activation times |w|
+    (flip_bound). Outputs stay finite to the last layer; a graph replay is bit-identical."""
+    st = bench.SeqStep(ctx, model05, M, chained=True)
+    info = st.info
+    say(f"chained prefill M={M}: {info.as_dict()}")
+    assert info.kernel == ql.SEQ_PREFILL_PASSES and info.passes == 96 and info.linears == 168
+    st.run(2)
+    assert st.finite()
+    ql_none = (1 << 64) - 1
+    y_of = {yo: i for i, yo in enumerate(st.y_offs)}
+    ys = [st.act.read(yo, (M, model05.shapes[lp][1]), np.float32) for yo, lp in zip(st.y_offs, st.order)]
+
+    def value(off, width):
+        return ys[y_of[off]] if off in y_of else st.act.read(off, (M, width), np.float32)
+
+    worst = 0.0
+    for i, (lp, f) in enumerate(zip(st.order, st.fuse)):
+        K, N = model05.shapes[lp]
+        t = model05.tensors[lp]
+        x = value(st.x_offs[i], K)
+        if f.norm_w_off != ql_none:
+            w = model05.arena.read(f.norm_w_off, (K,), np.float32)
+            x = orc.add_rmsnorm(x, w, f.norm_eps)[1]
+        if f.x2_off != ql_none:
+            x = orc.silu_mul(x, value(f.x2_off, K))
+        cols = _cols_sample(N)
+        ref = orc.gptq_linear_cols(t.qweight, t.qzeros, t.scales, x16(x), cols, None, bench.GROUP, w_f16=True)
+        if f.res_off != ql_none:
+            ref = ref + value(f.res_off, N)[:, cols]
+        got = np.ascontiguousarray(ys[i][:, cols])
+        atol = 1e-5 * max(1.0, float(np.sqrt(np.mean(x.astype(np.float64) ** 2))))
+        bar = atol + RTOL * np.abs(ref)
+        if f.norm_w_off != ql_none or f.x2_off != ql_none:
+            w16 = orc.dequantize_gptq_int4_f16(t.qweight, t.qzeros, t.scales, K, N, bench.GROUP)
+            bar = bar + flip_bound(x, orc.f16_bits_to_f32(w16[cols]))
+        err = np.abs(got.astype(np.float64) - ref)
+        worst = max(worst, float(err.max() / max(np.abs(ref).max(), 1e-30)))
+        k = np.unravel_index(np.argmax(err - bar), err.shape)
+        assert (err <= bar).all(), (f"M={M} linear {i} {lp}: |d| {err[k]:.3e} > bar {bar[k]:.3e} at {k} "
+                                    f"(ref {ref[k]:.3e})")
+    say(f"  chained prefill M={M}: 168 linears within bar, worst normwise {worst:.3e}")
+    # a graph replay of the whole pass-by-pass run gives the same bits
+    ctx.graph_begin()
+    st.seq.run()
+    g = ctx.graph_end()
+    for r in range(2):
+        g.launch()
+        st.seq.status()
+        for a, (yo, lp) in zip(ys, zip(st.y_offs, st.order)):
+            b = st.act.read(yo, (M, model05.shapes[lp][1]), np.float32)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"graph replay {r}"
+    g.destroy()
+    st.release()

@@ -427,7 +427,7 @@ def test_fused_residual_counts_as_a_dependency():
 def test_fused_validation():
     """Norm and GLU exclude each other; producers must run earlier and have the operand's width;
     norm weights are 16-byte aligned with eps in [0, 1]; an external residual must not overlap an
-    output; fusion is refused for prefill sequences."""
+    output; a fused prefill sequence (M > 16) takes fp32 x like any fused sequence."""
     c = Chain()
     h = c.ext(896)
     w = c.w.take(896 * 4)
@@ -459,10 +459,37 @@ def test_fused_validation():
     with pytest.raises(ql.QlError) as e:
         ql.plan_seq(c2.descs, 1, c2.x, c2.y, 256, fuse=[f(), f(x2_off=a)])
     assert e.value.name == "QL_E_INVALID"
-    # fusion is a decode feature (M <= 16)
+    # fp16 x is refused at M > 16 too
     c3 = Chain(M=32)
     ww = c3.w.take(896 * 4)
     c3.add(896, 896, c3.ext(896, es=2))
     with pytest.raises(ql.QlError) as e:
         ql.plan_seq(c3.descs, 32, c3.x, c3.y, 256, x_dtype=ql.DTYPE_F16, fuse=[f(norm_w_off=ww)])
     assert e.value.name == "QL_E_INVALID"
+
+
+@pytest.mark.parametrize("M", [17, 128, 512])
+def test_chained_prefill_runs_pass_by_pass(M):
+    """The model's dependency order at M > 16 (runForward(M = T)): the 0.5B layers chained
+    through their outputs plan as one GEMM launch per pass, 96 passes for 24 layers: the prefill
+    kernel for a pass whose 128 x 256 tiles reach 128 (gate/up at M = 512: 4 x 19 x 2), else the
+    chunked GEMM with K split (variant counts those passes); fp16 x is refused for a chained
+    prefill (the producers' outputs are fp32); independent linears keep the one-launch prefill."""
+    info = qwen_layers(Chain(M=M), 24).plan()
+    assert info.kernel == ql.SEQ_PREFILL_PASSES and info.passes == 96 and info.linears == 168
+    assert info.variant == (72 if M == 512 else 96)
+    # output tiles: 256 columns by 64 rows on the chunked GEMM at these M, 128 rows on the prefill
+    t64 = lambda N: -(-M // 64) * -(-N // 256)
+    t128 = lambda N: -(-M // 128) * -(-N // 256)
+    gu = 2 * (t128(4864) if M == 512 else t64(4864))
+    assert info.tiles == 24 * (t64(896) + 2 * t64(128) + t64(896) + gu + t64(896))
+    c = Chain(M=M)
+    y = c.add(896, 896, c.ext(896, es=2))
+    c.add(896, 896, y)
+    with pytest.raises(ql.QlError) as e:
+        c.plan(x_dtype=ql.DTYPE_F16)
+    assert e.value.name == "QL_E_INVALID" and "fp32 x" in str(e.value)
+    c = Chain(M=M)
+    for _ in range(3):
+        c.add(896, 896, c.ext(896))
+    assert c.plan().kernel == ql.SEQ_PREFILL and c.plan().passes == 1

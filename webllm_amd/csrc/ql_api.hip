@@ -40,15 +40,22 @@ struct ql_graph {
     hipGraphExec_t exec;
 };
 
-// One launch of a pass-by-pass sequence: the RMSNorm of an external input (e), a pass's strips
-// (s, lds), or the pass's part sums (sums).
+// One launch of a pass-by-pass sequence: an RMSNorm into a buffer (e), a SiLU-mul into a buffer
+// (o = silu(g) * u over n values), a pass's strips (s, lds), a pass's part sums (sums), or a
+// pass's prefill GEMM (p) or chunked GEMM (gb).
 struct SeqStep {
-    enum Kind { kNorm, kStrips, kPartSums } kind;
+    enum Kind { kNorm, kGlu, kStrips, kPartSums, kPrefill, kGemm } kind;
     const ql::PartSum* sums = nullptr;   // kPartSums: the device table, count entries
     int count = 0, M = 0, max_n = 0;
     ql::ElemArgs e{};
+    const float* g = nullptr;
+    const float* u = nullptr;
+    float* o = nullptr;
+    long long n = 0;
     ql::StripArgs s{};
     uint64_t lds = 0;
+    ql::PrefillArgs p{};
+    ql::GemmBatch gb{};
 };
 
 struct ql_seq {
@@ -325,10 +332,9 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
             if (descs[j].N != d->K)
                 return fail(QL_E_INVALID, "linear %d reads linear %d's output, but K=%d != N=%d", i, j, d->K,
                             descs[j].N);
-            if (prefill)
-                return fail(QL_E_INVALID, "linear %d reads linear %d's output: prefill sequences (M > %d) "
-                            "take independent linears (run each dependent pass as its own sequence)", i, j,
-                            ql::kGemvMaxM);
+            if (prefill && x_dtype != QL_DTYPE_F32)
+                return fail(QL_E_INVALID, "linear %d reads linear %d's output: a chained prefill sequence "
+                            "(M > %d) takes fp32 x (x_dtype QL_DTYPE_F32)", i, j, ql::kGemvMaxM);
             s.src = j;
             continue;
         }
@@ -398,8 +404,6 @@ int seq_resolve(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t*
         }
         any = any || s.fuse != 0;
     }
-    if (any && prefill)
-        return fail(QL_E_INVALID, "fused elementwise work runs in decode sequences (M = 1..%d)", ql::kGemvMaxM);
     // the fused staging reads fp32 words (norm weight, x2 and residual products are fp32)
     if (any && x_dtype != QL_DTYPE_F32)
         return fail(QL_E_INVALID, "fused sequences take fp32 x (x_dtype QL_DTYPE_F32)");
@@ -1044,6 +1048,296 @@ int prefill_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_a
     return QL_OK;
 }
 
+int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, uint64_t x_off, int M,
+               uint64_t y_off, float* partial, uint32_t* counters, int counter_base, int wg_begin,
+               ql::GemmLinear* out, bool no_split);
+
+// ---- chained prefill (M > 16): one GEMM launch per pass ----
+//
+// The model's dependency order at M > 16 (runForward(M = T) calls each layer's linears in turn):
+// each pass (the linears whose producers all ran in earlier passes) is one GEMM launch over the
+// pass's linears, reading fp32 x (a producer's output or an external input) rounded to fp16 as it
+// is staged, with a residual added at the store. A pass whose output tiles fill the device runs
+// the prefill kernel; a smaller one the chunked GEMM with K split across workgroups (the choice
+// ql_linear_batch makes), its partial sums and arrival counters in buffers of the sequence. A
+// fused RMSNorm or SiLU-mul input runs first, one launch per distinct input, into a buffer of the
+// sequence (fp32), as the reference runs its elementwise kernels between the GEMMs. Stream order
+// orders the passes.
+struct PrefillPasses {
+    std::vector<int> pass;
+    int depth = 0;
+    struct Input {
+        bool glu;
+        int x_src, x2_src;
+        uint64_t x_off, x2_off, w_off;
+        float eps;
+        int K;
+        uint64_t buf_off;
+    };
+    std::vector<Input> inputs;
+    std::vector<int> input_of;                   // per linear: index into inputs, or -1
+    std::vector<std::vector<int>> members;       // per pass: its linears
+    std::vector<ql::PrefillPlan> plans;
+    std::vector<char> chunked;                   // per pass: the chunked split-K GEMM
+    std::vector<int> chunk_tiles;                // per chunked pass: its output tiles
+    uint64_t input_bytes = 0;
+    uint64_t partial_bytes = 0;                  // the chunked passes' partial sums, reused in turn
+    int counters = 0;                            // their arrival counters (self-clearing)
+};
+
+bool seq_chained(const std::vector<ql::SeqSpec>& specs)
+{
+    for (const ql::SeqSpec& s : specs)
+        if (s.src >= 0 || s.src2 >= 0 || s.res_src >= 0 || s.fuse) return true;
+    return false;
+}
+
+void plan_prefill_passes(const std::vector<ql::SeqSpec>& specs, const ql_seq_fuse* fuse, const uint64_t* x_offs,
+                         int M, int grid, PrefillPasses* P)
+{
+    const int n = (int)specs.size();
+    P->depth = seq_pass_of(specs, &P->pass);
+    P->input_of.assign(n, -1);
+    for (int i = 0; i < n; i++) {
+        const ql::SeqSpec& sp = specs[i];
+        if (!(sp.fuse & (ql::kFuseNorm | ql::kFuseGlu))) continue;
+        PrefillPasses::Input in{};
+        in.glu = (sp.fuse & ql::kFuseGlu) != 0;
+        in.x_src = sp.src;
+        in.x_off = sp.src >= 0 ? 0 : x_offs[i];
+        in.x2_src = in.glu ? sp.src2 : -1;
+        in.x2_off = in.glu && sp.src2 < 0 ? fuse[i].x2_off : 0;
+        in.w_off = in.glu ? 0 : fuse[i].norm_w_off;
+        in.eps = in.glu ? 0.f : fuse[i].norm_eps;
+        in.K = sp.K;
+        int k = -1;
+        for (int q = 0; q < (int)P->inputs.size() && k < 0; q++) {
+            const PrefillPasses::Input& o = P->inputs[q];
+            if (o.glu == in.glu && o.x_src == in.x_src && o.x_off == in.x_off && o.x2_src == in.x2_src &&
+                o.x2_off == in.x2_off && o.w_off == in.w_off && o.eps == in.eps && o.K == in.K)
+                k = q;
+        }
+        if (k < 0) {
+            in.buf_off = P->input_bytes;
+            P->input_bytes += align256((uint64_t)M * in.K * 4);
+            k = (int)P->inputs.size();
+            P->inputs.push_back(in);
+        }
+        P->input_of[i] = k;
+    }
+    P->members.assign(P->depth, {});
+    for (int i = 0; i < n; i++) P->members[P->pass[i]].push_back(i);
+    P->plans.assign(P->depth, ql::PrefillPlan{});
+    P->chunked.assign(P->depth, 0);
+    P->chunk_tiles.assign(P->depth, 0);
+    for (int p = 0; p < P->depth; p++) {
+        std::vector<ql::SeqSpec> sub;
+        for (int i : P->members[p]) sub.push_back(specs[i]);
+        // the chunked GEMM when the pass's prefill tiles fill less than the device and every
+        // linear has the chunked form with one tile height (as ql_linear_batch chooses)
+        int tiles = 0, bm = 0;
+        bool chunk = (int)sub.size() <= ql::kMaxBatch;
+        for (const ql::SeqSpec& sp : sub) {
+            tiles += ql::prefill_tiles(M, sp.N);
+            ql_plan pl;
+            plan_impl(M, sp.N, sp.K, sp.group, &pl);
+            const int b = ql::gemm_shape(M, sp.N, sp.K, sp.group, ql::kPlanCUs).bm;
+            chunk = chunk && pl.kind == QL_KIND_GEMM_MFMA && (bm == 0 || b == bm);
+            bm = b;
+        }
+        if (chunk && tiles < ql::kPrefillMinTiles) {
+            P->chunked[p] = 1;
+            uint64_t part = 0;
+            int ctr = 0;
+            for (const ql::SeqSpec& sp : sub) {
+                const ql::GemmShape g = ql::gemm_shape(M, sp.N, sp.K, sp.group, ql::kPlanCUs);
+                part += align256(ql::gemm_partial_bytes(M, sp.N, g.split));
+                if (g.split > 1) ctr += g.tiles_n * g.tiles_m;
+                P->chunk_tiles[p] += g.tiles_n * g.tiles_m;
+            }
+            P->partial_bytes = std::max(P->partial_bytes, part);
+            P->counters = std::max(P->counters, ctr);
+        } else {
+            ql::plan_prefill(prefill_specs(sub), M, grid, &P->plans[p]);
+        }
+    }
+}
+
+void fill_prefill_passes_info(const PrefillPasses& P, int n, uint64_t bytes, ql_seq_info* info)
+{
+    memset(info, 0, sizeof *info);
+    info->linears = n;
+    info->passes = P.depth;
+    info->max_split = 1;
+    info->device_bytes = bytes;
+    info->kernel = QL_SEQ_PREFILL_PASSES;
+    info->split = 1;
+    for (const ql::PrefillPlan& pp : P.plans) {
+        info->tiles += (int32_t)pp.tasks.size();
+        info->grid = std::max(info->grid, pp.grid);
+        info->total_units += pp.total_units;
+        info->busiest_units += pp.busiest_units;
+    }
+    for (int p = 0; p < P.depth; p++) {
+        info->variant += P.chunked[p];              // passes on the chunked split-K GEMM
+        info->tiles += P.chunk_tiles[p];
+    }
+}
+
+uint64_t prefill_passes_bytes(const PrefillPasses& P)
+{
+    uint64_t bytes = P.input_bytes + P.partial_bytes + align256(4ull * P.counters);
+    for (int p = 0; p < P.depth; p++)
+        if (!P.chunked[p]) bytes += prefill_layout((int)P.members[p].size(), P.plans[p]).total;
+    return bytes;
+}
+
+int prefill_passes_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_arena* weights,
+                          ql_arena* act, const uint64_t* x_offs, int32_t M, const uint64_t* y_offs,
+                          const ql_seq_fuse* fuse, const std::vector<ql::SeqSpec>& specs, ql_seq** out)
+{
+    PrefillPasses P;
+    plan_prefill_passes(specs, fuse, x_offs, M, ctx->cu_count, &P);
+    ql_seq* q = new ql_seq();
+    q->device = ctx->device;
+    q->passes = true;
+    auto cleanup = [&](int rc) {
+        for (char* b : q->bufs) (void)hipFree(b);
+        (void)hipFree(q->dev);
+        delete q;
+        return rc;
+    };
+    const uint64_t buf_bytes = P.input_bytes + P.partial_bytes + align256(4ull * P.counters);
+    if (buf_bytes) {
+        hipError_t e = hipMalloc(&q->dev, buf_bytes);
+        if (e == hipSuccess && P.counters)
+            e = hipMemset(q->dev + P.input_bytes + P.partial_bytes, 0, 4ull * P.counters);
+        if (e != hipSuccess) return cleanup(hip_fail(e, "ql_seq_create pass buffers"));
+    }
+    float* const partial = reinterpret_cast<float*>(q->dev + P.input_bytes);
+    uint32_t* const counters = reinterpret_cast<uint32_t*>(q->dev + P.input_bytes + P.partial_bytes);
+    auto y_ptr = [&](int j) { return reinterpret_cast<float*>(act->base + y_offs[j]); };
+    auto ext_ptr = [&](int src, uint64_t off) -> const float* {
+        return src >= 0 ? y_ptr(src) : reinterpret_cast<const float*>(act->base + off);
+    };
+    std::vector<bool> made(P.inputs.size(), false);
+    for (int p = 0; p < P.depth; p++) {
+        // the pass's RMSNorm and SiLU-mul inputs
+        for (int i : P.members[p]) {
+            const int k = P.input_of[i];
+            if (k < 0 || made[k]) continue;
+            made[k] = true;
+            const PrefillPasses::Input& in = P.inputs[k];
+            float* buf = reinterpret_cast<float*>(q->dev + in.buf_off);
+            SeqStep st{};
+            if (in.glu) {
+                st.kind = SeqStep::kGlu;
+                st.g = ext_ptr(in.x_src, in.x_off);
+                st.u = ext_ptr(in.x2_src, in.x2_off);
+                st.o = buf;
+                st.n = (long long)M * in.K;
+            } else {
+                st.kind = SeqStep::kNorm;
+                st.e.x = ext_ptr(in.x_src, in.x_off);
+                st.e.w = reinterpret_cast<const float*>(weights->base + in.w_off);
+                st.e.y = buf;
+                st.e.M = M;
+                st.e.C = in.K;
+                st.e.eps = in.eps;
+                st.e.vec = in.K % 4 == 0 && reinterpret_cast<uintptr_t>(st.e.x) % 16 == 0 && in.w_off % 16 == 0;
+            }
+            q->steps.push_back(st);
+        }
+        const std::vector<int>& mem = P.members[p];
+        auto x_of = [&](int i) {
+            const int b = P.input_of[i];
+            return b >= 0 ? static_cast<const void*>(q->dev + P.inputs[b].buf_off)
+                          : static_cast<const void*>(ext_ptr(specs[i].src, x_offs[i]));
+        };
+        auto res_of = [&](int i) {
+            return specs[i].fuse & ql::kFuseRes ? ext_ptr(specs[i].res_src, fuse[i].res_off) : nullptr;
+        };
+        if (P.chunked[p]) {
+            // the pass's chunked GEMM: K split where its tiles leave CUs idle
+            SeqStep st{};
+            st.kind = SeqStep::kGemm;
+            ql::GemmBatch& b = st.gb;
+            b.count = (int)mem.size();
+            b.M = M;
+            b.x_dtype = QL_DTYPE_F32;
+            long tiles = 0;
+            for (int i : mem) {
+                const ql::GemmShape g = ql::gemm_shape(M, descs[i].N, descs[i].K, descs[i].group, ql::kPlanCUs);
+                tiles += (long)g.tiles_n * g.tiles_m;
+                b.bm = g.bm;
+            }
+            const bool no_split = tiles * 2 >= ql::kPlanCUs;
+            uint64_t off = 0;
+            int wg = 0, counter_base = 0;
+            for (size_t k = 0; k < mem.size(); k++) {
+                const int i = mem[k];
+                int rc = gemm_entry(&descs[i], weights, act, 0, M, y_offs[i],
+                                    reinterpret_cast<float*>(reinterpret_cast<char*>(partial) + off), counters,
+                                    counter_base, wg, &b.L[k], no_split);
+                if (rc) return cleanup(rc);
+                ql::GemmLinear& L = b.L[k];
+                L.x = x_of(i);
+                L.res = res_of(i);
+                if (L.split > 1) counter_base += L.tiles_n * L.tiles_m;
+                off += align256(ql::gemm_partial_bytes(M, descs[i].N, L.split));
+                wg += L.tiles_n * L.tiles_m * L.split;
+            }
+            b.wg_total = wg;
+            q->steps.push_back(st);
+            continue;
+        }
+        // the pass's prefill launch
+        const ql::PrefillPlan& pp = P.plans[p];
+        const PrefillLayout lay = prefill_layout((int)mem.size(), pp);
+        char* dev = nullptr;
+        hipError_t e = hipMalloc(&dev, lay.total);
+        if (e != hipSuccess) return cleanup(hip_fail(e, "ql_seq_create prefill tables"));
+        q->bufs.push_back(dev);
+        std::vector<ql::PrefillLinear> lin(mem.size());
+        for (size_t k = 0; k < mem.size(); k++) {
+            const int i = mem[k];
+            const ql::GemvLinear g = make_linear(&descs[i], weights);
+            ql::PrefillLinear& L = lin[k];
+            L = ql::PrefillLinear{};
+            L.qweight = g.qweight;
+            L.qzeros = g.qzeros;
+            L.scales = g.scales;
+            L.bias = g.bias;
+            L.x = x_of(i);
+            L.y = y_ptr(i);
+            L.res = res_of(i);
+            L.N = descs[i].N;
+            L.K = descs[i].K;
+            L.group = descs[i].group;
+        }
+        e = hipMemcpy(dev + lay.lin, lin.data(), sizeof(ql::PrefillLinear) * lin.size(), hipMemcpyHostToDevice);
+        if (e == hipSuccess && !pp.tasks.empty())
+            e = hipMemcpy(dev + lay.tasks, pp.tasks.data(), sizeof(ql::PrefillTask) * pp.tasks.size(),
+                          hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy(dev + lay.task_begin, pp.task_begin.data(), sizeof(int32_t) * pp.task_begin.size(),
+                          hipMemcpyHostToDevice);
+        if (e != hipSuccess) return cleanup(hip_fail(e, "ql_seq_create upload"));
+        SeqStep st{};
+        st.kind = SeqStep::kPrefill;
+        st.p.lin = reinterpret_cast<const ql::PrefillLinear*>(dev + lay.lin);
+        st.p.tasks = reinterpret_cast<const ql::PrefillTask*>(dev + lay.tasks);
+        st.p.task_begin = reinterpret_cast<const int32_t*>(dev + lay.task_begin);
+        st.p.M = M;
+        st.p.G = pp.grid;
+        st.p.x_f32 = 1;
+        q->steps.push_back(st);
+    }
+    fill_prefill_passes_info(P, n, prefill_passes_bytes(P), &q->info);
+    *out = q;
+    return QL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1326,7 +1620,7 @@ namespace {
 // counter_base (both used only when the linear splits K).
 int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, uint64_t x_off, int M,
                uint64_t y_off, float* partial, uint32_t* counters, int counter_base, int wg_begin,
-               ql::GemmLinear* out, bool no_split = false)
+               ql::GemmLinear* out, bool no_split)
 {
     ql::GemmShape s = ql::gemm_shape(M, d->N, d->K, d->group, ql::kPlanCUs);
     if (no_split) s.split = 1;
@@ -1340,6 +1634,7 @@ int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, ui
     L.y = reinterpret_cast<float*>(act->base + y_off);
     L.partial = partial;
     L.counters = counters + counter_base;
+    L.res = nullptr;
     L.N = d->N;
     L.K = d->K;
     L.group = d->group;
@@ -1446,7 +1741,7 @@ int linear_impl(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_
     if (p.kind == QL_KIND_GEMM_MFMA && gemv_aligned(d, x_off, y_off)) {
         if (prefill_batch(ctx, 1, d, weights, act, &x_off, x_dtype, M, &y_off, &rc)) return rc;
         ql::GemmBatch b{};
-        int rc2 = gemm_entry(d, weights, act, x_off, M, y_off, partial, ctx->counters, 0, 0, &b.L[0]);
+        int rc2 = gemm_entry(d, weights, act, x_off, M, y_off, partial, ctx->counters, 0, 0, &b.L[0], false);
         if (rc2) return rc2;
         b.count = 1;
         b.M = M;
@@ -1850,6 +2145,12 @@ int plan_seq_impl(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_
     std::vector<ql::SeqSpec> specs;
     int rc = seq_resolve(n, descs, M, x_offs, x_dtype, y_offs, UINT64_MAX, UINT64_MAX, &specs, fuse);
     if (rc) return rc;
+    if (M > ql::kGemvMaxM && seq_chained(specs)) {
+        PrefillPasses P;
+        plan_prefill_passes(specs, fuse, x_offs, M, grid, &P);
+        fill_prefill_passes_info(P, n, prefill_passes_bytes(P), info);
+        return QL_OK;
+    }
     if (M > ql::kGemvMaxM) {
         ql::PrefillPlan pp;
         ql::plan_prefill(prefill_specs(specs), M, grid, &pp);
@@ -1911,6 +2212,8 @@ int seq_create_impl(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, const ql_
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
     const bool fused = seq_fused(specs);
+    if (M > ql::kGemvMaxM && seq_chained(specs))
+        return prefill_passes_create(ctx, n, descs, weights, act, x_offs, M, y_offs, fuse, specs, out);
     if (M > ql::kGemvMaxM) return prefill_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, specs, out);
     if (!fused && ql::strip_eligible(specs, M))
         return strip_create(ctx, n, descs, weights, act, x_offs, x_dtype, M, y_offs, specs, out);
@@ -2040,6 +2343,9 @@ int ql_seq_run(ql_ctx* ctx, ql_seq* seq)
         for (const SeqStep& st : seq->steps) {
             switch (st.kind) {
             case SeqStep::kNorm: QL_HIP(ql::launch_add_rmsnorm(st.e, ctx->stream)); break;
+            case SeqStep::kGlu: QL_HIP(ql::launch_silu_mul(st.g, st.u, st.o, st.n, ctx->stream)); break;
+            case SeqStep::kPrefill: QL_HIP(ql::launch_prefill(st.p, true, ctx->stream)); break;
+            case SeqStep::kGemm: QL_HIP(ql::launch_gemm_batch(st.gb, ctx->stream)); break;
             case SeqStep::kStrips: QL_HIP(ql::launch_strips(st.s, st.lds, ctx->stream)); break;
             case SeqStep::kPartSums: QL_HIP(ql::launch_part_sums(st.sums, st.count, st.M, st.max_n, ctx->stream)); break;
             }

@@ -1,4 +1,4 @@
-// Prefill GEMM for GPTQ int4 linears, M > 16: y[M,N] = f16(x)[M,K] * f16(W)[N,K]^T (+ bias),
+// Prefill GEMM for GPTQ int4 linears, M > 16: y[M,N] = f16(x)[M,K] * f16(W)[N,K]^T (+ bias, + res),
 // fp32 accumulation. Same arithmetic as the reference's M > 1 path, gemm_nt_f16_from_f32.wgsl
 // (x rounded to fp16 on load, fp16 weights from the load-time dequant), but the weights are
 // dequantized from the packed int4 words inside the kernel, bit-identical to the load-time fp16
@@ -101,10 +101,12 @@ __device__ __forceinline__ void gemm_store(const GemmLinear& L, int M, int m0, i
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + 16 * tm + 4 * kq + r;
-                if (m < M)
-                    st_global(reinterpret_cast<f32x4*>(L.y + (size_t)m * N + ncol),
-                              f32x4{acc[tm][0][r] + bias.x, acc[tm][1][r] + bias.y, acc[tm][2][r] + bias.z,
-                                    acc[tm][3][r] + bias.w});
+                if (m < M) {
+                    f32x4 v = f32x4{acc[tm][0][r] + bias.x, acc[tm][1][r] + bias.y, acc[tm][2][r] + bias.z,
+                                    acc[tm][3][r] + bias.w};
+                    if (L.res) v += ld_global(reinterpret_cast<const f32x4*>(L.res + (size_t)m * N + ncol));
+                    st_global(reinterpret_cast<f32x4*>(L.y + (size_t)m * N + ncol), v);
+                }
             }
         return;
     }
@@ -179,6 +181,7 @@ __device__ __forceinline__ void gemm_store(const GemmLinear& L, int M, int m0, i
             if (!ok[i]) continue;
             f32x4 v = sum[i];
             if (L.bias) v += ld_global(reinterpret_cast<const f32x4*>(L.bias + col[i]));
+            if (L.res) v += ld_global(reinterpret_cast<const f32x4*>(L.res + off[i] / 4u));
             st_global(reinterpret_cast<f32x4*>(L.y + off[i] / 4u), v);
         }
     }

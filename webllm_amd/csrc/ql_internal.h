@@ -71,6 +71,7 @@ struct GemmLinear {
     float* y;                  // [M, N]
     float* partial;            // [split, M, N] (split > 1)
     uint32_t* counters;        // per-tile arrival counters (split > 1), zero between launches
+    const float* res;          // [M, N] added at the store, or nullptr
     int N, K, group, split, tiles_n, tiles_m, wg_begin;
 };
 struct GemmBatch {
@@ -101,6 +102,7 @@ struct PrefillLinear {
     const float* bias;         // [N] or nullptr
     const void* x;             // [M, K] fp16, or fp32 (PrefillArgs::x_f32)
     float* y;                  // [M, N]
+    const float* res;          // [M, N] added at the store, or nullptr
     int32_t N, K, group;
     int32_t tiles_m;           // batch mode: row tiles, and the linear's first tile number
     int32_t tile_begin;

@@ -323,11 +323,28 @@ void prefill_kernel(const PrefillArgs a)
         chunk(0);
         for (int c = 1; c < cu.nch; c++) chunk(c);
 
-        // 4. the tile's outputs, bias added: lane (j, kq) holds rows 16 tm + 4 kq + r of its 4
-        //    adjacent columns; streaming stores (the outputs are not read back by the launch)
+        // 4. the tile's outputs, bias (and a residual) added: lane (j, kq) holds rows
+        //    16 tm + 4 kq + r of its 4 adjacent columns; streaming stores (the outputs are not
+        //    read back by the launch)
         const PrefillLinear cl = lin_at<TABLE>(a, cu.li);
         const int ncol = cu.n0 + wave * 64 + 4 * j;
-        if (ncol < cl.N) {
+        if (ncol < cl.N && cl.res) {
+            // y = W.x + bias + res, rows past M skipped (the residual is read only where stored)
+            const f32x4 bias = Bs[q & 1][wave * 16 + j];
+            const size_t o0 = (size_t)(cu.m0 + 4 * kq) * cl.N + ncol;
+#pragma unroll
+            for (int tm = 0; tm < kMT; tm++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (cu.m0 + 16 * tm + 4 * kq + r < M) {
+                        const size_t o = o0 + (size_t)(16 * tm + r) * cl.N;
+                        const f32x4 rv = *reinterpret_cast<const f32x4*>(cl.res + o);
+                        __builtin_nontemporal_store(
+                            f32x4{acc[tm][0][r] + bias.x + rv.x, acc[tm][1][r] + bias.y + rv.y,
+                                  acc[tm][2][r] + bias.z + rv.z, acc[tm][3][r] + bias.w + rv.w},
+                            reinterpret_cast<f32x4*>(cl.y + o));
+                    }
+        } else if (ncol < cl.N) {
             const f32x4 bias = Bs[q & 1][wave * 16 + j];
             float* yb = cl.y + (size_t)(cu.m0 + 4 * kq) * cl.N + ncol;
             if (cu.m0 + kBM <= M) {

@@ -19,7 +19,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libqlinear.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "qlinear.h")
 
-SEQ_TILES, SEQ_STRIPS, SEQ_PREFILL, SEQ_STRIP_PASSES = 0, 1, 2, 3   # ql_seq_info.kernel
+SEQ_TILES, SEQ_STRIPS, SEQ_PREFILL, SEQ_STRIP_PASSES, SEQ_PREFILL_PASSES = 0, 1, 2, 3, 4   # ql_seq_info.kernel
 QL_NONE = (1 << 64) - 1
 NOALLOC_SCRATCH_BYTES = 8 << 20   # QL_NOALLOC_SCRATCH_BYTES
 DTYPE_F32 = 0
