@@ -40,6 +40,8 @@ from webllm_amd import synth  # noqa: E402
 
 METRIC = "int4 dequant-GEMV µs per Qwen-0.5B decode step; achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
+SEQ_KERNEL_NAMES = {ql.SEQ_TILES: "tiles", ql.SEQ_STRIPS: "strips", ql.SEQ_PREFILL: "prefill",
+                    ql.SEQ_STRIP_PASSES: "strip_passes", ql.SEQ_PREFILL_PASSES: "prefill_passes"}
 F16_PEAK_TFLOPS = 2500.0
 GROUP = 128
 
@@ -198,14 +200,17 @@ class Step:
 
 
 class SeqStep:
-    """The decode step as ONE persistent launch (ql_seq_*).
+    """A step of the model's linears as one sequence (ql_seq_*), enqueued by one ql_seq_run.
 
-    chained=False: the benchmark config as written, every linear on its own input (strips).
+    chained=False: the benchmark config as written, every linear on its own input (one strip
+    launch at M <= 16, one prefill launch above).
     chained=True: the layer's data flow (src/model/qwen.ts:398-482) with its elementwise work
-    folded into the launch (ql_seq_create_fused): q/k/v <- rmsnorm(h); h1 = h + o(q) (o reads q
-    in attention's place); gate/up <- rmsnorm(h1); h2 = h1 + down(silu(gate) * up); the next
-    layer's h = h2. Each linear waits on the device for what it reads, as after a pass break in
-    the reference (qwen.ts:556-559)."""
+    folded in (ql_seq_create_fused): q/k/v <- rmsnorm(h); h1 = h + o(q) (o reads q in
+    attention's place); gate/up <- rmsnorm(h1); h2 = h1 + down(silu(gate) * up); the next
+    layer's h = h2. Each linear runs after what it reads, as after a pass break in the reference
+    (qwen.ts:556-559): on the device inside one persistent launch (dependency-ordered tiles), or
+    pass by pass in stream order (streamed weights at M = 2..16: K-part strips and part sums;
+    M > 16: one GEMM launch per pass); info.kernel says which, info.launches how many."""
 
     def __init__(self, ctx, model: Model, M: int, seed: int = 0x5EED, chained: bool = True):
         self.ctx, self.model, self.M, self.x_dtype = ctx, model, M, ql.DTYPE_F32
@@ -656,7 +661,7 @@ def main():
         extra["step05_m1_chained"] = {
             "us": round(ms * 1e3, 1), "gbs": round(ch.bytes / (ms * 1e-3) / 1e9, 1),
             "passes": ch.info.passes, "tiles": ch.info.tiles, "reduces": ch.info.reduces,
-            "finite": ch.finite(),
+            "launches": ch.info.launches, "finite": ch.finite(),
             "note": "the same 168 linears as a layer consumes them, with the layer's elementwise "
                     "work folded into the one launch: (q,k,v) <- rmsnorm(h), h1 = h + o(q), "
                     "(gate,up) <- rmsnorm(h1), h2 = h1 + down(silu(gate) * up); 96 dependent "
@@ -733,7 +738,8 @@ def main():
                 tf = st.flops / (ms * 1e-3) / 1e12
                 pre[f"{M}_chained"] = {
                     "us": round(ms * 1e3, 1), "tflops": round(tf, 2), "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4),
-                    "passes": st.info.passes, "tasks": st.info.tiles, "finite": st.finite()}
+                    "passes": st.info.passes, "launches": st.info.launches,
+                    "chunked_passes": st.info.variant, "tiles": st.info.tiles, "finite": st.finite()}
                 st.release()
         pre["note"] = ("M x 168 linears, fp16 x, fp32 y. _one_launch: the config as written (each linear "
                        "on its own input) as one persistent prefill launch (tflops from the kernel "
@@ -742,8 +748,9 @@ def main():
                        "launches of 8 linears. _layered: the model's dependency order, one launch per "
                        "(q,k,v | o | gate,up | down) group (96 launches). _chained: the model's "
                        "dependency order as one sequence with the layer's RMSNorms, SiLU-mul and "
-                       "residuals (ql_seq_create_fused, fp32 x): per pass one prefill launch (96), "
-                       "plus one launch per RMSNorm or SiLU-mul input (72)")
+                       "residuals (ql_seq_create_fused, fp32 x): per pass one GEMM launch (96: the "
+                       "prefill kernel where its tiles fill the device, else the chunked split-K "
+                       "GEMM), plus one launch per RMSNorm or SiLU-mul input (72)")
         extra["prefill05"] = pre
         log(f"prefill: {pre}")
 
@@ -928,8 +935,8 @@ def main():
                     "us": round(ms * 1e3, 1), "gbs": round(gbs, 1),
                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": st.bytes,
                     "roofline_us": round(roof_us, 1), "target_us_70pct": round(roof_us / 0.7, 1),
-                    "launches": 1, "passes": st.info.passes, "tiles": st.info.tiles,
-                    "reduces": st.info.reduces}
+                    "launches": st.info.launches, "passes": st.info.passes, "tiles": st.info.tiles,
+                    "reduces": st.info.reduces, "kernel": SEQ_KERNEL_NAMES.get(st.info.kernel, "?")}
                 if chained:
                     s7[f"{M}_chained"]["finite"] = st.finite()
                 st.release()

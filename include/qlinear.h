@@ -301,6 +301,7 @@ typedef struct ql_seq_info {
                              weights (every linear: group 128, K a multiple of 512, N a multiple
                              of 512; M = 5..16, or 2..16 pass by pass); QL_SEQ_PREFILL_PASSES: the
                              passes that run the chunked split-K GEMM; 0 otherwise */
+    int32_t launches;     /* kernel launches one ql_seq_run enqueues */
 } ql_seq_info;
 /* plan only (host, pure) for a given grid size: validation and the figures above */
 int ql_plan_seq(int32_t n, const ql_gptq_desc* descs, int32_t M, const uint64_t* x_offs,

@@ -520,6 +520,7 @@ void fill_strip_info(const ql::StripPlan& p, int n, uint64_t scratch, ql_seq_inf
     info->split = p.split;
     info->stream = p.stream ? 1 : 0;
     info->variant = p.wide ? 1 : 0;
+    info->launches = p.wide ? 2 : 1;     // the wide strips' digits launch first
 }
 
 void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info* info)
@@ -538,6 +539,7 @@ void fill_seq_info(const ql::SeqPlanOut& p, int n, uint64_t scratch, ql_seq_info
     info->split = 1;
     info->stream = 0;
     info->variant = 0;
+    info->launches = 1;
 }
 
 int set_device(ql_ctx* ctx)
@@ -813,6 +815,7 @@ void fill_passes_info(const PassesPlan& P, int n, uint64_t bytes, int grid, ql_s
     info->kernel = QL_SEQ_STRIP_PASSES;
     info->split = 1;
     info->stream = 1;
+    info->launches = 2 * P.depth + (int32_t)P.inputs.size();   // strips and part sums; external norms
     for (const ql::StripPlan& sp : P.plans) {
         info->tiles += sp.strips;
         info->lds_bytes = std::max<uint64_t>(info->lds_bytes, sp.lds_bytes);
@@ -991,6 +994,7 @@ void fill_prefill_info(const ql::PrefillPlan& p, int n, int M, const std::vector
     info->busiest_units = p.busiest_units;
     info->kernel = QL_SEQ_PREFILL;
     info->split = 1;
+    info->launches = 1;
     (void)M;
     (void)specs;
 }
@@ -1172,6 +1176,7 @@ void fill_prefill_passes_info(const PrefillPasses& P, int n, uint64_t bytes, ql_
     info->device_bytes = bytes;
     info->kernel = QL_SEQ_PREFILL_PASSES;
     info->split = 1;
+    info->launches = P.depth + (int32_t)P.inputs.size();
     for (const ql::PrefillPlan& pp : P.plans) {
         info->tiles += (int32_t)pp.tasks.size();
         info->grid = std::max(info->grid, pp.grid);

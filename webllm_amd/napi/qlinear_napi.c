@@ -794,6 +794,8 @@ static napi_value js_seq_info(napi_env env, napi_callback_info info)
     napi_set_named_property(env, o, "kernel", kv);
     napi_set_named_property(env, o, "split", sv);
     napi_set_named_property(env, o, "stream", make_i32(env, si.stream));
+    napi_set_named_property(env, o, "variant", make_i32(env, si.variant));
+    napi_set_named_property(env, o, "launches", make_i32(env, si.launches));
     return o;
 }
 

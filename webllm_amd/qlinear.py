@@ -80,7 +80,7 @@ class SeqInfo(ctypes.Structure):
                 ("lds_bytes", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64),
                 ("total_units", ctypes.c_uint64), ("busiest_units", ctypes.c_uint64),
                 ("kernel", ctypes.c_int32), ("split", ctypes.c_int32), ("stream", ctypes.c_int32),
-                ("variant", ctypes.c_int32)]
+                ("variant", ctypes.c_int32), ("launches", ctypes.c_int32)]
 
     def as_dict(self) -> dict:
         return {f: getattr(self, f) for f, _ in self._fields_}
