@@ -743,8 +743,10 @@ void plan_strips_kparts(const std::vector<SeqSpec>& lin, int M, int grid, StripP
     p.grid = grid;
     int nstrips = 0;
     for (const SeqSpec& s : lin) nstrips += s.N / (kMaxStripBlocks * kCols);
-    // at least two parts (every output goes through the part sums), about one task per workgroup
-    const int target = std::max(2, (grid + nstrips - 1) / std::max(1, nstrips));
+    // at least two parts (every output goes through the part sums), and no more tasks than
+    // workgroups: a task's time is mostly its fixed latency (first loads, digits, stores), so a
+    // workgroup that runs two takes twice as long whatever their length
+    const int target = std::max(2, grid / std::max(1, nstrips));
     struct Item {
         StripTask t;
         uint64_t cost;
