@@ -464,7 +464,7 @@ SeqLayout seq_layout(const std::vector<ql::SeqSpec>& specs, const ql::SeqPlanOut
 // Device tables of a column-strip sequence: linears, strips, per-workgroup strip ranges, and
 // stored-7 qzeros words for linears without qzeros.
 struct StripLayout {
-    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, poff, in;
+    uint64_t lin, tasks, task_begin, sym_zeros, sym_words, poff, in, flat;
     uint64_t dimg, dimg_base, dimg_lin;   // the wide kernel's digit images and their tables
     int32_t dimg_count;
     uint64_t total;
@@ -491,6 +491,7 @@ StripLayout strip_layout(const std::vector<ql::SeqSpec>& specs, const ql::StripP
     L.sym_zeros = take(4 * std::max<uint64_t>(1, L.sym_words));
     L.poff = take(sizeof(int64_t) * std::max(1, n));
     L.in = take(sizeof(ql::StripIn) * std::max(1, n));
+    L.flat = take(p.staged ? sizeof(ql::StripFlat) * std::max<size_t>(1, p.tasks.size()) : 16);
     // strip_wide_kernel: one digit image per 512-k chunk of every linear (unless the activations
     // are staged through StripIn)
     const bool images = p.wide && !p.staged;
@@ -584,6 +585,18 @@ int strip_build(const std::vector<ql::SeqSpec>& specs, std::vector<ql::SeqLinear
     if (e == hipSuccess && sp.staged)
         e = ins ? hipMemcpy(dev + lay.in, ins->data(), sizeof(ql::StripIn) * n, hipMemcpyHostToDevice)
                 : hipErrorInvalidValue;
+    if (e == hipSuccess && sp.staged) {
+        // one record per task, workgroup k running task k
+        std::vector<ql::StripFlat> flat(sp.tasks.size());
+        for (size_t k = 0; k < flat.size(); k++) {
+            const int i = sp.tasks[k].linear;
+            flat[k].t = sp.tasks[k];
+            flat[k].L = lin[i];
+            flat[k].in = (*ins)[i];
+            flat[k].poff = poff ? (*poff)[i] : 0;
+        }
+        e = hipMemcpy(dev + lay.flat, flat.data(), sizeof(ql::StripFlat) * flat.size(), hipMemcpyHostToDevice);
+    }
     if (e == hipSuccess && sp.wide && !sp.staged) {
         std::vector<int32_t> base(n), owner;
         for (int i = 0; i < n; i++) {
@@ -611,6 +624,8 @@ int strip_build(const std::vector<ql::SeqSpec>& specs, std::vector<ql::SeqLinear
     a.ring = sp.ring;
     a.dimg = sp.wide && !sp.staged ? dev + lay.dimg : nullptr;
     a.in = sp.staged ? reinterpret_cast<const ql::StripIn*>(dev + lay.in) : nullptr;
+    a.flat = sp.staged ? reinterpret_cast<const ql::StripFlat*>(dev + lay.flat) : nullptr;
+    if (sp.staged) a.G = (int32_t)sp.tasks.size();
     a.dimg_base = reinterpret_cast<const int32_t*>(dev + lay.dimg_base);
     a.dimg_lin = reinterpret_cast<const int32_t*>(dev + lay.dimg_lin);
     a.dimg_count = lay.dimg_count;

@@ -380,6 +380,9 @@ struct StripArgs {
     // strip_wide_kernel, K-part plans: non-null to stage each linear's activations from its fp32
     // x through in[i] (no digit images)
     const struct StripIn* in;
+    // strip_wide_kernel with staged activations: workgroup w runs task flat[w] alone (G tasks),
+    // whose record carries its linear's table entry, so no table read waits on another
+    const struct StripFlat* flat;
 };
 
 // How a pass-by-pass linear's activations are formed while its strips stage them (x is the
@@ -388,6 +391,12 @@ struct StripArgs {
 struct StripIn {
     const float* x2;           // kind 1: [K]; kind 2: [M][K]
     int32_t kind;
+};
+struct StripFlat {
+    StripTask t;
+    SeqLinear L;               // the task's linear
+    StripIn in;
+    int64_t poff;              // the linear's partial sums at StripArgs::partial + poff
 };
 
 // Sums the K parts of strip tasks in a fixed order, with bias and an optional residual, into y:

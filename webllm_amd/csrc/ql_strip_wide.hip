@@ -242,9 +242,22 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     const int j = lane & 15;
     const int kq = lane >> 4;
     const int wg = blockIdx.x;
-    const int tb = tab(a.task_begin + wg);
-    const int te = tab(a.task_begin + wg + 1);
-    if (tb >= te) return;
+    // S = 1: workgroup w runs flat task w alone; its task, linear entry, staging and partial
+    // offset are one record, so their loads do not wait on one another
+    int tb = wg, te = wg + 1;
+    if constexpr (S == 0) {
+        tb = tab(a.task_begin + wg);
+        te = tab(a.task_begin + wg + 1);
+        if (tb >= te) return;
+    }
+    auto task_of = [&](int ti) {
+        if constexpr (S == 1) return tab(&a.flat[ti].t);
+        else return tab(a.tasks + ti);
+    };
+    auto lin_of = [&](int ti, const StripTask& t) -> const SeqLinear* {
+        if constexpr (S == 1) return &a.flat[ti].L;
+        else return a.lin + t.linear;
+    };
 
     // chunk buffers (digits, then {2^-(E+8), sum x}), the strips' bias, the zero-term transposition
     auto gst = [&](int buf) { return reinterpret_cast<float2*>(lds + buf * Lay::kBufB + Lay::kDigB); };
@@ -271,8 +284,8 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         int K, kind;
     };
     auto stage_open = [&](Stage& st, int ti) {
-        const StripTask t = tab(a.tasks + ti);
-        const SeqLinear* Lp = a.lin + t.linear;
+        const StripTask t = task_of(ti);
+        const SeqLinear* Lp = lin_of(ti, t);
         st.si = ti;
         st.sch = st.ch0 = t.ch0;
         st.chend = t.ch0 + t.chunks;
@@ -282,7 +295,7 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         if constexpr (S == 0) {
             st.ri = rsrc(a.dimg + (size_t)tab(a.dimg_base + t.linear) * Lay::kBufB);
         } else {
-            const StripIn in = tab(a.in + t.linear);
+            const StripIn in = tab(&a.flat[ti].in);
             const float* x = sptr(static_cast<const float*>(tab(&Lp->x)));
             st.ri = rsrc(x);
             st.K = tab(&Lp->K);
@@ -410,8 +423,8 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     };
     const uint32_t ls = 8u * (uint32_t)j;
     auto open = [&](Cur& c, int ti) {
-        const StripTask t = tab(a.tasks + ti);
-        const SeqLinear* Lp = a.lin + t.linear;
+        const StripTask t = task_of(ti);
+        const SeqLinear* Lp = lin_of(ti, t);
         c.ti = ti;
         c.g = t.ch0 * kCG;
         const int N = sreg(tab(&Lp->N));
@@ -574,8 +587,8 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
 
     int buf = 0;
     for (int ti = tb; ti < te; ti++) {
-        const StripTask t = tab(a.tasks + ti);
-        const SeqLinear* Lp = a.lin + t.linear;
+        const StripTask t = task_of(ti);
+        const SeqLinear* Lp = lin_of(ti, t);
         const int nch = t.ch0 + t.chunks;   // end of the task's chunks
         for (int ch = t.ch0; ch < nch; ch++) {
             stage_issue(sg);                 // past the last chunk: repeats it (never finished)
@@ -590,7 +603,10 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
                 // a whole task's outputs with the bias, or a K part's sums into its partial block
                 const bool whole = t.parts <= 1;
                 const int N = tab(&Lp->N);
-                float* const y = whole ? tab(&Lp->y) : a.partial + tab(a.poff + t.linear) + (size_t)t.part * M * N;
+                int64_t po = 0;
+                if constexpr (S == 1) po = tab(&a.flat[ti].poff);
+                else if (!whole) po = tab(a.poff + t.linear);
+                float* const y = whole ? tab(&Lp->y) : a.partial + po + (size_t)t.part * M * N;
                 const int col = (t.ct + wave) * kCols + 4 * j;
                 const f32x4 bvv = whole ? *reinterpret_cast<const f32x4*>(bias_lds((ti - tb) & 1) + wave * kCols + 4 * j)
                                         : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -741,8 +757,9 @@ hipError_t launch_strips_wide(const StripArgs& a, size_t lds, hipStream_t stream
 {
     void* args[] = {const_cast<StripArgs*>(&a)};
     if (a.in) {
-        // activations staged through StripIn: no digit images (K-part plans only)
-        if (a.ring != 4) return hipErrorInvalidValue;
+        // activations staged through StripIn: no digit images (K-part plans only), one
+        // workgroup per flat task
+        if (a.ring != 4 || !a.flat) return hipErrorInvalidValue;
         const void* fn = a.M <= 8 ? reinterpret_cast<const void*>(&strip_wide_kernel<0, 4, 1>)
                                   : reinterpret_cast<const void*>(&strip_wide_kernel<1, 4, 1>);
         return hipLaunchKernel(fn, dim3(a.G), dim3(kThreads), args, lds, stream);
