@@ -670,6 +670,17 @@ __global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, i
     const int m = i / n4, c = (i - m * n4) * 4;
     const size_t stride = (size_t)M * e.N;
     const float* p = e.part0 + (size_t)m * e.N + c;
+    // the bias, residual and (up to 16 blocks of) the input's sums of squares go out with the
+    // parts, so the lane waits for memory once
+    const f32x4 bv = e.bias ? ld_global(reinterpret_cast<const f32x4*>(e.bias + c)) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 rv = e.res ? ld_global(reinterpret_cast<const f32x4*>(e.res + (size_t)m * e.N + c)) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nb = e.in_ssq ? e.K / 256 : 0;
+    float sb[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int b = r + 4 * k;
+        sb[k] = b < nb ? ld_global(e.in_ssq + (size_t)m * nb + b) : 0.f;
+    }
     f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
     int q = r;
     for (; q + 12 < e.parts; q += 16) {
@@ -696,17 +707,15 @@ __global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, i
     if (e.in_ssq) {
         // the input row's sum of squares: lane r adds its 256-column blocks r, r + 4, ... in
         // order, then the quad as above (the same bits in every quad of the row)
-        const int nb = e.K / 256;
-        const float* sp = e.in_ssq + (size_t)m * nb;
-        float ss = 0.f;
-        for (int b = r; b < nb; b += 4) ss += ld_global(sp + b);
+        float ss = ((sb[0] + sb[1]) + sb[2]) + sb[3];
+        for (int b = r + 16; b < nb; b += 4) ss += ld_global(e.in_ssq + (size_t)m * nb + b);
         const float w = ss + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, ss), 0xB1, 0xF, 0xF, false));
         const float tot = w + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, w), 0x4E, 0xF, 0xF, false));
         const float rstd = 1.0f / sqrtf(tot / (float)e.K + e.eps);
         t *= rstd;
     }
-    if (e.bias) t += ld_global(reinterpret_cast<const f32x4*>(e.bias + c));
-    if (e.res) t += ld_global(reinterpret_cast<const f32x4*>(e.res + (size_t)m * e.N + c));
+    if (e.bias) t += bv;
+    if (e.res) t += rv;
     if (r == 0) st_global(reinterpret_cast<f32x4*>(e.y + (size_t)m * e.N + c), t);
     if (e.ssq) {
         // the quad's lanes hold the same t: the xor 1 and 2 steps double it exactly, so the
