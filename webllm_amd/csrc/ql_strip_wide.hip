@@ -12,10 +12,17 @@
 //   recombines them in its own registers; M 5..8 (L = 0): rows 4m + d in two 16-row tiles, as
 //   strip_kernel. (Three digits, 24 bits of each group's range, measured 1.9e-5 against the
 //   1e-5 + 1e-4 |ref| bar on the 7B down projections (K = 18944), so four are kept.)
-// * the zero-point term -s*z*sum(x) goes through one v_mfma_f32_16x16x4_f32 per column quarter
-//   and chunk (k = the chunk's 4 groups: A = the groups' row sums, B = -s*z of the lane's
-//   columns, loaded per lane for group chunk + kq), added to the sums once per chunk, instead of
-//   one FMA per output and job;
+// * one instruction per nibble half: the even-k nibbles are w & 0x0F0F0F0F (n, 0..15), the odd-k
+//   ones (w ^ 0x88888888) & 0xF0F0F0F0 (16 (n - 8) as a signed byte, one v_bitop3_b32), whose
+//   activation digits are formed at a 16 times smaller scale (26 bits of the chunk's range
+//   instead of 30); the offset -8 joins the zero-point term through the odd k's own row sums;
+// * one exponent per (chunk, row) instead of per (group, row): a chunk's jobs accumulate
+//   s * digits in the exponent's units (v_fma_mix_f32 on the fp16 scale as loaded, no
+//   conversion), and the chunk's sums join the outputs with one multiply-add by 2^-(E+8);
+// * the zero-point term -s*(z+1)*sum(x_even) - s*(z-7)*sum(x_odd) goes through two
+//   v_mfma_f32_16x16x4_f32 per column quarter and chunk (k = the chunk's 4 groups: A = the
+//   groups' row sums, B = the lane's columns' -s*(z+1) or -s*(z-7)), which start the chunk's sums
+//   (L = 1) instead of one FMA per output and job;
 // * every LDS address is a lane constant plus a compile-time offset, and positions never branch;
 // * the activation digits are computed once per (linear, chunk) by wide_digits_kernel, launched
 //   just before, as images of the LDS chunk buffer; each strip's workgroup copies the image
@@ -23,7 +30,7 @@
 //   46 of the 7B step's 255 vector instructions per job at M=16). The 7B step at M=16: 792-799
 //   against 827-832 us (the digits launch itself 24.7 us); M=8 unchanged within noise.
 // Each job's epilogue is then, per output, two integer recombinations, two conversions, one FMA
-// for the digit value and one multiply-add with scale * 2^-E.
+// for the digit value and one mixed-precision multiply-add with the fp16 scale.
 #include <type_traits>
 
 #include "ql_device.h"
@@ -94,7 +101,8 @@ struct WideLayout {
     static constexpr int kBbB = 4 * kKqB;               // per 64-k block
     static constexpr int kGB = kNB * kBbB;              // per group
     static constexpr int kDigB = kCG * kGB;             // digits of one chunk
-    static constexpr int kGstB = kCG * 16 * 8;          // {2^-(E+8), sum x} per (group, row < 16)
+    // {sum x over even k, over odd k} per (group, row < 16), then 2^-(E+8) and 2^(E+8) per row
+    static constexpr int kGstB = kCG * 16 * 8 + 2 * 16 * 4;
     static constexpr int kBufB = kDigB + kGstB;         // one chunk buffer
     static constexpr int kBiasB = 2 * kBlocks * kCols * 4;   // two strips' bias
     static constexpr int kZB = L == 0 ? kW * 16 * kCols * 4 : 0;   // zero-term transposition (L = 0)
@@ -108,19 +116,29 @@ struct WideLayout {
 };
 
 // Reductions over the 16 lanes of a row by DPP row rotations (every lane ends with the combined
-// value; the max is exact, and the sum's order is fixed per lane, so each run gives the same bits).
+// value; the sum's order is fixed per lane, so each run gives the same bits).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ void row_max_sum(float& amax, float& sum)
+__device__ __forceinline__ void row_sums(float& a, float& b)
 {
     // row_ror:8, row_ror:4, quad_perm [2,3,0,1], quad_perm [1,0,3,2]
-    amax = fmaxf(amax, dpp<0x128>(amax)); sum += dpp<0x128>(sum);
-    amax = fmaxf(amax, dpp<0x124>(amax)); sum += dpp<0x124>(sum);
-    amax = fmaxf(amax, dpp<0x4E>(amax));  sum += dpp<0x4E>(sum);
-    amax = fmaxf(amax, dpp<0xB1>(amax));  sum += dpp<0xB1>(sum);
+    a += dpp<0x128>(a); b += dpp<0x128>(b);
+    a += dpp<0x124>(a); b += dpp<0x124>(b);
+    a += dpp<0x4E>(a);  b += dpp<0x4E>(b);
+    a += dpp<0xB1>(a);  b += dpp<0xB1>(b);
+}
+// max over the wave's 64 lanes (exact; every lane ends with it)
+__device__ __forceinline__ float wave_max(float a)
+{
+    a = fmaxf(a, dpp<0x128>(a));
+    a = fmaxf(a, dpp<0x124>(a));
+    a = fmaxf(a, dpp<0x4E>(a));
+    a = fmaxf(a, dpp<0xB1>(a));
+    a = fmaxf(a, __shfl_xor(a, 16));
+    return fmaxf(a, __shfl_xor(a, 32));
 }
 
 // round(v) as an integer, halves rounded up (v_cvt_rpi_i32_f32: one instruction)
@@ -137,32 +155,43 @@ __device__ __forceinline__ uint32_t digits4_of(float v, float scale)
     return ((uint32_t)round_int(v * scale) + 0x00808080u) ^ 0x00808080u;
 }
 
+// One wave stages one row's chunk: lane 16 gg + c holds the 8 values of piece c (k 8c .. 8c+7) of
+// group gg. Returns the chunk's exponent E (max|x| * 2^E < 64 over the row's 512 values).
+__device__ __forceinline__ int chunk_exponent(const float v[8])
+{
+    const float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
+                             fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
+    return group_exponent(wave_max(amax));
+}
+
 // Digits of one 8-k piece owned by one of 16 consecutive lanes (one DPP row) that hold one
 // (group, row): writes its 16-byte-row halves (k order {0,2,4,6,1,3,5,7}) for each of the four
-// digits, rows digit_stride_u2 uint2 apart, and returns the group's {2^-(E+8), sum x} (2^-8:
-// the digit pairs of the epilogue carry 2^8).
-__device__ __forceinline__ float2 stage_piece(const float v[8], uint2* row0, int digit_stride_u2)
+// digits, rows digit_stride_u2 uint2 apart, and returns the group's {sum x over even k, over odd
+// k}. Even k: digits of round(x 2^(E+24)) (the weight operand is the nibble n); odd k: of
+// round(x 2^(E+20)) (the weight operand is 16 (n - 8)), so both products carry 2^(E+24).
+__device__ __forceinline__ float2 stage_piece(const float v[8], uint2* row0, int digit_stride_u2, int E)
 {
-    float amax = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
-                       fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
-    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-    row_max_sum(amax, sum);
-    const int E = group_exponent(amax);          // max|x| * 2^E < 64
+    float se = (v[0] + v[2]) + (v[4] + v[6]);
+    float so = (v[1] + v[3]) + (v[5] + v[7]);
+    row_sums(se, so);
     const float scale = ldexpf(1.f, E + 24);
+    const float sodd = ldexpf(1.f, E + 20);
     uint32_t ev[4], od[4];
     byte_transpose(digits4_of(v[0], scale), digits4_of(v[2], scale), digits4_of(v[4], scale),
                    digits4_of(v[6], scale), ev);
-    byte_transpose(digits4_of(v[1], scale), digits4_of(v[3], scale), digits4_of(v[5], scale),
-                   digits4_of(v[7], scale), od);
+    byte_transpose(digits4_of(v[1], sodd), digits4_of(v[3], sodd), digits4_of(v[5], sodd),
+                   digits4_of(v[7], sodd), od);
 #pragma unroll
     for (int i = 0; i < 4; i++) row0[i * digit_stride_u2] = uint2{ev[i], od[i]};
-    return float2{ldexpf(1.f, -E - 8), sum};
+    return float2{se, so};
 }
 
 // The activation digits of one chunk of one linear (workgroup j: image j), laid out as
 // strip_wide_kernel's LDS chunk buffer: digits of every (group, row < M, 8-k piece) by
-// stage_piece, zeros for rows M and up, then {2^-(E+8), sum x} per (group, row). Built in LDS, then
-// copied out whole. Each strip of the linear copies the image instead of computing it.
+// stage_piece, zeros for rows M and up, then the row sums per (group, row) and 2^-(E+8), 2^(E+8)
+// per row. Built in LDS, then copied out whole. Each strip of the linear copies the image instead
+// of computing it. Wave w of pass h stages row 8h + w: its 64 lanes are the chunk's 4 groups x 16
+// pieces, so the chunk's exponent is one wave reduction.
 template <int L>
 __global__ __launch_bounds__(kThreads) void wide_digits_kernel(const StripArgs a)
 {
@@ -183,12 +212,13 @@ __global__ __launch_bounds__(kThreads) void wide_digits_kernel(const StripArgs a
     const int items = kCG * M * 16;
     const int g0 = ch * kCG;
     float2* const gs = reinterpret_cast<float2*>(lds + Lay::kDigB);
+    float* const ex = reinterpret_cast<float*>(lds + Lay::kDigB + kCG * 16 * 8);
 #pragma unroll
     for (int h = 0; h < Lay::kH; h++) {
         const int idx = (int)threadIdx.x + kThreads * h;
-        if (idx < items) {                        // whole 16-lane groups: items is a multiple of 16
+        if (idx < items) {                        // whole waves: items is a multiple of 64
             const int item = idx >> 4, c = idx & 15;
-            const int gg = item / M, m = item - gg * M;
+            const int gg = item & 3, m = item >> 2;
             const uint32_t e = (uint32_t)m * (uint32_t)K + (uint32_t)((g0 + gg) * 128 + c * 8);
             float v[8];
             if (xdt == 0) {
@@ -205,8 +235,13 @@ __global__ __launch_bounds__(kThreads) void wide_digits_kernel(const StripArgs a
             // (c % 8) / 2 of its B operand, 8-byte half c % 2 of the 16-byte row
             const int row = L == 0 ? (m >> 2) * 16 + 4 * (m & 3) : m;
             char* const r0 = lds + gg * Lay::kGB + (c >> 3) * Lay::kBbB + ((c & 7) >> 1) * Lay::kKqB + row * 16 + (c & 1) * 8;
-            const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8);
+            const int E = chunk_exponent(v);
+            const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8, E);
             if (c == 0) gs[gg * 16 + m] = s2;
+            if ((idx & 63) == 0) {
+                ex[m] = ldexpf(1.f, -E - 8);
+                ex[16 + m] = ldexpf(1.f, E + 8);
+            }
         }
     }
     __syncthreads();
@@ -261,6 +296,8 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
 
     // chunk buffers (digits, then {2^-(E+8), sum x}), the strips' bias, the zero-term transposition
     auto gst = [&](int buf) { return reinterpret_cast<float2*>(lds + buf * Lay::kBufB + Lay::kDigB); };
+    // 2^-(E+8) of row m at [m], 2^(E+8) at [16 + m]
+    auto gex = [&](int buf) { return reinterpret_cast<float*>(lds + buf * Lay::kBufB + Lay::kDigB + kCG * 16 * 8); };
     float* const bias_base = reinterpret_cast<float*>(lds + 2 * Lay::kBufB);
     auto bias_lds = [&](int par) { return bias_base + par * (kBlocks * kCols); };
 
@@ -335,7 +372,7 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
             for (int h = 0; h < Lay::kH; h++) {
                 const int idx = min((int)threadIdx.x + kThreads * h, items - 1);
                 const int item = idx >> 4, c = idx & 15;
-                const int gg = item / M, m = item - gg * M;
+                const int gg = item & 3, m = item >> 2;
                 const uint32_t k = (uint32_t)((g0 + gg) * 128 + c * 8);
                 const uint32_t e = (uint32_t)m * (uint32_t)st.K + k;
                 xs[h][0] = __builtin_amdgcn_raw_buffer_load_b128(st.ri, e * 4u, 0, 0);
@@ -349,7 +386,7 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         zq = __builtin_amdgcn_raw_buffer_load_b32(st.rz, (uint32_t)kq * st.Gz + (uint32_t)(j >> 1) * 4u, (uint32_t)g0 * st.Gz, 0);
         sq = __builtin_amdgcn_raw_buffer_load_b64(st.rs, (uint32_t)kq * st.Gs + (uint32_t)j * 8u, (uint32_t)g0 * st.Gs, 0);
     };
-    float nsz[4];                           // -s * z of group (chunk + kq), the lane's columns
+    float nsz[4], nsz2[4];                  // -s (z+1), -s (z-7) of group (chunk + kq), the lane's columns
     // step 5: the staged image into buffer `buf`, its -s*z, the strip's bias
     auto stage_finish = [&](const Stage& st, int buf) {
         char* const dig = lds + buf * Lay::kBufB;
@@ -362,12 +399,13 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         } else {
             const int items = kCG * M * 16;
             float2* const gs = gst(buf);
+            float* const ex = gex(buf);
 #pragma unroll
             for (int h = 0; h < Lay::kH; h++) {
                 const int idx = (int)threadIdx.x + kThreads * h;
-                if (idx < items) {                // whole 16-lane groups: items is a multiple of 16
+                if (idx < items) {                // whole waves (one row each): items is a multiple of 64
                     const int item = idx >> 4, c = idx & 15;
-                    const int gg = item / M, m = item - gg * M;
+                    const int gg = item & 3, m = item >> 2;
                     const f32x4 x0 = __builtin_bit_cast(f32x4, xs[h][0]), x1 = __builtin_bit_cast(f32x4, xs[h][1]);
                     const f32x4 y0 = __builtin_bit_cast(f32x4, xs[h][2]), y1 = __builtin_bit_cast(f32x4, xs[h][3]);
                     float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -387,18 +425,26 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
                     // (c % 8) / 2 of its B operand, 8-byte half c % 2 of the 16-byte row
                     const int row = L == 0 ? (m >> 2) * 16 + 4 * (m & 3) : m;
                     char* const r0 = dig + gg * Lay::kGB + (c >> 3) * Lay::kBbB + ((c & 7) >> 1) * Lay::kKqB + row * 16 + (c & 1) * 8;
-                    const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8);
+                    const int E = chunk_exponent(v);
+                    const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8, E);
                     if (c == 0) gs[gg * 16 + m] = s2;
+                    if ((idx & 63) == 0) {
+                        ex[m] = ldexpf(1.f, -E - 8);
+                        ex[16 + m] = ldexpf(1.f, E + 8);
+                    }
                 }
             }
         }
-        // -s * z of the lane's columns 4j .. 4j+3 for group (chunk + kq), zero = stored + 1
+        // -s * z of the lane's columns 4j .. 4j+3 for group (chunk + kq), zero = stored + 1, for
+        // the even k; the odd k's weight operand 16 (n - 8) moves their zero to z - 8
         const uint32_t zw = zq >> (16 * (j & 1));
         const uint32_t sw[4] = {sq.x & 0xffffu, sq.x >> 16, sq.y & 0xffffu, sq.y >> 16};
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sw[u]);
-            nsz[u] = -s * (float)(((zw >> (4 * u)) & 15u) + 1u);
+            const int zs = (int)((zw >> (4 * u)) & 15u);
+            nsz[u] = -s * (float)(zs + 1);
+            nsz2[u] = -s * (float)(zs - 7);
         }
         if (st.sch == st.ch0) bias_lds((st.si - tb) & 1)[threadIdx.x] = st.has_bias ? bv : 0.f;
     };
@@ -452,10 +498,12 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
     };
 
     // accumulators: L = 1 rows 4kq + r of column 4j + u: acc[u][r]; L = 0 rows 4t + kq: acc[u][t],
-    // and the zero term in the MFMA layout (rows 4kq + r) in zacc, folded in at a strip's end
+    // and the zero term in the MFMA layout (rows 4kq + r) in zacc, folded in at a strip's end.
+    // cacc: the current chunk's sums in units of its exponent (acc's layout), folded into acc with
+    // one multiply-add by 2^-(E+8) at the chunk's end.
     typedef float f32x2 __attribute__((ext_vector_type(2)));
     typedef typename std::conditional<L == 0, f32x2, f32x4>::type Acc;
-    Acc acc[4];
+    Acc acc[4], cacc[4];
     f32x4 zacc[L == 0 ? 4 : 1];
     auto clear = [&]() {
 #pragma unroll
@@ -477,26 +525,20 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
 #pragma unroll
             for (int t = 0; t < KT; t++)
                 av[bb][t] = *reinterpret_cast<const i32x4*>(dig + bb * Lay::kBbB + t * Lay::kTileB);
-        const float2* const gs = gst(buf) + gg * 16;
+        // the scales of the lane's 4 columns, fp16 as loaded (the epilogue's v_fma_mix_f32 takes
+        // them without a conversion)
         const uint2 sv = sb[d];
-        float s[4];
-        s[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv.x & 0xffffu));
-        s[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv.x >> 16));
-        s[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv.y & 0xffffu));
-        s[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv.y >> 16));
-        // the weight nibbles of 64-k block bb, column quarter u, as bytes
+        const f16x2 s01 = __builtin_bit_cast(f16x2, sv.x), s23 = __builtin_bit_cast(f16x2, sv.y);
+        const _Float16 s[4] = {s01[0], s01[1], s23[0], s23[1]};
+        // the weight nibbles of 64-k block bb, column quarter u, as bytes: even k n, odd k 16 (n - 8)
         auto bq_of = [&](int bb, int u) {
             const uint4 w0 = wb[d][2 * bb], w1 = wb[d][2 * bb + 1];
             const uint32_t lo[4] = {w0.x, w0.y, w0.z, w0.w};
             const uint32_t hi[4] = {w1.x, w1.y, w1.z, w1.w};
-            return i32x4{(int)(lo[u] & 0x0F0F0F0Fu), (int)((lo[u] >> 4) & 0x0F0F0F0Fu),
-                         (int)(hi[u] & 0x0F0F0F0Fu), (int)((hi[u] >> 4) & 0x0F0F0F0Fu)};
+            return i32x4{(int)(lo[u] & 0x0F0F0F0Fu), (int)((lo[u] ^ 0x88888888u) & 0xF0F0F0F0u),
+                         (int)(hi[u] & 0x0F0F0F0Fu), (int)((hi[u] ^ 0x88888888u) & 0xF0F0F0F0u)};
         };
         if constexpr (L == 1) {
-            // e[r] = 2^-(E+8) of row 4kq + r (the digit pairs below carry 2^8)
-            const f32x4 g01 = *reinterpret_cast<const f32x4*>(gs + 4 * kq);
-            const f32x4 g23 = *reinterpret_cast<const f32x4*>(gs + 4 * kq + 2);
-            const float e[4] = {g01.x, g01.z, g23.x, g23.z};
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 i32x4 c[4];
@@ -512,22 +554,18 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
                     const int lo2 = c[0][r] + c[1][r] * 256;
                     const int hi2 = c[2][r] + c[3][r] * 256;
                     const float v = fmaf((float)lo2, 0x1p-16f, (float)hi2);
-                    acc[u][r] = fmaf(s[u] * e[r], v, acc[u][r]);
+                    cacc[u][r] = fmaf((float)s[u], v, cacc[u][r]);
                 }
 #if QL_WIDE_QREGION
-                asm volatile("" : "+v"(acc[u]));
+                asm volatile("" : "+v"(cacc[u]));
                 __builtin_amdgcn_sched_barrier(0);
 #endif
             }
             // keep this job's epilogue here: without a use, the compiler sinks every job's
             // epilogue to the end of the chunk and keeps all four jobs' MFMA results live
 #pragma unroll
-            for (int u = 0; u < 4; u++) asm volatile("" : "+v"(acc[u]));
+            for (int u = 0; u < 4; u++) asm volatile("" : "+v"(cacc[u]));
         } else {
-            // e[t] = 2^-(E+8) of row 4t + kq (the digit pairs below carry 2^8)
-            float e[2];
-#pragma unroll
-            for (int t = 0; t < 2; t++) e[t] = gs[4 * t + kq].x;
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 i32x4 c[2];
@@ -537,35 +575,61 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
 #pragma unroll
                     for (int t = 0; t < 2; t++) c[t] = mfma_i8(av[bb][t], bq, bb == 0 ? i32x4{0, 0, 0, 0} : c[t]);
                 }
-                // digit products (|c| < 2^18, digit 3 most significant) in two exact integer
+                // digit products (|c| < 2^21, digit 3 most significant) in two exact integer
                 // pairs: 2^8 * sum_d c_d 2^(8d-24) = (c0 + 2^8 c1) 2^-16 + (c2 + 2^8 c3)
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     const int lo2 = c[t][0] + c[t][1] * 256;
                     const int hi2 = c[t][2] + c[t][3] * 256;
                     const float v = fmaf((float)lo2, 0x1p-16f, (float)hi2);
-                    acc[u][t] = fmaf(s[u] * e[t], v, acc[u][t]);
+                    cacc[u][t] = fmaf((float)s[u], v, cacc[u][t]);
                 }
             }
             // keep this job's epilogue here: without a use, the compiler sinks every job's
             // epilogue to the end of the chunk and keeps all four jobs' MFMA results live
 #pragma unroll
-            for (int u = 0; u < 4; u++) asm volatile("" : "+v"(acc[u]));
+            for (int u = 0; u < 4; u++) asm volatile("" : "+v"(cacc[u]));
         }
     };
 
-    // the zero-point term of a chunk: rows i, columns 4j + u: sum over its 4 groups g of
-    // sum_x[g][i] * (-s z)[g][col] (lane (kq, i) holds A = sum_x of group kq, row i; lane (kq, j)
-    // holds B = -s z of group kq, its column of quarter u). The MFMA starts from zero and its
-    // result is added with ordinary adds: its internal sum is not one IEEE rounding, and fed the
-    // running sum as C it lost up to 2.8e-5 over the 148 groups of a 7B down projection.
-    auto zero_term = [&](int buf) {
-        const float sx = gst(buf)[kq * 16 + j].y;
+    // The zero-point term of a chunk: rows i, columns 4j + u: sum over its 4 groups g of
+    // sum_even[g][i] (-s (z+1))[g][col] + sum_odd[g][i] (-s (z-7))[g][col] (lane (kq, i) holds
+    // A = the sums of group kq, row i; lane (kq, j) holds B of group kq, its column of quarter u).
+    // L = 1: A in the chunk's exponent units, and the MFMAs start the chunk's sums (their
+    // internal sum is not one IEEE rounding, so they never take a running sum as C: fed acc, they
+    // lost up to 2.8e-5 over the 148 groups of a 7B down projection). L = 0: in the MFMA layout,
+    // added to zacc; the chunk's sums start from zero.
+    auto chunk_begin = [&](int buf) {
+        const float2 sx = gst(buf)[kq * 16 + j];
+        if constexpr (L == 1) {
+            const float xi = gex(buf)[16 + j];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const f32x4 z = mfma_f32_4(sx, nsz[u], f32x4{0.f, 0.f, 0.f, 0.f});
-            if constexpr (L == 1) acc[u] += z;
-            else zacc[u] += z;
+            for (int u = 0; u < 4; u++)
+                cacc[u] = mfma_f32_4(sx.y * xi, nsz2[u], mfma_f32_4(sx.x * xi, nsz[u], f32x4{0.f, 0.f, 0.f, 0.f}));
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                cacc[u] = Acc{};
+                zacc[u] += mfma_f32_4(sx.y, nsz2[u], mfma_f32_4(sx.x, nsz[u], f32x4{0.f, 0.f, 0.f, 0.f}));
+            }
+        }
+    };
+    // the chunk's sums into acc: times 2^-(E+8) of the row (L = 1: rows 4kq + r; L = 0: 4t + kq)
+    auto chunk_end = [&](int buf) {
+        const float* const ex = gex(buf);
+        if constexpr (L == 1) {
+            const f32x4 e = *reinterpret_cast<const f32x4*>(ex + 4 * kq);
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[u][r] = fmaf(e[r], cacc[u][r], acc[u][r]);
+        } else {
+            const float e0 = ex[kq], e1 = ex[4 + kq];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                acc[u][0] = fmaf(e0, cacc[u][0], acc[u][0]);
+                acc[u][1] = fmaf(e1, cacc[u][1], acc[u][1]);
+            }
         }
     };
 
@@ -592,13 +656,14 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
         const int nch = t.ch0 + t.chunks;   // end of the task's chunks
         for (int ch = t.ch0; ch < nch; ch++) {
             stage_issue(sg);                 // past the last chunk: repeats it (never finished)
+            chunk_begin(buf);
 #pragma unroll
             for (int gg = 0; gg < kCG; gg++) {
                 consume(gg % P, buf, gg);
                 fetch(gg % P, fc);
                 advance(fc);
             }
-            zero_term(buf);
+            chunk_end(buf);
             if (ch + 1 == nch) {
                 // a whole task's outputs with the bias, or a K part's sums into its partial block
                 const bool whole = t.parts <= 1;
