@@ -36,6 +36,9 @@ namespace {
 #ifndef QL_GEMM_DEPTH
 #define QL_GEMM_DEPTH 8
 #endif
+#ifndef QL_GEMM_DEPTH_F32
+#define QL_GEMM_DEPTH_F32 (QL_GEMM_DEPTH / 2)
+#endif
 #ifndef QL_GEMM_TARGET_WGS
 #define QL_GEMM_TARGET_WGS 1
 #endif
@@ -277,10 +280,19 @@ void gemm_kernel(const GemmBatch b)
     // one K step: this step's activations into LDS buffer d & 1 (its last readers finished
     // before the previous step's barrier), then 4 x MT MFMAs
     auto step = [&](int d) {
-        // pin the raw activations here: otherwise the f32 -> f16 conversion is hoisted next to
-        // the loads, which then have to complete at once
+        // pin the raw activations and packed words here: otherwise the f32 -> f16 conversion
+        // and the dequantization of all D steps are hoisted to the top of the ring's round,
+        // whose first wait then drains every load in flight (vmcnt(0) once per D steps)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int a = 0; a < AC * AV; a++) pin(xa[d][a]);
+        pin(wq[d]);
+        {
+            uint32_t s0 = sv[d].x, s1 = sv[d].y, z0 = zv[d];
+            asm volatile("" : "+v"(s0), "+v"(s1), "+v"(z0));
+            sv[d] = u32x2{s0, s1};
+            zv[d] = z0;
+        }
 #pragma unroll
         for (int a = 0; a < AC; a++)
             As[d & 1][akb[a]][arow[a]] = XF32 ? perm_f32(xa[d][2 * a], xa[d][2 * a + 1]) : perm_f16(xa[d][a]);
@@ -466,8 +478,8 @@ void gemm_chunk_kernel(const GemmBatch b)
 template <int BM, bool XF32>
 hipError_t launch_bm(const GemmBatch& b, hipStream_t stream)
 {
-    // f32 activations take twice the registers per step: half the depth
-    constexpr int D = XF32 ? QL_GEMM_DEPTH / 2 : QL_GEMM_DEPTH;
+    // f32 activations take twice the registers per step
+    constexpr int D = XF32 ? QL_GEMM_DEPTH_F32 : QL_GEMM_DEPTH;
     hipLaunchKernelGGL((gemm_kernel<BM, XF32, D>), dim3(b.wg_total), dim3(256), 0, stream, b);
     return hipGetLastError();
 }
