@@ -698,6 +698,11 @@ static void plan_strips_base(const std::vector<SeqSpec>& lin, int M, int grid, i
     if (two.busiest_units < out->busiest_units) *out = two;
 }
 
+// jobs in flight per wave of the no-padding kernel over whole-K strips (2 or 4)
+#ifndef QL_WIDE_RING
+#define QL_WIDE_RING 2
+#endif
+
 // The plan, then the no-padding kernel where it applies (QL_STRIP_WIDE=0 in the environment
 // keeps strip_kernel, for comparisons).
 static void plan_strips_final(const std::vector<SeqSpec>& lin, int M, int grid, int force_stream, StripPlan* out)
@@ -719,6 +724,7 @@ static void plan_strips_final(const std::vector<SeqSpec>& lin, int M, int grid, 
         for (const StripTask& t : out->tasks) whole = whole && t.nblk == kMaxStripBlocks;
         if (whole) {
             out->wide = true;
+            out->ring = QL_WIDE_RING;
             out->lds_bytes = strip_wide_lds(M);
         } else {
             plan_strips_base(lin, M, grid, force_stream, out);
