@@ -574,6 +574,59 @@ def traffic_from_profiles(workload: str):
     return json.load(open(p)).get(workload)
 
 
+def blas_reference(steps: int) -> dict:
+    """hipBLASLt's fp16 GEMM (torch.matmul, fp32 accumulation) on the 0.5B prefill shapes, beside
+    prefill_kernel: the 168 linears at M = 128 and 512 as dense fp16 weights (one library call
+    each, graph-replayed; the library's rate per call on these shapes) and one 8192^3 GEMM (what
+    it reaches where the shape is easy). A reference point for the MFMA fraction only: nothing
+    here runs on the int4 path."""
+    import torch
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    shapes = [(K, N) for (_, _, K, N) in synth.model_linears("0.5b")[:7]]
+    out = {}
+    for M in (128, 512):
+        xs = {K: torch.randn(M, K, device=dev, dtype=torch.float16) for K in {k for k, _ in shapes}}
+        ws = [torch.randn(N, K, device=dev, dtype=torch.float16) * 0.02 for K, N in shapes]
+        ys = [torch.empty(M, N, device=dev, dtype=torch.float16) for K, N in shapes]
+
+        def layer():
+            for (K, N), w, y in zip(shapes, ws, ys):
+                torch.matmul(xs[K], w.t(), out=y)
+        layer()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(24):
+                layer()
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) / steps * 1e6
+        flops = 24 * sum(2 * M * K * N for K, N in shapes)
+        out[f"{M}_step"] = {"us": round(us, 1), "tflops": round(flops / us / 1e6, 1),
+                            "frac": round(flops / us / 1e6 / F16_PEAK_TFLOPS, 4), "calls": 168}
+    a = torch.randn(8192, 8192, device=dev, dtype=torch.float16)
+    b = torch.randn(8192, 8192, device=dev, dtype=torch.float16)
+    for _ in range(3):
+        a @ b
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        a @ b
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / 10 * 1e6
+    out["8192_cube"] = {"us": round(us, 1), "tflops": round(2 * 8192 ** 3 / us / 1e6, 1),
+                        "frac": round(2 * 8192 ** 3 / us / 1e6 / F16_PEAK_TFLOPS, 4)}
+    out["note"] = ("torch.matmul fp16 x fp16 -> fp16 (hipBLASLt), dense fp16 weights of the 0.5B shapes "
+                   "(not int4): the library's rate on the prefill step's GEMMs and on a large square one")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -581,7 +634,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
                     help="all | step05 | headline | step7b | north | sweep | prefill | prefill_one | unpack | lmhead | "
-                         "attn | elem | cpu "
+                         "attn | elem | cpu | blas "
                          "(subsets for profiling: headline = the 0.5B step and its MALL-flushed "
                          "timing only; north = the 7B-shaped step at M=1 only)")
     ap.add_argument("--m7b", default="1,2,4,8,16", help="decode batch sizes for the 7B-shaped step")
@@ -598,6 +651,10 @@ def main():
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus "
               f"{args.gpus}. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.only == "blas":
+        print(json.dumps({"partial": "blas", "extra": {"blas_f16": blas_reference(max(10, args.steps))}}))
+        return
 
     ctx = ql.Context(0)
     info = ctx.info()
