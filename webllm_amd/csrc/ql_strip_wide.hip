@@ -165,11 +165,15 @@ __device__ __forceinline__ int chunk_exponent(const float v[8])
 }
 
 // Digits of one 8-k piece owned by one of 16 consecutive lanes (one DPP row) that hold one
-// (group, row): writes its 16-byte-row halves (k order {0,2,4,6,1,3,5,7}) for each of the four
-// digits, rows digit_stride_u2 uint2 apart, and returns the group's {sum x over even k, over odd
-// k}. Even k: digits of round(x 2^(E+24)) (the weight operand is the nibble n); odd k: of
-// round(x 2^(E+20)) (the weight operand is 16 (n - 8)), so both products carry 2^(E+24).
-__device__ __forceinline__ float2 stage_piece(const float v[8], uint2* row0, int digit_stride_u2, int E)
+// (group, row): for each of the four digits, its 16-byte-row halves (k order {0,2,4,6,1,3,5,7}) in
+// row[d], and the group's {sum x over even k, over odd k} in sums. Even k: digits of
+// round(x 2^(E+24)) (the weight operand is the nibble n); odd k: of round(x 2^(E+20)) (the weight
+// operand is 16 (n - 8)), so both products carry 2^(E+24).
+struct PieceDigits {
+    uint2 row[4];
+    float2 sums;
+};
+__device__ __forceinline__ PieceDigits piece_digits(const float v[8], int E)
 {
     float se = (v[0] + v[2]) + (v[4] + v[6]);
     float so = (v[1] + v[3]) + (v[5] + v[7]);
@@ -181,9 +185,27 @@ __device__ __forceinline__ float2 stage_piece(const float v[8], uint2* row0, int
                    digits4_of(v[6], scale), ev);
     byte_transpose(digits4_of(v[1], sodd), digits4_of(v[3], sodd), digits4_of(v[5], sodd),
                    digits4_of(v[7], sodd), od);
+    PieceDigits p;
 #pragma unroll
-    for (int i = 0; i < 4; i++) row0[i * digit_stride_u2] = uint2{ev[i], od[i]};
-    return float2{se, so};
+    for (int i = 0; i < 4; i++) p.row[i] = uint2{ev[i], od[i]};
+    p.sums = float2{se, so};
+    return p;
+}
+
+// Where digit d of piece c (k 8c .. 8c+7 of local group gg) of row m lies in a chunk buffer: 64-k
+// block c / 8, lane group (c % 8) / 2 of its B operand, 8-byte half c % 2 of a 16-byte row; L = 1
+// tile d, row m; L = 0 tile m / 4, row 4 (m % 4) + d. swz: the row index xor-ed with
+// swz_of(kq, bb, gg) (the digits launch's LDS staging, so that the 64 lanes of a wave, one row's
+// pieces, write distinct banks), or not (swz = false: the strips' own staging).
+__device__ __forceinline__ int swz_of(int kq, int bb, int gg) { return kq + 4 * bb + 8 * (gg & 1); }
+template <typename Lay, int L>
+__device__ __forceinline__ int digit_offset(int gg, int c, int m, int d, bool swz)
+{
+    const int bb = c >> 3, kq = (c & 7) >> 1;
+    const int tile = L == 0 ? m >> 2 : d;
+    int row = L == 0 ? 4 * (m & 3) + d : m;
+    if (swz) row ^= swz_of(kq, bb, gg);
+    return gg * Lay::kGB + bb * Lay::kBbB + kq * Lay::kKqB + tile * Lay::kTileB + row * 16 + (c & 1) * 8;
 }
 
 // The activation digits of one chunk of one linear (workgroup j: image j), laid out as
@@ -231,13 +253,12 @@ __global__ __launch_bounds__(kThreads) void wide_digits_kernel(const StripArgs a
 #pragma unroll
                 for (int q = 0; q < 8; q++) v[q] = (float)hv[q];
             }
-            // piece c covers k 8c .. 8c+7 of the group: 64-k block c / 8, lane group
-            // (c % 8) / 2 of its B operand, 8-byte half c % 2 of the 16-byte row
-            const int row = L == 0 ? (m >> 2) * 16 + 4 * (m & 3) : m;
-            char* const r0 = lds + gg * Lay::kGB + (c >> 3) * Lay::kBbB + ((c & 7) >> 1) * Lay::kKqB + row * 16 + (c & 1) * 8;
             const int E = chunk_exponent(v);
-            const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8, E);
-            if (c == 0) gs[gg * 16 + m] = s2;
+            const PieceDigits pd = piece_digits(v, E);
+#pragma unroll
+            for (int d = 0; d < 4; d++)
+                *reinterpret_cast<uint2*>(lds + digit_offset<Lay, L>(gg, c, m, d, true)) = pd.row[d];
+            if (c == 0) gs[gg * 16 + m] = pd.sums;
             if ((idx & 63) == 0) {
                 ex[m] = ldexpf(1.f, -E - 8);
                 ex[16 + m] = ldexpf(1.f, E + 8);
@@ -245,9 +266,18 @@ __global__ __launch_bounds__(kThreads) void wide_digits_kernel(const StripArgs a
         }
     }
     __syncthreads();
+    // out in the strips' layout: 16-byte unit u of the digits is (group, block, lane group, tile,
+    // row) with the row fastest; its LDS copy sits at the swizzled row
     char* const dst = a.dimg + (size_t)j * Lay::kBufB;
-    for (int o = threadIdx.x * 16; o < Lay::kBufB; o += kThreads * 16)
-        st_global(reinterpret_cast<u32x4*>(dst + o), *reinterpret_cast<const u32x4*>(lds + o));
+    for (int o = threadIdx.x * 16; o < Lay::kBufB; o += kThreads * 16) {
+        int src = o;
+        if (o < Lay::kDigB) {
+            const int u = o >> 4;
+            const int rest = (u >> 4) / Lay::kTiles;       // (group, block, lane group)
+            src = o ^ (swz_of(rest & 3, (rest >> 2) & 1, rest >> 3) << 4);
+        }
+        st_global(reinterpret_cast<u32x4*>(dst + o), *reinterpret_cast<const u32x4*>(lds + src));
+    }
 }
 
 // Waves per SIMD the M 5..8 instance is compiled for. At 4 it fits 128 VGPRs (some spilled) and
@@ -421,13 +451,12 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
 #pragma unroll
                         for (int q = 0; q < 8; q++) v[q] = v[q] * w2[q];
                     }
-                    // piece c covers k 8c .. 8c+7 of the group: 64-k block c / 8, lane group
-                    // (c % 8) / 2 of its B operand, 8-byte half c % 2 of the 16-byte row
-                    const int row = L == 0 ? (m >> 2) * 16 + 4 * (m & 3) : m;
-                    char* const r0 = dig + gg * Lay::kGB + (c >> 3) * Lay::kBbB + ((c & 7) >> 1) * Lay::kKqB + row * 16 + (c & 1) * 8;
                     const int E = chunk_exponent(v);
-                    const float2 s2 = stage_piece(v, reinterpret_cast<uint2*>(r0), L == 0 ? 2 : Lay::kTileB / 8, E);
-                    if (c == 0) gs[gg * 16 + m] = s2;
+                    const PieceDigits pd = piece_digits(v, E);
+#pragma unroll
+                    for (int d = 0; d < 4; d++)
+                        *reinterpret_cast<uint2*>(dig + digit_offset<Lay, L>(gg, c, m, d, false)) = pd.row[d];
+                    if (c == 0) gs[gg * 16 + m] = pd.sums;
                     if ((idx & 63) == 0) {
                         ex[m] = ldexpf(1.f, -E - 8);
                         ex[16 + m] = ldexpf(1.f, E + 8);
