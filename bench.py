@@ -1012,6 +1012,16 @@ def main():
         log(f"7B step: {s7}")
         m7.arena.release()
 
+    # the per-linear launches carry no elementwise work, the chained steps carry it inside their
+    # launch: add the measured elementwise launches per step for the like-for-like figure
+    if "elem" in extra:
+        pl = extra.get("step05_m1_per_linear_launches")
+        if pl:
+            pl["plus_elem_us"] = round(pl["us"] + extra["elem"]["05b"]["us_per_step"], 1)
+        pl = extra.get("step7b", {}).get("1_per_linear_launches")
+        if pl:
+            pl["plus_elem_us"] = round(pl["us"] + extra["elem"]["7b"]["us_per_step"], 1)
+
     if args.calib_copy:
         flush = ctx.arena(1 << 30)
         ctx.copy(flush, 0, flush, 1 << 29, 1 << 29)
