@@ -1976,7 +1976,7 @@ int ql_attention_decode(ql_ctx* ctx, ql_arena* act, uint64_t q_off, const ql_are
     a.G = n_head / n_kv_head;
     a.D = D;
     a.past = past_len;
-    a.scale = (float)(1.0 / std::sqrt((double)D));
+    a.scale = (float)(1.4426950408889634 / std::sqrt((double)D));   // log2(e) / sqrt(D): scores in base-2 units
     if (ql::plan_attention(&a)) return fail(QL_E_INVALID, "attention shape does not fit the workspace");
     QL_HIP(ql::launch_attention(a, ctx->stream));
     return QL_OK;

@@ -40,6 +40,25 @@ constexpr int kAttnMinBlocks = 256;      // fewer workgroups: give up sharing K/
 constexpr int kAttnMaxSplit = 128;      // key splits at most (the merge takes up to 256)
 constexpr int kKB = 4;                   // wave steps (4 keys each) whose K and V rows a lane holds
 
+// Scores are kept in base-2 units (the host folds log2(e) into the 1/sqrt(D) scale), so every
+// exponential is the hardware exp2 (v_exp_f32, about 1 ulp) instead of a library expf.
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Sum over the 16 lanes of a DPP row: row_ror:8, row_ror:4, quad_perm [2,3,0,1], [1,0,3,2]. Each
+// step adds a pair that commutes, so every lane ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += dpp_f<0x128>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x4E>(v);
+    return v + dpp_f<0xB1>(v);
+}
+
 // online-softmax state (m, l, acc) merged with another: the larger max wins, both sides rescaled;
 // a side without keys (m = -inf) contributes nothing
 template <int NJ>
@@ -47,8 +66,8 @@ __device__ __forceinline__ void merge_state(float& m, float& l, f32x4 (&acc)[NJ]
                                             const f32x4 (&ao)[NJ])
 {
     const float mn = fmaxf(m, mo);
-    const float sa = m == -INFINITY ? 0.f : expf(m - mn);
-    const float sb = mo == -INFINITY ? 0.f : expf(mo - mn);
+    const float sa = m == -INFINITY ? 0.f : ex2(m - mn);
+    const float sb = mo == -INFINITY ? 0.f : ex2(mo - mn);
     l = l * sa + lo * sb;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
@@ -123,10 +142,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a)
                     dot = fmaf(qv[g][j].z, kr[u][j].z, dot);
                     dot = fmaf(qv[g][j].w, kr[u][j].w, dot);
                 }
-                dot += __shfl_xor(dot, 8);
-                dot += __shfl_xor(dot, 4);
-                dot += __shfl_xor(dot, 2);
-                dot += __shfl_xor(dot, 1);
+                dot = row16_sum(dot);
                 sc[u] = i0 + 16 * u + wave * 4 + kq < n ? dot * a.scale : -INFINITY;
             }
             float bm = sc[0];
@@ -134,7 +150,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a)
             for (int u = 1; u < kKB; u++) bm = fmaxf(bm, sc[u]);
             const float mn = fmaxf(mr[g], bm);
             if (mn == -INFINITY) continue;                          // no key of this lane yet
-            const float r = expf(mr[g] - mn);                       // 0 while the state is empty
+            const float r = ex2(mr[g] - mn);                        // 0 while the state is empty
             lr[g] *= r;
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
@@ -145,7 +161,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a)
             }
 #pragma unroll
             for (int u = 0; u < kKB; u++) {
-                const float p = expf(sc[u] - mn);                   // 0 past the split's keys
+                const float p = ex2(sc[u] - mn);                    // 0 past the split's keys
                 lr[g] += p;
 #pragma unroll
                 for (int j = 0; j < NJ; j++) {
@@ -246,7 +262,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a)
         float e[4], l = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            e[r] = mi[r] != -INFINITY ? expf(mi[r] - mx) : 0.f;
+            e[r] = mi[r] != -INFINITY ? ex2(mi[r] - mx) : 0.f;
             l += li[r] * e[r];
         }
 #pragma unroll

@@ -197,7 +197,7 @@ struct AttnArgs {
     float* out;                // [M, H, D]
     float* ws;                 // key-split partials: [M, H, nsplit, D] sums, then [.., 2] max/sum
     int M, H, KV, G, D, past;
-    float scale;               // fp32(1 / sqrt(D))
+    float scale;               // fp32(log2(e) / sqrt(D)): scores in base-2 units for exp2
     // plan_attention fills these
     int gm, nj;                // kernel variant: heads per run (template), 64-float pieces of D
     int heads_per_run, runs_per_group, nsplit, chunk_cap;
