@@ -321,6 +321,7 @@ AttnFn attn_fn_nj(int gm)
     case 1: return attn_kernel<1, NJ>;
     case 2: return attn_kernel<2, NJ>;
     case 4: return attn_kernel<4, NJ>;
+    case 7: return NJ <= 2 ? attn_kernel<7, NJ <= 2 ? NJ : 2> : nullptr;
     default: return NJ <= 2 ? attn_kernel<8, NJ <= 2 ? NJ : 2> : nullptr;
     }
 }
@@ -340,7 +341,7 @@ size_t attn_lds_bytes(int gm, int cap, int D)
 
 }  // namespace
 
-// Heads per run (GM: 1, 2, 4 or 8, at most 16 f32x4 of query registers), key splits (enough
+// Heads per run (GM: 1, 2, 4, 7 or 8, at most 16 f32x4 of query registers), key splits (enough
 // workgroups, workspace within its capacity) and the LDS size. Runs of several
 // heads read each K/V row once for all of them; while the grid would still be short of
 // kAttnMinBlocks workgroups, fewer heads per run buy parallelism (the rows then come from L2).
@@ -366,7 +367,8 @@ int plan_attention(AttnArgs* a)
         const bool few = (long long)runs * a->M * ns < kAttnMinBlocks && gm > 1;
         if (!few && (ns == 1 || ws2 <= kAttnWsBytes)) {
             a->heads_per_run = hpr;
-            a->gm = gm;
+            // seven heads per kv head (Qwen2.5-7B, 28 / 4): an instance without a padding head
+            a->gm = gm == 8 && hpr == 7 ? 7 : gm;
             a->runs_per_group = (a->G + hpr - 1) / hpr;
             a->nsplit = ns;
             a->chunk_cap = ((tcap + ns - 1) / ns + 3) & ~3;
