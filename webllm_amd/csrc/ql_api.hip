@@ -1072,6 +1072,11 @@ int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, ui
                ql::GemmLinear* out, bool no_split);
 
 // ---- chained prefill (M > 16): one GEMM launch per pass ----
+
+// K segments from which a chained prefill pass's linear leaves its sums to a part-sum launch
+#ifndef QL_GEMM_DEFER_SPLIT
+#define QL_GEMM_DEFER_SPLIT 2
+#endif
 //
 // The model's dependency order at M > 16 (runForward(M = T) calls each layer's linears in turn):
 // each pass (the linears whose producers all ran in earlier passes) is one GEMM launch over the
@@ -1099,6 +1104,7 @@ struct PrefillPasses {
     std::vector<ql::PrefillPlan> plans;
     std::vector<char> chunked;                   // per pass: the chunked split-K GEMM
     std::vector<int> chunk_tiles;                // per chunked pass: its output tiles
+    std::vector<char> deferred;                  // per chunked pass: a part-sum launch follows it
     uint64_t input_bytes = 0;
     uint64_t partial_bytes = 0;                  // the chunked passes' partial sums, reused in turn
     int counters = 0;                            // their arrival counters (self-clearing)
@@ -1149,6 +1155,7 @@ void plan_prefill_passes(const std::vector<ql::SeqSpec>& specs, const ql_seq_fus
     P->plans.assign(P->depth, ql::PrefillPlan{});
     P->chunked.assign(P->depth, 0);
     P->chunk_tiles.assign(P->depth, 0);
+    P->deferred.assign(P->depth, 0);
     for (int p = 0; p < P->depth; p++) {
         std::vector<ql::SeqSpec> sub;
         for (int i : P->members[p]) sub.push_back(specs[i]);
@@ -1176,6 +1183,10 @@ void plan_prefill_passes(const std::vector<ql::SeqSpec>& specs, const ql_seq_fus
             }
             P->partial_bytes = std::max(P->partial_bytes, part);
             P->counters = std::max(P->counters, ctr);
+            // the split the pass's launch uses (none when its tiles alone fill the device)
+            if (P->chunk_tiles[p] * 2 < ql::kPlanCUs)
+                for (const ql::SeqSpec& sp : sub)
+                    if (ql::gemm_shape(M, sp.N, sp.K, sp.group, ql::kPlanCUs).split >= QL_GEMM_DEFER_SPLIT) P->deferred[p] = 1;
         } else {
             ql::plan_prefill(prefill_specs(sub), M, grid, &P->plans[p]);
         }
@@ -1201,6 +1212,7 @@ void fill_prefill_passes_info(const PrefillPasses& P, int n, uint64_t bytes, ql_
     for (int p = 0; p < P.depth; p++) {
         info->variant += P.chunked[p];              // passes on the chunked split-K GEMM
         info->tiles += P.chunk_tiles[p];
+        info->launches += P.deferred[p];            // their part-sum launches
     }
 }
 
@@ -1308,7 +1320,41 @@ int prefill_passes_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, con
                 wg += L.tiles_n * L.tiles_m * L.split;
             }
             b.wg_total = wg;
+            // linears split into many K segments leave their sums to a part-sum launch: one
+            // workgroup per tile adding every segment alone takes a round trip per two segments
+            std::vector<ql::PartSum> sums;
+            int max_n = 0;
+            for (size_t k = 0; k < mem.size(); k++) {
+                ql::GemmLinear& L = b.L[k];
+                if (L.split < QL_GEMM_DEFER_SPLIT) continue;
+                L.defer = 1;
+                ql::PartSum e{};
+                e.part0 = L.partial;
+                e.bias = L.bias;
+                e.res = L.res;
+                e.y = L.y;
+                e.parts = L.split;
+                e.N = L.N;
+                e.K = L.K;
+                max_n = std::max(max_n, e.N);
+                sums.push_back(e);
+            }
             q->steps.push_back(st);
+            if (sums.empty() != !P.deferred[p]) return cleanup(fail(QL_E_STATE, "chained prefill: part-sum plan mismatch"));
+            if (!sums.empty()) {
+                char* tab = nullptr;
+                hipError_t e = hipMalloc(&tab, sizeof(ql::PartSum) * sums.size());
+                if (e == hipSuccess) q->bufs.push_back(tab);
+                if (e == hipSuccess) e = hipMemcpy(tab, sums.data(), sizeof(ql::PartSum) * sums.size(), hipMemcpyHostToDevice);
+                if (e != hipSuccess) return cleanup(hip_fail(e, "ql_seq_create part sums"));
+                SeqStep ps{};
+                ps.kind = SeqStep::kPartSums;
+                ps.sums = reinterpret_cast<const ql::PartSum*>(tab);
+                ps.count = (int)sums.size();
+                ps.M = M;
+                ps.max_n = max_n;
+                q->steps.push_back(ps);
+            }
             continue;
         }
         // the pass's prefill launch
@@ -1646,6 +1692,7 @@ int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, ui
     if (no_split) s.split = 1;
     const ql::GemvLinear g = make_linear(d, weights);
     ql::GemmLinear& L = *out;
+    L.defer = 0;
     L.qweight = g.qweight;
     L.qzeros = g.qzeros;
     L.scales = g.scales;

@@ -130,6 +130,7 @@ __device__ __forceinline__ void gemm_store(const GemmLinear& L, int M, int m0, i
                         ((uint32_t)m * (uint32_t)N + (uint32_t)ncol) * 4u, seg * plane, kSC1);
             }
     }
+    if (L.defer) return;   // a part-sum launch adds the segments
     // this wave's partial stores are complete before the workgroup signals arrival
     __builtin_amdgcn_s_waitcnt(0);
     __shared__ uint32_t is_last;

@@ -73,6 +73,7 @@ struct GemmLinear {
     uint32_t* counters;        // per-tile arrival counters (split > 1), zero between launches
     const float* res;          // [M, N] added at the store, or nullptr
     int N, K, group, split, tiles_n, tiles_m, wg_begin;
+    int defer;                 // split > 1: store the partial sums only (a part-sum launch adds them)
 };
 struct GemmBatch {
     GemmLinear L[kMaxBatch];
