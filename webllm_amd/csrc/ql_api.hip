@@ -1714,6 +1714,34 @@ int gemm_entry(const ql_gptq_desc* d, const ql_arena* weights, ql_arena* act, ui
     return QL_OK;
 }
 
+// The batch's GEMM launch, then, for its linears split along K, one part-sum launch that adds
+// their segments (ascending order within each lane, bias, residual) where the last workgroup of
+// each tile would add them alone (a round trip per two segments).
+hipError_t launch_gemm_parts(ql::GemmBatch& b, hipStream_t stream)
+{
+    ql::PartSumArgs ps{};
+    ps.M = b.M;
+    int max_n = 0;
+    for (int i = 0; i < b.count; i++) {
+        ql::GemmLinear& L = b.L[i];
+        if (L.split < QL_GEMM_DEFER_SPLIT) continue;
+        L.defer = 1;
+        ql::PartSum& e = ps.e[ps.count++];
+        e = ql::PartSum{};
+        e.part0 = L.partial;
+        e.bias = L.bias;
+        e.res = L.res;
+        e.y = L.y;
+        e.parts = L.split;
+        e.N = L.N;
+        e.K = L.K;
+        max_n = std::max(max_n, L.N);
+    }
+    hipError_t e = ql::launch_gemm_batch(b, stream);
+    if (e == hipSuccess) e = ql::launch_part_sums_args(ps, max_n, stream);
+    return e;
+}
+
 }  // namespace
 
 namespace {
@@ -1815,7 +1843,7 @@ int linear_impl(ql_ctx* ctx, const ql_gptq_desc* d, const ql_arena* weights, ql_
         b.x_dtype = x_dtype;
         b.bm = ql::gemm_shape(M, d->N, d->K, d->group, ql::kPlanCUs).bm;
         b.wg_total = b.L[0].tiles_n * b.L[0].tiles_m * b.L[0].split;
-        QL_HIP(ql::launch_gemm_batch(b, ctx->stream));
+        QL_HIP(launch_gemm_parts(b, ctx->stream));
         return QL_OK;
     }
     ql::GemmArgs g;
@@ -2159,7 +2187,7 @@ int ql_linear_batch(ql_ctx* ctx, int32_t count, const ql_gptq_desc* descs,
             wg += L.tiles_n * L.tiles_m * L.split;
         }
         b.wg_total = wg;
-        QL_HIP(ql::launch_gemm_batch(b, ctx->stream));
+        QL_HIP(launch_gemm_parts(b, ctx->stream));
         return QL_OK;
     }
     if (!fused) {

@@ -415,6 +415,11 @@ struct PartSum {
     int32_t parts, N, K;       // N % 256 == 0 when ssq is set, K % 256 == 0 when in_ssq is
 };
 hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, hipStream_t stream);
+struct PartSumArgs {
+    PartSum e[kMaxBatch];
+    int count, M;
+};
+hipError_t launch_part_sums_args(const PartSumArgs& a, int max_n, hipStream_t stream);
 
 struct StripPlan {
     int grid = 0, strips = 0, split = 1;

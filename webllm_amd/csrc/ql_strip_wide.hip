@@ -753,10 +753,9 @@ __global__ __launch_bounds__(kThreads, L == 0 ? QL_WIDE_OCC0 : 2) void strip_wid
 // row's 1 / rms before bias and residual. With ssq set (N % 256 == 0: a workgroup's 64 quads are
 // 256 columns of one row), the workgroup also writes the sum of squares of its 256 outputs, in a
 // fixed order, for a consumer that RMSNorms y.
-__global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, int M)
+__device__ __forceinline__ void part_sum_entry(const PartSum& e, int M)
 {
     __shared__ float red[4];
-    const PartSum e = entries[blockIdx.y];
     const int n4 = e.N / 4;
     const int i = (int)(blockIdx.x * 256 + threadIdx.x) >> 2;   // 4-value group over [M][N]
     const int r = threadIdx.x & 3;
@@ -823,7 +822,26 @@ __global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, i
     }
 }
 
+__global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, int M)
+{
+    part_sum_entry(entries[blockIdx.y], M);
+}
+
+// the same with the entries in the kernel arguments (a batch of single-call linears)
+__global__ __launch_bounds__(256) void part_sum_args_kernel(const PartSumArgs a)
+{
+    part_sum_entry(a.e[blockIdx.y], a.M);
+}
+
 }  // namespace
+
+hipError_t launch_part_sums_args(const PartSumArgs& a, int max_n, hipStream_t stream)
+{
+    if (a.count < 1) return hipSuccess;
+    const int threads = a.M * (max_n / 4) * 4;
+    hipLaunchKernelGGL(part_sum_args_kernel, dim3((threads + 255) / 256, a.count), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, hipStream_t stream)
 {
