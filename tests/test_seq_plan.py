@@ -414,6 +414,22 @@ def test_fused_layers_plan_as_chained_tiles():
     assert ql.plan_seq(c2.descs, 1, c2.x, c2.y, 256, fuse=none).kernel == ql.SEQ_STRIPS
 
 
+@pytest.mark.parametrize("M", [128, 512])
+def test_fused_prefill_launches(M):
+    """The fused 0.5B layers at M > 16: per layer 4 GEMM passes and 2 RMSNorm launches, a
+    part-sum launch after each chunked pass, and a SiLU-mul launch only where gate and up do not
+    share one: at M = 128 the gate/up pass's part-sum launch writes silu(gate) * up (the down
+    linear's input) beside the two outputs; at M = 512 gate/up runs on the prefill kernel (no part
+    sums) and the SiLU-mul keeps its launch."""
+    c, fuse = fused_layers(Chain(M=M), 24)
+    info = ql.plan_seq(c.descs, M, c.x, c.y, 256, fuse=fuse)
+    assert info.kernel == ql.SEQ_PREFILL_PASSES and info.passes == 96 and info.linears == 168
+    if M == 128:
+        assert info.variant == 96 and info.launches == 24 * (4 + 2 + 4)
+    else:
+        assert info.variant == 72 and info.launches == 24 * (4 + 2 + 3 + 1)
+
+
 def test_fused_residual_counts_as_a_dependency():
     """A linear whose only link to an earlier one is its residual runs in a later pass."""
     c = Chain()
@@ -474,10 +490,13 @@ def test_chained_prefill_runs_pass_by_pass(M):
     through their outputs plan as one GEMM launch per pass, 96 passes for 24 layers: the prefill
     kernel for a pass whose 128 x 256 tiles reach 128 (gate/up at M = 512: 4 x 19 x 2), else the
     chunked GEMM with K split (variant counts those passes); fp16 x is refused for a chained
-    prefill (the producers' outputs are fp32); independent linears keep the one-launch prefill."""
+    prefill (the producers' outputs are fp32); independent linears keep the one-launch prefill.
+    Launches: one per pass plus a part-sum launch after each chunked pass with K split (every
+    chunked pass here: K = 896 splits 3 ways, K = 4864 19 ways)."""
     info = qwen_layers(Chain(M=M), 24).plan()
     assert info.kernel == ql.SEQ_PREFILL_PASSES and info.passes == 96 and info.linears == 168
     assert info.variant == (72 if M == 512 else 96)
+    assert info.launches == 96 + info.variant
     # output tiles: 256 columns by 64 rows on the chunked GEMM at these M, 128 rows on the prefill
     t64 = lambda N: -(-M // 64) * -(-N // 256)
     t128 = lambda N: -(-M // 128) * -(-N // 256)

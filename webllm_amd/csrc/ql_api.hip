@@ -47,6 +47,7 @@ struct SeqStep {
     enum Kind { kNorm, kGlu, kStrips, kPartSums, kPrefill, kGemm } kind;
     const ql::PartSum* sums = nullptr;   // kPartSums: the device table, count entries
     int count = 0, M = 0, max_n = 0;
+    bool glu = false;                    // kPartSums: SiLU-mul entries (part_sum_glu_kernel)
     ql::ElemArgs e{};
     const float* g = nullptr;
     const float* u = nullptr;
@@ -1105,6 +1106,8 @@ struct PrefillPasses {
     std::vector<char> chunked;                   // per pass: the chunked split-K GEMM
     std::vector<int> chunk_tiles;                // per chunked pass: its output tiles
     std::vector<char> deferred;                  // per chunked pass: a part-sum launch follows it
+    std::vector<char> folded;                    // per input: a SiLU-mul that its gate and up
+                                                 // linears' part-sum launch writes
     uint64_t input_bytes = 0;
     uint64_t partial_bytes = 0;                  // the chunked passes' partial sums, reused in turn
     int counters = 0;                            // their arrival counters (self-clearing)
@@ -1191,6 +1194,35 @@ void plan_prefill_passes(const std::vector<ql::SeqSpec>& specs, const ql_seq_fus
             ql::plan_prefill(prefill_specs(sub), M, grid, &P->plans[p]);
         }
     }
+    // a SiLU-mul of a gate and an up linear whose sums one part-sum launch adds (one pass, both
+    // split as many ways, one width, no residual on up) is written by that launch
+    P->folded.assign(P->inputs.size(), 0);
+    for (size_t k = 0; k < P->inputs.size(); k++) {
+        const PrefillPasses::Input& in = P->inputs[k];
+        const int g = in.x_src, u = in.x2_src;
+        if (!in.glu || g < 0 || u < 0 || P->pass[g] != P->pass[u] || !P->deferred[P->pass[g]]) continue;
+        const ql::SeqSpec& sg = specs[g];
+        const ql::SeqSpec& su = specs[u];
+        if (sg.N != in.K || su.N != in.K || (su.fuse & ql::kFuseRes)) continue;
+        const int split = ql::gemm_shape(M, sg.N, sg.K, sg.group, ql::kPlanCUs).split;
+        if (split < QL_GEMM_DEFER_SPLIT || ql::gemm_shape(M, su.N, su.K, su.group, ql::kPlanCUs).split != split)
+            continue;
+        P->folded[k] = 1;
+    }
+    // a part-sum launch adds SiLU-mul entries only or none: a pass with another linear that
+    // leaves its sums to the launch keeps its SiLU-muls as launches
+    for (int p = 0; p < P->depth; p++) {
+        std::vector<char> in_fold(n, 0);
+        for (size_t k = 0; k < P->inputs.size(); k++)
+            if (P->folded[k] && P->pass[P->inputs[k].x_src] == p) in_fold[P->inputs[k].x_src] = in_fold[P->inputs[k].x2_src] = 1;
+        bool all = true;
+        for (int i : P->members[p])
+            if (!in_fold[i] && ql::gemm_shape(M, specs[i].N, specs[i].K, specs[i].group, ql::kPlanCUs).split >= QL_GEMM_DEFER_SPLIT)
+                all = false;
+        if (!all)
+            for (size_t k = 0; k < P->inputs.size(); k++)
+                if (P->folded[k] && P->pass[P->inputs[k].x_src] == p) P->folded[k] = 0;
+    }
 }
 
 void fill_prefill_passes_info(const PrefillPasses& P, int n, uint64_t bytes, ql_seq_info* info)
@@ -1214,6 +1246,7 @@ void fill_prefill_passes_info(const PrefillPasses& P, int n, uint64_t bytes, ql_
         info->tiles += P.chunk_tiles[p];
         info->launches += P.deferred[p];            // their part-sum launches
     }
+    for (char f : P.folded) info->launches -= f;    // SiLU-muls written by those
 }
 
 uint64_t prefill_passes_bytes(const PrefillPasses& P)
@@ -1323,6 +1356,7 @@ int prefill_passes_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, con
             // linears split into many K segments leave their sums to a part-sum launch: one
             // workgroup per tile adding every segment alone takes a round trip per two segments
             std::vector<ql::PartSum> sums;
+            std::vector<int> sum_of(n, -1);
             int max_n = 0;
             for (size_t k = 0; k < mem.size(); k++) {
                 ql::GemmLinear& L = b.L[k];
@@ -1337,8 +1371,32 @@ int prefill_passes_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, con
                 e.N = L.N;
                 e.K = L.K;
                 max_n = std::max(max_n, e.N);
+                sum_of[mem[k]] = (int)sums.size();
                 sums.push_back(e);
             }
+            // SiLU-muls of this pass's gate and up linears: the gate's entry takes the up's
+            std::vector<char> drop(sums.size(), 0);
+            for (size_t k = 0; k < P.inputs.size(); k++) {
+                if (!P.folded[k] || P.pass[P.inputs[k].x_src] != p) continue;
+                const int ig = sum_of[P.inputs[k].x_src], iu = sum_of[P.inputs[k].x2_src];
+                if (ig < 0 || iu < 0 || drop[ig] || drop[iu] || sums[ig].yglu || sums[ig].parts != sums[iu].parts ||
+                    sums[ig].N != sums[iu].N || sums[iu].res)
+                    return cleanup(fail(QL_E_STATE, "chained prefill: SiLU-mul fold plan mismatch"));
+                ql::PartSum& e = sums[ig];
+                e.part0b = sums[iu].part0;
+                e.bias_b = sums[iu].bias;
+                e.yb = sums[iu].y;
+                e.yglu = reinterpret_cast<float*>(q->dev + P.inputs[k].buf_off);
+                drop[iu] = 1;
+                made[k] = true;
+            }
+            for (size_t k = sums.size(); k-- > 0;)
+                if (drop[k]) sums.erase(sums.begin() + k);
+            // a launch adds SiLU-mul entries only (their kernel) or none
+            int glu = 0;
+            for (const ql::PartSum& e : sums) glu += e.yglu != nullptr;
+            if (glu != 0 && glu != (int)sums.size())
+                return cleanup(fail(QL_E_STATE, "chained prefill: SiLU-mul fold plan mismatch"));
             q->steps.push_back(st);
             if (sums.empty() != !P.deferred[p]) return cleanup(fail(QL_E_STATE, "chained prefill: part-sum plan mismatch"));
             if (!sums.empty()) {
@@ -1353,6 +1411,7 @@ int prefill_passes_create(ql_ctx* ctx, int32_t n, const ql_gptq_desc* descs, con
                 ps.count = (int)sums.size();
                 ps.M = M;
                 ps.max_n = max_n;
+                ps.glu = glu != 0;
                 q->steps.push_back(ps);
             }
             continue;
@@ -2442,7 +2501,7 @@ int ql_seq_run(ql_ctx* ctx, ql_seq* seq)
             case SeqStep::kPrefill: QL_HIP(ql::launch_prefill(st.p, true, ctx->stream)); break;
             case SeqStep::kGemm: QL_HIP(ql::launch_gemm_batch(st.gb, ctx->stream)); break;
             case SeqStep::kStrips: QL_HIP(ql::launch_strips(st.s, st.lds, ctx->stream)); break;
-            case SeqStep::kPartSums: QL_HIP(ql::launch_part_sums(st.sums, st.count, st.M, st.max_n, ctx->stream)); break;
+            case SeqStep::kPartSums: QL_HIP(ql::launch_part_sums(st.sums, st.count, st.M, st.max_n, st.glu, ctx->stream)); break;
             }
         }
     } else if (seq->prefill) QL_HIP(ql::launch_prefill(seq->pargs, true, ctx->stream));

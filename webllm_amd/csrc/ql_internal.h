@@ -413,8 +413,15 @@ struct PartSum {
     const float* in_ssq;       // null, or the input's [M][K / 256] (its producer's ssq)
     float eps;
     int32_t parts, N, K;       // N % 256 == 0 when ssq is set, K % 256 == 0 when in_ssq is
+    // SiLU-mul of two linears of one pass (gate: this entry, up: the b fields, same N and
+    // parts), instead of a launch of its own: yb gets the up sums, yglu = silu(y) * yb (no ssq,
+    // no in_ssq)
+    const float* part0b;
+    const float* bias_b;
+    float* yb;
+    float* yglu;               // null: an ordinary entry (set in every entry of a glu launch)
 };
-hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, hipStream_t stream);
+hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, bool glu, hipStream_t stream);
 struct PartSumArgs {
     PartSum e[kMaxBatch];
     int count, M;

@@ -822,9 +822,90 @@ __device__ __forceinline__ void part_sum_entry(const PartSum& e, int M)
     }
 }
 
+// NP sums of as many parts each, lane r of a DPP quad adding parts p[j] + q * stride for
+// q = r, r + 4, ... in order (the loads of the NP sums in one loop, so that they go out together)
+// and the quad then combining them as (s0 + s1) + (s2 + s3) with quad_perm [1,0,3,2] then
+// [2,3,0,1]: every lane ends with the same bits, those of part_sum_entry's sums.
+template <int NP>
+__device__ __forceinline__ void quad_parts_sums(const float* const (&p)[NP], int parts, size_t stride, int r, f32x4 (&t)[NP])
+{
+    f32x4 v[NP];
+#pragma unroll
+    for (int j = 0; j < NP; j++) v[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int q = r;
+    for (; q + 12 < parts; q += 16) {
+        f32x4 a[NP][4];
+#pragma unroll
+        for (int j = 0; j < NP; j++)
+#pragma unroll
+            for (int h = 0; h < 4; h++) a[j][h] = ld_global(reinterpret_cast<const f32x4*>(p[j] + (size_t)(q + 4 * h) * stride));
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            v[j] += a[j][0];
+            v[j] += a[j][1];
+            v[j] += a[j][2];
+            v[j] += a[j][3];
+        }
+    }
+    for (; q < parts; q += 4) {
+        f32x4 a[NP];
+#pragma unroll
+        for (int j = 0; j < NP; j++) a[j] = ld_global(reinterpret_cast<const f32x4*>(p[j] + (size_t)q * stride));
+#pragma unroll
+        for (int j = 0; j < NP; j++) v[j] += a[j];
+    }
+#pragma unroll
+    for (int j = 0; j < NP; j++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float sk = v[j][k];
+            const float w = sk + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sk), 0xB1, 0xF, 0xF, false));
+            t[j][k] = w + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, w), 0x4E, 0xF, 0xF, false));
+        }
+}
+
+// silu(g) * u, as the SiLU-mul launch forms it (IEEE division, expf)
+__device__ __forceinline__ float silu_mul1(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+// An entry whose yglu is set: the gate linear's sums (+ bias, residual) into y, the up linear's
+// (the b fields: as many parts, + bias) into yb, and silu(y) * yb into yglu, in place of a
+// SiLU-mul launch of its own.
+__device__ __forceinline__ void part_sum_glu_entry(const PartSum& e, int M)
+{
+    const int n4 = e.N / 4;
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x) >> 2;
+    const int r = threadIdx.x & 3;
+    if (i >= M * n4) return;
+    const int m = i / n4, c = (i - m * n4) * 4;
+    const size_t stride = (size_t)M * e.N;
+    const size_t o = (size_t)m * e.N + c;
+    const f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 bv = e.bias ? ld_global(reinterpret_cast<const f32x4*>(e.bias + c)) : z;
+    const f32x4 rv = e.res ? ld_global(reinterpret_cast<const f32x4*>(e.res + o)) : z;
+    const f32x4 ubv = e.bias_b ? ld_global(reinterpret_cast<const f32x4*>(e.bias_b + c)) : z;
+    const float* const pp[2] = {e.part0 + o, e.part0b + o};
+    f32x4 tu[2];
+    quad_parts_sums<2>(pp, e.parts, stride, r, tu);
+    f32x4 t = tu[0], u = tu[1];
+    if (e.bias) t += bv;
+    if (e.res) t += rv;
+    if (e.bias_b) u += ubv;
+    if (r == 0) {
+        st_global(reinterpret_cast<f32x4*>(e.y + o), t);
+        st_global(reinterpret_cast<f32x4*>(e.yb + o), u);
+        st_global(reinterpret_cast<f32x4*>(e.yglu + o),
+                  f32x4{silu_mul1(t.x, u.x), silu_mul1(t.y, u.y), silu_mul1(t.z, u.z), silu_mul1(t.w, u.w)});
+    }
+}
+
 __global__ __launch_bounds__(256) void part_sum_kernel(const PartSum* entries, int M)
 {
     part_sum_entry(entries[blockIdx.y], M);
+}
+
+__global__ __launch_bounds__(256) void part_sum_glu_kernel(const PartSum* entries, int M)
+{
+    part_sum_glu_entry(entries[blockIdx.y], M);
 }
 
 // the same with the entries in the kernel arguments (a batch of single-call linears)
@@ -843,11 +924,14 @@ hipError_t launch_part_sums_args(const PartSumArgs& a, int max_n, hipStream_t st
     return hipGetLastError();
 }
 
-hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, hipStream_t stream)
+hipError_t launch_part_sums(const PartSum* entries_dev, int count, int M, int max_n, bool glu, hipStream_t stream)
 {
     if (count < 1) return hipSuccess;
     const int threads = M * (max_n / 4) * 4;
-    hipLaunchKernelGGL(part_sum_kernel, dim3((threads + 255) / 256, count), dim3(256), 0, stream, entries_dev, M);
+    if (glu)
+        hipLaunchKernelGGL(part_sum_glu_kernel, dim3((threads + 255) / 256, count), dim3(256), 0, stream, entries_dev, M);
+    else
+        hipLaunchKernelGGL(part_sum_kernel, dim3((threads + 255) / 256, count), dim3(256), 0, stream, entries_dev, M);
     return hipGetLastError();
 }
 
