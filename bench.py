@@ -807,7 +807,9 @@ def main():
                        "dependency order as one sequence with the layer's RMSNorms, SiLU-mul and "
                        "residuals (ql_seq_create_fused, fp32 x): per pass one GEMM launch (96: the "
                        "prefill kernel where its tiles fill the device, else the chunked split-K "
-                       "GEMM), plus one launch per RMSNorm or SiLU-mul input (72)")
+                       "GEMM), a part-sum launch after each chunked pass with K split, and one "
+                       "launch per RMSNorm (48) or SiLU-mul input (24; none where the gate/up pass's "
+                       "part-sum launch writes it)")
         extra["prefill05"] = pre
         log(f"prefill: {pre}")
 
